@@ -1,0 +1,217 @@
+"""Benchmark of welvet's Dense MatVec path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload q4k_4096x14336]
+
+A step is one batch-1 dequant-GEMV launch (y = W x, W packed, x and y f32 in
+HBM). Weights are N(0, 0.02) packed by the library's quant.Pack restatement,
+x ~ N(0, 1). Consecutive steps rotate over enough uploaded copies of W that
+the working set exceeds the 256 MB Infinity Cache, so every step streams W
+from HBM. Timing uses HIP events recorded on the stream the kernels run on.
+
+Prints ONE JSON line (the driver's contract) with `roofline` (algorithmic
+bytes / average kernel duration against 8 TB/s) and `cpu_baseline` (the CPU
+restatement of welvet's Go/SIMD path, timed on this host's cores over a
+bounded sample).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+MALL_BYTES = 256 << 20
+
+# name: (format, rows=out, cols=in, description)
+WORKLOADS = {
+    "q4k_4096x14336": ("Q4_K", 14336, 4096, "Q4_K dequant-GEMV 4096->14336 b=1"),
+    "q4k_4096x4096": ("Q4_K", 4096, 4096, "Q4_K dequant-GEMV 4096->4096 b=1"),
+    "q4k_14336x4096": ("Q4_K", 4096, 14336, "Q4_K dequant-GEMV 14336->4096 b=1"),
+    "q6k_4096x14336": ("Q6_K", 14336, 4096, "Q6_K dequant-GEMV 4096->14336 b=1"),
+    "q6k_4096x4096": ("Q6_K", 4096, 4096, "Q6_K dequant-GEMV 4096->4096 b=1"),
+    "q6k_14336x4096": ("Q6_K", 4096, 14336, "Q6_K dequant-GEMV 14336->4096 b=1"),
+    "q8_0_4096x14336": ("Q8_0", 14336, 4096, "Q8_0 dequant-GEMV 4096->14336 b=1"),
+    "q8_0_4096x4096": ("Q8_0", 4096, 4096, "Q8_0 dequant-GEMV 4096->4096 b=1"),
+    "q8_0_14336x4096": ("Q8_0", 4096, 14336, "Q8_0 dequant-GEMV 14336->4096 b=1"),
+    "q4_0_4096x4096": ("Q4_0", 4096, 4096, "Q4_0 dequant-GEMV 4096->4096 b=1"),
+    "ternary_2560x6912": ("NativeTernary", 6912, 2560, "DTypeTernary int8 GEMV 2560->6912 b=1"),
+    "ternary_6912x2560": ("NativeTernary", 2560, 6912, "DTypeTernary int8 GEMV 6912->2560 b=1"),
+}
+METRIC = "dequant-GEMV HBM GB/s (% of peak) at 4096->14336 Q4_K b=1; decode tokens/s"
+
+
+def algorithmic_bytes(packed, rows, cols, ternary):
+    """Packed weight bytes in the reference layout + x + y (int8 x for ternary)."""
+    x_bytes = cols if ternary else 4 * cols
+    return packed.nbytes + (4 if ternary else 0) + x_bytes + 4 * rows
+
+
+def make_weights(fmt, rows, cols, seed=1234):
+    rng = np.random.default_rng(seed)
+    if fmt == "NativeTernary":
+        t = rng.choice(np.array([-1, 0, 1], np.int8), size=rows * cols, p=[0.335, 0.33, 0.335])
+        s = np.float32(np.abs(rng.standard_normal(1 << 16).astype(np.float32) * np.float32(0.02)).mean())
+        return (t.astype(np.float32) * s).astype(np.float32), rng
+    return (rng.standard_normal(rows * cols, dtype=np.float32) * np.float32(0.02)).astype(np.float32), rng
+
+
+def cpu_baseline(packed, x, rows, cols, ternary, nbytes, budget_s, threads):
+    """CPU restatement of welvet's Go/SIMD Dense path (oracle/), timed here."""
+    import oracle
+    op = oracle.Packed(packed.fmt if not ternary else 0, rows, cols, packed.raw, packed.scales, packed.meta,
+                       packed.block_weights)
+    if ternary:
+        t0 = time.perf_counter()
+        oracle.ternary_i8_forward(packed.raw, np.float32(packed.tensor_scale), rows, cols, x)
+        one = time.perf_counter() - t0
+        n = max(1, min(200, int(budget_s / max(one, 1e-6))))
+        t0 = time.perf_counter()
+        for _ in range(n):
+            oracle.ternary_i8_forward(packed.raw, np.float32(packed.tensor_scale), rows, cols, x)
+        dt = (time.perf_counter() - t0) / n
+        return dict(value=round(nbytes / dt / 1e9, 3), unit="GB/s", cores=1, kind="port",
+                    sample=f"{n} full calls of forwardSIMDNarrowI8 restated (serial, re-expands codes per call, "
+                           f"as the reference), {dt * 1e3:.3f} ms/call")
+    t0 = time.perf_counter()
+    simd = oracle.SimdPath(op)
+    cache_s = time.perf_counter() - t0
+    simd.matvec(x, nthreads=threads)  # warm
+    t0 = time.perf_counter()
+    simd.matvec(x, nthreads=threads)
+    one = time.perf_counter() - t0
+    n = max(2, min(500, int(budget_s / max(one, 1e-6))))
+    t0 = time.perf_counter()
+    for _ in range(n):
+        simd.matvec(x, nthreads=threads)
+    dt = (time.perf_counter() - t0) / n
+    simd.close()
+    return dict(value=round(nbytes / dt / 1e9, 3), unit="GB/s", cores=threads, kind="port",
+                sample=f"{n} full GEMVs of the restated fused SIMD path (Ensure*SIMDCache projection built once in "
+                       f"{cache_s:.2f} s, not timed; f64 Dot*Row kernels, {threads} row-shard threads), "
+                       f"{dt * 1e3:.3f} ms/call")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--workload", default="q4k_4096x14336", choices=sorted(WORKLOADS))
+    ap.add_argument("--cpu-budget-s", type=float, default=12.0)
+    ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU (every box here has one MI355X); "
+              "multi-GPU sharding is described in DESIGN.md, not run. Use --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import welvet_amd as wv
+
+    fmt, rows, cols, desc = WORKLOADS[args.workload]
+    ternary = fmt == "NativeTernary"
+    print(f"[bench] {desc}: packing", file=sys.stderr, flush=True)
+    w, rng = make_weights(fmt, rows, cols)
+    packed = wv.pack(fmt, w, rows, cols)
+    del w
+    x = rng.standard_normal(cols, dtype=np.float32)
+    nbytes = algorithmic_bytes(packed, rows, cols, ternary)
+
+    wv.init(0)
+    copies = max(8, math.ceil(1.25 * MALL_BYTES / packed.nbytes))
+    print(f"[bench] uploading {copies} copies ({copies * packed.nbytes / 1e6:.0f} MB)", file=sys.stderr, flush=True)
+    blobs = [wv.upload(packed) for _ in range(copies)]
+    dev_bytes = blobs[0].info()["device_bytes"]
+    stream = torch.cuda.Stream()
+    sh = stream.cuda_stream
+    tx = torch.from_numpy(x).cuda()
+    ty = torch.empty(rows, device="cuda")
+    torch.cuda.synchronize()
+
+    # correctness gate on the benchmarked blob (full f64 reference is in tests/)
+    with torch.cuda.stream(stream):
+        blobs[0].matvec_dev(tx.data_ptr(), ty.data_ptr(), 1, sh)
+    stream.synchronize()
+    assert torch.isfinite(ty).all().item(), "non-finite output"
+
+    def run(n, first=0):
+        for i in range(n):
+            blobs[(first + i) % copies].matvec_dev(tx.data_ptr(), ty.data_ptr(), 1, sh)
+
+    with torch.cuda.stream(stream):
+        run(args.warmup)
+    stream.synchronize()
+
+    # timed region: K back-to-back launches, events on the kernels' stream
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    with torch.cuda.stream(stream):
+        run(args.steps)
+    e1.record(stream)
+    e1.synchronize()
+    torch.cuda.synchronize()
+    ms_total = e0.elapsed_time(e1)
+    ms_per_step = ms_total / args.steps
+    value = nbytes / (ms_per_step * 1e-3) / 1e9
+
+    # per-launch kernel duration: an event pair around every launch
+    nk = min(args.steps, 400)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(nk)]
+    with torch.cuda.stream(stream):
+        for i in range(nk):
+            evs[i][0].record(stream)
+            blobs[i % copies].matvec_dev(tx.data_ptr(), ty.data_ptr(), 1, sh)
+            evs[i][1].record(stream)
+    stream.synchronize()
+    durs = np.array([a.elapsed_time(b) for a, b in evs]) * 1e3  # us
+    kern_us = float(np.median(durs))
+    achieved = nbytes / (kern_us * 1e-6) / 1e9
+
+    result = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int32" if ternary else "f32",
+        "data": "synthetic: W ~ N(0,0.02) packed by the library's quant.Pack restatement, x ~ N(0,1)",
+        "config": {
+            "workload": desc, "format": fmt, "in": cols, "out": rows, "batch": 1,
+            "weight_copies_rotated": copies, "packed_bytes": int(packed.nbytes),
+            "device_bytes": int(dev_bytes), "algorithmic_bytes_per_step": int(nbytes),
+        },
+        "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
+        "roofline": {
+            "bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "kernel_us_median": round(kern_us, 3), "kernel_us_p10_p90": [round(float(np.percentile(durs, 10)), 3),
+                                                                          round(float(np.percentile(durs, 90)), 3)],
+        },
+    }
+    if not args.no_cpu:
+        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        print(f"[bench] cpu baseline ({threads} threads, ~{args.cpu_budget_s:.0f} s)", file=sys.stderr, flush=True)
+        result["cpu_baseline"] = cpu_baseline(packed, x, rows, cols, ternary, nbytes, args.cpu_budget_s, threads)
+    for b in blobs:
+        b.free()
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,145 @@
+/*
+ * welvet_hip.h — C ABI of the MI355X (gfx950) Dense MatVec library.
+ *
+ * Drop-in device backend for welvet's fused dequantize-and-dot path
+ * (github.com/openfluke/welvet). Plain C types only: a cgo / ctypes binding
+ * passes Go slices / numpy buffers as pointer + length.
+ *
+ * Conventions
+ *   - Every function returns 0 (WV_OK) or a negative WV_E_* code; the message
+ *     of the last failure on the calling thread is wv_last_error().
+ *   - Formats use quant.Format's numbering (quant/format.go:9-39). The
+ *     per-tensor DType packs of weights.Store (FormatNone + DType) use
+ *     WV_NATIVE_BASE + core.DType (core/dtype.go:11-52).
+ *   - A packed blob is uploaded once into HBM (copied; the caller keeps
+ *     ownership of its host buffers, which may be freed after the call) and
+ *     referenced by an opaque 64-bit handle afterwards.
+ *   - *_dev entry points take device pointers and a hipStream_t passed as
+ *     void* (NULL = the library's own stream for the current device); they
+ *     enqueue work and return without synchronising. Host-pointer entry
+ *     points copy in, compute and copy out synchronously.
+ *   - All entry points are thread-safe (handle table under a mutex,
+ *     thread-local error text).
+ */
+#ifndef WELVET_HIP_H
+#define WELVET_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ---- */
+#define WV_OK 0
+#define WV_E_ARG (-1)      /* null pointer / bad argument */
+#define WV_E_SHAPE (-2)    /* size mismatch (quant/helpers.go:94-114 wording) */
+#define WV_E_FORMAT (-3)   /* format not implemented (quant/errors.go:17-19) */
+#define WV_E_OOM (-4)      /* device memory exhausted (webgpu.IsAffineVRAMFull analogue) */
+#define WV_E_HIP (-5)      /* HIP runtime error */
+#define WV_E_NODEV (-6)    /* no HIP device */
+#define WV_E_HANDLE (-7)   /* unknown / freed handle */
+
+/* ---- formats: quant.Format values (quant/format.go:9-39) ---- */
+enum wv_format {
+    WV_FMT_NONE = 0,
+    WV_FMT_Q8_0 = 1, WV_FMT_Q4_0 = 2, WV_FMT_Q4_1 = 3, WV_FMT_Q5_0 = 4, WV_FMT_Q5_1 = 5,
+    WV_FMT_Q2_K = 6, WV_FMT_Q3_K = 7, WV_FMT_Q4_K = 8, WV_FMT_Q5_K = 9, WV_FMT_Q6_K = 10,
+    WV_FMT_IQ1_S = 11, WV_FMT_IQ2_XXS = 12, WV_FMT_IQ2_XS = 13, WV_FMT_IQ3_XXS = 14,
+    WV_FMT_IQ3_S = 15, WV_FMT_IQ4_NL = 16, WV_FMT_IQ4_XS = 17,
+    WV_FMT_TERNARY_PACKED = 18, WV_FMT_BINARY_PACKED = 19, WV_FMT_AFFINE_PACKED = 20
+};
+/* FormatNone stores: weights.Store{DType, Native, Scale} (weights/store.go:14-32). */
+#define WV_NATIVE_BASE 1000
+#define WV_NATIVE_TERNARY (WV_NATIVE_BASE + 19) /* core.DTypeTernary */
+
+/* ---- library ---- */
+
+/* Selects and initialises HIP device `device` for this process.
+ * Replaces: webgpu session creation (webgpu/dense.go:23-113). */
+int wv_init(int device);
+
+/* Text of the last error on the calling thread ("" if none). */
+const char *wv_last_error(void);
+
+/* Library version string. */
+const char *wv_version(void);
+
+/* ---- host-side packers: quant.Pack (quant/pack.go:4) ---- */
+
+/* Sizes Pack produces: *raw_len bytes of Blob.Raw, *n_scales / *n_mins floats
+ * of Blob.Scales / Blob.Mins, *n_meta bytes of Blob.Meta, *block_weights.
+ * Replaces the allocation arithmetic inside quant.Pack* (e.g. q4_0.go:15-16,
+ * kquant.go:70-73, iq.go:80-83). */
+int wv_pack_sizes(int format, int64_t rows, int64_t cols, size_t *raw_len,
+                  size_t *n_scales, size_t *n_mins, size_t *n_meta, int32_t *block_weights);
+
+/* quant.Pack(format, weights, rows, cols) (quant/pack.go:4): row-major f32
+ * weights[rows*cols] → caller-sized Raw/Scales/Mins/Meta buffers. */
+int wv_pack(int format, const float *weights, int64_t rows, int64_t cols,
+            uint8_t *raw, float *scales, float *mins, uint8_t *meta);
+
+/* weights.Store packing for FormatNone DTypeTernary (weights/native.go:249-267):
+ * codes[(n+3)/4] (4 codes per byte, LSB-first) and the absMax scale. */
+int wv_pack_native_ternary(const float *weights, int64_t n, uint8_t *codes, float *scale);
+
+/* ---- resident blobs ---- */
+
+/* Uploads a packed quant.Blob (quant/format.go:110-131) into HBM once.
+ * Replaces the per-call CreateBufferInit uploads of the WebGPU path
+ * (webgpu/dense.go:570-617) and the lazily built host SIMD caches
+ * (quant.EnsureFusedSIMDCache, quant/qx_simd.go:150). For WV_NATIVE_TERNARY,
+ * raw = Store.Native codes and tensor_scale = Store.Scale. */
+int wv_blob_upload(int format, int64_t rows, int64_t cols, int32_t block_weights,
+                   const uint8_t *raw, size_t raw_len,
+                   const float *scales, size_t n_scales,
+                   const float *mins, size_t n_mins,
+                   const uint8_t *meta, size_t n_meta,
+                   float tensor_scale, uint64_t *handle);
+
+/* Releases the device copy (host_release.go:15 analogue for the device side). */
+int wv_blob_free(uint64_t handle);
+
+/* Shape / residency of a blob: any out-pointer may be NULL. */
+int wv_blob_info(uint64_t handle, int *format, int64_t *rows, int64_t *cols,
+                 size_t *device_bytes, int *layout);
+
+/* ---- forward: quant.MatVec / dense.MatVecPackedBlob / dense.Forward ---- */
+
+/* y[batch*rows] = W x[batch*cols] for each of `batch` rows (y overwritten).
+ * Host pointers; synchronous. Replaces quant.MatVec (quant/matvec.go:5),
+ * dense.MatVecPackedBlob (layers/dense/simd.go:571) and the packed branch of
+ * dense.ForwardSIMD (layers/dense/simd.go:42-45) for linear, bias-free layers.
+ * For WV_NATIVE_TERNARY it is forwardSIMDNarrowI8 (layers/dense/simd.go:130-147):
+ * activations absmax-quantized to int8, exact int32 accumulators,
+ * y = f32(acc) * actScale * scale. */
+int wv_matvec(uint64_t handle, const float *x, float *y, int32_t batch);
+
+/* Device-pointer form of wv_matvec, enqueued on `stream`. */
+int wv_matvec_dev(uint64_t handle, const float *d_x, float *d_y, int32_t batch, void *stream);
+
+/* WV_NATIVE_TERNARY only: the exact int32 accumulators (batch*rows) and the
+ * per-batch-row activation scales (batch) of the int8 path, device pointers. */
+int wv_ternary_acc_dev(uint64_t handle, const float *d_x, int32_t *d_acc, float *d_act_scale,
+                       int32_t batch, void *stream);
+
+/* ---- backward: quant.MatVecT ---- */
+
+/* gx[batch*cols] += W^T gy[batch*rows] (gx NOT zeroed, quant/matvec_t.go:3-5).
+ * Host pointers; synchronous. Replaces quant.MatVecT (quant/matvec_t.go:5)
+ * as called from backwardSIMDPacked (layers/dense/simd_quant.go:103-126). */
+int wv_matvec_t(uint64_t handle, const float *gy, float *gx, int32_t batch);
+
+/* Device-pointer form of wv_matvec_t. */
+int wv_matvec_t_dev(uint64_t handle, const float *d_gy, float *d_gx, int32_t batch, void *stream);
+
+/* ---- streams ---- */
+
+/* Blocks until all work the library enqueued on `stream` (NULL = its own) is done. */
+int wv_sync(void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* WELVET_HIP_H */

@@ -1,0 +1,89 @@
+"""C-ABI library checks that need no GPU: symbols, host packers, error paths."""
+import os
+import re
+
+import numpy as np
+import pytest
+
+import oracle
+import welvet_amd as wv
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+PACKABLE = ["Q4_0", "Q8_0", "Q4_1", "Q5_0", "Q5_1", "Q2_K", "Q3_K", "Q4_K", "Q5_K", "Q6_K",
+            "IQ1_S", "IQ2_XXS", "IQ2_XS", "IQ3_XXS", "IQ3_S", "IQ4_NL", "IQ4_XS",
+            "TernaryPacked", "BinaryPacked"]
+
+
+def declared_symbols():
+    names = set()
+    for fn in os.listdir(os.path.join(ROOT, "include")):
+        if fn.endswith(".h"):
+            src = open(os.path.join(ROOT, "include", fn)).read()
+            names |= set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(wv_\w+)\s*\(", src, re.M))
+    return names
+
+
+def test_library_exports_every_declared_symbol():
+    L = wv.lib()
+    decl = declared_symbols()
+    assert decl, "no declarations parsed"
+    assert decl == set(wv.EXPORTS)
+    for name in decl:
+        assert hasattr(L, name), name
+    assert b"gfx950" in L.wv_version()
+
+
+@pytest.mark.parametrize("shape", [(16, 256), (5, 77), (64, 512), (3, 1000)])
+@pytest.mark.parametrize("fmt", PACKABLE)
+def test_host_packer_bit_exact_vs_oracle(fmt, shape):
+    rows, cols = shape
+    rng = np.random.default_rng(7 + rows)
+    w = (rng.standard_normal(rows * cols) * 0.02).astype(np.float32)
+    a = wv.pack(fmt, w, rows, cols)
+    b = oracle.pack(fmt, w, rows, cols)
+    assert np.array_equal(a.raw, b.raw)
+    if b.scales is not None:
+        assert np.array_equal(a.scales, b.scales)
+    if b.meta is not None:
+        assert np.array_equal(a.meta, b.meta)
+    assert a.block_weights == b.block_weights
+
+
+def test_host_packer_large_parallel_matches_oracle():
+    # exercises the multi-threaded block split (> 4096 blocks)
+    rng = np.random.default_rng(3)
+    rows, cols = 512, 4096
+    w = (rng.standard_normal(rows * cols) * 0.02).astype(np.float32)
+    for fmt in ("Q4_K", "Q6_K", "Q8_0", "Q4_0", "IQ4_NL"):
+        assert np.array_equal(wv.pack(fmt, w, rows, cols).raw, oracle.pack(fmt, w, rows, cols).raw), fmt
+
+
+def test_native_ternary_pack_matches_oracle():
+    rng = np.random.default_rng(5)
+    t = rng.choice([-1, 0, 1], size=2560 * 64, p=[0.335, 0.33, 0.335])
+    s = np.abs(rng.standard_normal(4096) * 0.02).mean().astype(np.float32)
+    w = (t * s).astype(np.float32)
+    p = wv.pack_native_ternary(w, 64, 2560)
+    codes, scale = oracle.pack_native_ternary(w)
+    assert np.array_equal(p.raw, codes)
+    assert np.float32(p.tensor_scale) == scale == np.float32(s)
+
+
+def test_error_paths_without_device():
+    with pytest.raises(wv.WelvetError) as e:
+        wv.pack_sizes("Q4_K", 0, 256)
+    assert e.value.code == -2
+    with pytest.raises(wv.WelvetError) as e:
+        wv.pack_sizes(20, 4, 64)  # AffinePacked: not built here
+    assert e.value.code == -3 and "not implemented" in str(e.value)
+    short = wv.PackedBlob("Q4_K", 4, 256, np.zeros(10, np.uint8), block_weights=256)
+    with pytest.raises(wv.WelvetError) as e:
+        wv.upload(short)
+    assert e.value.code == -2 and "raw short" in str(e.value)
+    bad = wv.PackedBlob(99, 4, 256, np.zeros(1024, np.uint8))
+    with pytest.raises(wv.WelvetError) as e:
+        wv.upload(bad)
+    assert e.value.code == -3
+    with pytest.raises(wv.WelvetError) as e:
+        wv.check(wv.lib().wv_blob_free(123456789))
+    assert e.value.code == -7

@@ -1,0 +1,185 @@
+"""GPU parity through the C ABI: libwelvet_hip on an MI355X vs the CPU oracle.
+
+Tolerances: f32 outputs within 1e-5 normwise relative
+error of the f64 textbook GEMV over the reference's dequantized weights
+(max|y_gpu - y_ref| / max|y_ref|); DTypeTernary int32 accumulators bit-exact.
+"""
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+import welvet_amd as wv
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+ALL = ["Q4_0", "Q8_0", "Q4_1", "Q5_0", "Q5_1", "Q2_K", "Q3_K", "Q4_K", "Q5_K", "Q6_K",
+       "IQ1_S", "IQ2_XXS", "IQ2_XS", "IQ3_XXS", "IQ3_S", "IQ4_NL", "IQ4_XS",
+       "TernaryPacked", "BinaryPacked"]
+PLANAR = {"Q4_K": "k-planar", "Q6_K": "k-planar", "Q8_0": "q8-planar", "Q4_0": "q4-planar"}
+
+
+@pytest.fixture(scope="module", autouse=True)
+def device():
+    print(f"[gpu] {__name__}: init device 0", flush=True)
+    wv.init(0)
+    yield
+
+
+def normwise(y, ref):
+    ref = np.asarray(ref, np.float64)
+    return float(np.abs(np.asarray(y, np.float64) - ref).max() / max(np.abs(ref).max(), 1e-30))
+
+
+def weights(rows, cols, seed):
+    rng = np.random.default_rng(seed)
+    return (rng.standard_normal(rows * cols) * 0.02).astype(np.float32), rng
+
+
+def upload(fmt, w, rows, cols, force_raw=False):
+    p = wv.pack(fmt, w, rows, cols)
+    old = os.environ.get("WV_FORCE_RAW")
+    os.environ["WV_FORCE_RAW"] = "1" if force_raw else "0"
+    try:
+        d = wv.upload(p)
+    finally:
+        if old is None:
+            os.environ.pop("WV_FORCE_RAW")
+        else:
+            os.environ["WV_FORCE_RAW"] = old
+    return p, d
+
+
+def oracle_packed(p):
+    return oracle.Packed(p.fmt, p.rows, p.cols, p.raw, p.scales, p.meta, p.block_weights)
+
+
+@pytest.mark.parametrize("fmt", ALL)
+@pytest.mark.parametrize("shape", [(96, 512), (7, 77), (33, 1000)])
+def test_matvec_small(fmt, shape):
+    rows, cols = shape
+    print(f"[gpu] matvec {fmt} {rows}x{cols}", flush=True)
+    w, rng = weights(rows, cols, 100 + rows)
+    x = rng.standard_normal((3, cols)).astype(np.float32)
+    p, d = upload(fmt, w, rows, cols)
+    ref = oracle.reference_y(oracle_packed(p), x)
+    y = d.matvec(x)
+    assert normwise(y, ref) <= TOL
+    y1 = d.matvec(x[1])
+    assert normwise(y1, ref[1]) <= TOL
+    d.free()
+
+
+@pytest.mark.parametrize("fmt", sorted(PLANAR))
+def test_planar_and_raw_layouts_agree(fmt):
+    rows, cols = 300, 2048
+    print(f"[gpu] layouts {fmt}", flush=True)
+    w, rng = weights(rows, cols, 5)
+    x = rng.standard_normal(cols).astype(np.float32)
+    p, dp = upload(fmt, w, rows, cols)
+    _, dr = upload(fmt, w, rows, cols, force_raw=True)
+    assert dp.info()["layout"] == PLANAR[fmt]
+    assert dr.info()["layout"] == "raw"
+    assert dp.info()["device_bytes"] <= p.nbytes + 4096  # same bytes as the reference blob (+ alignment)
+    ref = oracle.reference_y(oracle_packed(p), x)[0]
+    assert normwise(dp.matvec(x), ref) <= TOL
+    assert normwise(dr.matvec(x), ref) <= TOL
+
+
+@pytest.mark.parametrize("fmt", ["Q4_K", "Q8_0", "Q6_K"])
+@pytest.mark.parametrize("shape", [(4096, 4096), (14336, 4096), (4096, 14336)])
+def test_baseline_shapes(fmt, shape):
+    rows, cols = shape
+    print(f"[gpu] baseline {fmt} {cols}->{rows}", flush=True)
+    w, rng = weights(rows, cols, 42)
+    x = rng.standard_normal(cols).astype(np.float32)
+    p, d = upload(fmt, w, rows, cols)
+    ref = oracle.reference_y(oracle_packed(p), x)[0]
+    assert normwise(d.matvec(x), ref) <= TOL
+    d.free()
+
+
+def test_q4_0_baseline_4096():
+    w, rng = weights(4096, 4096, 1)
+    x = rng.standard_normal(4096).astype(np.float32)
+    p, d = upload("Q4_0", w, 4096, 4096)
+    ref = oracle.reference_y(oracle_packed(p), x)[0]
+    assert normwise(d.matvec(x), ref) <= TOL
+
+
+def ternary_weights(rows, cols, seed):
+    rng = np.random.default_rng(seed)
+    t = rng.choice([-1, 0, 1], size=rows * cols, p=[0.335, 0.33, 0.335]).astype(np.int8)
+    s = np.float32(np.abs(rng.standard_normal(1 << 16) * 0.02).astype(np.float32).mean())
+    return t, s, (t * s).astype(np.float32), rng
+
+
+@pytest.mark.parametrize("shape", [(6912, 2560), (2560, 6912), (37, 100), (64, 64)])
+def test_native_ternary_bit_exact(shape):
+    import torch
+    rows, cols = shape
+    print(f"[gpu] native ternary {cols}->{rows}", flush=True)
+    t, s, w, rng = ternary_weights(rows, cols, rows)
+    x = rng.standard_normal((2, cols)).astype(np.float32)
+    p = wv.pack_native_ternary(w, rows, cols)
+    d = wv.upload(p)
+    assert d.info()["layout"] == "ternary-i8"
+    y_ref, acc_ref, as_ref = oracle.ternary_i8_forward(p.raw, np.float32(p.tensor_scale), rows, cols, x)
+    tx = torch.from_numpy(x).cuda()
+    acc = torch.zeros(2 * rows, dtype=torch.int32, device="cuda")
+    act = torch.zeros(2, dtype=torch.float32, device="cuda")
+    y = torch.zeros(2 * rows, dtype=torch.float32, device="cuda")
+    d.ternary_acc_dev(tx.data_ptr(), acc.data_ptr(), act.data_ptr(), 2)
+    d.matvec_dev(tx.data_ptr(), y.data_ptr(), 2)
+    wv.sync()
+    assert np.array_equal(acc.cpu().numpy(), acc_ref)
+    assert np.array_equal(act.cpu().numpy(), as_ref)
+    assert np.array_equal(y.cpu().numpy(), y_ref)
+    assert np.array_equal(d.matvec(x).reshape(-1), y_ref)
+
+
+@pytest.mark.parametrize("fmt", ["Q4_0", "Q8_0", "Q4_K", "Q6_K", "IQ4_NL", "TernaryPacked", "BinaryPacked", "Q5_1"])
+def test_matvec_t_accumulates(fmt):
+    rows, cols = 300, 512
+    print(f"[gpu] matvec_t {fmt}", flush=True)
+    w, rng = weights(rows, cols, 9)
+    gy = rng.standard_normal((2, rows)).astype(np.float32)
+    gx0 = rng.standard_normal((2, cols)).astype(np.float32)
+    p, d = upload(fmt, w, rows, cols, force_raw=True)
+    wd = oracle.unpack(oracle_packed(p)).reshape(rows, cols).astype(np.float64)
+    want = gx0 + gy.astype(np.float64) @ wd
+    got = d.matvec_t(gy, gx0)
+    assert normwise(got, want) <= TOL
+
+
+def test_device_pointer_path_on_torch_stream():
+    import torch
+    rows, cols = 1024, 4096
+    w, rng = weights(rows, cols, 77)
+    x = rng.standard_normal(cols).astype(np.float32)
+    p, d = upload("Q4_K", w, rows, cols)
+    s = torch.cuda.Stream()
+    tx = torch.from_numpy(x).cuda()
+    ty = torch.empty(rows, device="cuda")
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s):
+        d.matvec_dev(tx.data_ptr(), ty.data_ptr(), 1, s.cuda_stream)
+    s.synchronize()
+    ref = oracle.reference_y(oracle_packed(p), x)[0]
+    assert normwise(ty.cpu().numpy(), ref) <= TOL
+
+
+def test_binary_g128_layout():
+    rows, cols = 64, 512
+    rng = np.random.default_rng(128)
+    words = rng.integers(0, 2**32, size=rows * cols // 32, dtype=np.uint64).astype(np.uint32)
+    scales = (np.abs(rng.standard_normal(rows * cols // 128)) * 0.02 + 1e-3).astype(np.float32)
+    p = wv.PackedBlob("BinaryPacked", rows, cols, words.view(np.uint8), scales, None, 128)
+    d = wv.upload(p)
+    x = rng.standard_normal(cols).astype(np.float32)
+    op = oracle.Packed(p.fmt, rows, cols, p.raw, scales, None, 128)
+    ref = oracle.reference_y(op, x)[0]
+    assert normwise(d.matvec(x), ref) <= TOL
+    assert normwise(oracle.matvec_scalar(op, x), ref) <= TOL

@@ -1,0 +1,220 @@
+"""welvet_amd — Python plumbing over libwelvet_hip.so (the C ABI in include/welvet_hip.h).
+
+The library is the MI355X (gfx950) backend of welvet's Dense MatVec path; this
+module only loads it with ctypes and moves numpy / torch buffers across the
+boundary, for the tests and the benchmark. Importing it fails loudly when the
+built library is missing: there is no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libwelvet_hip.so")
+
+# quant.Format numbering (quant/format.go:9-39) + FormatNone DTypeTernary.
+FORMATS = {
+    "Q8_0": 1, "Q4_0": 2, "Q4_1": 3, "Q5_0": 4, "Q5_1": 5,
+    "Q2_K": 6, "Q3_K": 7, "Q4_K": 8, "Q5_K": 9, "Q6_K": 10,
+    "IQ1_S": 11, "IQ2_XXS": 12, "IQ2_XS": 13, "IQ3_XXS": 14, "IQ3_S": 15,
+    "IQ4_NL": 16, "IQ4_XS": 17, "TernaryPacked": 18, "BinaryPacked": 19,
+    "NativeTernary": 1019,
+}
+FORMAT_NAMES = {v: k for k, v in FORMATS.items()}
+LAYOUTS = {0: "raw", 1: "k-planar", 2: "q8-planar", 3: "q4-planar", 4: "ternary-i8"}
+
+WV_E = {-1: "ARG", -2: "SHAPE", -3: "FORMAT", -4: "OOM", -5: "HIP", -6: "NODEV", -7: "HANDLE"}
+
+# Every symbol include/welvet_hip.h declares.
+EXPORTS = (
+    "wv_init", "wv_last_error", "wv_version", "wv_pack_sizes", "wv_pack",
+    "wv_pack_native_ternary", "wv_blob_upload", "wv_blob_free", "wv_blob_info",
+    "wv_matvec", "wv_matvec_dev", "wv_ternary_acc_dev", "wv_matvec_t",
+    "wv_matvec_t_dev", "wv_sync",
+)
+
+
+class WelvetError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"{WV_E.get(code, code)}: {msg}")
+        self.code = code
+
+
+_lib = None
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_SZ = ctypes.c_size_t
+
+
+def lib():
+    """The loaded library; raises if libwelvet_hip.so has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(f"{LIB_PATH} is missing: run `python -m welvet_amd.build` (no CPU fallback exists)")
+    L = ctypes.CDLL(LIB_PATH)
+    L.wv_init.argtypes = [ctypes.c_int]
+    L.wv_last_error.restype = ctypes.c_char_p
+    L.wv_version.restype = ctypes.c_char_p
+    L.wv_pack_sizes.argtypes = [ctypes.c_int, _I64, _I64, _P, _P, _P, _P, _P]
+    L.wv_pack.argtypes = [ctypes.c_int, _P, _I64, _I64, _P, _P, _P, _P]
+    L.wv_pack_native_ternary.argtypes = [_P, _I64, _P, _P]
+    L.wv_blob_upload.argtypes = [ctypes.c_int, _I64, _I64, ctypes.c_int32, _P, _SZ, _P, _SZ, _P, _SZ, _P, _SZ,
+                                 ctypes.c_float, _P]
+    L.wv_blob_free.argtypes = [ctypes.c_uint64]
+    L.wv_blob_info.argtypes = [ctypes.c_uint64, _P, _P, _P, _P, _P]
+    L.wv_matvec.argtypes = [ctypes.c_uint64, _P, _P, ctypes.c_int32]
+    L.wv_matvec_dev.argtypes = [ctypes.c_uint64, _P, _P, ctypes.c_int32, _P]
+    L.wv_ternary_acc_dev.argtypes = [ctypes.c_uint64, _P, _P, _P, ctypes.c_int32, _P]
+    L.wv_matvec_t.argtypes = [ctypes.c_uint64, _P, _P, ctypes.c_int32]
+    L.wv_matvec_t_dev.argtypes = [ctypes.c_uint64, _P, _P, ctypes.c_int32, _P]
+    L.wv_sync.argtypes = [_P]
+    _lib = L
+    return L
+
+
+def check(rc: int) -> None:
+    if rc != 0:
+        raise WelvetError(rc, lib().wv_last_error().decode())
+
+
+def _fmt(fmt) -> int:
+    return fmt if isinstance(fmt, int) else FORMATS[fmt]
+
+
+def init(device: int = 0) -> None:
+    check(lib().wv_init(device))
+
+
+class PackedBlob:
+    """Host-side quant.Blob fields (quant/format.go:110-131)."""
+
+    def __init__(self, fmt, rows, cols, raw, scales=None, meta=None, block_weights=0, tensor_scale=0.0):
+        self.fmt = _fmt(fmt)
+        self.rows, self.cols = int(rows), int(cols)
+        self.raw = np.ascontiguousarray(raw, np.uint8)
+        self.scales = None if scales is None or len(scales) == 0 else np.ascontiguousarray(scales, np.float32)
+        self.meta = None if meta is None or len(meta) == 0 else np.ascontiguousarray(meta, np.uint8)
+        self.block_weights = int(block_weights)
+        self.tensor_scale = float(tensor_scale)
+
+    @property
+    def name(self) -> str:
+        return FORMAT_NAMES.get(self.fmt, str(self.fmt))
+
+    @property
+    def nbytes(self) -> int:
+        """Packed bytes in the reference layout (Raw + Scales + Meta)."""
+        return self.raw.nbytes + (0 if self.scales is None else self.scales.nbytes) + (0 if self.meta is None else self.meta.nbytes)
+
+
+def pack_sizes(fmt, rows: int, cols: int):
+    raw, ns, nm, nmeta = _SZ(), _SZ(), _SZ(), _SZ()
+    bw = ctypes.c_int32()
+    check(lib().wv_pack_sizes(_fmt(fmt), rows, cols, ctypes.byref(raw), ctypes.byref(ns), ctypes.byref(nm),
+                              ctypes.byref(nmeta), ctypes.byref(bw)))
+    return raw.value, ns.value, nm.value, nmeta.value, bw.value
+
+
+def pack(fmt, w: np.ndarray, rows: int, cols: int) -> PackedBlob:
+    """quant.Pack (quant/pack.go:4) through the library's host packer."""
+    if _fmt(fmt) == FORMATS["NativeTernary"]:
+        return pack_native_ternary(w, rows, cols)
+    raw_n, ns, _, nmeta, bw = pack_sizes(fmt, rows, cols)
+    w = np.ascontiguousarray(w, np.float32).reshape(-1)
+    if w.size < rows * cols:
+        raise WelvetError(-2, f"Pack: bad shape rows={rows} cols={cols} len={w.size}")
+    raw = np.zeros(raw_n, np.uint8)
+    scales = np.zeros(ns, np.float32) if ns else None
+    meta = np.zeros(nmeta, np.uint8) if nmeta else None
+    check(lib().wv_pack(_fmt(fmt), w.ctypes.data, rows, cols, raw.ctypes.data,
+                        None if scales is None else scales.ctypes.data, None,
+                        None if meta is None else meta.ctypes.data))
+    return PackedBlob(fmt, rows, cols, raw, scales, meta, bw)
+
+
+def pack_native_ternary(w: np.ndarray, rows: int, cols: int) -> PackedBlob:
+    """weights.Store DTypeTernary pack (weights/native.go:249-267)."""
+    w = np.ascontiguousarray(w, np.float32).reshape(-1)[: rows * cols]
+    codes = np.zeros((w.size + 3) // 4, np.uint8)
+    scale = ctypes.c_float()
+    check(lib().wv_pack_native_ternary(w.ctypes.data, w.size, codes.ctypes.data, ctypes.byref(scale)))
+    return PackedBlob("NativeTernary", rows, cols, codes, None, None, 0, scale.value)
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data
+
+
+class DeviceBlob:
+    """A blob resident in HBM (wv_blob_upload); freed with free() or on GC."""
+
+    def __init__(self, packed: PackedBlob):
+        h = ctypes.c_uint64()
+        p = packed
+        check(lib().wv_blob_upload(p.fmt, p.rows, p.cols, p.block_weights, _p(p.raw), p.raw.size,
+                                   _p(p.scales), 0 if p.scales is None else p.scales.size, None, 0,
+                                   _p(p.meta), 0 if p.meta is None else p.meta.size,
+                                   ctypes.c_float(p.tensor_scale), ctypes.byref(h)))
+        self.handle = h.value
+        self.fmt, self.rows, self.cols = p.fmt, p.rows, p.cols
+        self.packed_bytes = p.nbytes
+
+    def info(self):
+        fmt, layout = ctypes.c_int(), ctypes.c_int()
+        rows, cols = ctypes.c_int64(), ctypes.c_int64()
+        nb = _SZ()
+        check(lib().wv_blob_info(self.handle, ctypes.byref(fmt), ctypes.byref(rows), ctypes.byref(cols),
+                                 ctypes.byref(nb), ctypes.byref(layout)))
+        return dict(format=FORMAT_NAMES.get(fmt.value, fmt.value), rows=rows.value, cols=cols.value,
+                    device_bytes=nb.value, layout=LAYOUTS.get(layout.value, layout.value))
+
+    def matvec(self, x: np.ndarray) -> np.ndarray:
+        """Host path: y = W x for x of shape (cols,) or (batch, cols)."""
+        x = np.ascontiguousarray(x, np.float32)
+        batch = x.size // self.cols
+        y = np.zeros((batch, self.rows), np.float32)
+        check(lib().wv_matvec(self.handle, x.ctypes.data, y.ctypes.data, batch))
+        return y.reshape(self.rows) if x.ndim == 1 else y
+
+    def matvec_t(self, gy: np.ndarray, gx: np.ndarray | None = None) -> np.ndarray:
+        """Host path: gx += W^T gy (gx starts at 0 when not given)."""
+        gy = np.ascontiguousarray(gy, np.float32)
+        batch = gy.size // self.rows
+        out = np.zeros((batch, self.cols), np.float32) if gx is None else np.array(gx, np.float32, copy=True).reshape(batch, self.cols)
+        check(lib().wv_matvec_t(self.handle, gy.ctypes.data, out.ctypes.data, batch))
+        return out.reshape(self.cols) if gy.ndim == 1 else out
+
+    def matvec_dev(self, x_ptr: int, y_ptr: int, batch: int = 1, stream: int | None = None) -> None:
+        check(lib().wv_matvec_dev(self.handle, x_ptr, y_ptr, batch, stream))
+
+    def matvec_t_dev(self, gy_ptr: int, gx_ptr: int, batch: int = 1, stream: int | None = None) -> None:
+        check(lib().wv_matvec_t_dev(self.handle, gy_ptr, gx_ptr, batch, stream))
+
+    def ternary_acc_dev(self, x_ptr: int, acc_ptr: int, act_ptr: int, batch: int = 1, stream: int | None = None) -> None:
+        check(lib().wv_ternary_acc_dev(self.handle, x_ptr, acc_ptr, act_ptr, batch, stream))
+
+    def free(self) -> None:
+        if self.handle:
+            check(lib().wv_blob_free(self.handle))
+            self.handle = 0
+
+    def __del__(self):
+        try:
+            if self.handle and _lib is not None:
+                _lib.wv_blob_free(self.handle)
+                self.handle = 0
+        except Exception:
+            pass
+
+
+def upload(packed: PackedBlob) -> DeviceBlob:
+    return DeviceBlob(packed)
+
+
+def sync(stream: int | None = None) -> None:
+    check(lib().wv_sync(stream))

@@ -1,0 +1,492 @@
+// runtime.hip — C ABI of libwelvet_hip: device selection, resident blob
+// table, upload-time re-layout and dispatch to the kernels in gemv.hip.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <atomic>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/welvet_hip.h"
+#include "wv_internal.h"
+
+namespace wv {
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+int hip_fail(hipError_t e, const char* what) {
+    if (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation)
+        return fail(WV_E_OOM, "%s: device memory exhausted (%s)", what, hipGetErrorString(e));
+    return fail(WV_E_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+struct DeviceState {
+    bool ready = false;
+    hipStream_t stream = nullptr;
+};
+
+std::mutex g_mu;  // guards g_blobs, g_next, g_dev
+std::unordered_map<uint64_t, DevBlob> g_blobs;
+uint64_t g_next = 1;
+DeviceState g_dev[64];
+int g_current = -1;
+
+int ensure_device_locked(int dev) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return fail(WV_E_NODEV, "wv_init: no HIP device");
+    if (dev < 0 || dev >= n || dev >= 64) return fail(WV_E_ARG, "wv_init: device %d out of range (count %d)", dev, n);
+    hipError_t e = hipSetDevice(dev);
+    if (e != hipSuccess) return hip_fail(e, "wv_init: hipSetDevice");
+    if (!g_dev[dev].ready) {
+        e = hipStreamCreateWithFlags(&g_dev[dev].stream, hipStreamNonBlocking);
+        if (e != hipSuccess) return hip_fail(e, "wv_init: hipStreamCreate");
+        g_dev[dev].ready = true;
+    }
+    g_current = dev;
+    return WV_OK;
+}
+
+int ensure_init() {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (g_current >= 0) {
+        hipSetDevice(g_current);
+        return WV_OK;
+    }
+    return ensure_device_locked(0);
+}
+
+hipStream_t stream_or_default(void* s, int dev) {
+    if (s) return static_cast<hipStream_t>(s);
+    return g_dev[dev].stream;
+}
+
+bool force_raw() {
+    const char* v = std::getenv("WV_FORCE_RAW");
+    return v && v[0] == '1';
+}
+
+inline float f32_at(const uint8_t* p) { float v; std::memcpy(&v, p, 4); return v; }
+
+// Host staging of a device image: byte buffer with 256-B aligned sections.
+struct Image {
+    std::vector<uint8_t> bytes;
+    size_t add(size_t n) {
+        size_t off = (bytes.size() + 255) & ~size_t(255);
+        bytes.resize(off + n);
+        return off;
+    }
+};
+
+// k-quant super-block → planes (requires cols % 256 == 0, so super-blocks
+// never straddle rows). Per row r, chunk j (32 columns):
+//   codes  [r][j] 16 B: 4-bit codes (Q4_K) or the low 4 bits (Q6_K);
+//   hi     [r][j]  8 B: Q6_K high 2 bits, arranged for the byte spread;
+//   dd     [r][sb] (d, dmin) f32 pair;
+//   grp    [r][j] (u'0, u'1, m0, m1) bytes (Q4_K) / (u'0, u'1) (Q6_K),
+// u' = max(u, 1): d*u/255 with u = 0 falls back to d/255 (kquant.go:179-182),
+// the same value u = 1 gives, so the kernel needs no branch.
+// Bytes per super-block equal the reference's (168 for Q4_K, 216 for Q6_K).
+bool relayout_k(const KSpec& sp, int fmt, const uint8_t* raw, int64_t rows, int64_t cols, Image& img,
+                size_t& o_codes, size_t& o_hi, size_t& o_dd, size_t& o_grp) {
+    const int64_t nsb_row = cols / 256, nch = cols / 32, sbb = k_super_bytes(sp);
+    const int64_t nsb = rows * nsb_row;
+    o_codes = img.add(size_t(rows * nch * 16));
+    o_hi = fmt == FMT_Q6_K ? img.add(size_t(rows * nch * 8)) : 0;
+    o_dd = img.add(size_t(nsb * 8));
+    o_grp = img.add(size_t(rows * nch * (fmt == FMT_Q6_K ? 2 : 4)));
+    uint8_t* codes = img.bytes.data() + o_codes;
+    uint8_t* hi = img.bytes.data() + o_hi;
+    float* dd = reinterpret_cast<float*>(img.bytes.data() + o_dd);
+    uint8_t* grp = img.bytes.data() + o_grp;
+    for (int64_t s = 0; s < nsb; ++s) {
+        const uint8_t* o = raw + s * sbb;
+        dd[2 * s] = f32_at(o);
+        dd[2 * s + 1] = f32_at(o + 4);
+        const uint8_t* q = o + (sp.has_dmin ? 40 : 24);
+        for (int p = 0; p < 8; ++p) {
+            const int64_t ci = s * 8 + p;  // chunk index within the matrix (row-major)
+            const uint8_t u0 = std::max<uint8_t>(o[8 + 2 * p], 1), u1 = std::max<uint8_t>(o[9 + 2 * p], 1);
+            if (fmt == FMT_Q6_K) {
+                grp[ci * 2] = u0;
+                grp[ci * 2 + 1] = u1;
+            } else {
+                grp[ci * 4] = u0;
+                grp[ci * 4 + 1] = u1;
+                grp[ci * 4 + 2] = o[24 + 2 * p];
+                grp[ci * 4 + 3] = o[25 + 2 * p];
+            }
+            uint8_t qv[32];
+            for (int k = 0; k < 32; ++k) {  // LSB-first bit stream (helpers.go:140-149)
+                const int64_t bit = int64_t(p * 32 + k) * sp.bits;
+                uint32_t v = q[bit >> 3] | (((bit >> 3) + 1 < (256 * sp.bits) / 8) ? uint32_t(q[(bit >> 3) + 1]) << 8 : 0u);
+                qv[k] = uint8_t((v >> (bit & 7)) & ((1u << sp.bits) - 1u));
+            }
+            uint8_t* c = codes + ci * 16;
+            for (int k = 0; k < 16; ++k) c[k] = uint8_t((qv[2 * k] & 15) | ((qv[2 * k + 1] & 15) << 4));
+            if (fmt == FMT_Q6_K) {
+                uint8_t* h = hi + ci * 8;
+                std::memset(h, 0, 8);
+                // spread word s = 2*w + half holds, in byte b, code 8w + 2b + half.
+                for (int sw = 0; sw < 8; ++sw) {
+                    const int w = sw >> 1, half = sw & 1, t = sw >> 2, f = sw & 3;
+                    for (int b = 0; b < 4; ++b) {
+                        const int k = 8 * w + 2 * b + half;
+                        h[t * 4 + b] |= uint8_t(((qv[k] >> 4) & 3) << (2 * f));
+                    }
+                }
+            }
+        }
+    }
+    return true;
+}
+
+int upload_image(const Image& img, DevBlob& b) {
+    void* d = nullptr;
+    hipError_t e = hipMalloc(&d, std::max<size_t>(img.bytes.size(), 256));
+    if (e != hipSuccess) return hip_fail(e, "wv_blob_upload: hipMalloc");
+    e = hipMemcpy(d, img.bytes.data(), img.bytes.size(), hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        hipFree(d);
+        return hip_fail(e, "wv_blob_upload: hipMemcpy");
+    }
+    b.base = d;
+    b.device_bytes = img.bytes.size();
+    return WV_OK;
+}
+
+bool lookup(uint64_t h, DevBlob& out) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    auto it = g_blobs.find(h);
+    if (it == g_blobs.end()) return false;
+    out = it->second;
+    return true;
+}
+
+bool supported_format(int fmt) {
+    return (fmt >= FMT_Q8_0 && fmt <= FMT_BINARY) || fmt == FMT_NATIVE_TERNARY;
+}
+
+const char* fmt_name(int f) {
+    static const char* names[] = {"none", "Q8_0", "Q4_0", "Q4_1", "Q5_0", "Q5_1", "Q2_K", "Q3_K",
+                                  "Q4_K", "Q5_K", "Q6_K", "IQ1_S", "IQ2_XXS", "IQ2_XS", "IQ3_XXS",
+                                  "IQ3_S", "IQ4_NL", "IQ4_XS", "TernaryPacked", "BinaryPacked", "AffinePacked"};
+    if (f >= 0 && f <= 20) return names[f];
+    if (f == FMT_NATIVE_TERNARY) return "native-ternary";
+    return "unknown";
+}
+
+// Raw bytes a blob must hold (quant.Pack sizes), or -1 if the format cannot
+// be sized from (rows, cols) alone.
+int64_t need_raw(int fmt, int64_t rows, int64_t cols, int32_t bw, const uint8_t* meta, size_t n_meta,
+                 int64_t* need_scales) {
+    const int64_t n = rows * cols;
+    *need_scales = 0;
+    if (fmt == FMT_NATIVE_TERNARY) return (n + 3) / 4;
+    if (fmt == FMT_BINARY && bw == 128) {
+        if (cols % 128 != 0) return -1;
+        *need_scales = rows * (cols / 128);
+        return rows * (cols / 32) * 4;
+    }
+    IQSpec is;
+    if (iq_spec(fmt, is)) {
+        if (n_meta >= 2) { is.bits = meta[0]; is.sg = meta[1]; }
+        if (is.bits <= 0 || is.bits > 8 || is.sg <= 0) return -1;
+        const int64_t padn = (n + is.sg - 1) / is.sg * is.sg;
+        *need_scales = padn / is.sg;
+        return (padn * is.bits + 7) / 8;
+    }
+    PackSizes ps;
+    if (!pack_sizes(fmt, rows, cols, ps)) return -1;
+    *need_scales = ps.scales;
+    return ps.raw;
+}
+
+}  // namespace
+}  // namespace wv
+
+using namespace wv;
+
+extern "C" {
+
+int wv_init(int device) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    return ensure_device_locked(device);
+}
+
+const char* wv_last_error(void) { return g_err.c_str(); }
+
+const char* wv_version(void) { return "welvet_hip 0.1 gfx950"; }
+
+int wv_pack_sizes(int format, int64_t rows, int64_t cols, size_t* raw_len, size_t* n_scales, size_t* n_mins,
+                  size_t* n_meta, int32_t* block_weights) {
+    PackSizes ps;
+    if (rows <= 0 || cols <= 0) return fail(WV_E_SHAPE, "PackSizes: bad shape rows=%lld cols=%lld", (long long)rows, (long long)cols);
+    if (!pack_sizes(format, rows, cols, ps))
+        return fail(WV_E_FORMAT, "quant: Pack not implemented for %s (native path TBD — no QAT fallback)", fmt_name(format));
+    if (raw_len) *raw_len = size_t(ps.raw);
+    if (n_scales) *n_scales = size_t(ps.scales);
+    if (n_mins) *n_mins = size_t(ps.mins);
+    if (n_meta) *n_meta = size_t(ps.meta);
+    if (block_weights) *block_weights = ps.block_weights;
+    return WV_OK;
+}
+
+int wv_pack(int format, const float* weights, int64_t rows, int64_t cols, uint8_t* raw, float* scales, float* mins,
+            uint8_t* meta) {
+    (void)mins;
+    PackSizes ps;
+    if (!weights || !raw) return fail(WV_E_ARG, "Pack: nil buffer");
+    if (rows <= 0 || cols <= 0) return fail(WV_E_SHAPE, "Pack: bad shape rows=%lld cols=%lld len=0", (long long)rows, (long long)cols);
+    if (!pack_sizes(format, rows, cols, ps))
+        return fail(WV_E_FORMAT, "quant: Pack not implemented for %s (native path TBD — no QAT fallback)", fmt_name(format));
+    if ((ps.scales && !scales) || (ps.meta && !meta)) return fail(WV_E_ARG, "Pack: %s needs scales/meta buffers", fmt_name(format));
+    if (!pack(format, weights, rows, cols, raw, scales, meta)) return fail(WV_E_FORMAT, "Pack: %s failed", fmt_name(format));
+    return WV_OK;
+}
+
+int wv_pack_native_ternary(const float* weights, int64_t n, uint8_t* codes, float* scale) {
+    if (!weights || !codes || !scale) return fail(WV_E_ARG, "packTernary: nil buffer");
+    if (n <= 0) return fail(WV_E_SHAPE, "packTernary: empty tensor");
+    pack_native_ternary(weights, n, codes, scale);
+    return WV_OK;
+}
+
+int wv_blob_upload(int format, int64_t rows, int64_t cols, int32_t block_weights, const uint8_t* raw, size_t raw_len,
+                   const float* scales, size_t n_scales, const float* mins, size_t n_mins, const uint8_t* meta,
+                   size_t n_meta, float tensor_scale, uint64_t* handle) {
+    (void)mins;
+    (void)n_mins;
+    if (!handle || !raw) return fail(WV_E_ARG, "wv_blob_upload: nil blob");
+    if (rows <= 0 || cols <= 0)
+        return fail(WV_E_SHAPE, "wv_blob_upload: bad shape rows=%lld cols=%lld", (long long)rows, (long long)cols);
+    if (!supported_format(format))
+        return fail(WV_E_FORMAT, "quant: MatVec not implemented for %s (native path TBD — no QAT fallback)", fmt_name(format));
+    int64_t need_sc = 0;
+    const int64_t need = need_raw(format, rows, cols, block_weights, meta, n_meta, &need_sc);
+    if (need < 0) return fail(WV_E_SHAPE, "wv_blob_upload: %s cannot hold rows=%lld cols=%lld", fmt_name(format), (long long)rows, (long long)cols);
+    if (int64_t(raw_len) < need)
+        return fail(WV_E_SHAPE, "wv_blob_upload: %s raw short: %zu bytes, need %lld", fmt_name(format), raw_len, (long long)need);
+    if (need_sc > 0 && (!scales || int64_t(n_scales) < need_sc)) {
+        // The reference substitutes scale 1 for missing ternary/binary scales
+        // (ternary.go:69-72); IQ needs every scale (iq.go:193-195).
+        if (format != FMT_TERNARY && format != FMT_BINARY)
+            return fail(WV_E_SHAPE, "wv_blob_upload: %s needs %lld scales, got %zu", fmt_name(format), (long long)need_sc, n_scales);
+    }
+    int rc = ensure_init();
+    if (rc) return rc;
+
+    DevBlob b;
+    b.fmt = format;
+    b.rows = rows;
+    b.cols = cols;
+    b.block_weights = block_weights;
+    b.tensor_scale = tensor_scale == 0.0f ? 1.0f : tensor_scale;  // expandNarrowToI8 (simd.go:153-156)
+    b.device = g_current;
+    Image img;
+    const bool raw_only = force_raw();
+    KSpec ks;
+    size_t o_codes = 0, o_hi = 0, o_blk = 0, o_grp = 0, o_raw = 0, o_sc = 0;
+    if (format == FMT_NATIVE_TERNARY) {
+        b.layout = LAYOUT_TERNARY_I8;
+        if (cols > 32768) return fail(WV_E_SHAPE, "wv_blob_upload: native ternary cols %lld > 32768", (long long)cols);
+        o_codes = img.add(size_t(need));
+        std::memcpy(img.bytes.data() + o_codes, raw, size_t(need));
+    } else if (!raw_only && (format == FMT_Q4_K || format == FMT_Q6_K) && cols % 256 == 0 && cols <= 65536 && k_spec(format, ks)) {
+        b.layout = LAYOUT_K_PLANAR;
+        relayout_k(ks, format, raw, rows, cols, img, o_codes, o_hi, o_blk, o_grp);
+    } else if (!raw_only && (format == FMT_Q8_0 || format == FMT_Q4_0) && cols % 32 == 0 && cols <= 65536) {
+        const int64_t nblk = rows * cols / 32;
+        const bool q8 = format == FMT_Q8_0;
+        b.layout = q8 ? LAYOUT_Q8_PLANAR : LAYOUT_Q4_PLANAR;
+        const int bb = q8 ? 36 : 20, cb = q8 ? 32 : 16;
+        o_codes = img.add(size_t(nblk * cb));
+        o_blk = img.add(size_t(nblk * 4));
+        for (int64_t k = 0; k < nblk; ++k) {
+            std::memcpy(img.bytes.data() + o_blk + k * 4, raw + k * bb, 4);
+            std::memcpy(img.bytes.data() + o_codes + k * cb, raw + k * bb + 4, size_t(cb));
+        }
+    } else {
+        b.layout = LAYOUT_RAW;
+        o_raw = img.add(size_t(need));
+        std::memcpy(img.bytes.data() + o_raw, raw, size_t(need));
+        b.raw_len = need;
+        IQSpec is;
+        if (iq_spec(format, is)) {
+            if (n_meta >= 2) { is.bits = meta[0]; is.sg = meta[1]; }
+            b.iq_bits = is.bits;
+            b.iq_sg = is.sg;
+        }
+        if (scales && n_scales) {
+            o_sc = img.add(n_scales * 4);
+            std::memcpy(img.bytes.data() + o_sc, scales, n_scales * 4);
+            b.n_scales = int64_t(n_scales);
+        }
+    }
+    rc = upload_image(img, b);
+    if (rc) return rc;
+    uint8_t* base = static_cast<uint8_t*>(b.base);
+    if (b.layout == LAYOUT_RAW) {
+        b.raw = base + o_raw;
+        b.scales = b.n_scales ? reinterpret_cast<const float*>(base + o_sc) : nullptr;
+    } else {
+        b.codes = base + o_codes;
+        b.codes_hi = o_hi ? base + o_hi : nullptr;
+        b.blk_scale = o_blk ? reinterpret_cast<const float*>(base + o_blk) : nullptr;
+        b.grp = o_grp ? reinterpret_cast<const uint32_t*>(base + o_grp) : nullptr;
+    }
+    std::lock_guard<std::mutex> lk(g_mu);
+    const uint64_t h = g_next++;
+    g_blobs[h] = b;
+    *handle = h;
+    return WV_OK;
+}
+
+int wv_blob_free(uint64_t handle) {
+    DevBlob b;
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        auto it = g_blobs.find(handle);
+        if (it == g_blobs.end()) return fail(WV_E_HANDLE, "wv_blob_free: unknown handle %llu", (unsigned long long)handle);
+        b = it->second;
+        g_blobs.erase(it);
+    }
+    hipSetDevice(b.device);
+    hipError_t e = hipFree(b.base);
+    if (e != hipSuccess) return hip_fail(e, "wv_blob_free: hipFree");
+    return WV_OK;
+}
+
+int wv_blob_info(uint64_t handle, int* format, int64_t* rows, int64_t* cols, size_t* device_bytes, int* layout) {
+    DevBlob b;
+    if (!lookup(handle, b)) return fail(WV_E_HANDLE, "wv_blob_info: unknown handle %llu", (unsigned long long)handle);
+    if (format) *format = b.fmt;
+    if (rows) *rows = b.rows;
+    if (cols) *cols = b.cols;
+    if (device_bytes) *device_bytes = b.device_bytes;
+    if (layout) *layout = b.layout;
+    return WV_OK;
+}
+
+int wv_matvec_dev(uint64_t handle, const float* d_x, float* d_y, int32_t batch, void* stream) {
+    DevBlob b;
+    if (!lookup(handle, b)) return fail(WV_E_HANDLE, "MatVec: unknown handle %llu", (unsigned long long)handle);
+    if (!d_x || !d_y) return fail(WV_E_ARG, "MatVec: nil x/y");
+    if (batch < 0) return fail(WV_E_SHAPE, "MatVec: negative batch %d", batch);
+    hipSetDevice(b.device);
+    const int e = launch_matvec(b, d_x, d_y, batch, stream_or_default(stream, b.device));
+    if (e != hipSuccess) return hip_fail(hipError_t(e), "MatVec: kernel launch");
+    return WV_OK;
+}
+
+int wv_ternary_acc_dev(uint64_t handle, const float* d_x, int32_t* d_acc, float* d_act_scale, int32_t batch, void* stream) {
+    DevBlob b;
+    if (!lookup(handle, b)) return fail(WV_E_HANDLE, "ternary acc: unknown handle %llu", (unsigned long long)handle);
+    if (b.layout != LAYOUT_TERNARY_I8) return fail(WV_E_FORMAT, "ternary acc: blob is %s, not native ternary", fmt_name(b.fmt));
+    if (!d_x || !d_acc) return fail(WV_E_ARG, "ternary acc: nil x/acc");
+    hipSetDevice(b.device);
+    const int e = launch_ternary_acc(b, d_x, d_acc, d_act_scale, batch, stream_or_default(stream, b.device));
+    if (e != hipSuccess) return hip_fail(hipError_t(e), "ternary acc: kernel launch");
+    return WV_OK;
+}
+
+int wv_matvec_t_dev(uint64_t handle, const float* d_gy, float* d_gx, int32_t batch, void* stream) {
+    DevBlob b;
+    if (!lookup(handle, b)) return fail(WV_E_HANDLE, "MatVecT: unknown handle %llu", (unsigned long long)handle);
+    if (!d_gy || !d_gx) return fail(WV_E_ARG, "MatVecT: nil gy/gx");
+    if (b.layout != LAYOUT_RAW)
+        return fail(WV_E_FORMAT, "quant: MatVecT not implemented on the resident %s layout (upload with WV_FORCE_RAW=1)", fmt_name(b.fmt));
+    hipSetDevice(b.device);
+    hipStream_t s = stream_or_default(stream, b.device);
+    float* part = nullptr;
+    const size_t nf = matvec_t_scratch_floats(b, batch);
+    hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&part), std::max<size_t>(nf, 1) * sizeof(float), s);
+    if (e != hipSuccess) return hip_fail(e, "MatVecT: scratch");
+    const int k = launch_matvec_t(b, d_gy, d_gx, batch, s, part);
+    hipFreeAsync(part, s);
+    if (k != hipSuccess) return hip_fail(hipError_t(k), "MatVecT: kernel launch");
+    return WV_OK;
+}
+
+int wv_matvec(uint64_t handle, const float* x, float* y, int32_t batch) {
+    DevBlob b;
+    if (!lookup(handle, b)) return fail(WV_E_HANDLE, "MatVec: unknown handle %llu", (unsigned long long)handle);
+    if (!x || !y) return fail(WV_E_ARG, "MatVec: nil x/y");
+    if (batch <= 0) return WV_OK;
+    hipSetDevice(b.device);
+    hipStream_t s = g_dev[b.device].stream;
+    const size_t nx = size_t(batch) * size_t(b.cols), ny = size_t(batch) * size_t(b.rows);
+    float *dx = nullptr, *dy = nullptr;
+    hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&dx), nx * 4, s);
+    if (e == hipSuccess) e = hipMallocAsync(reinterpret_cast<void**>(&dy), ny * 4, s);
+    if (e != hipSuccess) return hip_fail(e, "MatVec: staging");
+    e = hipMemcpyAsync(dx, x, nx * 4, hipMemcpyHostToDevice, s);
+    int rc = WV_OK;
+    if (e != hipSuccess) rc = hip_fail(e, "MatVec: copy x");
+    if (!rc) {
+        const int k = launch_matvec(b, dx, dy, batch, s);
+        if (k != hipSuccess) rc = hip_fail(hipError_t(k), "MatVec: kernel launch");
+    }
+    if (!rc) {
+        e = hipMemcpyAsync(y, dy, ny * 4, hipMemcpyDeviceToHost, s);
+        if (e != hipSuccess) rc = hip_fail(e, "MatVec: copy y");
+    }
+    hipFreeAsync(dx, s);
+    hipFreeAsync(dy, s);
+    e = hipStreamSynchronize(s);
+    if (!rc && e != hipSuccess) rc = hip_fail(e, "MatVec: sync");
+    return rc;
+}
+
+int wv_matvec_t(uint64_t handle, const float* gy, float* gx, int32_t batch) {
+    DevBlob b;
+    if (!lookup(handle, b)) return fail(WV_E_HANDLE, "MatVecT: unknown handle %llu", (unsigned long long)handle);
+    if (!gy || !gx) return fail(WV_E_ARG, "MatVecT: nil gy/gx");
+    if (batch <= 0) return WV_OK;
+    hipSetDevice(b.device);
+    hipStream_t s = g_dev[b.device].stream;
+    const size_t ng = size_t(batch) * size_t(b.rows), nx = size_t(batch) * size_t(b.cols);
+    float *dg = nullptr, *dx = nullptr;
+    hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&dg), ng * 4, s);
+    if (e == hipSuccess) e = hipMallocAsync(reinterpret_cast<void**>(&dx), nx * 4, s);
+    if (e != hipSuccess) return hip_fail(e, "MatVecT: staging");
+    int rc = WV_OK;
+    e = hipMemcpyAsync(dg, gy, ng * 4, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) e = hipMemcpyAsync(dx, gx, nx * 4, hipMemcpyHostToDevice, s);
+    if (e != hipSuccess) rc = hip_fail(e, "MatVecT: copy in");
+    if (!rc) rc = wv_matvec_t_dev(handle, dg, dx, batch, s);
+    if (!rc) {
+        e = hipMemcpyAsync(gx, dx, nx * 4, hipMemcpyDeviceToHost, s);
+        if (e != hipSuccess) rc = hip_fail(e, "MatVecT: copy out");
+    }
+    hipFreeAsync(dg, s);
+    hipFreeAsync(dx, s);
+    e = hipStreamSynchronize(s);
+    if (!rc && e != hipSuccess) rc = hip_fail(e, "MatVecT: sync");
+    return rc;
+}
+
+int wv_sync(void* stream) {
+    int rc = ensure_init();
+    if (rc) return rc;
+    hipError_t e = hipStreamSynchronize(stream_or_default(stream, g_current));
+    if (e != hipSuccess) return hip_fail(e, "wv_sync");
+    return WV_OK;
+}
+
+}  // extern "C"
