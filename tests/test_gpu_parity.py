@@ -18,7 +18,7 @@ TOL = 1e-5
 ALL = ["Q4_0", "Q8_0", "Q4_1", "Q5_0", "Q5_1", "Q2_K", "Q3_K", "Q4_K", "Q5_K", "Q6_K",
        "IQ1_S", "IQ2_XXS", "IQ2_XS", "IQ3_XXS", "IQ3_S", "IQ4_NL", "IQ4_XS",
        "TernaryPacked", "BinaryPacked"]
-PLANAR = {"Q4_K": "k-planar", "Q6_K": "k-planar", "Q8_0": "q8-planar", "Q4_0": "q4-planar"}
+PLANAR = {"Q4_K": "row-interleaved", "Q6_K": "row-interleaved", "Q8_0": "row-interleaved", "Q4_0": "row-interleaved"}
 
 
 @pytest.fixture(scope="module", autouse=True)
@@ -82,7 +82,9 @@ def test_planar_and_raw_layouts_agree(fmt):
     _, dr = upload(fmt, w, rows, cols, force_raw=True)
     assert dp.info()["layout"] == PLANAR[fmt]
     assert dr.info()["layout"] == "raw"
-    assert dp.info()["device_bytes"] <= p.nbytes + 4096  # same bytes as the reference blob (+ alignment)
+    # same bytes as the reference blob, for rows padded to the 64-row group (+ section alignment)
+    padded_rows = -(-rows // 64) * 64
+    assert p.nbytes <= dp.info()["device_bytes"] <= p.nbytes * padded_rows // rows + 4 * 256
     ref = oracle.reference_y(oracle_packed(p), x)[0]
     assert normwise(dp.matvec(x), ref) <= TOL
     assert normwise(dr.matvec(x), ref) <= TOL
@@ -99,6 +101,21 @@ def test_baseline_shapes(fmt, shape):
     ref = oracle.reference_y(oracle_packed(p), x)[0]
     assert normwise(d.matvec(x), ref) <= TOL
     d.free()
+
+
+@pytest.mark.parametrize("fmt", sorted(PLANAR))
+@pytest.mark.parametrize("shape,batch", [((1000, 2048), 11), ((130, 4096), 2), ((64, 256), 1)])
+def test_row_interleaved_split_and_batch(fmt, shape, batch):
+    """K split across blocks (last-block reduction), batch beyond one split launch."""
+    rows, cols = shape
+    print(f"[gpu] rpl split {fmt} {cols}->{rows} batch {batch}", flush=True)
+    w, rng = weights(rows, cols, 17)
+    x = rng.standard_normal((batch, cols)).astype(np.float32)
+    p, d = upload(fmt, w, rows, cols)
+    assert d.info()["layout"] == "row-interleaved"
+    ref = oracle.reference_y(oracle_packed(p), x)
+    for _ in range(2):  # the arrival tickets must be back at zero for the next launch
+        assert normwise(d.matvec(x), ref) <= TOL
 
 
 def test_q4_0_baseline_4096():

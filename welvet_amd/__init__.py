@@ -24,7 +24,7 @@ FORMATS = {
     "NativeTernary": 1019,
 }
 FORMAT_NAMES = {v: k for k, v in FORMATS.items()}
-LAYOUTS = {0: "raw", 1: "k-planar", 2: "q8-planar", 3: "q4-planar", 4: "ternary-i8"}
+LAYOUTS = {0: "raw", 1: "row-interleaved", 4: "ternary-i8"}
 
 WV_E = {-1: "ARG", -2: "SHAPE", -3: "FORMAT", -4: "OOM", -5: "HIP", -6: "NODEV", -7: "HANDLE"}
 

@@ -5,13 +5,8 @@
 //     (LAYOUT_RAW). Any format, any shape, including blocks that straddle rows.
 //     Semantics follow the reference decoders element by element
 //     (quant/*.go forEach* / unpack*), accumulating in f32.
-//   * k_gemv_planar<Policy>: batch-1 decode GEMV on re-laid-out planes
-//     (codes plane + scale planes, same byte count as the reference blob).
-//     Each lane owns fixed 32-column chunks and keeps that slice of x in
-//     VGPRs for the whole launch; waves walk rows, loading 16 B of codes per
-//     lane per chunk (coalesced: the 64 lanes of a load read 1 KiB
-//     contiguous), unpacking nibbles in registers and reducing row partials
-//     with cross-lane shuffles plus LDS when K is split across waves.
+//   * the row-interleaved fast path for Q4_K/Q6_K/Q8_0/Q4_0 lives in
+//     gemv_rpl.hip;
 //   * k_ternary_i8: the DTypeTernary int8 path (layers/dense/simd.go:130-147):
 //     activations absmax-quantized to int8 in LDS, codes unpacked to bytes in
 //     registers and multiplied with packed-dot v_dot4_i32_i8; exact int32.
@@ -19,6 +14,7 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <cstdlib>
 
 #include "wv_internal.h"
 
@@ -194,217 +190,6 @@ __global__ void __launch_bounds__(256) k_gemvt_reduce(const float* __restrict__ 
 }
 
 // ---------------------------------------------------------------------------
-// planar kernels
-// ---------------------------------------------------------------------------
-
-__device__ __forceinline__ float ub0(uint32_t v) { return float(v & 0xFFu); }
-__device__ __forceinline__ float ub1(uint32_t v) { return float((v >> 8) & 0xFFu); }
-__device__ __forceinline__ float ub2(uint32_t v) { return float((v >> 16) & 0xFFu); }
-__device__ __forceinline__ float ub3(uint32_t v) { return float(v >> 24); }
-
-// sum_k q_k x[k] for 8 unsigned 4-bit codes of one word (code k = nibble k).
-__device__ __forceinline__ float dot8_u4(uint32_t w, const float* x) {
-    const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
-    float a = ub0(lo) * x[0];
-    a = fmaf(ub0(hi), x[1], a);
-    a = fmaf(ub1(lo), x[2], a);
-    a = fmaf(ub1(hi), x[3], a);
-    a = fmaf(ub2(lo), x[4], a);
-    a = fmaf(ub2(hi), x[5], a);
-    a = fmaf(ub3(lo), x[6], a);
-    a = fmaf(ub3(hi), x[7], a);
-    return a;
-}
-// sum_k q_k x[k] for 4 unsigned byte codes.
-__device__ __forceinline__ float dot4_u8(uint32_t w, const float* x) {
-    float a = ub0(w) * x[0];
-    a = fmaf(ub1(w), x[1], a);
-    a = fmaf(ub2(w), x[2], a);
-    a = fmaf(ub3(w), x[3], a);
-    return a;
-}
-
-struct PlanarArgs {
-    const uint8_t* codes;    // row-major code plane
-    const uint8_t* codes_hi; // Q6_K: 2-bit high plane
-    const float* blk;        // k: (d, dmin) per super-block; Q8_0/Q4_0: scale per block
-    const uint32_t* grp;     // k: per-chunk (u0, u1, m0, m1); Q6_K reads u16 pairs
-    int64_t nchunks;         // K / 32
-};
-
-// Q4_K: chunk = 32 columns = groups (2p, 2p+1) of super-block jc/8.
-// w = dmin*m/127 + (d*u/255)*q  (quant/kquant.go:178-188).
-struct PolQ4K {
-    struct Raw { uint4 c; float2 dd; uint32_t g; };
-    static __device__ __forceinline__ Raw load(const PlanarArgs& a, int64_t row, int64_t jc) {
-        Raw r;
-        const int64_t ci = row * a.nchunks + jc;
-        r.c = *reinterpret_cast<const uint4*>(a.codes + ci * 16);
-        r.dd = reinterpret_cast<const float2*>(a.blk)[ci >> 3];
-        r.g = a.grp[ci];
-        return r;
-    }
-    static __device__ __forceinline__ float dot(const Raw& r, const float* x, float sx0, float sx1) {
-        const float a0 = dot8_u4(r.c.x, x) + dot8_u4(r.c.y, x + 8);
-        const float a1 = dot8_u4(r.c.z, x + 16) + dot8_u4(r.c.w, x + 24);
-        const float d255 = r.dd.x * (1.0f / 255.0f), dm127 = r.dd.y * (1.0f / 127.0f);
-        const float m0 = float(int8_t(r.g >> 16)), m1 = float(int32_t(r.g) >> 24);
-        return d255 * fmaf(ub1(r.g), a1, ub0(r.g) * a0) + dm127 * fmaf(m1, sx1, m0 * sx0);
-    }
-};
-
-// Q6_K: q = lo4 | hi2 << 4, w = (d*u/255)*(q-32).
-// hi plane per chunk: dword t, byte b, bits 2f..2f+1 hold the high bits of the
-// weight in byte b of spread word s = 4t+f (s = 2*word + nibble half).
-struct PolQ6K {
-    struct Raw { uint4 c; uint2 h; float d; uint32_t g; };
-    static __device__ __forceinline__ Raw load(const PlanarArgs& a, int64_t row, int64_t jc) {
-        Raw r;
-        const int64_t ci = row * a.nchunks + jc;
-        r.c = *reinterpret_cast<const uint4*>(a.codes + ci * 16);
-        r.h = *reinterpret_cast<const uint2*>(a.codes_hi + ci * 8);
-        r.d = a.blk[(ci >> 3) * 2];
-        r.g = reinterpret_cast<const uint16_t*>(a.grp)[ci];
-        return r;
-    }
-    static __device__ __forceinline__ float dot_word(uint32_t w, uint32_t h, int f0, const float* x) {
-        const uint32_t lo = (w & 0x0F0F0F0Fu) | (((h >> (2 * f0)) & 0x03030303u) << 4);
-        const uint32_t hi = ((w >> 4) & 0x0F0F0F0Fu) | (((h >> (2 * f0 + 2)) & 0x03030303u) << 4);
-        float a = ub0(lo) * x[0];
-        a = fmaf(ub0(hi), x[1], a);
-        a = fmaf(ub1(lo), x[2], a);
-        a = fmaf(ub1(hi), x[3], a);
-        a = fmaf(ub2(lo), x[4], a);
-        a = fmaf(ub2(hi), x[5], a);
-        a = fmaf(ub3(lo), x[6], a);
-        a = fmaf(ub3(hi), x[7], a);
-        return a;
-    }
-    static __device__ __forceinline__ float dot(const Raw& r, const float* x, float sx0, float sx1) {
-        const float a0 = dot_word(r.c.x, r.h.x, 0, x) + dot_word(r.c.y, r.h.x, 2, x + 8);
-        const float a1 = dot_word(r.c.z, r.h.y, 0, x + 16) + dot_word(r.c.w, r.h.y, 2, x + 24);
-        const float d255 = r.d * (1.0f / 255.0f);
-        return d255 * fmaf(ub1(r.g), fmaf(-32.0f, sx1, a1), ub0(r.g) * fmaf(-32.0f, sx0, a0));
-    }
-};
-
-// Q8_0: 32 int8 codes + f32 scale per block; codes biased by 128 so that the
-// byte converts unsigned: sum x*q = sum x*(q+128) - 128*sum x.
-struct PolQ8 {
-    struct Raw { uint4 c0, c1; float s; };
-    static __device__ __forceinline__ Raw load(const PlanarArgs& a, int64_t row, int64_t jc) {
-        Raw r;
-        const int64_t ci = row * a.nchunks + jc;
-        const uint4* p = reinterpret_cast<const uint4*>(a.codes + ci * 32);
-        r.c0 = p[0];
-        r.c1 = p[1];
-        r.s = a.blk[ci];
-        return r;
-    }
-    static __device__ __forceinline__ float dot(const Raw& r, const float* x, float sx0, float sx1) {
-        const uint32_t B = 0x80808080u;
-        float a = dot4_u8(r.c0.x ^ B, x) + dot4_u8(r.c0.y ^ B, x + 4);
-        a += dot4_u8(r.c0.z ^ B, x + 8) + dot4_u8(r.c0.w ^ B, x + 12);
-        a += dot4_u8(r.c1.x ^ B, x + 16) + dot4_u8(r.c1.y ^ B, x + 20);
-        a += dot4_u8(r.c1.z ^ B, x + 24) + dot4_u8(r.c1.w ^ B, x + 28);
-        return r.s * fmaf(-128.0f, sx0 + sx1, a);
-    }
-};
-
-// Q4_0: signed nibble q in [-8,7] stored two's-complement; q ^ 8 = q + 8.
-struct PolQ4 {
-    struct Raw { uint4 c; float s; };
-    static __device__ __forceinline__ Raw load(const PlanarArgs& a, int64_t row, int64_t jc) {
-        Raw r;
-        const int64_t ci = row * a.nchunks + jc;
-        r.c = *reinterpret_cast<const uint4*>(a.codes + ci * 16);
-        r.s = a.blk[ci];
-        return r;
-    }
-    static __device__ __forceinline__ float dot(const Raw& r, const float* x, float sx0, float sx1) {
-        const uint32_t B = 0x88888888u;
-        float a = dot8_u4(r.c.x ^ B, x) + dot8_u4(r.c.y ^ B, x + 8);
-        a += dot8_u4(r.c.z ^ B, x + 16) + dot8_u4(r.c.w ^ B, x + 24);
-        return r.s * fmaf(-8.0f, sx0 + sx1, a);
-    }
-};
-
-// Launch geometry: block = KW*RW waves. Wave (kw, rw) owns chunks
-// jc = (i*KW + kw)*64 + lane, i < CPL, of every row in its row range.
-template <class P, int CPL, int U>
-__global__ void __launch_bounds__(512) k_gemv_planar(PlanarArgs a, const float* __restrict__ x, float* __restrict__ y,
-                                                    int rows, int KW, int RPW) {
-    extern __shared__ float part[];  // [RW*RPW][KW]
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int kw = wave % KW, rw = wave / KW;
-    const int RW = (blockDim.x >> 6) / KW;
-    const int b = blockIdx.y;
-    const float* xb = x + int64_t(b) * a.nchunks * 32;
-    float* yb = y + int64_t(b) * rows;
-
-    float xr[CPL][32];
-    float sx[CPL][2];
-    int64_t jcs[CPL];
-    bool ok[CPL];
-#pragma unroll
-    for (int i = 0; i < CPL; ++i) {
-        jcs[i] = int64_t(i * KW + kw) * kWave + lane;
-        ok[i] = jcs[i] < a.nchunks;
-        const float4* xp = reinterpret_cast<const float4*>(xb + (ok[i] ? jcs[i] : 0) * 32);
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            float4 v = ok[i] ? xp[k] : make_float4(0.f, 0.f, 0.f, 0.f);
-            xr[i][4 * k] = v.x;
-            xr[i][4 * k + 1] = v.y;
-            xr[i][4 * k + 2] = v.z;
-            xr[i][4 * k + 3] = v.w;
-        }
-        float s0 = 0.f, s1 = 0.f;
-#pragma unroll
-        for (int k = 0; k < 16; ++k) {
-            s0 += xr[i][k];
-            s1 += xr[i][16 + k];
-        }
-        sx[i][0] = s0;
-        sx[i][1] = s1;
-    }
-
-    const int wg_rows = RW * RPW;
-    const int row0 = blockIdx.x * wg_rows + rw * RPW;
-    const int row1 = min(rows, row0 + RPW);
-    for (int r = row0; r < row1; r += U) {
-        typename P::Raw raw[U][CPL];
-#pragma unroll
-        for (int u = 0; u < U; ++u)
-#pragma unroll
-            for (int i = 0; i < CPL; ++i)
-                if (r + u < row1 && ok[i]) raw[u][i] = P::load(a, r + u, jcs[i]);
-        float acc[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            acc[u] = 0.f;
-#pragma unroll
-            for (int i = 0; i < CPL; ++i)
-                if (r + u < row1 && ok[i]) acc[u] += P::dot(raw[u][i], xr[i], sx[i][0], sx[i][1]);
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            float s = wave_sum(acc[u]);
-            if (lane == 0 && r + u < row1) part[(r + u - blockIdx.x * wg_rows) * KW + kw] = s;
-        }
-    }
-    __syncthreads();
-    for (int t = threadIdx.x; t < wg_rows; t += blockDim.x) {
-        const int row = blockIdx.x * wg_rows + t;
-        if (row < rows) {
-            float s = 0.f;
-            for (int k = 0; k < KW; ++k) s += part[t * KW + k];
-            yb[row] = s;
-        }
-    }
-}
-
-// ---------------------------------------------------------------------------
 // DTypeTernary int8 path
 // ---------------------------------------------------------------------------
 
@@ -517,9 +302,6 @@ int launch_raw_t(const DevBlob& b, const float* gy, float* gx, int batch, hipStr
 using RawFn = int (*)(const DevBlob&, const float*, float*, int, hipStream_t);
 using RawTFn = int (*)(const DevBlob&, const float*, float*, int, hipStream_t, float*, int);
 
-template <int F>
-constexpr RawFn raw_fn() { return &launch_raw<F>; }
-
 RawFn pick_raw(int fmt) {
     switch (fmt) {
     case FMT_Q4_0: return launch_raw<FMT_Q4_0>;
@@ -569,46 +351,6 @@ RawTFn pick_raw_t(int fmt) {
     }
 }
 
-PlanarArgs planar_args(const DevBlob& b) {
-    PlanarArgs a;
-    a.codes = b.codes;
-    a.codes_hi = b.codes_hi;
-    a.blk = b.blk_scale;
-    a.grp = b.grp;
-    a.nchunks = b.cols / 32;
-    return a;
-}
-
-// Chooses chunks-per-lane (CPL) and waves splitting K (KW) so a row's chunks
-// are covered, then rows-per-wave so the grid holds ~16 waves per CU.
-template <class P>
-int launch_planar(const DevBlob& b, const float* x, float* y, int batch, hipStream_t s) {
-    const int64_t nch = b.cols / 32;
-    int cpl, kw;
-    if (nch <= 64) { cpl = 1; kw = 1; }
-    else if (nch <= 128) { cpl = 2; kw = 1; }
-    else if (nch <= 64 * 8) { cpl = 1; kw = int((nch + 63) / 64); }
-    else if (nch <= 128 * 8) { cpl = 2; kw = int((nch + 127) / 128); }
-    else if (nch <= 256 * 8) { cpl = 4; kw = int((nch + 255) / 256); }
-    else return int(hipErrorInvalidValue);
-    const int rw = std::max(1, 4 / kw);
-    const int64_t target_waves = 256 * 16;
-    int64_t rpw = (b.rows * kw + target_waves - 1) / target_waves;
-    rpw = std::max<int64_t>(1, std::min<int64_t>(rpw, 64));
-    const int64_t wg_rows = rw * rpw;
-    dim3 grid(unsigned((b.rows + wg_rows - 1) / wg_rows), unsigned(batch));
-    dim3 block(unsigned(64 * kw * rw));
-    const size_t lds = size_t(wg_rows * kw) * sizeof(float);
-    const PlanarArgs a = planar_args(b);
-    const int R = int(b.rows), RPW = int(rpw);
-    switch (cpl) {
-    case 1: hipLaunchKernelGGL((k_gemv_planar<P, 1, 4>), grid, block, lds, s, a, x, y, R, kw, RPW); break;
-    case 2: hipLaunchKernelGGL((k_gemv_planar<P, 2, 4>), grid, block, lds, s, a, x, y, R, kw, RPW); break;
-    default: hipLaunchKernelGGL((k_gemv_planar<P, 4, 2>), grid, block, lds, s, a, x, y, R, kw, RPW); break;
-    }
-    return int(hipGetLastError());
-}
-
 int launch_ternary(const DevBlob& b, const float* x, float* y, int32_t* acc, float* act, int batch, hipStream_t s) {
     const int rows = int(b.rows), K = int(b.cols);
     const int rpb = 16;
@@ -624,12 +366,7 @@ int launch_matvec(const DevBlob& b, const float* d_x, float* d_y, int batch, voi
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (b.rows == 0 || batch == 0) return 0;
     switch (b.layout) {
-    case LAYOUT_K_PLANAR:
-        if (b.fmt == FMT_Q4_K) return launch_planar<PolQ4K>(b, d_x, d_y, batch, s);
-        if (b.fmt == FMT_Q6_K) return launch_planar<PolQ6K>(b, d_x, d_y, batch, s);
-        return int(hipErrorInvalidValue);
-    case LAYOUT_Q8_PLANAR: return launch_planar<PolQ8>(b, d_x, d_y, batch, s);
-    case LAYOUT_Q4_PLANAR: return launch_planar<PolQ4>(b, d_x, d_y, batch, s);
+    case LAYOUT_RPL: return launch_rpl(b, d_x, d_y, batch, s);
     case LAYOUT_TERNARY_I8: return launch_ternary(b, d_x, d_y, nullptr, nullptr, batch, s);
     default: {
         RawFn f = pick_raw(b.fmt);

@@ -1,0 +1,443 @@
+// gemv_rpl.hip — batch-1 dequant-GEMV on the row-interleaved ("one lane per
+// output row") device layout, for Q4_K, Q6_K, Q8_0 and Q4_0.
+//
+// Layout (built at upload, same byte count as the reference blob): rows are
+// taken 64 at a time (a row group = the 64 lanes of a wave); the codes of a
+// 32-column chunk are stored lane-interleaved so the 64 lanes of one load read
+// 1 KiB contiguous, and chunk-step-major, [j][rg][sb][lane][16 B] with j the
+// chunk's index inside its 256-column super-block: waves step through j in
+// lock-step order, so at any time the GPU as a whole streams one contiguous
+// window of the plane (DRAM-page friendly) instead of thousands of scattered
+// 8 KiB runs. Per-super-block metadata is [rg][sb][lane][...].
+//
+// Work split: wave = (row group, super-block): 64 rows x 256 columns, i.e. 8
+// chunks of 16 B per lane. A block holds W waves = W consecutive super-blocks
+// of one row group; gridDim.y = ceil(nsb / W) blocks split K. Each wave keeps
+// D chunks in flight (ring prefetch): issuing a whole slice at once makes every
+// wave wait for its first chunk until late in the launch, because vector loads
+// retire in issue order; a shallow ring keeps arrival and compute interleaved.
+// Each wave stages its 256 x values in its own LDS slice (one float4 per
+// lane, loaded ahead of the weights) and reads them back as wave-wide
+// broadcasts. Partial row sums of the W waves meet in LDS; when K is split
+// across blocks, each block writes its partial to a per-blob scratch row and
+// the last block of a row group (agent-scope atomic ticket) adds the partials
+// in split order, so the result does not depend on arrival order.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+#include <cstdlib>
+
+#include "wv_internal.h"
+
+namespace wv {
+namespace {
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+// Streaming (non-temporal) loads: weights are read once per launch.
+__device__ __forceinline__ uint4 ld_stream(const uint4* p) {
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint2 ld_stream(const uint2* p) {
+    const u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
+    return make_uint2(v.x, v.y);
+}
+
+__device__ __forceinline__ float ub0(uint32_t v) { return float(v & 0xFFu); }
+__device__ __forceinline__ float ub1(uint32_t v) { return float((v >> 8) & 0xFFu); }
+__device__ __forceinline__ float ub2(uint32_t v) { return float((v >> 16) & 0xFFu); }
+__device__ __forceinline__ float ub3(uint32_t v) { return float(v >> 24); }
+
+// sum_k q_k x[k] over the 16 unsigned 4-bit codes of two words (code k of
+// word w = nibble k). The nibbles are spread to bytes first; the asm barrier
+// keeps the compiler from folding the mask into each byte extraction, so
+// every byte converts with a single v_cvt_f32_ubyteN.
+__device__ __forceinline__ float dot16_u4(uint32_t w0, uint32_t w1, const float* x) {
+    uint32_t l0 = w0 & 0x0F0F0F0Fu, h0 = (w0 >> 4) & 0x0F0F0F0Fu;
+    uint32_t l1 = w1 & 0x0F0F0F0Fu, h1 = (w1 >> 4) & 0x0F0F0F0Fu;
+    asm("" : "+v"(l0), "+v"(h0), "+v"(l1), "+v"(h1));
+    float a = ub0(l0) * x[0];
+    a = fmaf(ub0(h0), x[1], a);
+    a = fmaf(ub1(l0), x[2], a);
+    a = fmaf(ub1(h0), x[3], a);
+    a = fmaf(ub2(l0), x[4], a);
+    a = fmaf(ub2(h0), x[5], a);
+    a = fmaf(ub3(l0), x[6], a);
+    a = fmaf(ub3(h0), x[7], a);
+    a = fmaf(ub0(l1), x[8], a);
+    a = fmaf(ub0(h1), x[9], a);
+    a = fmaf(ub1(l1), x[10], a);
+    a = fmaf(ub1(h1), x[11], a);
+    a = fmaf(ub2(l1), x[12], a);
+    a = fmaf(ub2(h1), x[13], a);
+    a = fmaf(ub3(l1), x[14], a);
+    a = fmaf(ub3(h1), x[15], a);
+    return a;
+}
+// sum_k q_k x[k] over 4 unsigned byte codes.
+__device__ __forceinline__ float dot4_u8(uint32_t w, const float* x, float a) {
+    a = fmaf(ub0(w), x[0], a);
+    a = fmaf(ub1(w), x[1], a);
+    a = fmaf(ub2(w), x[2], a);
+    a = fmaf(ub3(w), x[3], a);
+    return a;
+}
+
+// Per-format pieces. Ch = one chunk's codes for one lane; Sb = one
+// super-block's metadata for one lane; dot() = this lane's row partial for
+// chunk j (0..7) of the super-block, given x[32] and the two 16-column sums.
+struct RplQ4K {  // w = dmin*m/127 + (d*u/255)*q  (quant/kquant.go:178-188)
+    static constexpr bool kIntX = false;
+    struct Ch { uint4 c; };
+    struct Sb { uint4 g0, g1; float d255, dm127; };
+    static __device__ __forceinline__ Ch load_ch(const RplArgs& a, int64_t ci, int lane) {
+        return {ld_stream(reinterpret_cast<const uint4*>(a.codes) + ci * 64 + lane)};
+    }
+    static __device__ __forceinline__ Sb load_sb(const RplArgs& a, int64_t si, int lane) {
+        const uint4* m = reinterpret_cast<const uint4*>(a.meta) + (si * 64 + lane) * 2;
+        const float2 dd = reinterpret_cast<const float2*>(a.dd)[si * 64 + lane];
+        return {ld_stream(m), ld_stream(m + 1), dd.x * (1.0f / 255.0f), dd.y * (1.0f / 127.0f)};
+    }
+    static __device__ __forceinline__ float dot(const Ch& ch, const Sb& sb, int j, const float* x, float s0, float s1) {
+        const uint32_t gw[8] = {sb.g0.x, sb.g0.y, sb.g0.z, sb.g0.w, sb.g1.x, sb.g1.y, sb.g1.z, sb.g1.w};
+        const uint32_t g = gw[j];  // (u'0, u'1, m0, m1) bytes
+        const float a0 = dot16_u4(ch.c.x, ch.c.y, x), a1 = dot16_u4(ch.c.z, ch.c.w, x + 16);
+        const float m0 = float(int8_t(g >> 16)), m1 = float(int32_t(g) >> 24);
+        return fmaf(sb.d255, fmaf(ub1(g), a1, ub0(g) * a0), sb.dm127 * fmaf(m1, s1, m0 * s0));
+    }
+};
+
+// Q4_K with x held as 24-bit fixed point (X = round(x * 2^s), s per
+// 32-column chunk, |X| < 2^22) split into three byte planes X = X0 + 2^8 X1 +
+// 2^16 X2 (X0, X1 unsigned, X2 signed). The 4-bit codes multiply the planes
+// with packed-dot v_dot4 instructions; sum_j q_j X_j is exact in int32
+// (|.| < 16*15*2^22 < 2^31) and is converted to f32 once per 16-column group.
+// The fixed-point step adds at most 2^-23 of the chunk's max |x| per element.
+struct RplQ4KI : RplQ4K {
+    static constexpr bool kIntX = true;
+    // xi: 24 dwords [plane][lo w0..3 | hi w0..3], xm = (2^-s/255, sum0, sum1, -128*(sum0+sum1))
+    static __device__ __forceinline__ float dot_i(const Ch& ch, const Sb& sb, int j, const uint32_t* xi, float4 xm) {
+        const uint32_t gw[8] = {sb.g0.x, sb.g0.y, sb.g0.z, sb.g0.w, sb.g1.x, sb.g1.y, sb.g1.z, sb.g1.w};
+        const uint32_t g = gw[j];
+        const uint32_t wd[4] = {ch.c.x, ch.c.y, ch.c.z, ch.c.w};
+        int A[2][3] = {{0, 0, 0}, {0, 0, 0}};
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const int gi = w >> 1;
+            const uint32_t lo = wd[w] & 0x0F0F0F0Fu, hi = (wd[w] >> 4) & 0x0F0F0F0Fu;
+            A[gi][0] = int(__builtin_amdgcn_udot4(lo, xi[w], uint32_t(A[gi][0]), false));
+            A[gi][0] = int(__builtin_amdgcn_udot4(hi, xi[4 + w], uint32_t(A[gi][0]), false));
+            A[gi][1] = int(__builtin_amdgcn_udot4(lo, xi[8 + w], uint32_t(A[gi][1]), false));
+            A[gi][1] = int(__builtin_amdgcn_udot4(hi, xi[12 + w], uint32_t(A[gi][1]), false));
+            A[gi][2] = __builtin_amdgcn_sdot4(int(lo), int(xi[16 + w]), A[gi][2], false);
+            A[gi][2] = __builtin_amdgcn_sdot4(int(hi), int(xi[20 + w]), A[gi][2], false);
+        }
+        const int T0 = A[0][0] + (A[0][1] << 8) + (A[0][2] << 16);
+        const int T1 = A[1][0] + (A[1][1] << 8) + (A[1][2] << 16);
+        // (float)(int8)m = ub(m ^ 0x80) - 128; the -128 terms are folded into xm.w
+        const uint32_t gx = g ^ 0x80800000u;
+        const float mn = fmaf(ub3(gx), xm.z, fmaf(ub2(gx), xm.y, xm.w));
+        const float sc = sb.d255 * 255.0f * xm.x;  // d * 2^-s / 255
+        return fmaf(sc, fmaf(ub1(g), float(T1), ub0(g) * float(T0)), sb.dm127 * mn);
+    }
+};
+
+struct RplQ6K {  // q = lo4 | hi2 << 4, w = (d*u/255)*(q - 32)
+    static constexpr bool kIntX = false;
+    struct Ch { uint4 c; uint2 h; };
+    struct Sb { uint4 g; float d255; };
+    static __device__ __forceinline__ Ch load_ch(const RplArgs& a, int64_t ci, int lane) {
+        return {ld_stream(reinterpret_cast<const uint4*>(a.codes) + ci * 64 + lane),
+                ld_stream(reinterpret_cast<const uint2*>(a.hi) + ci * 64 + lane)};
+    }
+    static __device__ __forceinline__ Sb load_sb(const RplArgs& a, int64_t si, int lane) {
+        return {ld_stream(reinterpret_cast<const uint4*>(a.meta) + si * 64 + lane), reinterpret_cast<const float*>(a.dd)[(si * 64 + lane) * 2] * (1.0f / 255.0f)};
+    }
+    // 8 codes of code word w; the high-bit plane holds, in byte b of dword t,
+    // at bits 2f..2f+1, the top bits of the code in byte b of spread word
+    // s = 4t + f (s = 2*word + nibble half).
+    static __device__ __forceinline__ float dot8(uint32_t w, uint32_t h, int f0, const float* x) {
+        uint32_t lo = (w & 0x0F0F0F0Fu) | (((h >> (2 * f0)) & 0x03030303u) << 4);
+        uint32_t hi = ((w >> 4) & 0x0F0F0F0Fu) | (((h >> (2 * f0 + 2)) & 0x03030303u) << 4);
+        asm("" : "+v"(lo), "+v"(hi));
+        float a = ub0(lo) * x[0];
+        a = fmaf(ub0(hi), x[1], a);
+        a = fmaf(ub1(lo), x[2], a);
+        a = fmaf(ub1(hi), x[3], a);
+        a = fmaf(ub2(lo), x[4], a);
+        a = fmaf(ub2(hi), x[5], a);
+        a = fmaf(ub3(lo), x[6], a);
+        a = fmaf(ub3(hi), x[7], a);
+        return a;
+    }
+    static __device__ __forceinline__ float dot(const Ch& ch, const Sb& sb, int j, const float* x, float s0, float s1) {
+        const uint32_t gw[4] = {sb.g.x, sb.g.y, sb.g.z, sb.g.w};
+        const uint32_t g = gw[j >> 1] >> (16 * (j & 1));  // (u'0, u'1) bytes
+        const float a0 = dot8(ch.c.x, ch.h.x, 0, x) + dot8(ch.c.y, ch.h.x, 2, x + 8);
+        const float a1 = dot8(ch.c.z, ch.h.y, 0, x + 16) + dot8(ch.c.w, ch.h.y, 2, x + 24);
+        return sb.d255 * fmaf(ub1(g), fmaf(-32.0f, s1, a1), ub0(g) * fmaf(-32.0f, s0, a0));
+    }
+};
+
+struct RplQ8 {  // w = scale * q, q int8; q + 128 converts as an unsigned byte
+    static constexpr bool kIntX = false;
+    struct Ch { uint4 c0, c1; };
+    struct Sb { uint4 s0, s1; };
+    static __device__ __forceinline__ Ch load_ch(const RplArgs& a, int64_t ci, int lane) {
+        const uint4* p = reinterpret_cast<const uint4*>(a.codes) + (ci * 64 + lane) * 2;
+        return {ld_stream(p), ld_stream(p + 1)};
+    }
+    static __device__ __forceinline__ Sb load_sb(const RplArgs& a, int64_t si, int lane) {
+        const uint4* m = reinterpret_cast<const uint4*>(a.meta) + (si * 64 + lane) * 2;
+        return {ld_stream(m), ld_stream(m + 1)};
+    }
+    static __device__ __forceinline__ float dot(const Ch& ch, const Sb& sb, int j, const float* x, float s0, float s1) {
+        const uint32_t sw[8] = {sb.s0.x, sb.s0.y, sb.s0.z, sb.s0.w, sb.s1.x, sb.s1.y, sb.s1.z, sb.s1.w};
+        const uint32_t B = 0x80808080u;
+        uint32_t w[8] = {ch.c0.x ^ B, ch.c0.y ^ B, ch.c0.z ^ B, ch.c0.w ^ B, ch.c1.x ^ B, ch.c1.y ^ B, ch.c1.z ^ B, ch.c1.w ^ B};
+        float a = -128.0f * (s0 + s1);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) a = dot4_u8(w[k], x + 4 * k, a);
+        return __uint_as_float(sw[j]) * a;
+    }
+};
+
+struct RplQ4 {  // w = scale * q, q signed nibble; q ^ 8 = q + 8
+    static constexpr bool kIntX = false;
+    struct Ch { uint4 c; };
+    struct Sb { uint4 s0, s1; };
+    static __device__ __forceinline__ Ch load_ch(const RplArgs& a, int64_t ci, int lane) {
+        return {ld_stream(reinterpret_cast<const uint4*>(a.codes) + ci * 64 + lane)};
+    }
+    static __device__ __forceinline__ Sb load_sb(const RplArgs& a, int64_t si, int lane) {
+        const uint4* m = reinterpret_cast<const uint4*>(a.meta) + (si * 64 + lane) * 2;
+        return {ld_stream(m), ld_stream(m + 1)};
+    }
+    static __device__ __forceinline__ float dot(const Ch& ch, const Sb& sb, int j, const float* x, float s0, float s1) {
+        const uint32_t sw[8] = {sb.s0.x, sb.s0.y, sb.s0.z, sb.s0.w, sb.s1.x, sb.s1.y, sb.s1.z, sb.s1.w};
+        const uint32_t B = 0x88888888u;
+        const float a = dot16_u4(ch.c.x ^ B, ch.c.y ^ B, x) + dot16_u4(ch.c.z ^ B, ch.c.w ^ B, x + 16);
+        return __uint_as_float(sw[j]) * fmaf(-8.0f, s0 + s1, a);
+    }
+};
+
+template <class P, int D>
+__global__ void __launch_bounds__(1024) k_gemv_rpl(RplArgs a, const float* __restrict__ x, float* __restrict__ y) {
+    extern __shared__ float4 sm4[];
+    const int W = blockDim.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int rg = blockIdx.x, ks = blockIdx.y, b = blockIdx.z;
+    const int sb = ks * W + wave;
+    const bool active = sb < a.nsb;
+    const int sbc = active ? sb : a.nsb - 1;
+    const int64_t si = int64_t(rg) * a.nsb + sbc;
+    // chunk j of super-block si sits at plane index j*nsb_total + si
+    const int64_t nsb_total = int64_t(a.rg_count) * a.nsb;
+
+    // This wave's 256 x values: one float4 per lane, issued before the
+    // weights so that waiting for x does not wait for weight data (vector
+    // loads retire in issue order).
+    const float4 xv4 = reinterpret_cast<const float4*>(x + int64_t(b) * a.nsb * 256 + int64_t(sbc) * 256)[lane];
+    typename P::Ch ch[8];
+    const typename P::Sb sbm = P::load_sb(a, si, lane);
+#pragma unroll
+    for (int j = 0; j < D; ++j) ch[j] = P::load_ch(a, j * nsb_total + si, lane);
+
+    // Stage them in this wave's LDS slice (only this wave reads it, so a
+    // wave-level LDS wait replaces a block barrier and waves start computing
+    // as soon as their own data is in).
+    //   f32 policies: [256 x][16 sums of 16 columns]
+    //   int policies: per chunk 24 dwords of X byte planes + 4 floats meta
+    constexpr int kSlice = 256 + 16;
+    float* xs = reinterpret_cast<float*>(sm4) + wave * kSlice;
+    float* part = reinterpret_cast<float*>(sm4) + W * kSlice;  // [W*64]
+    float gsum = (xv4.x + xv4.y) + (xv4.z + xv4.w);
+    gsum += __shfl_xor(gsum, 1, 64);
+    gsum += __shfl_xor(gsum, 2, 64);  // lanes 4g..4g+3: sum of columns 16g..16g+15
+    if constexpr (!P::kIntX) {
+        reinterpret_cast<float4*>(xs)[lane] = xv4;
+        if ((lane & 3) == 0) xs[256 + (lane >> 2)] = gsum;
+    } else {
+        // lane = 8c + q holds columns 4q..4q+3 of chunk c
+        const int c = lane >> 3, q = lane & 7;
+        float m = fmaxf(fmaxf(fabsf(xv4.x), fabsf(xv4.y)), fmaxf(fabsf(xv4.z), fabsf(xv4.w)));
+        m = fmaxf(m, __shfl_xor(m, 1, 64));
+        m = fmaxf(m, __shfl_xor(m, 2, 64));
+        m = fmaxf(m, __shfl_xor(m, 4, 64));
+        int e = 0;
+        frexpf(m, &e);
+        const int sh = m > 0.f ? 22 - e : 0;  // |x| * 2^sh < 2^22
+        const int X0 = int(rintf(ldexpf(xv4.x, sh))), X1 = int(rintf(ldexpf(xv4.y, sh)));
+        const int X2 = int(rintf(ldexpf(xv4.z, sh))), X3 = int(rintf(ldexpf(xv4.w, sh)));
+        // code word w = q/2 covers columns 8w..8w+7; its lo spread word holds
+        // columns 8w+{0,2,4,6}, its hi spread word 8w+{1,3,5,7}: this lane
+        // supplies the byte pair at half (q & 1) of each.
+        uint16_t* h16 = reinterpret_cast<uint16_t*>(xs + c * 28);
+        const int w = q >> 1, half = q & 1;
+#pragma unroll
+        for (int pl = 0; pl < 3; ++pl) {
+            const int sb8 = 8 * pl;
+            const uint32_t blo = (uint32_t(X0 >> sb8) & 255u) | ((uint32_t(X2 >> sb8) & 255u) << 8);
+            const uint32_t bhi = (uint32_t(X1 >> sb8) & 255u) | ((uint32_t(X3 >> sb8) & 255u) << 8);
+            h16[(pl * 8 + w) * 2 + half] = uint16_t(blo);
+            h16[(pl * 8 + 4 + w) * 2 + half] = uint16_t(bhi);
+        }
+        const float s0 = __shfl(gsum, lane & ~7, 64), s1 = __shfl(gsum, (lane & ~7) + 4, 64);
+        if (q == 0) {
+            float* xm = xs + c * 28 + 24;
+            xm[0] = ldexpf(1.0f, -sh) * (1.0f / 255.0f);
+            xm[1] = s0;
+            xm[2] = s1;
+            xm[3] = -128.0f * (s0 + s1);
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    float acc = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        if (j + D < 8) ch[j + D] = P::load_ch(a, (j + D) * nsb_total + si, lane);
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (P::kIntX) {
+            if (active) {
+                const uint4* xq = reinterpret_cast<const uint4*>(xs + j * 28);
+                uint32_t xi[24];
+#pragma unroll
+                for (int k = 0; k < 6; ++k) {
+                    const uint4 t = xq[k];
+                    xi[4 * k] = t.x;
+                    xi[4 * k + 1] = t.y;
+                    xi[4 * k + 2] = t.z;
+                    xi[4 * k + 3] = t.w;
+                }
+                acc += P::dot_i(ch[j], sbm, j, xi, reinterpret_cast<const float4*>(xq)[6]);
+            }
+        } else {
+            if (active) {
+                const float4* xq = reinterpret_cast<const float4*>(xs + j * 32);
+                float xv[32];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    const float4 t = xq[k];
+                    xv[4 * k] = t.x;
+                    xv[4 * k + 1] = t.y;
+                    xv[4 * k + 2] = t.z;
+                    xv[4 * k + 3] = t.w;
+                }
+                const float2 s2 = reinterpret_cast<const float2*>(xs + 256)[j];
+                acc += P::dot(ch[j], sbm, j, xv, s2.x, s2.y);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    part[wave * 64 + lane] = acc;
+    __syncthreads();
+    if (wave != 0) return;
+    float s = 0.f;
+    for (int w = 0; w < W; ++w) s += part[w * 64 + lane];
+    const int row = rg * 64 + lane;
+    if (a.ksplit == 1) {
+        if (row < a.rows) y[int64_t(b) * a.rows + row] = s;
+        return;
+    }
+    // K split across gridDim.y blocks: publish the partial, take a ticket.
+    // Partials and tickets move only through agent-scope relaxed atomics
+    // (cache-bypassing sc1 accesses on gfx950), ordered by a wave-local wait
+    // for the stores before the ticket, so no L2 writeback/invalidate is needed.
+    const int64_t rows_pad = int64_t(a.rg_count) * 64;
+    float* pb = a.partial + int64_t(b) * a.ksplit * rows_pad;
+    __hip_atomic_store(pb + int64_t(ks) * rows_pad + row, s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_s_waitcnt(0);
+    uint32_t* ctr = a.counters + int64_t(b) * a.rg_count + rg;
+    uint32_t old = 0;
+    if (lane == 0) old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    old = __shfl(old, 0, 64);
+    if (old != uint32_t(a.ksplit - 1)) return;
+    float t = 0.f;
+    for (int k = 0; k < a.ksplit; ++k)
+        t += __hip_atomic_load(pb + int64_t(k) * rows_pad + row, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (row < a.rows) y[int64_t(b) * a.rows + row] = t;
+    if (lane == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Launch-geometry overrides for tuning sweeps, read once per process.
+int env_int(const char* name, int dflt) {
+    const char* v = std::getenv(name);
+    return v && *v ? std::atoi(v) : dflt;
+}
+int min_blocks() {
+    static const int v = env_int("WV_RPL_MIN_BLOCKS", 200);
+    return v;
+}
+int forced_waves() {
+    static const int v = env_int("WV_RPL_WAVES", 0);
+    return v;
+}
+int int_x() {
+    static const int v = env_int("WV_RPL_INT", 1);
+    return v;
+}
+int prefetch_depth() {
+    static const int v = env_int("WV_RPL_DEPTH", 2);
+    return v;
+}
+
+template <class P>
+int launch_rpl_t(const DevBlob& bl, const float* x, float* y, int batch, hipStream_t s) {
+    RplArgs a = bl.rpl;
+    // Waves per block W (super-blocks per block) and K split ks = ceil(nsb/W):
+    // among W = 16..4, prefer grids of >= 200 blocks (most of the 256 CUs),
+    // then the fewest idle waves (ks*W - nsb), then the largest W; the split
+    // is capped by the scratch the blob carries.
+    const int target = min_blocks();
+    int W = std::min(16, a.nsb), best_score = -1;
+    for (int w = std::min(16, a.nsb); w >= std::min(4, a.nsb); --w) {
+        const int k = (a.nsb + w - 1) / w;
+        if (k > bl.rpl_max_split) continue;
+        const bool fills = int64_t(a.rg_count) * k >= target;
+        const int idle = k * w - a.nsb;
+        const int score = (fills ? 1 << 20 : 0) + (1 << 10) * (64 - std::min(idle, 63)) + w;
+        if (score > best_score) {
+            best_score = score;
+            W = w;
+        }
+    }
+    const int fw = forced_waves();
+    if (fw > 0 && fw <= 16 && (a.nsb + fw - 1) / fw <= bl.rpl_max_split) W = fw;
+    int ksplit = (a.nsb + W - 1) / W;
+    a.ksplit = ksplit;
+    const size_t lds = size_t(W) * (256 + 16 + 64) * sizeof(float);  // kSlice + part per wave
+    auto kern = k_gemv_rpl<P, 2>;
+    if (prefetch_depth() == 3) kern = k_gemv_rpl<P, 3>;
+    if (prefetch_depth() >= 4) kern = k_gemv_rpl<P, 4>;
+    for (int b0 = 0; b0 < batch; b0 += bl.rpl_max_batch) {
+        const int nb = std::min(bl.rpl_max_batch, batch - b0);
+        dim3 grid(unsigned(a.rg_count), unsigned(ksplit), unsigned(ksplit > 1 ? nb : batch - b0));
+        hipLaunchKernelGGL(kern, grid, dim3(unsigned(64 * W)), lds, s, a, x + int64_t(b0) * a.nsb * 256,
+                           y + int64_t(b0) * a.rows);
+        if (ksplit == 1) break;  // one launch covers every batch row
+    }
+    return int(hipGetLastError());
+}
+
+}  // namespace
+
+int launch_rpl(const DevBlob& b, const float* d_x, float* d_y, int batch, void* stream) {
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    switch (b.fmt) {
+    case FMT_Q4_K: return int_x() ? launch_rpl_t<RplQ4KI>(b, d_x, d_y, batch, s) : launch_rpl_t<RplQ4K>(b, d_x, d_y, batch, s);
+    case FMT_Q6_K: return launch_rpl_t<RplQ6K>(b, d_x, d_y, batch, s);
+    case FMT_Q8_0: return launch_rpl_t<RplQ8>(b, d_x, d_y, batch, s);
+    case FMT_Q4_0: return launch_rpl_t<RplQ4>(b, d_x, d_y, batch, s);
+    default: return int(hipErrorInvalidValue);
+    }
+}
+
+}  // namespace wv

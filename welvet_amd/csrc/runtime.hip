@@ -10,6 +10,7 @@
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <thread>
 #include <unordered_map>
 #include <vector>
 
@@ -93,67 +94,101 @@ struct Image {
     }
 };
 
-// k-quant super-block → planes (requires cols % 256 == 0, so super-blocks
-// never straddle rows). Per row r, chunk j (32 columns):
-//   codes  [r][j] 16 B: 4-bit codes (Q4_K) or the low 4 bits (Q6_K);
-//   hi     [r][j]  8 B: Q6_K high 2 bits, arranged for the byte spread;
-//   dd     [r][sb] (d, dmin) f32 pair;
-//   grp    [r][j] (u'0, u'1, m0, m1) bytes (Q4_K) / (u'0, u'1) (Q6_K),
-// u' = max(u, 1): d*u/255 with u = 0 falls back to d/255 (kquant.go:179-182),
-// the same value u = 1 gives, so the kernel needs no branch.
-// Bytes per super-block equal the reference's (168 for Q4_K, 216 for Q6_K).
-bool relayout_k(const KSpec& sp, int fmt, const uint8_t* raw, int64_t rows, int64_t cols, Image& img,
-                size_t& o_codes, size_t& o_hi, size_t& o_dd, size_t& o_grp) {
-    const int64_t nsb_row = cols / 256, nch = cols / 32, sbb = k_super_bytes(sp);
-    const int64_t nsb = rows * nsb_row;
-    o_codes = img.add(size_t(rows * nch * 16));
-    o_hi = fmt == FMT_Q6_K ? img.add(size_t(rows * nch * 8)) : 0;
-    o_dd = img.add(size_t(nsb * 8));
-    o_grp = img.add(size_t(rows * nch * (fmt == FMT_Q6_K ? 2 : 4)));
-    uint8_t* codes = img.bytes.data() + o_codes;
-    uint8_t* hi = img.bytes.data() + o_hi;
-    float* dd = reinterpret_cast<float*>(img.bytes.data() + o_dd);
-    uint8_t* grp = img.bytes.data() + o_grp;
-    for (int64_t s = 0; s < nsb; ++s) {
-        const uint8_t* o = raw + s * sbb;
-        dd[2 * s] = f32_at(o);
-        dd[2 * s + 1] = f32_at(o + 4);
-        const uint8_t* q = o + (sp.has_dmin ? 40 : 24);
-        for (int p = 0; p < 8; ++p) {
-            const int64_t ci = s * 8 + p;  // chunk index within the matrix (row-major)
-            const uint8_t u0 = std::max<uint8_t>(o[8 + 2 * p], 1), u1 = std::max<uint8_t>(o[9 + 2 * p], 1);
-            if (fmt == FMT_Q6_K) {
-                grp[ci * 2] = u0;
-                grp[ci * 2 + 1] = u1;
-            } else {
-                grp[ci * 4] = u0;
-                grp[ci * 4 + 1] = u1;
-                grp[ci * 4 + 2] = o[24 + 2 * p];
-                grp[ci * 4 + 3] = o[25 + 2 * p];
-            }
-            uint8_t qv[32];
-            for (int k = 0; k < 32; ++k) {  // LSB-first bit stream (helpers.go:140-149)
-                const int64_t bit = int64_t(p * 32 + k) * sp.bits;
-                uint32_t v = q[bit >> 3] | (((bit >> 3) + 1 < (256 * sp.bits) / 8) ? uint32_t(q[(bit >> 3) + 1]) << 8 : 0u);
-                qv[k] = uint8_t((v >> (bit & 7)) & ((1u << sp.bits) - 1u));
-            }
-            uint8_t* c = codes + ci * 16;
-            for (int k = 0; k < 16; ++k) c[k] = uint8_t((qv[2 * k] & 15) | ((qv[2 * k + 1] & 15) << 4));
-            if (fmt == FMT_Q6_K) {
-                uint8_t* h = hi + ci * 8;
-                std::memset(h, 0, 8);
-                // spread word s = 2*w + half holds, in byte b, code 8w + 2b + half.
-                for (int sw = 0; sw < 8; ++sw) {
-                    const int w = sw >> 1, half = sw & 1, t = sw >> 2, f = sw & 3;
-                    for (int b = 0; b < 4; ++b) {
-                        const int k = 8 * w + 2 * b + half;
-                        h[t * 4 + b] |= uint8_t(((qv[k] >> 4) & 3) << (2 * f));
+// Row-interleaved layout for Q4_K / Q6_K / Q8_0 / Q4_0 (requires cols % 256
+// == 0): rows are grouped 64 at a time, one per lane of a wave, and every
+// plane is stored [row group][chunk or super-block][lane][bytes] so that one
+// wave-wide load reads contiguous memory. Byte count per 256 weights equals
+// the reference blob's (Q4_K 168, Q6_K 216, Q8_0 288, Q4_0 160); rows past
+// `rows` in the last group are zero (d = 0 / scale = 0, contributing 0).
+//   Q4_K: codes 16 B/chunk (LSB-first nibbles, as in the blob); meta per
+//         super-block 8 words (u'(2p), u'(2p+1), m(2p), m(2p+1)); dd (d, dmin).
+//         u' = max(u, 1): d*u/255 with u = 0 falls back to d/255
+//         (quant/kquant.go:179-182), the value u = 1 gives.
+//   Q6_K: low 4 code bits 16 B/chunk; high 2 bits 8 B/chunk arranged for
+//         the kernel's byte spread; meta 8 u16 (u'(2p), u'(2p+1)); dd.
+//   Q8_0 / Q4_0: codes 32 / 16 B per 32-block; meta 8 f32 block scales.
+// Code (and Q6_K high-bit) planes are chunk-step-major, [j][rg][sb][lane],
+// j = chunk index inside the super-block; meta/dd are [rg][sb][lane].
+struct RplOffsets {
+    size_t codes = 0, hi = 0, meta = 0, dd = 0;
+};
+void build_rpl(int fmt, const uint8_t* raw, int64_t rows, int64_t cols, Image& img, RplOffsets& o) {
+    const int64_t rg = (rows + 63) / 64, nch = cols / 32, nsb = cols / 256;
+    const int cb = fmt == FMT_Q8_0 ? 32 : 16, mb = fmt == FMT_Q6_K ? 16 : 32;
+    const bool kq = fmt == FMT_Q4_K || fmt == FMT_Q6_K;
+    o.codes = img.add(size_t(rg * nch * 64 * cb));
+    if (fmt == FMT_Q6_K) o.hi = img.add(size_t(rg * nch * 64 * 8));
+    o.meta = img.add(size_t(rg * nsb * 64 * mb));
+    if (kq) o.dd = img.add(size_t(rg * nsb * 64 * 8));
+    uint8_t* base = img.bytes.data();
+    uint8_t* codes = base + o.codes;
+    uint8_t* hi = base + o.hi;
+    uint8_t* meta = base + o.meta;
+    float* dd = reinterpret_cast<float*>(base + o.dd);
+    KSpec ks;
+    k_spec(fmt, ks);
+    const int64_t sbb = kq ? k_super_bytes(ks) : 0;
+    auto work = [&](int64_t g0, int64_t g1) {
+        for (int64_t g = g0; g < g1; ++g)
+            for (int lane = 0; lane < 64; ++lane) {
+                const int64_t row = g * 64 + lane;
+                if (row >= rows) continue;
+                for (int64_t sb = 0; sb < nsb; ++sb) {
+                    const int64_t mi = (g * nsb + sb) * 64 + lane;
+                    uint8_t* m = meta + mi * mb;
+                    if (kq) {
+                        const uint8_t* o8 = raw + (row * nsb + sb) * sbb;
+                        dd[2 * mi] = f32_at(o8);
+                        dd[2 * mi + 1] = f32_at(o8 + 4);
+                        for (int p = 0; p < 8; ++p) {
+                            const int64_t ci = ((p * rg + g) * nsb + sb) * 64 + lane;  // [j][rg][sb][lane]
+                            const uint8_t u0 = std::max<uint8_t>(o8[8 + 2 * p], 1), u1 = std::max<uint8_t>(o8[9 + 2 * p], 1);
+                            if (fmt == FMT_Q4_K) {
+                                m[4 * p] = u0;
+                                m[4 * p + 1] = u1;
+                                m[4 * p + 2] = o8[24 + 2 * p];
+                                m[4 * p + 3] = o8[25 + 2 * p];
+                                std::memcpy(codes + ci * 16, o8 + 40 + 16 * p, 16);
+                            } else {
+                                m[2 * p] = u0;
+                                m[2 * p + 1] = u1;
+                                const uint8_t* q = o8 + 24;  // 192 B of 6-bit codes
+                                uint8_t qv[32];
+                                for (int k = 0; k < 32; ++k) {  // LSB-first stream (helpers.go:140-149)
+                                    const int bit = (p * 32 + k) * 6;
+                                    const uint32_t v = q[bit >> 3] | ((bit >> 3) + 1 < 192 ? uint32_t(q[(bit >> 3) + 1]) << 8 : 0u);
+                                    qv[k] = uint8_t((v >> (bit & 7)) & 63u);
+                                }
+                                uint8_t* c = codes + ci * 16;
+                                for (int k = 0; k < 16; ++k) c[k] = uint8_t((qv[2 * k] & 15) | ((qv[2 * k + 1] & 15) << 4));
+                                uint8_t* h = hi + ci * 8;
+                                std::memset(h, 0, 8);
+                                // spread word s = 2*w + half holds code 8w + 2b + half in byte b
+                                for (int sw = 0; sw < 8; ++sw) {
+                                    const int w = sw >> 1, half = sw & 1, t = sw >> 2, f = sw & 3;
+                                    for (int b = 0; b < 4; ++b) h[t * 4 + b] |= uint8_t(((qv[8 * w + 2 * b + half] >> 4) & 3) << (2 * f));
+                                }
+                            }
+                        }
+                    } else {
+                        const int bb = fmt == FMT_Q8_0 ? 36 : 20;
+                        for (int p = 0; p < 8; ++p) {
+                            const uint8_t* blk = raw + (row * nch + sb * 8 + p) * bb;
+                            std::memcpy(m + 4 * p, blk, 4);
+                            std::memcpy(codes + (((p * rg + g) * nsb + sb) * 64 + lane) * cb, blk + 4, size_t(cb));
+                        }
                     }
                 }
             }
-        }
+    };
+    const int64_t nthreads = std::min<int64_t>(std::max(1u, std::thread::hardware_concurrency()), std::max<int64_t>(1, rg / 4));
+    std::vector<std::thread> th;
+    const int64_t per = (rg + nthreads - 1) / nthreads;
+    for (int64_t t = 0; t < nthreads; ++t) {
+        const int64_t g0 = t * per, g1 = std::min(rg, g0 + per);
+        if (g0 < g1) th.emplace_back(work, g0, g1);
     }
-    return true;
+    for (auto& t : th) t.join();
 }
 
 int upload_image(const Image& img, DevBlob& b) {
@@ -300,27 +335,17 @@ int wv_blob_upload(int format, int64_t rows, int64_t cols, int32_t block_weights
     b.device = g_current;
     Image img;
     const bool raw_only = force_raw();
-    KSpec ks;
-    size_t o_codes = 0, o_hi = 0, o_blk = 0, o_grp = 0, o_raw = 0, o_sc = 0;
+    RplOffsets ro;
+    size_t o_codes = 0, o_raw = 0, o_sc = 0;
     if (format == FMT_NATIVE_TERNARY) {
         b.layout = LAYOUT_TERNARY_I8;
         if (cols > 32768) return fail(WV_E_SHAPE, "wv_blob_upload: native ternary cols %lld > 32768", (long long)cols);
         o_codes = img.add(size_t(need));
         std::memcpy(img.bytes.data() + o_codes, raw, size_t(need));
-    } else if (!raw_only && (format == FMT_Q4_K || format == FMT_Q6_K) && cols % 256 == 0 && cols <= 65536 && k_spec(format, ks)) {
-        b.layout = LAYOUT_K_PLANAR;
-        relayout_k(ks, format, raw, rows, cols, img, o_codes, o_hi, o_blk, o_grp);
-    } else if (!raw_only && (format == FMT_Q8_0 || format == FMT_Q4_0) && cols % 32 == 0 && cols <= 65536) {
-        const int64_t nblk = rows * cols / 32;
-        const bool q8 = format == FMT_Q8_0;
-        b.layout = q8 ? LAYOUT_Q8_PLANAR : LAYOUT_Q4_PLANAR;
-        const int bb = q8 ? 36 : 20, cb = q8 ? 32 : 16;
-        o_codes = img.add(size_t(nblk * cb));
-        o_blk = img.add(size_t(nblk * 4));
-        for (int64_t k = 0; k < nblk; ++k) {
-            std::memcpy(img.bytes.data() + o_blk + k * 4, raw + k * bb, 4);
-            std::memcpy(img.bytes.data() + o_codes + k * cb, raw + k * bb + 4, size_t(cb));
-        }
+    } else if (!raw_only && (format == FMT_Q4_K || format == FMT_Q6_K || format == FMT_Q8_0 || format == FMT_Q4_0) &&
+               cols % 256 == 0) {
+        b.layout = LAYOUT_RPL;
+        build_rpl(format, raw, rows, cols, img, ro);
     } else {
         b.layout = LAYOUT_RAW;
         o_raw = img.add(size_t(need));
@@ -338,17 +363,37 @@ int wv_blob_upload(int format, int64_t rows, int64_t cols, int32_t block_weights
             b.n_scales = int64_t(n_scales);
         }
     }
+    // K-split scratch for the row-interleaved path: partial sums and arrival
+    // tickets (zeroed here; the last block of each row group re-zeroes its ticket).
+    size_t o_part = 0, o_ctr = 0, weight_bytes = img.bytes.size();
+    if (b.layout == LAYOUT_RPL) {
+        const int64_t rg = (rows + 63) / 64, nsb = cols / 256;
+        b.rpl_max_batch = 8;
+        b.rpl_max_split = int(std::max<int64_t>(1, (nsb + 3) / 4));
+        o_part = img.add(size_t(b.rpl_max_batch) * b.rpl_max_split * rg * 64 * sizeof(float));
+        o_ctr = img.add(size_t(b.rpl_max_batch) * rg * sizeof(uint32_t));
+    }
     rc = upload_image(img, b);
     if (rc) return rc;
+    b.device_bytes = weight_bytes;
     uint8_t* base = static_cast<uint8_t*>(b.base);
     if (b.layout == LAYOUT_RAW) {
         b.raw = base + o_raw;
         b.scales = b.n_scales ? reinterpret_cast<const float*>(base + o_sc) : nullptr;
-    } else {
+    } else if (b.layout == LAYOUT_TERNARY_I8) {
         b.codes = base + o_codes;
-        b.codes_hi = o_hi ? base + o_hi : nullptr;
-        b.blk_scale = o_blk ? reinterpret_cast<const float*>(base + o_blk) : nullptr;
-        b.grp = o_grp ? reinterpret_cast<const uint32_t*>(base + o_grp) : nullptr;
+    } else {
+        RplArgs& r = b.rpl;
+        r.codes = base + ro.codes;
+        r.hi = ro.hi ? base + ro.hi : nullptr;
+        r.meta = base + ro.meta;
+        r.dd = ro.dd ? reinterpret_cast<const float2_t*>(base + ro.dd) : nullptr;
+        r.partial = reinterpret_cast<float*>(base + o_part);
+        r.counters = reinterpret_cast<uint32_t*>(base + o_ctr);
+        r.rows = int(rows);
+        r.nsb = int(cols / 256);
+        r.rg_count = int((rows + 63) / 64);
+        r.ksplit = 1;
     }
     std::lock_guard<std::mutex> lk(g_mu);
     const uint64_t h = g_next++;

@@ -6,6 +6,10 @@
 
 namespace wv {
 
+struct float2_t {
+    float x, y;
+};
+
 // quant.Format values (quant/format.go:9-39).
 enum Fmt : int {
     FMT_NONE = 0, FMT_Q8_0 = 1, FMT_Q4_0 = 2, FMT_Q4_1 = 3, FMT_Q5_0 = 4, FMT_Q5_1 = 5,
@@ -73,11 +77,26 @@ void pack_native_ternary(const float* w, int64_t n, uint8_t* codes, float* scale
 
 // How a blob sits in HBM.
 enum Layout : int {
-    LAYOUT_RAW = 0,      // uploaded bytes verbatim; decoded per element (any shape / format)
-    LAYOUT_K_PLANAR = 1, // k-quants, cols % 256 == 0: codes plane + (d,dmin) plane + scale/min plane
-    LAYOUT_Q8_PLANAR = 2,// Q8_0, cols % 32 == 0: int8 codes plane + f32 scale plane
-    LAYOUT_Q4_PLANAR = 3,// Q4_0, cols % 32 == 0: nibble plane + f32 scale plane
-    LAYOUT_TERNARY_I8 = 4,// DTypeTernary, cols % 64 == 0: 2-bit codes rows (as uploaded)
+    LAYOUT_RAW = 0,        // uploaded bytes verbatim; decoded per element (any shape / format)
+    LAYOUT_RPL = 1,        // Q4_K/Q6_K/Q8_0/Q4_0 with cols % 256 == 0: row-interleaved planes (gemv_rpl.hip)
+    LAYOUT_TERNARY_I8 = 4, // DTypeTernary: 2-bit codes rows (as uploaded)
+};
+
+// Device view of a row-interleaved blob. Rows are grouped 64 at a time (one
+// wave's lanes); chunk = 32 columns, super-block (sb) = 256 columns.
+//   codes [j][rg][sb][lane][CB]   CB = 16 B (4-bit codes), 32 B (Q8_0); j = chunk in sb
+//   hi    [j][rg][sb][lane][8 B]  Q6_K high 2 bits
+//   meta  [rg][sb][lane][MB]      MB = 32 B (Q4_K scale/min bytes, Q8_0/Q4_0
+//                                  f32 block scales) or 16 B (Q6_K scales)
+//   dd    [rg][sb][lane] (d, dmin) f32 pair (k-quants)
+struct RplArgs {
+    const uint8_t* codes;
+    const uint8_t* hi;
+    const uint8_t* meta;
+    const float2_t* dd;
+    float* partial;       // [batch chunk][ksplit][rg*64] partial sums when K is split
+    uint32_t* counters;   // [batch chunk][rg] arrival tickets, zero between launches
+    int rows, nsb, rg_count, ksplit;
 };
 
 // Device view of one blob. Pointers are into one hipMalloc'd allocation.
@@ -94,16 +113,18 @@ struct DevBlob {
     const float* scales = nullptr;
     int64_t n_scales = 0;
     int iq_bits = 0, iq_sg = 0;  // Meta[0], Meta[1] for IQ (iq.go:187-190)
-    // planar layouts
-    const uint8_t* codes = nullptr;   // row-major code plane
-    const uint8_t* codes_hi = nullptr;// Q6_K high-2-bit plane
-    const float* blk_scale = nullptr; // Q8_0/Q4_0 per-block f32 scales; k-quants (d,dmin) pairs
-    const uint32_t* grp = nullptr;    // k-quants: per 32-column chunk (u0,u1,m0,m1) bytes
-    void* base = nullptr;             // allocation owner
-    size_t device_bytes = 0;
+    // LAYOUT_TERNARY_I8
+    const uint8_t* codes = nullptr;
+    // LAYOUT_RPL
+    RplArgs rpl{};
+    int rpl_max_split = 1;  // capacity of rpl.partial per batch row
+    int rpl_max_batch = 1;  // batch rows one split launch can carry
+    void* base = nullptr;   // allocation owner
+    size_t device_bytes = 0;  // weight bytes (excludes scratch)
 };
 
-// Kernel launchers (gemv.hip). Return a hipError_t as int.
+// Kernel launchers (gemv.hip, gemv_rpl.hip). Return a hipError_t as int.
+int launch_rpl(const DevBlob& b, const float* d_x, float* d_y, int batch, void* stream);
 int launch_matvec(const DevBlob& b, const float* d_x, float* d_y, int batch, void* stream);
 int launch_matvec_t(const DevBlob& b, const float* d_gy, float* d_gx, int batch, void* stream, float* d_scratch);
 size_t matvec_t_scratch_floats(const DevBlob& b, int batch);
