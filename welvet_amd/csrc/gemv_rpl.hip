@@ -385,7 +385,11 @@ int int_x() {
     return v;
 }
 int prefetch_depth() {
-    static const int v = env_int("WV_RPL_DEPTH", 2);
+    static const int v = env_int("WV_RPL_DEPTH", 4);
+    return v;
+}
+int lds_floor() {
+    static const int v = env_int("WV_RPL_LDS_MIN", 0);
     return v;
 }
 
@@ -413,7 +417,8 @@ int launch_rpl_t(const DevBlob& bl, const float* x, float* y, int batch, hipStre
     if (fw > 0 && fw <= 16 && (a.nsb + fw - 1) / fw <= bl.rpl_max_split) W = fw;
     int ksplit = (a.nsb + W - 1) / W;
     a.ksplit = ksplit;
-    const size_t lds = size_t(W) * (256 + 16 + 64) * sizeof(float);  // kSlice + part per wave
+    size_t lds = size_t(W) * (256 + 16 + 64) * sizeof(float);  // kSlice + part per wave
+    lds = std::max(lds, size_t(lds_floor()));
     auto kern = k_gemv_rpl<P, 2>;
     if (prefetch_depth() == 3) kern = k_gemv_rpl<P, 3>;
     if (prefetch_depth() >= 4) kern = k_gemv_rpl<P, 4>;
