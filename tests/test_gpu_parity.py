@@ -148,6 +148,7 @@ def test_native_ternary_bit_exact(shape):
     acc = torch.zeros(2 * rows, dtype=torch.int32, device="cuda")
     act = torch.zeros(2, dtype=torch.float32, device="cuda")
     y = torch.zeros(2 * rows, dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()  # the library's stream does not wait for torch's
     d.ternary_acc_dev(tx.data_ptr(), acc.data_ptr(), act.data_ptr(), 2)
     d.matvec_dev(tx.data_ptr(), y.data_ptr(), 2)
     wv.sync()
@@ -169,6 +170,44 @@ def test_matvec_t_accumulates(fmt):
     want = gx0 + gy.astype(np.float64) @ wd
     got = d.matvec_t(gy, gx0)
     assert normwise(got, want) <= TOL
+
+
+@pytest.mark.parametrize("fmt", sorted(PLANAR))
+@pytest.mark.parametrize("shape,batch", [((64, 512), 2), ((300, 2048), 2), ((1000, 2048), 3), ((130, 256), 1), ((300, 1024), 18)])
+def test_matvec_t_row_interleaved(fmt, shape, batch):
+    """gx += W^T gy on the resident row-interleaved layout: one slice (direct) and sliced + reduce."""
+    rows, cols = shape
+    print(f"[gpu] matvec_t rpl {fmt} {rows}x{cols} batch {batch}", flush=True)
+    w, rng = weights(rows, cols, 23 + rows)
+    gy = rng.standard_normal((batch, rows)).astype(np.float32)
+    gx0 = rng.standard_normal((batch, cols)).astype(np.float32)
+    p, d = upload(fmt, w, rows, cols)
+    assert d.info()["layout"] == "row-interleaved"
+    wd = oracle.unpack(oracle_packed(p)).reshape(rows, cols).astype(np.float64)
+    want = gx0 + gy.astype(np.float64) @ wd
+    for _ in range(2):
+        assert normwise(d.matvec_t(gy, gx0), want) <= TOL
+    d.free()
+
+
+@pytest.mark.parametrize("fmt", ["Q4_K", "Q6_K"])
+def test_matvec_t_row_interleaved_baseline(fmt):
+    import torch
+    rows, cols = 14336, 4096
+    print(f"[gpu] matvec_t rpl baseline {fmt} {rows}x{cols}", flush=True)
+    w, rng = weights(rows, cols, 31)
+    gy = rng.standard_normal(rows).astype(np.float32)
+    p, d = upload(fmt, w, rows, cols)
+    wd = oracle.unpack(oracle_packed(p)).reshape(rows, cols)
+    want = gy.astype(np.float64) @ wd.astype(np.float64)
+    del wd
+    tg = torch.from_numpy(gy).cuda()
+    tx = torch.zeros(cols, device="cuda")
+    torch.cuda.synchronize()  # the library's stream does not wait for torch's
+    d.matvec_t_dev(tg.data_ptr(), tx.data_ptr(), 1)
+    wv.sync()
+    assert normwise(tx.cpu().numpy(), want) <= TOL
+    d.free()
 
 
 def test_device_pointer_path_on_torch_stream():

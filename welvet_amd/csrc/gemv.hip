@@ -376,7 +376,13 @@ int launch_matvec(const DevBlob& b, const float* d_x, float* d_y, int batch, voi
     }
 }
 
+void launch_gemvt_reduce(const float* part, float* gx, int64_t cols, int nsplit, int batch, void* stream) {
+    hipLaunchKernelGGL(k_gemvt_reduce, dim3(unsigned((cols + 255) / 256), unsigned(batch)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), part, gx, cols, nsplit);
+}
+
 size_t matvec_t_scratch_floats(const DevBlob& b, int batch) {
+    if (b.layout == LAYOUT_RPL) return 0;
     const int64_t nsplit = std::max<int64_t>(1, std::min<int64_t>(64, b.rows / 64));
     return size_t(nsplit) * size_t(b.cols) * size_t(batch);
 }
@@ -384,6 +390,7 @@ size_t matvec_t_scratch_floats(const DevBlob& b, int batch) {
 int launch_matvec_t(const DevBlob& b, const float* d_gy, float* d_gx, int batch, void* stream, float* d_scratch) {
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (b.rows == 0 || batch == 0) return 0;
+    if (b.layout == LAYOUT_RPL) return launch_rpl_matvec_t(b, d_gy, d_gx, batch, stream);
     if (b.layout != LAYOUT_RAW) return int(hipErrorInvalidValue);
     RawTFn f = pick_raw_t(b.fmt);
     if (!f) return int(hipErrorInvalidValue);

@@ -224,6 +224,24 @@ struct RplQ4 {  // w = scale * q, q signed nibble; q ^ 8 = q + 8
     }
 };
 
+// sum_{k<n} p[k*stride], k ascending, read with cache-bypassing agent-scope
+// loads issued B at a time (so their latencies overlap) and added in order.
+template <int B = 8>
+__device__ __forceinline__ float sum_partials(const float* p, int64_t stride, int n) {
+    float t = 0.f;
+    int k = 0;
+    for (; k + B <= n; k += B) {
+        float v[B];
+#pragma unroll
+        for (int i = 0; i < B; ++i)
+            v[i] = __hip_atomic_load(p + int64_t(k + i) * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+        for (int i = 0; i < B; ++i) t += v[i];
+    }
+    for (; k < n; ++k) t += __hip_atomic_load(p + int64_t(k) * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return t;
+}
+
 template <class P, int D>
 __global__ void __launch_bounds__(1024) k_gemv_rpl(RplArgs a, const float* __restrict__ x, float* __restrict__ y) {
     extern __shared__ float4 sm4[];
@@ -360,9 +378,7 @@ __global__ void __launch_bounds__(1024) k_gemv_rpl(RplArgs a, const float* __res
     if (lane == 0) old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     old = __shfl(old, 0, 64);
     if (old != uint32_t(a.ksplit - 1)) return;
-    float t = 0.f;
-    for (int k = 0; k < a.ksplit; ++k)
-        t += __hip_atomic_load(pb + int64_t(k) * rows_pad + row, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const float t = sum_partials(pb + row, rows_pad, a.ksplit);
     if (row < a.rows) y[int64_t(b) * a.rows + row] = t;
     if (lane == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -432,6 +448,274 @@ int launch_rpl_t(const DevBlob& bl, const float* x, float* y, int batch, hipStre
     return int(hipGetLastError());
 }
 
+// ---------------------------------------------------------------------------
+// gx += W^T gy on the row-interleaved layout (quant.MatVecT).
+//
+// Lane = row, as in the forward layout, so the sum over rows runs across
+// lanes. A wave owns one chunk pair (64 columns) of one super-block and walks
+// a slice of row groups, accumulating per-lane column partials in registers
+// (acc[c] += coef_group(row) * ucode(row, c), plus one offset term per
+// 16-column group: the k-quant min or the code bias). Only after the slice
+// does it reduce across lanes, with a reduce-scatter that leaves column l in
+// lane l. The 4 waves of a block are the 4 chunk pairs of one super-block, so
+// they read the same metadata lines together (HBM once, L2 after). Slices
+// write partials [b][slice][cols] that a fixed-order pass adds to gx; a
+// single slice adds to gx directly.
+// ---------------------------------------------------------------------------
+
+// acc[2b], acc[2b+1] += coef * (nibbles 2b, 2b+1 of v), b = 0..3
+__device__ __forceinline__ void tacc_nib(uint32_t v, float coef, float* acc) {
+    uint32_t l = v & 0x0F0F0F0Fu, h = (v >> 4) & 0x0F0F0F0Fu;
+    asm("" : "+v"(l), "+v"(h));
+    acc[0] = fmaf(ub0(l), coef, acc[0]);
+    acc[1] = fmaf(ub0(h), coef, acc[1]);
+    acc[2] = fmaf(ub1(l), coef, acc[2]);
+    acc[3] = fmaf(ub1(h), coef, acc[3]);
+    acc[4] = fmaf(ub2(l), coef, acc[4]);
+    acc[5] = fmaf(ub2(h), coef, acc[5]);
+    acc[6] = fmaf(ub3(l), coef, acc[6]);
+    acc[7] = fmaf(ub3(h), coef, acc[7]);
+}
+// acc[k] += coef * byte k of v
+__device__ __forceinline__ void tacc_u8(uint32_t v, float coef, float* acc) {
+    asm("" : "+v"(v));
+    acc[0] = fmaf(ub0(v), coef, acc[0]);
+    acc[1] = fmaf(ub1(v), coef, acc[1]);
+    acc[2] = fmaf(ub2(v), coef, acc[2]);
+    acc[3] = fmaf(ub3(v), coef, acc[3]);
+}
+
+// Per-format metadata of one chunk pair (jp) and the accumulate step for
+// chunk jj of the pair. off[0..1] collect the per-group offsets.
+struct TQ4K : RplQ4K {
+    struct TM { uint2 g; float2 dd; };  // (u'0,u'1,m0,m1) bytes of chunks 2jp, 2jp+1
+    static __device__ __forceinline__ TM load_tm(const RplArgs& a, int64_t si, int lane, int jp) {
+        const uint2* m = reinterpret_cast<const uint2*>(a.meta) + (si * 64 + lane) * 4 + jp;
+        const float2 dd = reinterpret_cast<const float2*>(a.dd)[si * 64 + lane];
+        return {ld_stream(m), dd};
+    }
+    template <int jj>
+    static __device__ __forceinline__ void tacc(const Ch& ch, const TM& t, float gy, float* acc, float* off) {
+        const uint32_t g = jj ? t.g.y : t.g.x;
+        const float gd = gy * (t.dd.x * (1.0f / 255.0f));
+        const float c0 = gd * ub0(g), c1 = gd * ub1(g);
+        const float gm = gy * (t.dd.y * (1.0f / 127.0f));
+        off[0] = fmaf(gm, float(int8_t(g >> 16)), off[0]);
+        off[1] = fmaf(gm, float(int32_t(g) >> 24), off[1]);
+        tacc_nib(ch.c.x, c0, acc);
+        tacc_nib(ch.c.y, c0, acc + 8);
+        tacc_nib(ch.c.z, c1, acc + 16);
+        tacc_nib(ch.c.w, c1, acc + 24);
+    }
+};
+
+struct TQ6K : RplQ6K {
+    struct TM { uint32_t g; float d; };  // (u'0,u'1) of chunk 2jp | (u'0,u'1) of 2jp+1 << 16
+    static __device__ __forceinline__ TM load_tm(const RplArgs& a, int64_t si, int lane, int jp) {
+        const uint32_t* m = reinterpret_cast<const uint32_t*>(a.meta) + (si * 64 + lane) * 4 + jp;
+        return {*m, reinterpret_cast<const float*>(a.dd)[(si * 64 + lane) * 2]};
+    }
+    // q = lo4 | hi2 << 4 spread to bytes as in RplQ6K::dot8
+    static __device__ __forceinline__ void tacc6(uint32_t w, uint32_t h, int f0, float coef, float* acc) {
+        uint32_t lo = (w & 0x0F0F0F0Fu) | (((h >> (2 * f0)) & 0x03030303u) << 4);
+        uint32_t hi = ((w >> 4) & 0x0F0F0F0Fu) | (((h >> (2 * f0 + 2)) & 0x03030303u) << 4);
+        asm("" : "+v"(lo), "+v"(hi));
+        acc[0] = fmaf(ub0(lo), coef, acc[0]);
+        acc[1] = fmaf(ub0(hi), coef, acc[1]);
+        acc[2] = fmaf(ub1(lo), coef, acc[2]);
+        acc[3] = fmaf(ub1(hi), coef, acc[3]);
+        acc[4] = fmaf(ub2(lo), coef, acc[4]);
+        acc[5] = fmaf(ub2(hi), coef, acc[5]);
+        acc[6] = fmaf(ub3(lo), coef, acc[6]);
+        acc[7] = fmaf(ub3(hi), coef, acc[7]);
+    }
+    template <int jj>
+    static __device__ __forceinline__ void tacc(const Ch& ch, const TM& t, float gy, float* acc, float* off) {
+        const uint32_t g = t.g >> (16 * jj);
+        const float gd = gy * (t.d * (1.0f / 255.0f));
+        const float c0 = gd * ub0(g), c1 = gd * ub1(g);
+        off[0] = fmaf(-32.0f, c0, off[0]);
+        off[1] = fmaf(-32.0f, c1, off[1]);
+        tacc6(ch.c.x, ch.h.x, 0, c0, acc);
+        tacc6(ch.c.y, ch.h.x, 2, c0, acc + 8);
+        tacc6(ch.c.z, ch.h.y, 0, c1, acc + 16);
+        tacc6(ch.c.w, ch.h.y, 2, c1, acc + 24);
+    }
+};
+
+struct TQ8 : RplQ8 {
+    struct TM { uint2 s; };  // f32 scales of chunks 2jp, 2jp+1
+    static __device__ __forceinline__ TM load_tm(const RplArgs& a, int64_t si, int lane, int jp) {
+        return {ld_stream(reinterpret_cast<const uint2*>(a.meta) + (si * 64 + lane) * 4 + jp)};
+    }
+    template <int jj>
+    static __device__ __forceinline__ void tacc(const Ch& ch, const TM& t, float gy, float* acc, float* off) {
+        const float c = gy * __uint_as_float(jj ? t.s.y : t.s.x);
+        off[0] = fmaf(-128.0f, c, off[0]);
+        off[1] = fmaf(-128.0f, c, off[1]);
+        const uint32_t B = 0x80808080u;
+        tacc_u8(ch.c0.x ^ B, c, acc);
+        tacc_u8(ch.c0.y ^ B, c, acc + 4);
+        tacc_u8(ch.c0.z ^ B, c, acc + 8);
+        tacc_u8(ch.c0.w ^ B, c, acc + 12);
+        tacc_u8(ch.c1.x ^ B, c, acc + 16);
+        tacc_u8(ch.c1.y ^ B, c, acc + 20);
+        tacc_u8(ch.c1.z ^ B, c, acc + 24);
+        tacc_u8(ch.c1.w ^ B, c, acc + 28);
+    }
+};
+
+struct TQ4 : RplQ4 {
+    struct TM { uint2 s; };
+    static __device__ __forceinline__ TM load_tm(const RplArgs& a, int64_t si, int lane, int jp) {
+        return {ld_stream(reinterpret_cast<const uint2*>(a.meta) + (si * 64 + lane) * 4 + jp)};
+    }
+    template <int jj>
+    static __device__ __forceinline__ void tacc(const Ch& ch, const TM& t, float gy, float* acc, float* off) {
+        const float c = gy * __uint_as_float(jj ? t.s.y : t.s.x);
+        off[0] = fmaf(-8.0f, c, off[0]);
+        off[1] = fmaf(-8.0f, c, off[1]);
+        const uint32_t B = 0x88888888u;
+        tacc_nib(ch.c.x ^ B, c, acc);
+        tacc_nib(ch.c.y ^ B, c, acc + 8);
+        tacc_nib(ch.c.z ^ B, c, acc + 16);
+        tacc_nib(ch.c.w ^ B, c, acc + 24);
+    }
+};
+
+template <class P, int GP>
+__global__ void __launch_bounds__(256) k_gemvt_rpl(RplArgs a, const float* __restrict__ gy, float* __restrict__ gx,
+                                                  float* __restrict__ part, uint32_t* __restrict__ tickets) {
+    const int jp = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int sb = blockIdx.x, slice = blockIdx.y, b = blockIdx.z;
+    const int nslices = gridDim.y;
+    const int g0 = slice * GP;
+    const int64_t nsb_total = int64_t(a.rg_count) * a.nsb;
+    const int64_t cols = int64_t(a.nsb) * 256;
+    const float* gyb = gy + int64_t(b) * a.rows;
+
+    float acc[64], off[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < 64; ++k) acc[k] = 0.f;
+
+    // GP row groups per slice, fully unrolled with a 2-deep register ring so
+    // that every index is static and no load sits under a branch (either would
+    // make the next use wait for all outstanding loads). Row groups past the
+    // end are clamped to the last one and contribute gy = 0.
+    struct Set {
+        typename P::Ch c0, c1;
+        typename P::TM tm;
+        float gy;
+    };
+    auto load = [&](int i, Set& st) {
+        const int g = min(g0 + i, a.rg_count - 1);
+        const int64_t si = int64_t(g) * a.nsb + sb;
+        st.c0 = P::load_ch(a, (2 * jp) * nsb_total + si, lane);
+        st.c1 = P::load_ch(a, (2 * jp + 1) * nsb_total + si, lane);
+        st.tm = P::load_tm(a, si, lane, jp);
+        st.gy = gyb[min(g * 64 + lane, a.rows - 1)];
+    };
+    constexpr int R = GP < 2 ? GP : 2;
+    Set ring[R];
+#pragma unroll
+    for (int i = 0; i < R; ++i) load(i, ring[i]);
+#pragma unroll
+    for (int i = 0; i < GP; ++i) {
+        Set& st = ring[i % R];
+        __builtin_amdgcn_sched_barrier(0);
+        const int row = (g0 + i) * 64 + lane;
+        const float gv = row < a.rows ? st.gy : 0.f;
+        P::template tacc<0>(st.c0, st.tm, gv, acc, off);
+        P::template tacc<1>(st.c1, st.tm, gv, acc + 32, off + 2);
+        __builtin_amdgcn_sched_barrier(0);
+        if (i + R < GP) load(i + R, ring[i % R]);
+    }
+
+    // Reduce-scatter over the 64 lanes: at mask m each lane keeps half of its
+    // 2m values and adds its partner's copy of that half; lane l ends with
+    // column l of this wave's 64.
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+        const bool hi = (lane & m) != 0;
+#pragma unroll
+        for (int i = 0; i < m; ++i) {
+            const float keep = hi ? acc[i + m] : acc[i];
+            const float send = hi ? acc[i] : acc[i + m];
+            acc[i] = keep + __shfl_xor(send, m, 64);
+        }
+    }
+    // Group offsets: column l is in local group l >> 4 = 2*bit5 + bit4.
+    {
+        const bool hi = (lane & 32) != 0;
+        const float k0 = hi ? off[2] : off[0], s0 = hi ? off[0] : off[2];
+        const float k1 = hi ? off[3] : off[1], s1 = hi ? off[1] : off[3];
+        off[0] = k0 + __shfl_xor(s0, 32, 64);
+        off[1] = k1 + __shfl_xor(s1, 32, 64);
+    }
+    float o = (lane & 16) ? off[1] : off[0];
+    const float os = (lane & 16) ? off[0] : off[1];
+    o += __shfl_xor(os, 16, 64);
+#pragma unroll
+    for (int m = 8; m >= 1; m >>= 1) o += __shfl_xor(o, m, 64);
+
+    const float total = acc[0] + o;
+    const int64_t col = int64_t(sb) * 256 + jp * 64 + lane;
+    float* gxb = gx + int64_t(b) * cols;
+    if (nslices == 1) {
+        gxb[col] += total;
+        return;
+    }
+    // Several slices: publish this slice's partial through cache-bypassing
+    // agent-scope stores, then the last block of this (super-block, batch
+    // row) to arrive adds the slices in slice order and resets the ticket.
+    float* pb = part + int64_t(b) * nslices * cols;
+    __hip_atomic_store(pb + int64_t(slice) * cols + col, total, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_s_waitcnt(0);
+    __shared__ uint32_t is_last;
+    __syncthreads();
+    uint32_t* tk = tickets + int64_t(b) * a.nsb + sb;
+    if (threadIdx.x == 0)
+        is_last = __hip_atomic_fetch_add(tk, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == uint32_t(nslices - 1);
+    __syncthreads();
+    if (!is_last) return;
+    gxb[col] += sum_partials<32>(pb + col, cols, nslices);
+    if (threadIdx.x == 0) __hip_atomic_store(tk, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Row-group slices for `batch` rows: about 512 blocks; each slice takes GP
+// (1, 2, 4 or 8) row groups.
+int rplt_blocks() {
+    static const int v = env_int("WV_RPLT_BLOCKS", 512);
+    return v;
+}
+
+void rpl_t_plan(const RplArgs& a, int batch, int& slices, int& g_per) {
+    const int64_t per_slice = int64_t(a.nsb) * std::max(1, batch);
+    const int64_t target = rplt_blocks();
+    const int64_t s = std::min<int64_t>(a.rg_count, std::max<int64_t>(1, (target + per_slice - 1) / per_slice));
+    const int64_t need = (a.rg_count + s - 1) / s;
+    g_per = need <= 1 ? 1 : need <= 2 ? 2 : need <= 4 ? 4 : 8;
+    slices = int((a.rg_count + g_per - 1) / g_per);
+}
+
+template <class P>
+int launch_rpl_tr(const DevBlob& bl, const float* gy, float* gx, int batch, hipStream_t s) {
+    const RplArgs& a = bl.rpl;
+    const int64_t cols = int64_t(a.nsb) * 256;
+    for (int b0 = 0; b0 < batch; b0 += kRplTMaxBatch) {
+        const int nb = std::min(kRplTMaxBatch, batch - b0);
+        int slices = 1, g_per = 1;
+        rpl_t_plan(a, nb, slices, g_per);
+        auto kern = g_per == 1 ? k_gemvt_rpl<P, 1> : g_per == 2 ? k_gemvt_rpl<P, 2> : g_per == 4 ? k_gemvt_rpl<P, 4> : k_gemvt_rpl<P, 8>;
+        dim3 grid(unsigned(a.nsb), unsigned(slices), unsigned(nb));
+        hipLaunchKernelGGL(kern, grid, dim3(256), 0, s, a, gy + int64_t(b0) * a.rows, gx + int64_t(b0) * cols,
+                           bl.rpl_t_partial, bl.rpl_t_tickets);
+    }
+    return int(hipGetLastError());
+}
+
 }  // namespace
 
 int launch_rpl(const DevBlob& b, const float* d_x, float* d_y, int batch, void* stream) {
@@ -441,6 +725,27 @@ int launch_rpl(const DevBlob& b, const float* d_x, float* d_y, int batch, void* 
     case FMT_Q6_K: return launch_rpl_t<RplQ6K>(b, d_x, d_y, batch, s);
     case FMT_Q8_0: return launch_rpl_t<RplQ8>(b, d_x, d_y, batch, s);
     case FMT_Q4_0: return launch_rpl_t<RplQ4>(b, d_x, d_y, batch, s);
+    default: return int(hipErrorInvalidValue);
+    }
+}
+
+size_t rpl_t_scratch_floats(const RplArgs& a) {
+    size_t most = 0;
+    for (int nb = 1; nb <= kRplTMaxBatch; ++nb) {
+        int slices = 1, g_per = 1;
+        rpl_t_plan(a, nb, slices, g_per);
+        if (slices > 1) most = std::max(most, size_t(slices) * size_t(nb) * size_t(a.nsb) * 256);
+    }
+    return most;
+}
+
+int launch_rpl_matvec_t(const DevBlob& b, const float* d_gy, float* d_gx, int batch, void* stream) {
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    switch (b.fmt) {
+    case FMT_Q4_K: return launch_rpl_tr<TQ4K>(b, d_gy, d_gx, batch, s);
+    case FMT_Q6_K: return launch_rpl_tr<TQ6K>(b, d_gy, d_gx, batch, s);
+    case FMT_Q8_0: return launch_rpl_tr<TQ8>(b, d_gy, d_gx, batch, s);
+    case FMT_Q4_0: return launch_rpl_tr<TQ4>(b, d_gy, d_gx, batch, s);
     default: return int(hipErrorInvalidValue);
     }
 }

@@ -365,13 +365,22 @@ int wv_blob_upload(int format, int64_t rows, int64_t cols, int32_t block_weights
     }
     // K-split scratch for the row-interleaved path: partial sums and arrival
     // tickets (zeroed here; the last block of each row group re-zeroes its ticket).
-    size_t o_part = 0, o_ctr = 0, weight_bytes = img.bytes.size();
+    size_t o_part = 0, o_ctr = 0, o_tpart = 0, o_tctr = 0, weight_bytes = img.bytes.size();
     if (b.layout == LAYOUT_RPL) {
         const int64_t rg = (rows + 63) / 64, nsb = cols / 256;
         b.rpl_max_batch = 8;
         b.rpl_max_split = int(std::max<int64_t>(1, (nsb + 3) / 4));
         o_part = img.add(size_t(b.rpl_max_batch) * b.rpl_max_split * rg * 64 * sizeof(float));
         o_ctr = img.add(size_t(b.rpl_max_batch) * rg * sizeof(uint32_t));
+        RplArgs shape{};
+        shape.rows = int(rows);
+        shape.nsb = int(nsb);
+        shape.rg_count = int(rg);
+        const size_t tf = rpl_t_scratch_floats(shape);
+        if (tf) {
+            o_tpart = img.add(tf * sizeof(float));
+            o_tctr = img.add(size_t(kRplTMaxBatch) * nsb * sizeof(uint32_t));
+        }
     }
     rc = upload_image(img, b);
     if (rc) return rc;
@@ -394,6 +403,10 @@ int wv_blob_upload(int format, int64_t rows, int64_t cols, int32_t block_weights
         r.nsb = int(cols / 256);
         r.rg_count = int((rows + 63) / 64);
         r.ksplit = 1;
+        if (o_tpart) {
+            b.rpl_t_partial = reinterpret_cast<float*>(base + o_tpart);
+            b.rpl_t_tickets = reinterpret_cast<uint32_t*>(base + o_tctr);
+        }
     }
     std::lock_guard<std::mutex> lk(g_mu);
     const uint64_t h = g_next++;
@@ -454,10 +467,16 @@ int wv_matvec_t_dev(uint64_t handle, const float* d_gy, float* d_gx, int32_t bat
     DevBlob b;
     if (!lookup(handle, b)) return fail(WV_E_HANDLE, "MatVecT: unknown handle %llu", (unsigned long long)handle);
     if (!d_gy || !d_gx) return fail(WV_E_ARG, "MatVecT: nil gy/gx");
-    if (b.layout != LAYOUT_RAW)
-        return fail(WV_E_FORMAT, "quant: MatVecT not implemented on the resident %s layout (upload with WV_FORCE_RAW=1)", fmt_name(b.fmt));
+    if (b.layout == LAYOUT_TERNARY_I8)
+        return fail(WV_E_FORMAT, "quant: MatVecT not implemented for %s", fmt_name(b.fmt));
+    if (batch <= 0) return WV_OK;
     hipSetDevice(b.device);
     hipStream_t s = stream_or_default(stream, b.device);
+    if (b.layout == LAYOUT_RPL) {
+        const int k = launch_matvec_t(b, d_gy, d_gx, batch, s, nullptr);
+        if (k != hipSuccess) return hip_fail(hipError_t(k), "MatVecT: kernel launch");
+        return WV_OK;
+    }
     float* part = nullptr;
     const size_t nf = matvec_t_scratch_floats(b, batch);
     hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&part), std::max<size_t>(nf, 1) * sizeof(float), s);

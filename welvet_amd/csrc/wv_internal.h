@@ -99,6 +99,8 @@ struct RplArgs {
     int rows, nsb, rg_count, ksplit;
 };
 
+constexpr int kRplTMaxBatch = 16;  // batch rows per MatVecT launch on LAYOUT_RPL
+
 // Device view of one blob. Pointers are into one hipMalloc'd allocation.
 struct DevBlob {
     int fmt = 0;
@@ -119,6 +121,8 @@ struct DevBlob {
     RplArgs rpl{};
     int rpl_max_split = 1;  // capacity of rpl.partial per batch row
     int rpl_max_batch = 1;  // batch rows one split launch can carry
+    float* rpl_t_partial = nullptr;    // MatVecT slice partials [batch][slice][cols]
+    uint32_t* rpl_t_tickets = nullptr;  // MatVecT arrival tickets [batch][nsb], zero between launches
     void* base = nullptr;   // allocation owner
     size_t device_bytes = 0;  // weight bytes (excludes scratch)
 };
@@ -127,6 +131,12 @@ struct DevBlob {
 int launch_rpl(const DevBlob& b, const float* d_x, float* d_y, int batch, void* stream);
 int launch_matvec(const DevBlob& b, const float* d_x, float* d_y, int batch, void* stream);
 int launch_matvec_t(const DevBlob& b, const float* d_gy, float* d_gx, int batch, void* stream, float* d_scratch);
+// MatVecT on LAYOUT_RPL uses the blob's own scratch (rpl_t_partial / rpl_t_tickets).
+int launch_rpl_matvec_t(const DevBlob& b, const float* d_gy, float* d_gx, int batch, void* stream);
+// Partial floats that scratch needs (batch rows are taken kRplTMaxBatch per launch).
+size_t rpl_t_scratch_floats(const RplArgs& a);
+// gx[b][c] += sum_k part[(b*nsplit + k)*cols + c], k ascending.
+void launch_gemvt_reduce(const float* part, float* gx, int64_t cols, int nsplit, int batch, void* stream);
 size_t matvec_t_scratch_floats(const DevBlob& b, int batch);
 int launch_ternary_acc(const DevBlob& b, const float* d_x, int32_t* d_acc, float* d_act_scale, int batch, void* stream);
 
