@@ -124,6 +124,20 @@ int wv_matvec_dev(uint64_t handle, const float *d_x, float *d_y, int32_t batch, 
 int wv_ternary_acc_dev(uint64_t handle, const float *d_x, int32_t *d_acc, float *d_act_scale,
                        int32_t batch, void *stream);
 
+/* ---- batched prefill: M token rows through the same Dense layer ---- */
+
+/* Y[M*rows] = X[M*cols] W^T for a block of M token rows (Y overwritten).
+ * Replaces forwardSIMDBlockFused (layers/dense/simd_block.go:17-39) and the
+ * batch loop of forwardSIMDQ4_0 (layers/dense/simd.go:294-299), which run M
+ * independent GEMVs. Row-interleaved Q4_K blobs use fp16 MFMA with f32
+ * accumulation (results within 2e-3 normwise of the f64 reference, not the
+ * 1e-5 of wv_matvec); every other blob runs the batched GEMV kernels of
+ * wv_matvec_dev. Device pointers, enqueued on `stream`. */
+int wv_matmul_dev(uint64_t handle, const float *d_x, float *d_y, int32_t m, void *stream);
+
+/* Host-pointer form of wv_matmul_dev; synchronous. */
+int wv_matmul(uint64_t handle, const float *x, float *y, int32_t m);
+
 /* ---- backward: quant.MatVecT ---- */
 
 /* gx[batch*cols] += W^T gy[batch*rows] (gx NOT zeroed, quant/matvec_t.go:3-5).

@@ -1,0 +1,106 @@
+"""GPU parity of the batched prefill (wv_matmul*) through the C ABI.
+
+Row-interleaved Q4_K blobs run the fp16-MFMA GEMM; the bar there is the
+north-star's bf16/fp16-MFMA tolerance: max|Y - Y_ref| / max|Y_ref| <= 2e-3
+against the f64 textbook product over the reference's dequantized weights
+(which is what welvet's M independent f64-accumulated GEMVs compute, up to
+one f32 rounding). Blobs without an MFMA kernel run the batched GEMV kernels
+and keep the GEMV bar of 1e-5.
+"""
+import numpy as np
+import pytest
+
+import oracle
+import welvet_amd as wv
+
+pytestmark = pytest.mark.gpu
+
+TOL_MFMA = 2e-3
+TOL_F32 = 1e-5
+
+
+@pytest.fixture(scope="module", autouse=True)
+def device():
+    print(f"[gpu] {__name__}: init device 0", flush=True)
+    wv.init(0)
+    yield
+
+
+def normwise(y, ref):
+    ref = np.asarray(ref, np.float64)
+    return float(np.abs(np.asarray(y, np.float64) - ref).max() / max(np.abs(ref).max(), 1e-30))
+
+
+def rowwise(y, ref):
+    ref = np.asarray(ref, np.float64)
+    err = np.abs(np.asarray(y, np.float64) - ref).max(axis=1)
+    return float((err / np.maximum(np.abs(ref).max(axis=1), 1e-30)).max())
+
+
+def packed_q4k(rows, cols, seed):
+    rng = np.random.default_rng(seed)
+    w = (rng.standard_normal(rows * cols, dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+    p = wv.pack("Q4_K", w, rows, cols)
+    wd = oracle.unpack(oracle.Packed(p.fmt, rows, cols, p.raw, p.scales, p.meta, p.block_weights))
+    return p, wd.reshape(rows, cols).astype(np.float64), rng
+
+
+@pytest.mark.parametrize("shape", [(256, 1024), (200, 512), (64, 256), (448, 2048)])
+@pytest.mark.parametrize("m", [1, 7, 32, 33, 64, 65, 128, 130])
+def test_prefill_q4k_small(shape, m):
+    rows, cols = shape
+    print(f"[gpu] prefill q4k {cols}->{rows} M={m}", flush=True)
+    p, wd, rng = packed_q4k(rows, cols, rows + m)
+    d = wv.upload(p)
+    assert d.info()["layout"] == "row-interleaved"
+    x = rng.standard_normal((m, cols)).astype(np.float32)
+    ref = x.astype(np.float64) @ wd.T
+    for _ in range(2):  # split-K scratch is per call; results must not depend on the previous call
+        y = d.matmul(x)
+        assert normwise(y, ref) <= TOL_MFMA
+        assert rowwise(y, ref) <= 4 * TOL_MFMA
+    d.free()
+
+
+_BASE = {}
+
+
+@pytest.mark.parametrize("shape", [(14336, 4096), (4096, 14336)])
+@pytest.mark.parametrize("m", [32, 128, 512])
+def test_prefill_q4k_baseline(shape, m):
+    """Q4_K 4096->14336 and 14336->4096 at M = 32, 128, 512."""
+    import torch
+    rows, cols = shape
+    print(f"[gpu] prefill baseline q4k {cols}->{rows} M={m}", flush=True)
+    if shape not in _BASE:
+        _BASE.clear()
+        p, wd, _ = packed_q4k(rows, cols, 4242)
+        _BASE[shape] = (p, wd.T.copy(), wv.upload(p))
+    p, wdt, d = _BASE[shape]
+    rng = np.random.default_rng(m)
+    x = rng.standard_normal((m, cols)).astype(np.float32)
+    ref = x.astype(np.float64) @ wdt
+    tx = torch.from_numpy(x).cuda()
+    ty = torch.empty((m, rows), device="cuda")
+    torch.cuda.synchronize()
+    d.matmul_dev(tx.data_ptr(), ty.data_ptr(), m)
+    wv.sync()
+    y = ty.cpu().numpy()
+    err = normwise(y, ref)
+    print(f"[gpu]   normwise err {err:.3e}", flush=True)
+    assert err <= TOL_MFMA
+
+
+@pytest.mark.parametrize("fmt", ["Q8_0", "Q6_K", "IQ4_NL"])
+def test_prefill_other_formats_use_batched_gemv(fmt):
+    rows, cols, m = 300, 1024, 9
+    print(f"[gpu] prefill {fmt} via batched gemv", flush=True)
+    rng = np.random.default_rng(5)
+    w = (rng.standard_normal(rows * cols) * 0.02).astype(np.float32)
+    p = wv.pack(fmt, w, rows, cols)
+    d = wv.upload(p)
+    x = rng.standard_normal((m, cols)).astype(np.float32)
+    op = oracle.Packed(p.fmt, rows, cols, p.raw, p.scales, p.meta, p.block_weights)
+    ref = oracle.reference_y(op, x)
+    assert normwise(d.matmul(x), ref) <= TOL_F32
+    d.free()

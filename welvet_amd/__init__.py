@@ -33,7 +33,7 @@ EXPORTS = (
     "wv_init", "wv_last_error", "wv_version", "wv_pack_sizes", "wv_pack",
     "wv_pack_native_ternary", "wv_blob_upload", "wv_blob_free", "wv_blob_info",
     "wv_matvec", "wv_matvec_dev", "wv_ternary_acc_dev", "wv_matvec_t",
-    "wv_matvec_t_dev", "wv_sync",
+    "wv_matvec_t_dev", "wv_matmul", "wv_matmul_dev", "wv_sync",
 )
 
 
@@ -72,6 +72,8 @@ def lib():
     L.wv_ternary_acc_dev.argtypes = [ctypes.c_uint64, _P, _P, _P, ctypes.c_int32, _P]
     L.wv_matvec_t.argtypes = [ctypes.c_uint64, _P, _P, ctypes.c_int32]
     L.wv_matvec_t_dev.argtypes = [ctypes.c_uint64, _P, _P, ctypes.c_int32, _P]
+    L.wv_matmul.argtypes = [ctypes.c_uint64, _P, _P, ctypes.c_int32]
+    L.wv_matmul_dev.argtypes = [ctypes.c_uint64, _P, _P, ctypes.c_int32, _P]
     L.wv_sync.argtypes = [_P]
     _lib = L
     return L
@@ -188,6 +190,17 @@ class DeviceBlob:
         out = np.zeros((batch, self.cols), np.float32) if gx is None else np.array(gx, np.float32, copy=True).reshape(batch, self.cols)
         check(lib().wv_matvec_t(self.handle, gy.ctypes.data, out.ctypes.data, batch))
         return out.reshape(self.cols) if gy.ndim == 1 else out
+
+    def matmul(self, x: np.ndarray) -> np.ndarray:
+        """Host path of the batched prefill: Y = X W^T for X of shape (M, cols)."""
+        x = np.ascontiguousarray(x, np.float32)
+        m = x.size // self.cols
+        y = np.zeros((m, self.rows), np.float32)
+        check(lib().wv_matmul(self.handle, x.ctypes.data, y.ctypes.data, m))
+        return y
+
+    def matmul_dev(self, x_ptr: int, y_ptr: int, m: int, stream: int | None = None) -> None:
+        check(lib().wv_matmul_dev(self.handle, x_ptr, y_ptr, m, stream))
 
     def matvec_dev(self, x_ptr: int, y_ptr: int, batch: int = 1, stream: int | None = None) -> None:
         check(lib().wv_matvec_dev(self.handle, x_ptr, y_ptr, batch, stream))

@@ -1,0 +1,278 @@
+// gemm_rpl.hip — batched prefill on the row-interleaved Q4_K layout:
+// Y[M][rows] = X[M][cols] * W^T with fp16 MFMA (v_mfma_f32_32x32x16_f16) and
+// f32 accumulation. It replaces welvet's M independent GEMVs for a token block
+// (forwardSIMDBlockFused, layers/dense/simd_block.go:17-39), within the 2e-3
+// tolerance of an fp16 contraction.
+//
+// X is first converted once to fp16 (k_x_f16), so the GEMM streams half the
+// bytes for the operand every N-tile re-reads and spends no VALU on it. Global
+// loads run D K-steps ahead of use in a register ring: a step holds only 64
+// columns, so one step of look-ahead would expose a full memory latency per
+// step.
+//
+// Tiles: a block computes BM tokens x 128 output rows (two 64-row groups),
+// stepping K by 64 columns (two 32-column chunks of a super-block), with both
+// operands double-buffered in LDS as fp16 [row][64 + 8 pad]. Per K-step each
+// of the 256 threads dequantizes one (row, chunk) of W: 16 bytes of nibbles
+// -> 32 fp16 weights with packed-half math (0x6400 | q is 1024 + q exactly;
+// subtract 1024, then fma with the group's scale and min), and copies one or
+// more 8-column blocks of fp16 X. Within every 8-column block both operands are
+// stored in the same permuted k order [0,4,1,5,2,6,3,7], the order in which
+// the nibble extraction produces pairs; a dot product over the block does not
+// depend on the order. K is split over gridDim.z when the tile grid alone
+// would leave CUs idle; the splits' partials meet in a fixed-order sum.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+
+#include "wv_internal.h"
+
+namespace wv {
+namespace {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int BN = 128;       // output rows per block (2 row groups)
+constexpr int BK = 64;        // columns per K-step
+constexpr int LDK = BK + 8;   // LDS row stride in halves (144 B: conflict-free 16 B row reads)
+
+__device__ __forceinline__ uint4 ld_nt(const uint4* p) {
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ uint32_t pack_h2(float a, float b) {
+    const half2v h = {_Float16(a), _Float16(b)};
+    return __builtin_bit_cast(uint32_t, h);
+}
+
+// 8 weights of code word v (nibble k = column k) -> 4 half2 in k order
+// [0,4,1,5,2,6,3,7]: w = sc*q + mn computed as fma(q, sc, mn) in fp16.
+__device__ __forceinline__ uint4 dequant8(uint32_t v, half2v sc, half2v mn) {
+    const half2v k1024 = {_Float16(1024.0f), _Float16(1024.0f)};
+    uint32_t p[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t hb = ((v >> (4 * i)) & 0x000F000Fu) | 0x64006400u;
+        const half2v q = __builtin_bit_cast(half2v, hb) - k1024;
+        p[i] = __builtin_bit_cast(uint32_t, q * sc + mn);
+    }
+    return make_uint4(p[0], p[1], p[2], p[3]);
+}
+
+struct GemmArgs {
+    RplArgs w;
+    const uint4* xh;  // [M][K/8] fp16 8-column blocks in permuted k order
+    float* y;         // [M][rows] (splits == 1) or partials [split][M][rows]
+    int M, K;
+    int sb_per_split;
+};
+
+// X f32 [n8 blocks of 8] -> fp16 blocks in k order [0,4,1,5,2,6,3,7].
+__global__ void __launch_bounds__(256) k_x_f16(const float4* __restrict__ x, uint4* __restrict__ xh, int64_t n8) {
+    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= n8) return;
+    const float4 lo = x[2 * i], hi = x[2 * i + 1];
+    xh[i] = make_uint4(pack_h2(lo.x, hi.x), pack_h2(lo.y, hi.y), pack_h2(lo.z, hi.z), pack_h2(lo.w, hi.w));
+}
+
+template <int BM, int WM, int D>
+__global__ void __launch_bounds__(256) k_gemm_q4k(GemmArgs ga) {
+    constexpr int WN = 4 / WM;
+    constexpr int TM = BM / WM / 32, TN = BN / WN / 32;
+    constexpr int XB = BM * (BK / 8) / 256;  // 8-column X blocks per thread per K-step
+    static_assert(XB >= 1, "BM too small");
+    static_assert(4 % D == 0, "D must divide the 4 K-steps of a super-block");
+    __shared__ __attribute__((aligned(16))) _Float16 xs[2][BM * LDK];
+    __shared__ __attribute__((aligned(16))) _Float16 ws[2][BN * LDK];
+
+    const RplArgs& a = ga.w;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int wm = wave / WN, wn = wave % WN;
+    const int nblk = blockIdx.x, mblk = blockIdx.y, split = blockIdx.z;
+    const int sb0 = split * ga.sb_per_split;
+    const int sb1 = min(a.nsb, sb0 + ga.sb_per_split);
+    const int steps = (sb1 - sb0) * 4;
+    const int64_t nsb_total = int64_t(a.rg_count) * a.nsb;
+    const int kb8 = ga.K / 8;
+
+    // This thread's W slot: row group gl of the block, chunk jj of the step.
+    const int gl = (t >> 6) & 1, jj = t >> 7;
+    const int g = min(nblk * 2 + gl, a.rg_count - 1);
+    const int wrow = gl * 64 + lane;
+
+    struct Regs {
+        uint4 c;
+        uint32_t meta;
+        float2 dd;
+        uint4 xv[XB];
+    };
+    auto load = [&](int s, Regs& r) {
+        const int sb = sb0 + s / 4, j = 2 * (s & 3) + jj;
+        const int64_t si = int64_t(g) * a.nsb + sb;
+        r.c = ld_nt(reinterpret_cast<const uint4*>(a.codes) + (int64_t(j) * nsb_total + si) * 64 + lane);
+        r.meta = reinterpret_cast<const uint32_t*>(a.meta)[(si * 64 + lane) * 8 + j];
+        r.dd = reinterpret_cast<const float2*>(a.dd)[si * 64 + lane];
+        const int k8 = sb * 32 + (s & 3) * 8;
+#pragma unroll
+        for (int i = 0; i < XB; ++i) {
+            const int f = t + 256 * i, m = min(mblk * BM + f / 8, ga.M - 1);
+            r.xv[i] = ga.xh[int64_t(m) * kb8 + k8 + f % 8];
+        }
+    };
+    auto store = [&](const Regs& r, int buf) {
+        // W: 32 weights of row wrow, columns 32*jj .. 32*jj+31 of the step.
+        const uint32_t gm = r.meta;  // (u'0, u'1, m0, m1)
+        const float d255 = r.dd.x * (1.0f / 255.0f), dm127 = r.dd.y * (1.0f / 127.0f);
+        const _Float16 sc0 = _Float16(d255 * float(gm & 0xFFu)), sc1 = _Float16(d255 * float((gm >> 8) & 0xFFu));
+        const _Float16 mn0 = _Float16(dm127 * float(int8_t(gm >> 16))), mn1 = _Float16(dm127 * float(int32_t(gm) >> 24));
+        const half2v s0 = {sc0, sc0}, s1 = {sc1, sc1}, n0 = {mn0, mn0}, n1 = {mn1, mn1};
+        uint4* wd = reinterpret_cast<uint4*>(&ws[buf][wrow * LDK + 32 * jj]);
+        wd[0] = dequant8(r.c.x, s0, n0);
+        wd[1] = dequant8(r.c.y, s0, n0);
+        wd[2] = dequant8(r.c.z, s1, n1);
+        wd[3] = dequant8(r.c.w, s1, n1);
+#pragma unroll
+        for (int i = 0; i < XB; ++i) {
+            const int f = t + 256 * i;
+            *reinterpret_cast<uint4*>(&xs[buf][(f / 8) * LDK + 8 * (f % 8)]) = r.xv[i];
+        }
+    };
+
+    f32x16 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    // D register slots; slot d holds step s with s % D == d. Loads are
+    // unconditional (indices clamped to the last step) so that every wait
+    // is an exact count.
+    // The scheduling barriers keep every slot's loads in program order, in
+    // the prologue as in the loop: if the two orders differ, the wait at the
+    // loop head becomes a wait for all outstanding loads.
+    Regs ring[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        load(min(d, steps - 1), ring[d]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    for (int s0 = 0; s0 < steps; s0 += D) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            const int s = s0 + d, buf = s & 1;
+            store(ring[d], buf);
+            __builtin_amdgcn_sched_barrier(0);
+            load(min(s + D, steps - 1), ring[d]);
+            __builtin_amdgcn_sched_barrier(0);
+            __syncthreads();
+#pragma unroll
+            for (int ks = 0; ks < BK / 16; ++ks) {
+                half8 af[TM], bf[TN];
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+                    af[i] = *reinterpret_cast<const half8*>(
+                        &xs[buf][(wm * (BM / WM) + i * 32 + (lane & 31)) * LDK + ks * 16 + 8 * (lane >> 5)]);
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    bf[j] = *reinterpret_cast<const half8*>(
+                        &ws[buf][(wn * (BN / WN) + j * 32 + (lane & 31)) * LDK + ks * 16 + 8 * (lane >> 5)]);
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+            }
+        }
+    }
+
+    // C[i][j] of a 32x32 tile: lane holds j = lane % 32, i = 8*(r/4) + 4*(lane/32) + r%4.
+    float* out = ga.y + int64_t(split) * ga.M * a.rows;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const int n = nblk * BN + wn * (BN / WN) + j * 32 + (lane & 31);
+            if (n >= a.rows) continue;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int m = mblk * BM + wm * (BM / WM) + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                if (m < ga.M) out[int64_t(m) * a.rows + n] = acc[i][j][r];
+            }
+        }
+}
+
+// y[i] = sum_k part[k*n + i], k ascending.
+__global__ void __launch_bounds__(256) k_split_sum(const float* __restrict__ part, float* __restrict__ y, int64_t n,
+                                                  int splits) {
+    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= n) return;
+    float s = 0.f;
+    for (int k = 0; k < splits; ++k) s += part[int64_t(k) * n + i];
+    y[i] = s;
+}
+
+template <int BM, int WM>
+void launch_bm(const GemmArgs& ga, dim3 grid, hipStream_t s) {
+    hipLaunchKernelGGL((k_gemm_q4k<BM, WM, 4>), grid, dim3(256), 0, s, ga);
+}
+
+}  // namespace
+
+bool gemm_supported(const DevBlob& b) { return b.layout == LAYOUT_RPL && b.fmt == FMT_Q4_K; }
+
+void gemm_plan(const DevBlob& b, int M, int& bm, int& splits, int& sb_per_split) {
+    const RplArgs& a = b.rpl;
+    bm = M <= 32 ? 32 : M <= 64 ? 64 : 128;
+    const int64_t tiles = int64_t((a.rows + BN - 1) / BN) * ((M + bm - 1) / bm);
+    // Split K only while the tile grid alone leaves CUs idle (~384 blocks fill
+    // the 256 CUs at the 1-2 blocks each that the register/LDS budget allows).
+    int want = int(std::max<int64_t>(1, (384 + tiles - 1) / tiles));
+    want = std::min(want, std::max(1, a.nsb / 2));  // each split >= 2 super-blocks
+    sb_per_split = (a.nsb + want - 1) / want;
+    splits = (a.nsb + sb_per_split - 1) / sb_per_split;
+}
+
+// Scratch floats: the fp16 copy of X (M*K halves) followed by the split-K partials.
+size_t gemm_scratch_floats(const DevBlob& b, int M) {
+    int bm = 0, splits = 1, per = 0;
+    gemm_plan(b, M, bm, splits, per);
+    const size_t xh = (size_t(M) * size_t(b.cols) / 2 + 63) / 64 * 64;
+    return xh + (splits > 1 ? size_t(splits) * size_t(M) * size_t(b.rows) : 0);
+}
+
+int launch_gemm(const DevBlob& b, const float* d_x, float* d_y, int M, void* stream, float* d_scratch) {
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (!gemm_supported(b) || !d_scratch) return int(hipErrorInvalidValue);
+    int bm = 0, splits = 1, per = 0;
+    gemm_plan(b, M, bm, splits, per);
+    const int64_t n8 = int64_t(M) * b.cols / 8;
+    uint4* xh = reinterpret_cast<uint4*>(d_scratch);
+    float* part = d_scratch + (size_t(M) * size_t(b.cols) / 2 + 63) / 64 * 64;
+    hipLaunchKernelGGL(k_x_f16, dim3(unsigned((n8 + 255) / 256)), dim3(256), 0, s, reinterpret_cast<const float4*>(d_x),
+                       xh, n8);
+    GemmArgs ga;
+    ga.w = b.rpl;
+    ga.xh = xh;
+    ga.y = splits > 1 ? part : d_y;
+    ga.M = M;
+    ga.K = int(b.cols);
+    ga.sb_per_split = per;
+    dim3 grid(unsigned((b.rows + BN - 1) / BN), unsigned((M + bm - 1) / bm), unsigned(splits));
+    if (bm == 32) launch_bm<32, 1>(ga, grid, s);
+    else if (bm == 64) launch_bm<64, 2>(ga, grid, s);
+    else launch_bm<128, 2>(ga, grid, s);
+    if (splits > 1) {
+        const int64_t n = int64_t(M) * b.rows;
+        hipLaunchKernelGGL(k_split_sum, dim3(unsigned((n + 255) / 256)), dim3(256), 0, s, part, d_y, n, splits);
+    }
+    return int(hipGetLastError());
+}
+
+}  // namespace wv

@@ -487,6 +487,58 @@ int wv_matvec_t_dev(uint64_t handle, const float* d_gy, float* d_gx, int32_t bat
     return WV_OK;
 }
 
+int wv_matmul_dev(uint64_t handle, const float* d_x, float* d_y, int32_t m, void* stream) {
+    DevBlob b;
+    if (!lookup(handle, b)) return fail(WV_E_HANDLE, "MatMul: unknown handle %llu", (unsigned long long)handle);
+    if (!d_x || !d_y) return fail(WV_E_ARG, "MatMul: nil x/y");
+    if (m < 0) return fail(WV_E_ARG, "MatMul: negative row count %d", m);
+    if (m == 0) return WV_OK;
+    hipSetDevice(b.device);
+    hipStream_t s = stream_or_default(stream, b.device);
+    if (!gemm_supported(b)) {
+        const int k = launch_matvec(b, d_x, d_y, m, s);
+        if (k != hipSuccess) return hip_fail(hipError_t(k), "MatMul: kernel launch");
+        return WV_OK;
+    }
+    float* part = nullptr;
+    const size_t nf = gemm_scratch_floats(b, m);
+    if (nf) {
+        hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&part), nf * sizeof(float), s);
+        if (e != hipSuccess) return hip_fail(e, "MatMul: split-K scratch");
+    }
+    const int k = launch_gemm(b, d_x, d_y, m, s, part);
+    if (part) hipFreeAsync(part, s);
+    if (k != hipSuccess) return hip_fail(hipError_t(k), "MatMul: kernel launch");
+    return WV_OK;
+}
+
+int wv_matmul(uint64_t handle, const float* x, float* y, int32_t m) {
+    DevBlob b;
+    if (!lookup(handle, b)) return fail(WV_E_HANDLE, "MatMul: unknown handle %llu", (unsigned long long)handle);
+    if (!x || !y) return fail(WV_E_ARG, "MatMul: nil x/y");
+    if (m <= 0) return m < 0 ? fail(WV_E_ARG, "MatMul: negative row count %d", m) : WV_OK;
+    hipSetDevice(b.device);
+    hipStream_t s = g_dev[b.device].stream;
+    const size_t nx = size_t(m) * size_t(b.cols), ny = size_t(m) * size_t(b.rows);
+    float *dx = nullptr, *dy = nullptr;
+    hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&dx), nx * 4, s);
+    if (e == hipSuccess) e = hipMallocAsync(reinterpret_cast<void**>(&dy), ny * 4, s);
+    if (e != hipSuccess) return hip_fail(e, "MatMul: staging");
+    int rc = WV_OK;
+    e = hipMemcpyAsync(dx, x, nx * 4, hipMemcpyHostToDevice, s);
+    if (e != hipSuccess) rc = hip_fail(e, "MatMul: copy x");
+    if (!rc) rc = wv_matmul_dev(handle, dx, dy, m, s);
+    if (!rc) {
+        e = hipMemcpyAsync(y, dy, ny * 4, hipMemcpyDeviceToHost, s);
+        if (e != hipSuccess) rc = hip_fail(e, "MatMul: copy y");
+    }
+    hipFreeAsync(dx, s);
+    hipFreeAsync(dy, s);
+    e = hipStreamSynchronize(s);
+    if (!rc && e != hipSuccess) rc = hip_fail(e, "MatMul: sync");
+    return rc;
+}
+
 int wv_matvec(uint64_t handle, const float* x, float* y, int32_t batch) {
     DevBlob b;
     if (!lookup(handle, b)) return fail(WV_E_HANDLE, "MatVec: unknown handle %llu", (unsigned long long)handle);

@@ -131,6 +131,10 @@ struct DevBlob {
 int launch_rpl(const DevBlob& b, const float* d_x, float* d_y, int batch, void* stream);
 int launch_matvec(const DevBlob& b, const float* d_x, float* d_y, int batch, void* stream);
 int launch_matvec_t(const DevBlob& b, const float* d_gy, float* d_gx, int batch, void* stream, float* d_scratch);
+// Batched prefill GEMM (gemm_rpl.hip): fp16 MFMA on the row-interleaved Q4_K layout.
+bool gemm_supported(const DevBlob& b);
+size_t gemm_scratch_floats(const DevBlob& b, int M);
+int launch_gemm(const DevBlob& b, const float* d_x, float* d_y, int M, void* stream, float* d_scratch);
 // MatVecT on LAYOUT_RPL uses the blob's own scratch (rpl_t_partial / rpl_t_tickets).
 int launch_rpl_matvec_t(const DevBlob& b, const float* d_gy, float* d_gx, int batch, void* stream);
 // Partial floats that scratch needs (batch rows are taken kRplTMaxBatch per launch).
