@@ -51,6 +51,11 @@ PREFILL = {
     for (i, o) in ((4096, 14336), (14336, 4096)) for m in (32, 128, 512)
 }
 MFMA_F16_PEAK_TFLOPS = 2500.0
+# 32-layer decoder, hidden 4096, 32/8 heads x 128, SwiGLU 14336, vocab 32000, Q4_K, KV 2048
+DECODE = {
+    "decode_32l": dict(n_layers=32, hidden=4096, n_heads=32, n_kv_heads=8, head_dim=128, ffn=14336, vocab=32000,
+                       kv=2048, distinct_layers=4),
+}
 # Per-dispatch TCC counters of the GEMV kernel (KiB), medians over the timed
 # launches of `rocprofv3 --pmc FETCH_SIZE` and `--pmc WRITE_SIZE` runs of
 # `bench.py --no-cpu --steps 200 --warmup 20 --copy-probe 64 --workload W`.
@@ -121,7 +126,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=200)
-    ap.add_argument("--workload", default="q4k_4096x14336", choices=sorted(WORKLOADS) + sorted(PREFILL))
+    ap.add_argument("--workload", default="q4k_4096x14336",
+                    choices=sorted(WORKLOADS) + sorted(PREFILL) + sorted(DECODE))
     ap.add_argument("--cpu-budget-s", type=float, default=12.0)
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -142,6 +148,8 @@ def main():
 
     if args.workload in PREFILL:
         return prefill_main(args, torch, wv)
+    if args.workload in DECODE:
+        return decode_main(args, wv)
     fmt, rows, cols, desc = WORKLOADS[args.workload]
     ternary = fmt == "NativeTernary"
     print(f"[bench] {desc}: packing", file=sys.stderr, flush=True)
@@ -326,6 +334,114 @@ def prefill_main(args, torch, wv):
             "sample": f"{n} of the M row GEMVs the reference runs for this block (restated fused SIMD path, "
                       f"{threads} row-shard threads), {dt * 1e3:.3f} ms per row"}
     for b in blobs:
+        b.free()
+    print(json.dumps(result), flush=True)
+
+
+def decode_main(args, wv):
+    """One step = one greedy decode token of the whole 32-layer model at KV length 2048."""
+    from welvet_amd.decode import Config, Decoder
+    spec = DECODE[args.workload]
+    kv = spec["kv"]
+    cfg = Config(n_layers=spec["n_layers"], hidden=spec["hidden"], n_heads=spec["n_heads"],
+                 n_kv_heads=spec["n_kv_heads"], head_dim=spec["head_dim"], ffn=spec["ffn"], vocab=spec["vocab"],
+                 max_seq=kv, rope_theta=5e5, rms_eps=1e-5)
+    rng = np.random.default_rng(1234)
+    shapes = [("q", cfg.q_dim, cfg.hidden), ("k", cfg.kv_dim, cfg.hidden), ("v", cfg.kv_dim, cfg.hidden),
+              ("o", cfg.hidden, cfg.q_dim), ("gate", cfg.ffn, cfg.hidden), ("up", cfg.ffn, cfg.hidden),
+              ("down", cfg.hidden, cfg.ffn)]
+    wv.init(0)
+    t0 = time.perf_counter()
+    packed_sets = []
+    for _ in range(spec["distinct_layers"]):
+        ps = []
+        for _, r, c in shapes:
+            w = (rng.standard_normal(r * c, dtype=np.float32) * np.float32(0.02))
+            ps.append(wv.pack("Q4_K", w, r, c))
+        packed_sets.append(ps)
+        print(f"[bench] packed a layer's weights ({time.perf_counter() - t0:.1f} s)", file=sys.stderr, flush=True)
+    wl = rng.standard_normal(cfg.vocab * cfg.hidden, dtype=np.float32) * np.float32(0.02)
+    p_lm = wv.pack("Q4_K", wl, cfg.vocab, cfg.hidden)
+    del wl
+    emb = rng.standard_normal((cfg.vocab, cfg.hidden), dtype=np.float32)
+    dec = Decoder(cfg)
+    blobs = []
+    layer_bytes = sum(p.nbytes for p in packed_sets[0])
+    for L in range(cfg.n_layers):
+        bl = [wv.upload(p) for p in packed_sets[L % len(packed_sets)]]
+        blobs += bl
+        dec.set_layer(L, bl, np.ones(cfg.hidden, np.float32), np.ones(cfg.hidden, np.float32))
+        k = rng.standard_normal((kv - 1, cfg.kv_dim), dtype=np.float32)
+        v = rng.standard_normal((kv - 1, cfg.kv_dim), dtype=np.float32)
+        dec.set_kv(L, 0, k, v)
+    lm = wv.upload(p_lm)
+    dec.set_output(lm, np.ones(cfg.hidden, np.float32), emb)
+    print(f"[bench] model resident ({time.perf_counter() - t0:.1f} s)", file=sys.stderr, flush=True)
+    dec.use_graph(True)
+    pos, tok = kv - 1, 1
+    steps = max(8, min(args.steps, 200))
+    warmup = max(2, min(args.warmup, 10))
+    dec.generate(tok, pos, warmup, advance_pos=False)
+    t1 = time.perf_counter()
+    toks = dec.generate(tok, pos, steps, advance_pos=False)
+    dt = time.perf_counter() - t1
+    tps = steps / dt
+    kv_bytes = cfg.n_layers * 2 * kv * cfg.kv_dim * 4
+    step_bytes = cfg.n_layers * layer_bytes + p_lm.nbytes + kv_bytes
+    gbs = step_bytes * tps / 1e9
+    result = {
+        "metric": "decode tokens/s, 32-layer Q4_K decoder (BASELINE config 5)",
+        "value": round(tps, 2), "unit": "tokens/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "ms_per_step": round(1e3 / tps, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32 (Q4_K weights, f32 activations and KV cache)",
+        "data": (f"synthetic random init: {spec['distinct_layers']} distinct layers of N(0,0.02) Q4_K weights cycled "
+                 f"over {cfg.n_layers} resident layer copies, KV cache N(0,1) for {kv - 1} positions, greedy step at "
+                 f"position {pos} (KV length {kv}) replayed as one HIP graph per token"),
+        "config": {"workload": "32-layer decoder decode step, hidden 4096, 32/8 heads x 128, SwiGLU 14336, "
+                               "vocab 32000, RoPE 5e5, RMSNorm eps 1e-5, KV 2048 f32, batch 1",
+                   "bytes_per_step": step_bytes, "weight_bytes_per_step": step_bytes - kv_bytes,
+                   "kv_bytes_per_step": kv_bytes, "last_tokens": [int(t) for t in toks[-4:]]},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+    }
+    if not args.no_cpu:
+        import oracle
+        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        per_layer = 0.0
+        for p in packed_sets[0]:
+            op = oracle.Packed(p.fmt, p.rows, p.cols, p.raw, p.scales, p.meta, p.block_weights)
+            simd = oracle.SimdPath(op)
+            x = rng.standard_normal(p.cols, dtype=np.float32)
+            simd.matvec(x, nthreads=threads)
+            n, t2 = 0, time.perf_counter()
+            while n < 3:
+                simd.matvec(x, nthreads=threads)
+                n += 1
+            per_layer += (time.perf_counter() - t2) / n
+            simd.close()
+        from oracle import decode_ref
+        kc = rng.standard_normal((kv, cfg.kv_dim))
+        vc = rng.standard_normal((kv, cfg.kv_dim))
+        q = rng.standard_normal(cfg.q_dim)
+        t2 = time.perf_counter()
+        decode_ref.attention(q, kc, vc, kv, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim)
+        per_layer += time.perf_counter() - t2
+        op = oracle.Packed(p_lm.fmt, p_lm.rows, p_lm.cols, p_lm.raw, p_lm.scales, p_lm.meta, p_lm.block_weights)
+        simd = oracle.SimdPath(op)
+        x = rng.standard_normal(p_lm.cols, dtype=np.float32)
+        simd.matvec(x, nthreads=threads)
+        t2 = time.perf_counter()
+        simd.matvec(x, nthreads=threads)
+        lm_t = time.perf_counter() - t2
+        simd.close()
+        tok_s = cfg.n_layers * per_layer + lm_t
+        result["cpu_baseline"] = {
+            "value": round(1.0 / tok_s, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"one layer's 7 projections (restated fused SIMD path, {threads} row-shard threads) and its "
+                      f"f64 attention over {kv} positions, x{cfg.n_layers} layers, plus the LM head: "
+                      f"{tok_s * 1e3:.1f} ms per token"}
+    dec.free()
+    for b in blobs + [lm]:
         b.free()
     print(json.dumps(result), flush=True)
 

@@ -148,6 +148,54 @@ int wv_matvec_t(uint64_t handle, const float *gy, float *gx, int32_t batch);
 /* Device-pointer form of wv_matvec_t. */
 int wv_matvec_t_dev(uint64_t handle, const float *d_gy, float *d_gx, int32_t batch, void *stream);
 
+/* ---- device decode step (greedy), for a decoder whose projections are resident blobs ---- */
+
+/* Dimensions of a decoder (model/transformer config; layers/mha/config.go,
+ * layers/swiglu/config.go, layers/rmsnorm/config.go). head_dim 64 or 128,
+ * n_heads a multiple of n_kv_heads with at most 8 query heads per KV head. */
+typedef struct wv_decoder_config {
+    int32_t n_layers, hidden, n_heads, n_kv_heads, head_dim, ffn, vocab, max_seq;
+    double rope_theta, rms_eps;
+} wv_decoder_config;
+
+/* Creates a decoder: activations, f32 KV caches [max_seq][n_kv_heads*head_dim]
+ * per layer (zeroed) and its own stream on the current device. */
+int wv_decoder_create(const wv_decoder_config *cfg, uint64_t *decoder);
+
+/* Layer `layer`'s projections as resident blobs {Q, K, V, O, gate, up, down}
+ * (shapes as in mha.Layer Q/K/V/O and swiglu.Layer Gate/Up/Down, rows = out)
+ * and its two RMSNorm gammas (host, hidden floats each). The blobs must stay
+ * allocated while the decoder uses them. Replaces the per-layer sequence of
+ * model/transformer/forward.go:55-77. */
+int wv_decoder_set_layer(uint64_t decoder, int32_t layer, const uint64_t *blobs, const float *attn_norm,
+                         const float *ffn_norm);
+
+/* LM head blob (vocab x hidden), final RMSNorm gamma (NULL = no final norm,
+ * forward.go:80-86) and the f32 embedding table (vocab x hidden, host). */
+int wv_decoder_set_output(uint64_t decoder, uint64_t lm_head, const float *final_norm, const float *embedding);
+
+/* Writes KV-cache rows first_pos .. first_pos+n_pos-1 of `layer` (host k, v:
+ * n_pos rows of n_kv_heads*head_dim floats), as the prompt's prefill would. */
+int wv_decoder_set_kv(uint64_t decoder, int32_t layer, int32_t first_pos, int32_t n_pos, const float *k,
+                      const float *v);
+
+/* Non-zero: capture the whole step once into a HIP graph and replay it. */
+int wv_decoder_use_graph(uint64_t decoder, int32_t enable);
+
+/* Runs n_steps greedy decode steps from input `token` at position `pos`:
+ * each step is ForwardTokens for one new token (forward.go:26-90: RMSNorm,
+ * Q/K/V, RoPE, KV append, GQA causal attention, O + residual, RMSNorm, SwiGLU
+ * + residual, final norm, LM head) followed by argmax, whose token feeds the
+ * next step. advance_pos != 0 moves the position on by one per step (real
+ * generation); 0 recomputes position `pos` each step. tokens_out (host,
+ * n_steps, may be NULL) receives the generated tokens, last_logits (host,
+ * vocab, may be NULL) the last step's logits. Synchronous. */
+int wv_decoder_generate(uint64_t decoder, int32_t token, int32_t pos, int32_t n_steps, int32_t advance_pos,
+                        int32_t *tokens_out, float *last_logits);
+
+/* Releases the decoder (not the blobs it references). */
+int wv_decoder_free(uint64_t decoder);
+
 /* ---- streams ---- */
 
 /* Blocks until all work the library enqueued on `stream` (NULL = its own) is done. */

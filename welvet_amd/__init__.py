@@ -34,6 +34,8 @@ EXPORTS = (
     "wv_pack_native_ternary", "wv_blob_upload", "wv_blob_free", "wv_blob_info",
     "wv_matvec", "wv_matvec_dev", "wv_ternary_acc_dev", "wv_matvec_t",
     "wv_matvec_t_dev", "wv_matmul", "wv_matmul_dev", "wv_sync",
+    "wv_decoder_create", "wv_decoder_set_layer", "wv_decoder_set_output", "wv_decoder_set_kv",
+    "wv_decoder_use_graph", "wv_decoder_generate", "wv_decoder_free",
 )
 
 
@@ -75,6 +77,14 @@ def lib():
     L.wv_matmul.argtypes = [ctypes.c_uint64, _P, _P, ctypes.c_int32]
     L.wv_matmul_dev.argtypes = [ctypes.c_uint64, _P, _P, ctypes.c_int32, _P]
     L.wv_sync.argtypes = [_P]
+    L.wv_decoder_create.argtypes = [_P, _P]
+    L.wv_decoder_set_layer.argtypes = [ctypes.c_uint64, ctypes.c_int32, _P, _P, _P]
+    L.wv_decoder_set_output.argtypes = [ctypes.c_uint64, ctypes.c_uint64, _P, _P]
+    L.wv_decoder_set_kv.argtypes = [ctypes.c_uint64, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, _P, _P]
+    L.wv_decoder_use_graph.argtypes = [ctypes.c_uint64, ctypes.c_int32]
+    L.wv_decoder_generate.argtypes = [ctypes.c_uint64, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
+                                      _P, _P]
+    L.wv_decoder_free.argtypes = [ctypes.c_uint64]
     _lib = L
     return L
 

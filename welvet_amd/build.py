@@ -27,7 +27,7 @@ HIP_FLAGS = [
 ]
 CXX_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-pthread", "-ffp-contract=off", "-Wall"]
 
-HIP_SOURCES = ["runtime.hip", "gemv.hip", "gemv_rpl.hip", "gemm_rpl.hip"]
+HIP_SOURCES = ["runtime.hip", "gemv.hip", "gemv_rpl.hip", "gemm_rpl.hip", "decode.hip"]
 CXX_SOURCES = ["pack.cpp"]
 
 

@@ -1,0 +1,800 @@
+// decode.hip — one greedy decode step of welvet's transformer decoder on the
+// device: embedding row, per layer RMSNorm -> Q/K/V GEMVs -> RoPE + KV-cache
+// append -> GQA attention -> O GEMV + residual -> RMSNorm -> gate/up GEMVs
+// with SiLU(gate)*up -> down GEMV + residual; final RMSNorm, LM head, argmax
+// (model/transformer/forward.go:26-90 for one new token; layers/mha/cpu.go,
+// attn.go, rope.go; layers/swiglu/cpu.go; layers/rmsnorm/cpu.go).
+//
+// Everything stays in HBM between kernels. The position and the input token
+// live in device memory, so the whole step can be captured once into a HIP
+// graph and replayed: the step ends by writing its argmax into the input
+// token slot and (optionally) advancing the position, so replays generate
+// tokens with no host round trip. Projections on the row-interleaved layout
+// fold the residual add and SiLU(gate)*up into the GEMV's output store.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/welvet_hip.h"
+#include "rt_internal.h"
+
+namespace wv {
+namespace {
+
+constexpr int kChunk = 64;  // KV positions per attention block
+
+// h = table[token] (embedding lookup, clamped token id). Block 0 also builds
+// this step's RoPE table: angle_d = pos / theta^(2d/hd) with theta^(2d/hd)
+// precomputed on the host as the reference computes it (f64 math.Pow,
+// layers/mha/rope.go:14), cs[d] = (cos, sin) in f64.
+__global__ void __launch_bounds__(256) k_embed(const float* __restrict__ table, const int32_t* __restrict__ tok,
+                                               float* __restrict__ h, int hidden, int vocab,
+                                               const double* __restrict__ freq_div, double2* __restrict__ cs,
+                                               int half, const int32_t* __restrict__ d_pos) {
+    const int t = min(max(*tok, 0), vocab - 1);
+    for (int i = blockIdx.x * 256 + threadIdx.x; i < hidden; i += gridDim.x * 256)
+        h[i] = table[int64_t(t) * hidden + i];
+    if (blockIdx.x == 0) {
+        const double pos = double(*d_pos);
+        for (int d = threadIdx.x; d < half; d += 256) {
+            const double angle = pos / freq_div[d];
+            cs[d] = make_double2(cos(angle), sin(angle));
+        }
+    }
+}
+
+// y = f32((x * inv) * gamma), inv = 1 / sqrt(sum(x^2)/dim + eps) in f64
+// (layers/rmsnorm/cpu.go:70-85). gamma == nullptr means ones. Each thread
+// loads its float4s once (dim % 4 == 0, dim <= 4 * 4096) and keeps them.
+__global__ void __launch_bounds__(1024) k_rmsnorm(const float* __restrict__ x, const float* __restrict__ gamma,
+                                                  float* __restrict__ y, int dim, double eps) {
+    __shared__ double part[16];
+    constexpr int R = 4;
+    const int n4 = dim / 4;
+    float4 xv[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int i = threadIdx.x + 1024 * r;
+        xv[r] = i < n4 ? reinterpret_cast<const float4*>(x)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    double s = 0.0;
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+        s += double(xv[r].x) * xv[r].x + double(xv[r].y) * xv[r].y + double(xv[r].z) * xv[r].z +
+             double(xv[r].w) * xv[r].w;
+    for (int m = 32; m >= 1; m >>= 1) s += __shfl_xor(s, m, 64);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
+    __syncthreads();
+    double tot = 0.0;
+    for (int w = 0; w < 16; ++w) tot += part[w];
+    const double inv = 1.0 / sqrt(tot / double(dim) + eps);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int i = threadIdx.x + 1024 * r;
+        if (i >= n4) break;
+        const float4 g = gamma ? reinterpret_cast<const float4*>(gamma)[i] : make_float4(1.f, 1.f, 1.f, 1.f);
+        float4 o;
+        o.x = float(double(xv[r].x) * inv * double(g.x));
+        o.y = float(double(xv[r].y) * inv * double(g.y));
+        o.z = float(double(xv[r].z) * inv * double(g.z));
+        o.w = float(double(xv[r].w) * inv * double(g.w));
+        reinterpret_cast<float4*>(y)[i] = o;
+    }
+}
+
+// Rotate-half RoPE on q (n_heads) and k (n_kv) with this step's cos/sin
+// table (layers/mha/rope.go:6-21), then append k and v as row pos % max_seq of
+// the layer's cache (layers/mha/cpu.go:178-193). One thread per pair.
+__global__ void __launch_bounds__(256) k_rope_kv(float* __restrict__ q, const float* __restrict__ k,
+                                                 const float* __restrict__ v, float* __restrict__ kc,
+                                                 float* __restrict__ vc, const int32_t* __restrict__ d_pos,
+                                                 const double2* __restrict__ cs, int n_heads, int n_kv, int hd,
+                                                 int max_seq) {
+    const int pos = *d_pos;
+    const int half = hd / 2;
+    const int kv_dim = n_kv * hd;
+    const int64_t row = int64_t(pos % max_seq) * kv_dim;
+    const int nq = n_heads * half, nk = n_kv * half;
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < nq + nk) {
+        const bool isq = i < nq;
+        const int j = isq ? i : i - nq;
+        const int h = j / half, d = j % half;
+        const double2 r = cs[d];
+        const float* src = isq ? q + h * hd : k + h * hd;
+        const double v0 = src[d], v1 = src[d + half];
+        const float o0 = float(v0 * r.x - v1 * r.y), o1 = float(v0 * r.y + v1 * r.x);
+        if (isq) {
+            q[h * hd + d] = o0;
+            q[h * hd + d + half] = o1;
+        } else {
+            kc[row + h * hd + d] = o0;
+            kc[row + h * hd + d + half] = o1;
+        }
+    }
+    for (int e = i; e < kv_dim; e += gridDim.x * 256) vc[row + e] = v[e];
+}
+
+// Flash-decoding partials for one KV head and one chunk of kChunk positions:
+// the G = n_heads / n_kv query heads that share the KV head read its K and V
+// rows once (layers/mha/attn.go:40-118: score = q.k * scale over the causal
+// positions kPos <= pos, max-subtracted softmax, sum of p * v). Per (head,
+// chunk) it writes o[HD] (unnormalised), the chunk max m and sum l.
+template <int HD>
+__global__ void __launch_bounds__(256) k_attn_part(const float* __restrict__ q, const float* __restrict__ kc,
+                                                   const float* __restrict__ vc, const int32_t* __restrict__ d_pos,
+                                                   float* __restrict__ part, int n_heads, int n_kv, int max_seq,
+                                                   int n_chunks, float scale) {
+    constexpr int LD = HD + 1;
+    __shared__ float tile[kChunk * LD];
+    __shared__ __attribute__((aligned(16))) float es[8][kChunk];
+    extern __shared__ float qs[];  // [G][HD]
+    const int kvh = blockIdx.x, c = blockIdx.y;
+    const int G = n_heads / n_kv;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int kv_len = min(*d_pos + 1, max_seq);
+    const int p0 = c * kChunk;
+    const int nvalid = min(kChunk, kv_len - p0);
+    const int kv_dim = n_kv * HD;
+    if (nvalid <= 0) {
+        for (int g = wave; g < G; g += 4) {
+            float* o = part + (int64_t(kvh * G + g) * n_chunks + c) * (HD + 2);
+            if (lane == 0) {
+                o[HD] = -INFINITY;
+                o[HD + 1] = 0.f;
+            }
+        }
+        return;
+    }
+    // K and V rows of the chunk: all loads issued up front (rows past the end
+    // are clamped to the last valid one and get zero weight below), V kept in
+    // registers while the scores are computed; q after them.
+    constexpr int Q4 = HD / 4;               // float4 per row
+    constexpr int NL = kChunk * Q4 / 256;    // float4 per thread
+    float4 kv4[NL], vv4[NL];
+#pragma unroll
+    for (int r = 0; r < NL; ++r) {
+        const int i = t + 256 * r, p = min(i / Q4, nvalid - 1), d4 = i % Q4;
+        kv4[r] = reinterpret_cast<const float4*>(kc + int64_t(p0 + p) * kv_dim + kvh * HD)[d4];
+    }
+#pragma unroll
+    for (int r = 0; r < NL; ++r) {
+        const int i = t + 256 * r, p = min(i / Q4, nvalid - 1), d4 = i % Q4;
+        vv4[r] = reinterpret_cast<const float4*>(vc + int64_t(p0 + p) * kv_dim + kvh * HD)[d4];
+    }
+    for (int i = t; i < G * HD; i += 256) qs[i] = q[kvh * G * HD + i];
+#pragma unroll
+    for (int r = 0; r < NL; ++r) {
+        const int i = t + 256 * r;
+        float* row = tile + (i / Q4) * LD + 4 * (i % Q4);
+        row[0] = kv4[r].x;
+        row[1] = kv4[r].y;
+        row[2] = kv4[r].z;
+        row[3] = kv4[r].w;
+    }
+    __syncthreads();
+    // scores: one wave per query head, one lane per position (4 partial sums)
+    for (int g = wave; g < G; g += 4) {
+        const float4* qg = reinterpret_cast<const float4*>(qs + g * HD);
+        const float* kr = tile + lane * LD;
+        float s4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int d4 = 0; d4 < Q4; ++d4) {
+            const float4 qv = qg[d4];
+            float& a = s4[d4 & 3];
+            a = fmaf(qv.x, kr[4 * d4], a);
+            a = fmaf(qv.y, kr[4 * d4 + 1], a);
+            a = fmaf(qv.z, kr[4 * d4 + 2], a);
+            a = fmaf(qv.w, kr[4 * d4 + 3], a);
+        }
+        float s = (s4[0] + s4[1]) + (s4[2] + s4[3]);
+        s = lane < nvalid ? s * scale : -INFINITY;
+        float m = s;
+        for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        const float e = lane < nvalid ? expf(s - m) : 0.f;
+        float l = e;
+        for (int o = 32; o >= 1; o >>= 1) l += __shfl_xor(l, o, 64);
+        es[g][lane] = e;
+        if (lane == 0) {
+            float* o = part + (int64_t(kvh * G + g) * n_chunks + c) * (HD + 2);
+            o[HD] = m;
+            o[HD + 1] = l;
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < NL; ++r) {
+        const int i = t + 256 * r;
+        float* row = tile + (i / Q4) * LD + 4 * (i % Q4);
+        row[0] = vv4[r].x;
+        row[1] = vv4[r].y;
+        row[2] = vv4[r].z;
+        row[3] = vv4[r].w;
+    }
+    __syncthreads();
+    // o[d] = sum_p e_p v[p][d] over all kChunk rows (e_p = 0 past the end)
+    for (int g = wave; g < G; g += 4) {
+        float* o = part + (int64_t(kvh * G + g) * n_chunks + c) * (HD + 2);
+        const float4* e4 = reinterpret_cast<const float4*>(es[g]);
+#pragma unroll
+        for (int d = lane; d < HD; d += 64) {
+            float a4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int p4 = 0; p4 < kChunk / 4; ++p4) {
+                const float4 ev = e4[p4];
+                float& a = a4[p4 & 3];
+                a = fmaf(ev.x, tile[(4 * p4) * LD + d], a);
+                a = fmaf(ev.y, tile[(4 * p4 + 1) * LD + d], a);
+                a = fmaf(ev.z, tile[(4 * p4 + 2) * LD + d], a);
+                a = fmaf(ev.w, tile[(4 * p4 + 3) * LD + d], a);
+            }
+            o[d] = (a4[0] + a4[1]) + (a4[2] + a4[3]);
+        }
+    }
+}
+
+// out[h][d] = sum_c o_c[d] e^{m_c - M} / sum_c l_c e^{m_c - M}, chunks in
+// order; thread c owns chunk c for the max and the weights (nc <= 1024).
+__global__ void __launch_bounds__(256) k_attn_combine(const float* __restrict__ part, float* __restrict__ out, int hd,
+                                                      int n_chunks, const int32_t* __restrict__ d_pos, int max_seq) {
+    __shared__ float wsc[1024];
+    __shared__ float red[4];
+    const int h = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int kv_len = min(*d_pos + 1, max_seq);
+    const int nc = min(n_chunks, (kv_len + kChunk - 1) / kChunk);
+    const float* ph = part + int64_t(h) * n_chunks * (hd + 2);
+    float mloc[4], lloc[4];
+    float M = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int c = t + 256 * r;
+        mloc[r] = c < nc ? ph[c * (hd + 2) + hd] : -INFINITY;
+        lloc[r] = c < nc ? ph[c * (hd + 2) + hd + 1] : 0.f;
+        M = fmaxf(M, mloc[r]);
+    }
+    for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+    if (lane == 0) red[wave] = M;
+    __syncthreads();
+    M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
+    float L = 0.f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int c = t + 256 * r;
+        const float w = c < nc ? expf(mloc[r] - M) : 0.f;
+        if (c < nc) wsc[c] = w;
+        L += lloc[r] * w;
+    }
+    for (int o = 32; o >= 1; o >>= 1) L += __shfl_xor(L, o, 64);
+    if (lane == 0) red[wave] = L;
+    __syncthreads();
+    L = (red[0] + red[1]) + (red[2] + red[3]);
+    const float inv = L > 0.f ? 1.0f / L : 0.f;
+    for (int d = t; d < hd; d += 256) {
+        float acc = 0.f;
+        int c = 0;
+        for (; c + 8 <= nc; c += 8) {
+            float v[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = ph[(c + i) * (hd + 2) + d];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc = fmaf(v[i], wsc[c + i], acc);
+        }
+        for (; c < nc; ++c) acc = fmaf(ph[c * (hd + 2) + d], wsc[c], acc);
+        out[h * hd + d] = acc * inv;
+    }
+}
+
+__global__ void __launch_bounds__(256) k_add(float* __restrict__ y, const float* __restrict__ a, int n) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) y[i] += a[i];
+}
+
+// out = silu(g) * u (layers/swiglu/cpu.go:41-53)
+__global__ void __launch_bounds__(256) k_silu_mul(const float* __restrict__ g, const float* __restrict__ u,
+                                                  float* __restrict__ out, int n) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) {
+        const float x = g[i];
+        out[i] = x / (1.0f + expf(-x)) * u[i];
+    }
+}
+
+// next = argmax(logits) (lowest index on ties), recorded as generated token
+// number *nstep; the next step's input token becomes `next`, and the
+// position advances when `advance` is set. state = {pos, tok, next, nstep}.
+__global__ void __launch_bounds__(1024) k_argmax_advance(const float* __restrict__ logits, int n,
+                                                         int32_t* __restrict__ state, int32_t* __restrict__ gen,
+                                                         int gen_cap, int advance) {
+    __shared__ float bv[16];
+    __shared__ int bi[16];
+    float v = -INFINITY;
+    int idx = 0x7fffffff;
+    for (int i = threadIdx.x; i < n; i += 1024) {
+        const float x = logits[i];
+        if (x > v || (x == v && i < idx)) {
+            v = x;
+            idx = i;
+        }
+    }
+    for (int m = 32; m >= 1; m >>= 1) {
+        const float ov = __shfl_xor(v, m, 64);
+        const int oi = __shfl_xor(idx, m, 64);
+        if (ov > v || (ov == v && oi < idx)) {
+            v = ov;
+            idx = oi;
+        }
+    }
+    if ((threadIdx.x & 63) == 0) {
+        bv[threadIdx.x >> 6] = v;
+        bi[threadIdx.x >> 6] = idx;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < 16; ++w)
+            if (bv[w] > v || (bv[w] == v && bi[w] < idx)) {
+                v = bv[w];
+                idx = bi[w];
+            }
+        state[2] = idx;
+        state[1] = idx;
+        const int k = state[3];
+        if (k < gen_cap) gen[k] = idx;
+        state[3] = k + 1;
+        if (advance) state[0] += 1;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Decoder object
+// ---------------------------------------------------------------------------
+
+struct Layer {
+    DevBlob w[7];  // q, k, v, o, gate, up, down
+    // Decoder-owned fused copies (row-interleaved blobs only): Q|K|V stacked
+    // (one launch writes q, k, v contiguously) and gate/up row pairs (one
+    // launch with the SwiGLU epilogue).
+    DevBlob qkv{}, gu{};
+    bool has_qkv = false, has_gu = false;
+    float* attn_norm = nullptr;
+    float* ffn_norm = nullptr;
+    float* kc = nullptr;
+    float* vc = nullptr;
+    bool set = false;
+};
+
+struct Decoder {
+    wv_decoder_config c{};
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::vector<Layer> layers;
+    DevBlob lm{};
+    bool lm_set = false;
+    float* final_norm = nullptr;
+    float* embed = nullptr;
+    // activations and state
+    float *h = nullptr, *n = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr;
+    float *g = nullptr, *u = nullptr, *logits = nullptr, *part = nullptr;
+    int32_t* d_state = nullptr;  // {pos, token, next, step}
+    int32_t* d_pos = nullptr;    // = d_state
+    int32_t* d_tok = nullptr;    // = d_state + 1
+    int32_t* d_gen = nullptr;    // [max_seq] generated tokens
+    double* freq_div = nullptr;  // [head_dim/2] theta^(2d/hd)
+    double2* cs = nullptr;       // [head_dim/2] this step's (cos, sin)
+    int n_chunks = 0;
+    std::vector<void*> allocs;
+    bool use_graph = false;
+    int graph_advance = -1;
+    hipGraphExec_t exec = nullptr;
+    hipGraph_t graph = nullptr;
+};
+
+// WV_DECODER_FUSE=0 keeps every projection as its own launch (for comparisons).
+bool fusion_off() {
+    static const bool off = [] {
+        const char* v = std::getenv("WV_DECODER_FUSE");
+        return v && v[0] == '0';
+    }();
+    return off;
+}
+
+std::mutex g_dmu;
+std::unordered_map<uint64_t, Decoder*> g_decs;
+uint64_t g_dnext = 1;
+
+Decoder* find(uint64_t h) {
+    std::lock_guard<std::mutex> lk(g_dmu);
+    auto it = g_decs.find(h);
+    return it == g_decs.end() ? nullptr : it->second;
+}
+
+int dalloc(Decoder& d, void** p, size_t bytes, const char* what) {
+    hipError_t e = hipMalloc(p, std::max<size_t>(bytes, 256));
+    if (e != hipSuccess) return rt_hip_fail(e, what);
+    d.allocs.push_back(*p);
+    return WV_OK;
+}
+
+void drop_fused(Layer& ly) {
+    if (ly.has_qkv) hipFree(ly.qkv.base);
+    if (ly.has_gu) hipFree(ly.gu.base);
+    ly.has_qkv = ly.has_gu = false;
+}
+
+void release(Decoder* d) {
+    if (d->exec) hipGraphExecDestroy(d->exec);
+    if (d->graph) hipGraphDestroy(d->graph);
+    for (Layer& ly : d->layers) drop_fused(ly);
+    for (void* p : d->allocs) hipFree(p);
+    if (d->stream) hipStreamDestroy(d->stream);
+    delete d;
+}
+
+// y (op)= W x for one projection: fused epilogue on the row-interleaved layout,
+// separate elementwise kernels otherwise.
+int proj(Decoder& d, const DevBlob& w, const float* x, float* y, int mode, const float* aux, float* tmp) {
+    if (w.layout == LAYOUT_RPL) return launch_rpl(w, x, y, 1, d.stream, mode, aux);
+    const int rows = int(w.rows);
+    float* out = mode == RPL_STORE ? y : tmp;
+    int e = launch_matvec(w, x, out, 1, d.stream);
+    if (e) return e;
+    if (mode == RPL_ADD) hipLaunchKernelGGL(k_add, dim3((rows + 255) / 256), dim3(256), 0, d.stream, y, tmp, rows);
+    if (mode == RPL_SILU_MUL)
+        hipLaunchKernelGGL(k_silu_mul, dim3((rows + 255) / 256), dim3(256), 0, d.stream, aux, tmp, y, rows);
+    return int(hipGetLastError());
+}
+
+// Enqueues one whole step on d.stream (token and position from device memory).
+int enqueue_step(Decoder& d, int advance) {
+    const wv_decoder_config& c = d.c;
+    const int hd = c.head_dim, kv_dim = c.n_kv_heads * hd, q_dim = c.n_heads * hd;
+    const float scale = float(1.0 / std::sqrt(double(hd)));
+    const int G = c.n_heads / c.n_kv_heads;
+    hipLaunchKernelGGL(k_embed, dim3((c.hidden + 255) / 256), dim3(256), 0, d.stream, d.embed, d.d_tok, d.h, c.hidden,
+                       c.vocab, d.freq_div, d.cs, hd / 2, d.d_pos);
+    float* tmp = d.logits;  // scratch for the non-fused projection epilogues (>= max(rows) floats)
+    for (int L = 0; L < c.n_layers; ++L) {
+        Layer& ly = d.layers[L];
+        hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(1024), 0, d.stream, d.h, ly.attn_norm, d.n, c.hidden, c.rms_eps);
+        int e = 0;
+        if (ly.has_qkv) {
+            e = launch_rpl(ly.qkv, d.n, d.q, 1, d.stream);  // q, k, v are contiguous
+        } else {
+            e = proj(d, ly.w[0], d.n, d.q, RPL_STORE, nullptr, tmp);
+            if (!e) e = proj(d, ly.w[1], d.n, d.k, RPL_STORE, nullptr, tmp);
+            if (!e) e = proj(d, ly.w[2], d.n, d.v, RPL_STORE, nullptr, tmp);
+        }
+        if (e) return e;
+        const int pairs = (c.n_heads + c.n_kv_heads) * (hd / 2);
+        hipLaunchKernelGGL(k_rope_kv, dim3(unsigned((pairs + 255) / 256)), dim3(256), 0, d.stream, d.q, d.k, d.v, ly.kc,
+                           ly.vc, d.d_pos, d.cs, c.n_heads, c.n_kv_heads, hd, c.max_seq);
+        const dim3 ag(unsigned(c.n_kv_heads), unsigned(d.n_chunks));
+        const size_t qsh = size_t(G) * hd * sizeof(float);
+        if (hd == 128)
+            hipLaunchKernelGGL(k_attn_part<128>, ag, dim3(256), qsh, d.stream, d.q, ly.kc, ly.vc, d.d_pos, d.part,
+                               c.n_heads, c.n_kv_heads, c.max_seq, d.n_chunks, scale);
+        else
+            hipLaunchKernelGGL(k_attn_part<64>, ag, dim3(256), qsh, d.stream, d.q, ly.kc, ly.vc, d.d_pos, d.part,
+                               c.n_heads, c.n_kv_heads, c.max_seq, d.n_chunks, scale);
+        hipLaunchKernelGGL(k_attn_combine, dim3(unsigned(c.n_heads)), dim3(256), 0, d.stream, d.part, d.att, hd,
+                           d.n_chunks, d.d_pos, c.max_seq);
+        (void)q_dim;
+        (void)kv_dim;
+        e = proj(d, ly.w[3], d.att, d.h, RPL_ADD, nullptr, tmp);
+        if (e) return e;
+        hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(1024), 0, d.stream, d.h, ly.ffn_norm, d.n, c.hidden, c.rms_eps);
+        if (ly.has_gu) {
+            e = launch_rpl(ly.gu, d.n, d.u, 1, d.stream, RPL_SWIGLU);
+        } else {
+            e = proj(d, ly.w[4], d.n, d.g, RPL_STORE, nullptr, tmp);
+            if (!e) e = proj(d, ly.w[5], d.n, d.u, RPL_SILU_MUL, d.g, tmp);
+        }
+        if (!e) e = proj(d, ly.w[6], d.u, d.h, RPL_ADD, nullptr, tmp);
+        if (e) return e;
+    }
+    const float* fin = d.h;
+    if (d.final_norm) {
+        hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(1024), 0, d.stream, d.h, d.final_norm, d.n, c.hidden, c.rms_eps);
+        fin = d.n;
+    }
+    int e = proj(d, d.lm, fin, d.logits, RPL_STORE, nullptr, nullptr);
+    if (e) return e;
+    hipLaunchKernelGGL(k_argmax_advance, dim3(1), dim3(1024), 0, d.stream, d.logits, c.vocab, d.d_state, d.d_gen,
+                       c.max_seq, advance);
+    return int(hipGetLastError());
+}
+
+int ready(const Decoder& d) {
+    for (int L = 0; L < d.c.n_layers; ++L)
+        if (!d.layers[L].set) return rt_fail(WV_E_ARG, "decoder: layer %d has no weights (wv_decoder_set_layer)", L);
+    if (!d.lm_set || !d.embed) return rt_fail(WV_E_ARG, "decoder: no LM head / embedding (wv_decoder_set_output)");
+    return WV_OK;
+}
+
+int run_steps(Decoder& d, int n_steps, int advance) {
+    if (!d.use_graph) {
+        for (int i = 0; i < n_steps; ++i) {
+            const int e = enqueue_step(d, advance);
+            if (e) return rt_hip_fail(hipError_t(e), "decoder step: launch");
+        }
+        return WV_OK;
+    }
+    if (!d.exec || d.graph_advance != advance) {
+        if (d.exec) {
+            hipGraphExecDestroy(d.exec);
+            hipGraphDestroy(d.graph);
+            d.exec = nullptr;
+            d.graph = nullptr;
+        }
+        hipError_t e = hipStreamBeginCapture(d.stream, hipStreamCaptureModeThreadLocal);
+        if (e != hipSuccess) return rt_hip_fail(e, "decoder: begin capture");
+        const int k = enqueue_step(d, advance);
+        hipGraph_t g = nullptr;
+        e = hipStreamEndCapture(d.stream, &g);
+        if (k) {
+            if (g) hipGraphDestroy(g);
+            return rt_hip_fail(hipError_t(k), "decoder: captured launch");
+        }
+        if (e != hipSuccess) return rt_hip_fail(e, "decoder: end capture");
+        e = hipGraphInstantiate(&d.exec, g, nullptr, nullptr, 0);
+        if (e != hipSuccess) {
+            hipGraphDestroy(g);
+            return rt_hip_fail(e, "decoder: instantiate");
+        }
+        d.graph = g;
+        d.graph_advance = advance;
+    }
+    for (int i = 0; i < n_steps; ++i) {
+        hipError_t e = hipGraphLaunch(d.exec, d.stream);
+        if (e != hipSuccess) return rt_hip_fail(e, "decoder: graph launch");
+    }
+    return WV_OK;
+}
+
+}  // namespace
+}  // namespace wv
+
+using namespace wv;
+
+extern "C" {
+
+int wv_decoder_create(const wv_decoder_config* cfg, uint64_t* handle) {
+    if (!cfg || !handle) return rt_fail(WV_E_ARG, "wv_decoder_create: nil argument");
+    const wv_decoder_config& c = *cfg;
+    if (c.n_layers <= 0 || c.hidden <= 0 || c.n_heads <= 0 || c.n_kv_heads <= 0 || c.ffn <= 0 || c.vocab <= 0 ||
+        c.max_seq <= 0)
+        return rt_fail(WV_E_SHAPE, "wv_decoder_create: non-positive dimension");
+    if (c.head_dim != 64 && c.head_dim != 128) return rt_fail(WV_E_SHAPE, "wv_decoder_create: head_dim %d (64 or 128)", c.head_dim);
+    if (c.n_heads % c.n_kv_heads || c.n_heads / c.n_kv_heads > 8)
+        return rt_fail(WV_E_SHAPE, "wv_decoder_create: %d heads over %d KV heads", c.n_heads, c.n_kv_heads);
+    if (c.rope_theta <= 0 || c.rms_eps <= 0) return rt_fail(WV_E_ARG, "wv_decoder_create: rope_theta and rms_eps must be > 0");
+    if (c.hidden % 4 || c.hidden > 16384) return rt_fail(WV_E_SHAPE, "wv_decoder_create: hidden %d (a multiple of 4, <= 16384)", c.hidden);
+    if (c.max_seq > kChunk * 1024) return rt_fail(WV_E_SHAPE, "wv_decoder_create: max_seq %d > %d", c.max_seq, kChunk * 1024);
+    int rc = rt_ensure_init();
+    if (rc) return rc;
+    Decoder* d = new Decoder();
+    d->c = c;
+    d->device = rt_current_device();
+    d->layers.resize(size_t(c.n_layers));
+    d->n_chunks = (c.max_seq + kChunk - 1) / kChunk;
+    hipError_t e = hipStreamCreateWithFlags(&d->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        delete d;
+        return rt_hip_fail(e, "wv_decoder_create: stream");
+    }
+    const size_t kv_dim = size_t(c.n_kv_heads) * c.head_dim, q_dim = size_t(c.n_heads) * c.head_dim;
+    const size_t wide = std::max({size_t(c.hidden), q_dim, size_t(c.ffn), size_t(c.vocab)});
+    struct B { float** p; size_t n; };
+    B bufs[] = {{&d->h, size_t(c.hidden)}, {&d->n, size_t(c.hidden)}, {&d->q, q_dim + 2 * kv_dim},
+                {&d->att, q_dim}, {&d->g, size_t(c.ffn)}, {&d->u, size_t(c.ffn)}, {&d->logits, wide},
+                {&d->part, size_t(c.n_heads) * d->n_chunks * (c.head_dim + 2)}};
+    for (B& b : bufs) {
+        rc = dalloc(*d, reinterpret_cast<void**>(b.p), b.n * sizeof(float), "wv_decoder_create: buffers");
+        if (rc) {
+            release(d);
+            return rc;
+        }
+    }
+    d->k = d->q + q_dim;  // q | k | v contiguous, as the fused QKV projection writes them
+    d->v = d->k + kv_dim;
+    void* ints = nullptr;
+    rc = dalloc(*d, &ints, (4 + size_t(c.max_seq)) * sizeof(int32_t), "wv_decoder_create: state");
+    if (rc) {
+        release(d);
+        return rc;
+    }
+    void* tabs = nullptr;
+    rc = dalloc(*d, &tabs, size_t(c.head_dim / 2) * (sizeof(double) + sizeof(double2)), "wv_decoder_create: RoPE table");
+    if (rc) {
+        release(d);
+        return rc;
+    }
+    d->cs = static_cast<double2*>(tabs);
+    d->freq_div = reinterpret_cast<double*>(d->cs + c.head_dim / 2);
+    {
+        std::vector<double> fd(size_t(c.head_dim / 2));
+        for (int i = 0; i < c.head_dim / 2; ++i) fd[size_t(i)] = std::pow(c.rope_theta, double(2 * i) / double(c.head_dim));
+        e = hipMemcpy(d->freq_div, fd.data(), fd.size() * sizeof(double), hipMemcpyHostToDevice);
+        if (e != hipSuccess) {
+            release(d);
+            return rt_hip_fail(e, "wv_decoder_create: RoPE table");
+        }
+    }
+    d->d_state = static_cast<int32_t*>(ints);
+    d->d_pos = d->d_state;
+    d->d_tok = d->d_state + 1;
+    d->d_gen = d->d_state + 4;
+    for (int L = 0; L < c.n_layers; ++L) {
+        Layer& ly = d->layers[L];
+        const size_t cache = size_t(c.max_seq) * kv_dim * sizeof(float);
+        rc = dalloc(*d, reinterpret_cast<void**>(&ly.kc), cache, "wv_decoder_create: K cache");
+        if (!rc) rc = dalloc(*d, reinterpret_cast<void**>(&ly.vc), cache, "wv_decoder_create: V cache");
+        if (!rc) rc = dalloc(*d, reinterpret_cast<void**>(&ly.attn_norm), size_t(c.hidden) * 4, "wv_decoder_create: norms");
+        if (!rc) rc = dalloc(*d, reinterpret_cast<void**>(&ly.ffn_norm), size_t(c.hidden) * 4, "wv_decoder_create: norms");
+        if (!rc) {
+            e = hipMemsetAsync(ly.kc, 0, cache, d->stream);
+            if (e == hipSuccess) e = hipMemsetAsync(ly.vc, 0, cache, d->stream);
+            if (e != hipSuccess) rc = rt_hip_fail(e, "wv_decoder_create: clear cache");
+        }
+        if (rc) {
+            release(d);
+            return rc;
+        }
+    }
+    e = hipStreamSynchronize(d->stream);
+    if (e != hipSuccess) {
+        release(d);
+        return rt_hip_fail(e, "wv_decoder_create: sync");
+    }
+    std::lock_guard<std::mutex> lk(g_dmu);
+    *handle = g_dnext++;
+    g_decs[*handle] = d;
+    return WV_OK;
+}
+
+int wv_decoder_set_layer(uint64_t dec, int32_t layer, const uint64_t* blobs, const float* attn_norm,
+                         const float* ffn_norm) {
+    Decoder* d = find(dec);
+    if (!d) return rt_fail(WV_E_HANDLE, "wv_decoder_set_layer: unknown decoder %llu", (unsigned long long)dec);
+    if (!blobs || !attn_norm || !ffn_norm) return rt_fail(WV_E_ARG, "wv_decoder_set_layer: nil argument");
+    const wv_decoder_config& c = d->c;
+    if (layer < 0 || layer >= c.n_layers) return rt_fail(WV_E_ARG, "wv_decoder_set_layer: layer %d of %d", layer, c.n_layers);
+    const int64_t q_dim = int64_t(c.n_heads) * c.head_dim, kv_dim = int64_t(c.n_kv_heads) * c.head_dim;
+    const int64_t want[7][2] = {{q_dim, c.hidden}, {kv_dim, c.hidden}, {kv_dim, c.hidden}, {c.hidden, q_dim},
+                                {c.ffn, c.hidden}, {c.ffn, c.hidden}, {c.hidden, c.ffn}};
+    static const char* names[7] = {"Q", "K", "V", "O", "gate", "up", "down"};
+    Layer& ly = d->layers[layer];
+    for (int i = 0; i < 7; ++i) {
+        DevBlob b;
+        if (!rt_lookup(blobs[i], b)) return rt_fail(WV_E_HANDLE, "wv_decoder_set_layer: %s blob %llu unknown", names[i], (unsigned long long)blobs[i]);
+        if (b.rows != want[i][0] || b.cols != want[i][1])
+            return rt_fail(WV_E_SHAPE, "wv_decoder_set_layer: %s is %lldx%lld, want %lldx%lld", names[i], (long long)b.rows,
+                           (long long)b.cols, (long long)want[i][0], (long long)want[i][1]);
+        ly.w[i] = b;
+    }
+    hipSetDevice(d->device);
+    hipError_t e = hipMemcpy(ly.attn_norm, attn_norm, size_t(c.hidden) * 4, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(ly.ffn_norm, ffn_norm, size_t(c.hidden) * 4, hipMemcpyHostToDevice);
+    if (e != hipSuccess) return rt_hip_fail(e, "wv_decoder_set_layer: norms");
+    drop_fused(ly);
+    const DevBlob* w = ly.w;
+    auto rpl_same = [&](int i, int j) {
+        return w[i].layout == LAYOUT_RPL && w[j].layout == LAYOUT_RPL && w[i].fmt == w[j].fmt;
+    };
+    if (!fusion_off() && rpl_same(0, 1) && rpl_same(0, 2) && w[0].rows % 64 == 0 && w[1].rows % 64 == 0) {
+        const int k = rpl_fuse_rows(w, 3, ly.qkv, d->stream);
+        if (k != hipSuccess) return rt_hip_fail(hipError_t(k), "wv_decoder_set_layer: fuse Q|K|V");
+        ly.has_qkv = true;
+    }
+    if (!fusion_off() && rpl_same(4, 5) && w[4].rows % 32 == 0) {
+        const int k = rpl_fuse_pairs(w[4], w[5], ly.gu, d->stream);
+        if (k != hipSuccess) return rt_hip_fail(hipError_t(k), "wv_decoder_set_layer: fuse gate/up");
+        ly.has_gu = true;
+    }
+    ly.set = true;
+    if (d->exec) {  // weights changed: capture again on the next graph run
+        hipGraphExecDestroy(d->exec);
+        hipGraphDestroy(d->graph);
+        d->exec = nullptr;
+        d->graph = nullptr;
+    }
+    return WV_OK;
+}
+
+int wv_decoder_set_output(uint64_t dec, uint64_t lm_head, const float* final_norm, const float* embedding) {
+    Decoder* d = find(dec);
+    if (!d) return rt_fail(WV_E_HANDLE, "wv_decoder_set_output: unknown decoder %llu", (unsigned long long)dec);
+    if (!embedding) return rt_fail(WV_E_ARG, "wv_decoder_set_output: nil embedding table");
+    const wv_decoder_config& c = d->c;
+    DevBlob b;
+    if (!rt_lookup(lm_head, b)) return rt_fail(WV_E_HANDLE, "wv_decoder_set_output: LM head blob unknown");
+    if (b.rows != c.vocab || b.cols != c.hidden)
+        return rt_fail(WV_E_SHAPE, "wv_decoder_set_output: LM head is %lldx%lld, want %dx%d", (long long)b.rows,
+                       (long long)b.cols, c.vocab, c.hidden);
+    hipSetDevice(d->device);
+    int rc = WV_OK;
+    if (final_norm && !d->final_norm) rc = dalloc(*d, reinterpret_cast<void**>(&d->final_norm), size_t(c.hidden) * 4, "final norm");
+    if (!rc && !d->embed) rc = dalloc(*d, reinterpret_cast<void**>(&d->embed), size_t(c.vocab) * c.hidden * 4, "embedding");
+    if (rc) return rc;
+    hipError_t e = hipSuccess;
+    if (final_norm) e = hipMemcpy(d->final_norm, final_norm, size_t(c.hidden) * 4, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(d->embed, embedding, size_t(c.vocab) * c.hidden * 4, hipMemcpyHostToDevice);
+    if (e != hipSuccess) return rt_hip_fail(e, "wv_decoder_set_output: copy");
+    d->lm = b;
+    d->lm_set = true;
+    return WV_OK;
+}
+
+int wv_decoder_set_kv(uint64_t dec, int32_t layer, int32_t first_pos, int32_t n_pos, const float* k, const float* v) {
+    Decoder* d = find(dec);
+    if (!d) return rt_fail(WV_E_HANDLE, "wv_decoder_set_kv: unknown decoder %llu", (unsigned long long)dec);
+    const wv_decoder_config& c = d->c;
+    if (layer < 0 || layer >= c.n_layers || !k || !v) return rt_fail(WV_E_ARG, "wv_decoder_set_kv: bad layer or nil rows");
+    if (first_pos < 0 || n_pos < 0 || int64_t(first_pos) + n_pos > c.max_seq)
+        return rt_fail(WV_E_SHAPE, "wv_decoder_set_kv: rows %d..%d outside max_seq %d", first_pos, first_pos + n_pos, c.max_seq);
+    const size_t kv_dim = size_t(c.n_kv_heads) * c.head_dim, off = size_t(first_pos) * kv_dim, n = size_t(n_pos) * kv_dim;
+    hipSetDevice(d->device);
+    hipError_t e = hipMemcpy(d->layers[layer].kc + off, k, n * 4, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(d->layers[layer].vc + off, v, n * 4, hipMemcpyHostToDevice);
+    if (e != hipSuccess) return rt_hip_fail(e, "wv_decoder_set_kv: copy");
+    return WV_OK;
+}
+
+int wv_decoder_use_graph(uint64_t dec, int32_t enable) {
+    Decoder* d = find(dec);
+    if (!d) return rt_fail(WV_E_HANDLE, "wv_decoder_use_graph: unknown decoder %llu", (unsigned long long)dec);
+    d->use_graph = enable != 0;
+    return WV_OK;
+}
+
+int wv_decoder_generate(uint64_t dec, int32_t token, int32_t pos, int32_t n_steps, int32_t advance_pos,
+                        int32_t* tokens_out, float* last_logits) {
+    Decoder* d = find(dec);
+    if (!d) return rt_fail(WV_E_HANDLE, "wv_decoder_generate: unknown decoder %llu", (unsigned long long)dec);
+    const wv_decoder_config& c = d->c;
+    if (n_steps < 0 || n_steps > c.max_seq) return rt_fail(WV_E_ARG, "wv_decoder_generate: step count %d outside 0..max_seq", n_steps);
+    if (pos < 0 || int64_t(pos) + (advance_pos ? n_steps : 1) > c.max_seq)
+        return rt_fail(WV_E_SHAPE, "wv_decoder_generate: positions %d.. exceed max_seq %d", pos, c.max_seq);
+    int rc = ready(*d);
+    if (rc) return rc;
+    hipSetDevice(d->device);
+    const int32_t init[4] = {pos, token, -1, 0};
+    hipError_t e = hipMemcpyAsync(d->d_state, init, sizeof init, hipMemcpyHostToDevice, d->stream);
+    if (e != hipSuccess) return rt_hip_fail(e, "wv_decoder_generate: state");
+    rc = run_steps(*d, n_steps, advance_pos ? 1 : 0);
+    if (rc) return rc;
+    if (tokens_out && n_steps > 0) {
+        e = hipMemcpyAsync(tokens_out, d->d_gen, size_t(n_steps) * sizeof(int32_t), hipMemcpyDeviceToHost, d->stream);
+        if (e != hipSuccess) return rt_hip_fail(e, "wv_decoder_generate: tokens");
+    }
+    if (last_logits && n_steps > 0) {
+        e = hipMemcpyAsync(last_logits, d->logits, size_t(c.vocab) * 4, hipMemcpyDeviceToHost, d->stream);
+        if (e != hipSuccess) return rt_hip_fail(e, "wv_decoder_generate: logits");
+    }
+    e = hipStreamSynchronize(d->stream);
+    if (e != hipSuccess) return rt_hip_fail(e, "wv_decoder_generate: sync");
+    return WV_OK;
+}
+
+int wv_decoder_free(uint64_t dec) {
+    Decoder* d = nullptr;
+    {
+        std::lock_guard<std::mutex> lk(g_dmu);
+        auto it = g_decs.find(dec);
+        if (it == g_decs.end()) return rt_fail(WV_E_HANDLE, "wv_decoder_free: unknown decoder %llu", (unsigned long long)dec);
+        d = it->second;
+        g_decs.erase(it);
+    }
+    hipSetDevice(d->device);
+    hipStreamSynchronize(d->stream);
+    release(d);
+    return WV_OK;
+}
+
+}  // extern "C"

@@ -242,6 +242,24 @@ __device__ __forceinline__ float sum_partials(const float* p, int64_t stride, in
     return t;
 }
 
+// Writes one output of the forward kernel under the launch's epilogue mode.
+__device__ __forceinline__ void store_y(const RplArgs& a, float* y, int64_t idx, float s) {
+    if (a.mode == RPL_ADD) {
+        s += y[idx];
+    } else if (a.mode == RPL_SILU_MUL) {
+        const float g = a.aux[idx];
+        s *= g / (1.0f + expf(-g));
+    }
+    y[idx] = s;
+}
+
+// RPL_SWIGLU store: even lane = gate row, odd lane = up row of one output.
+// Every lane of the wave must call it (it shuffles).
+__device__ __forceinline__ void store_swiglu(const RplArgs& a, float* y, int b, int row, int lane, float s) {
+    const float u = __shfl_xor(s, 1, 64);
+    if (!(lane & 1) && row < a.rows) y[int64_t(b) * (a.rows / 2) + row / 2] = s / (1.0f + expf(-s)) * u;
+}
+
 template <class P, int D>
 __global__ void __launch_bounds__(1024) k_gemv_rpl(RplArgs a, const float* __restrict__ x, float* __restrict__ y) {
     extern __shared__ float4 sm4[];
@@ -361,7 +379,8 @@ __global__ void __launch_bounds__(1024) k_gemv_rpl(RplArgs a, const float* __res
     for (int w = 0; w < W; ++w) s += part[w * 64 + lane];
     const int row = rg * 64 + lane;
     if (a.ksplit == 1) {
-        if (row < a.rows) y[int64_t(b) * a.rows + row] = s;
+        if (a.mode == RPL_SWIGLU) store_swiglu(a, y, b, row, lane, s);
+        else if (row < a.rows) store_y(a, y, int64_t(b) * a.rows + row, s);
         return;
     }
     // K split across gridDim.y blocks: publish the partial, take a ticket.
@@ -379,7 +398,8 @@ __global__ void __launch_bounds__(1024) k_gemv_rpl(RplArgs a, const float* __res
     old = __shfl(old, 0, 64);
     if (old != uint32_t(a.ksplit - 1)) return;
     const float t = sum_partials(pb + row, rows_pad, a.ksplit);
-    if (row < a.rows) y[int64_t(b) * a.rows + row] = t;
+    if (a.mode == RPL_SWIGLU) store_swiglu(a, y, b, row, lane, t);
+    else if (row < a.rows) store_y(a, y, int64_t(b) * a.rows + row, t);
     if (lane == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -410,8 +430,10 @@ int lds_floor() {
 }
 
 template <class P>
-int launch_rpl_t(const DevBlob& bl, const float* x, float* y, int batch, hipStream_t s) {
+int launch_rpl_t(const DevBlob& bl, const float* x, float* y, int batch, hipStream_t s, int mode, const float* aux) {
     RplArgs a = bl.rpl;
+    a.mode = mode;
+    a.aux = aux;
     // Waves per block W (super-blocks per block) and K split ks = ceil(nsb/W):
     // among W = 16..4, prefer grids of >= 200 blocks (most of the 256 CUs),
     // then the fewest idle waves (ks*W - nsb), then the largest W; the split
@@ -441,8 +463,11 @@ int launch_rpl_t(const DevBlob& bl, const float* x, float* y, int batch, hipStre
     for (int b0 = 0; b0 < batch; b0 += bl.rpl_max_batch) {
         const int nb = std::min(bl.rpl_max_batch, batch - b0);
         dim3 grid(unsigned(a.rg_count), unsigned(ksplit), unsigned(ksplit > 1 ? nb : batch - b0));
-        hipLaunchKernelGGL(kern, grid, dim3(unsigned(64 * W)), lds, s, a, x + int64_t(b0) * a.nsb * 256,
-                           y + int64_t(b0) * a.rows);
+        RplArgs ab = a;
+        if (aux) ab.aux = aux + int64_t(b0) * a.rows;
+        const int64_t ystride = mode == RPL_SWIGLU ? a.rows / 2 : a.rows;
+        hipLaunchKernelGGL(kern, grid, dim3(unsigned(64 * W)), lds, s, ab, x + int64_t(b0) * a.nsb * 256,
+                           y + int64_t(b0) * ystride);
         if (ksplit == 1) break;  // one launch covers every batch row
     }
     return int(hipGetLastError());
@@ -718,15 +743,179 @@ int launch_rpl_tr(const DevBlob& bl, const float* gy, float* gx, int batch, hipS
 
 }  // namespace
 
-int launch_rpl(const DevBlob& b, const float* d_x, float* d_y, int batch, void* stream) {
+int launch_rpl(const DevBlob& b, const float* d_x, float* d_y, int batch, void* stream, int mode, const float* aux) {
     hipStream_t s = static_cast<hipStream_t>(stream);
     switch (b.fmt) {
-    case FMT_Q4_K: return int_x() ? launch_rpl_t<RplQ4KI>(b, d_x, d_y, batch, s) : launch_rpl_t<RplQ4K>(b, d_x, d_y, batch, s);
-    case FMT_Q6_K: return launch_rpl_t<RplQ6K>(b, d_x, d_y, batch, s);
-    case FMT_Q8_0: return launch_rpl_t<RplQ8>(b, d_x, d_y, batch, s);
-    case FMT_Q4_0: return launch_rpl_t<RplQ4>(b, d_x, d_y, batch, s);
+    case FMT_Q4_K:
+        return int_x() ? launch_rpl_t<RplQ4KI>(b, d_x, d_y, batch, s, mode, aux)
+                       : launch_rpl_t<RplQ4K>(b, d_x, d_y, batch, s, mode, aux);
+    case FMT_Q6_K: return launch_rpl_t<RplQ6K>(b, d_x, d_y, batch, s, mode, aux);
+    case FMT_Q8_0: return launch_rpl_t<RplQ8>(b, d_x, d_y, batch, s, mode, aux);
+    case FMT_Q4_0: return launch_rpl_t<RplQ4>(b, d_x, d_y, batch, s, mode, aux);
     default: return int(hipErrorInvalidValue);
     }
+}
+
+namespace {
+
+// Bytes per (row group, super-block, lane) item of each image section.
+struct RplItems {
+    int cb, hb, mb, db;  // code chunk (x8 planes), high-bit chunk (x8), metadata, (d, dmin)
+};
+bool rpl_items(int fmt, RplItems& it) {
+    switch (fmt) {
+    case FMT_Q4_K: it = {16, 0, 32, 8}; return true;
+    case FMT_Q6_K: it = {16, 8, 16, 8}; return true;
+    case FMT_Q8_0: it = {32, 0, 32, 0}; return true;
+    case FMT_Q4_0: it = {16, 0, 32, 0}; return true;
+    default: return false;
+    }
+}
+
+// dst[p][G][sb][L] = (L even ? a : b)[p][G/2][sb][32*(G%2) + L/2], items of
+// isz bytes (a multiple of 8), G < 2*rg_in: rows 2i / 2i+1 <- a / b row i.
+__global__ void __launch_bounds__(256) k_rpl_pairs(uint8_t* __restrict__ dst, const uint8_t* __restrict__ a,
+                                                   const uint8_t* __restrict__ b, int isz, int64_t rg_in, int64_t nsb,
+                                                   int64_t planes) {
+    const int64_t n = planes * 2 * rg_in * nsb * 64;
+    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= n) return;
+    const int L = int(i & 63);
+    int64_t r = i >> 6;
+    const int64_t sb = r % nsb;
+    r /= nsb;
+    const int64_t G = r % (2 * rg_in);
+    const int64_t p = r / (2 * rg_in);
+    const uint8_t* src = (L & 1) ? b : a;
+    const int64_t si = ((p * rg_in + G / 2) * nsb + sb) * 64 + 32 * (G & 1) + (L >> 1);
+    const uint2* s2 = reinterpret_cast<const uint2*>(src + si * isz);
+    uint2* d2 = reinterpret_cast<uint2*>(dst + i * isz);
+    for (int k = 0; k < isz / 8; ++k) d2[k] = s2[k];
+}
+
+struct FusedLayout {
+    size_t codes, hi, meta, dd, part, ctr, total, weights;
+};
+FusedLayout fused_layout(const RplItems& it, int64_t rg, int64_t nsb, int max_batch, int max_split) {
+    FusedLayout f{};
+    auto add = [&](size_t n) {
+        const size_t off = (f.total + 255) & ~size_t(255);
+        f.total = off + n;
+        return off;
+    };
+    const size_t per = size_t(rg) * size_t(nsb) * 64;
+    f.codes = add(per * 8 * it.cb);
+    f.hi = it.hb ? add(per * 8 * it.hb) : 0;
+    f.meta = add(per * it.mb);
+    f.dd = it.db ? add(per * it.db) : 0;
+    f.weights = f.total;
+    f.part = add(size_t(max_batch) * max_split * rg * 64 * sizeof(float));
+    f.ctr = add(size_t(max_batch) * rg * sizeof(uint32_t));
+    return f;
+}
+
+int finish_fused(const DevBlob& proto, int64_t rows, int64_t rg, const FusedLayout& f, uint8_t* base, DevBlob& out,
+                 hipStream_t s) {
+    out = DevBlob{};
+    out.fmt = proto.fmt;
+    out.rows = rows;
+    out.cols = proto.cols;
+    out.layout = LAYOUT_RPL;
+    out.device = proto.device;
+    out.base = base;
+    out.device_bytes = f.weights;
+    out.rpl_max_batch = 8;
+    out.rpl_max_split = int(std::max<int64_t>(1, (proto.rpl.nsb + 3) / 4));
+    RplArgs& r = out.rpl;
+    r.codes = base + f.codes;
+    r.hi = f.hi ? base + f.hi : nullptr;
+    r.meta = base + f.meta;
+    r.dd = f.dd ? reinterpret_cast<const float2_t*>(base + f.dd) : nullptr;
+    r.partial = reinterpret_cast<float*>(base + f.part);
+    r.counters = reinterpret_cast<uint32_t*>(base + f.ctr);
+    r.rows = int(rows);
+    r.nsb = proto.rpl.nsb;
+    r.rg_count = int(rg);
+    r.ksplit = 1;
+    return int(hipMemsetAsync(base + f.part, 0, f.total - f.part, s));
+}
+
+}  // namespace
+
+int rpl_fuse_rows(const DevBlob* parts, int n, DevBlob& out, void* stream) {
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    RplItems it{};
+    if (n <= 0 || !rpl_items(parts[0].fmt, it)) return int(hipErrorInvalidValue);
+    int64_t rg = 0, rows = 0;
+    for (int i = 0; i < n; ++i) {
+        const DevBlob& b = parts[i];
+        if (b.layout != LAYOUT_RPL || b.fmt != parts[0].fmt || b.cols != parts[0].cols || b.rows % 64)
+            return int(hipErrorInvalidValue);
+        rg += b.rpl.rg_count;
+        rows += b.rows;
+    }
+    const int64_t nsb = parts[0].rpl.nsb;
+    const FusedLayout f = fused_layout(it, rg, nsb, 8, int(std::max<int64_t>(1, (nsb + 3) / 4)));
+    void* base = nullptr;
+    hipError_t e = hipMalloc(&base, f.total);
+    if (e != hipSuccess) return int(e);
+    uint8_t* b8 = static_cast<uint8_t*>(base);
+    int64_t g0 = 0;
+    for (int i = 0; i < n && e == hipSuccess; ++i) {
+        const RplArgs& r = parts[i].rpl;
+        const size_t per = size_t(r.rg_count) * nsb * 64, off = size_t(g0) * nsb * 64;
+        const size_t per_all = size_t(rg) * nsb * 64;
+        for (int p = 0; p < 8 && e == hipSuccess; ++p) {
+            e = hipMemcpyAsync(b8 + f.codes + (p * per_all + off) * it.cb, r.codes + p * per * it.cb, per * it.cb,
+                               hipMemcpyDeviceToDevice, s);
+            if (it.hb && e == hipSuccess)
+                e = hipMemcpyAsync(b8 + f.hi + (p * per_all + off) * it.hb, r.hi + p * per * it.hb, per * it.hb,
+                                   hipMemcpyDeviceToDevice, s);
+        }
+        if (e == hipSuccess) e = hipMemcpyAsync(b8 + f.meta + off * it.mb, r.meta, per * it.mb, hipMemcpyDeviceToDevice, s);
+        if (it.db && e == hipSuccess)
+            e = hipMemcpyAsync(b8 + f.dd + off * it.db, r.dd, per * it.db, hipMemcpyDeviceToDevice, s);
+        g0 += r.rg_count;
+    }
+    if (e == hipSuccess) e = hipError_t(finish_fused(parts[0], rows, rg, f, b8, out, s));
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) {
+        hipFree(base);
+        out = DevBlob{};
+    }
+    return int(e);
+}
+
+int rpl_fuse_pairs(const DevBlob& a, const DevBlob& b, DevBlob& out, void* stream) {
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    RplItems it{};
+    if (!rpl_items(a.fmt, it) || a.layout != LAYOUT_RPL || b.layout != LAYOUT_RPL || a.fmt != b.fmt ||
+        a.rows != b.rows || a.cols != b.cols || a.rows % 32)
+        return int(hipErrorInvalidValue);
+    const int64_t rg_in = a.rpl.rg_count, rg = 2 * rg_in, nsb = a.rpl.nsb;
+    const FusedLayout f = fused_layout(it, rg, nsb, 8, int(std::max<int64_t>(1, (nsb + 3) / 4)));
+    void* base = nullptr;
+    hipError_t e = hipMalloc(&base, f.total);
+    if (e != hipSuccess) return int(e);
+    uint8_t* b8 = static_cast<uint8_t*>(base);
+    auto run = [&](size_t off, const uint8_t* pa, const uint8_t* pb, int isz, int64_t planes) {
+        const int64_t n = planes * rg * nsb * 64;
+        hipLaunchKernelGGL(k_rpl_pairs, dim3(unsigned((n + 255) / 256)), dim3(256), 0, s, b8 + off, pa, pb, isz, rg_in,
+                           nsb, planes);
+    };
+    run(f.codes, a.rpl.codes, b.rpl.codes, it.cb, 8);
+    if (it.hb) run(f.hi, a.rpl.hi, b.rpl.hi, it.hb, 8);
+    run(f.meta, a.rpl.meta, b.rpl.meta, it.mb, 1);
+    if (it.db)
+        run(f.dd, reinterpret_cast<const uint8_t*>(a.rpl.dd), reinterpret_cast<const uint8_t*>(b.rpl.dd), it.db, 1);
+    e = hipGetLastError();
+    if (e == hipSuccess) e = hipError_t(finish_fused(a, 2 * a.rows, rg, f, b8, out, s));
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) {
+        hipFree(base);
+        out = DevBlob{};
+    }
+    return int(e);
 }
 
 size_t rpl_t_scratch_floats(const RplArgs& a) {

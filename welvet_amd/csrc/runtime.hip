@@ -253,6 +253,24 @@ int64_t need_raw(int fmt, int64_t rows, int64_t cols, int32_t bw, const uint8_t*
 }
 
 }  // namespace
+
+// Helpers shared with the other HIP translation units (rt_internal.h).
+int rt_fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+int rt_hip_fail(hipError_t e, const char* what) { return hip_fail(e, what); }
+int rt_ensure_init() { return ensure_init(); }
+bool rt_lookup(uint64_t h, DevBlob& out) { return lookup(h, out); }
+int rt_current_device() {
+    std::lock_guard<std::mutex> lk(g_mu);
+    return g_current;
+}
 }  // namespace wv
 
 using namespace wv;

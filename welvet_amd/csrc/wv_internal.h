@@ -97,7 +97,14 @@ struct RplArgs {
     float* partial;       // [batch chunk][ksplit][rg*64] partial sums when K is split
     uint32_t* counters;   // [batch chunk][rg] arrival tickets, zero between launches
     int rows, nsb, rg_count, ksplit;
+    // Output epilogue of the forward kernel: RPL_STORE y = Wx;
+    // RPL_ADD y += Wx (residual); RPL_SILU_MUL y = silu(aux) * Wx (SwiGLU up);
+    // RPL_SWIGLU on a gate/up row-pair blob (row 2i gate i, row 2i+1 up i):
+    // y[i] = silu(gate_i) * up_i, y holding rows/2 values per batch row.
+    int mode;
+    const float* aux;  // [batch][rows] gate values for RPL_SILU_MUL
 };
+enum RplMode { RPL_STORE = 0, RPL_ADD = 1, RPL_SILU_MUL = 2, RPL_SWIGLU = 3 };
 
 constexpr int kRplTMaxBatch = 16;  // batch rows per MatVecT launch on LAYOUT_RPL
 
@@ -128,9 +135,17 @@ struct DevBlob {
 };
 
 // Kernel launchers (gemv.hip, gemv_rpl.hip). Return a hipError_t as int.
-int launch_rpl(const DevBlob& b, const float* d_x, float* d_y, int batch, void* stream);
+int launch_rpl(const DevBlob& b, const float* d_x, float* d_y, int batch, void* stream, int mode = RPL_STORE,
+               const float* aux = nullptr);
 int launch_matvec(const DevBlob& b, const float* d_x, float* d_y, int batch, void* stream);
 int launch_matvec_t(const DevBlob& b, const float* d_gy, float* d_gx, int batch, void* stream, float* d_scratch);
+// Fused row-interleaved images (gemv_rpl.hip), built on the device from
+// resident blobs of one format and width: rpl_fuse_rows stacks the parts'
+// rows (each part's rows a multiple of 64); rpl_fuse_pairs interleaves two
+// equal blobs row by row (row 2i from a, row 2i+1 from b; rows a multiple of
+// 32) for RPL_SWIGLU. The result owns a new allocation (out.base).
+int rpl_fuse_rows(const DevBlob* parts, int n, DevBlob& out, void* stream);
+int rpl_fuse_pairs(const DevBlob& a, const DevBlob& b, DevBlob& out, void* stream);
 // Batched prefill GEMM (gemm_rpl.hip): fp16 MFMA on the row-interleaved Q4_K layout.
 bool gemm_supported(const DevBlob& b);
 size_t gemm_scratch_floats(const DevBlob& b, int M);
