@@ -36,10 +36,17 @@ constexpr int kChunk = 64;  // KV positions per attention block
 __global__ void __launch_bounds__(256) k_embed(const float* __restrict__ table, const int32_t* __restrict__ tok,
                                                float* __restrict__ h, int hidden, int vocab,
                                                const double* __restrict__ freq_div, double2* __restrict__ cs,
-                                               int half, const int32_t* __restrict__ d_pos) {
+                                               int half, const int32_t* __restrict__ d_pos, float* __restrict__ ss) {
     const int t = min(max(*tok, 0), vocab - 1);
     for (int i = blockIdx.x * 256 + threadIdx.x; i < hidden; i += gridDim.x * 256)
         h[i] = table[int64_t(t) * hidden + i];
+    if (ss) {  // sums of h^2 per 64 elements, for the first layer's fused RMSNorm
+        const int i = blockIdx.x * 256 + threadIdx.x;
+        const float v = i < hidden ? table[int64_t(t) * hidden + i] : 0.f;
+        float q = v * v;
+        for (int m = 32; m >= 1; m >>= 1) q += __shfl_xor(q, m, 64);
+        if ((threadIdx.x & 63) == 0 && i < hidden) ss[i >> 6] = q;
+    }
     if (blockIdx.x == 0) {
         const double pos = double(*d_pos);
         for (int d = threadIdx.x; d < half; d += 256) {
@@ -88,49 +95,23 @@ __global__ void __launch_bounds__(1024) k_rmsnorm(const float* __restrict__ x, c
     }
 }
 
-// Rotate-half RoPE on q (n_heads) and k (n_kv) with this step's cos/sin
-// table (layers/mha/rope.go:6-21), then append k and v as row pos % max_seq of
-// the layer's cache (layers/mha/cpu.go:178-193). One thread per pair.
-__global__ void __launch_bounds__(256) k_rope_kv(float* __restrict__ q, const float* __restrict__ k,
-                                                 const float* __restrict__ v, float* __restrict__ kc,
-                                                 float* __restrict__ vc, const int32_t* __restrict__ d_pos,
-                                                 const double2* __restrict__ cs, int n_heads, int n_kv, int hd,
-                                                 int max_seq) {
-    const int pos = *d_pos;
-    const int half = hd / 2;
-    const int kv_dim = n_kv * hd;
-    const int64_t row = int64_t(pos % max_seq) * kv_dim;
-    const int nq = n_heads * half, nk = n_kv * half;
-    const int i = blockIdx.x * 256 + threadIdx.x;
-    if (i < nq + nk) {
-        const bool isq = i < nq;
-        const int j = isq ? i : i - nq;
-        const int h = j / half, d = j % half;
-        const double2 r = cs[d];
-        const float* src = isq ? q + h * hd : k + h * hd;
-        const double v0 = src[d], v1 = src[d + half];
-        const float o0 = float(v0 * r.x - v1 * r.y), o1 = float(v0 * r.y + v1 * r.x);
-        if (isq) {
-            q[h * hd + d] = o0;
-            q[h * hd + d + half] = o1;
-        } else {
-            kc[row + h * hd + d] = o0;
-            kc[row + h * hd + d + half] = o1;
-        }
-    }
-    for (int e = i; e < kv_dim; e += gridDim.x * 256) vc[row + e] = v[e];
-}
-
 // Flash-decoding partials for one KV head and one chunk of kChunk positions:
 // the G = n_heads / n_kv query heads that share the KV head read its K and V
 // rows once (layers/mha/attn.go:40-118: score = q.k * scale over the causal
 // positions kPos <= pos, max-subtracted softmax, sum of p * v). Per (head,
 // chunk) it writes o[HD] (unnormalised), the chunk max m and sum l.
+//
+// RoPE and the KV append are folded in: q arrives unrotated and each block
+// rotates its G heads in LDS with this step's cos/sin table; the block whose
+// chunk holds position pos rotates the new k row of its KV head, uses it and
+// the new v row in place of the cache's row pos, and writes both to the cache
+// (layers/mha/cpu.go:178-193, rope.go:6-21).
 template <int HD>
-__global__ void __launch_bounds__(256) k_attn_part(const float* __restrict__ q, const float* __restrict__ kc,
-                                                   const float* __restrict__ vc, const int32_t* __restrict__ d_pos,
+__global__ void __launch_bounds__(256) k_attn_part(const float* __restrict__ q, float* __restrict__ kc,
+                                                   float* __restrict__ vc, const int32_t* __restrict__ d_pos,
                                                    float* __restrict__ part, int n_heads, int n_kv, int max_seq,
-                                                   int n_chunks, float scale) {
+                                                   int n_chunks, float scale, const float* __restrict__ k_new,
+                                                   const float* __restrict__ v_new, const double2* __restrict__ cs) {
     constexpr int LD = HD + 1;
     __shared__ float tile[kChunk * LD];
     __shared__ __attribute__((aligned(16))) float es[8][kChunk];
@@ -138,10 +119,12 @@ __global__ void __launch_bounds__(256) k_attn_part(const float* __restrict__ q, 
     const int kvh = blockIdx.x, c = blockIdx.y;
     const int G = n_heads / n_kv;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int kv_len = min(*d_pos + 1, max_seq);
+    const int pos = *d_pos;
+    const int kv_len = min(pos + 1, max_seq);
     const int p0 = c * kChunk;
     const int nvalid = min(kChunk, kv_len - p0);
     const int kv_dim = n_kv * HD;
+    const int pnew = pos % max_seq - p0;  // row of this step's k/v inside the chunk (if in [0, kChunk))
     if (nvalid <= 0) {
         for (int g = wave; g < G; g += 4) {
             float* o = part + (int64_t(kvh * G + g) * n_chunks + c) * (HD + 2);
@@ -168,7 +151,37 @@ __global__ void __launch_bounds__(256) k_attn_part(const float* __restrict__ q, 
         const int i = t + 256 * r, p = min(i / Q4, nvalid - 1), d4 = i % Q4;
         vv4[r] = reinterpret_cast<const float4*>(vc + int64_t(p0 + p) * kv_dim + kvh * HD)[d4];
     }
-    for (int i = t; i < G * HD; i += 256) qs[i] = q[kvh * G * HD + i];
+    // q heads of this KV group, rotated: one thread per pair (g, d < HD/2)
+    constexpr int H2 = HD / 2;
+    for (int i = t; i < G * H2; i += 256) {
+        const int g = i / H2, d = i % H2;
+        const float* qg = q + (kvh * G + g) * HD;
+        const double2 r = cs[d];
+        const double v0 = qg[d], v1 = qg[d + H2];
+        qs[g * HD + d] = float(v0 * r.x - v1 * r.y);
+        qs[g * HD + d + H2] = float(v0 * r.y + v1 * r.x);
+    }
+    // this step's row: rotated k and v replace what the cache held
+#pragma unroll
+    for (int r = 0; r < NL; ++r) {
+        const int i = t + 256 * r;
+        if (i / Q4 != pnew) continue;
+        const int d0 = 4 * (i % Q4);
+        const float* kn = k_new + kvh * HD;
+        float kr[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int d = d0 + e, dm = d % H2;
+            const double2 rc = cs[dm];
+            const double a0 = kn[dm], a1 = kn[dm + H2];
+            kr[e] = d < H2 ? float(a0 * rc.x - a1 * rc.y) : float(a0 * rc.y + a1 * rc.x);
+        }
+        kv4[r] = make_float4(kr[0], kr[1], kr[2], kr[3]);
+        vv4[r] = reinterpret_cast<const float4*>(v_new + kvh * HD)[i % Q4];
+        const int64_t crow = int64_t(pos % max_seq) * kv_dim + kvh * HD;
+        reinterpret_cast<float4*>(kc + crow)[i % Q4] = kv4[r];
+        reinterpret_cast<float4*>(vc + crow)[i % Q4] = vv4[r];
+    }
 #pragma unroll
     for (int r = 0; r < NL; ++r) {
         const int i = t + 256 * r;
@@ -385,6 +398,9 @@ struct Decoder {
     int32_t* d_pos = nullptr;    // = d_state
     int32_t* d_tok = nullptr;    // = d_state + 1
     int32_t* d_gen = nullptr;    // [max_seq] generated tokens
+    float* ss_a = nullptr;       // [hidden/64] partial sums of h^2 for the attention norm / final norm
+    float* ss_b = nullptr;       // [hidden/64] partial sums of h^2 for the FFN norm
+    bool fused_norm = false;     // every norm folded into its consumer GEMV
     double* freq_div = nullptr;  // [head_dim/2] theta^(2d/hd)
     double2* cs = nullptr;       // [head_dim/2] this step's (cos, sin)
     int n_chunks = 0;
@@ -453,39 +469,57 @@ int proj(Decoder& d, const DevBlob& w, const float* x, float* y, int mode, const
 // Enqueues one whole step on d.stream (token and position from device memory).
 int enqueue_step(Decoder& d, int advance) {
     const wv_decoder_config& c = d.c;
-    const int hd = c.head_dim, kv_dim = c.n_kv_heads * hd, q_dim = c.n_heads * hd;
+    const int hd = c.head_dim;
     const float scale = float(1.0 / std::sqrt(double(hd)));
     const int G = c.n_heads / c.n_kv_heads;
+    const bool fn = d.fused_norm;
+    const int nss = c.hidden / 64;
     hipLaunchKernelGGL(k_embed, dim3((c.hidden + 255) / 256), dim3(256), 0, d.stream, d.embed, d.d_tok, d.h, c.hidden,
-                       c.vocab, d.freq_div, d.cs, hd / 2, d.d_pos);
+                       c.vocab, d.freq_div, d.cs, hd / 2, d.d_pos, fn ? d.ss_a : nullptr);
     float* tmp = d.logits;  // scratch for the non-fused projection epilogues (>= max(rows) floats)
+    auto normed = [&](const float* gamma, const float* ss, int mode, float* ss_out) {
+        RplExtra ex;
+        ex.mode = mode;
+        ex.nrm_gamma = gamma;
+        ex.nrm_ss = ss;
+        ex.nrm_n = nss;
+        ex.nrm_eps = c.rms_eps;
+        ex.ss_out = ss_out;
+        return ex;
+    };
     for (int L = 0; L < c.n_layers; ++L) {
         Layer& ly = d.layers[L];
-        hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(1024), 0, d.stream, d.h, ly.attn_norm, d.n, c.hidden, c.rms_eps);
         int e = 0;
-        if (ly.has_qkv) {
-            e = launch_rpl(ly.qkv, d.n, d.q, 1, d.stream);  // q, k, v are contiguous
+        if (fn) {
+            e = launch_rpl_ex(ly.qkv, d.h, d.q, 1, d.stream, normed(ly.attn_norm, d.ss_a, RPL_STORE, nullptr));
         } else {
-            e = proj(d, ly.w[0], d.n, d.q, RPL_STORE, nullptr, tmp);
-            if (!e) e = proj(d, ly.w[1], d.n, d.k, RPL_STORE, nullptr, tmp);
-            if (!e) e = proj(d, ly.w[2], d.n, d.v, RPL_STORE, nullptr, tmp);
+            hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(1024), 0, d.stream, d.h, ly.attn_norm, d.n, c.hidden, c.rms_eps);
+            if (ly.has_qkv) {
+                e = launch_rpl(ly.qkv, d.n, d.q, 1, d.stream);  // q, k, v are contiguous
+            } else {
+                e = proj(d, ly.w[0], d.n, d.q, RPL_STORE, nullptr, tmp);
+                if (!e) e = proj(d, ly.w[1], d.n, d.k, RPL_STORE, nullptr, tmp);
+                if (!e) e = proj(d, ly.w[2], d.n, d.v, RPL_STORE, nullptr, tmp);
+            }
         }
         if (e) return e;
-        const int pairs = (c.n_heads + c.n_kv_heads) * (hd / 2);
-        hipLaunchKernelGGL(k_rope_kv, dim3(unsigned((pairs + 255) / 256)), dim3(256), 0, d.stream, d.q, d.k, d.v, ly.kc,
-                           ly.vc, d.d_pos, d.cs, c.n_heads, c.n_kv_heads, hd, c.max_seq);
         const dim3 ag(unsigned(c.n_kv_heads), unsigned(d.n_chunks));
         const size_t qsh = size_t(G) * hd * sizeof(float);
         if (hd == 128)
             hipLaunchKernelGGL(k_attn_part<128>, ag, dim3(256), qsh, d.stream, d.q, ly.kc, ly.vc, d.d_pos, d.part,
-                               c.n_heads, c.n_kv_heads, c.max_seq, d.n_chunks, scale);
+                               c.n_heads, c.n_kv_heads, c.max_seq, d.n_chunks, scale, d.k, d.v, d.cs);
         else
             hipLaunchKernelGGL(k_attn_part<64>, ag, dim3(256), qsh, d.stream, d.q, ly.kc, ly.vc, d.d_pos, d.part,
-                               c.n_heads, c.n_kv_heads, c.max_seq, d.n_chunks, scale);
+                               c.n_heads, c.n_kv_heads, c.max_seq, d.n_chunks, scale, d.k, d.v, d.cs);
         hipLaunchKernelGGL(k_attn_combine, dim3(unsigned(c.n_heads)), dim3(256), 0, d.stream, d.part, d.att, hd,
                            d.n_chunks, d.d_pos, c.max_seq);
-        (void)q_dim;
-        (void)kv_dim;
+        if (fn) {
+            e = launch_rpl_ex(ly.w[3], d.att, d.h, 1, d.stream, normed(nullptr, nullptr, RPL_ADD, d.ss_b));
+            if (!e) e = launch_rpl_ex(ly.gu, d.h, d.u, 1, d.stream, normed(ly.ffn_norm, d.ss_b, RPL_SWIGLU, nullptr));
+            if (!e) e = launch_rpl_ex(ly.w[6], d.u, d.h, 1, d.stream, normed(nullptr, nullptr, RPL_ADD, d.ss_a));
+            if (e) return e;
+            continue;
+        }
         e = proj(d, ly.w[3], d.att, d.h, RPL_ADD, nullptr, tmp);
         if (e) return e;
         hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(1024), 0, d.stream, d.h, ly.ffn_norm, d.n, c.hidden, c.rms_eps);
@@ -498,22 +532,46 @@ int enqueue_step(Decoder& d, int advance) {
         if (!e) e = proj(d, ly.w[6], d.u, d.h, RPL_ADD, nullptr, tmp);
         if (e) return e;
     }
-    const float* fin = d.h;
-    if (d.final_norm) {
-        hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(1024), 0, d.stream, d.h, d.final_norm, d.n, c.hidden, c.rms_eps);
-        fin = d.n;
+    int e = 0;
+    if (fn && d.final_norm) {
+        e = launch_rpl_ex(d.lm, d.h, d.logits, 1, d.stream, normed(d.final_norm, d.ss_a, RPL_STORE, nullptr));
+    } else {
+        const float* fin = d.h;
+        if (d.final_norm) {
+            hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(1024), 0, d.stream, d.h, d.final_norm, d.n, c.hidden,
+                               c.rms_eps);
+            fin = d.n;
+        }
+        e = proj(d, d.lm, fin, d.logits, RPL_STORE, nullptr, nullptr);
     }
-    int e = proj(d, d.lm, fin, d.logits, RPL_STORE, nullptr, nullptr);
     if (e) return e;
     hipLaunchKernelGGL(k_argmax_advance, dim3(1), dim3(1024), 0, d.stream, d.logits, c.vocab, d.d_state, d.d_gen,
                        c.max_seq, advance);
     return int(hipGetLastError());
 }
 
-int ready(const Decoder& d) {
+// Every norm can be folded into its consumer when all projections are on the
+// row-interleaved layout with Q|K|V and gate/up fused (the residual GEMVs then
+// produce the sums of squares the next norm needs).
+bool can_fuse_norms(const Decoder& d) {
+    if (fusion_off() || d.c.hidden % 256) return false;
+    for (const Layer& ly : d.layers)
+        if (!ly.has_qkv || !ly.has_gu || ly.w[3].layout != LAYOUT_RPL || ly.w[6].layout != LAYOUT_RPL) return false;
+    return d.lm.layout == LAYOUT_RPL;
+}
+
+int ready(Decoder& d) {
     for (int L = 0; L < d.c.n_layers; ++L)
         if (!d.layers[L].set) return rt_fail(WV_E_ARG, "decoder: layer %d has no weights (wv_decoder_set_layer)", L);
     if (!d.lm_set || !d.embed) return rt_fail(WV_E_ARG, "decoder: no LM head / embedding (wv_decoder_set_output)");
+    const bool fn = can_fuse_norms(d);
+    if (fn != d.fused_norm && d.exec) {
+        hipGraphExecDestroy(d.exec);
+        hipGraphDestroy(d.graph);
+        d.exec = nullptr;
+        d.graph = nullptr;
+    }
+    d.fused_norm = fn;
     return WV_OK;
 }
 
@@ -592,6 +650,7 @@ int wv_decoder_create(const wv_decoder_config* cfg, uint64_t* handle) {
     const size_t wide = std::max({size_t(c.hidden), q_dim, size_t(c.ffn), size_t(c.vocab)});
     struct B { float** p; size_t n; };
     B bufs[] = {{&d->h, size_t(c.hidden)}, {&d->n, size_t(c.hidden)}, {&d->q, q_dim + 2 * kv_dim},
+                {&d->ss_a, size_t(c.hidden / 64 + 1)}, {&d->ss_b, size_t(c.hidden / 64 + 1)},
                 {&d->att, q_dim}, {&d->g, size_t(c.ffn)}, {&d->u, size_t(c.ffn)}, {&d->logits, wide},
                 {&d->part, size_t(c.n_heads) * d->n_chunks * (c.head_dim + 2)}};
     for (B& b : bufs) {

@@ -242,8 +242,9 @@ __device__ __forceinline__ float sum_partials(const float* p, int64_t stride, in
     return t;
 }
 
-// Writes one output of the forward kernel under the launch's epilogue mode.
-__device__ __forceinline__ void store_y(const RplArgs& a, float* y, int64_t idx, float s) {
+// Writes one output of the forward kernel under the launch's epilogue mode
+// and returns the stored value.
+__device__ __forceinline__ float store_y(const RplArgs& a, float* y, int64_t idx, float s) {
     if (a.mode == RPL_ADD) {
         s += y[idx];
     } else if (a.mode == RPL_SILU_MUL) {
@@ -251,13 +252,25 @@ __device__ __forceinline__ void store_y(const RplArgs& a, float* y, int64_t idx,
         s *= g / (1.0f + expf(-g));
     }
     y[idx] = s;
+    return s;
 }
 
-// RPL_SWIGLU store: even lane = gate row, odd lane = up row of one output.
-// Every lane of the wave must call it (it shuffles).
-__device__ __forceinline__ void store_swiglu(const RplArgs& a, float* y, int b, int row, int lane, float s) {
-    const float u = __shfl_xor(s, 1, 64);
-    if (!(lane & 1) && row < a.rows) y[int64_t(b) * (a.rows / 2) + row / 2] = s / (1.0f + expf(-s)) * u;
+// Epilogue of one row group (all 64 lanes of the wave call it): store, and
+// for a fused-RMSNorm producer the sum of the group's stored y^2.
+__device__ __forceinline__ void finish_rows(const RplArgs& a, float* y, int b, int rg, int lane, float s) {
+    const int row = rg * 64 + lane;
+    if (a.mode == RPL_SWIGLU) {
+        const float u = __shfl_xor(s, 1, 64);
+        if (!(lane & 1) && row < a.rows) y[int64_t(b) * (a.rows / 2) + row / 2] = s / (1.0f + expf(-s)) * u;
+        return;
+    }
+    float v = 0.f;
+    if (row < a.rows) v = store_y(a, y, int64_t(b) * a.rows + row, s);
+    if (a.ss_out) {
+        float q = v * v;
+        for (int m = 32; m >= 1; m >>= 1) q += __shfl_xor(q, m, 64);
+        if (lane == 0) a.ss_out[int64_t(b) * a.rg_count + rg] = q;
+    }
 }
 
 template <class P, int D>
@@ -277,11 +290,27 @@ __global__ void __launch_bounds__(1024) k_gemv_rpl(RplArgs a, const float* __res
     // This wave's 256 x values: one float4 per lane, issued before the
     // weights so that waiting for x does not wait for weight data (vector
     // loads retire in issue order).
-    const float4 xv4 = reinterpret_cast<const float4*>(x + int64_t(b) * a.nsb * 256 + int64_t(sbc) * 256)[lane];
+    float4 xv4 = reinterpret_cast<const float4*>(x + int64_t(b) * a.nsb * 256 + int64_t(sbc) * 256)[lane];
+    float4 gv4 = make_float4(1.f, 1.f, 1.f, 1.f);
+    double ssp = 0.0;
+    if (a.nrm_gamma) {
+        gv4 = reinterpret_cast<const float4*>(a.nrm_gamma + int64_t(sbc) * 256)[lane];
+        for (int i = lane; i < a.nrm_n; i += 64) ssp += a.nrm_ss[int64_t(b) * a.nrm_n + i];
+    }
     typename P::Ch ch[8];
     const typename P::Sb sbm = P::load_sb(a, si, lane);
 #pragma unroll
     for (int j = 0; j < D; ++j) ch[j] = P::load_ch(a, j * nsb_total + si, lane);
+    if (a.nrm_gamma) {
+        // RMSNorm of x folded in (layers/rmsnorm/cpu.go:70-85): f64 total of
+        // the producer's partial sums, y = f32((x * inv) * gamma).
+        for (int m = 32; m >= 1; m >>= 1) ssp += __shfl_xor(ssp, m, 64);
+        const double inv = 1.0 / sqrt(ssp / double(a.nsb * 256) + a.nrm_eps);
+        xv4.x = float(double(xv4.x) * inv * double(gv4.x));
+        xv4.y = float(double(xv4.y) * inv * double(gv4.y));
+        xv4.z = float(double(xv4.z) * inv * double(gv4.z));
+        xv4.w = float(double(xv4.w) * inv * double(gv4.w));
+    }
 
     // Stage them in this wave's LDS slice (only this wave reads it, so a
     // wave-level LDS wait replaces a block barrier and waves start computing
@@ -379,8 +408,7 @@ __global__ void __launch_bounds__(1024) k_gemv_rpl(RplArgs a, const float* __res
     for (int w = 0; w < W; ++w) s += part[w * 64 + lane];
     const int row = rg * 64 + lane;
     if (a.ksplit == 1) {
-        if (a.mode == RPL_SWIGLU) store_swiglu(a, y, b, row, lane, s);
-        else if (row < a.rows) store_y(a, y, int64_t(b) * a.rows + row, s);
+        finish_rows(a, y, b, rg, lane, s);
         return;
     }
     // K split across gridDim.y blocks: publish the partial, take a ticket.
@@ -398,8 +426,7 @@ __global__ void __launch_bounds__(1024) k_gemv_rpl(RplArgs a, const float* __res
     old = __shfl(old, 0, 64);
     if (old != uint32_t(a.ksplit - 1)) return;
     const float t = sum_partials(pb + row, rows_pad, a.ksplit);
-    if (a.mode == RPL_SWIGLU) store_swiglu(a, y, b, row, lane, t);
-    else if (row < a.rows) store_y(a, y, int64_t(b) * a.rows + row, t);
+    finish_rows(a, y, b, rg, lane, t);
     if (lane == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -430,10 +457,17 @@ int lds_floor() {
 }
 
 template <class P>
-int launch_rpl_t(const DevBlob& bl, const float* x, float* y, int batch, hipStream_t s, int mode, const float* aux) {
+int launch_rpl_t(const DevBlob& bl, const float* x, float* y, int batch, hipStream_t s, const RplExtra& ex) {
     RplArgs a = bl.rpl;
+    const int mode = ex.mode;
+    const float* aux = ex.aux;
     a.mode = mode;
     a.aux = aux;
+    a.nrm_gamma = ex.nrm_gamma;
+    a.nrm_ss = ex.nrm_ss;
+    a.nrm_n = ex.nrm_n;
+    a.nrm_eps = ex.nrm_eps;
+    a.ss_out = ex.ss_out;
     // Waves per block W (super-blocks per block) and K split ks = ceil(nsb/W):
     // among W = 16..4, prefer grids of >= 200 blocks (most of the 256 CUs),
     // then the fewest idle waves (ks*W - nsb), then the largest W; the split
@@ -465,6 +499,8 @@ int launch_rpl_t(const DevBlob& bl, const float* x, float* y, int batch, hipStre
         dim3 grid(unsigned(a.rg_count), unsigned(ksplit), unsigned(ksplit > 1 ? nb : batch - b0));
         RplArgs ab = a;
         if (aux) ab.aux = aux + int64_t(b0) * a.rows;
+        if (ab.nrm_ss) ab.nrm_ss += int64_t(b0) * a.nrm_n;
+        if (ab.ss_out) ab.ss_out += int64_t(b0) * a.rg_count;
         const int64_t ystride = mode == RPL_SWIGLU ? a.rows / 2 : a.rows;
         hipLaunchKernelGGL(kern, grid, dim3(unsigned(64 * W)), lds, s, ab, x + int64_t(b0) * a.nsb * 256,
                            y + int64_t(b0) * ystride);
@@ -743,17 +779,23 @@ int launch_rpl_tr(const DevBlob& bl, const float* gy, float* gx, int batch, hipS
 
 }  // namespace
 
-int launch_rpl(const DevBlob& b, const float* d_x, float* d_y, int batch, void* stream, int mode, const float* aux) {
+int launch_rpl_ex(const DevBlob& b, const float* d_x, float* d_y, int batch, void* stream, const RplExtra& ex) {
     hipStream_t s = static_cast<hipStream_t>(stream);
     switch (b.fmt) {
     case FMT_Q4_K:
-        return int_x() ? launch_rpl_t<RplQ4KI>(b, d_x, d_y, batch, s, mode, aux)
-                       : launch_rpl_t<RplQ4K>(b, d_x, d_y, batch, s, mode, aux);
-    case FMT_Q6_K: return launch_rpl_t<RplQ6K>(b, d_x, d_y, batch, s, mode, aux);
-    case FMT_Q8_0: return launch_rpl_t<RplQ8>(b, d_x, d_y, batch, s, mode, aux);
-    case FMT_Q4_0: return launch_rpl_t<RplQ4>(b, d_x, d_y, batch, s, mode, aux);
+        return int_x() ? launch_rpl_t<RplQ4KI>(b, d_x, d_y, batch, s, ex) : launch_rpl_t<RplQ4K>(b, d_x, d_y, batch, s, ex);
+    case FMT_Q6_K: return launch_rpl_t<RplQ6K>(b, d_x, d_y, batch, s, ex);
+    case FMT_Q8_0: return launch_rpl_t<RplQ8>(b, d_x, d_y, batch, s, ex);
+    case FMT_Q4_0: return launch_rpl_t<RplQ4>(b, d_x, d_y, batch, s, ex);
     default: return int(hipErrorInvalidValue);
     }
+}
+
+int launch_rpl(const DevBlob& b, const float* d_x, float* d_y, int batch, void* stream, int mode, const float* aux) {
+    RplExtra ex;
+    ex.mode = mode;
+    ex.aux = aux;
+    return launch_rpl_ex(b, d_x, d_y, batch, stream, ex);
 }
 
 namespace {

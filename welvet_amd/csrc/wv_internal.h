@@ -103,6 +103,27 @@ struct RplArgs {
     // y[i] = silu(gate_i) * up_i, y holding rows/2 values per batch row.
     int mode;
     const float* aux;  // [batch][rows] gate values for RPL_SILU_MUL
+    // Fused RMSNorm of x (nrm_gamma != nullptr): x is scaled by
+    // inv * gamma, inv = 1/sqrt(sum(x^2)/cols + eps), with sum(x^2) given as
+    // nrm_n partial sums per batch row in nrm_ss (written by the producer).
+    const float* nrm_gamma;
+    const float* nrm_ss;
+    int nrm_n;
+    double nrm_eps;
+    // With RPL_ADD: per-row-group sums of the updated y^2 ([batch][rg]), the
+    // partials the next fused RMSNorm consumes.
+    float* ss_out;
+};
+
+// Options of one forward launch on the row-interleaved layout.
+struct RplExtra {
+    int mode = 0;
+    const float* aux = nullptr;
+    const float* nrm_gamma = nullptr;
+    const float* nrm_ss = nullptr;
+    int nrm_n = 0;
+    double nrm_eps = 0.0;
+    float* ss_out = nullptr;
 };
 enum RplMode { RPL_STORE = 0, RPL_ADD = 1, RPL_SILU_MUL = 2, RPL_SWIGLU = 3 };
 
@@ -137,6 +158,7 @@ struct DevBlob {
 // Kernel launchers (gemv.hip, gemv_rpl.hip). Return a hipError_t as int.
 int launch_rpl(const DevBlob& b, const float* d_x, float* d_y, int batch, void* stream, int mode = RPL_STORE,
                const float* aux = nullptr);
+int launch_rpl_ex(const DevBlob& b, const float* d_x, float* d_y, int batch, void* stream, const RplExtra& ex);
 int launch_matvec(const DevBlob& b, const float* d_x, float* d_y, int batch, void* stream);
 int launch_matvec_t(const DevBlob& b, const float* d_gy, float* d_gx, int batch, void* stream, float* d_scratch);
 // Fused row-interleaved images (gemv_rpl.hip), built on the device from
