@@ -118,6 +118,34 @@ def test_row_interleaved_split_and_batch(fmt, shape, batch):
         assert normwise(d.matvec(x), ref) <= TOL
 
 
+# Shapes that select each launch plan of the row-interleaved forward kernel:
+# lanes per row L (1, 2, 4) with one or two super-blocks per wave S for
+# K <= 4096, and a K split across blocks for wider matrices.
+PLAN_SHAPES = [
+    ((12800, 1024), ["Q4_K", "Q6_K", "Q8_0", "Q4_0"]),  # L=1 S=1
+    ((8192, 1024), ["Q4_K", "Q6_K", "Q8_0", "Q4_0"]),   # L=2 S=1
+    ((1000, 2048), ["Q4_K", "Q6_K", "Q8_0", "Q4_0"]),   # L=4 S=2
+    ((8192, 8192), ["Q4_K", "Q8_0"]),                   # K split 2
+    ((2048, 16640), ["Q4_K", "Q6_K", "Q8_0", "Q4_0"]),  # K split 5 over 13-wave blocks
+    ((6400, 16640), ["Q4_K"]),                          # K split 2, 65 super-blocks
+]
+
+
+@pytest.mark.parametrize("shape,fmt", [(sh, f) for sh, fs in PLAN_SHAPES for f in fs])
+def test_row_interleaved_plans(shape, fmt):
+    rows, cols = shape
+    print(f"[gpu] rpl plan {fmt} {cols}->{rows}", flush=True)
+    w, rng = weights(rows, cols, 3)
+    batch = 10 if rows * cols <= 40_000_000 else 2  # > 8 batch rows: two launches when K is split
+    x = rng.standard_normal((batch, cols)).astype(np.float32)
+    p, d = upload(fmt, w, rows, cols)
+    assert d.info()["layout"] == "row-interleaved"
+    ref = oracle.reference_y(oracle_packed(p), x)
+    for _ in range(2):
+        assert normwise(d.matvec(x), ref) <= TOL
+    d.free()
+
+
 def test_q4_0_baseline_4096():
     w, rng = weights(4096, 4096, 1)
     x = rng.standard_normal(4096).astype(np.float32)

@@ -40,12 +40,12 @@ __global__ void __launch_bounds__(256) k_embed(const float* __restrict__ table, 
     const int t = min(max(*tok, 0), vocab - 1);
     for (int i = blockIdx.x * 256 + threadIdx.x; i < hidden; i += gridDim.x * 256)
         h[i] = table[int64_t(t) * hidden + i];
-    if (ss) {  // sums of h^2 per 64 elements, for the first layer's fused RMSNorm
+    if (ss) {  // sums of h^2 per 16 elements, for the first layer's fused RMSNorm
         const int i = blockIdx.x * 256 + threadIdx.x;
         const float v = i < hidden ? table[int64_t(t) * hidden + i] : 0.f;
         float q = v * v;
-        for (int m = 32; m >= 1; m >>= 1) q += __shfl_xor(q, m, 64);
-        if ((threadIdx.x & 63) == 0 && i < hidden) ss[i >> 6] = q;
+        for (int m = 8; m >= 1; m >>= 1) q += __shfl_xor(q, m, 64);
+        if ((threadIdx.x & 15) == 0 && i < hidden) ss[i >> 4] = q;
     }
     if (blockIdx.x == 0) {
         const double pos = double(*d_pos);
@@ -398,8 +398,8 @@ struct Decoder {
     int32_t* d_pos = nullptr;    // = d_state
     int32_t* d_tok = nullptr;    // = d_state + 1
     int32_t* d_gen = nullptr;    // [max_seq] generated tokens
-    float* ss_a = nullptr;       // [hidden/64] partial sums of h^2 for the attention norm / final norm
-    float* ss_b = nullptr;       // [hidden/64] partial sums of h^2 for the FFN norm
+    float* ss_a = nullptr;       // [hidden/16] partial sums of h^2 for the attention norm / final norm
+    float* ss_b = nullptr;       // [hidden/16] partial sums of h^2 for the FFN norm
     bool fused_norm = false;     // every norm folded into its consumer GEMV
     double* freq_div = nullptr;  // [head_dim/2] theta^(2d/hd)
     double2* cs = nullptr;       // [head_dim/2] this step's (cos, sin)
@@ -473,7 +473,7 @@ int enqueue_step(Decoder& d, int advance) {
     const float scale = float(1.0 / std::sqrt(double(hd)));
     const int G = c.n_heads / c.n_kv_heads;
     const bool fn = d.fused_norm;
-    const int nss = c.hidden / 64;
+    const int nss = c.hidden / 16;  // sum-of-squares partials per 16 rows
     hipLaunchKernelGGL(k_embed, dim3((c.hidden + 255) / 256), dim3(256), 0, d.stream, d.embed, d.d_tok, d.h, c.hidden,
                        c.vocab, d.freq_div, d.cs, hd / 2, d.d_pos, fn ? d.ss_a : nullptr);
     float* tmp = d.logits;  // scratch for the non-fused projection epilogues (>= max(rows) floats)
@@ -650,7 +650,7 @@ int wv_decoder_create(const wv_decoder_config* cfg, uint64_t* handle) {
     const size_t wide = std::max({size_t(c.hidden), q_dim, size_t(c.ffn), size_t(c.vocab)});
     struct B { float** p; size_t n; };
     B bufs[] = {{&d->h, size_t(c.hidden)}, {&d->n, size_t(c.hidden)}, {&d->q, q_dim + 2 * kv_dim},
-                {&d->ss_a, size_t(c.hidden / 64 + 1)}, {&d->ss_b, size_t(c.hidden / 64 + 1)},
+                {&d->ss_a, size_t(c.hidden / 16 + 1)}, {&d->ss_b, size_t(c.hidden / 16 + 1)},
                 {&d->att, q_dim}, {&d->g, size_t(c.ffn)}, {&d->u, size_t(c.ffn)}, {&d->logits, wide},
                 {&d->part, size_t(c.n_heads) * d->n_chunks * (c.head_dim + 2)}};
     for (B& b : bufs) {

@@ -101,6 +101,16 @@ struct RplQ4K {  // w = dmin*m/127 + (d*u/255)*q  (quant/kquant.go:178-188)
         const float2 dd = reinterpret_cast<const float2*>(a.dd)[si * 64 + lane];
         return {ld_stream(m), ld_stream(m + 1), dd.x * (1.0f / 255.0f), dd.y * (1.0f / 127.0f)};
     }
+    // Chunk j's metadata word, and an Sb whose chunk-0 word is w (lets a
+    // kernel pick a word per lane and call dot with j = 0).
+    static __device__ __forceinline__ uint32_t word(const Sb& sb, int j) {
+        const uint32_t gw[8] = {sb.g0.x, sb.g0.y, sb.g0.z, sb.g0.w, sb.g1.x, sb.g1.y, sb.g1.z, sb.g1.w};
+        return gw[j];
+    }
+    static __device__ __forceinline__ Sb with_word(Sb sb, uint32_t w) {
+        sb.g0.x = w;
+        return sb;
+    }
     static __device__ __forceinline__ float dot(const Ch& ch, const Sb& sb, int j, const float* x, float s0, float s1) {
         const uint32_t gw[8] = {sb.g0.x, sb.g0.y, sb.g0.z, sb.g0.w, sb.g1.x, sb.g1.y, sb.g1.z, sb.g1.w};
         const uint32_t g = gw[j];  // (u'0, u'1, m0, m1) bytes
@@ -173,6 +183,14 @@ struct RplQ6K {  // q = lo4 | hi2 << 4, w = (d*u/255)*(q - 32)
         a = fmaf(ub3(hi), x[7], a);
         return a;
     }
+    static __device__ __forceinline__ uint32_t word(const Sb& sb, int j) {
+        const uint32_t gw[4] = {sb.g.x, sb.g.y, sb.g.z, sb.g.w};
+        return gw[j >> 1] >> (16 * (j & 1));
+    }
+    static __device__ __forceinline__ Sb with_word(Sb sb, uint32_t w) {
+        sb.g.x = w;
+        return sb;
+    }
     static __device__ __forceinline__ float dot(const Ch& ch, const Sb& sb, int j, const float* x, float s0, float s1) {
         const uint32_t gw[4] = {sb.g.x, sb.g.y, sb.g.z, sb.g.w};
         const uint32_t g = gw[j >> 1] >> (16 * (j & 1));  // (u'0, u'1) bytes
@@ -193,6 +211,14 @@ struct RplQ8 {  // w = scale * q, q int8; q + 128 converts as an unsigned byte
     static __device__ __forceinline__ Sb load_sb(const RplArgs& a, int64_t si, int lane) {
         const uint4* m = reinterpret_cast<const uint4*>(a.meta) + (si * 64 + lane) * 2;
         return {ld_stream(m), ld_stream(m + 1)};
+    }
+    static __device__ __forceinline__ uint32_t word(const Sb& sb, int j) {
+        const uint32_t sw[8] = {sb.s0.x, sb.s0.y, sb.s0.z, sb.s0.w, sb.s1.x, sb.s1.y, sb.s1.z, sb.s1.w};
+        return sw[j];
+    }
+    static __device__ __forceinline__ Sb with_word(Sb sb, uint32_t w) {
+        sb.s0.x = w;
+        return sb;
     }
     static __device__ __forceinline__ float dot(const Ch& ch, const Sb& sb, int j, const float* x, float s0, float s1) {
         const uint32_t sw[8] = {sb.s0.x, sb.s0.y, sb.s0.z, sb.s0.w, sb.s1.x, sb.s1.y, sb.s1.z, sb.s1.w};
@@ -215,6 +241,14 @@ struct RplQ4 {  // w = scale * q, q signed nibble; q ^ 8 = q + 8
     static __device__ __forceinline__ Sb load_sb(const RplArgs& a, int64_t si, int lane) {
         const uint4* m = reinterpret_cast<const uint4*>(a.meta) + (si * 64 + lane) * 2;
         return {ld_stream(m), ld_stream(m + 1)};
+    }
+    static __device__ __forceinline__ uint32_t word(const Sb& sb, int j) {
+        const uint32_t sw[8] = {sb.s0.x, sb.s0.y, sb.s0.z, sb.s0.w, sb.s1.x, sb.s1.y, sb.s1.z, sb.s1.w};
+        return sw[j];
+    }
+    static __device__ __forceinline__ Sb with_word(Sb sb, uint32_t w) {
+        sb.s0.x = w;
+        return sb;
     }
     static __device__ __forceinline__ float dot(const Ch& ch, const Sb& sb, int j, const float* x, float s0, float s1) {
         const uint32_t sw[8] = {sb.s0.x, sb.s0.y, sb.s0.z, sb.s0.w, sb.s1.x, sb.s1.y, sb.s1.z, sb.s1.w};
@@ -255,109 +289,167 @@ __device__ __forceinline__ float store_y(const RplArgs& a, float* y, int64_t idx
     return s;
 }
 
-// Epilogue of one row group (all 64 lanes of the wave call it): store, and
-// for a fused-RMSNorm producer the sum of the group's stored y^2.
-__device__ __forceinline__ void finish_rows(const RplArgs& a, float* y, int b, int rg, int lane, float s) {
-    const int row = rg * 64 + lane;
+// Epilogue of one wave of output rows (all 64 lanes call it; lanes with
+// `valid` own row `row`): store, and for a fused-RMSNorm producer the sums of
+// the stored y^2 over each 16 consecutive rows ([batch][rg_count*4]).
+__device__ __forceinline__ void finish_rows(const RplArgs& a, float* y, int b, int row, bool valid, int lane, float s) {
     if (a.mode == RPL_SWIGLU) {
         const float u = __shfl_xor(s, 1, 64);
-        if (!(lane & 1) && row < a.rows) y[int64_t(b) * (a.rows / 2) + row / 2] = s / (1.0f + expf(-s)) * u;
+        if (valid && !(lane & 1) && row < a.rows) y[int64_t(b) * (a.rows / 2) + row / 2] = s / (1.0f + expf(-s)) * u;
         return;
     }
     float v = 0.f;
-    if (row < a.rows) v = store_y(a, y, int64_t(b) * a.rows + row, s);
+    if (valid && row < a.rows) v = store_y(a, y, int64_t(b) * a.rows + row, s);
     if (a.ss_out) {
         float q = v * v;
-        for (int m = 32; m >= 1; m >>= 1) q += __shfl_xor(q, m, 64);
-        if (lane == 0) a.ss_out[int64_t(b) * a.rg_count + rg] = q;
+        for (int m = 8; m >= 1; m >>= 1) q += __shfl_xor(q, m, 64);
+        if (valid && (lane & 15) == 0) a.ss_out[int64_t(b) * a.rg_count * 4 + row / 16] = q;
     }
 }
 
-template <class P, int D>
+// L-way pick of a per-chunk metadata word: chunk base + lg (lg < L). The
+// candidates pass through empty asm statements so that the compiler keeps the
+// selects as v_cndmask: seen as elements of one vector, a per-lane index would
+// become a dynamically indexed extract, which goes through scratch memory.
+template <int L>
+__device__ __forceinline__ uint32_t pick(const uint32_t* c, int lg) {
+    if constexpr (L == 1) {
+        return c[0];
+    } else if constexpr (L == 2) {
+        uint32_t c0 = c[0], c1 = c[1];
+        asm("" : "+v"(c0), "+v"(c1));
+        return (lg & 1) ? c1 : c0;
+    } else {
+        uint32_t c0 = c[0], c1 = c[1], c2 = c[2], c3 = c[3];
+        asm("" : "+v"(c0), "+v"(c1), "+v"(c2), "+v"(c3));
+        const uint32_t lo = (lg & 1) ? c1 : c0, hi = (lg & 1) ? c3 : c2;
+        return (lg & 2) ? hi : lo;
+    }
+}
+
+// The row-interleaved forward kernel.
+//   Block (hx, ks, b): row group rg = hx / L, row subgroup h = hx % L (R = 64/L
+//   rows), K slice ks, batch row b. W waves; wave w owns S consecutive
+//   super-blocks starting at (ks*W + w)*S.
+//   Lane = (lg, r) = (lane / R, lane % R): row rg*64 + h*R + r; lane group lg
+//   takes chunks lg, lg+L, ... of each super-block, so one load instruction
+//   reads L runs of R*16 bytes.
+//   Per lane: T = S*8/L chunk steps, D of them in flight (ring).
+// L > 1 splits a 64-row group over L blocks and S > 1 lets a wave cover more
+// columns, so that shapes with few rows fill the GPU without a K split.
+template <class P, int L, int S, int D>
 __global__ void __launch_bounds__(1024) k_gemv_rpl(RplArgs a, const float* __restrict__ x, float* __restrict__ y) {
+    constexpr int R = 64 / L;
+    constexpr int CPL = 8 / L;    // chunks per super-block per lane
+    constexpr int T = S * CPL;    // chunk steps per lane
+    constexpr int DD = D < T ? D : T;
     extern __shared__ float4 sm4[];
     const int W = blockDim.x >> 6;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
-    const int rg = blockIdx.x, ks = blockIdx.y, b = blockIdx.z;
-    const int sb = ks * W + wave;
-    const bool active = sb < a.nsb;
-    const int sbc = active ? sb : a.nsb - 1;
-    const int64_t si = int64_t(rg) * a.nsb + sbc;
-    // chunk j of super-block si sits at plane index j*nsb_total + si
+    const int lg = lane / R, r = lane % R;
+    const int hx = blockIdx.x, ks = blockIdx.y, b = blockIdx.z;
+    const int rg = hx / L, h = hx % L;
+    const int sl = h * R + r;  // this lane's row slot inside the row group
+    const int sb0 = (ks * W + wave) * S;
     const int64_t nsb_total = int64_t(a.rg_count) * a.nsb;
+    bool act[S];
+    int64_t si[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+        act[s] = sb0 + s < a.nsb;
+        si[s] = int64_t(rg) * a.nsb + (act[s] ? sb0 + s : a.nsb - 1);
+    }
 
-    // This wave's 256 x values: one float4 per lane, issued before the
+    // x for the S super-blocks (one float4 per lane each), issued before the
     // weights so that waiting for x does not wait for weight data (vector
-    // loads retire in issue order).
-    float4 xv4 = reinterpret_cast<const float4*>(x + int64_t(b) * a.nsb * 256 + int64_t(sbc) * 256)[lane];
-    float4 gv4 = make_float4(1.f, 1.f, 1.f, 1.f);
+    // loads retire in issue order); then the metadata and the first chunks.
+    float4 xv4[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+        xv4[s] = reinterpret_cast<const float4*>(x + int64_t(b) * a.nsb * 256 + (si[s] - int64_t(rg) * a.nsb) * 256)[lane];
+    float4 gv4[S];
     double ssp = 0.0;
     if (a.nrm_gamma) {
-        gv4 = reinterpret_cast<const float4*>(a.nrm_gamma + int64_t(sbc) * 256)[lane];
+#pragma unroll
+        for (int s = 0; s < S; ++s)
+            gv4[s] = reinterpret_cast<const float4*>(a.nrm_gamma + (si[s] - int64_t(rg) * a.nsb) * 256)[lane];
         for (int i = lane; i < a.nrm_n; i += 64) ssp += a.nrm_ss[int64_t(b) * a.nrm_n + i];
     }
-    typename P::Ch ch[8];
-    const typename P::Sb sbm = P::load_sb(a, si, lane);
+    typename P::Sb sbm[S];
 #pragma unroll
-    for (int j = 0; j < D; ++j) ch[j] = P::load_ch(a, j * nsb_total + si, lane);
+    for (int s = 0; s < S; ++s) sbm[s] = P::load_sb(a, si[s], sl);
+    auto chunk_index = [&](int t) {  // plane index of step t's chunk for this lane
+        const int s = t / CPL, j = lg + L * (t % CPL);
+        return int64_t(j) * nsb_total + si[s];
+    };
+    typename P::Ch ch[T];
+#pragma unroll
+    for (int t = 0; t < DD; ++t) ch[t] = P::load_ch(a, chunk_index(t), sl);
     if (a.nrm_gamma) {
         // RMSNorm of x folded in (layers/rmsnorm/cpu.go:70-85): f64 total of
         // the producer's partial sums, y = f32((x * inv) * gamma).
         for (int m = 32; m >= 1; m >>= 1) ssp += __shfl_xor(ssp, m, 64);
         const double inv = 1.0 / sqrt(ssp / double(a.nsb * 256) + a.nrm_eps);
-        xv4.x = float(double(xv4.x) * inv * double(gv4.x));
-        xv4.y = float(double(xv4.y) * inv * double(gv4.y));
-        xv4.z = float(double(xv4.z) * inv * double(gv4.z));
-        xv4.w = float(double(xv4.w) * inv * double(gv4.w));
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            xv4[s].x = float(double(xv4[s].x) * inv * double(gv4[s].x));
+            xv4[s].y = float(double(xv4[s].y) * inv * double(gv4[s].y));
+            xv4[s].z = float(double(xv4[s].z) * inv * double(gv4[s].z));
+            xv4[s].w = float(double(xv4[s].w) * inv * double(gv4[s].w));
+        }
     }
 
-    // Stage them in this wave's LDS slice (only this wave reads it, so a
-    // wave-level LDS wait replaces a block barrier and waves start computing
-    // as soon as their own data is in).
+    // Stage x in this wave's LDS slice (only this wave reads it, so a
+    // wave-level LDS wait replaces a block barrier), one kSlice per super-block:
     //   f32 policies: [256 x][16 sums of 16 columns]
     //   int policies: per chunk 24 dwords of X byte planes + 4 floats meta
     constexpr int kSlice = 256 + 16;
-    float* xs = reinterpret_cast<float*>(sm4) + wave * kSlice;
-    float* part = reinterpret_cast<float*>(sm4) + W * kSlice;  // [W*64]
-    float gsum = (xv4.x + xv4.y) + (xv4.z + xv4.w);
-    gsum += __shfl_xor(gsum, 1, 64);
-    gsum += __shfl_xor(gsum, 2, 64);  // lanes 4g..4g+3: sum of columns 16g..16g+15
-    if constexpr (!P::kIntX) {
-        reinterpret_cast<float4*>(xs)[lane] = xv4;
-        if ((lane & 3) == 0) xs[256 + (lane >> 2)] = gsum;
-    } else {
-        // lane = 8c + q holds columns 4q..4q+3 of chunk c
-        const int c = lane >> 3, q = lane & 7;
-        float m = fmaxf(fmaxf(fabsf(xv4.x), fabsf(xv4.y)), fmaxf(fabsf(xv4.z), fabsf(xv4.w)));
-        m = fmaxf(m, __shfl_xor(m, 1, 64));
-        m = fmaxf(m, __shfl_xor(m, 2, 64));
-        m = fmaxf(m, __shfl_xor(m, 4, 64));
-        int e = 0;
-        frexpf(m, &e);
-        const int sh = m > 0.f ? 22 - e : 0;  // |x| * 2^sh < 2^22
-        const int X0 = int(rintf(ldexpf(xv4.x, sh))), X1 = int(rintf(ldexpf(xv4.y, sh)));
-        const int X2 = int(rintf(ldexpf(xv4.z, sh))), X3 = int(rintf(ldexpf(xv4.w, sh)));
-        // code word w = q/2 covers columns 8w..8w+7; its lo spread word holds
-        // columns 8w+{0,2,4,6}, its hi spread word 8w+{1,3,5,7}: this lane
-        // supplies the byte pair at half (q & 1) of each.
-        uint16_t* h16 = reinterpret_cast<uint16_t*>(xs + c * 28);
-        const int w = q >> 1, half = q & 1;
+    float* xw = reinterpret_cast<float*>(sm4) + wave * (S * kSlice);
+    float* part = reinterpret_cast<float*>(sm4) + W * (S * kSlice);  // [W*64]
 #pragma unroll
-        for (int pl = 0; pl < 3; ++pl) {
-            const int sb8 = 8 * pl;
-            const uint32_t blo = (uint32_t(X0 >> sb8) & 255u) | ((uint32_t(X2 >> sb8) & 255u) << 8);
-            const uint32_t bhi = (uint32_t(X1 >> sb8) & 255u) | ((uint32_t(X3 >> sb8) & 255u) << 8);
-            h16[(pl * 8 + w) * 2 + half] = uint16_t(blo);
-            h16[(pl * 8 + 4 + w) * 2 + half] = uint16_t(bhi);
-        }
-        const float s0 = __shfl(gsum, lane & ~7, 64), s1 = __shfl(gsum, (lane & ~7) + 4, 64);
-        if (q == 0) {
-            float* xm = xs + c * 28 + 24;
-            xm[0] = ldexpf(1.0f, -sh) * (1.0f / 255.0f);
-            xm[1] = s0;
-            xm[2] = s1;
-            xm[3] = -128.0f * (s0 + s1);
+    for (int s = 0; s < S; ++s) {
+        float* xs = xw + s * kSlice;
+        const float4 xv = xv4[s];
+        float gsum = (xv.x + xv.y) + (xv.z + xv.w);
+        gsum += __shfl_xor(gsum, 1, 64);
+        gsum += __shfl_xor(gsum, 2, 64);  // lanes 4g..4g+3: sum of columns 16g..16g+15
+        if constexpr (!P::kIntX) {
+            reinterpret_cast<float4*>(xs)[lane] = xv;
+            if ((lane & 3) == 0) xs[256 + (lane >> 2)] = gsum;
+        } else {
+            // lane = 8c + q holds columns 4q..4q+3 of chunk c
+            const int c = lane >> 3, q = lane & 7;
+            float m = fmaxf(fmaxf(fabsf(xv.x), fabsf(xv.y)), fmaxf(fabsf(xv.z), fabsf(xv.w)));
+            m = fmaxf(m, __shfl_xor(m, 1, 64));
+            m = fmaxf(m, __shfl_xor(m, 2, 64));
+            m = fmaxf(m, __shfl_xor(m, 4, 64));
+            int e = 0;
+            frexpf(m, &e);
+            const int sh = m > 0.f ? 22 - e : 0;  // |x| * 2^sh < 2^22
+            const int X0 = int(rintf(ldexpf(xv.x, sh))), X1 = int(rintf(ldexpf(xv.y, sh)));
+            const int X2 = int(rintf(ldexpf(xv.z, sh))), X3 = int(rintf(ldexpf(xv.w, sh)));
+            // code word w = q/2 covers columns 8w..8w+7; its lo spread word holds
+            // columns 8w+{0,2,4,6}, its hi spread word 8w+{1,3,5,7}: this lane
+            // supplies the byte pair at half (q & 1) of each.
+            uint16_t* h16 = reinterpret_cast<uint16_t*>(xs + c * 28);
+            const int w = q >> 1, half = q & 1;
+#pragma unroll
+            for (int pl = 0; pl < 3; ++pl) {
+                const int sb8 = 8 * pl;
+                const uint32_t blo = (uint32_t(X0 >> sb8) & 255u) | ((uint32_t(X2 >> sb8) & 255u) << 8);
+                const uint32_t bhi = (uint32_t(X1 >> sb8) & 255u) | ((uint32_t(X3 >> sb8) & 255u) << 8);
+                h16[(pl * 8 + w) * 2 + half] = uint16_t(blo);
+                h16[(pl * 8 + 4 + w) * 2 + half] = uint16_t(bhi);
+            }
+            const float s0 = __shfl(gsum, lane & ~7, 64), s1 = __shfl(gsum, (lane & ~7) + 4, 64);
+            if (q == 0) {
+                float* xm = xs + c * 28 + 24;
+                xm[0] = ldexpf(1.0f, -sh) * (1.0f / 255.0f);
+                xm[1] = s0;
+                xm[2] = s1;
+                xm[3] = -128.0f * (s0 + s1);
+            }
         }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -366,49 +458,64 @@ __global__ void __launch_bounds__(1024) k_gemv_rpl(RplArgs a, const float* __res
 
     float acc = 0.f;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        if (j + D < 8) ch[j + D] = P::load_ch(a, (j + D) * nsb_total + si, lane);
+    for (int t = 0; t < T; ++t) {
+        if (t + DD < T) ch[t + DD] = P::load_ch(a, chunk_index(t + DD), sl);
         __builtin_amdgcn_sched_barrier(0);
-        if constexpr (P::kIntX) {
-            if (active) {
+        const int s = t / CPL, jb = L * (t % CPL);  // chunk = jb + lg
+        if (act[s]) {
+            // this step's metadata word for chunk jb + lg, moved to slot 0
+            typename P::Sb mv = sbm[s];
+            int jsel = jb;
+            if constexpr (L > 1) {
+                uint32_t cand[L];
+#pragma unroll
+                for (int i = 0; i < L; ++i) cand[i] = P::word(sbm[s], jb + i);
+                mv = P::with_word(sbm[s], pick<L>(cand, lg));
+                jsel = 0;
+            }
+            const float* xs = xw + s * kSlice;
+            const int j = jb + lg;
+            if constexpr (P::kIntX) {
                 const uint4* xq = reinterpret_cast<const uint4*>(xs + j * 28);
                 uint32_t xi[24];
 #pragma unroll
                 for (int k = 0; k < 6; ++k) {
-                    const uint4 t = xq[k];
-                    xi[4 * k] = t.x;
-                    xi[4 * k + 1] = t.y;
-                    xi[4 * k + 2] = t.z;
-                    xi[4 * k + 3] = t.w;
+                    const uint4 tq = xq[k];
+                    xi[4 * k] = tq.x;
+                    xi[4 * k + 1] = tq.y;
+                    xi[4 * k + 2] = tq.z;
+                    xi[4 * k + 3] = tq.w;
                 }
-                acc += P::dot_i(ch[j], sbm, j, xi, reinterpret_cast<const float4*>(xq)[6]);
-            }
-        } else {
-            if (active) {
+                acc += P::dot_i(ch[t], mv, jsel, xi, reinterpret_cast<const float4*>(xq)[6]);
+            } else {
                 const float4* xq = reinterpret_cast<const float4*>(xs + j * 32);
                 float xv[32];
 #pragma unroll
                 for (int k = 0; k < 8; ++k) {
-                    const float4 t = xq[k];
-                    xv[4 * k] = t.x;
-                    xv[4 * k + 1] = t.y;
-                    xv[4 * k + 2] = t.z;
-                    xv[4 * k + 3] = t.w;
+                    const float4 tq = xq[k];
+                    xv[4 * k] = tq.x;
+                    xv[4 * k + 1] = tq.y;
+                    xv[4 * k + 2] = tq.z;
+                    xv[4 * k + 3] = tq.w;
                 }
                 const float2 s2 = reinterpret_cast<const float2*>(xs + 256)[j];
-                acc += P::dot(ch[j], sbm, j, xv, s2.x, s2.y);
+                acc += P::dot(ch[t], mv, jsel, xv, s2.x, s2.y);
             }
         }
         __builtin_amdgcn_sched_barrier(0);
     }
+    // the L lane groups of a row hold partial sums of different chunks
+#pragma unroll
+    for (int o = R; o < 64; o <<= 1) acc += __shfl_xor(acc, o, 64);
     part[wave * 64 + lane] = acc;
     __syncthreads();
     if (wave != 0) return;
-    float s = 0.f;
-    for (int w = 0; w < W; ++w) s += part[w * 64 + lane];
-    const int row = rg * 64 + lane;
+    float sum = 0.f;
+    for (int w = 0; w < W; ++w) sum += part[w * 64 + lane];
+    const int row = rg * 64 + sl;
+    const bool valid = lane < R;
     if (a.ksplit == 1) {
-        finish_rows(a, y, b, rg, lane, s);
+        finish_rows(a, y, b, row, valid, lane, sum);
         return;
     }
     // K split across gridDim.y blocks: publish the partial, take a ticket.
@@ -417,16 +524,16 @@ __global__ void __launch_bounds__(1024) k_gemv_rpl(RplArgs a, const float* __res
     // for the stores before the ticket, so no L2 writeback/invalidate is needed.
     const int64_t rows_pad = int64_t(a.rg_count) * 64;
     float* pb = a.partial + int64_t(b) * a.ksplit * rows_pad;
-    __hip_atomic_store(pb + int64_t(ks) * rows_pad + row, s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (valid) __hip_atomic_store(pb + int64_t(ks) * rows_pad + row, sum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     __builtin_amdgcn_s_waitcnt(0);
-    uint32_t* ctr = a.counters + int64_t(b) * a.rg_count + rg;
+    uint32_t* ctr = a.counters + int64_t(b) * a.rg_count * 4 + hx;
     uint32_t old = 0;
     if (lane == 0) old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     old = __shfl(old, 0, 64);
     if (old != uint32_t(a.ksplit - 1)) return;
-    const float t = sum_partials(pb + row, rows_pad, a.ksplit);
-    finish_rows(a, y, b, rg, lane, t);
+    const float tsum = valid ? sum_partials(pb + row, rows_pad, a.ksplit) : 0.f;
+    finish_rows(a, y, b, row, valid, lane, tsum);
     if (lane == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -447,13 +554,65 @@ int int_x() {
     static const int v = env_int("WV_RPL_INT", 1);
     return v;
 }
-int prefetch_depth() {
-    static const int v = env_int("WV_RPL_DEPTH", 4);
-    return v;
-}
 int lds_floor() {
     static const int v = env_int("WV_RPL_LDS_MIN", 0);
     return v;
+}
+
+// Launch plan of the forward kernel: lanes per row L, super-blocks per wave
+// S, waves per block W and K split (measured on MI355X):
+//   * up to 16 super-blocks (K <= 4096): one wave per super-block, and L
+//     doubles (to 4) until the grid (row groups x L) has >= 180 blocks; a lane
+//     keeps >= 4 chunk steps, so L = 4 takes two super-blocks per wave.
+//     4096x4096 runs in 5.1 us with L=4 S=2 against 7.2 us with L=1.
+//   * wider: L = S = 1 and K split over blocks of W = 16..4 waves (more
+//     super-blocks per wave or more lanes per row measured slower there:
+//     4096x14336 takes 11.2 us split 4 ways, 12.4-21 us otherwise); W prefers
+//     grids of >= min_blocks() blocks, then the fewest idle waves, then the
+//     largest W, and the split is capped by the scratch the blob carries.
+struct RplPlan {
+    int L, S, W, ksplit;
+};
+RplPlan rpl_plan(const DevBlob& bl) {
+    const RplArgs& a = bl.rpl;
+    RplPlan p{1, 1, 1, 1};
+    static const int fl = env_int("WV_RPL_L", 0), fs = env_int("WV_RPL_S", 0);
+    if (a.nsb <= 16) {
+        while (p.L < 4 && int64_t(a.rg_count) * p.L < 180) p.L *= 2;
+        if (p.L == 4 && a.nsb >= 2) p.S = 2;
+    } else {
+        const int target = min_blocks();
+        int best = -1;
+        for (int w = 16; w >= 4; --w) {
+            const int k = (a.nsb + w - 1) / w;
+            if (k > bl.rpl_max_split) continue;
+            const bool fills = int64_t(a.rg_count) * k >= target;
+            const int idle = k * w - a.nsb;
+            const int score = (fills ? 1 << 20 : 0) + (1 << 10) * (64 - std::min(idle, 63)) + w;
+            if (score > best) {
+                best = score;
+                p.W = w;
+            }
+        }
+    }
+    if (fl == 1 || fl == 2 || fl == 4) p.L = fl;
+    if (fs == 1 || fs == 2 || fs == 4) p.S = fs;
+    const int waves = (a.nsb + p.S - 1) / p.S;
+    if (a.nsb <= 16 || fl || fs) p.W = std::min(16, waves);
+    const int fw = forced_waves();
+    if (fw > 0 && fw <= 16) p.W = fw;
+    p.W = std::min(p.W, waves);
+    p.ksplit = (waves + p.W - 1) / p.W;
+    if (p.ksplit > bl.rpl_max_split) {  // overrides beyond the scratch: fall back to the widest blocks
+        p.W = std::min(16, waves);
+        p.ksplit = (waves + p.W - 1) / p.W;
+    }
+    return p;
+}
+
+template <class P, int L, int S>
+void launch_rpl_ls(const RplArgs& a, const RplPlan& p, dim3 grid, size_t lds, hipStream_t s, const float* x, float* y) {
+    hipLaunchKernelGGL((k_gemv_rpl<P, L, S, 4>), grid, dim3(unsigned(64 * p.W)), lds, s, a, x, y);
 }
 
 template <class P>
@@ -468,43 +627,32 @@ int launch_rpl_t(const DevBlob& bl, const float* x, float* y, int batch, hipStre
     a.nrm_n = ex.nrm_n;
     a.nrm_eps = ex.nrm_eps;
     a.ss_out = ex.ss_out;
-    // Waves per block W (super-blocks per block) and K split ks = ceil(nsb/W):
-    // among W = 16..4, prefer grids of >= 200 blocks (most of the 256 CUs),
-    // then the fewest idle waves (ks*W - nsb), then the largest W; the split
-    // is capped by the scratch the blob carries.
-    const int target = min_blocks();
-    int W = std::min(16, a.nsb), best_score = -1;
-    for (int w = std::min(16, a.nsb); w >= std::min(4, a.nsb); --w) {
-        const int k = (a.nsb + w - 1) / w;
-        if (k > bl.rpl_max_split) continue;
-        const bool fills = int64_t(a.rg_count) * k >= target;
-        const int idle = k * w - a.nsb;
-        const int score = (fills ? 1 << 20 : 0) + (1 << 10) * (64 - std::min(idle, 63)) + w;
-        if (score > best_score) {
-            best_score = score;
-            W = w;
-        }
-    }
-    const int fw = forced_waves();
-    if (fw > 0 && fw <= 16 && (a.nsb + fw - 1) / fw <= bl.rpl_max_split) W = fw;
-    int ksplit = (a.nsb + W - 1) / W;
-    a.ksplit = ksplit;
-    size_t lds = size_t(W) * (256 + 16 + 64) * sizeof(float);  // kSlice + part per wave
+    const RplPlan p = rpl_plan(bl);
+    a.ksplit = p.ksplit;
+    size_t lds = size_t(p.W) * (p.S * (256 + 16) + 64) * sizeof(float);  // x slices + partial row sums
     lds = std::max(lds, size_t(lds_floor()));
-    auto kern = k_gemv_rpl<P, 2>;
-    if (prefetch_depth() == 3) kern = k_gemv_rpl<P, 3>;
-    if (prefetch_depth() >= 4) kern = k_gemv_rpl<P, 4>;
     for (int b0 = 0; b0 < batch; b0 += bl.rpl_max_batch) {
         const int nb = std::min(bl.rpl_max_batch, batch - b0);
-        dim3 grid(unsigned(a.rg_count), unsigned(ksplit), unsigned(ksplit > 1 ? nb : batch - b0));
+        dim3 grid(unsigned(a.rg_count * p.L), unsigned(p.ksplit), unsigned(p.ksplit > 1 ? nb : batch - b0));
         RplArgs ab = a;
         if (aux) ab.aux = aux + int64_t(b0) * a.rows;
         if (ab.nrm_ss) ab.nrm_ss += int64_t(b0) * a.nrm_n;
-        if (ab.ss_out) ab.ss_out += int64_t(b0) * a.rg_count;
+        if (ab.ss_out) ab.ss_out += int64_t(b0) * a.rg_count * 4;
         const int64_t ystride = mode == RPL_SWIGLU ? a.rows / 2 : a.rows;
-        hipLaunchKernelGGL(kern, grid, dim3(unsigned(64 * W)), lds, s, ab, x + int64_t(b0) * a.nsb * 256,
-                           y + int64_t(b0) * ystride);
-        if (ksplit == 1) break;  // one launch covers every batch row
+        const float* xb = x + int64_t(b0) * a.nsb * 256;
+        float* yb = y + int64_t(b0) * ystride;
+        switch (p.L * 8 + p.S) {
+        case 9: launch_rpl_ls<P, 1, 1>(ab, p, grid, lds, s, xb, yb); break;
+        case 10: launch_rpl_ls<P, 1, 2>(ab, p, grid, lds, s, xb, yb); break;
+        case 12: launch_rpl_ls<P, 1, 4>(ab, p, grid, lds, s, xb, yb); break;
+        case 17: launch_rpl_ls<P, 2, 1>(ab, p, grid, lds, s, xb, yb); break;
+        case 18: launch_rpl_ls<P, 2, 2>(ab, p, grid, lds, s, xb, yb); break;
+        case 20: launch_rpl_ls<P, 2, 4>(ab, p, grid, lds, s, xb, yb); break;
+        case 33: launch_rpl_ls<P, 4, 1>(ab, p, grid, lds, s, xb, yb); break;
+        case 34: launch_rpl_ls<P, 4, 2>(ab, p, grid, lds, s, xb, yb); break;
+        default: launch_rpl_ls<P, 4, 4>(ab, p, grid, lds, s, xb, yb); break;
+        }
+        if (p.ksplit == 1) break;  // one launch covers every batch row
     }
     return int(hipGetLastError());
 }
@@ -852,7 +1000,7 @@ FusedLayout fused_layout(const RplItems& it, int64_t rg, int64_t nsb, int max_ba
     f.dd = it.db ? add(per * it.db) : 0;
     f.weights = f.total;
     f.part = add(size_t(max_batch) * max_split * rg * 64 * sizeof(float));
-    f.ctr = add(size_t(max_batch) * rg * sizeof(uint32_t));
+    f.ctr = add(size_t(max_batch) * rg * 4 * sizeof(uint32_t));
     return f;
 }
 

@@ -389,7 +389,7 @@ int wv_blob_upload(int format, int64_t rows, int64_t cols, int32_t block_weights
         b.rpl_max_batch = 8;
         b.rpl_max_split = int(std::max<int64_t>(1, (nsb + 3) / 4));
         o_part = img.add(size_t(b.rpl_max_batch) * b.rpl_max_split * rg * 64 * sizeof(float));
-        o_ctr = img.add(size_t(b.rpl_max_batch) * rg * sizeof(uint32_t));
+        o_ctr = img.add(size_t(b.rpl_max_batch) * rg * 4 * sizeof(uint32_t));  // per (row group, row subgroup)
         RplArgs shape{};
         shape.rows = int(rows);
         shape.nsb = int(nsb);

@@ -95,7 +95,7 @@ struct RplArgs {
     const uint8_t* meta;
     const float2_t* dd;
     float* partial;       // [batch chunk][ksplit][rg*64] partial sums when K is split
-    uint32_t* counters;   // [batch chunk][rg] arrival tickets, zero between launches
+    uint32_t* counters;   // [batch chunk][rg*4] arrival tickets per row subgroup, zero between launches
     int rows, nsb, rg_count, ksplit;
     // Output epilogue of the forward kernel: RPL_STORE y = Wx;
     // RPL_ADD y += Wx (residual); RPL_SILU_MUL y = silu(aux) * Wx (SwiGLU up);
@@ -110,8 +110,8 @@ struct RplArgs {
     const float* nrm_ss;
     int nrm_n;
     double nrm_eps;
-    // With RPL_ADD: per-row-group sums of the updated y^2 ([batch][rg]), the
-    // partials the next fused RMSNorm consumes.
+    // With RPL_ADD: sums of the updated y^2 over each 16 rows
+    // ([batch][rg*4]), the partials the next fused RMSNorm consumes.
     float* ss_out;
 };
 
