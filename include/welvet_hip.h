@@ -158,7 +158,7 @@ typedef struct wv_decoder_config {
     double rope_theta, rms_eps;
 } wv_decoder_config;
 
-/* Creates a decoder: activations, f32 KV caches [max_seq][n_kv_heads*head_dim]
+/* Creates a decoder: activations, f32 KV caches (head-major [n_kv_heads][max_seq][head_dim])
  * per layer (zeroed) and its own stream on the current device. */
 int wv_decoder_create(const wv_decoder_config *cfg, uint64_t *decoder);
 

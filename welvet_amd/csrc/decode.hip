@@ -95,6 +95,9 @@ __global__ void __launch_bounds__(1024) k_rmsnorm(const float* __restrict__ x, c
     }
 }
 
+// The KV caches are head-major, [n_kv][max_seq][HD], so the K (and V) rows of
+// one chunk of one head are one contiguous kChunk*HD*4-byte run.
+//
 // Flash-decoding partials for one KV head and one chunk of kChunk positions:
 // the G = n_heads / n_kv query heads that share the KV head read its K and V
 // rows once (layers/mha/attn.go:40-118: score = q.k * scale over the causal
@@ -123,7 +126,6 @@ __global__ void __launch_bounds__(256) k_attn_part(const float* __restrict__ q, 
     const int kv_len = min(pos + 1, max_seq);
     const int p0 = c * kChunk;
     const int nvalid = min(kChunk, kv_len - p0);
-    const int kv_dim = n_kv * HD;
     const int pnew = pos % max_seq - p0;  // row of this step's k/v inside the chunk (if in [0, kChunk))
     if (nvalid <= 0) {
         for (int g = wave; g < G; g += 4) {
@@ -144,12 +146,12 @@ __global__ void __launch_bounds__(256) k_attn_part(const float* __restrict__ q, 
 #pragma unroll
     for (int r = 0; r < NL; ++r) {
         const int i = t + 256 * r, p = min(i / Q4, nvalid - 1), d4 = i % Q4;
-        kv4[r] = reinterpret_cast<const float4*>(kc + int64_t(p0 + p) * kv_dim + kvh * HD)[d4];
+        kv4[r] = reinterpret_cast<const float4*>(kc + (int64_t(kvh) * max_seq + p0 + p) * HD)[d4];
     }
 #pragma unroll
     for (int r = 0; r < NL; ++r) {
         const int i = t + 256 * r, p = min(i / Q4, nvalid - 1), d4 = i % Q4;
-        vv4[r] = reinterpret_cast<const float4*>(vc + int64_t(p0 + p) * kv_dim + kvh * HD)[d4];
+        vv4[r] = reinterpret_cast<const float4*>(vc + (int64_t(kvh) * max_seq + p0 + p) * HD)[d4];
     }
     // q heads of this KV group, rotated: one thread per pair (g, d < HD/2)
     constexpr int H2 = HD / 2;
@@ -178,7 +180,7 @@ __global__ void __launch_bounds__(256) k_attn_part(const float* __restrict__ q, 
         }
         kv4[r] = make_float4(kr[0], kr[1], kr[2], kr[3]);
         vv4[r] = reinterpret_cast<const float4*>(v_new + kvh * HD)[i % Q4];
-        const int64_t crow = int64_t(pos % max_seq) * kv_dim + kvh * HD;
+        const int64_t crow = (int64_t(kvh) * max_seq + pos % max_seq) * HD;
         reinterpret_cast<float4*>(kc + crow)[i % Q4] = kv4[r];
         reinterpret_cast<float4*>(vc + crow)[i % Q4] = vv4[r];
     }
@@ -797,10 +799,18 @@ int wv_decoder_set_kv(uint64_t dec, int32_t layer, int32_t first_pos, int32_t n_
     if (layer < 0 || layer >= c.n_layers || !k || !v) return rt_fail(WV_E_ARG, "wv_decoder_set_kv: bad layer or nil rows");
     if (first_pos < 0 || n_pos < 0 || int64_t(first_pos) + n_pos > c.max_seq)
         return rt_fail(WV_E_SHAPE, "wv_decoder_set_kv: rows %d..%d outside max_seq %d", first_pos, first_pos + n_pos, c.max_seq);
-    const size_t kv_dim = size_t(c.n_kv_heads) * c.head_dim, off = size_t(first_pos) * kv_dim, n = size_t(n_pos) * kv_dim;
+    const size_t hd = size_t(c.head_dim), kv_dim = size_t(c.n_kv_heads) * hd;
     hipSetDevice(d->device);
-    hipError_t e = hipMemcpy(d->layers[layer].kc + off, k, n * 4, hipMemcpyHostToDevice);
-    if (e == hipSuccess) e = hipMemcpy(d->layers[layer].vc + off, v, n * 4, hipMemcpyHostToDevice);
+    hipError_t e = hipSuccess;
+    // host rows [pos][kv head][hd] -> device head-major [kv head][max_seq][hd]
+    for (int kh = 0; kh < c.n_kv_heads && e == hipSuccess && n_pos > 0; ++kh) {
+        const size_t dst = (size_t(kh) * c.max_seq + size_t(first_pos)) * hd;
+        e = hipMemcpy2D(d->layers[layer].kc + dst, hd * 4, k + kh * hd, kv_dim * 4, hd * 4, size_t(n_pos),
+                        hipMemcpyHostToDevice);
+        if (e == hipSuccess)
+            e = hipMemcpy2D(d->layers[layer].vc + dst, hd * 4, v + kh * hd, kv_dim * 4, hd * 4, size_t(n_pos),
+                            hipMemcpyHostToDevice);
+    }
     if (e != hipSuccess) return rt_hip_fail(e, "wv_decoder_set_kv: copy");
     return WV_OK;
 }
