@@ -1,9 +1,9 @@
 // gemv.hip — gfx950 kernels of the Dense MatVec path.
 //
 // Three families:
-//   * k_gemv_raw / k_gemvt_raw: decode each weight from the uploaded bytes
-//     (LAYOUT_RAW). Any format, any shape, including blocks that straddle rows.
-//     Semantics follow the reference decoders element by element
+//   * k_gemv_raw16 (cols % 256 == 0) and k_gemv_raw / k_gemvt_raw (any shape,
+//     including blocks that straddle rows): the reference layout as uploaded
+//     (LAYOUT_RAW), every format; semantics follow the reference decoders
 //     (quant/*.go forEach* / unpack*), accumulating in f32.
 //   * the row-interleaved fast path for Q4_K/Q6_K/Q8_0/Q4_0 lives in
 //     gemv_rpl.hip;
@@ -22,6 +22,15 @@ namespace wv {
 namespace {
 
 constexpr int kWave = 64;
+
+// WV_RAW16=0 forces the per-weight decoder on the reference layout (for comparisons).
+bool raw16_off() {
+    static const bool off = [] {
+        const char* v = std::getenv("WV_RAW16");
+        return v && v[0] == '0';
+    }();
+    return off;
+}
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -164,6 +173,212 @@ __global__ void __launch_bounds__(256) k_gemv_raw(RawArgs a, const float* __rest
     if (lane == 0) y[int64_t(b) * a.rows + row] = acc;
 }
 
+// ---------------------------------------------------------------------------
+// Vectorized decode of the reference layout (cols % 256 == 0).
+//
+// Every format stores, per 16 consecutive weights of a row, an LSB-first run
+// of 16 codes of BITS bits (2*BITS bytes, byte aligned) sharing one affine
+// map w = alpha * f(q) + beta (f = identity, except the IQ4_NL grid and the
+// ternary {-1, 0, +1, 0} table; Q4_0 and Q8_0 become affine through q ^ bias).
+// So sum_k w_k x_k = alpha * sum_k f(q_k) x_k + beta * sum_k x_k. A lane takes
+// one such 16-weight run at a time for R = 4 rows at once, reusing its 16 x
+// values (read through L1) across the rows; the codes come in as aligned
+// dwords and are realigned with v_alignbyte and cut with bit-field extracts
+// at compile-time offsets.
+// ---------------------------------------------------------------------------
+
+struct Grp {
+    const uint8_t* codes;  // first code byte (2-byte aligned)
+    float alpha, beta;
+};
+
+template <int F>
+struct RawF;
+template <> struct RawF<FMT_Q4_0> {
+    static constexpr int BITS = 4;
+    static __device__ Grp grp(const RawArgs& a, int64_t row, int64_t f) {  // q4_0.go:93-99
+        const uint8_t* o = a.raw + (f >> 5) * 20;
+        const float s = ld_f32(o);
+        return {o + 4 + ((f >> 4) & 1) * 8, s, -8.0f * s};
+    }
+    static __device__ float fq(uint32_t q) { return float(q ^ 8u); }
+};
+template <> struct RawF<FMT_Q8_0> {
+    static constexpr int BITS = 8;
+    static __device__ Grp grp(const RawArgs& a, int64_t row, int64_t f) {  // q8_0.go:58-63
+        const uint8_t* o = a.raw + (f >> 5) * 36;
+        const float s = ld_f32(o);
+        return {o + 4 + ((f >> 4) & 1) * 16, s, -128.0f * s};
+    }
+    static __device__ float fq(uint32_t q) { return float(q ^ 0x80u); }
+};
+template <> struct RawF<FMT_Q4_1> {
+    static constexpr int BITS = 4;
+    static __device__ Grp grp(const RawArgs& a, int64_t row, int64_t f) {  // q4_1.go:63-72
+        const uint8_t* o = a.raw + (f >> 5) * 24;
+        return {o + 8 + ((f >> 4) & 1) * 8, ld_f32(o), ld_f32(o + 4)};
+    }
+    static __device__ float fq(uint32_t q) { return float(q); }
+};
+template <> struct RawF<FMT_Q5_0> {
+    static constexpr int BITS = 5;
+    static __device__ Grp grp(const RawArgs& a, int64_t row, int64_t f) {  // q5_0.go:55-63
+        const uint8_t* o = a.raw + (f >> 5) * 24;
+        const float s = ld_f32(o);
+        return {o + 4 + ((f >> 4) & 1) * 10, s, -16.0f * s};
+    }
+    static __device__ float fq(uint32_t q) { return float(q); }
+};
+template <> struct RawF<FMT_Q5_1> {
+    static constexpr int BITS = 5;
+    static __device__ Grp grp(const RawArgs& a, int64_t row, int64_t f) {  // q5_1.go:59-67
+        const uint8_t* o = a.raw + (f >> 5) * 28;
+        return {o + 8 + ((f >> 4) & 1) * 10, ld_f32(o), ld_f32(o + 4)};
+    }
+    static __device__ float fq(uint32_t q) { return float(q); }
+};
+template <int F>
+struct RawK {  // kquant.go:178-188: sc = d*u/255 (0 -> d/255), w = dmin*m/127 + q*sc, Q6_K: sc*(q - 32)
+    using S = KSpecC<F>;
+    static constexpr int BITS = S::bits;
+    static constexpr int SBB = 8 + 16 + (S::has_dmin ? 16 : 0) + 256 * S::bits / 8;
+    static constexpr int QOFF = S::has_dmin ? 40 : 24;
+    static __device__ Grp grp(const RawArgs& a, int64_t row, int64_t f) {
+        const uint8_t* o = a.raw + (f >> 8) * SBB;
+        const int g = int((f >> 4) & 15);
+        const float d = ld_f32(o);
+        float sc = d * float(o[8 + g]) / 255.0f;
+        if (sc == 0.0f) sc = d / 255.0f;
+        if constexpr (S::has_dmin) {
+            const float mn = ld_f32(o + 4) * float(int8_t(o[24 + g])) / 127.0f;
+            return {o + QOFF + g * 2 * BITS, sc, mn};
+        } else {
+            return {o + QOFF + g * 2 * BITS, sc, -float(S::mid) * sc};
+        }
+    }
+    static __device__ float fq(uint32_t q) { return float(q); }
+};
+template <> struct RawF<FMT_Q2_K> : RawK<FMT_Q2_K> {};
+template <> struct RawF<FMT_Q3_K> : RawK<FMT_Q3_K> {};
+template <> struct RawF<FMT_Q4_K> : RawK<FMT_Q4_K> {};
+template <> struct RawF<FMT_Q5_K> : RawK<FMT_Q5_K> {};
+template <> struct RawF<FMT_Q6_K> : RawK<FMT_Q6_K> {};
+template <int F, int B, int SG>
+struct RawIQ {  // iq.go:169-207, one scale per SG weights of the flat stream
+    static constexpr int BITS = B;
+    static __device__ Grp grp(const RawArgs& a, int64_t row, int64_t f) {
+        const float s = a.scales[f / SG];
+        const uint8_t* c = a.raw + (f * B) / 8;
+        if constexpr (B == 1) return {c, 2.0f * s, -s};
+        else if constexpr (F == FMT_IQ4_NL) return {c, s, 0.0f};
+        else {
+            constexpr float mid = B == 2 ? 1.5f : B == 3 ? 3.5f : 7.5f;
+            return {c, s, -mid * s};
+        }
+    }
+    static __device__ float fq(uint32_t q) {
+        if constexpr (F == FMT_IQ4_NL) return kIQ4NLGrid[q & 15];
+        else return float(q);
+    }
+};
+template <> struct RawF<FMT_IQ1_S> : RawIQ<FMT_IQ1_S, 1, 32> {};
+template <> struct RawF<FMT_IQ2_XXS> : RawIQ<FMT_IQ2_XXS, 2, 32> {};
+template <> struct RawF<FMT_IQ2_XS> : RawIQ<FMT_IQ2_XS, 2, 16> {};
+template <> struct RawF<FMT_IQ3_XXS> : RawIQ<FMT_IQ3_XXS, 3, 32> {};
+template <> struct RawF<FMT_IQ3_S> : RawIQ<FMT_IQ3_S, 3, 16> {};
+template <> struct RawF<FMT_IQ4_NL> : RawIQ<FMT_IQ4_NL, 4, 32> {};
+template <> struct RawF<FMT_IQ4_XS> : RawIQ<FMT_IQ4_XS, 4, 16> {};
+template <> struct RawF<FMT_TERNARY> {
+    static constexpr int BITS = 2;
+    static __device__ Grp grp(const RawArgs& a, int64_t row, int64_t f) {  // ternary.go:53-82
+        const int64_t g = f >> 4;
+        return {a.raw + g * 4, g < a.n_scales ? a.scales[g] : 1.0f, 0.0f};
+    }
+    static __device__ float fq(uint32_t q) { return q == 0 ? -1.0f : (q == 2 ? 1.0f : 0.0f); }
+};
+template <> struct RawF<FMT_BINARY> {
+    static constexpr int BITS = 1;
+    static __device__ Grp grp(const RawArgs& a, int64_t row, int64_t f) {
+        if (a.g128) {  // binary_g128.go:107-139, row-aligned words and groups
+            const int64_t col = f - row * a.cols;
+            const int64_t si = row * (a.cols >> 7) + (col >> 7);
+            const float s = si < a.n_scales ? a.scales[si] : 1.0f;
+            return {a.raw + (row * (a.cols >> 5) + (col >> 5)) * 4 + ((col >> 4) & 1) * 2, 2.0f * s, -s};
+        }
+        const int64_t g = f >> 5;  // binary.go:49-75
+        const float s = g < a.n_scales ? a.scales[g] : 1.0f;
+        return {a.raw + g * 4 + ((f >> 4) & 1) * 2, 2.0f * s, -s};
+    }
+    static __device__ float fq(uint32_t q) { return float(q); }
+};
+
+// The 16 codes of a run: 2*BITS bytes at p (2-byte aligned), read as aligned
+// dwords and realigned.
+template <int BITS>
+__device__ __forceinline__ void load_run(const uint8_t* p, uint32_t* w) {
+    constexpr int NB = 2 * BITS;           // bytes of the run
+    constexpr int NW = (NB + 2 + 3) / 4;   // dwords that cover it from the aligned base
+    const uintptr_t ad = reinterpret_cast<uintptr_t>(p);
+    const uint32_t* base = reinterpret_cast<const uint32_t*>(ad & ~uintptr_t(3));
+    const uint32_t m = uint32_t(ad & 3);
+    uint32_t d[NW];
+#pragma unroll
+    for (int i = 0; i < NW; ++i) d[i] = base[i];
+#pragma unroll
+    for (int i = 0; i < (NB + 3) / 4; ++i) w[i] = __builtin_amdgcn_alignbyte(i + 1 < NW ? d[i + 1] : 0u, d[i], m);
+}
+template <int BITS>
+__device__ __forceinline__ uint32_t code_at(const uint32_t* w, int k) {
+    const int bit = k * BITS, wi = bit >> 5, off = bit & 31;
+    if (off + BITS <= 32) return (w[wi] >> off) & ((1u << BITS) - 1u);
+    return __builtin_amdgcn_alignbit(w[wi + 1], w[wi], off) & ((1u << BITS) - 1u);
+}
+
+template <int F>
+__global__ void __launch_bounds__(256) k_gemv_raw16(RawArgs a, const float* __restrict__ x, float* __restrict__ y) {
+    using P = RawF<F>;
+    constexpr int R = 4;  // rows per wave
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int64_t row0 = (int64_t(blockIdx.x) * 4 + wave) * R;
+    if (row0 >= a.rows) return;
+    const int b = blockIdx.y;
+    const float* xb = x + int64_t(b) * a.cols;
+    const int64_t nsg = a.cols >> 4;
+    int64_t rowc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) rowc[r] = min<int64_t>(row0 + r, a.rows - 1);
+    float acc[R] = {};
+    for (int64_t s = lane; s < nsg; s += 64) {
+        const int64_t c0 = s << 4;
+        const float4* xp = reinterpret_cast<const float4*>(xb + c0);
+        const float4 x0 = xp[0], x1 = xp[1], x2 = xp[2], x3 = xp[3];
+        const float xv[16] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w,
+                              x2.x, x2.y, x2.z, x2.w, x3.x, x3.y, x3.z, x3.w};
+        Grp g[R];
+        uint32_t w[R][(2 * P::BITS + 3) / 4];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            g[r] = P::grp(a, rowc[r], rowc[r] * a.cols + c0);
+            load_run<P::BITS>(g[r].codes, w[r]);
+        }
+        float xs = 0.f;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) xs += xv[k];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            float d = 0.f;
+#pragma unroll
+            for (int k = 0; k < 16; ++k) d = fmaf(P::fq(code_at<P::BITS>(w[r], k)), xv[k], d);
+            acc[r] = fmaf(g[r].alpha, d, fmaf(g[r].beta, xs, acc[r]));
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const float v = wave_sum(acc[r]);
+        if (lane == 0 && row0 + r < a.rows) y[int64_t(b) * a.rows + row0 + r] = v;
+    }
+}
+
 // Partial gx over a row slice: part[(b*nsplit + split)*cols + c] = sum_{r in slice} w(r,c) gy[b][r].
 template <int F>
 __global__ void __launch_bounds__(256) k_gemvt_raw(RawArgs a, const float* __restrict__ gy, float* __restrict__ part,
@@ -282,8 +497,27 @@ RawArgs raw_args(const DevBlob& b) {
     return a;
 }
 
+// The run-vectorized kernel needs whole runs of 16 weights per row and the
+// format's standard IQ bit width and scale group (Meta may override them).
+template <int F>
+bool raw16_ok(const DevBlob& b) {
+    if (b.cols % 256 != 0 || raw16_off()) return false;
+    if constexpr (F >= FMT_IQ1_S && F <= FMT_IQ4_XS) {
+        IQSpec sp;
+        iq_spec(F, sp);
+        return b.iq_bits == sp.bits && b.iq_sg == sp.sg;
+    }
+    if constexpr (F == FMT_BINARY) return b.block_weights != 128 || b.cols % 128 == 0;
+    return true;
+}
+
 template <int F>
 int launch_raw(const DevBlob& b, const float* x, float* y, int batch, hipStream_t s) {
+    if (raw16_ok<F>(b)) {
+        dim3 grid(unsigned((b.rows + 15) / 16), unsigned(batch));
+        hipLaunchKernelGGL(k_gemv_raw16<F>, grid, dim3(256), 0, s, raw_args(b), x, y);
+        return int(hipGetLastError());
+    }
     dim3 grid(unsigned((b.rows + 3) / 4), unsigned(batch));
     hipLaunchKernelGGL(k_gemv_raw<F>, grid, dim3(256), 0, s, raw_args(b), x, y);
     return int(hipGetLastError());

@@ -366,7 +366,9 @@ int wv_blob_upload(int format, int64_t rows, int64_t cols, int32_t block_weights
         build_rpl(format, raw, rows, cols, img, ro);
     } else {
         b.layout = LAYOUT_RAW;
-        o_raw = img.add(size_t(need));
+        // 16 bytes of padding: the vectorized decoder reads whole aligned
+        // dwords around each run of codes, up to 4 bytes past the last one.
+        o_raw = img.add(size_t(need) + 16);
         std::memcpy(img.bytes.data() + o_raw, raw, size_t(need));
         b.raw_len = need;
         IQSpec is;
