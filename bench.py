@@ -134,6 +134,9 @@ def main():
     ap.add_argument("--traffic-kib", type=float, nargs=2, metavar=("FETCH_KIB", "WRITE_KIB"),
                     help="override the per-dispatch FETCH_SIZE and WRITE_SIZE (KiB) of the GEMV kernel "
                          "(rocprofv3 --pmc of this command) used for roofline.traffic")
+    ap.add_argument("--graph", action="store_true",
+                    help="replay the timed launches from a captured HIP graph (for kernels shorter than the "
+                         "host's per-launch cost, where stream launches would time the host)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="also run plain device-to-device copies of MIB MiB (torch copy_) for counter calibration")
     args = ap.parse_args()
@@ -192,12 +195,29 @@ def main():
         run(args.warmup)
     stream.synchronize()
 
+    graph = None
+    if args.graph:
+        # one graph of `copies` launches (one per weight copy), replayed
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            run(copies)
+        stream.synchronize()
+        for _ in range(2):
+            graph.replay()
+        stream.synchronize()
+        reps = max(1, args.steps // copies)
+        args.steps = reps * copies
+
     # timed region: K back-to-back launches, events on the kernels' stream
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     e0.record(stream)
     with torch.cuda.stream(stream):
-        run(args.steps)
+        if graph is not None:
+            for _ in range(args.steps // copies):
+                graph.replay()
+        else:
+            run(args.steps)
     e1.record(stream)
     e1.synchronize()
     torch.cuda.synchronize()
@@ -233,6 +253,7 @@ def main():
         "config": {
             "workload": desc, "format": fmt, "in": cols, "out": rows, "batch": 1,
             "weight_copies_rotated": copies, "packed_bytes": int(packed.nbytes),
+            "launch": "HIP graph replay" if args.graph else "stream launches",
             "device_bytes": int(dev_bytes), "algorithmic_bytes_per_step": int(nbytes),
         },
         "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),

@@ -201,7 +201,7 @@ template <> struct RawF<FMT_Q4_0> {
         const float s = ld_f32(o);
         return {o + 4 + ((f >> 4) & 1) * 8, s, -8.0f * s};
     }
-    static __device__ float fq(uint32_t q) { return float(q ^ 8u); }
+    static __device__ float fq(uint32_t q, const float* tab) { return float(q ^ 8u); }
 };
 template <> struct RawF<FMT_Q8_0> {
     static constexpr int BITS = 8;
@@ -210,7 +210,7 @@ template <> struct RawF<FMT_Q8_0> {
         const float s = ld_f32(o);
         return {o + 4 + ((f >> 4) & 1) * 16, s, -128.0f * s};
     }
-    static __device__ float fq(uint32_t q) { return float(q ^ 0x80u); }
+    static __device__ float fq(uint32_t q, const float* tab) { return float(q ^ 0x80u); }
 };
 template <> struct RawF<FMT_Q4_1> {
     static constexpr int BITS = 4;
@@ -218,7 +218,7 @@ template <> struct RawF<FMT_Q4_1> {
         const uint8_t* o = a.raw + (f >> 5) * 24;
         return {o + 8 + ((f >> 4) & 1) * 8, ld_f32(o), ld_f32(o + 4)};
     }
-    static __device__ float fq(uint32_t q) { return float(q); }
+    static __device__ float fq(uint32_t q, const float* tab) { return float(q); }
 };
 template <> struct RawF<FMT_Q5_0> {
     static constexpr int BITS = 5;
@@ -227,7 +227,7 @@ template <> struct RawF<FMT_Q5_0> {
         const float s = ld_f32(o);
         return {o + 4 + ((f >> 4) & 1) * 10, s, -16.0f * s};
     }
-    static __device__ float fq(uint32_t q) { return float(q); }
+    static __device__ float fq(uint32_t q, const float* tab) { return float(q); }
 };
 template <> struct RawF<FMT_Q5_1> {
     static constexpr int BITS = 5;
@@ -235,7 +235,7 @@ template <> struct RawF<FMT_Q5_1> {
         const uint8_t* o = a.raw + (f >> 5) * 28;
         return {o + 8 + ((f >> 4) & 1) * 10, ld_f32(o), ld_f32(o + 4)};
     }
-    static __device__ float fq(uint32_t q) { return float(q); }
+    static __device__ float fq(uint32_t q, const float* tab) { return float(q); }
 };
 template <int F>
 struct RawK {  // kquant.go:178-188: sc = d*u/255 (0 -> d/255), w = dmin*m/127 + q*sc, Q6_K: sc*(q - 32)
@@ -256,7 +256,7 @@ struct RawK {  // kquant.go:178-188: sc = d*u/255 (0 -> d/255), w = dmin*m/127 +
             return {o + QOFF + g * 2 * BITS, sc, -float(S::mid) * sc};
         }
     }
-    static __device__ float fq(uint32_t q) { return float(q); }
+    static __device__ float fq(uint32_t q, const float* tab) { return float(q); }
 };
 template <> struct RawF<FMT_Q2_K> : RawK<FMT_Q2_K> {};
 template <> struct RawF<FMT_Q3_K> : RawK<FMT_Q3_K> {};
@@ -276,8 +276,8 @@ struct RawIQ {  // iq.go:169-207, one scale per SG weights of the flat stream
             return {c, s, -mid * s};
         }
     }
-    static __device__ float fq(uint32_t q) {
-        if constexpr (F == FMT_IQ4_NL) return kIQ4NLGrid[q & 15];
+    static __device__ float fq(uint32_t q, const float* tab) {
+        if constexpr (F == FMT_IQ4_NL) return tab[q & 15];  // the grid staged in LDS
         else return float(q);
     }
 };
@@ -294,7 +294,7 @@ template <> struct RawF<FMT_TERNARY> {
         const int64_t g = f >> 4;
         return {a.raw + g * 4, g < a.n_scales ? a.scales[g] : 1.0f, 0.0f};
     }
-    static __device__ float fq(uint32_t q) { return q == 0 ? -1.0f : (q == 2 ? 1.0f : 0.0f); }
+    static __device__ float fq(uint32_t q, const float* tab) { return q == 0 ? -1.0f : (q == 2 ? 1.0f : 0.0f); }
 };
 template <> struct RawF<FMT_BINARY> {
     static constexpr int BITS = 1;
@@ -309,7 +309,7 @@ template <> struct RawF<FMT_BINARY> {
         const float s = g < a.n_scales ? a.scales[g] : 1.0f;
         return {a.raw + g * 4 + ((f >> 4) & 1) * 2, 2.0f * s, -s};
     }
-    static __device__ float fq(uint32_t q) { return float(q); }
+    static __device__ float fq(uint32_t q, const float* tab) { return float(q); }
 };
 
 // The 16 codes of a run: 2*BITS bytes at p (2-byte aligned), read as aligned
@@ -338,6 +338,11 @@ template <int F>
 __global__ void __launch_bounds__(256) k_gemv_raw16(RawArgs a, const float* __restrict__ x, float* __restrict__ y) {
     using P = RawF<F>;
     constexpr int R = 4;  // rows per wave
+    __shared__ float tab[16];  // IQ4_NL grid: a per-lane index into a register table would go through scratch
+    if constexpr (F == FMT_IQ4_NL) {
+        if (threadIdx.x < 16) tab[threadIdx.x] = kIQ4NLGrid[threadIdx.x];
+        __syncthreads();
+    }
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int64_t row0 = (int64_t(blockIdx.x) * 4 + wave) * R;
     if (row0 >= a.rows) return;
@@ -368,7 +373,7 @@ __global__ void __launch_bounds__(256) k_gemv_raw16(RawArgs a, const float* __re
         for (int r = 0; r < R; ++r) {
             float d = 0.f;
 #pragma unroll
-            for (int k = 0; k < 16; ++k) d = fmaf(P::fq(code_at<P::BITS>(w[r], k)), xv[k], d);
+            for (int k = 0; k < 16; ++k) d = fmaf(P::fq(code_at<P::BITS>(w[r], k), tab), xv[k], d);
             acc[r] = fmaf(g[r].alpha, d, fmaf(g[r].beta, xs, acc[r]));
         }
     }
@@ -483,6 +488,98 @@ __global__ void __launch_bounds__(256) k_ternary_i8(const uint8_t* __restrict__ 
     }
 }
 
+// DTypeTernary int8 GEMV for K % 64 == 0 and K <= 8192: the block's 16 rows
+// of codes (NC uint4 per lane per row) are requested first, since they do not
+// depend on x; x is then quantized from float4 registers (NX per thread) while
+// they arrive, exactly as quantizeActsI8 (layers/dense/simd.go:526-549):
+// absmax, act = max/127 (1 if 0), q = round-half-away(f32(x / act)) clamped.
+// The permuted LDS layout puts byte b of word 4*(4c+d)+k at xq[64c + 16d +
+// 4b + k], matching the byte spread (code word d of uint4 c >> 2k) & 0x03030303.
+template <int NC, int NX>
+__global__ void __launch_bounds__(256) k_ternary_i8v(const uint8_t* __restrict__ codes, float scale, int rows, int K,
+                                                    const float* __restrict__ x, float* __restrict__ y,
+                                                    int32_t* __restrict__ acc_out, float* __restrict__ act_out) {
+    constexpr int RW = 4;  // rows per wave
+    extern __shared__ uint32_t lds[];  // K/4 words of permuted xq
+    __shared__ float red_f[4];
+    __shared__ int red_i[4];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int b = blockIdx.y;
+    const int r0 = blockIdx.x * 16 + wave * RW;
+    const int c64 = K / 64;  // uint4 per row
+    uint4 cv[RW][NC];
+#pragma unroll
+    for (int rw = 0; rw < RW; ++rw) {
+        const uint4* rowp = reinterpret_cast<const uint4*>(codes + int64_t(min(r0 + rw, rows - 1)) * (K / 4));
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            const int i = lane + 64 * c;
+            cv[rw][c] = i < c64 ? rowp[i] : make_uint4(0u, 0u, 0u, 0u);
+        }
+    }
+    const float4* xb = reinterpret_cast<const float4*>(x + int64_t(b) * K);
+    float4 xv[NX];
+    float m = 0.f;
+#pragma unroll
+    for (int n = 0; n < NX; ++n) {
+        const int i = tid + 256 * n;
+        xv[n] = i < K / 4 ? xb[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+        m = fmaxf(m, fmaxf(fmaxf(fabsf(xv[n].x), fabsf(xv[n].y)), fmaxf(fabsf(xv[n].z), fabsf(xv[n].w))));
+    }
+    m = wave_max(m);
+    if (lane == 0) red_f[wave] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red_f[0], red_f[1]), fmaxf(red_f[2], red_f[3]));
+    float act = m / 127.0f;
+    if (act == 0.0f) act = 1.0f;
+    uint8_t* l8 = reinterpret_cast<uint8_t*>(lds);
+    int sq = 0;
+#pragma unroll
+    for (int n = 0; n < NX; ++n) {
+        const int i = tid + 256 * n;  // float4 index: x[4i .. 4i+3]
+        if (i < K / 4) {
+            const float e4[4] = {xv[n].x, xv[n].y, xv[n].z, xv[n].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                int q = int(roundf(e4[e] / act));
+                q = q > 127 ? 127 : (q < -128 ? -128 : q);
+                sq += q;
+                l8[(i >> 2) * 16 + e * 4 + (i & 3)] = uint8_t(int8_t(q));  // j = 4i + e
+            }
+        }
+    }
+    sq = wave_sum_i(sq);
+    if (lane == 0) red_i[wave] = sq;
+    __syncthreads();
+    sq = red_i[0] + red_i[1] + red_i[2] + red_i[3];
+    if (act_out && blockIdx.x == 0 && tid == 0) act_out[b] = act;
+#pragma unroll
+    for (int rw = 0; rw < RW; ++rw) {
+        int acc = 0;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            const int i = lane + 64 * c;
+            if (i < c64) {
+                const uint32_t wd[4] = {cv[rw][c].x, cv[rw][c].y, cv[rw][c].z, cv[rw][c].w};
+#pragma unroll
+                for (int d = 0; d < 4; ++d) {
+                    const uint4 xw = reinterpret_cast<const uint4*>(lds)[i * 4 + d];
+                    const uint32_t xk[4] = {xw.x, xw.y, xw.z, xw.w};
+#pragma unroll
+                    for (int k = 0; k < 4; ++k)
+                        acc = __builtin_amdgcn_sdot4(int((wd[d] >> (2 * k)) & 0x03030303u), int(xk[k]), acc, false);
+                }
+            }
+        }
+        acc = wave_sum_i(acc) - sq;  // codes are t+1: sum (t+1)*xq - sum xq
+        const int r = r0 + rw;
+        if (lane == 0 && r < rows) {
+            if (acc_out) acc_out[int64_t(b) * rows + r] = acc;
+            if (y) y[int64_t(b) * rows + r] = float(acc) * act * scale;  // simd.go:142
+        }
+    }
+}
+
 RawArgs raw_args(const DevBlob& b) {
     RawArgs a;
     a.raw = b.raw;
@@ -585,8 +682,35 @@ RawTFn pick_raw_t(int fmt) {
     }
 }
 
+template <int NC, int NX>
+void launch_ternary_v(const DevBlob& b, const float* x, float* y, int32_t* acc, float* act, int batch, hipStream_t s) {
+    const int rows = int(b.rows), K = int(b.cols);
+    dim3 grid(unsigned((rows + 15) / 16), unsigned(batch));
+    hipLaunchKernelGGL((k_ternary_i8v<NC, NX>), grid, dim3(256), size_t(K), s, b.codes, b.tensor_scale, rows, K, x, y,
+                       acc, act);
+}
+
 int launch_ternary(const DevBlob& b, const float* x, float* y, int32_t* acc, float* act, int batch, hipStream_t s) {
     const int rows = int(b.rows), K = int(b.cols);
+    if (K % 64 == 0 && K <= 8192) {  // NC = ceil(K/4096) uint4 per lane per row, NX = ceil(K/1024) float4 of x
+        const int nc = (K + 4095) / 4096, nx = (K + 1023) / 1024;
+        if (nc == 1) {
+            switch (nx) {
+            case 1: launch_ternary_v<1, 1>(b, x, y, acc, act, batch, s); break;
+            case 2: launch_ternary_v<1, 2>(b, x, y, acc, act, batch, s); break;
+            case 3: launch_ternary_v<1, 3>(b, x, y, acc, act, batch, s); break;
+            default: launch_ternary_v<1, 4>(b, x, y, acc, act, batch, s); break;
+            }
+        } else {
+            switch (nx) {
+            case 5: launch_ternary_v<2, 5>(b, x, y, acc, act, batch, s); break;
+            case 6: launch_ternary_v<2, 6>(b, x, y, acc, act, batch, s); break;
+            case 7: launch_ternary_v<2, 7>(b, x, y, acc, act, batch, s); break;
+            default: launch_ternary_v<2, 8>(b, x, y, acc, act, batch, s); break;
+            }
+        }
+        return int(hipGetLastError());
+    }
     const int rpb = 16;
     dim3 grid(unsigned((rows + rpb - 1) / rpb), unsigned(batch));
     const size_t lds = size_t((K + 3) / 4) * 4;
