@@ -16,6 +16,7 @@
 #include <cstdint>
 #include <cstdlib>
 
+#include "wave_ops.h"
 #include "wv_internal.h"
 
 namespace wv {
@@ -32,21 +33,9 @@ bool raw16_off() {
     return off;
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
-    return v;
-}
-__device__ __forceinline__ int wave_sum_i(int v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
-    return v;
-}
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, kWave));
-    return v;
-}
+__device__ __forceinline__ float wave_sum(float v) { return wave_total(v); }
+__device__ __forceinline__ int wave_sum_i(int v) { return wave_total_i(v); }
+__device__ __forceinline__ float wave_max(float v) { return wave_maximum(v); }
 
 __device__ __forceinline__ float ld_f32(const uint8_t* p) {
     // 4-byte aligned in every layout that reaches here (block sizes are multiples of 4).
@@ -488,42 +477,50 @@ __global__ void __launch_bounds__(256) k_ternary_i8(const uint8_t* __restrict__ 
     }
 }
 
-// DTypeTernary int8 GEMV for K % 64 == 0 and K <= 8192: the block's 16 rows
-// of codes (NC uint4 per lane per row) are requested first, since they do not
-// depend on x; x is then quantized from float4 registers (NX per thread) while
-// they arrive, exactly as quantizeActsI8 (layers/dense/simd.go:526-549):
-// absmax, act = max/127 (1 if 0), q = round-half-away(f32(x / act)) clamped.
-// The permuted LDS layout puts byte b of word 4*(4c+d)+k at xq[64c + 16d +
-// 4b + k], matching the byte spread (code word d of uint4 c >> 2k) & 0x03030303.
-template <int NC, int NX>
+// DTypeTernary int8 GEMV for K % 64 == 0 and K <= 8192 (layers/dense/
+// simd.go:130-147 with quantizeActsI8, simd.go:526-549). A block of four
+// waves covers 4*RW rows of one batch row:
+//  * x is requested first (NX float4 per thread), then the block's codes (NC
+//    uint4 per lane per row), so the activation quantization overlaps the
+//    codes' arrival;
+//  * absmax over x, act = max/127 (1 if 0), q = round-half-away(f32(x / act))
+//    clamped to [-128, 127], with the exact f32 division of the reference;
+//  * xq is stored in LDS laid out for the dot: dword (d*C + c)*4 + k, C = K/64,
+//    holds in byte b the value xq[64c + 16d + 4b + k], which is what byte b of
+//    code word d of uint4 c meets after >> 2k & 0x03030303. Lane c reads its
+//    four uint4 (d = 0..3) once for all its rows, and consecutive lanes read
+//    consecutive uint4 (no bank conflicts). A thread quantizes four
+//    consecutive x (byte b of four dwords k); a DPP quad transpose gives each
+//    lane of the quad one whole dword to store;
+//  * codes are t+1 in {0,1,2}: sum (t+1)*xq - sum xq on v_dot4_i32_i8, exact.
+template <int NC, int NX, int RW>
 __global__ void __launch_bounds__(256) k_ternary_i8v(const uint8_t* __restrict__ codes, float scale, int rows, int K,
                                                     const float* __restrict__ x, float* __restrict__ y,
                                                     int32_t* __restrict__ acc_out, float* __restrict__ act_out) {
-    constexpr int RW = 4;  // rows per wave
-    extern __shared__ uint32_t lds[];  // K/4 words of permuted xq
+    extern __shared__ uint32_t lds[];  // K/4 dwords of xq in the dot layout
     __shared__ float red_f[4];
     __shared__ int red_i[4];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int b = blockIdx.y;
-    const int r0 = blockIdx.x * 16 + wave * RW;
-    const int c64 = K / 64;  // uint4 per row
+    const int r0 = blockIdx.x * (4 * RW) + wave * RW;
+    const int c64 = K / 64, k4 = K / 4;
+    const float4* xb = reinterpret_cast<const float4*>(x + int64_t(b) * K);
+    float4 xv[NX];
+#pragma unroll
+    for (int n = 0; n < NX; ++n) xv[n] = xb[min(tid + 256 * n, k4 - 1)];
+    __builtin_amdgcn_sched_barrier(0);  // keep the x requests ahead of the codes
     uint4 cv[RW][NC];
 #pragma unroll
     for (int rw = 0; rw < RW; ++rw) {
-        const uint4* rowp = reinterpret_cast<const uint4*>(codes + int64_t(min(r0 + rw, rows - 1)) * (K / 4));
+        const uint4* rowp = reinterpret_cast<const uint4*>(codes + int64_t(min(r0 + rw, rows - 1)) * k4);
 #pragma unroll
-        for (int c = 0; c < NC; ++c) {
-            const int i = lane + 64 * c;
-            cv[rw][c] = i < c64 ? rowp[i] : make_uint4(0u, 0u, 0u, 0u);
-        }
+        for (int c = 0; c < NC; ++c) cv[rw][c] = rowp[min(lane + 64 * c, c64 - 1)];
     }
-    const float4* xb = reinterpret_cast<const float4*>(x + int64_t(b) * K);
-    float4 xv[NX];
+    __builtin_amdgcn_sched_barrier(0);
     float m = 0.f;
 #pragma unroll
     for (int n = 0; n < NX; ++n) {
-        const int i = tid + 256 * n;
-        xv[n] = i < K / 4 ? xb[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+        if (tid + 256 * n >= k4) xv[n] = make_float4(0.f, 0.f, 0.f, 0.f);
         m = fmaxf(m, fmaxf(fmaxf(fabsf(xv[n].x), fabsf(xv[n].y)), fmaxf(fabsf(xv[n].z), fabsf(xv[n].w))));
     }
     m = wave_max(m);
@@ -532,39 +529,43 @@ __global__ void __launch_bounds__(256) k_ternary_i8v(const uint8_t* __restrict__
     m = fmaxf(fmaxf(red_f[0], red_f[1]), fmaxf(red_f[2], red_f[3]));
     float act = m / 127.0f;
     if (act == 0.0f) act = 1.0f;
-    uint8_t* l8 = reinterpret_cast<uint8_t*>(lds);
     int sq = 0;
+    const int qd = lane & 3;
 #pragma unroll
     for (int n = 0; n < NX; ++n) {
-        const int i = tid + 256 * n;  // float4 index: x[4i .. 4i+3]
-        if (i < K / 4) {
-            const float e4[4] = {xv[n].x, xv[n].y, xv[n].z, xv[n].w};
+        const int i = tid + 256 * n;  // float4 index: x[4i + e] = xq[64c + 16d + 4b + k], c = i>>4, d = (i>>2)&3, b = i&3, k = e
+        const float e4[4] = {xv[n].x, xv[n].y, xv[n].z, xv[n].w};
+        uint32_t pk = 0;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                int q = int(roundf(e4[e] / act));
-                q = q > 127 ? 127 : (q < -128 ? -128 : q);
-                sq += q;
-                l8[(i >> 2) * 16 + e * 4 + (i & 3)] = uint8_t(int8_t(q));  // j = 4i + e
-            }
+        for (int e = 0; e < 4; ++e) {
+            int q = int(roundf(e4[e] / act));
+            q = q > 127 ? 127 : (q < -128 ? -128 : q);
+            sq += q;
+            pk |= (uint32_t(q) & 0xffu) << (8 * e);
         }
+        const uint32_t dw = quad_byte_transpose(pk, qd);  // bytes b = 0..3 of dword k = qd
+        if (i < k4) lds[(((i >> 2) & 3) * c64 + (i >> 4)) * 4 + qd] = dw;
     }
     sq = wave_sum_i(sq);
     if (lane == 0) red_i[wave] = sq;
     __syncthreads();
     sq = red_i[0] + red_i[1] + red_i[2] + red_i[3];
     if (act_out && blockIdx.x == 0 && tid == 0) act_out[b] = act;
+    uint4 xw[NC][4];
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int d = 0; d < 4; ++d) xw[c][d] = reinterpret_cast<const uint4*>(lds)[d * c64 + min(lane + 64 * c, c64 - 1)];
 #pragma unroll
     for (int rw = 0; rw < RW; ++rw) {
         int acc = 0;
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
-            const int i = lane + 64 * c;
-            if (i < c64) {
+            if (lane + 64 * c < c64) {
                 const uint32_t wd[4] = {cv[rw][c].x, cv[rw][c].y, cv[rw][c].z, cv[rw][c].w};
 #pragma unroll
                 for (int d = 0; d < 4; ++d) {
-                    const uint4 xw = reinterpret_cast<const uint4*>(lds)[i * 4 + d];
-                    const uint32_t xk[4] = {xw.x, xw.y, xw.z, xw.w};
+                    const uint32_t xk[4] = {xw[c][d].x, xw[c][d].y, xw[c][d].z, xw[c][d].w};
 #pragma unroll
                     for (int k = 0; k < 4; ++k)
                         acc = __builtin_amdgcn_sdot4(int((wd[d] >> (2 * k)) & 0x03030303u), int(xk[k]), acc, false);
@@ -685,9 +686,16 @@ RawTFn pick_raw_t(int fmt) {
 template <int NC, int NX>
 void launch_ternary_v(const DevBlob& b, const float* x, float* y, int32_t* acc, float* act, int batch, hipStream_t s) {
     const int rows = int(b.rows), K = int(b.cols);
-    dim3 grid(unsigned((rows + 15) / 16), unsigned(batch));
-    hipLaunchKernelGGL((k_ternary_i8v<NC, NX>), grid, dim3(256), size_t(K), s, b.codes, b.tensor_scale, rows, K, x, y,
-                       acc, act);
+    // 8 rows per wave while that still leaves ~200 blocks (measured on 2560/4096/6912 shapes)
+    if constexpr (NC == 1) {
+        if ((rows + 31) / 32 >= 192) {
+            hipLaunchKernelGGL((k_ternary_i8v<NC, NX, 8>), dim3(unsigned((rows + 31) / 32), unsigned(batch)), dim3(256),
+                               size_t(K), s, b.codes, b.tensor_scale, rows, K, x, y, acc, act);
+            return;
+        }
+    }
+    hipLaunchKernelGGL((k_ternary_i8v<NC, NX, 4>), dim3(unsigned((rows + 15) / 16), unsigned(batch)), dim3(256), size_t(K),
+                       s, b.codes, b.tensor_scale, rows, K, x, y, acc, act);
 }
 
 int launch_ternary(const DevBlob& b, const float* x, float* y, int32_t* acc, float* act, int batch, hipStream_t s) {
