@@ -81,7 +81,7 @@ def check_against_oracle(dec, ref, token, pos, steps):
 
 @pytest.mark.parametrize("fmt", ["Q4_K", "Q5_K", "Q8_0"])
 def test_decode_small_hd64(fmt):
-    """2 layers, GQA 4/2, head_dim 64; KV crosses a 64-position chunk boundary."""
+    """2 layers, GQA 4/2, head_dim 64; the steps cross a 32-position chunk boundary (positions 62-65)."""
     print(f"[gpu] decode small hd64 {fmt}", flush=True)
     cfg = Config(n_layers=2, hidden=256, n_heads=4, n_kv_heads=2, head_dim=64, ffn=512, vocab=300, max_seq=96)
     dec, ref, keep = build(cfg, fmt, 7, kv_fill=62)
@@ -103,6 +103,16 @@ def test_decode_hd128_gqa4():
     cfg = Config(n_layers=2, hidden=512, n_heads=4, n_kv_heads=1, head_dim=128, ffn=768, vocab=500, max_seq=200)
     dec, ref, keep = build(cfg, "Q4_K", 9, kv_fill=150)
     check_against_oracle(dec, ref, token=3, pos=150, steps=3)
+    dec.free()
+
+
+@pytest.mark.parametrize("max_seq,kv_fill,hd", [(3000, 2900, 128), (6000, 5600, 64)])
+def test_decode_long_cache(max_seq, kv_fill, hd):
+    """Caches of 94 and 188 chunks of 32 positions: the combine variants past one wave of chunks."""
+    print(f"[gpu] decode long cache max_seq {max_seq} hd {hd}", flush=True)
+    cfg = Config(n_layers=1, hidden=256, n_heads=4, n_kv_heads=2, head_dim=hd, ffn=512, vocab=300, max_seq=max_seq)
+    dec, ref, keep = build(cfg, "Q4_K", 31, kv_fill=kv_fill)
+    check_against_oracle(dec, ref, token=9, pos=kv_fill, steps=2)
     dec.free()
 
 

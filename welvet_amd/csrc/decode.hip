@@ -23,11 +23,12 @@
 
 #include "../../include/welvet_hip.h"
 #include "rt_internal.h"
+#include "wave_ops.h"
 
 namespace wv {
 namespace {
 
-constexpr int kChunk = 64;  // KV positions per attention block
+constexpr int kChunk = 32;  // KV positions per attention block
 
 // h = table[token] (embedding lookup, clamped token id). Block 0 also builds
 // this step's RoPE table: angle_d = pos / theta^(2d/hd) with theta^(2d/hd)
@@ -109,66 +110,89 @@ __global__ void __launch_bounds__(1024) k_rmsnorm(const float* __restrict__ x, c
 // chunk holds position pos rotates the new k row of its KV head, uses it and
 // the new v row in place of the cache's row pos, and writes both to the cache
 // (layers/mha/cpu.go:178-193, rope.go:6-21).
+//
+// Every block computes only after its own data arrives, so the step costs
+// about the last block's arrival plus one block's compute: q and the cos/sin
+// pairs are requested first, then K, then V, so the q rotation, the K tile
+// and the scores proceed while V is still in flight.
 template <int HD>
 __global__ void __launch_bounds__(256) k_attn_part(const float* __restrict__ q, float* __restrict__ kc,
                                                    float* __restrict__ vc, const int32_t* __restrict__ d_pos,
                                                    float* __restrict__ part, int n_heads, int n_kv, int max_seq,
                                                    int n_chunks, float scale, const float* __restrict__ k_new,
                                                    const float* __restrict__ v_new, const double2* __restrict__ cs) {
-    constexpr int LD = HD + 1;
-    __shared__ float tile[kChunk * LD];
-    __shared__ __attribute__((aligned(16))) float es[8][kChunk];
+    constexpr int C = kChunk, LD = HD + 1, Q4 = HD / 4, H2 = HD / 2;
+    constexpr int NL = C * Q4 / 256;         // float4 of K (and of V) per thread
+    constexpr int LPP = 64 / C, DW = HD / LPP;  // lanes per position in the score pass, dims per lane
+    constexpr int QP = (8 * H2 + 255) / 256;    // q rotation pairs per thread (up to 8 heads per KV head)
+    static_assert(NL >= 1 && LPP >= 1 && LPP <= 4, "chunk shape");
+    __shared__ float ktile[C * LD];
+    __shared__ __attribute__((aligned(16))) float vtile[C * HD];
+    __shared__ __attribute__((aligned(16))) float es[8][C];
     extern __shared__ float qs[];  // [G][HD]
     const int kvh = blockIdx.x, c = blockIdx.y;
     const int G = n_heads / n_kv;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int pos = *d_pos;
     const int kv_len = min(pos + 1, max_seq);
-    const int p0 = c * kChunk;
-    const int nvalid = min(kChunk, kv_len - p0);
-    const int pnew = pos % max_seq - p0;  // row of this step's k/v inside the chunk (if in [0, kChunk))
-    if (nvalid <= 0) {
-        for (int g = wave; g < G; g += 4) {
-            float* o = part + (int64_t(kvh * G + g) * n_chunks + c) * (HD + 2);
-            if (lane == 0) {
-                o[HD] = -INFINITY;
-                o[HD + 1] = 0.f;
-            }
-        }
-        return;
+    const int p0 = c * C;
+    const int nvalid = min(C, kv_len - p0);
+    if (nvalid <= 0) return;  // past the causal end: the combine reads only the chunks below kv_len
+    const int pnew = pos % max_seq - p0;  // row of this step's k/v inside the chunk (if in [0, C))
+    const bool has_new = pnew >= 0 && pnew < C;
+    float qa[QP], qb[QP];
+    double2 rq[QP];
+    const float* qh = q + kvh * G * HD;
+#pragma unroll
+    for (int j = 0; j < QP; ++j) {
+        const int i = min(t + 256 * j, G * H2 - 1), g = i / H2, d = i % H2;
+        qa[j] = qh[g * HD + d];
+        qb[j] = qh[g * HD + d + H2];
+        rq[j] = cs[d];
     }
-    // K and V rows of the chunk: all loads issued up front (rows past the end
-    // are clamped to the last valid one and get zero weight below), V kept in
-    // registers while the scores are computed; q after them.
-    constexpr int Q4 = HD / 4;               // float4 per row
-    constexpr int NL = kChunk * Q4 / 256;    // float4 per thread
+    __builtin_amdgcn_sched_barrier(0);
+    // K and V rows of the chunk (rows past the end are clamped to the last valid one and get zero weight)
     float4 kv4[NL], vv4[NL];
-#pragma unroll
-    for (int r = 0; r < NL; ++r) {
-        const int i = t + 256 * r, p = min(i / Q4, nvalid - 1), d4 = i % Q4;
-        kv4[r] = reinterpret_cast<const float4*>(kc + (int64_t(kvh) * max_seq + p0 + p) * HD)[d4];
-    }
-#pragma unroll
-    for (int r = 0; r < NL; ++r) {
-        const int i = t + 256 * r, p = min(i / Q4, nvalid - 1), d4 = i % Q4;
-        vv4[r] = reinterpret_cast<const float4*>(vc + (int64_t(kvh) * max_seq + p0 + p) * HD)[d4];
-    }
-    // q heads of this KV group, rotated: one thread per pair (g, d < HD/2)
-    constexpr int H2 = HD / 2;
-    for (int i = t; i < G * H2; i += 256) {
-        const int g = i / H2, d = i % H2;
-        const float* qg = q + (kvh * G + g) * HD;
-        const double2 r = cs[d];
-        const double v0 = qg[d], v1 = qg[d + H2];
-        qs[g * HD + d] = float(v0 * r.x - v1 * r.y);
-        qs[g * HD + d + H2] = float(v0 * r.y + v1 * r.x);
-    }
-    // this step's row: rotated k and v replace what the cache held
+    const float4* kb = reinterpret_cast<const float4*>(kc + (int64_t(kvh) * max_seq + p0) * HD);
+    const float4* vb = reinterpret_cast<const float4*>(vc + (int64_t(kvh) * max_seq + p0) * HD);
 #pragma unroll
     for (int r = 0; r < NL; ++r) {
         const int i = t + 256 * r;
-        if (i / Q4 != pnew) continue;
-        const int d0 = 4 * (i % Q4);
+        kv4[r] = kb[min(i / Q4, nvalid - 1) * Q4 + i % Q4];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int r = 0; r < NL; ++r) {
+        const int i = t + 256 * r;
+        vv4[r] = vb[min(i / Q4, nvalid - 1) * Q4 + i % Q4];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // q heads of this KV group, rotated: one thread per pair (g, d < HD/2)
+#pragma unroll
+    for (int j = 0; j < QP; ++j) {
+        const int i = t + 256 * j;
+        if (i < G * H2) {
+            const int g = i / H2, d = i % H2;
+            const double v0 = qa[j], v1 = qb[j];
+            qs[g * HD + d] = float(v0 * rq[j].x - v1 * rq[j].y);
+            qs[g * HD + d + H2] = float(v0 * rq[j].y + v1 * rq[j].x);
+        }
+    }
+    // K tile (row pnew comes from this step's k below). Element stores keep
+    // the loaded arrays in registers.
+#pragma unroll
+    for (int r = 0; r < NL; ++r) {
+        const int i = t + 256 * r;
+        if (i / Q4 == pnew) continue;
+        float* row = ktile + (i / Q4) * LD + 4 * (i % Q4);
+        row[0] = kv4[r].x;
+        row[1] = kv4[r].y;
+        row[2] = kv4[r].z;
+        row[3] = kv4[r].w;
+    }
+    float4 vnew = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (has_new && t < Q4) {  // this step's row: rotated k and v, into the tiles and the cache
+        const int d0 = 4 * t;
         const float* kn = k_new + kvh * HD;
         float kr[4];
 #pragma unroll
@@ -178,29 +202,25 @@ __global__ void __launch_bounds__(256) k_attn_part(const float* __restrict__ q, 
             const double a0 = kn[dm], a1 = kn[dm + H2];
             kr[e] = d < H2 ? float(a0 * rc.x - a1 * rc.y) : float(a0 * rc.y + a1 * rc.x);
         }
-        kv4[r] = make_float4(kr[0], kr[1], kr[2], kr[3]);
-        vv4[r] = reinterpret_cast<const float4*>(v_new + kvh * HD)[i % Q4];
+        vnew = reinterpret_cast<const float4*>(v_new + kvh * HD)[t];
+        float* row = ktile + pnew * LD + d0;
+        row[0] = kr[0];
+        row[1] = kr[1];
+        row[2] = kr[2];
+        row[3] = kr[3];
         const int64_t crow = (int64_t(kvh) * max_seq + pos % max_seq) * HD;
-        reinterpret_cast<float4*>(kc + crow)[i % Q4] = kv4[r];
-        reinterpret_cast<float4*>(vc + crow)[i % Q4] = vv4[r];
-    }
-#pragma unroll
-    for (int r = 0; r < NL; ++r) {
-        const int i = t + 256 * r;
-        float* row = tile + (i / Q4) * LD + 4 * (i % Q4);
-        row[0] = kv4[r].x;
-        row[1] = kv4[r].y;
-        row[2] = kv4[r].z;
-        row[3] = kv4[r].w;
+        reinterpret_cast<float4*>(kc + crow)[t] = make_float4(kr[0], kr[1], kr[2], kr[3]);
+        reinterpret_cast<float4*>(vc + crow)[t] = vnew;
     }
     __syncthreads();
-    // scores: one wave per query head, one lane per position (4 partial sums)
+    // scores: one wave per query head, LPP lanes per position
     for (int g = wave; g < G; g += 4) {
-        const float4* qg = reinterpret_cast<const float4*>(qs + g * HD);
-        const float* kr = tile + lane * LD;
+        const int p = lane / LPP, h = lane % LPP;
+        const float* kr = ktile + p * LD + h * DW;
+        const float4* qg = reinterpret_cast<const float4*>(qs + g * HD + h * DW);
         float s4[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int d4 = 0; d4 < Q4; ++d4) {
+#pragma unroll 8
+        for (int d4 = 0; d4 < DW / 4; ++d4) {
             const float4 qv = qg[d4];
             float& a = s4[d4 & 3];
             a = fmaf(qv.x, kr[4 * d4], a);
@@ -209,84 +229,148 @@ __global__ void __launch_bounds__(256) k_attn_part(const float* __restrict__ q, 
             a = fmaf(qv.w, kr[4 * d4 + 3], a);
         }
         float s = (s4[0] + s4[1]) + (s4[2] + s4[3]);
-        s = lane < nvalid ? s * scale : -INFINITY;
-        float m = s;
-        for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-        const float e = lane < nvalid ? expf(s - m) : 0.f;
-        float l = e;
-        for (int o = 32; o >= 1; o >>= 1) l += __shfl_xor(l, o, 64);
-        es[g][lane] = e;
+        if (LPP >= 2) s += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(s), 0xb1, 0xf, 0xf, false));  // lane ^ 1
+        if (LPP >= 4) s += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(s), 0x4e, 0xf, 0xf, false));  // lane ^ 2
+        s = p < nvalid ? s * scale : -INFINITY;
+        const float m = wave_maximum(s);
+        const float e = (p < nvalid && h == 0) ? expf(s - m) : 0.f;
+        const float l = wave_total(e);
+        if (h == 0) es[g][p] = e;
         if (lane == 0) {
             float* o = part + (int64_t(kvh * G + g) * n_chunks + c) * (HD + 2);
             o[HD] = m;
             o[HD + 1] = l;
         }
     }
-    __syncthreads();
 #pragma unroll
     for (int r = 0; r < NL; ++r) {
         const int i = t + 256 * r;
-        float* row = tile + (i / Q4) * LD + 4 * (i % Q4);
-        row[0] = vv4[r].x;
-        row[1] = vv4[r].y;
-        row[2] = vv4[r].z;
-        row[3] = vv4[r].w;
+        if (i / Q4 == pnew) continue;
+        float* vr = vtile + 4 * i;
+        vr[0] = vv4[r].x;
+        vr[1] = vv4[r].y;
+        vr[2] = vv4[r].z;
+        vr[3] = vv4[r].w;
+    }
+    if (has_new && t < Q4) {
+        float* vr = vtile + pnew * HD + 4 * t;
+        vr[0] = vnew.x;
+        vr[1] = vnew.y;
+        vr[2] = vnew.z;
+        vr[3] = vnew.w;
     }
     __syncthreads();
-    // o[d] = sum_p e_p v[p][d] over all kChunk rows (e_p = 0 past the end)
+    // o[d] = sum_p e_p v[p][d] over all C rows (e_p = 0 past the end)
     for (int g = wave; g < G; g += 4) {
         float* o = part + (int64_t(kvh * G + g) * n_chunks + c) * (HD + 2);
         const float4* e4 = reinterpret_cast<const float4*>(es[g]);
 #pragma unroll
         for (int d = lane; d < HD; d += 64) {
             float a4[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int p4 = 0; p4 < kChunk / 4; ++p4) {
+#pragma unroll 4
+            for (int p4 = 0; p4 < C / 4; ++p4) {
                 const float4 ev = e4[p4];
                 float& a = a4[p4 & 3];
-                a = fmaf(ev.x, tile[(4 * p4) * LD + d], a);
-                a = fmaf(ev.y, tile[(4 * p4 + 1) * LD + d], a);
-                a = fmaf(ev.z, tile[(4 * p4 + 2) * LD + d], a);
-                a = fmaf(ev.w, tile[(4 * p4 + 3) * LD + d], a);
+                a = fmaf(ev.x, vtile[(4 * p4) * HD + d], a);
+                a = fmaf(ev.y, vtile[(4 * p4 + 1) * HD + d], a);
+                a = fmaf(ev.z, vtile[(4 * p4 + 2) * HD + d], a);
+                a = fmaf(ev.w, vtile[(4 * p4 + 3) * HD + d], a);
             }
             o[d] = (a4[0] + a4[1]) + (a4[2] + a4[3]);
         }
     }
 }
 
-// out[h][d] = sum_c o_c[d] e^{m_c - M} / sum_c l_c e^{m_c - M}, chunks in
-// order; thread c owns chunk c for the max and the weights (nc <= 1024).
-__global__ void __launch_bounds__(256) k_attn_combine(const float* __restrict__ part, float* __restrict__ out, int hd,
+// out[h][d] = sum_c o_c[d] e^{m_c - M} / sum_c l_c e^{m_c - M} over the nc
+// chunks below kv_len, for nc <= 64*NCL. Every load is issued up front: lane
+// j of the wave holds the weights of chunks j, j+64, ... (DPP max and sum),
+// wave w accumulates chunks w, w+4, ... in order with each weight broadcast by
+// readlane, and the four waves' sums are added in LDS.
+template <int HD, int NCL>
+__global__ void __launch_bounds__(256) k_attn_combine(const float* __restrict__ part, float* __restrict__ out,
                                                       int n_chunks, const int32_t* __restrict__ d_pos, int max_seq) {
-    __shared__ float wsc[1024];
+    constexpr int ND = HD / 64, PW = 16 * NCL;
+    __shared__ float red[4][HD];
+    const int h = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int kv_len = min(*d_pos + 1, max_seq);
+    const int nc = min(n_chunks, (kv_len + kChunk - 1) / kChunk);
+    const float* ph = part + int64_t(h) * n_chunks * (HD + 2);
+    float mc[NCL], lc[NCL];
+#pragma unroll
+    for (int j = 0; j < NCL; ++j) {
+        const int cc = lane + 64 * j, cl = min(cc, nc - 1);
+        mc[j] = cc < nc ? ph[cl * (HD + 2) + HD] : -INFINITY;
+        lc[j] = ph[cl * (HD + 2) + HD + 1];
+    }
+    float ov[PW][ND];
+#pragma unroll
+    for (int k = 0; k < PW; ++k) {
+        const int cc = min(wave + 4 * k, nc - 1);
+#pragma unroll
+        for (int j = 0; j < ND; ++j) ov[k][j] = ph[cc * (HD + 2) + lane + 64 * j];
+    }
+    float m = mc[0];
+#pragma unroll
+    for (int j = 1; j < NCL; ++j) m = fmaxf(m, mc[j]);
+    const float M = wave_maximum(m);
+    float w[NCL], lw = 0.f;
+#pragma unroll
+    for (int j = 0; j < NCL; ++j) {
+        w[j] = lane + 64 * j < nc ? expf(mc[j] - M) : 0.f;
+        lw += lc[j] * w[j];
+    }
+    const float L = wave_total(lw);
+    float acc[ND];
+#pragma unroll
+    for (int j = 0; j < ND; ++j) acc[j] = 0.f;
+#pragma unroll
+    for (int k = 0; k < PW; ++k) {
+        const int cc = wave + 4 * k;  // weight register (4k)/64, lane cc % 64
+        const float wk = cc < nc ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w[(4 * k) / 64]), cc % 64)) : 0.f;
+#pragma unroll
+        for (int j = 0; j < ND; ++j) acc[j] = fmaf(ov[k][j], wk, acc[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < ND; ++j) red[wave][lane + 64 * j] = acc[j];
+    __syncthreads();
+    if (t < HD) out[h * HD + t] = ((red[0][t] + red[1][t]) + (red[2][t] + red[3][t])) * (L > 0.f ? 1.0f / L : 0.f);
+}
+
+// The same for any nc <= 2048: thread c owns chunks c, c+256, ... for the max
+// and the weights; chunks are summed in order, eight loads in flight.
+__global__ void __launch_bounds__(256) k_attn_combine_long(const float* __restrict__ part, float* __restrict__ out,
+                                                           int hd, int n_chunks, const int32_t* __restrict__ d_pos,
+                                                           int max_seq) {
+    constexpr int R = 8;
+    __shared__ float wsc[256 * R];
     __shared__ float red[4];
     const int h = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int kv_len = min(*d_pos + 1, max_seq);
     const int nc = min(n_chunks, (kv_len + kChunk - 1) / kChunk);
     const float* ph = part + int64_t(h) * n_chunks * (hd + 2);
-    float mloc[4], lloc[4];
+    float mloc[R], lloc[R];
     float M = -INFINITY;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
+    for (int r = 0; r < R; ++r) {
         const int c = t + 256 * r;
         mloc[r] = c < nc ? ph[c * (hd + 2) + hd] : -INFINITY;
         lloc[r] = c < nc ? ph[c * (hd + 2) + hd + 1] : 0.f;
         M = fmaxf(M, mloc[r]);
     }
-    for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+    M = wave_maximum(M);
     if (lane == 0) red[wave] = M;
     __syncthreads();
     M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     __syncthreads();
     float L = 0.f;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
+    for (int r = 0; r < R; ++r) {
         const int c = t + 256 * r;
         const float w = c < nc ? expf(mloc[r] - M) : 0.f;
         if (c < nc) wsc[c] = w;
         L += lloc[r] * w;
     }
-    for (int o = 32; o >= 1; o >>= 1) L += __shfl_xor(L, o, 64);
+    L = wave_total(L);
     if (lane == 0) red[wave] = L;
     __syncthreads();
     L = (red[0] + red[1]) + (red[2] + red[3]);
@@ -469,6 +553,22 @@ int proj(Decoder& d, const DevBlob& w, const float* x, float* y, int mode, const
 }
 
 // Enqueues one whole step on d.stream (token and position from device memory).
+// The combine variant is fixed by the chunk count the cache can reach.
+void launch_combine(Decoder& d, int hd) {
+    const dim3 grid(unsigned(d.c.n_heads));
+    const int nc = d.n_chunks;
+    if (nc <= 64 && hd == 128)
+        hipLaunchKernelGGL((k_attn_combine<128, 1>), grid, dim3(256), 0, d.stream, d.part, d.att, nc, d.d_pos, d.c.max_seq);
+    else if (nc <= 64)
+        hipLaunchKernelGGL((k_attn_combine<64, 1>), grid, dim3(256), 0, d.stream, d.part, d.att, nc, d.d_pos, d.c.max_seq);
+    else if (nc <= 128 && hd == 128)
+        hipLaunchKernelGGL((k_attn_combine<128, 2>), grid, dim3(256), 0, d.stream, d.part, d.att, nc, d.d_pos, d.c.max_seq);
+    else if (nc <= 128)
+        hipLaunchKernelGGL((k_attn_combine<64, 2>), grid, dim3(256), 0, d.stream, d.part, d.att, nc, d.d_pos, d.c.max_seq);
+    else
+        hipLaunchKernelGGL(k_attn_combine_long, grid, dim3(256), 0, d.stream, d.part, d.att, hd, nc, d.d_pos, d.c.max_seq);
+}
+
 int enqueue_step(Decoder& d, int advance) {
     const wv_decoder_config& c = d.c;
     const int hd = c.head_dim;
@@ -513,8 +613,7 @@ int enqueue_step(Decoder& d, int advance) {
         else
             hipLaunchKernelGGL(k_attn_part<64>, ag, dim3(256), qsh, d.stream, d.q, ly.kc, ly.vc, d.d_pos, d.part,
                                c.n_heads, c.n_kv_heads, c.max_seq, d.n_chunks, scale, d.k, d.v, d.cs);
-        hipLaunchKernelGGL(k_attn_combine, dim3(unsigned(c.n_heads)), dim3(256), 0, d.stream, d.part, d.att, hd,
-                           d.n_chunks, d.d_pos, c.max_seq);
+        launch_combine(d, hd);
         if (fn) {
             e = launch_rpl_ex(ly.w[3], d.att, d.h, 1, d.stream, normed(nullptr, nullptr, RPL_ADD, d.ss_b));
             if (!e) e = launch_rpl_ex(ly.gu, d.h, d.u, 1, d.stream, normed(ly.ffn_norm, d.ss_b, RPL_SWIGLU, nullptr));
@@ -635,7 +734,7 @@ int wv_decoder_create(const wv_decoder_config* cfg, uint64_t* handle) {
         return rt_fail(WV_E_SHAPE, "wv_decoder_create: %d heads over %d KV heads", c.n_heads, c.n_kv_heads);
     if (c.rope_theta <= 0 || c.rms_eps <= 0) return rt_fail(WV_E_ARG, "wv_decoder_create: rope_theta and rms_eps must be > 0");
     if (c.hidden % 4 || c.hidden > 16384) return rt_fail(WV_E_SHAPE, "wv_decoder_create: hidden %d (a multiple of 4, <= 16384)", c.hidden);
-    if (c.max_seq > kChunk * 1024) return rt_fail(WV_E_SHAPE, "wv_decoder_create: max_seq %d > %d", c.max_seq, kChunk * 1024);
+    if (c.max_seq > kChunk * 2048) return rt_fail(WV_E_SHAPE, "wv_decoder_create: max_seq %d > %d", c.max_seq, kChunk * 2048);
     int rc = rt_ensure_init();
     if (rc) return rc;
     Decoder* d = new Decoder();
