@@ -36,7 +36,7 @@ def lib():
         L = ctypes.CDLL(_LIB_PATH)
         L.or_pack_sizes.argtypes = [ctypes.c_int, _I64, _I64, _P]
         L.or_pack.argtypes = [ctypes.c_int, _P, _I64, _I64, _P, _P, _P, _P]
-        blob_args = [ctypes.c_int, _I64, _I64, ctypes.c_int32, _P, _I64, _P, _I64, _P, _I64]
+        blob_args = [ctypes.c_int, _I64, _I64, ctypes.c_int32, _P, _I64, _P, _I64, _P, _I64, _P, _I64]
         L.or_unpack.argtypes = blob_args + [_P]
         L.or_matvec_scalar.argtypes = blob_args + [_P, _P]
         L.or_matvec_t_scalar.argtypes = blob_args + [_P, _P]
@@ -64,11 +64,12 @@ def _ptr(a):
 class Packed:
     """The quant.Blob fields (format.go:110-131) as numpy arrays."""
 
-    def __init__(self, fmt, rows, cols, raw, scales, meta, block_weights):
+    def __init__(self, fmt, rows, cols, raw, scales, meta, block_weights, mins=None):
         self.fmt = fmt if isinstance(fmt, int) else FMT[fmt]
         self.rows, self.cols = int(rows), int(cols)
         self.raw = np.ascontiguousarray(raw, dtype=np.uint8)
         self.scales = None if scales is None or len(scales) == 0 else np.ascontiguousarray(scales, dtype=np.float32)
+        self.mins = None if mins is None or len(mins) == 0 else np.ascontiguousarray(mins, dtype=np.float32)
         self.meta = None if meta is None or len(meta) == 0 else np.ascontiguousarray(meta, dtype=np.uint8)
         self.block_weights = int(block_weights)
 
@@ -80,6 +81,7 @@ class Packed:
         return (self.fmt, self.rows, self.cols, self.block_weights,
                 _ptr(self.raw), self.raw.size,
                 _ptr(self.scales), 0 if self.scales is None else self.scales.size,
+                _ptr(self.mins), 0 if self.mins is None else self.mins.size,
                 _ptr(self.meta), 0 if self.meta is None else self.meta.size)
 
 
@@ -91,12 +93,14 @@ def pack(fmt, w, rows, cols) -> Packed:
     w = np.ascontiguousarray(w, dtype=np.float32).reshape(-1)
     raw = np.zeros(int(sz[0]), np.uint8)
     scales = np.zeros(int(sz[1]), np.float32)
+    mins = np.zeros(int(sz[2]), np.float32)
     meta = np.zeros(int(sz[3]), np.uint8)
     rc = lib().or_pack(f, w.ctypes.data, rows, cols, raw.ctypes.data,
-                       scales.ctypes.data if sz[1] else None, None, meta.ctypes.data if sz[3] else None)
+                       scales.ctypes.data if sz[1] else None, mins.ctypes.data if sz[2] else None,
+                       meta.ctypes.data if sz[3] else None)
     if rc != 0:
         raise ValueError("oracle: pack failed")
-    return Packed(f, rows, cols, raw, scales, meta, int(sz[4]))
+    return Packed(f, rows, cols, raw, scales, meta, int(sz[4]), mins)
 
 
 def unpack(p: Packed) -> np.ndarray:

@@ -75,7 +75,7 @@ class DenseW:
 
     def __init__(self, packed):
         p = oracle.Packed(packed.fmt, packed.rows, packed.cols, packed.raw, packed.scales, packed.meta,
-                          packed.block_weights)
+                          packed.block_weights, getattr(packed, "mins", None))
         self.w = oracle.unpack(p).reshape(packed.rows, packed.cols).astype(np.float64)
 
     def __call__(self, x32: np.ndarray) -> np.ndarray:

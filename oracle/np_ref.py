@@ -243,10 +243,26 @@ def pack(fmt: str, w: np.ndarray, rows: int, cols: int):
         bitsv = ((b >= 0) & m).astype(np.uint32)
         words = (bitsv << np.arange(32, dtype=np.uint32)).sum(axis=1).astype("<u4")
         return dict(raw=words.view(np.uint8), scales=scale, meta=None, block_weights=32)
+    if fmt == "AffinePacked":  # PackAffine4, group 64 along cols (affine_pack.go:15-86)
+        if cols % 64:
+            raise ValueError("AffinePacked: cols must be a multiple of 64")
+        g = w.reshape(rows, cols // 64, 64)
+        mn = g.min(axis=2)
+        mx = g.max(axis=2)
+        s = ((mx - mn) / F32(15)).astype(F32)
+        bad = (s == 0) | ~np.isfinite(s)
+        s[bad] = 1
+        mn[bad] = 0
+        inv = (F32(1) / s).astype(F32)
+        t = ((g - mn[:, :, None]).astype(F32) * inv[:, :, None]).astype(F32)
+        code = np.clip(round_half_away(t.astype(np.float64)), 0, 15).astype(np.uint32).reshape(-1, 8)
+        words = (code << (4 * np.arange(8, dtype=np.uint32))).sum(axis=1).astype("<u4")
+        return dict(raw=words.view(np.uint8), scales=s.reshape(-1), mins=mn.reshape(-1).astype(F32),
+                    meta=np.array([4], np.uint8), block_weights=64)
     raise ValueError(f"unsupported format {fmt}")
 
 
-def unpack(fmt: str, rows: int, cols: int, raw, scales=None, meta=None, block_weights=0):
+def unpack(fmt: str, rows: int, cols: int, raw, scales=None, meta=None, block_weights=0, mins=None):
     """Dequantize to float32[rows*cols] with the reference's f32 formulas."""
     raw = np.asarray(raw, dtype=np.uint8)
     n = rows * cols
@@ -323,6 +339,12 @@ def unpack(fmt: str, rows: int, cols: int, raw, scales=None, meta=None, block_we
         bitsv = (words[:, None] >> np.arange(32, dtype=np.uint32)) & 1
         s = np.asarray(scales, F32)[:, None]
         return np.where(bitsv == 1, s, -s).astype(F32).reshape(-1)[:n]
+    if fmt == "AffinePacked":  # decodeRowAffine (affine_g64.go:124-161): f32(s*code) + beta
+        g = block_weights or 64
+        code = np.stack([raw & 0xF, raw >> 4], axis=1).reshape(rows, cols // g, g).astype(F32)
+        s = np.asarray(scales, F32).reshape(rows, cols // g, 1)
+        beta = np.asarray(mins, F32).reshape(rows, cols // g, 1)
+        return ((s * code).astype(F32) + beta).astype(F32).reshape(-1)
     raise ValueError(f"unsupported format {fmt}")
 
 

@@ -130,6 +130,10 @@ int or_pack_sizes(int fmt, int64_t rows, int64_t cols, int64_t out[5]) {
     case OR_Q5_1: out[0] = (n + 31) / 32 * 28; out[4] = 32; return 0;
     case OR_TERNARY: out[0] = (n + 15) / 16 * 4; out[1] = (n + 15) / 16; out[4] = 16; return 0;
     case OR_BINARY: out[0] = (n + 31) / 32 * 4; out[1] = (n + 31) / 32; out[4] = 32; return 0;
+    case OR_AFFINE: /* PackAffine4 (affine_pack.go:15-41): 4-bit codes, group 64 along cols */
+        if (cols % 64) return -1;
+        out[0] = n / 2; out[1] = out[2] = n / 64; out[3] = 1; out[4] = 64;
+        return 0;
     default: break;
     }
     if (kspec_for(fmt, &ks)) { out[0] = (n + 255) / 256 * ksuper_bytes(&ks); out[4] = 256; return 0; }
@@ -402,9 +406,44 @@ static void pack_binary(const float *w, int64_t n, uint8_t *raw, float *scales) 
     }
 }
 
+/* PackAffine4 (affine_pack.go:15-86) with group g: per group min/max in f32,
+ * s = (max - min)/15 (s == 0, NaN or Inf → s = 1, min = 0), code =
+ * round(f64(f32((v - min) * f32(1/s)))) half away, clamped to [0, 15], eight
+ * codes per little-endian u32 LSB-first; scales = s, mins = min, meta = {4}
+ * (BlobFromMLXAffine4, affine_g64.go:22-78). */
+static void pack_affine(const float *w, int64_t rows, int64_t cols, int g, uint8_t *raw, float *scales, float *mins,
+                        uint8_t *meta) {
+    const float levels = 15.0f;
+    int64_t gpr = cols / g;
+    for (int64_t r = 0; r < rows; r++) {
+        for (int64_t gi = 0; gi < gpr; gi++) {
+            const float *v = w + r * cols + gi * g;
+            float mn = v[0], mx = v[0];
+            for (int j = 1; j < g; j++) {
+                if (v[j] < mn) mn = v[j];
+                if (v[j] > mx) mx = v[j];
+            }
+            float sc = (mx - mn) / levels;
+            if (sc == 0 || isnan(sc) || isinf(sc)) { sc = 1; mn = 0; }
+            scales[r * gpr + gi] = sc;
+            mins[r * gpr + gi] = mn;
+            float inv = 1 / sc;
+            for (int wi = 0; wi < g / 8; wi++) {
+                uint32_t word = 0;
+                for (int j = 0; j < 8; j++) {
+                    float t = (v[wi * 8 + j] - mn) * inv;
+                    long code = clamp_l(round_to_int((double)t), 0, 15);
+                    word |= (uint32_t)code << (4 * j);
+                }
+                put_u32(raw + ((r * cols + gi * g) / 8 + wi) * 4, word);
+            }
+        }
+    }
+    meta[0] = 4;
+}
+
 int or_pack(int fmt, const float *w, int64_t rows, int64_t cols,
             uint8_t *raw, float *scales, float *mins, uint8_t *meta) {
-    (void)mins;
     int64_t sz[5];
     if (or_pack_sizes(fmt, rows, cols, sz) != 0) return -1;
     int64_t n = rows * cols;
@@ -418,6 +457,7 @@ int or_pack(int fmt, const float *w, int64_t rows, int64_t cols,
     case OR_Q5_1: pack_q5_1(w, n, raw); return 0;
     case OR_TERNARY: pack_ternary(w, n, raw, scales); return 0;
     case OR_BINARY: pack_binary(w, n, raw, scales); return 0;
+    case OR_AFFINE: pack_affine(w, rows, cols, 64, raw, scales, mins, meta); return 0;
     default: break;
     }
     if (kspec_for(fmt, &ks)) { pack_k(&ks, w, n, raw); return 0; }
@@ -434,6 +474,7 @@ typedef struct {
     int fmt; int64_t rows, cols; int32_t bw;
     const uint8_t *raw; int64_t raw_len;
     const float *scales; int64_t ns;
+    const float *mins; int64_t nm;
     const uint8_t *meta; int64_t nmeta;
 } blob_t;
 
@@ -606,6 +647,26 @@ static int walk(const blob_t *b, visit_fn fn, void *ctx) {
         }
         return 0;
     }
+    if (b->fmt == OR_AFFINE) { /* decodeRowAffine (affine_g64.go:124-161): w = f32(s*code) + beta */
+        int bits = b->nmeta > 0 && b->meta[0] > 0 ? b->meta[0] : 4;
+        int g = b->bw > 0 ? b->bw : 64, cpw = 32 / bits;
+        if (bits != 4 || b->cols % g || g % cpw) return -1;
+        int64_t wpr = b->cols / cpw, gpr = b->cols / g;
+        uint32_t mask = (1u << bits) - 1;
+        for (int64_t r = 0; r < b->rows; r++)
+            for (int64_t gi = 0; gi < gpr; gi++) {
+                int64_t si = r * gpr + gi;
+                float sc = si < b->ns ? b->scales[si] : 1, beta = si < b->nm ? b->mins[si] : 0;
+                for (int wi = 0; wi < g / cpw; wi++) {
+                    uint32_t word = get_u32(b->raw + (r * wpr + gi * (g / cpw) + wi) * 4);
+                    for (int j = 0; j < cpw; j++) {
+                        float code = (float)((word >> (j * bits)) & mask);
+                        fn(ctx, r * b->cols + gi * g + wi * cpw + j, sc * code + beta);
+                    }
+                }
+            }
+        return 0;
+    }
     if (iqspec_for(b->fmt, &is)) { /* forEachIQ (iq.go:182-207) */
         if (b->nmeta >= 2) { is.bits = b->meta[0]; is.sg = b->meta[1]; }
         bitr_t br = {b->raw, b->raw_len, 0};
@@ -636,8 +697,9 @@ static void visit_mvt(void *ctx, int64_t i, float w) {
 }
 
 int or_unpack(int fmt, int64_t rows, int64_t cols, int32_t bw, const uint8_t *raw, int64_t raw_len,
-              const float *scales, int64_t ns, const uint8_t *meta, int64_t nmeta, float *out) {
-    blob_t b = {fmt, rows, cols, bw, raw, raw_len, scales, ns, meta, nmeta};
+              const float *scales, int64_t ns, const float *mins, int64_t nm, const uint8_t *meta, int64_t nmeta,
+              float *out) {
+    blob_t b = {fmt, rows, cols, bw, raw, raw_len, scales, ns, mins, nm, meta, nmeta};
     memset(out, 0, (size_t)(rows * cols) * sizeof(float));
     return walk(&b, visit_store, out);
 }
@@ -670,20 +732,65 @@ static void matvec_g128(const blob_t *b, const float *x, float *y) {
     free(sum_all);
 }
 
+/* matVecAffine (affine_g64.go:178-267): f32 sumX per group (sequential),
+ * per group f32 codeDot = sum code*x, acc += s*codeDot + beta*sumX[g]. */
+static int matvec_affine(const blob_t *b, const float *x, float *y) {
+    int bits = b->nmeta > 0 && b->meta[0] > 0 ? b->meta[0] : 4;
+    int g = b->bw > 0 ? b->bw : 64, cpw = 32 / bits;
+    if (bits != 4 || b->cols % g || g % cpw) return -1;
+    int64_t wpr = b->cols / cpw, gpr = b->cols / g;
+    uint32_t mask = (1u << bits) - 1;
+    float *sum_x = (float *)malloc((size_t)gpr * sizeof(float));
+    for (int64_t gi = 0; gi < gpr; gi++) {
+        float s = 0;
+        for (int j = 0; j < g; j++) s += x[gi * g + j];
+        sum_x[gi] = s;
+    }
+    for (int64_t r = 0; r < b->rows; r++) {
+        float acc = 0;
+        for (int64_t gi = 0; gi < gpr; gi++) {
+            float sc = b->scales[r * gpr + gi], beta = b->mins[r * gpr + gi], code_dot = 0;
+            for (int wi = 0; wi < g / cpw; wi++) {
+                uint32_t word = get_u32(b->raw + (r * wpr + gi * (g / cpw) + wi) * 4);
+                const float *xb = x + gi * g + wi * cpw;
+                for (int j = 0; j < cpw; j++) code_dot += (float)((word >> (j * bits)) & mask) * xb[j];
+            }
+            acc += sc * code_dot + beta * sum_x[gi];
+        }
+        y[r] = acc;
+    }
+    free(sum_x);
+    return 0;
+}
+
+/* matVecTAffine (affine_g64.go:269-286): rows with gy == 0 are skipped,
+ * otherwise gx[j] += w[r][j] * gy[r] over the decoded row. */
+typedef struct { const blob_t *b; const float *gy; float *gx; } mvt_aff_ctx;
+static void visit_mvt_affine(void *ctx, int64_t i, float w) {
+    mvt_aff_ctx *c = (mvt_aff_ctx *)ctx;
+    float g = c->gy[i / c->b->cols];
+    if (g != 0) c->gx[i % c->b->cols] += w * g;
+}
+
 int or_matvec_scalar(int fmt, int64_t rows, int64_t cols, int32_t bw, const uint8_t *raw, int64_t raw_len,
-                     const float *scales, int64_t ns, const uint8_t *meta, int64_t nmeta,
-                     const float *x, float *y) {
-    blob_t b = {fmt, rows, cols, bw, raw, raw_len, scales, ns, meta, nmeta};
+                     const float *scales, int64_t ns, const float *mins, int64_t nm, const uint8_t *meta,
+                     int64_t nmeta, const float *x, float *y) {
+    blob_t b = {fmt, rows, cols, bw, raw, raw_len, scales, ns, mins, nm, meta, nmeta};
     if (is_g128(&b)) { matvec_g128(&b, x, y); return 0; }
+    if (fmt == OR_AFFINE) return matvec_affine(&b, x, y);
     for (int64_t r = 0; r < rows; r++) y[r] = 0;
     mv_ctx c = {&b, x, y};
     return walk(&b, visit_mv, &c);
 }
 
 int or_matvec_t_scalar(int fmt, int64_t rows, int64_t cols, int32_t bw, const uint8_t *raw, int64_t raw_len,
-                       const float *scales, int64_t ns, const uint8_t *meta, int64_t nmeta,
-                       const float *gy, float *gx) {
-    blob_t b = {fmt, rows, cols, bw, raw, raw_len, scales, ns, meta, nmeta};
+                       const float *scales, int64_t ns, const float *mins, int64_t nm, const uint8_t *meta,
+                       int64_t nmeta, const float *gy, float *gx) {
+    blob_t b = {fmt, rows, cols, bw, raw, raw_len, scales, ns, mins, nm, meta, nmeta};
+    if (fmt == OR_AFFINE) {
+        mvt_aff_ctx c = {&b, gy, gx};
+        return walk(&b, visit_mvt_affine, &c);
+    }
     mv_ctx c = {&b, gy, gx};
     return walk(&b, visit_mvt, &c);
 }
@@ -870,8 +977,22 @@ static double q4_0_row_tail(const float *in, const float *scales, const uint32_t
     return sum;
 }
 
-/* One output row of the fused path for any projected format. */
-static float simd_row(const simd_t *s, const float *x, int64_t o) {
+/* DotAffineRow (simd/dot_k.go:140-165): per group f64 accQ = sum x*code,
+ * sum += accQ*s + beta*f64(sumX[g]) with the f32 group sums of AffineSumX. */
+static double dot_affine_row(const float *in, const float *scales, const float *mins, const float *sum_x,
+                             const int8_t *qs, int64_t basew, int64_t n, int g, int64_t scale_base) {
+    double sum = 0;
+    for (int64_t gi = 0; gi < n / g; gi++) {
+        double sc = scales[scale_base + gi], beta = mins[scale_base + gi], accq = 0;
+        for (int j = 0; j < g; j++) accq += (double)in[gi * g + j] * (double)(uint8_t)qs[basew + gi * g + j];
+        sum += accq * sc + beta * (double)sum_x[gi];
+    }
+    return sum;
+}
+
+/* One output row of the fused path for any projected format (sum_x: the
+ * AffineSumX group sums of x, for AffinePacked). */
+static float simd_row(const simd_t *s, const float *x, int64_t o, const float *sum_x) {
     int64_t in = s->cols, basew = o * in;
     switch (s->fmt) {
     case OR_Q4_0: { /* dotQ4_0RowSimd (dot_q4_amd64.go:8-22) */
@@ -897,6 +1018,7 @@ static float simd_row(const simd_t *s, const float *x, int64_t o) {
         return (float)sum;
     }
     case OR_Q5_1: return (float)dot_q5_1_row(x, s->scales, s->mins, s->qs, basew, in);
+    case OR_AFFINE: return (float)dot_affine_row(x, s->scales, s->mins, sum_x, s->qs, basew, in, s->sg, o * (in / s->sg));
     case OR_TERNARY: return (float)dot_tile_f64(x, s->f32 + basew, in);
     case OR_BINARY: return (float)dot_tile_f64(x, s->f32 + basew, in);
     default: break;
@@ -907,12 +1029,27 @@ static float simd_row(const simd_t *s, const float *x, int64_t o) {
 }
 
 void *or_simd_prepare(int fmt, int64_t rows, int64_t cols, int32_t bw, const uint8_t *raw, int64_t raw_len,
-                      const float *scales, int64_t ns, const uint8_t *meta, int64_t nmeta) {
+                      const float *scales, int64_t ns, const float *mins, int64_t nm, const uint8_t *meta,
+                      int64_t nmeta) {
     simd_t *s = (simd_t *)calloc(1, sizeof(simd_t));
     s->fmt = fmt; s->rows = rows; s->cols = cols;
     int64_t n = rows * cols;
     kspec_t ks; iqspec_t is;
-    blob_t b = {fmt, rows, cols, bw, raw, raw_len, scales, ns, meta, nmeta};
+    blob_t b = {fmt, rows, cols, bw, raw, raw_len, scales, ns, mins, nm, meta, nmeta};
+    if (fmt == OR_AFFINE) { /* EnsureAffineSIMDCache (k_iq_simd.go:187-240): codes to Int8QS */
+        int g = bw > 0 ? bw : 64;
+        int bits = nmeta > 0 && meta[0] > 0 ? meta[0] : 4;
+        int64_t gpr = cols / g;
+        if (bits != 4 || cols % g || ns < rows * gpr || nm < rows * gpr || raw_len < n / 2) { free(s); return NULL; }
+        s->qs = (int8_t *)malloc((size_t)n);
+        for (int64_t i = 0; i < n; i++) s->qs[i] = (int8_t)((raw[i / 2] >> (4 * (i & 1))) & 15);
+        s->scales = (float *)malloc((size_t)ns * 4);
+        s->mins = (float *)malloc((size_t)nm * 4);
+        memcpy(s->scales, scales, (size_t)ns * 4);
+        memcpy(s->mins, mins, (size_t)nm * 4);
+        s->sg = g;
+        return s;
+    }
     if (fmt == OR_Q4_0 || fmt == OR_Q4_1) { /* EnsureQ4SIMDCache / EnsureQ41SIMDCache (q4_simd.go:7-35, qx_simd.go:34-65) */
         int bb = fmt == OR_Q4_0 ? 20 : 24, qo = fmt == OR_Q4_0 ? 4 : 8;
         int64_t blocks = (n + 31) / 32;
@@ -980,7 +1117,7 @@ void *or_simd_prepare(int fmt, int64_t rows, int64_t cols, int32_t bw, const uin
     }
     if (fmt == OR_TERNARY || (fmt == OR_BINARY && bw != 128)) { /* EnsureFloatCache (qx_simd.go:181-201) */
         s->f32 = (float *)malloc((size_t)n * 4);
-        or_unpack(fmt, rows, cols, bw, raw, raw_len, scales, ns, meta, nmeta, s->f32);
+        or_unpack(fmt, rows, cols, bw, raw, raw_len, scales, ns, mins, nm, meta, nmeta, s->f32);
         return s;
     }
     if (fmt == OR_BINARY && bw == 128) { /* native packed G128 (no inflate) */
@@ -1024,7 +1161,18 @@ static void *simd_worker(void *arg) {
             }
         }
     }
-    for (; o < j->hi; o++) j->y[o] = simd_row(s, j->x, o);
+    float *sum_x = NULL;
+    if (s->fmt == OR_AFFINE) { /* gemvAffineRowsF32 (gemv_parallel.go:331-339): AffineSumX per worker */
+        int64_t gpr = s->cols / s->sg;
+        sum_x = (float *)malloc((size_t)gpr * sizeof(float));
+        for (int64_t gi = 0; gi < gpr; gi++) {
+            float t = 0;
+            for (int k = 0; k < s->sg; k++) t += j->x[gi * s->sg + k];
+            sum_x[gi] = t;
+        }
+    }
+    for (; o < j->hi; o++) j->y[o] = simd_row(s, j->x, o, sum_x);
+    free(sum_x);
     return NULL;
 }
 

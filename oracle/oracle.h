@@ -46,12 +46,16 @@ int or_pack(int fmt, const float *w, int64_t rows, int64_t cols,
 int or_unpack(int fmt, int64_t rows, int64_t cols, int32_t block_weights,
               const uint8_t *raw, int64_t raw_len,
               const float *scales, int64_t n_scales,
+              const float *mins, int64_t n_mins,
               const uint8_t *meta, int64_t n_meta, float *out);
 
-/* quant.MatVec (quant/matvec.go:5): y overwritten, flat-order f32 walk. */
+/* quant.MatVec (quant/matvec.go:5): y overwritten, flat-order f32 walk
+ * (AffinePacked: the per-group form of affine_g64.go:178-267). mins is
+ * Blob.Mins (AffinePacked biases; NULL for every other format). */
 int or_matvec_scalar(int fmt, int64_t rows, int64_t cols, int32_t block_weights,
                      const uint8_t *raw, int64_t raw_len,
                      const float *scales, int64_t n_scales,
+                     const float *mins, int64_t n_mins,
                      const uint8_t *meta, int64_t n_meta,
                      const float *x, float *y);
 
@@ -59,6 +63,7 @@ int or_matvec_scalar(int fmt, int64_t rows, int64_t cols, int32_t block_weights,
 int or_matvec_t_scalar(int fmt, int64_t rows, int64_t cols, int32_t block_weights,
                        const uint8_t *raw, int64_t raw_len,
                        const float *scales, int64_t n_scales,
+                       const float *mins, int64_t n_mins,
                        const uint8_t *meta, int64_t n_meta,
                        const float *gy, float *gx);
 
@@ -73,6 +78,7 @@ void or_gemv_f64(const float *w, int64_t rows, int64_t cols, const float *x, dou
 void *or_simd_prepare(int fmt, int64_t rows, int64_t cols, int32_t block_weights,
                       const uint8_t *raw, int64_t raw_len,
                       const float *scales, int64_t n_scales,
+                      const float *mins, int64_t n_mins,
                       const uint8_t *meta, int64_t n_meta);
 void or_simd_free(void *h);
 /* y = W x for `batch` rows of x (batch*cols) → y (batch*rows), using

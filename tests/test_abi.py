@@ -74,7 +74,7 @@ def test_error_paths_without_device():
         wv.pack_sizes("Q4_K", 0, 256)
     assert e.value.code == -2
     with pytest.raises(wv.WelvetError) as e:
-        wv.pack_sizes(20, 4, 64)  # AffinePacked: not built here
+        wv.pack_sizes(0, 4, 64)  # FormatNone has no quant.Pack
     assert e.value.code == -3 and "not implemented" in str(e.value)
     short = wv.PackedBlob("Q4_K", 4, 256, np.zeros(10, np.uint8), block_weights=256)
     with pytest.raises(wv.WelvetError) as e:
@@ -87,3 +87,31 @@ def test_error_paths_without_device():
     with pytest.raises(wv.WelvetError) as e:
         wv.check(wv.lib().wv_blob_free(123456789))
     assert e.value.code == -7
+
+
+@pytest.mark.parametrize("shape", [(16, 256), (64, 512), (3, 64), (7, 1088)])
+def test_host_packer_affine_bit_exact_vs_oracle(shape):
+    rows, cols = shape
+    rng = np.random.default_rng(11 + rows)
+    w = (rng.standard_normal(rows * cols) * 0.02).astype(np.float32)
+    a = wv.pack("AffinePacked", w, rows, cols)
+    b = oracle.pack("AffinePacked", w, rows, cols)
+    assert np.array_equal(a.raw, b.raw) and np.array_equal(a.scales, b.scales) and np.array_equal(a.mins, b.mins)
+    assert list(a.meta) == [4] and a.block_weights == 64
+    assert a.nbytes == rows * cols // 2 + 2 * 4 * (rows * cols // 64) + 1
+
+
+def test_affine_pack_and_upload_errors():
+    """PackAffine4 rejects cols % 64 != 0 (affine_pack.go:29-31); uploads need 4-bit
+    codes and a bias per group (the fused path's cache checks, k_iq_simd.go:201-215)."""
+    with pytest.raises(wv.WelvetError):
+        wv.pack("AffinePacked", np.zeros(5 * 77, np.float32), 5, 77)
+    rows, cols = 4, 128
+    words = np.zeros(rows * cols // 2, np.uint8)
+    scales = np.ones(rows * cols // 64, np.float32)
+    p = wv.PackedBlob("AffinePacked", rows, cols, words, scales, np.array([3], np.uint8), 64, mins=scales)
+    with pytest.raises(wv.WelvetError, match="bits=3"):
+        wv.upload(p)
+    p = wv.PackedBlob("AffinePacked", rows, cols, words, scales, np.array([4], np.uint8), 64)
+    with pytest.raises(wv.WelvetError, match="mins"):
+        wv.upload(p)

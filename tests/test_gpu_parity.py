@@ -53,7 +53,7 @@ def upload(fmt, w, rows, cols, force_raw=False):
 
 
 def oracle_packed(p):
-    return oracle.Packed(p.fmt, p.rows, p.cols, p.raw, p.scales, p.meta, p.block_weights)
+    return oracle.Packed(p.fmt, p.rows, p.cols, p.raw, p.scales, p.meta, p.block_weights, p.mins)
 
 
 @pytest.mark.parametrize("fmt", ALL)
@@ -267,3 +267,60 @@ def test_binary_g128_layout():
     ref = oracle.reference_y(op, x)[0]
     assert normwise(d.matvec(x), ref) <= TOL
     assert normwise(oracle.matvec_scalar(op, x), ref) <= TOL
+
+
+# ---------------------------------------------------------------- AffinePacked (quant/affine_*.go)
+
+@pytest.mark.parametrize("shape", [(96, 512), (33, 320), (16, 4096), (3, 64)])
+def test_affine_matvec(shape):
+    """Packed by PackAffine4 (group 64): the run-vectorised kernel when cols % 256 == 0, else the per-weight one."""
+    rows, cols = shape
+    print(f"[gpu] affine matvec {rows}x{cols}", flush=True)
+    w, rng = weights(rows, cols, 300 + rows)
+    x = rng.standard_normal((2, cols)).astype(np.float32)
+    p, d = upload("AffinePacked", w, rows, cols)
+    ref = oracle.reference_y(oracle_packed(p), x)
+    assert normwise(d.matvec(x), ref) <= TOL
+    assert normwise(d.matvec(x[1]), ref[1]) <= TOL
+    d.free()
+
+
+@pytest.mark.parametrize("group,cols", [(32, 512), (128, 1024), (8, 256)])
+def test_affine_mlx_groups(group, cols):
+    """BlobFromMLXAffine4-style blobs (affine_g64.go:22-78) with other group widths: random
+    4-bit words, per-group scales and biases; group 8 takes the per-weight kernel."""
+    rows = 40
+    print(f"[gpu] affine group {group} cols {cols}", flush=True)
+    rng = np.random.default_rng(group)
+    words = rng.integers(0, 2**32, size=rows * cols // 8, dtype=np.uint64).astype(np.uint32)
+    ng = rows * cols // group
+    scales = (np.abs(rng.standard_normal(ng)) * 0.01 + 1e-3).astype(np.float32)
+    mins = (rng.standard_normal(ng) * 0.05).astype(np.float32)
+    p = wv.PackedBlob("AffinePacked", rows, cols, words.view(np.uint8), scales, np.array([4], np.uint8), group,
+                      mins=mins)
+    d = wv.upload(p)
+    x = rng.standard_normal(cols).astype(np.float32)
+    op = oracle_packed(p)
+    ref = oracle.reference_y(op, x)[0]
+    assert normwise(d.matvec(x), ref) <= TOL
+    assert normwise(oracle.matvec_scalar(op, x), ref) <= TOL
+    gy = rng.standard_normal(rows).astype(np.float32)
+    gx0 = rng.standard_normal(cols).astype(np.float32)
+    wd = oracle.unpack(op).reshape(rows, cols).astype(np.float64)
+    assert normwise(d.matvec_t(gy, gx0), gx0 + gy.astype(np.float64) @ wd) <= TOL
+    d.free()
+
+
+def test_affine_matvec_t_accumulates():
+    rows, cols = 300, 512
+    print("[gpu] affine matvec_t", flush=True)
+    w, rng = weights(rows, cols, 19)
+    gy = rng.standard_normal((2, rows)).astype(np.float32)
+    gy[0, 5] = 0.0  # matVecTAffine skips such rows; with finite weights the sum is the same
+    gx0 = rng.standard_normal((2, cols)).astype(np.float32)
+    p, d = upload("AffinePacked", w, rows, cols)
+    wd = oracle.unpack(oracle_packed(p)).reshape(rows, cols).astype(np.float64)
+    want = gx0 + gy.astype(np.float64) @ wd
+    assert normwise(d.matvec_t(gy, gx0), want) <= TOL
+    assert normwise(oracle.matvec_t_scalar(oracle_packed(p), gy[0], gx0[0]), want[0]) <= TOL
+    d.free()

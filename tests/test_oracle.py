@@ -275,3 +275,104 @@ def test_native_ternary_pack_and_int8_path():
     brute = t.reshape(rows, cols).astype(np.int64) @ xq.astype(np.int64)
     assert np.array_equal(acc, brute.astype(np.int32))
     assert np.array_equal(y, (acc.astype(np.float32) * xs).astype(np.float32) * scale)
+
+
+# ---------------------------------------------------------------- AffinePacked (quant/affine_*.go)
+
+@pytest.mark.parametrize("shape", [(8, 256), (3, 64), (5, 576)])
+def test_affine_c_oracle_matches_numpy_restatement(shape):
+    rows, cols = shape
+    rng = np.random.default_rng(rows * 7 + cols)
+    w = (rng.standard_normal(rows * cols) * 0.02).astype(np.float32)
+    p = oracle.pack("AffinePacked", w, rows, cols)
+    r = np_ref.pack("AffinePacked", w, rows, cols)
+    assert np.array_equal(p.raw, r["raw"])
+    assert np.array_equal(p.scales, r["scales"]) and np.array_equal(p.mins, r["mins"])
+    assert list(p.meta) == [4] and p.block_weights == 64
+    wc = oracle.unpack(p)
+    wn = np_ref.unpack("AffinePacked", rows, cols, p.raw, p.scales, p.meta, p.block_weights, p.mins)
+    assert np.array_equal(wc, wn)
+
+
+def test_affine_grid_roundtrip_and_bytes():
+    """A group on the grid min + k*s (min -0.5, s 1/16, k = 0..15 each used) packs to codes k
+    (nibble j of little-endian word = element j), scale 1/16, min -0.5, and decodes exactly."""
+    k = np.array([(5 * j + 3) % 16 for j in range(64)], np.int64)
+    k[:2] = (0, 15)  # min and max present
+    w = (np.float32(-0.5) + k.astype(np.float32) * np.float32(0.0625)).astype(np.float32)
+    p = oracle.pack("AffinePacked", w, 1, 64)
+    assert p.scales.tolist() == [0.0625] and p.mins.tolist() == [-0.5]
+    want = bytes((int(k[2 * b]) | (int(k[2 * b + 1]) << 4)) for b in range(32))
+    assert bytes(p.raw) == want
+    assert np.array_equal(oracle.unpack(p), w)
+
+
+def test_affine_special_groups():
+    """affine_pack.go:49-56: a group with max == min gets s = 1 and min = 0, so
+    the codes are round-half-away(v) clamped to [0, 15]; ties round away."""
+    zero = np.zeros(64, np.float32)
+    half = np.full(64, 0.5, np.float32)
+    big = np.full(64, 20.0, np.float32)
+    ties = np.zeros(64, np.float32)
+    ties[1] = 15.0  # s = 1, min = 0
+    ties[2:6] = (2.5, 3.5, 0.5, 14.5)
+    w = np.concatenate([zero, half, big, ties])
+    p = oracle.pack("AffinePacked", w, 1, 256)
+    assert p.scales.tolist() == [1.0, 1.0, 1.0, 1.0] and p.mins.tolist() == [0.0, 0.0, 0.0, 0.0]
+    codes = np.stack([p.raw & 15, p.raw >> 4], axis=1).reshape(-1)
+    assert not codes[:64].any()
+    assert (codes[64:128] == 1).all()  # 0.5 -> 1 (half away), decodes to 1.0
+    assert (codes[128:192] == 15).all()  # clamp
+    assert codes[192:198].tolist() == [0, 15, 3, 4, 1, 15]
+    assert oracle.unpack(p)[64] == 1.0
+
+
+def test_affine_matvec_closed_form_and_f64():
+    """Groups on exact binary grids (s = 1/16, min -0.5; s = 1/8, min 0.25) and
+    x = 1: every product and sum is exact, so y is the plain sum of the weights
+    (s*sum(code) + beta*64 per group); random blobs: scalar MatVec and the
+    fused SIMD path against the f64 GEMV."""
+    rows, cols = 3, 128
+    rng = np.random.default_rng(20)
+    w = np.zeros((rows, cols), np.float32)
+    for r in range(rows):
+        k1, k2 = rng.integers(0, 16, 64), rng.integers(0, 16, 64)
+        k1[:2], k2[:2] = (0, 15), (15, 0)
+        w[r, :64] = -0.5 + k1 * 0.0625
+        w[r, 64:] = 0.25 + k2 * 0.125
+    p = oracle.pack("AffinePacked", w.reshape(-1), rows, cols)
+    assert p.scales.tolist() == [0.0625, 0.125] * rows and p.mins.tolist() == [-0.5, 0.25] * rows
+    x = np.ones(cols, np.float32)
+    want = w.astype(np.float64).sum(axis=1)
+    assert np.array_equal(oracle.matvec_scalar(p, x).astype(np.float64), want)
+    assert np.array_equal(oracle.SimdPath(p).matvec(x, nthreads=1).astype(np.float64).reshape(-1), want)
+    rng = np.random.default_rng(21)
+    rows, cols = 67, 512
+    w = (rng.standard_normal(rows * cols) * 0.02).astype(np.float32)
+    x = rng.standard_normal(cols).astype(np.float32)
+    p = oracle.pack("AffinePacked", w, rows, cols)
+    ref = oracle.reference_y(p, x)[0]
+    scale = np.abs(ref).max()
+    assert np.abs(oracle.matvec_scalar(p, x) - ref).max() / scale < 1e-5
+    simd = oracle.SimdPath(p)
+    y1 = simd.matvec(x, nthreads=1)
+    assert np.array_equal(y1, simd.matvec(x, nthreads=4))
+    assert np.abs(y1 - ref).max() / scale < 1e-6
+
+
+def test_affine_matvec_t_skips_zero_rows():
+    """matVecTAffine (affine_g64.go:269-286) accumulates into gx and skips rows whose gy is 0."""
+    rng = np.random.default_rng(22)
+    rows, cols = 9, 192
+    w = (rng.standard_normal(rows * cols) * 0.02).astype(np.float32)
+    gy = rng.standard_normal(rows).astype(np.float32)
+    gy[[1, 4]] = 0
+    gx0 = rng.standard_normal(cols).astype(np.float32)
+    p = oracle.pack("AffinePacked", w, rows, cols)
+    wd = oracle.unpack(p).reshape(rows, cols).astype(np.float64)
+    got = oracle.matvec_t_scalar(p, gy, gx0)
+    want = gx0 + wd.T @ gy
+    assert np.abs(got - want).max() / np.abs(want).max() < 1e-5
+    neg = np.full(cols, -0.0, np.float32)  # a skipped row leaves -0.0 untouched
+    gz = np.zeros(rows, np.float32)
+    assert np.signbit(oracle.matvec_t_scalar(p, gz, neg)).all()

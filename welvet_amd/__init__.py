@@ -20,7 +20,7 @@ FORMATS = {
     "Q8_0": 1, "Q4_0": 2, "Q4_1": 3, "Q5_0": 4, "Q5_1": 5,
     "Q2_K": 6, "Q3_K": 7, "Q4_K": 8, "Q5_K": 9, "Q6_K": 10,
     "IQ1_S": 11, "IQ2_XXS": 12, "IQ2_XS": 13, "IQ3_XXS": 14, "IQ3_S": 15,
-    "IQ4_NL": 16, "IQ4_XS": 17, "TernaryPacked": 18, "BinaryPacked": 19,
+    "IQ4_NL": 16, "IQ4_XS": 17, "TernaryPacked": 18, "BinaryPacked": 19, "AffinePacked": 20,
     "NativeTernary": 1019,
 }
 FORMAT_NAMES = {v: k for k, v in FORMATS.items()}
@@ -105,11 +105,12 @@ def init(device: int = 0) -> None:
 class PackedBlob:
     """Host-side quant.Blob fields (quant/format.go:110-131)."""
 
-    def __init__(self, fmt, rows, cols, raw, scales=None, meta=None, block_weights=0, tensor_scale=0.0):
+    def __init__(self, fmt, rows, cols, raw, scales=None, meta=None, block_weights=0, tensor_scale=0.0, mins=None):
         self.fmt = _fmt(fmt)
         self.rows, self.cols = int(rows), int(cols)
         self.raw = np.ascontiguousarray(raw, np.uint8)
         self.scales = None if scales is None or len(scales) == 0 else np.ascontiguousarray(scales, np.float32)
+        self.mins = None if mins is None or len(mins) == 0 else np.ascontiguousarray(mins, np.float32)
         self.meta = None if meta is None or len(meta) == 0 else np.ascontiguousarray(meta, np.uint8)
         self.block_weights = int(block_weights)
         self.tensor_scale = float(tensor_scale)
@@ -120,8 +121,9 @@ class PackedBlob:
 
     @property
     def nbytes(self) -> int:
-        """Packed bytes in the reference layout (Raw + Scales + Meta)."""
-        return self.raw.nbytes + (0 if self.scales is None else self.scales.nbytes) + (0 if self.meta is None else self.meta.nbytes)
+        """Packed bytes in the reference layout (Raw + Scales + Mins + Meta)."""
+        return (self.raw.nbytes + (0 if self.scales is None else self.scales.nbytes)
+                + (0 if self.mins is None else self.mins.nbytes) + (0 if self.meta is None else self.meta.nbytes))
 
 
 def pack_sizes(fmt, rows: int, cols: int):
@@ -136,17 +138,16 @@ def pack(fmt, w: np.ndarray, rows: int, cols: int) -> PackedBlob:
     """quant.Pack (quant/pack.go:4) through the library's host packer."""
     if _fmt(fmt) == FORMATS["NativeTernary"]:
         return pack_native_ternary(w, rows, cols)
-    raw_n, ns, _, nmeta, bw = pack_sizes(fmt, rows, cols)
+    raw_n, ns, nmins, nmeta, bw = pack_sizes(fmt, rows, cols)
     w = np.ascontiguousarray(w, np.float32).reshape(-1)
     if w.size < rows * cols:
         raise WelvetError(-2, f"Pack: bad shape rows={rows} cols={cols} len={w.size}")
     raw = np.zeros(raw_n, np.uint8)
     scales = np.zeros(ns, np.float32) if ns else None
+    mins = np.zeros(nmins, np.float32) if nmins else None
     meta = np.zeros(nmeta, np.uint8) if nmeta else None
-    check(lib().wv_pack(_fmt(fmt), w.ctypes.data, rows, cols, raw.ctypes.data,
-                        None if scales is None else scales.ctypes.data, None,
-                        None if meta is None else meta.ctypes.data))
-    return PackedBlob(fmt, rows, cols, raw, scales, meta, bw)
+    check(lib().wv_pack(_fmt(fmt), w.ctypes.data, rows, cols, raw.ctypes.data, _p(scales), _p(mins), _p(meta)))
+    return PackedBlob(fmt, rows, cols, raw, scales, meta, bw, mins=mins)
 
 
 def pack_native_ternary(w: np.ndarray, rows: int, cols: int) -> PackedBlob:
@@ -169,7 +170,8 @@ class DeviceBlob:
         h = ctypes.c_uint64()
         p = packed
         check(lib().wv_blob_upload(p.fmt, p.rows, p.cols, p.block_weights, _p(p.raw), p.raw.size,
-                                   _p(p.scales), 0 if p.scales is None else p.scales.size, None, 0,
+                                   _p(p.scales), 0 if p.scales is None else p.scales.size,
+                                   _p(p.mins), 0 if p.mins is None else p.mins.size,
                                    _p(p.meta), 0 if p.meta is None else p.meta.size,
                                    ctypes.c_float(p.tensor_scale), ctypes.byref(h)))
         self.handle = h.value

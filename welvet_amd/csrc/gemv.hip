@@ -61,6 +61,8 @@ struct RawArgs {
     int64_t rows, cols;
     int iq_bits, iq_sg;
     int g128;  // BinaryPacked with BlockWeights == 128 (row-aligned groups)
+    const float* mins;  // AffinePacked biases, one per group of `group` weights
+    int64_t group;
 };
 
 template <int F>
@@ -130,6 +132,10 @@ __device__ __forceinline__ float decode(const RawArgs& a, int64_t i, int64_t row
         uint32_t c = (ld_u32(a.raw + g * 4) >> ((i & 15) * 2)) & 3u;
         float s = g < a.n_scales ? a.scales[g] : 1.0f;
         return c == 0 ? -s : (c == 2 ? s : 0.0f);
+    } else if constexpr (F == FMT_AFFINE) {  // decodeRowAffine (affine_g64.go:124-161), 4-bit codes
+        const uint32_t code = (uint32_t(a.raw[i >> 1]) >> ((i & 1) * 4)) & 15u;
+        const int64_t g = i / a.group;  // cols % group == 0: flat group = row * groups_per_row + col / group
+        return a.scales[g] * float(code) + a.mins[g];
     } else if constexpr (F == FMT_BINARY) {
         if (a.g128) {  // binary_g128.go:107-139, row-aligned groups
             int64_t wpr = a.cols >> 5, gpr = a.cols >> 7;
@@ -284,6 +290,14 @@ template <> struct RawF<FMT_TERNARY> {
         return {a.raw + g * 4, g < a.n_scales ? a.scales[g] : 1.0f, 0.0f};
     }
     static __device__ float fq(uint32_t q, const float* tab) { return q == 0 ? -1.0f : (q == 2 ? 1.0f : 0.0f); }
+};
+template <> struct RawF<FMT_AFFINE> {
+    static constexpr int BITS = 4;
+    static __device__ Grp grp(const RawArgs& a, int64_t row, int64_t f) {  // affine_g64.go:140-160
+        const int64_t g = f / a.group;
+        return {a.raw + (f >> 1), a.scales[g], a.mins[g]};
+    }
+    static __device__ float fq(uint32_t q, const float* tab) { return float(q); }
 };
 template <> struct RawF<FMT_BINARY> {
     static constexpr int BITS = 1;
@@ -592,6 +606,8 @@ RawArgs raw_args(const DevBlob& b) {
     a.iq_bits = b.iq_bits;
     a.iq_sg = b.iq_sg;
     a.g128 = (b.fmt == FMT_BINARY && b.block_weights == 128) ? 1 : 0;
+    a.mins = b.mins;
+    a.group = b.block_weights > 0 ? b.block_weights : 64;
     return a;
 }
 
@@ -606,6 +622,7 @@ bool raw16_ok(const DevBlob& b) {
         return b.iq_bits == sp.bits && b.iq_sg == sp.sg;
     }
     if constexpr (F == FMT_BINARY) return b.block_weights != 128 || b.cols % 128 == 0;
+    if constexpr (F == FMT_AFFINE) return b.block_weights % 16 == 0;  // a run of 16 never straddles groups
     return true;
 }
 
@@ -655,6 +672,7 @@ RawFn pick_raw(int fmt) {
     case FMT_IQ4_XS: return launch_raw<FMT_IQ4_XS>;
     case FMT_TERNARY: return launch_raw<FMT_TERNARY>;
     case FMT_BINARY: return launch_raw<FMT_BINARY>;
+    case FMT_AFFINE: return launch_raw<FMT_AFFINE>;
     default: return nullptr;
     }
 }
@@ -679,6 +697,7 @@ RawTFn pick_raw_t(int fmt) {
     case FMT_IQ4_XS: return launch_raw_t<FMT_IQ4_XS>;
     case FMT_TERNARY: return launch_raw_t<FMT_TERNARY>;
     case FMT_BINARY: return launch_raw_t<FMT_BINARY>;
+    case FMT_AFFINE: return launch_raw_t<FMT_AFFINE>;
     default: return nullptr;
     }
 }

@@ -311,6 +311,42 @@ void pack_binary(const float* w, int64_t n, uint8_t* raw, float* scales) {
     });
 }
 
+// ---- AffinePacked (quant/affine_pack.go:15-86, BlobFromMLXAffine4 affine_g64.go:22-78) ----
+// Groups of g along each row (cols % g == 0, so flat group gi starts at gi*g):
+// f32 min/max, s = (max - min)/15 (0, NaN or Inf -> s = 1 and min = 0),
+// code = round(f64(f32((v - min) * f32(1/s)))) clamped to [0, 15], eight codes
+// per little-endian u32 LSB-first; Scales = s, Mins = min, Meta = {4}.
+void pack_affine(const float* w, int64_t rows, int64_t cols, int g, uint8_t* raw, float* scales, float* mins,
+                 uint8_t* meta) {
+    parallel_blocks(rows * (cols / g), [&](int64_t lo, int64_t hi) {
+        for (int64_t gi = lo; gi < hi; ++gi) {
+            const float* v = w + gi * g;
+            float mn = v[0], mx = v[0];
+            for (int j = 1; j < g; ++j) {
+                mn = v[j] < mn ? v[j] : mn;
+                mx = v[j] > mx ? v[j] : mx;
+            }
+            float s = (mx - mn) / 15.0f;
+            if (s == 0 || std::isnan(s) || std::isinf(s)) {
+                s = 1;
+                mn = 0;
+            }
+            scales[gi] = s;
+            mins[gi] = mn;
+            const float inv = 1 / s;
+            for (int wi = 0; wi < g / 8; ++wi) {
+                uint32_t word = 0;
+                for (int j = 0; j < 8; ++j) {
+                    const float t = (v[wi * 8 + j] - mn) * inv;
+                    word |= uint32_t(clampl(go_round(double(t)), 0, 15)) << (4 * j);
+                }
+                std::memcpy(raw + (gi * g / 8 + wi) * 4, &word, 4);
+            }
+        }
+    });
+    meta[0] = 4;
+}
+
 }  // namespace
 
 bool pack_sizes(int fmt, int64_t rows, int64_t cols, PackSizes& out) {
@@ -327,6 +363,13 @@ bool pack_sizes(int fmt, int64_t rows, int64_t cols, PackSizes& out) {
     case FMT_Q5_1: out.raw = (n + 31) / 32 * 28; out.block_weights = 32; return true;
     case FMT_TERNARY: out.raw = (n + 15) / 16 * 4; out.scales = (n + 15) / 16; out.block_weights = 16; return true;
     case FMT_BINARY: out.raw = (n + 31) / 32 * 4; out.scales = (n + 31) / 32; out.block_weights = 32; return true;
+    case FMT_AFFINE:  // PackAffine4 with the default group of 64 (affine_pack.go:11-13)
+        if (cols % 64) return false;
+        out.raw = n / 2;
+        out.scales = out.mins = n / 64;
+        out.meta = 1;
+        out.block_weights = 64;
+        return true;
     default: break;
     }
     if (k_spec(fmt, ks)) { out.raw = (n + 255) / 256 * k_super_bytes(ks); out.block_weights = 256; return true; }
@@ -341,7 +384,8 @@ bool pack_sizes(int fmt, int64_t rows, int64_t cols, PackSizes& out) {
     return false;
 }
 
-bool pack(int fmt, const float* w, int64_t rows, int64_t cols, uint8_t* raw, float* scales, uint8_t* meta) {
+bool pack(int fmt, const float* w, int64_t rows, int64_t cols, uint8_t* raw, float* scales, float* mins,
+          uint8_t* meta) {
     PackSizes sz;
     if (!pack_sizes(fmt, rows, cols, sz)) return false;
     const int64_t n = rows * cols;
@@ -356,6 +400,7 @@ bool pack(int fmt, const float* w, int64_t rows, int64_t cols, uint8_t* raw, flo
     case FMT_Q5_1: pack_asym32(w, n, raw, 31, 28, true); return true;
     case FMT_TERNARY: pack_ternary(w, n, raw, scales); return true;
     case FMT_BINARY: pack_binary(w, n, raw, scales); return true;
+    case FMT_AFFINE: pack_affine(w, rows, cols, 64, raw, scales, mins, meta); return true;
     default: break;
     }
     if (k_spec(fmt, ks)) { pack_k(ks, w, n, raw); return true; }

@@ -214,7 +214,19 @@ bool lookup(uint64_t h, DevBlob& out) {
 }
 
 bool supported_format(int fmt) {
-    return (fmt >= FMT_Q8_0 && fmt <= FMT_BINARY) || fmt == FMT_NATIVE_TERNARY;
+    return (fmt >= FMT_Q8_0 && fmt <= FMT_AFFINE) || fmt == FMT_NATIVE_TERNARY;
+}
+
+// InferAffineBlockWeights (affine_g64.go:99-122): keep BlockWeights when the
+// scales fit it, else 64 when they fit that, else cols / (scales per row).
+int32_t infer_affine_group(int64_t rows, int64_t cols, int32_t bw, size_t n_scales) {
+    if (bw > 0 && cols % bw == 0 && int64_t(n_scales) == rows * (cols / bw)) return bw;
+    if (cols % 64 == 0 && int64_t(n_scales) == rows * (cols / 64)) return 64;
+    if (int64_t(n_scales) % rows == 0) {
+        const int64_t gpr = int64_t(n_scales) / rows;
+        if (gpr > 0 && cols % gpr == 0) return int32_t(cols / gpr);
+    }
+    return bw > 0 ? bw : 64;
 }
 
 const char* fmt_name(int f) {
@@ -233,6 +245,11 @@ int64_t need_raw(int fmt, int64_t rows, int64_t cols, int32_t bw, const uint8_t*
     const int64_t n = rows * cols;
     *need_scales = 0;
     if (fmt == FMT_NATIVE_TERNARY) return (n + 3) / 4;
+    if (fmt == FMT_AFFINE) {  // 4-bit codes, groups of bw along each row (affine_g64.go:34-47)
+        if (bw <= 0 || bw % 8 || cols % bw) return -1;
+        *need_scales = rows * (cols / bw);
+        return n / 2;
+    }
     if (fmt == FMT_BINARY && bw == 128) {
         if (cols % 128 != 0) return -1;
         *need_scales = rows * (cols / 128);
@@ -302,14 +319,14 @@ int wv_pack_sizes(int format, int64_t rows, int64_t cols, size_t* raw_len, size_
 
 int wv_pack(int format, const float* weights, int64_t rows, int64_t cols, uint8_t* raw, float* scales, float* mins,
             uint8_t* meta) {
-    (void)mins;
     PackSizes ps;
     if (!weights || !raw) return fail(WV_E_ARG, "Pack: nil buffer");
     if (rows <= 0 || cols <= 0) return fail(WV_E_SHAPE, "Pack: bad shape rows=%lld cols=%lld len=0", (long long)rows, (long long)cols);
     if (!pack_sizes(format, rows, cols, ps))
         return fail(WV_E_FORMAT, "quant: Pack not implemented for %s (native path TBD — no QAT fallback)", fmt_name(format));
-    if ((ps.scales && !scales) || (ps.meta && !meta)) return fail(WV_E_ARG, "Pack: %s needs scales/meta buffers", fmt_name(format));
-    if (!pack(format, weights, rows, cols, raw, scales, meta)) return fail(WV_E_FORMAT, "Pack: %s failed", fmt_name(format));
+    if ((ps.scales && !scales) || (ps.mins && !mins) || (ps.meta && !meta))
+        return fail(WV_E_ARG, "Pack: %s needs scales/mins/meta buffers", fmt_name(format));
+    if (!pack(format, weights, rows, cols, raw, scales, mins, meta)) return fail(WV_E_FORMAT, "Pack: %s failed", fmt_name(format));
     return WV_OK;
 }
 
@@ -323,13 +340,21 @@ int wv_pack_native_ternary(const float* weights, int64_t n, uint8_t* codes, floa
 int wv_blob_upload(int format, int64_t rows, int64_t cols, int32_t block_weights, const uint8_t* raw, size_t raw_len,
                    const float* scales, size_t n_scales, const float* mins, size_t n_mins, const uint8_t* meta,
                    size_t n_meta, float tensor_scale, uint64_t* handle) {
-    (void)mins;
-    (void)n_mins;
     if (!handle || !raw) return fail(WV_E_ARG, "wv_blob_upload: nil blob");
     if (rows <= 0 || cols <= 0)
         return fail(WV_E_SHAPE, "wv_blob_upload: bad shape rows=%lld cols=%lld", (long long)rows, (long long)cols);
     if (!supported_format(format))
         return fail(WV_E_FORMAT, "quant: MatVec not implemented for %s (native path TBD — no QAT fallback)", fmt_name(format));
+    if (format == FMT_AFFINE) {
+        // The fused path takes 4-bit codes only and every group's scale and
+        // bias (EnsureAffineSIMDCache, k_iq_simd.go:187-215; simd_k_iq.go:57-67).
+        const int bits = n_meta > 0 && meta[0] > 0 ? meta[0] : 4;
+        if (bits != 4) return fail(WV_E_FORMAT, "wv_blob_upload: AffinePacked bits=%d not supported (want 4)", bits);
+        block_weights = infer_affine_group(rows, cols, block_weights, n_scales);
+        const int64_t groups = block_weights > 0 && cols % block_weights == 0 ? rows * (cols / block_weights) : 0;
+        if (!mins || int64_t(n_mins) < groups)
+            return fail(WV_E_SHAPE, "wv_blob_upload: AffinePacked needs %lld mins, got %zu", (long long)groups, n_mins);
+    }
     int64_t need_sc = 0;
     const int64_t need = need_raw(format, rows, cols, block_weights, meta, n_meta, &need_sc);
     if (need < 0) return fail(WV_E_SHAPE, "wv_blob_upload: %s cannot hold rows=%lld cols=%lld", fmt_name(format), (long long)rows, (long long)cols);
@@ -354,7 +379,7 @@ int wv_blob_upload(int format, int64_t rows, int64_t cols, int32_t block_weights
     Image img;
     const bool raw_only = force_raw();
     RplOffsets ro;
-    size_t o_codes = 0, o_raw = 0, o_sc = 0;
+    size_t o_codes = 0, o_raw = 0, o_sc = 0, o_mn = 0;
     if (format == FMT_NATIVE_TERNARY) {
         b.layout = LAYOUT_TERNARY_I8;
         if (cols > 32768) return fail(WV_E_SHAPE, "wv_blob_upload: native ternary cols %lld > 32768", (long long)cols);
@@ -376,6 +401,11 @@ int wv_blob_upload(int format, int64_t rows, int64_t cols, int32_t block_weights
             if (n_meta >= 2) { is.bits = meta[0]; is.sg = meta[1]; }
             b.iq_bits = is.bits;
             b.iq_sg = is.sg;
+        }
+        if (format == FMT_AFFINE) {
+            b.n_mins = rows * (cols / block_weights);
+            o_mn = img.add(size_t(b.n_mins) * 4);
+            std::memcpy(img.bytes.data() + o_mn, mins, size_t(b.n_mins) * 4);
         }
         if (scales && n_scales) {
             o_sc = img.add(n_scales * 4);
@@ -409,6 +439,7 @@ int wv_blob_upload(int format, int64_t rows, int64_t cols, int32_t block_weights
     if (b.layout == LAYOUT_RAW) {
         b.raw = base + o_raw;
         b.scales = b.n_scales ? reinterpret_cast<const float*>(base + o_sc) : nullptr;
+        b.mins = b.n_mins ? reinterpret_cast<const float*>(base + o_mn) : nullptr;
     } else if (b.layout == LAYOUT_TERNARY_I8) {
         b.codes = base + o_codes;
     } else {

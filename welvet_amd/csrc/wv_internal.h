@@ -70,7 +70,8 @@ struct PackSizes {
     int32_t block_weights = 0;
 };
 bool pack_sizes(int fmt, int64_t rows, int64_t cols, PackSizes& out);
-bool pack(int fmt, const float* w, int64_t rows, int64_t cols, uint8_t* raw, float* scales, uint8_t* meta);
+bool pack(int fmt, const float* w, int64_t rows, int64_t cols, uint8_t* raw, float* scales, float* mins,
+          uint8_t* meta);
 void pack_native_ternary(const float* w, int64_t n, uint8_t* codes, float* scale);
 
 // ---- device residency ----
@@ -142,6 +143,8 @@ struct DevBlob {
     int64_t raw_len = 0;
     const float* scales = nullptr;
     int64_t n_scales = 0;
+    const float* mins = nullptr;  // AffinePacked biases (Blob.Mins), one per group of block_weights
+    int64_t n_mins = 0;
     int iq_bits = 0, iq_sg = 0;  // Meta[0], Meta[1] for IQ (iq.go:187-190)
     // LAYOUT_TERNARY_I8
     const uint8_t* codes = nullptr;
