@@ -98,6 +98,20 @@ int wv_blob_upload(int format, int64_t rows, int64_t cols, int32_t block_weights
                    const uint8_t *meta, size_t n_meta,
                    float tensor_scale, uint64_t *handle);
 
+/* Uploads a packed blob straight from its ENTITY wire bytes, replacing
+ * entity.DecodePackedBlob (model/entity/packed.go:37-76; the same layout as
+ * weights.DecodePackedWire, weights/packed_wire.go:57-110) plus the host SIMD
+ * cache build: wire = u32 ns | u32 nm | u32 nr | f32 scales[ns] |
+ * f32 mins[nm] | raw[nr], little-endian, no padding. The wire carries no
+ * Meta or BlockWeights: IQ formats take their default bit width and scale
+ * group, BinaryPacked infers g128 from the scale count
+ * (InferBinaryBlockWeights, quant/binary_g128.go:79-94) and AffinePacked its
+ * group (InferAffineBlockWeights, quant/affine_g64.go:99-122). Errors match
+ * the reference's wording: "packed wire too short", "packed wire truncated
+ * (need N, have M)". FormatNone payloads (raw f32) are not packed blobs. */
+int wv_blob_upload_wire(int format, int64_t rows, int64_t cols, const uint8_t *wire, size_t wire_len,
+                        uint64_t *handle);
+
 /* Releases the device copy (host_release.go:15 analogue for the device side). */
 int wv_blob_free(uint64_t handle);
 

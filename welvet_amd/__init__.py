@@ -31,7 +31,7 @@ WV_E = {-1: "ARG", -2: "SHAPE", -3: "FORMAT", -4: "OOM", -5: "HIP", -6: "NODEV",
 # Every symbol include/welvet_hip.h declares.
 EXPORTS = (
     "wv_init", "wv_last_error", "wv_version", "wv_pack_sizes", "wv_pack",
-    "wv_pack_native_ternary", "wv_blob_upload", "wv_blob_free", "wv_blob_info",
+    "wv_pack_native_ternary", "wv_blob_upload", "wv_blob_upload_wire", "wv_blob_free", "wv_blob_info",
     "wv_matvec", "wv_matvec_dev", "wv_ternary_acc_dev", "wv_matvec_t",
     "wv_matvec_t_dev", "wv_matmul", "wv_matmul_dev", "wv_sync",
     "wv_decoder_create", "wv_decoder_set_layer", "wv_decoder_set_output", "wv_decoder_set_kv",
@@ -67,6 +67,7 @@ def lib():
     L.wv_pack_native_ternary.argtypes = [_P, _I64, _P, _P]
     L.wv_blob_upload.argtypes = [ctypes.c_int, _I64, _I64, ctypes.c_int32, _P, _SZ, _P, _SZ, _P, _SZ, _P, _SZ,
                                  ctypes.c_float, _P]
+    L.wv_blob_upload_wire.argtypes = [ctypes.c_int, _I64, _I64, _P, _SZ, _P]
     L.wv_blob_free.argtypes = [ctypes.c_uint64]
     L.wv_blob_info.argtypes = [ctypes.c_uint64, _P, _P, _P, _P, _P]
     L.wv_matvec.argtypes = [ctypes.c_uint64, _P, _P, ctypes.c_int32]
@@ -177,6 +178,25 @@ class DeviceBlob:
         self.handle = h.value
         self.fmt, self.rows, self.cols = p.fmt, p.rows, p.cols
         self.packed_bytes = p.nbytes
+
+    @classmethod
+    def from_wire(cls, fmt, rows: int, cols: int, wire) -> "DeviceBlob":
+        """Uploads an ENTITY packed-blob wire (ns, nm, nr, scales, mins, raw) with
+        wv_blob_upload_wire; `wire` is any buffer (bytes, numpy, a memoryview of
+        an mmap), read in place."""
+        buf = np.frombuffer(wire, np.uint8)
+        h = ctypes.c_uint64()
+        check(lib().wv_blob_upload_wire(_fmt(fmt), int(rows), int(cols), buf.ctypes.data if buf.size else None,
+                                        buf.size, ctypes.byref(h)))
+        self = cls.__new__(cls)
+        self.handle = h.value
+        self.fmt, self.rows, self.cols = _fmt(fmt), int(rows), int(cols)
+        if buf.size >= 12:
+            ns, nm, nr = (int(v) for v in buf[:12].view("<u4"))
+            self.packed_bytes = nr + 4 * (ns + nm)
+        else:
+            self.packed_bytes = 0
+        return self
 
     def info(self):
         fmt, layout = ctypes.c_int(), ctypes.c_int()

@@ -466,6 +466,34 @@ int wv_blob_upload(int format, int64_t rows, int64_t cols, int32_t block_weights
     return WV_OK;
 }
 
+int wv_blob_upload_wire(int format, int64_t rows, int64_t cols, const uint8_t* wire, size_t wire_len,
+                        uint64_t* handle) {
+    if (!handle || !wire) return fail(WV_E_ARG, "wv_blob_upload_wire: nil wire");
+    if (format == FMT_NONE || format == FMT_NATIVE_TERNARY)
+        return fail(WV_E_FORMAT, "entity: not a packed quant blob (format=%s)", fmt_name(format));
+    if (wire_len < 12) return fail(WV_E_SHAPE, "packed wire too short");
+    uint32_t hdr[3];
+    std::memcpy(hdr, wire, 12);
+    const uint64_t ns = hdr[0], nm = hdr[1], nr = hdr[2];
+    const uint64_t need = 12 + ns * 4 + nm * 4 + nr;
+    if (wire_len < need)
+        return fail(WV_E_SHAPE, "packed wire truncated (need %llu, have %zu)", (unsigned long long)need, wire_len);
+    // The float arrays may sit at any byte offset of a mapped file: copy them out.
+    std::vector<float> sc(ns), mn(nm);
+    if (ns) std::memcpy(sc.data(), wire + 12, ns * 4);
+    if (nm) std::memcpy(mn.data(), wire + 12 + ns * 4, nm * 4);
+    const uint8_t* raw = wire + 12 + ns * 4 + nm * 4;
+    int32_t bw = 0;
+    if (format == FMT_BINARY) {
+        bw = (cols % 128 == 0 && int64_t(ns) == rows * (cols / 128)) ? 128 : 32;
+    } else if (format != FMT_AFFINE) {
+        PackSizes ps;
+        if (pack_sizes(format, rows, cols, ps)) bw = ps.block_weights;
+    }
+    return wv_blob_upload(format, rows, cols, bw, raw, size_t(nr), ns ? sc.data() : nullptr, size_t(ns),
+                          nm ? mn.data() : nullptr, size_t(nm), nullptr, 0, 0.0f, handle);
+}
+
 int wv_blob_free(uint64_t handle) {
     DevBlob b;
     {
