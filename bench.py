@@ -45,6 +45,12 @@ WORKLOADS = {
     "ternary_2560x6912": ("NativeTernary", 6912, 2560, "DTypeTernary int8 GEMV 2560->6912 b=1"),
     "ternary_6912x2560": ("NativeTernary", 2560, 6912, "DTypeTernary int8 GEMV 6912->2560 b=1"),
 }
+# Every other packed format at the headline shape (reference-layout kernels).
+WORKLOADS.update({
+    f"{f.lower()}_4096x14336": (f, 14336, 4096, f"{f} dequant-GEMV 4096->14336 b=1")
+    for f in ("Q4_0", "Q4_1", "Q5_0", "Q5_1", "Q2_K", "Q3_K", "Q5_K", "IQ1_S", "IQ2_XXS", "IQ2_XS", "IQ3_XXS",
+              "IQ3_S", "IQ4_NL", "IQ4_XS", "TernaryPacked", "BinaryPacked", "AffinePacked")
+})
 # Batched prefill through the same Dense API (wv_matmul_dev): name -> (format, rows, cols, M, description)
 PREFILL = {
     f"q4k_prefill_{i}x{o}_m{m}": ("Q4_K", o, i, m, f"Q4_K prefill GEMM {i}->{o} M={m} (fp16 MFMA)")
@@ -89,7 +95,7 @@ def cpu_baseline(packed, x, rows, cols, ternary, nbytes, budget_s, threads):
     """CPU restatement of welvet's Go/SIMD Dense path (oracle/), timed here."""
     import oracle
     op = oracle.Packed(packed.fmt if not ternary else 0, rows, cols, packed.raw, packed.scales, packed.meta,
-                       packed.block_weights)
+                       packed.block_weights, packed.mins)
     if ternary:
         t0 = time.perf_counter()
         oracle.ternary_i8_forward(packed.raw, np.float32(packed.tensor_scale), rows, cols, x)
