@@ -71,7 +71,7 @@ DECODE = {
 COPY_FETCH_SCALE = 65536.0 / 32779.5
 COPY_WRITE_SCALE = 65536.0 / 65536.0
 PMC_KIB = {
-    "q4k_4096x14336": (18932.5, 56.0),
+    "q4k_4096x14336": (18951.5, 56.0),
 }
 METRIC = "dequant-GEMV HBM GB/s (% of peak) at 4096->14336 Q4_K b=1; decode tokens/s"
 
