@@ -44,8 +44,7 @@ __global__ void __launch_bounds__(256) k_embed(const float* __restrict__ table, 
     if (ss) {  // sums of h^2 per 16 elements, for the first layer's fused RMSNorm
         const int i = blockIdx.x * 256 + threadIdx.x;
         const float v = i < hidden ? table[int64_t(t) * hidden + i] : 0.f;
-        float q = v * v;
-        for (int m = 8; m >= 1; m >>= 1) q += __shfl_xor(q, m, 64);
+        const float q = row_sum16(v * v);
         if ((threadIdx.x & 15) == 0 && i < hidden) ss[i >> 4] = q;
     }
     if (blockIdx.x == 0) {
@@ -76,7 +75,7 @@ __global__ void __launch_bounds__(1024) k_rmsnorm(const float* __restrict__ x, c
     for (int r = 0; r < R; ++r)
         s += double(xv[r].x) * xv[r].x + double(xv[r].y) * xv[r].y + double(xv[r].z) * xv[r].z +
              double(xv[r].w) * xv[r].w;
-    for (int m = 32; m >= 1; m >>= 1) s += __shfl_xor(s, m, 64);
+    s = wave_total_f64(s);
     if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
     __syncthreads();
     double tot = 0.0;

@@ -28,6 +28,7 @@
 #include <cstdint>
 #include <cstdlib>
 
+#include "wave_ops.h"
 #include "wv_internal.h"
 
 namespace wv {
@@ -294,15 +295,14 @@ __device__ __forceinline__ float store_y(const RplArgs& a, float* y, int64_t idx
 // the stored y^2 over each 16 consecutive rows ([batch][rg_count*4]).
 __device__ __forceinline__ void finish_rows(const RplArgs& a, float* y, int b, int row, bool valid, int lane, float s) {
     if (a.mode == RPL_SWIGLU) {
-        const float u = __shfl_xor(s, 1, 64);
+        const float u = quad_xor1(s);
         if (valid && !(lane & 1) && row < a.rows) y[int64_t(b) * (a.rows / 2) + row / 2] = s / (1.0f + expf(-s)) * u;
         return;
     }
     float v = 0.f;
     if (valid && row < a.rows) v = store_y(a, y, int64_t(b) * a.rows + row, s);
     if (a.ss_out) {
-        float q = v * v;
-        for (int m = 8; m >= 1; m >>= 1) q += __shfl_xor(q, m, 64);
+        const float q = row_sum16(v * v);
         if (valid && (lane & 15) == 0) a.ss_out[int64_t(b) * a.rg_count * 4 + row / 16] = q;
     }
 }
@@ -389,7 +389,7 @@ __global__ void __launch_bounds__(1024) k_gemv_rpl(RplArgs a, const float* __res
     if (a.nrm_gamma) {
         // RMSNorm of x folded in (layers/rmsnorm/cpu.go:70-85): f64 total of
         // the producer's partial sums, y = f32((x * inv) * gamma).
-        for (int m = 32; m >= 1; m >>= 1) ssp += __shfl_xor(ssp, m, 64);
+        ssp = wave_total_f64(ssp);
         const double inv = 1.0 / sqrt(ssp / double(a.nsb * 256) + a.nrm_eps);
 #pragma unroll
         for (int s = 0; s < S; ++s) {
@@ -412,8 +412,8 @@ __global__ void __launch_bounds__(1024) k_gemv_rpl(RplArgs a, const float* __res
         float* xs = xw + s * kSlice;
         const float4 xv = xv4[s];
         float gsum = (xv.x + xv.y) + (xv.z + xv.w);
-        gsum += __shfl_xor(gsum, 1, 64);
-        gsum += __shfl_xor(gsum, 2, 64);  // lanes 4g..4g+3: sum of columns 16g..16g+15
+        gsum += quad_xor1(gsum);
+        gsum += quad_xor2(gsum);  // lanes 4g..4g+3: sum of columns 16g..16g+15
         if constexpr (!P::kIntX) {
             reinterpret_cast<float4*>(xs)[lane] = xv;
             if ((lane & 3) == 0) xs[256 + (lane >> 2)] = gsum;
@@ -421,9 +421,9 @@ __global__ void __launch_bounds__(1024) k_gemv_rpl(RplArgs a, const float* __res
             // lane = 8c + q holds columns 4q..4q+3 of chunk c
             const int c = lane >> 3, q = lane & 7;
             float m = fmaxf(fmaxf(fabsf(xv.x), fabsf(xv.y)), fmaxf(fabsf(xv.z), fabsf(xv.w)));
-            m = fmaxf(m, __shfl_xor(m, 1, 64));
-            m = fmaxf(m, __shfl_xor(m, 2, 64));
-            m = fmaxf(m, __shfl_xor(m, 4, 64));
+            m = fmaxf(m, quad_xor1(m));
+            m = fmaxf(m, quad_xor2(m));
+            m = fmaxf(m, half_mirror(m));  // max over lanes 8c..8c+7
             int e = 0;
             frexpf(m, &e);
             const int sh = m > 0.f ? 22 - e : 0;  // |x| * 2^sh < 2^22
@@ -442,7 +442,8 @@ __global__ void __launch_bounds__(1024) k_gemv_rpl(RplArgs a, const float* __res
                 h16[(pl * 8 + w) * 2 + half] = uint16_t(blo);
                 h16[(pl * 8 + 4 + w) * 2 + half] = uint16_t(bhi);
             }
-            const float s0 = __shfl(gsum, lane & ~7, 64), s1 = __shfl(gsum, (lane & ~7) + 4, 64);
+            // for q == 0: this quad's column sum and the other quad's (lanes 8c+4..8c+7)
+            const float s0 = gsum, s1 = half_mirror(gsum);
             if (q == 0) {
                 float* xm = xs + c * 28 + 24;
                 xm[0] = ldexpf(1.0f, -sh) * (1.0f / 255.0f);
@@ -530,7 +531,7 @@ __global__ void __launch_bounds__(1024) k_gemv_rpl(RplArgs a, const float* __res
     uint32_t* ctr = a.counters + int64_t(b) * a.rg_count * 4 + hx;
     uint32_t old = 0;
     if (lane == 0) old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    old = __shfl(old, 0, 64);
+    old = uint32_t(__builtin_amdgcn_readlane(int(old), 0));
     if (old != uint32_t(a.ksplit - 1)) return;
     const float tsum = valid ? sum_partials(pb + row, rows_pad, a.ksplit) : 0.f;
     finish_rows(a, y, b, row, valid, lane, tsum);

@@ -59,6 +59,52 @@ __device__ __forceinline__ float wave_maximum(float f) {
     return __int_as_float(__builtin_amdgcn_readlane(v, 63));
 }
 
+// Exchanges inside a quad of lanes (quad_perm): the value of lane ^ 1 / lane ^ 2.
+__device__ __forceinline__ float quad_xor1(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xb1, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float quad_xor2(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4e, 0xf, 0xf, false));
+}
+// The value of lane 7 - (lane & 7) of the same 8-lane half row (row_half_mirror):
+// after a quad reduction, the other quad's result.
+__device__ __forceinline__ float half_mirror(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xf, 0xf, false));
+}
+
+// Sum over each 16-lane row into every lane of the row, by row_ror 8, 4, 2, 1:
+// rotating 16 lanes by 8 is lane ^ 8, and each later rotation adds the same
+// pairs as the xor butterfly (the partial sums are periodic by then), so the
+// result equals a __shfl_xor(8, 4, 2, 1) butterfly bit for bit.
+__device__ __forceinline__ float row_sum16(float v) {
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xf, 0xf, false));
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x124, 0xf, 0xf, false));
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x122, 0xf, 0xf, false));
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x121, 0xf, 0xf, false));
+    return v;
+}
+
+// f64 total over the wave on the same DPP tree (both 32-bit halves move together).
+template <int Ctrl, int RowMask = 0xf, int BankMask = 0xf>
+__device__ __forceinline__ double dpp_f64(double v) {
+    const unsigned long long b = static_cast<unsigned long long>(__double_as_longlong(v));
+    const uint32_t lo = uint32_t(dpp_i<Ctrl, RowMask, BankMask>(0, int(uint32_t(b))));
+    const uint32_t hi = uint32_t(dpp_i<Ctrl, RowMask, BankMask>(0, int(uint32_t(b >> 32))));
+    return __longlong_as_double(static_cast<long long>((static_cast<unsigned long long>(hi) << 32) | lo));
+}
+__device__ __forceinline__ double wave_total_f64(double v) {
+    v += dpp_f64<kDppRowShr1>(v);
+    v += dpp_f64<kDppRowShr2>(v);
+    v += dpp_f64<kDppRowShr4, 0xf, 0xe>(v);
+    v += dpp_f64<kDppRowShr8, 0xf, 0xc>(v);
+    v += dpp_f64<kDppRowBcast15, 0xa>(v);
+    v += dpp_f64<kDppRowBcast31, 0xc>(v);
+    const unsigned long long b = static_cast<unsigned long long>(__double_as_longlong(v));
+    const uint32_t lo = uint32_t(__builtin_amdgcn_readlane(int(uint32_t(b)), 63));
+    const uint32_t hi = uint32_t(__builtin_amdgcn_readlane(int(uint32_t(b >> 32)), 63));
+    return __longlong_as_double(static_cast<long long>((static_cast<unsigned long long>(hi) << 32) | lo));
+}
+
 // Quad transpose of bytes: lane q of each group of four holds P_q; returns to
 // lane q the dword whose byte j is byte q of P_j (quad_perm rotations).
 __device__ __forceinline__ uint32_t quad_byte_transpose(uint32_t p, int q) {
