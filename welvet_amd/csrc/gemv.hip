@@ -24,6 +24,15 @@ namespace {
 
 constexpr int kWave = 64;
 
+// WV_RAW16_KW=1|2|4 fixes the K parts of the run-vectorized kernel (tuning sweeps).
+int raw16_kw() {
+    static const int v = [] {
+        const char* e = std::getenv("WV_RAW16_KW");
+        return e && *e ? std::atoi(e) : 0;
+    }();
+    return v == 1 || v == 2 || v == 4 ? v : 0;
+}
+
 // WV_RAW16=0 forces the per-weight decoder on the reference layout (for comparisons).
 bool raw16_off() {
     static const bool off = [] {
@@ -337,53 +346,96 @@ __device__ __forceinline__ uint32_t code_at(const uint32_t* w, int k) {
     return __builtin_amdgcn_alignbit(w[wi + 1], w[wi], off) & ((1u << BITS) - 1u);
 }
 
-template <int F>
+// One block = 4 waves = 4/KW groups of R = 4 rows; the KW waves of a group
+// take interleaved runs of the same rows (K split inside the block) and
+// their row sums meet in LDS in a fixed order.
+template <int F, int U, int KW>
 __global__ void __launch_bounds__(256) k_gemv_raw16(RawArgs a, const float* __restrict__ x, float* __restrict__ y) {
     using P = RawF<F>;
     constexpr int R = 4;  // rows per wave
+    __shared__ float red[4][R];
     __shared__ float tab[16];  // IQ4_NL grid: a per-lane index into a register table would go through scratch
     if constexpr (F == FMT_IQ4_NL) {
         if (threadIdx.x < 16) tab[threadIdx.x] = kIQ4NLGrid[threadIdx.x];
         __syncthreads();
     }
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int64_t row0 = (int64_t(blockIdx.x) * 4 + wave) * R;
-    if (row0 >= a.rows) return;
+    const int kp = wave % KW;  // this wave's K part
+    const int64_t row0 = (int64_t(blockIdx.x) * (4 / KW) + wave / KW) * R;
+    if (KW == 1 && row0 >= a.rows) return;  // with KW > 1 every wave reaches the barrier below
     const int b = blockIdx.y;
     const float* xb = x + int64_t(b) * a.cols;
     const int64_t nsg = a.cols >> 4;
     int64_t rowc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) rowc[r] = min<int64_t>(row0 + r, a.rows - 1);
+    // U runs per lane in flight: every load of U consecutive runs (lane, lane+64, ...)
+    // is issued before any of them is used; indices past the row are clamped
+    // to its last run (read, not used), so the load phase has no branches.
+    constexpr int NB = 2 * P::BITS, NW = (NB + 2 + 3) / 4;
     float acc[R] = {};
-    for (int64_t s = lane; s < nsg; s += 64) {
-        const int64_t c0 = s << 4;
-        const float4* xp = reinterpret_cast<const float4*>(xb + c0);
-        const float4 x0 = xp[0], x1 = xp[1], x2 = xp[2], x3 = xp[3];
-        const float xv[16] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w,
-                              x2.x, x2.y, x2.z, x2.w, x3.x, x3.y, x3.z, x3.w};
-        Grp g[R];
-        uint32_t w[R][(2 * P::BITS + 3) / 4];
+    for (int64_t s0 = kp * 64 + lane; s0 < nsg; s0 += 64 * KW * U) {
+        float4 xq[U][4];
+        Grp g[U][R];
+        uint32_t dw[U][R][NW], mis[U][R];
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            g[r] = P::grp(a, rowc[r], rowc[r] * a.cols + c0);
-            load_run<P::BITS>(g[r].codes, w[r]);
+        for (int u = 0; u < U; ++u) {
+            const int64_t c0 = min<int64_t>(s0 + 64 * KW * u, nsg - 1) << 4;
+            const float4* xp = reinterpret_cast<const float4*>(xb + c0);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) xq[u][k] = xp[k];
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                g[u][r] = P::grp(a, rowc[r], rowc[r] * a.cols + c0);
+                const uintptr_t ad = reinterpret_cast<uintptr_t>(g[u][r].codes);
+                const uint32_t* base = reinterpret_cast<const uint32_t*>(ad & ~uintptr_t(3));
+                mis[u][r] = uint32_t(ad & 3);
+#pragma unroll
+                for (int i = 0; i < NW; ++i) dw[u][r][i] = base[i];
+            }
         }
-        float xs = 0.f;
 #pragma unroll
-        for (int k = 0; k < 16; ++k) xs += xv[k];
+        for (int u = 0; u < U; ++u) {
+            if (s0 + 64 * KW * u >= nsg) continue;
+            const float xv[16] = {xq[u][0].x, xq[u][0].y, xq[u][0].z, xq[u][0].w, xq[u][1].x, xq[u][1].y,
+                                  xq[u][1].z, xq[u][1].w, xq[u][2].x, xq[u][2].y, xq[u][2].z, xq[u][2].w,
+                                  xq[u][3].x, xq[u][3].y, xq[u][3].z, xq[u][3].w};
+            float xs = 0.f;
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            float d = 0.f;
+            for (int k = 0; k < 16; ++k) xs += xv[k];
 #pragma unroll
-            for (int k = 0; k < 16; ++k) d = fmaf(P::fq(code_at<P::BITS>(w[r], k), tab), xv[k], d);
-            acc[r] = fmaf(g[r].alpha, d, fmaf(g[r].beta, xs, acc[r]));
+            for (int r = 0; r < R; ++r) {
+                uint32_t w[(NB + 3) / 4];  // the run's bytes realigned to a dword boundary
+#pragma unroll
+                for (int i = 0; i < (NB + 3) / 4; ++i)
+                    w[i] = __builtin_amdgcn_alignbyte(i + 1 < NW ? dw[u][r][i + 1] : 0u, dw[u][r][i], mis[u][r]);
+                float d = 0.f;
+#pragma unroll
+                for (int k = 0; k < 16; ++k) d = fmaf(P::fq(code_at<P::BITS>(w, k), tab), xv[k], d);
+                acc[r] = fmaf(g[u][r].alpha, d, fmaf(g[u][r].beta, xs, acc[r]));
+            }
         }
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const float v = wave_sum(acc[r]);
-        if (lane == 0 && row0 + r < a.rows) y[int64_t(b) * a.rows + row0 + r] = v;
+        if (KW == 1) {
+            if (lane == 0 && row0 + r < a.rows) y[int64_t(b) * a.rows + row0 + r] = v;
+        } else if (lane == 0) {
+            red[wave][r] = v;
+        }
+    }
+    if constexpr (KW > 1) {
+        __syncthreads();
+        const int t = threadIdx.x;
+        if (t < (4 / KW) * R) {
+            const int grp = t / R, r = t % R;
+            float v = 0.f;
+#pragma unroll
+            for (int k = 0; k < KW; ++k) v += red[grp * KW + k][r];
+            const int64_t row = (int64_t(blockIdx.x) * (4 / KW) + grp) * R + r;
+            if (row < a.rows) y[int64_t(b) * a.rows + row] = v;
+        }
     }
 }
 
@@ -629,8 +681,23 @@ bool raw16_ok(const DevBlob& b) {
 template <int F>
 int launch_raw(const DevBlob& b, const float* x, float* y, int batch, hipStream_t s) {
     if (raw16_ok<F>(b)) {
-        dim3 grid(unsigned((b.rows + 15) / 16), unsigned(batch));
-        hipLaunchKernelGGL(k_gemv_raw16<F>, grid, dim3(256), 0, s, raw_args(b), x, y);
+        // IQ4_NL's grid lookups (LDS) overlap the next runs' loads; for the
+        // others the extra registers of 4 runs in flight cost more than they hide.
+        constexpr int U = F == FMT_IQ4_NL ? 4 : 1;
+        // K parts per row group (measured at 4096->14336): the fewest that give
+        // about 4 waves per SIMD, never more parts than the row has runs of 64;
+        // IQ4_NL's 4-run ring already holds as many registers as a SIMD has.
+        const int64_t quads = (b.rows + 3) / 4, nsg = b.cols / 16;
+        int kw = raw16_kw();
+        if (kw <= 0) kw = U > 1 || quads >= 4096 ? 1 : (quads * 2 >= 4096 ? 2 : 4);
+        while (kw > 1 && nsg < 64 * kw) kw /= 2;
+        const dim3 g(unsigned((quads * kw + 3) / 4), unsigned(batch));
+        if (kw == 4)
+            hipLaunchKernelGGL((k_gemv_raw16<F, U, 4>), g, dim3(256), 0, s, raw_args(b), x, y);
+        else if (kw == 2)
+            hipLaunchKernelGGL((k_gemv_raw16<F, U, 2>), g, dim3(256), 0, s, raw_args(b), x, y);
+        else
+            hipLaunchKernelGGL((k_gemv_raw16<F, U, 1>), g, dim3(256), 0, s, raw_args(b), x, y);
         return int(hipGetLastError());
     }
     dim3 grid(unsigned((b.rows + 3) / 4), unsigned(batch));
