@@ -4,8 +4,10 @@
 // (forwardSIMDBlockFused, layers/dense/simd_block.go:17-39), within the 2e-3
 // tolerance of an fp16 contraction.
 //
-// X is first converted once to fp16 (k_x_f16), so the GEMM streams half the
-// bytes for the operand every N-tile re-reads and spends no VALU on it. Global
+// For token tiles of 64 and more, X is first converted once to fp16
+// (k_x_f16), so the GEMM streams half the bytes for the operand every N-tile
+// re-reads and spends no VALU on it. A 32-token tile reads X as f32 and packs
+// it while staging instead (one launch less; its X traffic is small). Global
 // loads run D K-steps ahead of use in a register ring: a step holds only 64
 // columns, so one step of look-ahead would expose a full memory latency per
 // step.
@@ -66,7 +68,8 @@ __device__ __forceinline__ uint4 dequant8(uint32_t v, half2v sc, half2v mn) {
 
 struct GemmArgs {
     RplArgs w;
-    const uint4* xh;  // [M][K/8] fp16 8-column blocks in permuted k order
+    const uint4* xh;  // [M][K/8] fp16 8-column blocks in permuted k order (BM >= 64)
+    const float* x;   // [M][K] f32, packed while staged (BM == 32)
     float* y;         // [M][rows] (splits == 1) or partials [split][M][rows]
     int M, K;
     int sb_per_split;
@@ -82,6 +85,7 @@ __global__ void __launch_bounds__(256) k_x_f16(const float4* __restrict__ x, uin
 
 template <int BM, int WM, int D>
 __global__ void __launch_bounds__(256) k_gemm_q4k(GemmArgs ga) {
+    constexpr bool kXF32 = BM == 32;
     constexpr int WN = 4 / WM;
     constexpr int TM = BM / WM / 32, TN = BN / WN / 32;
     constexpr int XB = BM * (BK / 8) / 256;  // 8-column X blocks per thread per K-step
@@ -109,7 +113,8 @@ __global__ void __launch_bounds__(256) k_gemm_q4k(GemmArgs ga) {
         uint4 c;
         uint32_t meta;
         float2 dd;
-        uint4 xv[XB];
+        uint4 xv[XB];  // fp16 block, or (f32 X) columns 0..3 as bits
+        float4 xh[kXF32 ? XB : 1];  // (f32 X) columns 4..7
     };
     auto load = [&](int s, Regs& r) {
         const int sb = sb0 + s / 4, j = 2 * (s & 3) + jj;
@@ -121,7 +126,13 @@ __global__ void __launch_bounds__(256) k_gemm_q4k(GemmArgs ga) {
 #pragma unroll
         for (int i = 0; i < XB; ++i) {
             const int f = t + 256 * i, m = min(mblk * BM + f / 8, ga.M - 1);
-            r.xv[i] = ga.xh[int64_t(m) * kb8 + k8 + f % 8];
+            if constexpr (kXF32) {
+                const float4* xp = reinterpret_cast<const float4*>(ga.x + (int64_t(m) * kb8 + k8 + f % 8) * 8);
+                r.xv[i] = __builtin_bit_cast(uint4, xp[0]);
+                r.xh[i] = xp[1];
+            } else {
+                r.xv[i] = ga.xh[int64_t(m) * kb8 + k8 + f % 8];
+            }
         }
     };
     auto store = [&](const Regs& r, int buf) {
@@ -139,7 +150,12 @@ __global__ void __launch_bounds__(256) k_gemm_q4k(GemmArgs ga) {
 #pragma unroll
         for (int i = 0; i < XB; ++i) {
             const int f = t + 256 * i;
-            *reinterpret_cast<uint4*>(&xs[buf][(f / 8) * LDK + 8 * (f % 8)]) = r.xv[i];
+            uint4 v = r.xv[i];
+            if constexpr (kXF32) {  // k order [0,4,1,5,2,6,3,7], as the nibble extraction pairs W
+                const float4 lo = __builtin_bit_cast(float4, r.xv[i]), hi = r.xh[i];
+                v = make_uint4(pack_h2(lo.x, hi.x), pack_h2(lo.y, hi.y), pack_h2(lo.z, hi.z), pack_h2(lo.w, hi.w));
+            }
+            *reinterpret_cast<uint4*>(&xs[buf][(f / 8) * LDK + 8 * (f % 8)]) = v;
         }
     };
 
@@ -239,27 +255,34 @@ void gemm_plan(const DevBlob& b, int M, int& bm, int& splits, int& sb_per_split)
     splits = (a.nsb + sb_per_split - 1) / sb_per_split;
 }
 
-// Scratch floats: the fp16 copy of X (M*K halves) followed by the split-K partials.
+// Scratch floats: the fp16 copy of X (M*K halves, token tiles of 64 and more)
+// followed by the split-K partials.
 size_t gemm_scratch_floats(const DevBlob& b, int M) {
     int bm = 0, splits = 1, per = 0;
     gemm_plan(b, M, bm, splits, per);
-    const size_t xh = (size_t(M) * size_t(b.cols) / 2 + 63) / 64 * 64;
+    const size_t xh = bm == 32 ? 0 : (size_t(M) * size_t(b.cols) / 2 + 63) / 64 * 64;
     return xh + (splits > 1 ? size_t(splits) * size_t(M) * size_t(b.rows) : 0);
 }
 
 int launch_gemm(const DevBlob& b, const float* d_x, float* d_y, int M, void* stream, float* d_scratch) {
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if (!gemm_supported(b) || !d_scratch) return int(hipErrorInvalidValue);
+    if (!gemm_supported(b)) return int(hipErrorInvalidValue);
     int bm = 0, splits = 1, per = 0;
     gemm_plan(b, M, bm, splits, per);
-    const int64_t n8 = int64_t(M) * b.cols / 8;
-    uint4* xh = reinterpret_cast<uint4*>(d_scratch);
-    float* part = d_scratch + (size_t(M) * size_t(b.cols) / 2 + 63) / 64 * 64;
-    hipLaunchKernelGGL(k_x_f16, dim3(unsigned((n8 + 255) / 256)), dim3(256), 0, s, reinterpret_cast<const float4*>(d_x),
-                       xh, n8);
+    if (gemm_scratch_floats(b, M) && !d_scratch) return int(hipErrorInvalidValue);
+    uint4* xh = nullptr;
+    float* part = d_scratch;
+    if (bm != 32) {
+        const int64_t n8 = int64_t(M) * b.cols / 8;
+        xh = reinterpret_cast<uint4*>(d_scratch);
+        part = d_scratch + (size_t(M) * size_t(b.cols) / 2 + 63) / 64 * 64;
+        hipLaunchKernelGGL(k_x_f16, dim3(unsigned((n8 + 255) / 256)), dim3(256), 0, s,
+                           reinterpret_cast<const float4*>(d_x), xh, n8);
+    }
     GemmArgs ga;
     ga.w = b.rpl;
     ga.xh = xh;
+    ga.x = d_x;
     ga.y = splits > 1 ? part : d_y;
     ga.M = M;
     ga.K = int(b.cols);
