@@ -454,13 +454,24 @@ __global__ void __launch_bounds__(256) k_gemvt_raw(RawArgs a, const float* __res
     part[(int64_t(b) * gridDim.y + split) * a.cols + c] = acc;
 }
 
-__global__ void __launch_bounds__(256) k_gemvt_reduce(const float* __restrict__ part, float* __restrict__ gx,
+__global__ void __launch_bounds__(64) k_gemvt_reduce(const float* __restrict__ part, float* __restrict__ gx,
                                                      int64_t cols, int nsplit) {
-    const int64_t c = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    const int64_t c = int64_t(blockIdx.x) * 64 + threadIdx.x;
     const int b = blockIdx.y;
     if (c >= cols) return;
+    // Partials are added in split order; each group of 8 loads is issued
+    // before any of them is added, so the latency is paid once per group.
+    const float* p = part + int64_t(b) * nsplit * cols + c;
     float s = 0.0f;
-    for (int k = 0; k < nsplit; ++k) s += part[(int64_t(b) * nsplit + k) * cols + c];
+    int k = 0;
+    for (; k + 8 <= nsplit; k += 8) {
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = p[int64_t(k + j) * cols];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) s += v[j];
+    }
+    for (; k < nsplit; ++k) s += p[int64_t(k) * cols];
     gx[int64_t(b) * cols + c] += s;
 }
 
@@ -710,7 +721,7 @@ int launch_raw_t(const DevBlob& b, const float* gy, float* gx, int batch, hipStr
     const int rps = int((b.rows + nsplit - 1) / nsplit);
     dim3 grid(unsigned((b.cols + 255) / 256), unsigned(nsplit), unsigned(batch));
     hipLaunchKernelGGL(k_gemvt_raw<F>, grid, dim3(256), 0, s, raw_args(b), gy, part, rps);
-    hipLaunchKernelGGL(k_gemvt_reduce, dim3(unsigned((b.cols + 255) / 256), unsigned(batch)), dim3(256), 0, s, part,
+    hipLaunchKernelGGL(k_gemvt_reduce, dim3(unsigned((b.cols + 63) / 64), unsigned(batch)), dim3(64), 0, s, part,
                        gx, b.cols, nsplit);
     return int(hipGetLastError());
 }
@@ -829,7 +840,7 @@ int launch_matvec(const DevBlob& b, const float* d_x, float* d_y, int batch, voi
 }
 
 void launch_gemvt_reduce(const float* part, float* gx, int64_t cols, int nsplit, int batch, void* stream) {
-    hipLaunchKernelGGL(k_gemvt_reduce, dim3(unsigned((cols + 255) / 256), unsigned(batch)), dim3(256), 0,
+    hipLaunchKernelGGL(k_gemvt_reduce, dim3(unsigned((cols + 63) / 64), unsigned(batch)), dim3(64), 0,
                        static_cast<hipStream_t>(stream), part, gx, cols, nsplit);
 }
 

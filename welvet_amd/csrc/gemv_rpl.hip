@@ -795,7 +795,7 @@ struct TQ4 : RplQ4 {
 
 template <class P, int GP>
 __global__ void __launch_bounds__(256) k_gemvt_rpl(RplArgs a, const float* __restrict__ gy, float* __restrict__ gx,
-                                                  float* __restrict__ part, uint32_t* __restrict__ tickets) {
+                                                  float* __restrict__ part) {
     const int jp = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int sb = blockIdx.x, slice = blockIdx.y, b = blockIdx.z;
@@ -876,22 +876,10 @@ __global__ void __launch_bounds__(256) k_gemvt_rpl(RplArgs a, const float* __res
         gxb[col] += total;
         return;
     }
-    // Several slices: publish this slice's partial through cache-bypassing
-    // agent-scope stores, then the last block of this (super-block, batch
-    // row) to arrive adds the slices in slice order and resets the ticket.
-    float* pb = part + int64_t(b) * nslices * cols;
-    __hip_atomic_store(pb + int64_t(slice) * cols + col, total, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __builtin_amdgcn_s_waitcnt(0);
-    __shared__ uint32_t is_last;
-    __syncthreads();
-    uint32_t* tk = tickets + int64_t(b) * a.nsb + sb;
-    if (threadIdx.x == 0)
-        is_last = __hip_atomic_fetch_add(tk, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == uint32_t(nslices - 1);
-    __syncthreads();
-    if (!is_last) return;
-    gxb[col] += sum_partials<32>(pb + col, cols, nslices);
-    if (threadIdx.x == 0) __hip_atomic_store(tk, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // Several slices: store this slice's partial; a separate launch adds the
+    // slices in slice order (a last-arriving-block tail costs more here than
+    // the extra launch: its ticket round trips bypass the caches).
+    part[(int64_t(b) * nslices + slice) * cols + col] = total;
 }
 
 // Row-group slices for `batch` rows: about 512 blocks; each slice takes GP
@@ -921,7 +909,8 @@ int launch_rpl_tr(const DevBlob& bl, const float* gy, float* gx, int batch, hipS
         auto kern = g_per == 1 ? k_gemvt_rpl<P, 1> : g_per == 2 ? k_gemvt_rpl<P, 2> : g_per == 4 ? k_gemvt_rpl<P, 4> : k_gemvt_rpl<P, 8>;
         dim3 grid(unsigned(a.nsb), unsigned(slices), unsigned(nb));
         hipLaunchKernelGGL(kern, grid, dim3(256), 0, s, a, gy + int64_t(b0) * a.rows, gx + int64_t(b0) * cols,
-                           bl.rpl_t_partial, bl.rpl_t_tickets);
+                           bl.rpl_t_partial);
+        if (slices > 1) launch_gemvt_reduce(bl.rpl_t_partial, gx + int64_t(b0) * cols, cols, slices, nb, s);
     }
     return int(hipGetLastError());
 }

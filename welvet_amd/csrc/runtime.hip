@@ -415,7 +415,7 @@ int wv_blob_upload(int format, int64_t rows, int64_t cols, int32_t block_weights
     }
     // K-split scratch for the row-interleaved path: partial sums and arrival
     // tickets (zeroed here; the last block of each row group re-zeroes its ticket).
-    size_t o_part = 0, o_ctr = 0, o_tpart = 0, o_tctr = 0, weight_bytes = img.bytes.size();
+    size_t o_part = 0, o_ctr = 0, o_tpart = 0, weight_bytes = img.bytes.size();
     if (b.layout == LAYOUT_RPL) {
         const int64_t rg = (rows + 63) / 64, nsb = cols / 256;
         b.rpl_max_batch = 8;
@@ -429,7 +429,6 @@ int wv_blob_upload(int format, int64_t rows, int64_t cols, int32_t block_weights
         const size_t tf = rpl_t_scratch_floats(shape);
         if (tf) {
             o_tpart = img.add(tf * sizeof(float));
-            o_tctr = img.add(size_t(kRplTMaxBatch) * nsb * sizeof(uint32_t));
         }
     }
     rc = upload_image(img, b);
@@ -456,7 +455,6 @@ int wv_blob_upload(int format, int64_t rows, int64_t cols, int32_t block_weights
         r.ksplit = 1;
         if (o_tpart) {
             b.rpl_t_partial = reinterpret_cast<float*>(base + o_tpart);
-            b.rpl_t_tickets = reinterpret_cast<uint32_t*>(base + o_tctr);
         }
     }
     std::lock_guard<std::mutex> lk(g_mu);

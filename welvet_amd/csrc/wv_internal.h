@@ -153,7 +153,6 @@ struct DevBlob {
     int rpl_max_split = 1;  // capacity of rpl.partial per batch row
     int rpl_max_batch = 1;  // batch rows one split launch can carry
     float* rpl_t_partial = nullptr;    // MatVecT slice partials [batch][slice][cols]
-    uint32_t* rpl_t_tickets = nullptr;  // MatVecT arrival tickets [batch][nsb], zero between launches
     void* base = nullptr;   // allocation owner
     size_t device_bytes = 0;  // weight bytes (excludes scratch)
 };
@@ -175,7 +174,7 @@ int rpl_fuse_pairs(const DevBlob& a, const DevBlob& b, DevBlob& out, void* strea
 bool gemm_supported(const DevBlob& b);
 size_t gemm_scratch_floats(const DevBlob& b, int M);
 int launch_gemm(const DevBlob& b, const float* d_x, float* d_y, int M, void* stream, float* d_scratch);
-// MatVecT on LAYOUT_RPL uses the blob's own scratch (rpl_t_partial / rpl_t_tickets).
+// MatVecT on LAYOUT_RPL uses the blob's own scratch (rpl_t_partial).
 int launch_rpl_matvec_t(const DevBlob& b, const float* d_gy, float* d_gx, int batch, void* stream);
 // Partial floats that scratch needs (batch rows are taken kRplTMaxBatch per launch).
 size_t rpl_t_scratch_floats(const RplArgs& a);
