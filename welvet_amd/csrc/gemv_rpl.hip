@@ -259,24 +259,6 @@ struct RplQ4 {  // w = scale * q, q signed nibble; q ^ 8 = q + 8
     }
 };
 
-// sum_{k<n} p[k*stride], k ascending, read with cache-bypassing agent-scope
-// loads issued B at a time (so their latencies overlap) and added in order.
-template <int B = 8>
-__device__ __forceinline__ float sum_partials(const float* p, int64_t stride, int n) {
-    float t = 0.f;
-    int k = 0;
-    for (; k + B <= n; k += B) {
-        float v[B];
-#pragma unroll
-        for (int i = 0; i < B; ++i)
-            v[i] = __hip_atomic_load(p + int64_t(k + i) * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-#pragma unroll
-        for (int i = 0; i < B; ++i) t += v[i];
-    }
-    for (; k < n; ++k) t += __hip_atomic_load(p + int64_t(k) * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return t;
-}
-
 // Writes one output of the forward kernel under the launch's epilogue mode
 // and returns the stored value.
 __device__ __forceinline__ float store_y(const RplArgs& a, float* y, int64_t idx, float s) {
@@ -519,23 +501,33 @@ __global__ void __launch_bounds__(1024) k_gemv_rpl(RplArgs a, const float* __res
         finish_rows(a, y, b, row, valid, lane, sum);
         return;
     }
-    // K split across gridDim.y blocks: publish the partial, take a ticket.
-    // Partials and tickets move only through agent-scope relaxed atomics
-    // (cache-bypassing sc1 accesses on gfx950), ordered by a wave-local wait
-    // for the stores before the ticket, so no L2 writeback/invalidate is needed.
+    // K split across gridDim.y blocks: store the partial; k_rpl_ksum adds the
+    // splits and applies the epilogue in a second launch.
     const int64_t rows_pad = int64_t(a.rg_count) * 64;
-    float* pb = a.partial + int64_t(b) * a.ksplit * rows_pad;
-    if (valid) __hip_atomic_store(pb + int64_t(ks) * rows_pad + row, sum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __builtin_amdgcn_s_waitcnt(0);
-    uint32_t* ctr = a.counters + int64_t(b) * a.rg_count * 4 + hx;
-    uint32_t old = 0;
-    if (lane == 0) old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    old = uint32_t(__builtin_amdgcn_readlane(int(old), 0));
-    if (old != uint32_t(a.ksplit - 1)) return;
-    const float tsum = valid ? sum_partials(pb + row, rows_pad, a.ksplit) : 0.f;
-    finish_rows(a, y, b, row, valid, lane, tsum);
-    if (lane == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (valid) a.partial[(int64_t(b) * a.ksplit + ks) * rows_pad + row] = sum;
+}
+
+// Tail of a K-split forward launch: one wave per (64-row group, batch row)
+// adds the ksplit partials in split order (8 loads issued before each group
+// of adds) and applies the launch's epilogue. A last-arriving-block tail in
+// the forward kernel instead costs more: its ticket and partials must bypass
+// the caches, about 1.5 us per round trip on MI355X.
+__global__ void __launch_bounds__(64) k_rpl_ksum(RplArgs a, float* __restrict__ y) {
+    const int rg = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
+    const int64_t rows_pad = int64_t(a.rg_count) * 64;
+    const int row = rg * 64 + lane;
+    const float* p = a.partial + int64_t(b) * a.ksplit * rows_pad + row;
+    float s = 0.f;
+    int k = 0;
+    for (; k + 8 <= a.ksplit; k += 8) {
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = p[int64_t(k + j) * rows_pad];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) s += v[j];
+    }
+    for (; k < a.ksplit; ++k) s += p[int64_t(k) * rows_pad];
+    finish_rows(a, y, b, row, true, lane, s);
 }
 
 // Launch-geometry overrides for tuning sweeps, read once per process.
@@ -654,6 +646,7 @@ int launch_rpl_t(const DevBlob& bl, const float* x, float* y, int batch, hipStre
         default: launch_rpl_ls<P, 4, 4>(ab, p, grid, lds, s, xb, yb); break;
         }
         if (p.ksplit == 1) break;  // one launch covers every batch row
+        hipLaunchKernelGGL(k_rpl_ksum, dim3(unsigned(a.rg_count), unsigned(nb)), dim3(64), 0, s, ab, yb);
     }
     return int(hipGetLastError());
 }
@@ -974,7 +967,7 @@ __global__ void __launch_bounds__(256) k_rpl_pairs(uint8_t* __restrict__ dst, co
 }
 
 struct FusedLayout {
-    size_t codes, hi, meta, dd, part, ctr, total, weights;
+    size_t codes, hi, meta, dd, part, total, weights;
 };
 FusedLayout fused_layout(const RplItems& it, int64_t rg, int64_t nsb, int max_batch, int max_split) {
     FusedLayout f{};
@@ -990,7 +983,6 @@ FusedLayout fused_layout(const RplItems& it, int64_t rg, int64_t nsb, int max_ba
     f.dd = it.db ? add(per * it.db) : 0;
     f.weights = f.total;
     f.part = add(size_t(max_batch) * max_split * rg * 64 * sizeof(float));
-    f.ctr = add(size_t(max_batch) * rg * 4 * sizeof(uint32_t));
     return f;
 }
 
@@ -1012,7 +1004,6 @@ int finish_fused(const DevBlob& proto, int64_t rows, int64_t rg, const FusedLayo
     r.meta = base + f.meta;
     r.dd = f.dd ? reinterpret_cast<const float2_t*>(base + f.dd) : nullptr;
     r.partial = reinterpret_cast<float*>(base + f.part);
-    r.counters = reinterpret_cast<uint32_t*>(base + f.ctr);
     r.rows = int(rows);
     r.nsb = proto.rpl.nsb;
     r.rg_count = int(rg);

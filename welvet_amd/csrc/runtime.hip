@@ -413,15 +413,14 @@ int wv_blob_upload(int format, int64_t rows, int64_t cols, int32_t block_weights
             b.n_scales = int64_t(n_scales);
         }
     }
-    // K-split scratch for the row-interleaved path: partial sums and arrival
-    // tickets (zeroed here; the last block of each row group re-zeroes its ticket).
-    size_t o_part = 0, o_ctr = 0, o_tpart = 0, weight_bytes = img.bytes.size();
+    // K-split scratch for the row-interleaved path: forward partial sums
+    // [batch][split][rows] and MatVecT slice partials.
+    size_t o_part = 0, o_tpart = 0, weight_bytes = img.bytes.size();
     if (b.layout == LAYOUT_RPL) {
         const int64_t rg = (rows + 63) / 64, nsb = cols / 256;
         b.rpl_max_batch = 8;
         b.rpl_max_split = int(std::max<int64_t>(1, (nsb + 3) / 4));
         o_part = img.add(size_t(b.rpl_max_batch) * b.rpl_max_split * rg * 64 * sizeof(float));
-        o_ctr = img.add(size_t(b.rpl_max_batch) * rg * 4 * sizeof(uint32_t));  // per (row group, row subgroup)
         RplArgs shape{};
         shape.rows = int(rows);
         shape.nsb = int(nsb);
@@ -448,7 +447,6 @@ int wv_blob_upload(int format, int64_t rows, int64_t cols, int32_t block_weights
         r.meta = base + ro.meta;
         r.dd = ro.dd ? reinterpret_cast<const float2_t*>(base + ro.dd) : nullptr;
         r.partial = reinterpret_cast<float*>(base + o_part);
-        r.counters = reinterpret_cast<uint32_t*>(base + o_ctr);
         r.rows = int(rows);
         r.nsb = int(cols / 256);
         r.rg_count = int((rows + 63) / 64);

@@ -96,7 +96,6 @@ struct RplArgs {
     const uint8_t* meta;
     const float2_t* dd;
     float* partial;       // [batch chunk][ksplit][rg*64] partial sums when K is split
-    uint32_t* counters;   // [batch chunk][rg*4] arrival tickets per row subgroup, zero between launches
     int rows, nsb, rg_count, ksplit;
     // Output epilogue of the forward kernel: RPL_STORE y = Wx;
     // RPL_ADD y += Wx (residual); RPL_SILU_MUL y = silu(aux) * Wx (SwiGLU up);
