@@ -106,7 +106,7 @@ def test_baseline_shapes(fmt, shape):
 @pytest.mark.parametrize("fmt", sorted(PLANAR))
 @pytest.mark.parametrize("shape,batch", [((1000, 2048), 11), ((130, 4096), 2), ((64, 256), 1)])
 def test_row_interleaved_split_and_batch(fmt, shape, batch):
-    """K split across blocks (last-block reduction), batch beyond one split launch."""
+    """K split across blocks (partials added by a second launch), batch beyond one split launch."""
     rows, cols = shape
     print(f"[gpu] rpl split {fmt} {cols}->{rows} batch {batch}", flush=True)
     w, rng = weights(rows, cols, 17)
@@ -114,7 +114,7 @@ def test_row_interleaved_split_and_batch(fmt, shape, batch):
     p, d = upload(fmt, w, rows, cols)
     assert d.info()["layout"] == "row-interleaved"
     ref = oracle.reference_y(oracle_packed(p), x)
-    for _ in range(2):  # the arrival tickets must be back at zero for the next launch
+    for _ in range(2):  # the blob's split scratch is reused by the next launch
         assert normwise(d.matvec(x), ref) <= TOL
 
 
@@ -186,18 +186,27 @@ def test_native_ternary_bit_exact(shape):
     assert np.array_equal(d.matvec(x).reshape(-1), y_ref)
 
 
-@pytest.mark.parametrize("fmt", ["Q4_0", "Q8_0", "Q4_K", "Q6_K", "IQ4_NL", "TernaryPacked", "BinaryPacked", "Q5_1"])
-def test_matvec_t_accumulates(fmt):
-    rows, cols = 300, 512
-    print(f"[gpu] matvec_t {fmt}", flush=True)
-    w, rng = weights(rows, cols, 9)
-    gy = rng.standard_normal((2, rows)).astype(np.float32)
-    gx0 = rng.standard_normal((2, cols)).astype(np.float32)
+@pytest.mark.parametrize("fmt", ALL + ["AffinePacked"])
+@pytest.mark.parametrize("shape,batch", [((300, 512), 2), ((100, 1280), 1), ((33, 1000), 2), ((520, 2304), 3)])
+def test_matvec_t_accumulates(fmt, shape, batch):
+    """gx += W^T gy on the reference layout. cols % 256 == 0 takes the run kernel:
+    300x512 in 4 row slices + reduce, 100x1280 in one slice added directly (two
+    column tiles, the second partly past the row), 520x2304 in 8 slices over 3
+    tiles with batch 3; 33x1000 takes the per-weight kernel."""
+    rows, cols = shape
+    if fmt == "AffinePacked" and cols % 64:
+        pytest.skip("AffinePacked packs whole 64-groups per row")
+    print(f"[gpu] matvec_t {fmt} {rows}x{cols} batch {batch}", flush=True)
+    w, rng = weights(rows, cols, 9 + rows)
+    gy = rng.standard_normal((batch, rows)).astype(np.float32)
+    gx0 = rng.standard_normal((batch, cols)).astype(np.float32)
     p, d = upload(fmt, w, rows, cols, force_raw=True)
+    assert d.info()["layout"] == "raw"
     wd = oracle.unpack(oracle_packed(p)).reshape(rows, cols).astype(np.float64)
     want = gx0 + gy.astype(np.float64) @ wd
-    got = d.matvec_t(gy, gx0)
-    assert normwise(got, want) <= TOL
+    for _ in range(2):
+        assert normwise(d.matvec_t(gy, gx0), want) <= TOL
+    d.free()
 
 
 @pytest.mark.parametrize("fmt", sorted(PLANAR))

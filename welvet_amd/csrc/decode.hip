@@ -414,13 +414,36 @@ __global__ void __launch_bounds__(1024) k_argmax_advance(const float* __restrict
     __shared__ int bi[16];
     float v = -INFINITY;
     int idx = 0x7fffffff;
-    for (int i = threadIdx.x; i < n; i += 1024) {
-        const float x = logits[i];
+    auto take = [&](float x, int i) {
         if (x > v || (x == v && i < idx)) {
             v = x;
             idx = i;
         }
+    };
+    // float4 loads, U per thread issued before any compare, so a pass costs
+    // one memory round trip (32000 logits: one pass of 8 per thread).
+    constexpr int U = 8;
+    const int n4 = n >> 2;
+    const float4* l4 = reinterpret_cast<const float4*>(logits);
+    for (int base = 0; base < n4; base += 1024 * U) {
+        float4 r[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int i4 = base + u * 1024 + int(threadIdx.x);
+            r[u] = i4 < n4 ? l4[i4] : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int i = 4 * (base + u * 1024 + int(threadIdx.x));
+            if (i < 4 * n4) {
+                take(r[u].x, i);
+                take(r[u].y, i + 1);
+                take(r[u].z, i + 2);
+                take(r[u].w, i + 3);
+            }
+        }
     }
+    for (int i = 4 * n4 + int(threadIdx.x); i < n; i += 1024) take(logits[i], i);
     for (int m = 32; m >= 1; m >>= 1) {
         const float ov = __shfl_xor(v, m, 64);
         const int oi = __shfl_xor(idx, m, 64);

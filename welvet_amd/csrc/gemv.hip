@@ -1,7 +1,7 @@
 // gemv.hip — gfx950 kernels of the Dense MatVec path.
 //
 // Three families:
-//   * k_gemv_raw16 (cols % 256 == 0) and k_gemv_raw / k_gemvt_raw (any shape,
+//   * k_gemv_raw16 / k_gemvt_raw16 (cols % 256 == 0) and k_gemv_raw / k_gemvt_raw (any shape,
 //     including blocks that straddle rows): the reference layout as uploaded
 //     (LAYOUT_RAW), every format; semantics follow the reference decoders
 //     (quant/*.go forEach* / unpack*), accumulating in f32.
@@ -324,20 +324,14 @@ template <> struct RawF<FMT_BINARY> {
     static __device__ float fq(uint32_t q, const float* tab) { return float(q); }
 };
 
-// The 16 codes of a run: 2*BITS bytes at p (2-byte aligned), read as aligned
-// dwords and realigned.
-template <int BITS>
-__device__ __forceinline__ void load_run(const uint8_t* p, uint32_t* w) {
-    constexpr int NB = 2 * BITS;           // bytes of the run
-    constexpr int NW = (NB + 2 + 3) / 4;   // dwords that cover it from the aligned base
-    const uintptr_t ad = reinterpret_cast<uintptr_t>(p);
-    const uint32_t* base = reinterpret_cast<const uint32_t*>(ad & ~uintptr_t(3));
-    const uint32_t m = uint32_t(ad & 3);
-    uint32_t d[NW];
-#pragma unroll
-    for (int i = 0; i < NW; ++i) d[i] = base[i];
-#pragma unroll
-    for (int i = 0; i < (NB + 3) / 4; ++i) w[i] = __builtin_amdgcn_alignbyte(i + 1 < NW ? d[i + 1] : 0u, d[i], m);
+// The dword-aligned start of a run's code bytes at p (2-byte aligned) and the
+// byte offset of p in it. The start is formed by pointer arithmetic on p, not
+// through an integer: an integer round trip loses the global address space,
+// and the loads become flat loads, which also count against the LDS counter
+// so that every wait on them is a full wait.
+__device__ __forceinline__ const uint32_t* run_base(const uint8_t* p, uint32_t& mis) {
+    mis = uint32_t(reinterpret_cast<uintptr_t>(p)) & 3u;
+    return reinterpret_cast<const uint32_t*>(p - mis);
 }
 template <int BITS>
 __device__ __forceinline__ uint32_t code_at(const uint32_t* w, int k) {
@@ -373,6 +367,12 @@ __global__ void __launch_bounds__(256) k_gemv_raw16(RawArgs a, const float* __re
     // is issued before any of them is used; indices past the row are clamped
     // to its last run (read, not used), so the load phase has no branches.
     constexpr int NB = 2 * P::BITS, NW = (NB + 2 + 3) / 4;
+    // Load order (measured at 4096->14336): formats whose header is a plain
+    // scale (and min) issue every row's codes first and the headers after;
+    // the k-quants (two exact divisions per run), IQ4_NL and Affine keep each
+    // row's header arithmetic next to its loads, where it overlaps the other
+    // rows' loads (two-phase: Q4_1 -13 %, Q5_0 -12 %, Binary -10 %; Q5_K +26 %).
+    constexpr bool kTwoPhase = !(F >= FMT_Q2_K && F <= FMT_Q6_K) && F != FMT_IQ4_NL && F != FMT_AFFINE;
     float acc[R] = {};
     for (int64_t s0 = kp * 64 + lane; s0 < nsg; s0 += 64 * KW * U) {
         float4 xq[U][4];
@@ -386,13 +386,25 @@ __global__ void __launch_bounds__(256) k_gemv_raw16(RawArgs a, const float* __re
             for (int k = 0; k < 4; ++k) xq[u][k] = xp[k];
 #pragma unroll
             for (int r = 0; r < R; ++r) {
-                g[u][r] = P::grp(a, rowc[r], rowc[r] * a.cols + c0);
-                const uintptr_t ad = reinterpret_cast<uintptr_t>(g[u][r].codes);
-                const uint32_t* base = reinterpret_cast<const uint32_t*>(ad & ~uintptr_t(3));
-                mis[u][r] = uint32_t(ad & 3);
+                if constexpr (!kTwoPhase) g[u][r] = P::grp(a, rowc[r], rowc[r] * a.cols + c0);
+                const uint32_t* base =
+                    run_base(kTwoPhase ? P::grp(a, rowc[r], rowc[r] * a.cols + c0).codes : g[u][r].codes, mis[u][r]);
 #pragma unroll
                 for (int i = 0; i < NW; ++i) dw[u][r][i] = base[i];
             }
+        }
+        if constexpr (kTwoPhase) {
+            // The loads above used only the codes address of grp(); its header
+            // loads and alpha/beta arithmetic follow here, so no header
+            // arithmetic waits between one row's loads and the next's.
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int64_t c0 = min<int64_t>(s0 + 64 * KW * u, nsg - 1) << 4;
+#pragma unroll
+                for (int r = 0; r < R; ++r) g[u][r] = P::grp(a, rowc[r], rowc[r] * a.cols + c0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
@@ -436,6 +448,96 @@ __global__ void __launch_bounds__(256) k_gemv_raw16(RawArgs a, const float* __re
             const int64_t row = (int64_t(blockIdx.x) * (4 / KW) + grp) * R + r;
             if (row < a.rows) y[int64_t(b) * a.rows + row] = v;
         }
+    }
+}
+
+// MatVecT on the reference layout by runs (cols % 256 == 0, the layouts of
+// k_gemv_raw16): gx[c] += sum_r w(r,c) gy[r] with w = alpha*f(q) + beta per
+// run of 16 columns. Lane = one run of a 64-run column tile (blockIdx.x); the
+// kRawTWaves waves of a block take rows r0 + w, r0 + w + kRawTWaves, ... of
+// the block's row slice (blockIdx.y). A lane keeps 16 column sums of
+// (gy*alpha)*f(q) and one sum of gy*beta for the whole run, with the runs of
+// U rows in flight, and the waves' sums meet in LDS in wave order. Several
+// slices write part[(b*slices + slice)*cols + c] for k_gemvt_reduce; one
+// slice adds to gx directly.
+constexpr int kRawTWaves = 8;
+template <int F>
+__global__ void __launch_bounds__(64 * kRawTWaves) k_gemvt_raw16(RawArgs a, const float* __restrict__ gy,
+                                                                  float* __restrict__ gx, float* __restrict__ part,
+                                                                  int rows_per_slice) {
+    using P = RawF<F>;
+    constexpr int WB = kRawTWaves, U = 4;
+    constexpr int NB = 2 * P::BITS, NW = (NB + 2 + 3) / 4;
+    __shared__ float tab[16];
+    __shared__ float red[WB][64 * 16];
+    if constexpr (F == FMT_IQ4_NL) {
+        if (threadIdx.x < 16) tab[threadIdx.x] = kIQ4NLGrid[threadIdx.x];
+        __syncthreads();
+    }
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int slice = blockIdx.y, b = blockIdx.z;
+    const int64_t nsg = a.cols >> 4;
+    const int64_t c0 = min<int64_t>(int64_t(blockIdx.x) * 64 + lane, nsg - 1) << 4;
+    const int64_t r0 = int64_t(slice) * rows_per_slice;
+    const int64_t r1 = min<int64_t>(a.rows, r0 + rows_per_slice);
+    const float* g = gy + int64_t(b) * a.rows;
+    float acc[16] = {};
+    float off = 0.f;
+    for (int64_t rb = r0 + wave; rb < r1; rb += WB * U) {
+        // Rows past the slice are clamped to its last row (read, not used).
+        // Phase 1 issues the code loads of all U rows (only the codes
+        // address of grp() is used, so its header loads and arithmetic are
+        // dropped here); phase 2 calls grp() again for alpha and beta, whose
+        // header loads queue behind the codes. A barrier keeps each phase's
+        // loads ahead of the arithmetic that waits on them.
+        int64_t rr[U];
+        uint32_t dw[U][NW], mis[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            rr[u] = min<int64_t>(rb + WB * u, r1 - 1);
+            const uint32_t* base = run_base(P::grp(a, rr[u], rr[u] * a.cols + c0).codes, mis[u]);
+#pragma unroll
+            for (int i = 0; i < NW; ++i) dw[u][i] = base[i];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        Grp gr[U];
+        float gv[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            gr[u] = P::grp(a, rr[u], rr[u] * a.cols + c0);
+            gv[u] = g[rr[u]];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        // No branch per row: a branch would let the compiler sink that row's
+        // loads into it, and the rows' loads would no longer overlap. Rows
+        // past the slice add exact zeros (selects, so no 0 * inf).
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const bool live = rb + WB * u < r1;
+            uint32_t w[(NB + 3) / 4];
+#pragma unroll
+            for (int i = 0; i < (NB + 3) / 4; ++i)
+                w[i] = __builtin_amdgcn_alignbyte(i + 1 < NW ? dw[u][i + 1] : 0u, dw[u][i], mis[u]);
+            const float coef = live ? gv[u] * gr[u].alpha : 0.f;
+            off += live ? gv[u] * gr[u].beta : 0.f;
+#pragma unroll
+            for (int k = 0; k < 16; ++k) acc[k] = fmaf(coef, P::fq(code_at<P::BITS>(w, k), tab), acc[k]);
+        }
+    }
+    float* rw = red[wave] + lane * 16;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) rw[k] = acc[k] + off;
+    __syncthreads();
+    for (int cc = threadIdx.x; cc < 64 * 16; cc += 64 * WB) {
+        float v = 0.f;
+#pragma unroll
+        for (int w = 0; w < WB; ++w) v += red[w][cc];
+        const int64_t col = int64_t(blockIdx.x) * 1024 + cc;
+        if (col >= a.cols) continue;
+        if (gridDim.y == 1)
+            gx[int64_t(b) * a.cols + col] += v;
+        else
+            part[(int64_t(b) * gridDim.y + slice) * a.cols + col] = v;
     }
 }
 
@@ -716,8 +818,37 @@ int launch_raw(const DevBlob& b, const float* x, float* y, int batch, hipStream_
     return int(hipGetLastError());
 }
 
+// Row slices of the run-vectorized MatVecT: about rawt_blocks() (1024) blocks over
+// the column tiles, at most 128 slices and at least 64 rows per slice (so
+// the partials stay small next to the weights).
+int rawt_blocks() {
+    static const int v = [] {
+        const char* e = std::getenv("WV_RAWT_BLOCKS");
+        return e && *e ? std::atoi(e) : 1024;
+    }();
+    return v;
+}
+int raw_t16_slices(const DevBlob& b) {
+    const int64_t tiles = (b.cols / 16 + 63) / 64;
+    const int64_t want = (rawt_blocks() + tiles - 1) / tiles;
+    return int(std::max<int64_t>(1, std::min<int64_t>({want, 128, b.rows / 64})));
+}
+// Row splits of the per-weight MatVecT.
+int raw_t_splits(const DevBlob& b) { return int(std::max<int64_t>(1, std::min<int64_t>(64, b.rows / 64))); }
+
 template <int F>
-int launch_raw_t(const DevBlob& b, const float* gy, float* gx, int batch, hipStream_t s, float* part, int nsplit) {
+int launch_raw_t(const DevBlob& b, const float* gy, float* gx, int batch, hipStream_t s, float* part) {
+    if (raw16_ok<F>(b)) {
+        const int ns = raw_t16_slices(b);
+        const int rps = int((b.rows + ns - 1) / ns);
+        const dim3 grid(unsigned((b.cols / 16 + 63) / 64), unsigned(ns), unsigned(batch));
+        hipLaunchKernelGGL(k_gemvt_raw16<F>, grid, dim3(64 * kRawTWaves), 0, s, raw_args(b), gy, gx, part, rps);
+        if (ns > 1)
+            hipLaunchKernelGGL(k_gemvt_reduce, dim3(unsigned((b.cols + 63) / 64), unsigned(batch)), dim3(64), 0, s,
+                               part, gx, b.cols, ns);
+        return int(hipGetLastError());
+    }
+    const int nsplit = raw_t_splits(b);
     const int rps = int((b.rows + nsplit - 1) / nsplit);
     dim3 grid(unsigned((b.cols + 255) / 256), unsigned(nsplit), unsigned(batch));
     hipLaunchKernelGGL(k_gemvt_raw<F>, grid, dim3(256), 0, s, raw_args(b), gy, part, rps);
@@ -727,7 +858,7 @@ int launch_raw_t(const DevBlob& b, const float* gy, float* gx, int batch, hipStr
 }
 
 using RawFn = int (*)(const DevBlob&, const float*, float*, int, hipStream_t);
-using RawTFn = int (*)(const DevBlob&, const float*, float*, int, hipStream_t, float*, int);
+using RawTFn = int (*)(const DevBlob&, const float*, float*, int, hipStream_t, float*);
 
 RawFn pick_raw(int fmt) {
     switch (fmt) {
@@ -846,8 +977,8 @@ void launch_gemvt_reduce(const float* part, float* gx, int64_t cols, int nsplit,
 
 size_t matvec_t_scratch_floats(const DevBlob& b, int batch) {
     if (b.layout == LAYOUT_RPL) return 0;
-    const int64_t nsplit = std::max<int64_t>(1, std::min<int64_t>(64, b.rows / 64));
-    return size_t(nsplit) * size_t(b.cols) * size_t(batch);
+    const int64_t n = std::max(raw_t_splits(b), raw_t16_slices(b));  // covers either kernel
+    return size_t(n) * size_t(b.cols) * size_t(batch);
 }
 
 int launch_matvec_t(const DevBlob& b, const float* d_gy, float* d_gx, int batch, void* stream, float* d_scratch) {
@@ -857,8 +988,7 @@ int launch_matvec_t(const DevBlob& b, const float* d_gy, float* d_gx, int batch,
     if (b.layout != LAYOUT_RAW) return int(hipErrorInvalidValue);
     RawTFn f = pick_raw_t(b.fmt);
     if (!f) return int(hipErrorInvalidValue);
-    const int nsplit = int(std::max<int64_t>(1, std::min<int64_t>(64, b.rows / 64)));
-    return f(b, d_gy, d_gx, batch, s, d_scratch, nsplit);
+    return f(b, d_gy, d_gx, batch, s, d_scratch);
 }
 
 int launch_ternary_acc(const DevBlob& b, const float* d_x, int32_t* d_acc, float* d_act, int batch, void* stream) {
