@@ -20,8 +20,8 @@
 // lane, loaded ahead of the weights) and reads them back as wave-wide
 // broadcasts. Partial row sums of the W waves meet in LDS; when K is split
 // across blocks, each block writes its partial to a per-blob scratch row and
-// the last block of a row group (agent-scope atomic ticket) adds the partials
-// in split order, so the result does not depend on arrival order.
+// a second launch (k_rpl_ksum) adds the partials in split order, so the
+// result does not depend on arrival order.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
