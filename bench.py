@@ -2,6 +2,10 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload q4k_4096x14336]
 
+Other workloads (--workload): every packed format at 4096->14336, the
+batched prefill GEMM (q4k_prefill_*), MatVecT (<fmt>_t_<in>x<out>) and the
+32-layer decode step (decode_32l).
+
 A step is one batch-1 dequant-GEMV launch (y = W x, W packed, x and y f32 in
 HBM). Weights are N(0, 0.02) packed by the library's quant.Pack restatement,
 x ~ N(0, 1). Consecutive steps rotate over enough uploaded copies of W that
@@ -55,6 +59,12 @@ WORKLOADS.update({
 PREFILL = {
     f"q4k_prefill_{i}x{o}_m{m}": ("Q4_K", o, i, m, f"Q4_K prefill GEMM {i}->{o} M={m} (fp16 MFMA)")
     for (i, o) in ((4096, 14336), (14336, 4096)) for m in (32, 128, 512)
+}
+# quant.MatVecT (gx += W^T gy, wv_matvec_t_dev) of a Dense layer's weight:
+# name -> (format, rows, cols, description); rows = the layer's out, cols = its in.
+MATVECT = {
+    f"{f.lower()}_t_{i}x{o}": (f, o, i, f"{f} MatVecT of the {i}->{o} weight (gx[{i}] += W^T gy[{o}]) b=1")
+    for f in ("Q4_K", "Q6_K", "Q8_0", "Q5_K", "Q4_1", "IQ4_NL") for (i, o) in ((4096, 14336), (14336, 4096))
 }
 MFMA_F16_PEAK_TFLOPS = 2500.0
 # 32-layer decoder, hidden 4096, 32/8 heads x 128, SwiGLU 14336, vocab 32000, Q4_K, KV 2048
@@ -133,7 +143,7 @@ def main():
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--workload", default="q4k_4096x14336",
-                    choices=sorted(WORKLOADS) + sorted(PREFILL) + sorted(DECODE))
+                    choices=sorted(WORKLOADS) + sorted(PREFILL) + sorted(MATVECT) + sorted(DECODE))
     ap.add_argument("--cpu-budget-s", type=float, default=12.0)
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -157,6 +167,8 @@ def main():
 
     if args.workload in PREFILL:
         return prefill_main(args, torch, wv)
+    if args.workload in MATVECT:
+        return matvect_main(args, torch, wv)
     if args.workload in DECODE:
         return decode_main(args, wv)
     fmt, rows, cols, desc = WORKLOADS[args.workload]
@@ -360,6 +372,81 @@ def prefill_main(args, torch, wv):
             "value": round(2.0 * rows * cols / dt / 1e12, 5), "unit": "TFLOP/s", "cores": threads, "kind": "port",
             "sample": f"{n} of the M row GEMVs the reference runs for this block (restated fused SIMD path, "
                       f"{threads} row-shard threads), {dt * 1e3:.3f} ms per row"}
+    for b in blobs:
+        b.free()
+    print(json.dumps(result), flush=True)
+
+
+def matvect_main(args, torch, wv):
+    """One step = gx += W^T gy for one weight (the backward GEMV of a Dense layer)."""
+    fmt, rows, cols, desc = MATVECT[args.workload]
+    print(f"[bench] {desc}: packing", file=sys.stderr, flush=True)
+    w, rng = make_weights(fmt, rows, cols)
+    packed = wv.pack(fmt, w, rows, cols)
+    del w
+    gy = rng.standard_normal(rows, dtype=np.float32)
+    nbytes = packed.nbytes + 4 * rows + 8 * cols  # weights + gy + gx read and written
+    wv.init(0)
+    copies = max(8, math.ceil(1.25 * MALL_BYTES / packed.nbytes))
+    blobs = [wv.upload(packed) for _ in range(copies)]
+    layout = blobs[0].info()["layout"]
+    stream = torch.cuda.Stream()
+    sh = stream.cuda_stream
+    tg = torch.from_numpy(gy).cuda()
+    tx = torch.zeros(cols, device="cuda")
+    torch.cuda.synchronize()
+    launch = wv.lib().wv_matvec_t_dev
+    handles = [b.handle for b in blobs]
+    gp, xp = tg.data_ptr(), tx.data_ptr()
+
+    def run(n):
+        rc = 0
+        for i in range(n):
+            rc |= launch(handles[i % copies], gp, xp, 1, sh)
+        wv.check(rc)
+
+    run(1)
+    stream.synchronize()
+    assert torch.isfinite(tx).all().item(), "non-finite output"
+    steps = max(20, min(args.steps, 1000))
+    warmup = max(5, min(args.warmup, 100))
+    run(warmup)
+    stream.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    run(steps)
+    e1.record(stream)
+    e1.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    result = {
+        "metric": f"MatVecT HBM GB/s, {desc}",
+        "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "ms_per_step": round(ms, 6), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: W ~ N(0,0.02) packed by the library's quant.Pack restatement, gy ~ N(0,1)",
+        "config": {"workload": desc, "format": fmt, "rows": rows, "cols": cols, "layout": layout,
+                   "weight_copies_rotated": copies, "algorithmic_bytes_per_step": nbytes},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "step_us": round(ms * 1e3, 3)},
+    }
+    if not args.no_cpu:
+        import oracle
+        op = oracle.Packed(packed.fmt, rows, cols, packed.raw, packed.scales, packed.meta, packed.block_weights,
+                           packed.mins)
+        gx = np.zeros(cols, np.float32)
+        n = 0
+        t0 = time.perf_counter()
+        while n < 1000 and (n == 0 or time.perf_counter() - t0 < args.cpu_budget_s):
+            gx = oracle.matvec_t_scalar(op, gy, gx)
+            n += 1
+        dt = (time.perf_counter() - t0) / n
+        result["cpu_baseline"] = {
+            "value": round(nbytes / dt / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"{n} calls of the restated scalar quant.MatVecT (the reference's only MatVecT path, "
+                      f"serial), {dt * 1e3:.3f} ms/call"}
     for b in blobs:
         b.free()
     print(json.dumps(result), flush=True)

@@ -224,14 +224,45 @@ __global__ void __launch_bounds__(256) k_gemm_q4k(GemmArgs ga) {
         }
 }
 
-// y[i] = sum_k part[k*n + i], k ascending.
+// y[i] = sum_k part[k*n + i], k ascending; each thread owns 4 consecutive
+// outputs (float4 when n % 4 == 0 and y is 16-byte aligned; the partials
+// always are) and issues up to 8 splits' loads before adding them.
 __global__ void __launch_bounds__(256) k_split_sum(const float* __restrict__ part, float* __restrict__ y, int64_t n,
                                                   int splits) {
-    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
-    if (i >= n) return;
-    float s = 0.f;
-    for (int k = 0; k < splits; ++k) s += part[int64_t(k) * n + i];
-    y[i] = s;
+    const int64_t i4 = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i4 * 4 >= n) return;
+    if ((n & 3) || (reinterpret_cast<uintptr_t>(y) & 15)) {  // ragged or unaligned: scalar, in the same order
+        for (int64_t i = i4 * 4; i < min<int64_t>(n, i4 * 4 + 4); ++i) {
+            float s = 0.f;
+            for (int k = 0; k < splits; ++k) s += part[int64_t(k) * n + i];
+            y[i] = s;
+        }
+        return;
+    }
+    const float4* p = reinterpret_cast<const float4*>(part) + i4;
+    const int64_t n4 = n >> 2;
+    float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+    int k = 0;
+    for (; k + 8 <= splits; k += 8) {
+        float4 v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = p[int64_t(k + j) * n4];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            s.x += v[j].x;
+            s.y += v[j].y;
+            s.z += v[j].z;
+            s.w += v[j].w;
+        }
+    }
+    for (; k < splits; ++k) {
+        const float4 v = p[int64_t(k) * n4];
+        s.x += v.x;
+        s.y += v.y;
+        s.z += v.z;
+        s.w += v.w;
+    }
+    reinterpret_cast<float4*>(y)[i4] = s;
 }
 
 template <int BM, int WM>
@@ -293,7 +324,7 @@ int launch_gemm(const DevBlob& b, const float* d_x, float* d_y, int M, void* str
     else launch_bm<128, 2>(ga, grid, s);
     if (splits > 1) {
         const int64_t n = int64_t(M) * b.rows;
-        hipLaunchKernelGGL(k_split_sum, dim3(unsigned((n + 255) / 256)), dim3(256), 0, s, part, d_y, n, splits);
+        hipLaunchKernelGGL(k_split_sum, dim3(unsigned((n / 4 + 1 + 255) / 256)), dim3(256), 0, s, part, d_y, n, splits);
     }
     return int(hipGetLastError());
 }
