@@ -62,6 +62,25 @@ def test_prefill_q4k_small(shape, m):
     d.free()
 
 
+@pytest.mark.parametrize("shape", [(256, 1024), (200, 512), (448, 2048), (1000, 4096)])
+@pytest.mark.parametrize("m", [256, 300])
+def test_prefill_q4k_wide(shape, m):
+    """Token blocks of 256 and more (several 128-token tiles): padded rows, a
+    ragged last token tile, and K split over blocks (every shape here leaves
+    CUs idle)."""
+    rows, cols = shape
+    print(f"[gpu] prefill wide q4k {cols}->{rows} M={m}", flush=True)
+    p, wd, rng = packed_q4k(rows, cols, rows + m)
+    d = wv.upload(p)
+    x = rng.standard_normal((m, cols)).astype(np.float32)
+    ref = x.astype(np.float64) @ wd.T
+    for _ in range(2):
+        y = d.matmul(x)
+        assert normwise(y, ref) <= TOL_MFMA
+        assert rowwise(y, ref) <= 4 * TOL_MFMA
+    d.free()
+
+
 _BASE = {}
 
 
