@@ -333,3 +333,27 @@ def test_affine_matvec_t_accumulates():
     assert normwise(d.matvec_t(gy, gx0), want) <= TOL
     assert normwise(oracle.matvec_t_scalar(oracle_packed(p), gy[0], gx0[0]), want[0]) <= TOL
     d.free()
+
+
+@pytest.mark.parametrize("fmt", ["Q4_K", "Q6_K", "Q8_0", "Q4_0", "Q5_K", "IQ4_NL", "Q4_1"])
+@pytest.mark.parametrize("shape", [(300, 2048), (130, 8192)])
+def test_nonfinite_x_propagates(fmt, shape):
+    """A NaN in x makes every output NaN, as in the reference's float
+    accumulation (w * NaN is NaN for every w). An infinite x leaves no output
+    finite (the reference gives +-inf, or NaN where w = 0 or infinities cancel).
+    The int-x Q4_K path relies on its float group sums for this: the
+    fixed-point x planes alone would drop the non-finite value. 130x8192
+    splits K over blocks."""
+    rows, cols = shape
+    print(f"[gpu] nonfinite x {fmt} {cols}->{rows}", flush=True)
+    w, rng = weights(rows, cols, 77)
+    p, d = upload(fmt, w, rows, cols)
+    x = rng.standard_normal((3, cols)).astype(np.float32)
+    x[0, cols // 3] = np.nan
+    x[1, cols - 5] = np.inf
+    y = d.matvec(x)
+    assert np.isnan(y[0]).all()
+    assert not np.isfinite(y[1]).any()
+    ref = oracle.reference_y(oracle_packed(p), x[2:])[0]
+    assert normwise(y[2], ref) <= TOL  # the finite batch row is unaffected
+    d.free()

@@ -148,7 +148,10 @@ struct RplQ4KI : RplQ4K {
         }
         const int T0 = A[0][0] + (A[0][1] << 8) + (A[0][2] << 16);
         const int T1 = A[1][0] + (A[1][1] << 8) + (A[1][2] << 16);
-        // (float)(int8)m = ub(m ^ 0x80) - 128; the -128 terms are folded into xm.w
+        // (float)(int8)m = ub(m ^ 0x80) - 128; the -128 terms are folded into xm.w.
+        // The group sums stay floats: a NaN or infinite x (which the fixed-point
+        // planes would turn into a finite value) makes this term, and so the
+        // row, non-finite, as the reference's float arithmetic does.
         const uint32_t gx = g ^ 0x80800000u;
         const float mn = fmaf(ub3(gx), xm.z, fmaf(ub2(gx), xm.y, xm.w));
         const float sc = sb.d255 * 255.0f * xm.x;  // d * 2^-s / 255
