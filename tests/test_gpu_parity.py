@@ -120,12 +120,15 @@ def test_row_interleaved_split_and_batch(fmt, shape, batch):
 
 # Shapes that select each launch plan of the row-interleaved forward kernel:
 # lanes per row L (1, 2, 4) with one or two super-blocks per wave S for
-# K <= 4096, and a K split across blocks for wider matrices.
+# K <= 4096; for wider matrices L = S = 4 with no K split when those blocks
+# fill the GPU in one pass, else a K split across blocks.
 PLAN_SHAPES = [
     ((12800, 1024), ["Q4_K", "Q6_K", "Q8_0", "Q4_0"]),  # L=1 S=1
     ((8192, 1024), ["Q4_K", "Q6_K", "Q8_0", "Q4_0"]),   # L=2 S=1
     ((1000, 2048), ["Q4_K", "Q6_K", "Q8_0", "Q4_0"]),   # L=4 S=2
-    ((8192, 8192), ["Q4_K", "Q8_0"]),                   # K split 2
+    ((8192, 8192), ["Q4_K", "Q8_0"]),                   # L=4 S=4, 8-wave blocks, no split
+    ((3000, 13312), ["Q4_K", "Q6_K", "Q8_0", "Q4_0"]),  # L=4 S=4, 13 waves, padded last row group
+    ((4096, 11008), ["Q4_K", "Q6_K"]),                  # L=4 S=4, 43 super-blocks: last wave has 3
     ((2048, 16640), ["Q4_K", "Q6_K", "Q8_0", "Q4_0"]),  # K split 5 over 13-wave blocks
     ((6400, 16640), ["Q4_K"]),                          # K split 2, 65 super-blocks
 ]

@@ -561,11 +561,15 @@ int lds_floor() {
 //     doubles (to 4) until the grid (row groups x L) has >= 180 blocks; a lane
 //     keeps >= 4 chunk steps, so L = 4 takes two super-blocks per wave.
 //     4096x4096 runs in 5.1 us with L=4 S=2 against 7.2 us with L=1.
-//   * wider: L = S = 1 and K split over blocks of W = 16..4 waves (more
-//     super-blocks per wave or more lanes per row measured slower there:
-//     4096x14336 takes 11.2 us split 4 ways, 12.4-21 us otherwise); W prefers
-//     grids of >= min_blocks() blocks, then the fewest idle waves, then the
-//     largest W, and the split is capped by the scratch the blob carries.
+//   * wider, when 4 x (row groups) blocks of W = ceil(nsb / 4) waves fill the
+//     GPU (>= 180) in one resident pass (<= 256 x floor(16 / W)): L = 4, S = 4
+//     and no K split. 14336->4096 runs in 10.5 us against 11.0 us split 4
+//     ways, 8192->4096 in 6.9 against 8.1; 14336->8192 (too many blocks)
+//     takes 19.4 against 17.3.
+//   * otherwise L = S = 1 and K split over blocks of W = 16..4 waves; W
+//     prefers grids of >= min_blocks() blocks, then the fewest idle waves,
+//     then the largest W, and the split is capped by the scratch the blob
+//     carries.
 struct RplPlan {
     int L, S, W, ksplit;
 };
@@ -576,6 +580,13 @@ RplPlan rpl_plan(const DevBlob& bl) {
     if (a.nsb <= 16) {
         while (p.L < 4 && int64_t(a.rg_count) * p.L < 180) p.L *= 2;
         if (p.L == 4 && a.nsb >= 2) p.S = 2;
+    } else if (const int w4 = (a.nsb + 3) / 4;
+               w4 <= 16 && int64_t(a.rg_count) * 4 >= 180 && int64_t(a.rg_count) * 4 <= 256 * (16 / w4)) {
+        // No K split: L = 4, S = 4, one block per 16-row subgroup covering
+        // all of K, when those blocks fill the GPU in one resident pass.
+        p.L = 4;
+        p.S = 4;
+        p.W = w4;
     } else {
         const int target = min_blocks();
         int best = -1;
