@@ -490,9 +490,10 @@ __global__ void __launch_bounds__(1024) k_gemv_rpl(RplArgs a, const float* __res
         }
         __builtin_amdgcn_sched_barrier(0);
     }
-    // the L lane groups of a row hold partial sums of different chunks
-#pragma unroll
-    for (int o = R; o < 64; o <<= 1) acc += __shfl_xor(acc, o, 64);
+    // the L lane groups of a row hold partial sums of different chunks; a lane
+    // swap with both operands equal is the xor-16 / xor-32 butterfly step
+    if constexpr (R <= 16) acc = reduce_scatter16(acc, acc);
+    if constexpr (R <= 32) acc = reduce_scatter32(acc, acc);
     part[wave * 64 + lane] = acc;
     __syncthreads();
     if (wave != 0) return;
@@ -849,32 +850,49 @@ __global__ void __launch_bounds__(256) k_gemvt_rpl(RplArgs a, const float* __res
         if (i + R < GP) load(i + R, ring[i % R]);
     }
 
-    // Reduce-scatter over the 64 lanes: at mask m each lane keeps half of its
-    // 2m values and adds its partner's copy of that half; lane l ends with
-    // column l of this wave's 64.
+    // Reduce-scatter over the 64 lanes: at each level a lane keeps half of
+    // its 2m values and adds its partner's copy of that half; lane l ends
+    // with column l of this wave's 64. Every level runs on the VALU: lane
+    // swaps for m = 32 and 16, DPP for m = 8 (l ^ 8), 4 (partner l ^ 7, which
+    // also differs in bit 2), 2 and 1.
 #pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-        const bool hi = (lane & m) != 0;
+    for (int i = 0; i < 32; ++i) acc[i] = reduce_scatter32(acc[i], acc[i + 32]);
 #pragma unroll
-        for (int i = 0; i < m; ++i) {
-            const float keep = hi ? acc[i + m] : acc[i];
-            const float send = hi ? acc[i] : acc[i + m];
-            acc[i] = keep + __shfl_xor(send, m, 64);
+    for (int i = 0; i < 16; ++i) acc[i] = reduce_scatter16(acc[i], acc[i + 16]);
+    {
+        const bool hi = (lane & 8) != 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float keep = hi ? acc[i + 8] : acc[i], send = hi ? acc[i] : acc[i + 8];
+            acc[i] = keep + row_xor8(send);
         }
     }
-    // Group offsets: column l is in local group l >> 4 = 2*bit5 + bit4.
     {
-        const bool hi = (lane & 32) != 0;
-        const float k0 = hi ? off[2] : off[0], s0 = hi ? off[0] : off[2];
-        const float k1 = hi ? off[3] : off[1], s1 = hi ? off[1] : off[3];
-        off[0] = k0 + __shfl_xor(s0, 32, 64);
-        off[1] = k1 + __shfl_xor(s1, 32, 64);
-    }
-    float o = (lane & 16) ? off[1] : off[0];
-    const float os = (lane & 16) ? off[0] : off[1];
-    o += __shfl_xor(os, 16, 64);
+        const bool hi = (lane & 4) != 0;
 #pragma unroll
-    for (int m = 8; m >= 1; m >>= 1) o += __shfl_xor(o, m, 64);
+        for (int i = 0; i < 4; ++i) {
+            const float keep = hi ? acc[i + 4] : acc[i], send = hi ? acc[i] : acc[i + 4];
+            acc[i] = keep + half_mirror(send);
+        }
+    }
+    {
+        const bool hi = (lane & 2) != 0;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const float keep = hi ? acc[i + 2] : acc[i], send = hi ? acc[i] : acc[i + 2];
+            acc[i] = keep + quad_xor2(send);
+        }
+    }
+    {
+        const bool hi = (lane & 1) != 0;
+        const float keep = hi ? acc[1] : acc[0], send = hi ? acc[0] : acc[1];
+        acc[0] = keep + quad_xor1(send);
+    }
+    // Group offsets: column l is in local group l >> 4 = 2*bit5 + bit4; after
+    // the two swap levels every lane of a 16-lane row adds up its row.
+    off[0] = reduce_scatter32(off[0], off[2]);
+    off[1] = reduce_scatter32(off[1], off[3]);
+    const float o = row_sum16(reduce_scatter16(off[0], off[1]));
 
     const float total = acc[0] + o;
     const int64_t col = int64_t(sb) * 256 + jp * 64 + lane;
@@ -1065,7 +1083,7 @@ int rpl_fuse_rows(const DevBlob* parts, int n, DevBlob& out, void* stream) {
     if (e == hipSuccess) e = hipError_t(finish_fused(parts[0], rows, rg, f, b8, out, s));
     if (e == hipSuccess) e = hipStreamSynchronize(s);
     if (e != hipSuccess) {
-        hipFree(base);
+        (void)hipFree(base);  // cleanup after the error being returned
         out = DevBlob{};
     }
     return int(e);
@@ -1097,7 +1115,7 @@ int rpl_fuse_pairs(const DevBlob& a, const DevBlob& b, DevBlob& out, void* strea
     if (e == hipSuccess) e = hipError_t(finish_fused(a, 2 * a.rows, rg, f, b8, out, s));
     if (e == hipSuccess) e = hipStreamSynchronize(s);
     if (e != hipSuccess) {
-        hipFree(base);
+        (void)hipFree(base);  // cleanup after the error being returned
         out = DevBlob{};
     }
     return int(e);

@@ -105,6 +105,26 @@ __device__ __forceinline__ double wave_total_f64(double v) {
     return __longlong_as_double(static_cast<long long>((static_cast<unsigned long long>(hi) << 32) | lo));
 }
 
+// One reduce-scatter step over the lane pairs (l, l ^ 32): lanes below 32
+// return a(l) + a(l + 32), lanes from 32 return b(l - 32) + b(l). gfx950's
+// v_permlane32_swap exchanges a's upper 32 lanes with b's lower 32, so the
+// two results hold, in every lane, its own kept value and its partner's.
+__device__ __forceinline__ float reduce_scatter32(float a, float b) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+// The same over the pairs (l, l ^ 16) with v_permlane16_swap (odd 16-lane
+// rows of a exchanged with even rows of b): lanes with bit 4 clear return
+// a(l) + a(l + 16), the others b(l - 16) + b(l).
+__device__ __forceinline__ float reduce_scatter16(float a, float b) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+// The value of lane l ^ 8 (row_ror 8 inside each 16-lane row).
+__device__ __forceinline__ float row_xor8(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xf, 0xf, false));
+}
+
 // Quad transpose of bytes: lane q of each group of four holds P_q; returns to
 // lane q the dword whose byte j is byte q of P_j (quad_perm rotations).
 __device__ __forceinline__ uint32_t quad_byte_transpose(uint32_t p, int q) {
