@@ -106,6 +106,27 @@ def test_decode_hd128_gqa4():
     dec.free()
 
 
+@pytest.mark.parametrize("hd", [64, 128])
+def test_decode_gqa8(hd):
+    """Eight query heads per KV head (the register attention kernel's widest
+    case); the cache ends inside a chunk and the steps append into it."""
+    print(f"[gpu] decode gqa8 hd {hd}", flush=True)
+    cfg = Config(n_layers=2, hidden=512, n_heads=8, n_kv_heads=1, head_dim=hd, ffn=768, vocab=400, max_seq=128)
+    dec, ref, keep = build(cfg, "Q4_K", 17, kv_fill=70)
+    check_against_oracle(dec, ref, token=5, pos=70, steps=3)
+    dec.free()
+
+
+@pytest.mark.parametrize("hd", [64, 128])
+def test_decode_gqa3_tile_kernel(hd):
+    """Three query heads per KV head: the attention falls back to the LDS-tile kernel."""
+    print(f"[gpu] decode gqa3 hd {hd}", flush=True)
+    cfg = Config(n_layers=2, hidden=384, n_heads=6, n_kv_heads=2, head_dim=hd, ffn=512, vocab=300, max_seq=100)
+    dec, ref, keep = build(cfg, "Q4_K", 23, kv_fill=45)
+    check_against_oracle(dec, ref, token=8, pos=45, steps=3)
+    dec.free()
+
+
 @pytest.mark.parametrize("max_seq,kv_fill,hd", [(3000, 2900, 128), (6000, 5600, 64)])
 def test_decode_long_cache(max_seq, kv_fill, hd):
     """Caches of 94 and 188 chunks of 32 positions: the combine variants past one wave of chunks."""

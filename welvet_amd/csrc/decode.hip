@@ -120,12 +120,17 @@ __global__ void __launch_bounds__(256) k_attn_part(const float* __restrict__ q, 
                                                    float* __restrict__ part, int n_heads, int n_kv, int max_seq,
                                                    int n_chunks, float scale, const float* __restrict__ k_new,
                                                    const float* __restrict__ v_new, const double2* __restrict__ cs) {
-    constexpr int C = kChunk, LD = HD + 1, Q4 = HD / 4, H2 = HD / 2;
+    constexpr int C = kChunk, Q4 = HD / 4, H2 = HD / 2;
     constexpr int NL = C * Q4 / 256;         // float4 of K (and of V) per thread
-    constexpr int LPP = 64 / C, DW = HD / LPP;  // lanes per position in the score pass, dims per lane
     constexpr int QP = (8 * H2 + 255) / 256;    // q rotation pairs per thread (up to 8 heads per KV head)
-    static_assert(NL >= 1 && LPP >= 1 && LPP <= 4, "chunk shape");
-    __shared__ float ktile[C * LD];
+    static_assert(NL >= 1 && C == 32, "chunk shape");
+    // K tile: the score pass gives position p to lanes p and p + 32, one half
+    // of the head dimensions each. The upper half of a row starts HO words in
+    // (HO = 32 mod 64) and rows are KLD = 1 mod 32 words apart, so the 64 lanes
+    // of a read hit 64 different banks (and each 32-lane half 32 different
+    // banks): with the halves HD/2 apart they met in pairs.
+    constexpr int HO = H2 % 64 == 32 ? H2 : H2 + 32, KLD = HO + H2 + 1;
+    __shared__ float ktile[C * KLD];
     __shared__ __attribute__((aligned(16))) float vtile[C * HD];
     __shared__ __attribute__((aligned(16))) float es[8][C];
     extern __shared__ float qs[];  // [G][HD]
@@ -183,7 +188,8 @@ __global__ void __launch_bounds__(256) k_attn_part(const float* __restrict__ q, 
     for (int r = 0; r < NL; ++r) {
         const int i = t + 256 * r;
         if (i / Q4 == pnew) continue;
-        float* row = ktile + (i / Q4) * LD + 4 * (i % Q4);
+        const int c4 = 4 * (i % Q4);
+        float* row = ktile + (i / Q4) * KLD + (c4 < H2 ? c4 : c4 - H2 + HO);
         row[0] = kv4[r].x;
         row[1] = kv4[r].y;
         row[2] = kv4[r].z;
@@ -202,7 +208,7 @@ __global__ void __launch_bounds__(256) k_attn_part(const float* __restrict__ q, 
             kr[e] = d < H2 ? float(a0 * rc.x - a1 * rc.y) : float(a0 * rc.y + a1 * rc.x);
         }
         vnew = reinterpret_cast<const float4*>(v_new + kvh * HD)[t];
-        float* row = ktile + pnew * LD + d0;
+        float* row = ktile + pnew * KLD + (d0 < H2 ? d0 : d0 - H2 + HO);
         row[0] = kr[0];
         row[1] = kr[1];
         row[2] = kr[2];
@@ -212,14 +218,15 @@ __global__ void __launch_bounds__(256) k_attn_part(const float* __restrict__ q, 
         reinterpret_cast<float4*>(vc + crow)[t] = vnew;
     }
     __syncthreads();
-    // scores: one wave per query head, LPP lanes per position
+    // scores: one wave per query head; lanes p and p + 32 take the lower and
+    // upper half of position p's dimensions
     for (int g = wave; g < G; g += 4) {
-        const int p = lane / LPP, h = lane % LPP;
-        const float* kr = ktile + p * LD + h * DW;
-        const float4* qg = reinterpret_cast<const float4*>(qs + g * HD + h * DW);
+        const int p = lane & 31, h = lane >> 5;
+        const float* kr = ktile + p * KLD + h * HO;
+        const float4* qg = reinterpret_cast<const float4*>(qs + g * HD + h * H2);
         float s4[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll 8
-        for (int d4 = 0; d4 < DW / 4; ++d4) {
+        for (int d4 = 0; d4 < H2 / 4; ++d4) {
             const float4 qv = qg[d4];
             float& a = s4[d4 & 3];
             a = fmaf(qv.x, kr[4 * d4], a);
@@ -228,8 +235,7 @@ __global__ void __launch_bounds__(256) k_attn_part(const float* __restrict__ q, 
             a = fmaf(qv.w, kr[4 * d4 + 3], a);
         }
         float s = (s4[0] + s4[1]) + (s4[2] + s4[3]);
-        if (LPP >= 2) s += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(s), 0xb1, 0xf, 0xf, false));  // lane ^ 1
-        if (LPP >= 4) s += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(s), 0x4e, 0xf, 0xf, false));  // lane ^ 2
+        s = reduce_scatter32(s, s);  // + the other half (lane ^ 32)
         s = p < nvalid ? s * scale : -INFINITY;
         const float m = wave_maximum(s);
         const float e = (p < nvalid && h == 0) ? expf(s - m) : 0.f;
@@ -277,6 +283,262 @@ __global__ void __launch_bounds__(256) k_attn_part(const float* __restrict__ q, 
             }
             o[d] = (a4[0] + a4[1]) + (a4[2] + a4[3]);
         }
+    }
+}
+
+// Lane-group sums for k_attn_reg. pair_scatter<B> is one reduce-scatter step
+// over the lanes that differ in lane bit B: lanes with the bit clear return
+// a + a(partner), the others b + b(partner). Bits 5 and 4 use gfx950's lane
+// swaps; bits 3..0 use DPP (row_ror 8, half_mirror, quad xor 2, quad xor 1).
+// half_mirror pairs l with l ^ 7, which differs in bit 2: applied top-down
+// after bits 4 and 3 and before bits 1 and 0, the pairs still tile every
+// 8-lane group, so the steps sum over all of it.
+template <int B>
+__device__ __forceinline__ float lane_partner(float v) {
+    static_assert(B >= 0 && B <= 3, "DPP partner");
+    if constexpr (B == 3) return row_xor8(v);
+    else if constexpr (B == 2) return half_mirror(v);
+    else if constexpr (B == 1) return quad_xor2(v);
+    else return quad_xor1(v);
+}
+template <int B>
+__device__ __forceinline__ float pair_scatter(float a, float b, int lane) {
+    if constexpr (B == 5) return reduce_scatter32(a, b);
+    else if constexpr (B == 4) return reduce_scatter16(a, b);
+    else {
+        const bool hi = (lane >> B) & 1;
+        const float keep = hi ? b : a, send = hi ? a : b;
+        return keep + lane_partner<B>(send);
+    }
+}
+// Sum over lane bits B..0 into every lane.
+template <int B>
+__device__ __forceinline__ float group_allsum(float s) {
+    if constexpr (B < 0) return s;
+    else return group_allsum<B - 1>(s + lane_partner<B>(s));
+}
+// Totals of v[0..M) over the lanes that differ in lane bits B..0 (M a power of
+// two <= 2^(B+1)): bits B, B-1, ... scatter while more than one value is left
+// and the bits below that add. Lane l returns the total of v[i] for i given
+// by its bits B..B-log2(M)+1, highest bit most significant.
+template <int B, int M, int N>
+__device__ __forceinline__ float group_scatter(float (&v)[N], int lane) {
+    if constexpr (M == 1) {
+        return group_allsum<B>(v[0]);
+    } else {
+#pragma unroll
+        for (int j = 0; j < M / 2; ++j) v[j] = pair_scatter<B>(v[j], v[j + M / 2], lane);
+        return group_scatter<B - 1, M / 2>(v, lane);
+    }
+}
+// Max and sum over each 32-lane half of the wave, in every lane of the half.
+__device__ __forceinline__ float half_wave_max(float v) {
+    v = fmaxf(v, quad_xor1(v));
+    v = fmaxf(v, quad_xor2(v));
+    v = fmaxf(v, half_mirror(v));
+    v = fmaxf(v, row_xor8(v));
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float half_wave_sum(float v) {
+    v = group_allsum<3>(v);
+    return reduce_scatter16(v, v);
+}
+
+constexpr int ilog2(int n) { return n <= 1 ? 0 : 1 + ilog2(n / 2); }
+
+// The flash-decoding partials of k_attn_part for G = 1, 2, 4 or 8 query heads
+// per KV head, computed from registers: K and V stay where they are loaded and
+// only the q heads, the scores and the partial outputs pass through LDS.
+//
+// Thread t holds column t % Q4 (4 dims) of rows t / Q4 + r * RS (r < NL) of
+// the chunk, Q4 = HD/4 lanes to a row, so the loads are the chunk's
+// contiguous K (then V) run. Scores: each thread forms the NV = NL*G 4-dim
+// partial dots of its rows and heads, and a reduce-scatter over the Q4 lanes
+// of its row group leaves every (row, head) total in a lane (about 2 VALU
+// operations per value instead of a shared K tile). Softmax: one 32-lane half
+// wave per head. Output: each thread sums e[g][row] * v[row] over its NL rows
+// for G heads x 4 dims, a reduce-scatter over the lane bits that select the
+// row inside the wave halves the values, and the four waves' parts are added
+// in LDS in wave order.
+template <int HD, int G>
+__global__ void __launch_bounds__(256) k_attn_reg(const float* __restrict__ q, float* __restrict__ kc,
+                                                  float* __restrict__ vc, const int32_t* __restrict__ d_pos,
+                                                  float* __restrict__ part, int max_seq, int n_chunks, float scale,
+                                                  const float* __restrict__ k_new, const float* __restrict__ v_new,
+                                                  const double2* __restrict__ cs) {
+    constexpr int C = kChunk, Q4 = HD / 4, H2 = HD / 2, LQ = ilog2(Q4);
+    constexpr int RS = 256 / Q4;  // rows between one thread's rows
+    constexpr int NL = C / RS;    // rows per thread
+    constexpr int NV = NL * G;    // partial dots per thread
+    constexpr int NO = 4 * G;     // partial outputs per thread (G heads x 4 dims)
+    constexpr int LR = 6 - LQ;    // lane bits that select the row inside a wave
+    constexpr int NR = NO >> LR;  // partial outputs per lane after the in-wave row sum
+    constexpr int QP = (G * H2 + 255) / 256;
+    static_assert(C == 32 && NL >= 1 && NV <= Q4 && NR >= 1 && (G == 1 || G == 2 || G == 4 || G == 8), "shape");
+    __shared__ __attribute__((aligned(16))) float qs[G * HD];
+    __shared__ float ss[G][C];
+    __shared__ float red[4][NR][64];
+    const int kvh = blockIdx.x, c = blockIdx.y;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int pos = *d_pos;
+    const int kv_len = min(pos + 1, max_seq);
+    const int p0 = c * C;
+    const int nvalid = min(C, kv_len - p0);
+    if (nvalid <= 0) return;  // past the causal end: the combine reads only the chunks below kv_len
+    const int pnew = pos % max_seq - p0;
+    const bool has_new = pnew >= 0 && pnew < C;
+    const int col = t % Q4, row0 = t / Q4, d0 = 4 * col;
+    // q pairs of this KV group, this step's k and v column (the block holding pos)
+    float qa[QP], qb[QP];
+    double2 rq[QP];
+    const float* qh = q + kvh * G * HD;
+#pragma unroll
+    for (int j = 0; j < QP; ++j) {
+        const int i = min(t + 256 * j, G * H2 - 1), g = i / H2, d = i % H2;
+        qa[j] = qh[g * HD + d];
+        qb[j] = qh[g * HD + d + H2];
+        rq[j] = cs[d];
+    }
+    float4 ka = make_float4(0.f, 0.f, 0.f, 0.f), kb4 = ka, vnew = ka;
+    double2 rk[4] = {};
+    if (has_new) {
+        const int dm = d0 % H2;
+        ka = *reinterpret_cast<const float4*>(k_new + kvh * HD + dm);
+        kb4 = *reinterpret_cast<const float4*>(k_new + kvh * HD + dm + H2);
+        vnew = *reinterpret_cast<const float4*>(v_new + kvh * HD + d0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) rk[e] = cs[dm + e];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    float4 kv4[NL], vv4[NL];
+    const float4* kb = reinterpret_cast<const float4*>(kc + (int64_t(kvh) * max_seq + p0) * HD);
+    const float4* vb = reinterpret_cast<const float4*>(vc + (int64_t(kvh) * max_seq + p0) * HD);
+#pragma unroll
+    for (int r = 0; r < NL; ++r) kv4[r] = kb[min(row0 + RS * r, nvalid - 1) * Q4 + col];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int r = 0; r < NL; ++r) vv4[r] = vb[min(row0 + RS * r, nvalid - 1) * Q4 + col];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < QP; ++j) {
+        const int i = t + 256 * j;
+        if (i < G * H2) {
+            const int g = i / H2, d = i % H2;
+            const double v0 = qa[j], v1 = qb[j];
+            qs[g * HD + d] = float(v0 * rq[j].x - v1 * rq[j].y);
+            qs[g * HD + d + H2] = float(v0 * rq[j].y + v1 * rq[j].x);
+        }
+    }
+    __syncthreads();
+    float4 qv[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) qv[g] = *reinterpret_cast<const float4*>(qs + g * HD + d0);
+    if (has_new) {  // the rotated new k and the new v replace the cache's row pnew, and are appended to the cache
+        float x0[4] = {ka.x, ka.y, ka.z, ka.w}, x1[4] = {kb4.x, kb4.y, kb4.z, kb4.w};
+        float kr[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            // keeps the widening here: hoisted next to the loads it would wait
+            // for them before the K and V loads are issued
+            asm volatile("" : "+v"(x0[e]), "+v"(x1[e]));
+            const double a0 = x0[e], a1 = x1[e];
+            kr[e] = d0 < H2 ? float(a0 * rk[e].x - a1 * rk[e].y) : float(a0 * rk[e].y + a1 * rk[e].x);
+        }
+        const float4 knew = make_float4(kr[0], kr[1], kr[2], kr[3]);
+#pragma unroll
+        for (int r = 0; r < NL; ++r) {
+            const bool mine = row0 + RS * r == pnew;
+            kv4[r].x = mine ? kr[0] : kv4[r].x;
+            kv4[r].y = mine ? kr[1] : kv4[r].y;
+            kv4[r].z = mine ? kr[2] : kv4[r].z;
+            kv4[r].w = mine ? kr[3] : kv4[r].w;
+            vv4[r].x = mine ? vnew.x : vv4[r].x;
+            vv4[r].y = mine ? vnew.y : vv4[r].y;
+            vv4[r].z = mine ? vnew.z : vv4[r].z;
+            vv4[r].w = mine ? vnew.w : vv4[r].w;
+        }
+        if (pnew >= row0 && (pnew - row0) % RS == 0) {
+            const int64_t crow = (int64_t(kvh) * max_seq + pos % max_seq) * HD;
+            *reinterpret_cast<float4*>(kc + crow + d0) = knew;
+            *reinterpret_cast<float4*>(vc + crow + d0) = vnew;
+        }
+    }
+    // scores
+    float sv[NV];
+#pragma unroll
+    for (int r = 0; r < NL; ++r)
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            float a = qv[g].x * kv4[r].x;
+            a = fmaf(qv[g].y, kv4[r].y, a);
+            a = fmaf(qv[g].z, kv4[r].z, a);
+            sv[r * G + g] = fmaf(qv[g].w, kv4[r].w, a);
+        }
+    {
+        const float s = group_scatter<LQ - 1, NV>(sv, lane);
+        constexpr int DUP = Q4 / NV;  // lanes holding each total
+        if (col % DUP == 0) {
+            const int vi = col / DUP, r = vi / G, g = vi % G, row = row0 + RS * r;
+            ss[g][row] = row < nvalid ? s * scale : -INFINITY;
+        }
+    }
+    __syncthreads();
+    // softmax over the chunk: head `wave` in the lower half wave, head wave + 4
+    // in the upper one (for G <= 4 it repeats the lower half's head and stores nothing)
+    if (wave < G) {
+        const int p = lane & 31, g = wave + 4 * (lane >> 5);
+        const int gs = g < G ? g : wave;
+        {
+            const float s = ss[gs][p];
+            const float m = half_wave_max(s);
+            const float e = p < nvalid ? expf(s - m) : 0.f;
+            const float l = half_wave_sum(e);
+            if (g < G) {
+                ss[g][p] = e;
+                if (p == 0) {
+                    float* o = part + (int64_t(kvh * G + g) * n_chunks + c) * (HD + 2);
+                    o[HD] = m;
+                    o[HD + 1] = l;
+                }
+            }
+        }
+    }
+    __syncthreads();
+    // o[g][d] = sum_p e[g][p] v[p][d]
+    float acc[NO];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        float a[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int r = 0; r < NL; ++r) {
+            const float w = ss[g][row0 + RS * r];
+            a[0] = fmaf(w, vv4[r].x, a[0]);
+            a[1] = fmaf(w, vv4[r].y, a[1]);
+            a[2] = fmaf(w, vv4[r].z, a[2]);
+            a[3] = fmaf(w, vv4[r].w, a[3]);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[4 * g + e] = a[e];
+    }
+#pragma unroll
+    for (int j = 0; j < NO / 2; ++j) acc[j] = pair_scatter<5>(acc[j], acc[j + NO / 2], lane);
+    if constexpr (LR == 2) {
+#pragma unroll
+        for (int j = 0; j < NO / 4; ++j) acc[j] = pair_scatter<4>(acc[j], acc[j + NO / 4], lane);
+    }
+#pragma unroll
+    for (int j = 0; j < NR; ++j) red[wave][j][lane] = acc[j];
+    __syncthreads();
+    for (int o = t; o < G * HD; o += 256) {
+        const int g = o / HD, d = o % HD, vi = 4 * g + (d & 3);
+        int ln = d / 4 + 32 * (vi / (NO / 2)), j = vi % (NO / 2);
+        if constexpr (LR == 2) {
+            ln += 16 * (j / (NO / 4));
+            j %= NO / 4;
+        }
+        const float s = (red[0][j][ln] + red[1][j][ln]) + (red[2][j][ln] + red[3][j][ln]);
+        part[(int64_t(kvh * G + g) * n_chunks + c) * (HD + 2) + d] = s;
     }
 }
 
@@ -591,6 +853,39 @@ void launch_combine(Decoder& d, int hd) {
         hipLaunchKernelGGL(k_attn_combine_long, grid, dim3(256), 0, d.stream, d.part, d.att, hd, nc, d.d_pos, d.c.max_seq);
 }
 
+// Attention partials of one layer: the register kernel for G = 1, 2, 4, 8
+// query heads per KV head, the LDS-tile kernel otherwise.
+void launch_attn(Decoder& d, Layer& ly, int G, float scale) {
+    const wv_decoder_config& c = d.c;
+    const dim3 ag(unsigned(c.n_kv_heads), unsigned(d.n_chunks));
+    auto reg = [&](auto kern) {
+        hipLaunchKernelGGL(kern, ag, dim3(256), 0, d.stream, d.q, ly.kc, ly.vc, d.d_pos, d.part, c.max_seq,
+                           d.n_chunks, scale, d.k, d.v, d.cs);
+    };
+    if (c.head_dim == 128) {
+        switch (G) {
+            case 1: return reg(k_attn_reg<128, 1>);
+            case 2: return reg(k_attn_reg<128, 2>);
+            case 4: return reg(k_attn_reg<128, 4>);
+            case 8: return reg(k_attn_reg<128, 8>);
+        }
+    } else {
+        switch (G) {
+            case 1: return reg(k_attn_reg<64, 1>);
+            case 2: return reg(k_attn_reg<64, 2>);
+            case 4: return reg(k_attn_reg<64, 4>);
+            case 8: return reg(k_attn_reg<64, 8>);
+        }
+    }
+    const size_t qsh = size_t(G) * c.head_dim * sizeof(float);
+    if (c.head_dim == 128)
+        hipLaunchKernelGGL(k_attn_part<128>, ag, dim3(256), qsh, d.stream, d.q, ly.kc, ly.vc, d.d_pos, d.part,
+                           c.n_heads, c.n_kv_heads, c.max_seq, d.n_chunks, scale, d.k, d.v, d.cs);
+    else
+        hipLaunchKernelGGL(k_attn_part<64>, ag, dim3(256), qsh, d.stream, d.q, ly.kc, ly.vc, d.d_pos, d.part,
+                           c.n_heads, c.n_kv_heads, c.max_seq, d.n_chunks, scale, d.k, d.v, d.cs);
+}
+
 int enqueue_step(Decoder& d, int advance) {
     const wv_decoder_config& c = d.c;
     const int hd = c.head_dim;
@@ -627,14 +922,7 @@ int enqueue_step(Decoder& d, int advance) {
             }
         }
         if (e) return e;
-        const dim3 ag(unsigned(c.n_kv_heads), unsigned(d.n_chunks));
-        const size_t qsh = size_t(G) * hd * sizeof(float);
-        if (hd == 128)
-            hipLaunchKernelGGL(k_attn_part<128>, ag, dim3(256), qsh, d.stream, d.q, ly.kc, ly.vc, d.d_pos, d.part,
-                               c.n_heads, c.n_kv_heads, c.max_seq, d.n_chunks, scale, d.k, d.v, d.cs);
-        else
-            hipLaunchKernelGGL(k_attn_part<64>, ag, dim3(256), qsh, d.stream, d.q, ly.kc, ly.vc, d.d_pos, d.part,
-                               c.n_heads, c.n_kv_heads, c.max_seq, d.n_chunks, scale, d.k, d.v, d.cs);
+        launch_attn(d, ly, G, scale);
         launch_combine(d, hd);
         if (fn) {
             e = launch_rpl_ex(ly.w[3], d.att, d.h, 1, d.stream, normed(nullptr, nullptr, RPL_ADD, d.ss_b));
