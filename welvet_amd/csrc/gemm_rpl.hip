@@ -23,6 +23,10 @@
 // the nibble extraction produces pairs; a dot product over the block does not
 // depend on the order. K is split over gridDim.z when the tile grid alone
 // would leave CUs idle; the splits' partials meet in a fixed-order sum.
+//
+// Token blocks of more than 64 use k_gemm_q4k_pw instead: W goes from the
+// planes straight into MFMA B operands (a lane swap puts the row-interleaved
+// chunks into the 32x32x16 operand layout) and only X passes through LDS.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -224,6 +228,152 @@ __global__ void __launch_bounds__(256) k_gemm_q4k(GemmArgs ga) {
         }
 }
 
+// Packed-W variant for token tiles of 128: W never passes through LDS.
+// Each of the 4 waves owns one 64-row group of the block's 256 rows and loads
+// its row group's codes straight from the row-interleaved planes (lane l = row
+// l, 16 bytes = 32 columns per chunk). One v_permlane32_swap per code-word
+// pair turns that into MFMA B operands: after swapping words 0|1 (columns
+// 0-7 | 8-15) between lanes l and l + 32, the first result holds rows 0-31
+// with columns 0-7 in lanes 0-31 and 8-15 in lanes 32-63 (the 32x32x16 B
+// layout of the first 32-row tile), the second the same for rows 32-63. Each
+// wave dequantizes only its own rows (no copy shared through LDS), so the
+// LDS carries X alone: per K-step a block writes 16 KB of fp16 X and each
+// wave reads 16 KB back for 32 MFMAs (128 tokens x 64 rows x 64 columns),
+// against 96 KB per 16 MFMAs per wave with fp16 W tiles.
+template <int TM, int D>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) k_gemm_q4k_pw(GemmArgs ga) {
+    constexpr int BM = 32 * TM;
+    constexpr int BNW = 256;                 // output rows per block: 4 waves x 64
+    constexpr int XB = BM * (BK / 8) / 256;  // 8-column X blocks per thread per K-step
+    static_assert(XB >= 1 && 4 % D == 0, "shape");
+    __shared__ __attribute__((aligned(16))) _Float16 xs[2][BM * LDK];
+
+    const RplArgs& a = ga.w;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int nblk = blockIdx.x, mblk = blockIdx.y, split = blockIdx.z;
+    const int sb0 = split * ga.sb_per_split;
+    const int sb1 = min(a.nsb, sb0 + ga.sb_per_split);
+    const int steps = (sb1 - sb0) * 4;
+    const int64_t nsb_total = int64_t(a.rg_count) * a.nsb;
+    const int kb8 = ga.K / 8;
+    const int g = min(nblk * 4 + wave, a.rg_count - 1);  // this wave's row group
+
+    struct Regs {
+        uint4 c[2];      // codes of the step's two chunks (this lane's row)
+        uint32_t mw[2];  // their metadata words (u'0, u'1, m0, m1)
+        float2 dd;       // (d, dmin) of the super-block
+        uint4 xv[XB];    // fp16 X blocks
+    };
+    auto load = [&](int s, Regs& r) {
+        const int sb = sb0 + s / 4;
+        const int64_t si = int64_t(g) * a.nsb + sb;
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) {
+            const int j = 2 * (s & 3) + jj;
+            r.c[jj] = ld_nt(reinterpret_cast<const uint4*>(a.codes) + (int64_t(j) * nsb_total + si) * 64 + lane);
+            r.mw[jj] = reinterpret_cast<const uint32_t*>(a.meta)[(si * 64 + lane) * 8 + j];
+        }
+        r.dd = reinterpret_cast<const float2*>(a.dd)[si * 64 + lane];
+        const int k8 = sb * 32 + (s & 3) * 8;
+#pragma unroll
+        for (int i = 0; i < XB; ++i) {
+            const int f = t + 256 * i, m = min(mblk * BM + f / 8, ga.M - 1);
+            r.xv[i] = ga.xh[int64_t(m) * kb8 + k8 + f % 8];
+        }
+    };
+
+    f32x16 acc[TM][2];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    Regs ring[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        load(min(d, steps - 1), ring[d]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    for (int s0 = 0; s0 < steps; s0 += D) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            const int s = s0 + d, buf = s & 1;
+#pragma unroll
+            for (int i = 0; i < XB; ++i) {
+                const int f = t + 256 * i;
+                *reinterpret_cast<uint4*>(&xs[buf][(f / 8) * LDK + 8 * (f % 8)]) = ring[d].xv[i];
+            }
+            const uint4 c0 = ring[d].c[0], c1 = ring[d].c[1];
+            const uint32_t mw0 = ring[d].mw[0], mw1 = ring[d].mw[1];
+            const float2 dd = ring[d].dd;
+            __builtin_amdgcn_sched_barrier(0);
+            load(min(s + D, steps - 1), ring[d]);
+            __builtin_amdgcn_sched_barrier(0);
+            // B operands: [chunk][tile][k16 step] as fp16 in k order [0,4,1,5,2,6,3,7]
+            half8 bf[2][2][2];
+            {
+                const auto d2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(dd.x), __float_as_uint(dd.x), false, false);
+                const auto m2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(dd.y), __float_as_uint(dd.y), false, false);
+#pragma unroll
+                for (int jj = 0; jj < 2; ++jj) {
+                    const uint4 c = jj ? c1 : c0;
+                    const uint32_t w = jj ? mw1 : mw0;
+                    const auto k0 = __builtin_amdgcn_permlane32_swap(c.x, c.y, false, false);  // columns 0-15
+                    const auto k1 = __builtin_amdgcn_permlane32_swap(c.z, c.w, false, false);  // columns 16-31
+                    const auto mt = __builtin_amdgcn_permlane32_swap(w, w, false, false);
+#pragma unroll
+                    for (int T = 0; T < 2; ++T) {
+                        const float d255 = __uint_as_float(d2[T]) * (1.0f / 255.0f);
+                        const float dm127 = __uint_as_float(m2[T]) * (1.0f / 127.0f);
+                        const uint32_t gm = mt[T];
+                        const _Float16 sc0 = _Float16(d255 * float(gm & 0xFFu));
+                        const _Float16 sc1 = _Float16(d255 * float((gm >> 8) & 0xFFu));
+                        const _Float16 mn0 = _Float16(dm127 * float(int8_t(gm >> 16)));
+                        const _Float16 mn1 = _Float16(dm127 * float(int32_t(gm) >> 24));
+                        const half2v s0 = {sc0, sc0}, s1 = {sc1, sc1}, n0 = {mn0, mn0}, n1 = {mn1, mn1};
+                        bf[jj][T][0] = __builtin_bit_cast(half8, dequant8(k0[T], s0, n0));
+                        bf[jj][T][1] = __builtin_bit_cast(half8, dequant8(k1[T], s1, n1));
+                    }
+                }
+            }
+            __syncthreads();
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+                for (int kk = 0; kk < 2; ++kk) {
+                    const int ks = 2 * jj + kk;
+                    half8 af[TM];
+#pragma unroll
+                    for (int i = 0; i < TM; ++i)
+                        af[i] = *reinterpret_cast<const half8*>(
+                            &xs[buf][(i * 32 + (lane & 31)) * LDK + ks * 16 + 8 * (lane >> 5)]);
+#pragma unroll
+                    for (int i = 0; i < TM; ++i)
+#pragma unroll
+                        for (int T = 0; T < 2; ++T)
+                            acc[i][T] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[jj][T][kk], acc[i][T], 0, 0, 0);
+                }
+        }
+    }
+
+    // C[i][j] of a 32x32 tile: lane holds j = lane % 32, i = 8*(r/4) + 4*(lane/32) + r%4.
+    float* out = ga.y + int64_t(split) * ga.M * a.rows;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int T = 0; T < 2; ++T) {
+            const int n = (nblk * 4 + wave) * 64 + T * 32 + (lane & 31);
+            if (n >= a.rows) continue;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int m = mblk * BM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                if (m < ga.M) out[int64_t(m) * a.rows + n] = acc[i][T][r];
+            }
+        }
+}
+
 // y[i] = sum_k part[k*n + i], k ascending; each thread owns 4 consecutive
 // outputs (float4 when n % 4 == 0 and y is 16-byte aligned; the partials
 // always are) and issues up to 8 splits' loads before adding them.
@@ -274,13 +424,22 @@ void launch_bm(const GemmArgs& ga, dim3 grid, hipStream_t s) {
 
 bool gemm_supported(const DevBlob& b) { return b.layout == LAYOUT_RPL && b.fmt == FMT_Q4_K; }
 
+// bm 32 / 64: k_gemm_q4k (128-row tiles); bm 128: k_gemm_q4k_pw (256-row
+// tiles, one block per CU).
 void gemm_plan(const DevBlob& b, int M, int& bm, int& splits, int& sb_per_split) {
     const RplArgs& a = b.rpl;
     bm = M <= 32 ? 32 : M <= 64 ? 64 : 128;
-    const int64_t tiles = int64_t((a.rows + BN - 1) / BN) * ((M + bm - 1) / bm);
-    // Split K only while the tile grid alone leaves CUs idle (~384 blocks fill
-    // the 256 CUs at the 1-2 blocks each that the register/LDS budget allows).
-    int want = int(std::max<int64_t>(1, (384 + tiles - 1) / tiles));
+    int want = 1;
+    if (bm == 128) {
+        // Split K while whole tiles leave CUs idle, never past one block per CU.
+        const int64_t tiles = int64_t((a.rows + 255) / 256) * ((M + 127) / 128);
+        want = int(std::max<int64_t>(1, 256 / tiles));
+    } else {
+        const int64_t tiles = int64_t((a.rows + BN - 1) / BN) * ((M + bm - 1) / bm);
+        // Split K only while the tile grid alone leaves CUs idle (~384 blocks fill
+        // the 256 CUs at the 1-2 blocks each that the register/LDS budget allows).
+        want = int(std::max<int64_t>(1, (384 + tiles - 1) / tiles));
+    }
     want = std::min(want, std::max(1, a.nsb / 2));  // each split >= 2 super-blocks
     sb_per_split = (a.nsb + want - 1) / want;
     splits = (a.nsb + sb_per_split - 1) / sb_per_split;
@@ -318,10 +477,14 @@ int launch_gemm(const DevBlob& b, const float* d_x, float* d_y, int M, void* str
     ga.M = M;
     ga.K = int(b.cols);
     ga.sb_per_split = per;
-    dim3 grid(unsigned((b.rows + BN - 1) / BN), unsigned((M + bm - 1) / bm), unsigned(splits));
-    if (bm == 32) launch_bm<32, 1>(ga, grid, s);
-    else if (bm == 64) launch_bm<64, 2>(ga, grid, s);
-    else launch_bm<128, 2>(ga, grid, s);
+    if (bm == 128) {
+        const dim3 grid(unsigned((b.rows + 255) / 256), unsigned((M + 127) / 128), unsigned(splits));
+        hipLaunchKernelGGL((k_gemm_q4k_pw<4, 4>), grid, dim3(256), 0, s, ga);
+    } else {
+        const dim3 grid(unsigned((b.rows + BN - 1) / BN), unsigned((M + bm - 1) / bm), unsigned(splits));
+        if (bm == 32) launch_bm<32, 1>(ga, grid, s);
+        else launch_bm<64, 2>(ga, grid, s);
+    }
     if (splits > 1) {
         const int64_t n = int64_t(M) * b.rows;
         hipLaunchKernelGGL(k_split_sum, dim3(unsigned((n / 4 + 1 + 255) / 256)), dim3(256), 0, s, part, d_y, n, splits);
