@@ -70,6 +70,25 @@ __device__ __forceinline__ uint4 dequant8(uint32_t v, half2v sc, half2v mn) {
     return make_uint4(p[0], p[1], p[2], p[3]);
 }
 
+// The same 8 weights in k order [0,2,4,6,1,3,5,7]: the even and odd nibbles
+// are masked to bytes once each, and v_perm_b32 interleaves two of those bytes
+// with the 0x64 exponent byte per half2 (7 instructions for the spread
+// instead of 11).
+__device__ __forceinline__ uint4 dequant8p(uint32_t v, half2v sc, half2v mn) {
+    const half2v k1024 = {_Float16(1024.0f), _Float16(1024.0f)};
+    const uint32_t lo = v & 0x0F0F0F0Fu, hi = (v >> 4) & 0x0F0F0F0Fu;
+    const uint32_t e = 0x64646464u;
+    const uint32_t hb[4] = {__builtin_amdgcn_perm(e, lo, 0x04010400u), __builtin_amdgcn_perm(e, lo, 0x04030402u),
+                            __builtin_amdgcn_perm(e, hi, 0x04010400u), __builtin_amdgcn_perm(e, hi, 0x04030402u)};
+    uint32_t p[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const half2v q = __builtin_bit_cast(half2v, hb[i]) - k1024;
+        p[i] = __builtin_bit_cast(uint32_t, q * sc + mn);
+    }
+    return make_uint4(p[0], p[1], p[2], p[3]);
+}
+
 struct GemmArgs {
     RplArgs w;
     const uint4* xh;  // [M][K/8] fp16 8-column blocks in permuted k order (BM >= 64)
@@ -79,12 +98,17 @@ struct GemmArgs {
     int sb_per_split;
 };
 
-// X f32 [n8 blocks of 8] -> fp16 blocks in k order [0,4,1,5,2,6,3,7].
+// X f32 [n8 blocks of 8] -> fp16 blocks in k order [0,4,1,5,2,6,3,7]
+// (dequant8, ORD 0) or [0,2,4,6,1,3,5,7] (dequant8p, ORD 1).
+template <int ORD>
 __global__ void __launch_bounds__(256) k_x_f16(const float4* __restrict__ x, uint4* __restrict__ xh, int64_t n8) {
     const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
     if (i >= n8) return;
     const float4 lo = x[2 * i], hi = x[2 * i + 1];
-    xh[i] = make_uint4(pack_h2(lo.x, hi.x), pack_h2(lo.y, hi.y), pack_h2(lo.z, hi.z), pack_h2(lo.w, hi.w));
+    if constexpr (ORD == 0)
+        xh[i] = make_uint4(pack_h2(lo.x, hi.x), pack_h2(lo.y, hi.y), pack_h2(lo.z, hi.z), pack_h2(lo.w, hi.w));
+    else
+        xh[i] = make_uint4(pack_h2(lo.x, lo.z), pack_h2(hi.x, hi.z), pack_h2(lo.y, lo.w), pack_h2(hi.y, hi.w));
 }
 
 template <int BM, int WM, int D>
@@ -311,7 +335,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
             __builtin_amdgcn_sched_barrier(0);
             load(min(s + D, steps - 1), ring[d]);
             __builtin_amdgcn_sched_barrier(0);
-            // B operands: [chunk][tile][k16 step] as fp16 in k order [0,4,1,5,2,6,3,7]
+            // B operands: [chunk][tile][k16 step] as fp16 in k order [0,2,4,6,1,3,5,7]
             half8 bf[2][2][2];
             {
                 const auto d2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(dd.x), __float_as_uint(dd.x), false, false);
@@ -333,8 +357,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
                         const _Float16 mn0 = _Float16(dm127 * float(int8_t(gm >> 16)));
                         const _Float16 mn1 = _Float16(dm127 * float(int32_t(gm) >> 24));
                         const half2v s0 = {sc0, sc0}, s1 = {sc1, sc1}, n0 = {mn0, mn0}, n1 = {mn1, mn1};
-                        bf[jj][T][0] = __builtin_bit_cast(half8, dequant8(k0[T], s0, n0));
-                        bf[jj][T][1] = __builtin_bit_cast(half8, dequant8(k1[T], s1, n1));
+                        bf[jj][T][0] = __builtin_bit_cast(half8, dequant8p(k0[T], s0, n0));
+                        bf[jj][T][1] = __builtin_bit_cast(half8, dequant8p(k1[T], s1, n1));
                     }
                 }
             }
@@ -466,8 +490,12 @@ int launch_gemm(const DevBlob& b, const float* d_x, float* d_y, int M, void* str
         const int64_t n8 = int64_t(M) * b.cols / 8;
         xh = reinterpret_cast<uint4*>(d_scratch);
         part = d_scratch + (size_t(M) * size_t(b.cols) / 2 + 63) / 64 * 64;
-        hipLaunchKernelGGL(k_x_f16, dim3(unsigned((n8 + 255) / 256)), dim3(256), 0, s,
-                           reinterpret_cast<const float4*>(d_x), xh, n8);
+        if (bm == 128)
+            hipLaunchKernelGGL(k_x_f16<1>, dim3(unsigned((n8 + 255) / 256)), dim3(256), 0, s,
+                               reinterpret_cast<const float4*>(d_x), xh, n8);
+        else
+            hipLaunchKernelGGL(k_x_f16<0>, dim3(unsigned((n8 + 255) / 256)), dim3(256), 0, s,
+                               reinterpret_cast<const float4*>(d_x), xh, n8);
     }
     GemmArgs ga;
     ga.w = b.rpl;
