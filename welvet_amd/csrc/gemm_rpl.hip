@@ -448,15 +448,17 @@ void launch_bm(const GemmArgs& ga, dim3 grid, hipStream_t s) {
 
 bool gemm_supported(const DevBlob& b) { return b.layout == LAYOUT_RPL && b.fmt == FMT_Q4_K; }
 
-// bm 32 / 64: k_gemm_q4k (128-row tiles); bm 128: k_gemm_q4k_pw (256-row
-// tiles, one block per CU).
+// Token tiles from kPwMin up run k_gemm_q4k_pw (256-row tiles, one block per
+// CU); smaller ones k_gemm_q4k (128-row tiles). At M = 32 both kernels take
+// 20.5 us, and k_gemm_q4k needs no fp16 copy of X.
+constexpr int kPwMin = 128;
 void gemm_plan(const DevBlob& b, int M, int& bm, int& splits, int& sb_per_split) {
     const RplArgs& a = b.rpl;
     bm = M <= 32 ? 32 : M <= 64 ? 64 : 128;
     int want = 1;
-    if (bm == 128) {
+    if (bm >= kPwMin) {
         // Split K while whole tiles leave CUs idle, never past one block per CU.
-        const int64_t tiles = int64_t((a.rows + 255) / 256) * ((M + 127) / 128);
+        const int64_t tiles = int64_t((a.rows + 255) / 256) * ((M + bm - 1) / bm);
         want = int(std::max<int64_t>(1, 256 / tiles));
     } else {
         const int64_t tiles = int64_t((a.rows + BN - 1) / BN) * ((M + bm - 1) / bm);
@@ -474,7 +476,7 @@ void gemm_plan(const DevBlob& b, int M, int& bm, int& splits, int& sb_per_split)
 size_t gemm_scratch_floats(const DevBlob& b, int M) {
     int bm = 0, splits = 1, per = 0;
     gemm_plan(b, M, bm, splits, per);
-    const size_t xh = bm == 32 ? 0 : (size_t(M) * size_t(b.cols) / 2 + 63) / 64 * 64;
+    const size_t xh = bm == 32 && bm < kPwMin ? 0 : (size_t(M) * size_t(b.cols) / 2 + 63) / 64 * 64;
     return xh + (splits > 1 ? size_t(splits) * size_t(M) * size_t(b.rows) : 0);
 }
 
@@ -486,11 +488,12 @@ int launch_gemm(const DevBlob& b, const float* d_x, float* d_y, int M, void* str
     if (gemm_scratch_floats(b, M) && !d_scratch) return int(hipErrorInvalidValue);
     uint4* xh = nullptr;
     float* part = d_scratch;
-    if (bm != 32) {
+    const bool pw = bm >= kPwMin;
+    if (bm != 32 || pw) {
         const int64_t n8 = int64_t(M) * b.cols / 8;
         xh = reinterpret_cast<uint4*>(d_scratch);
         part = d_scratch + (size_t(M) * size_t(b.cols) / 2 + 63) / 64 * 64;
-        if (bm == 128)
+        if (pw)
             hipLaunchKernelGGL(k_x_f16<1>, dim3(unsigned((n8 + 255) / 256)), dim3(256), 0, s,
                                reinterpret_cast<const float4*>(d_x), xh, n8);
         else
@@ -505,8 +508,9 @@ int launch_gemm(const DevBlob& b, const float* d_x, float* d_y, int M, void* str
     ga.M = M;
     ga.K = int(b.cols);
     ga.sb_per_split = per;
-    if (bm == 128) {
-        const dim3 grid(unsigned((b.rows + 255) / 256), unsigned((M + 127) / 128), unsigned(splits));
+    if (pw) {
+        const dim3 grid(unsigned((b.rows + 255) / 256), unsigned((M + bm - 1) / bm), unsigned(splits));
+        static_assert(kPwMin == 128, "token tiles below 128 would need k_gemm_q4k_pw<bm / 32, 4>");
         hipLaunchKernelGGL((k_gemm_q4k_pw<4, 4>), grid, dim3(256), 0, s, ga);
     } else {
         const dim3 grid(unsigned((b.rows + BN - 1) / BN), unsigned((M + bm - 1) / bm), unsigned(splits));
