@@ -110,7 +110,7 @@ def test_prefill_q4k_baseline(shape, m):
     assert err <= TOL_MFMA
 
 
-@pytest.mark.parametrize("fmt", ["Q8_0", "Q6_K", "IQ4_NL"])
+@pytest.mark.parametrize("fmt", ["Q8_0", "Q6_K", "Q5_K", "IQ4_NL"])
 def test_prefill_other_formats_use_batched_gemv(fmt):
     rows, cols, m = 300, 1024, 9
     print(f"[gpu] prefill {fmt} via batched gemv", flush=True)

@@ -47,6 +47,8 @@ __device__ __forceinline__ uint2 ld_stream(const uint2* p) {
     return make_uint2(v.x, v.y);
 }
 
+__device__ __forceinline__ uint32_t ld_stream(const uint32_t* p) { return __builtin_nontemporal_load(p); }
+
 __device__ __forceinline__ float ub0(uint32_t v) { return float(v & 0xFFu); }
 __device__ __forceinline__ float ub1(uint32_t v) { return float((v >> 8) & 0xFFu); }
 __device__ __forceinline__ float ub2(uint32_t v) { return float((v >> 16) & 0xFFu); }
@@ -155,6 +157,43 @@ struct RplQ4KI : RplQ4K {
         const uint32_t gx = g ^ 0x80800000u;
         const float mn = fmaf(ub3(gx), xm.z, fmaf(ub2(gx), xm.y, xm.w));
         const float sc = sb.d255 * 255.0f * xm.x;  // d * 2^-s / 255
+        return fmaf(sc, fmaf(ub1(g), float(T1), ub0(g) * float(T0)), sb.dm127 * mn);
+    }
+};
+
+// Q5_K: the low 4 code bits as Q4_K's nibbles, plus a 32-bit plane per chunk
+// with the fifth bits. Byte b of that plane holds, at bit s, the fifth bit of
+// the code in byte b of spread word s = 2*word + nibble half, so that
+// ((h >> s) & 0x01010101) << 4 completes spread word s. Codes reach 31: a
+// 16-column group sum stays below 16*31*2^22 < 2^31, exact in int32.
+struct RplQ5KI : RplQ4KI {
+    struct Ch { uint4 c; uint32_t h; };
+    static __device__ __forceinline__ Ch load_ch(const RplArgs& a, int64_t ci, int lane) {
+        return {ld_stream(reinterpret_cast<const uint4*>(a.codes) + ci * 64 + lane),
+                ld_stream(reinterpret_cast<const uint32_t*>(a.hi) + ci * 64 + lane)};
+    }
+    static __device__ __forceinline__ float dot_i(const Ch& ch, const Sb& sb, int j, const uint32_t* xi, float4 xm) {
+        const uint32_t gw[8] = {sb.g0.x, sb.g0.y, sb.g0.z, sb.g0.w, sb.g1.x, sb.g1.y, sb.g1.z, sb.g1.w};
+        const uint32_t g = gw[j];
+        const uint32_t wd[4] = {ch.c.x, ch.c.y, ch.c.z, ch.c.w};
+        int A[2][3] = {{0, 0, 0}, {0, 0, 0}};
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const int gi = w >> 1;
+            const uint32_t lo = (wd[w] & 0x0F0F0F0Fu) | (((ch.h >> (2 * w)) & 0x01010101u) << 4);
+            const uint32_t hi = ((wd[w] >> 4) & 0x0F0F0F0Fu) | (((ch.h >> (2 * w + 1)) & 0x01010101u) << 4);
+            A[gi][0] = int(__builtin_amdgcn_udot4(lo, xi[w], uint32_t(A[gi][0]), false));
+            A[gi][0] = int(__builtin_amdgcn_udot4(hi, xi[4 + w], uint32_t(A[gi][0]), false));
+            A[gi][1] = int(__builtin_amdgcn_udot4(lo, xi[8 + w], uint32_t(A[gi][1]), false));
+            A[gi][1] = int(__builtin_amdgcn_udot4(hi, xi[12 + w], uint32_t(A[gi][1]), false));
+            A[gi][2] = __builtin_amdgcn_sdot4(int(lo), int(xi[16 + w]), A[gi][2], false);
+            A[gi][2] = __builtin_amdgcn_sdot4(int(hi), int(xi[20 + w]), A[gi][2], false);
+        }
+        const int T0 = A[0][0] + (A[0][1] << 8) + (A[0][2] << 16);
+        const int T1 = A[1][0] + (A[1][1] << 8) + (A[1][2] << 16);
+        const uint32_t gx = g ^ 0x80800000u;
+        const float mn = fmaf(ub3(gx), xm.z, fmaf(ub2(gx), xm.y, xm.w));
+        const float sc = sb.d255 * 255.0f * xm.x;
         return fmaf(sc, fmaf(ub1(g), float(T1), ub0(g) * float(T0)), sb.dm127 * mn);
     }
 };
@@ -727,6 +766,41 @@ struct TQ4K : RplQ4K {
     }
 };
 
+struct TQ5K : RplQ5KI {
+    using TM = TQ4K::TM;
+    static __device__ __forceinline__ TM load_tm(const RplArgs& a, int64_t si, int lane, int jp) {
+        return TQ4K::load_tm(a, si, lane, jp);
+    }
+    // the 8 codes of code word w: low nibbles plus the fifth bits of spread
+    // words f0 (even codes) and f0 + 1 (odd codes), as in RplQ5KI::dot_i
+    static __device__ __forceinline__ void tacc5(uint32_t w, uint32_t h, int f0, float coef, float* acc) {
+        uint32_t lo = (w & 0x0F0F0F0Fu) | (((h >> f0) & 0x01010101u) << 4);
+        uint32_t hi = ((w >> 4) & 0x0F0F0F0Fu) | (((h >> (f0 + 1)) & 0x01010101u) << 4);
+        asm("" : "+v"(lo), "+v"(hi));
+        acc[0] = fmaf(ub0(lo), coef, acc[0]);
+        acc[1] = fmaf(ub0(hi), coef, acc[1]);
+        acc[2] = fmaf(ub1(lo), coef, acc[2]);
+        acc[3] = fmaf(ub1(hi), coef, acc[3]);
+        acc[4] = fmaf(ub2(lo), coef, acc[4]);
+        acc[5] = fmaf(ub2(hi), coef, acc[5]);
+        acc[6] = fmaf(ub3(lo), coef, acc[6]);
+        acc[7] = fmaf(ub3(hi), coef, acc[7]);
+    }
+    template <int jj>
+    static __device__ __forceinline__ void tacc(const Ch& ch, const TM& t, float gy, float* acc, float* off) {
+        const uint32_t g = jj ? t.g.y : t.g.x;
+        const float gd = gy * (t.dd.x * (1.0f / 255.0f));
+        const float c0 = gd * ub0(g), c1 = gd * ub1(g);
+        const float gm = gy * (t.dd.y * (1.0f / 127.0f));
+        off[0] = fmaf(gm, float(int8_t(g >> 16)), off[0]);
+        off[1] = fmaf(gm, float(int32_t(g) >> 24), off[1]);
+        tacc5(ch.c.x, ch.h, 0, c0, acc);
+        tacc5(ch.c.y, ch.h, 2, c0, acc + 8);
+        tacc5(ch.c.z, ch.h, 4, c1, acc + 16);
+        tacc5(ch.c.w, ch.h, 6, c1, acc + 24);
+    }
+};
+
 struct TQ6K : RplQ6K {
     struct TM { uint32_t g; float d; };  // (u'0,u'1) of chunk 2jp | (u'0,u'1) of 2jp+1 << 16
     static __device__ __forceinline__ TM load_tm(const RplArgs& a, int64_t si, int lane, int jp) {
@@ -947,6 +1021,7 @@ int launch_rpl_ex(const DevBlob& b, const float* d_x, float* d_y, int batch, voi
     switch (b.fmt) {
     case FMT_Q4_K:
         return int_x() ? launch_rpl_t<RplQ4KI>(b, d_x, d_y, batch, s, ex) : launch_rpl_t<RplQ4K>(b, d_x, d_y, batch, s, ex);
+    case FMT_Q5_K: return launch_rpl_t<RplQ5KI>(b, d_x, d_y, batch, s, ex);
     case FMT_Q6_K: return launch_rpl_t<RplQ6K>(b, d_x, d_y, batch, s, ex);
     case FMT_Q8_0: return launch_rpl_t<RplQ8>(b, d_x, d_y, batch, s, ex);
     case FMT_Q4_0: return launch_rpl_t<RplQ4>(b, d_x, d_y, batch, s, ex);
@@ -970,6 +1045,7 @@ struct RplItems {
 bool rpl_items(int fmt, RplItems& it) {
     switch (fmt) {
     case FMT_Q4_K: it = {16, 0, 32, 8}; return true;
+    case FMT_Q5_K: it = {16, 4, 32, 8}; return true;
     case FMT_Q6_K: it = {16, 8, 16, 8}; return true;
     case FMT_Q8_0: it = {32, 0, 32, 0}; return true;
     case FMT_Q4_0: it = {16, 0, 32, 0}; return true;
@@ -978,7 +1054,7 @@ bool rpl_items(int fmt, RplItems& it) {
 }
 
 // dst[p][G][sb][L] = (L even ? a : b)[p][G/2][sb][32*(G%2) + L/2], items of
-// isz bytes (a multiple of 8), G < 2*rg_in: rows 2i / 2i+1 <- a / b row i.
+// isz bytes (a multiple of 4), G < 2*rg_in: rows 2i / 2i+1 <- a / b row i.
 __global__ void __launch_bounds__(256) k_rpl_pairs(uint8_t* __restrict__ dst, const uint8_t* __restrict__ a,
                                                    const uint8_t* __restrict__ b, int isz, int64_t rg_in, int64_t nsb,
                                                    int64_t planes) {
@@ -993,9 +1069,9 @@ __global__ void __launch_bounds__(256) k_rpl_pairs(uint8_t* __restrict__ dst, co
     const int64_t p = r / (2 * rg_in);
     const uint8_t* src = (L & 1) ? b : a;
     const int64_t si = ((p * rg_in + G / 2) * nsb + sb) * 64 + 32 * (G & 1) + (L >> 1);
-    const uint2* s2 = reinterpret_cast<const uint2*>(src + si * isz);
-    uint2* d2 = reinterpret_cast<uint2*>(dst + i * isz);
-    for (int k = 0; k < isz / 8; ++k) d2[k] = s2[k];
+    const uint32_t* s4 = reinterpret_cast<const uint32_t*>(src + si * isz);
+    uint32_t* d4 = reinterpret_cast<uint32_t*>(dst + i * isz);
+    for (int k = 0; k < isz / 4; ++k) d4[k] = s4[k];
 }
 
 struct FusedLayout {
@@ -1135,6 +1211,7 @@ int launch_rpl_matvec_t(const DevBlob& b, const float* d_gy, float* d_gx, int ba
     hipStream_t s = static_cast<hipStream_t>(stream);
     switch (b.fmt) {
     case FMT_Q4_K: return launch_rpl_tr<TQ4K>(b, d_gy, d_gx, batch, s);
+    case FMT_Q5_K: return launch_rpl_tr<TQ5K>(b, d_gy, d_gx, batch, s);
     case FMT_Q6_K: return launch_rpl_tr<TQ6K>(b, d_gy, d_gx, batch, s);
     case FMT_Q8_0: return launch_rpl_tr<TQ8>(b, d_gy, d_gx, batch, s);
     case FMT_Q4_0: return launch_rpl_tr<TQ4>(b, d_gy, d_gx, batch, s);

@@ -94,16 +94,18 @@ struct Image {
     }
 };
 
-// Row-interleaved layout for Q4_K / Q6_K / Q8_0 / Q4_0 (requires cols % 256
-// == 0): rows are grouped 64 at a time, one per lane of a wave, and every
+// Row-interleaved layout for Q4_K / Q5_K / Q6_K / Q8_0 / Q4_0 (requires cols
+// % 256 == 0): rows are grouped 64 at a time, one per lane of a wave, and every
 // plane is stored [row group][chunk or super-block][lane][bytes] so that one
 // wave-wide load reads contiguous memory. Byte count per 256 weights equals
-// the reference blob's (Q4_K 168, Q6_K 216, Q8_0 288, Q4_0 160); rows past
+// the reference blob's (Q4_K 168, Q5_K 200, Q6_K 216, Q8_0 288, Q4_0 160); rows past
 // `rows` in the last group are zero (d = 0 / scale = 0, contributing 0).
 //   Q4_K: codes 16 B/chunk (LSB-first nibbles, as in the blob); meta per
 //         super-block 8 words (u'(2p), u'(2p+1), m(2p), m(2p+1)); dd (d, dmin).
 //         u' = max(u, 1): d*u/255 with u = 0 falls back to d/255
 //         (quant/kquant.go:179-182), the value u = 1 gives.
+//   Q5_K: low 4 code bits 16 B/chunk; fifth bits 4 B/chunk arranged for the
+//         kernel's byte spread; meta and dd as Q4_K.
 //   Q6_K: low 4 code bits 16 B/chunk; high 2 bits 8 B/chunk arranged for
 //         the kernel's byte spread; meta 8 u16 (u'(2p), u'(2p+1)); dd.
 //   Q8_0 / Q4_0: codes 32 / 16 B per 32-block; meta 8 f32 block scales.
@@ -115,9 +117,10 @@ struct RplOffsets {
 void build_rpl(int fmt, const uint8_t* raw, int64_t rows, int64_t cols, Image& img, RplOffsets& o) {
     const int64_t rg = (rows + 63) / 64, nch = cols / 32, nsb = cols / 256;
     const int cb = fmt == FMT_Q8_0 ? 32 : 16, mb = fmt == FMT_Q6_K ? 16 : 32;
-    const bool kq = fmt == FMT_Q4_K || fmt == FMT_Q6_K;
+    const bool kq = fmt == FMT_Q4_K || fmt == FMT_Q5_K || fmt == FMT_Q6_K;
     o.codes = img.add(size_t(rg * nch * 64 * cb));
     if (fmt == FMT_Q6_K) o.hi = img.add(size_t(rg * nch * 64 * 8));
+    if (fmt == FMT_Q5_K) o.hi = img.add(size_t(rg * nch * 64 * 4));
     o.meta = img.add(size_t(rg * nsb * 64 * mb));
     if (kq) o.dd = img.add(size_t(rg * nsb * 64 * 8));
     uint8_t* base = img.bytes.data();
@@ -149,6 +152,26 @@ void build_rpl(int fmt, const uint8_t* raw, int64_t rows, int64_t cols, Image& i
                                 m[4 * p + 2] = o8[24 + 2 * p];
                                 m[4 * p + 3] = o8[25 + 2 * p];
                                 std::memcpy(codes + ci * 16, o8 + 40 + 16 * p, 16);
+                            } else if (fmt == FMT_Q5_K) {
+                                m[4 * p] = u0;
+                                m[4 * p + 1] = u1;
+                                m[4 * p + 2] = o8[24 + 2 * p];
+                                m[4 * p + 3] = o8[25 + 2 * p];
+                                const uint8_t* q = o8 + 40;  // 160 B of 5-bit codes
+                                uint8_t qv[32];
+                                for (int k = 0; k < 32; ++k) {  // LSB-first stream (helpers.go:140-149)
+                                    const int bit = (p * 32 + k) * 5;
+                                    const uint32_t v = q[bit >> 3] | ((bit >> 3) + 1 < 160 ? uint32_t(q[(bit >> 3) + 1]) << 8 : 0u);
+                                    qv[k] = uint8_t((v >> (bit & 7)) & 31u);
+                                }
+                                uint8_t* c = codes + ci * 16;
+                                for (int k = 0; k < 16; ++k) c[k] = uint8_t((qv[2 * k] & 15) | ((qv[2 * k + 1] & 15) << 4));
+                                // byte b, bit s of the fifth-bit word: code 8w + 2b + half, s = 2w + half
+                                uint8_t* h = hi + ci * 4;
+                                std::memset(h, 0, 4);
+                                for (int sw = 0; sw < 8; ++sw)
+                                    for (int b = 0; b < 4; ++b)
+                                        h[b] |= uint8_t(((qv[8 * (sw >> 1) + 2 * b + (sw & 1)] >> 4) & 1) << sw);
                             } else {
                                 m[2 * p] = u0;
                                 m[2 * p + 1] = u1;
@@ -385,7 +408,8 @@ int wv_blob_upload(int format, int64_t rows, int64_t cols, int32_t block_weights
         if (cols > 32768) return fail(WV_E_SHAPE, "wv_blob_upload: native ternary cols %lld > 32768", (long long)cols);
         o_codes = img.add(size_t(need));
         std::memcpy(img.bytes.data() + o_codes, raw, size_t(need));
-    } else if (!raw_only && (format == FMT_Q4_K || format == FMT_Q6_K || format == FMT_Q8_0 || format == FMT_Q4_0) &&
+    } else if (!raw_only &&
+               (format == FMT_Q4_K || format == FMT_Q5_K || format == FMT_Q6_K || format == FMT_Q8_0 || format == FMT_Q4_0) &&
                cols % 256 == 0) {
         b.layout = LAYOUT_RPL;
         build_rpl(format, raw, rows, cols, img, ro);
