@@ -64,7 +64,7 @@ PREFILL = {
 # name -> (format, rows, cols, description); rows = the layer's out, cols = its in.
 MATVECT = {
     f"{f.lower()}_t_{i}x{o}": (f, o, i, f"{f} MatVecT of the {i}->{o} weight (gx[{i}] += W^T gy[{o}]) b=1")
-    for f in ("Q4_K", "Q6_K", "Q8_0", "Q5_K", "Q4_1", "IQ4_NL") for (i, o) in ((4096, 14336), (14336, 4096))
+    for f in ("Q4_K", "Q6_K", "Q8_0", "Q5_K", "Q3_K", "Q2_K", "Q4_1", "IQ4_NL") for (i, o) in ((4096, 14336), (14336, 4096))
 }
 MFMA_F16_PEAK_TFLOPS = 2500.0
 # 32-layer decoder, hidden 4096, 32/8 heads x 128, SwiGLU 14336, vocab 32000, Q4_K, KV 2048

@@ -79,7 +79,7 @@ def check_against_oracle(dec, ref, token, pos, steps):
     return toks
 
 
-@pytest.mark.parametrize("fmt", ["Q4_K", "Q5_K", "Q8_0"])
+@pytest.mark.parametrize("fmt", ["Q4_K", "Q5_K", "Q8_0", "Q3_K"])
 def test_decode_small_hd64(fmt):
     """2 layers, GQA 4/2, head_dim 64; the steps cross a 32-position chunk boundary (positions 62-65)."""
     print(f"[gpu] decode small hd64 {fmt}", flush=True)

@@ -161,27 +161,50 @@ struct RplQ4KI : RplQ4K {
     }
 };
 
-// Q5_K: the low 4 code bits as Q4_K's nibbles, plus a 32-bit plane per chunk
-// with the fifth bits. Byte b of that plane holds, at bit s, the fifth bit of
-// the code in byte b of spread word s = 2*word + nibble half, so that
-// ((h >> s) & 0x01010101) << 4 completes spread word s. Codes reach 31: a
-// 16-column group sum stays below 16*31*2^22 < 2^31, exact in int32.
-struct RplQ5KI : RplQ4KI {
+// Q2_K, Q3_K and Q5_K with the int-dot x planes of RplQ4KI. A chunk's codes
+// are rebuilt as the 8 spread words of Q4_K (spread word s = 2*word + half
+// holds, in byte b, the code of column 8*(s/2) + 2b + s%2), from:
+//   B = 5: the low nibbles as in Q4_K, plus a 32-bit plane whose byte b holds
+//          at bit s the fifth bit of that code: ((h >> s) & 0x01010101) << 4;
+//   B = 2, 3: a 64-bit plane of the low two bits, dword s/4 holding at bits
+//          2(s%4)..2(s%4)+1 of byte b the code of spread word s, plus for
+//          B = 3 the third bits as B = 5's fifth bits, shifted by 2.
+// Codes reach 2^B - 1 <= 31: a 16-column group sum stays below
+// 16*31*2^22 < 2^31, exact in int32.
+template <int B>
+struct RplKxI : RplQ4KI {
     struct Ch { uint4 c; uint32_t h; };
     static __device__ __forceinline__ Ch load_ch(const RplArgs& a, int64_t ci, int lane) {
-        return {ld_stream(reinterpret_cast<const uint4*>(a.codes) + ci * 64 + lane),
-                ld_stream(reinterpret_cast<const uint32_t*>(a.hi) + ci * 64 + lane)};
+        Ch r;
+        if constexpr (B == 5) {
+            r.c = ld_stream(reinterpret_cast<const uint4*>(a.codes) + ci * 64 + lane);
+        } else {
+            const uint2 v = ld_stream(reinterpret_cast<const uint2*>(a.codes) + ci * 64 + lane);
+            r.c = make_uint4(v.x, v.y, 0u, 0u);
+        }
+        r.h = B == 2 ? 0u : ld_stream(reinterpret_cast<const uint32_t*>(a.hi) + ci * 64 + lane);
+        return r;
+    }
+    // spread word s of the chunk (s a compile-time constant after unrolling)
+    static __device__ __forceinline__ uint32_t spread(const Ch& ch, int s) {
+        const uint32_t wd[4] = {ch.c.x, ch.c.y, ch.c.z, ch.c.w};
+        if constexpr (B == 5) {
+            const uint32_t nib = (s & 1) ? (wd[s >> 1] >> 4) & 0x0F0F0F0Fu : wd[s >> 1] & 0x0F0F0F0Fu;
+            return nib | (((ch.h >> s) & 0x01010101u) << 4);
+        } else {
+            const uint32_t lo2 = (wd[s >> 2] >> (2 * (s & 3))) & 0x03030303u;
+            if constexpr (B == 2) return lo2;
+            else return lo2 | (((ch.h >> s) & 0x01010101u) << 2);
+        }
     }
     static __device__ __forceinline__ float dot_i(const Ch& ch, const Sb& sb, int j, const uint32_t* xi, float4 xm) {
         const uint32_t gw[8] = {sb.g0.x, sb.g0.y, sb.g0.z, sb.g0.w, sb.g1.x, sb.g1.y, sb.g1.z, sb.g1.w};
         const uint32_t g = gw[j];
-        const uint32_t wd[4] = {ch.c.x, ch.c.y, ch.c.z, ch.c.w};
         int A[2][3] = {{0, 0, 0}, {0, 0, 0}};
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
             const int gi = w >> 1;
-            const uint32_t lo = (wd[w] & 0x0F0F0F0Fu) | (((ch.h >> (2 * w)) & 0x01010101u) << 4);
-            const uint32_t hi = ((wd[w] >> 4) & 0x0F0F0F0Fu) | (((ch.h >> (2 * w + 1)) & 0x01010101u) << 4);
+            const uint32_t lo = spread(ch, 2 * w), hi = spread(ch, 2 * w + 1);
             A[gi][0] = int(__builtin_amdgcn_udot4(lo, xi[w], uint32_t(A[gi][0]), false));
             A[gi][0] = int(__builtin_amdgcn_udot4(hi, xi[4 + w], uint32_t(A[gi][0]), false));
             A[gi][1] = int(__builtin_amdgcn_udot4(lo, xi[8 + w], uint32_t(A[gi][1]), false));
@@ -766,16 +789,16 @@ struct TQ4K : RplQ4K {
     }
 };
 
-struct TQ5K : RplQ5KI {
+template <int B>
+struct TKx : RplKxI<B> {
+    using Ch = typename RplKxI<B>::Ch;
     using TM = TQ4K::TM;
     static __device__ __forceinline__ TM load_tm(const RplArgs& a, int64_t si, int lane, int jp) {
         return TQ4K::load_tm(a, si, lane, jp);
     }
-    // the 8 codes of code word w: low nibbles plus the fifth bits of spread
-    // words f0 (even codes) and f0 + 1 (odd codes), as in RplQ5KI::dot_i
-    static __device__ __forceinline__ void tacc5(uint32_t w, uint32_t h, int f0, float coef, float* acc) {
-        uint32_t lo = (w & 0x0F0F0F0Fu) | (((h >> f0) & 0x01010101u) << 4);
-        uint32_t hi = ((w >> 4) & 0x0F0F0F0Fu) | (((h >> (f0 + 1)) & 0x01010101u) << 4);
+    // the 8 codes of code word w (spread words 2w, 2w + 1), column order
+    static __device__ __forceinline__ void tacc_w(const Ch& ch, int w, float coef, float* acc) {
+        uint32_t lo = RplKxI<B>::spread(ch, 2 * w), hi = RplKxI<B>::spread(ch, 2 * w + 1);
         asm("" : "+v"(lo), "+v"(hi));
         acc[0] = fmaf(ub0(lo), coef, acc[0]);
         acc[1] = fmaf(ub0(hi), coef, acc[1]);
@@ -794,10 +817,10 @@ struct TQ5K : RplQ5KI {
         const float gm = gy * (t.dd.y * (1.0f / 127.0f));
         off[0] = fmaf(gm, float(int8_t(g >> 16)), off[0]);
         off[1] = fmaf(gm, float(int32_t(g) >> 24), off[1]);
-        tacc5(ch.c.x, ch.h, 0, c0, acc);
-        tacc5(ch.c.y, ch.h, 2, c0, acc + 8);
-        tacc5(ch.c.z, ch.h, 4, c1, acc + 16);
-        tacc5(ch.c.w, ch.h, 6, c1, acc + 24);
+        tacc_w(ch, 0, c0, acc);
+        tacc_w(ch, 1, c0, acc + 8);
+        tacc_w(ch, 2, c1, acc + 16);
+        tacc_w(ch, 3, c1, acc + 24);
     }
 };
 
@@ -1021,7 +1044,9 @@ int launch_rpl_ex(const DevBlob& b, const float* d_x, float* d_y, int batch, voi
     switch (b.fmt) {
     case FMT_Q4_K:
         return int_x() ? launch_rpl_t<RplQ4KI>(b, d_x, d_y, batch, s, ex) : launch_rpl_t<RplQ4K>(b, d_x, d_y, batch, s, ex);
-    case FMT_Q5_K: return launch_rpl_t<RplQ5KI>(b, d_x, d_y, batch, s, ex);
+    case FMT_Q2_K: return launch_rpl_t<RplKxI<2>>(b, d_x, d_y, batch, s, ex);
+    case FMT_Q3_K: return launch_rpl_t<RplKxI<3>>(b, d_x, d_y, batch, s, ex);
+    case FMT_Q5_K: return launch_rpl_t<RplKxI<5>>(b, d_x, d_y, batch, s, ex);
     case FMT_Q6_K: return launch_rpl_t<RplQ6K>(b, d_x, d_y, batch, s, ex);
     case FMT_Q8_0: return launch_rpl_t<RplQ8>(b, d_x, d_y, batch, s, ex);
     case FMT_Q4_0: return launch_rpl_t<RplQ4>(b, d_x, d_y, batch, s, ex);
@@ -1045,6 +1070,8 @@ struct RplItems {
 bool rpl_items(int fmt, RplItems& it) {
     switch (fmt) {
     case FMT_Q4_K: it = {16, 0, 32, 8}; return true;
+    case FMT_Q2_K: it = {8, 0, 32, 8}; return true;
+    case FMT_Q3_K: it = {8, 4, 32, 8}; return true;
     case FMT_Q5_K: it = {16, 4, 32, 8}; return true;
     case FMT_Q6_K: it = {16, 8, 16, 8}; return true;
     case FMT_Q8_0: it = {32, 0, 32, 0}; return true;
@@ -1211,7 +1238,9 @@ int launch_rpl_matvec_t(const DevBlob& b, const float* d_gy, float* d_gx, int ba
     hipStream_t s = static_cast<hipStream_t>(stream);
     switch (b.fmt) {
     case FMT_Q4_K: return launch_rpl_tr<TQ4K>(b, d_gy, d_gx, batch, s);
-    case FMT_Q5_K: return launch_rpl_tr<TQ5K>(b, d_gy, d_gx, batch, s);
+    case FMT_Q2_K: return launch_rpl_tr<TKx<2>>(b, d_gy, d_gx, batch, s);
+    case FMT_Q3_K: return launch_rpl_tr<TKx<3>>(b, d_gy, d_gx, batch, s);
+    case FMT_Q5_K: return launch_rpl_tr<TKx<5>>(b, d_gy, d_gx, batch, s);
     case FMT_Q6_K: return launch_rpl_tr<TQ6K>(b, d_gy, d_gx, batch, s);
     case FMT_Q8_0: return launch_rpl_tr<TQ8>(b, d_gy, d_gx, batch, s);
     case FMT_Q4_0: return launch_rpl_tr<TQ4>(b, d_gy, d_gx, batch, s);

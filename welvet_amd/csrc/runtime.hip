@@ -94,11 +94,12 @@ struct Image {
     }
 };
 
-// Row-interleaved layout for Q4_K / Q5_K / Q6_K / Q8_0 / Q4_0 (requires cols
-// % 256 == 0): rows are grouped 64 at a time, one per lane of a wave, and every
+// Row-interleaved layout for the k-quants, Q8_0 and Q4_0 (requires cols % 256
+// == 0): rows are grouped 64 at a time, one per lane of a wave, and every
 // plane is stored [row group][chunk or super-block][lane][bytes] so that one
 // wave-wide load reads contiguous memory. Byte count per 256 weights equals
-// the reference blob's (Q4_K 168, Q5_K 200, Q6_K 216, Q8_0 288, Q4_0 160); rows past
+// the reference blob's (Q2_K 104, Q3_K 136, Q4_K 168, Q5_K 200, Q6_K 216, Q8_0
+// 288, Q4_0 160); rows past
 // `rows` in the last group are zero (d = 0 / scale = 0, contributing 0).
 //   Q4_K: codes 16 B/chunk (LSB-first nibbles, as in the blob); meta per
 //         super-block 8 words (u'(2p), u'(2p+1), m(2p), m(2p+1)); dd (d, dmin).
@@ -106,6 +107,8 @@ struct Image {
 //         (quant/kquant.go:179-182), the value u = 1 gives.
 //   Q5_K: low 4 code bits 16 B/chunk; fifth bits 4 B/chunk arranged for the
 //         kernel's byte spread; meta and dd as Q4_K.
+//   Q2_K / Q3_K: low 2 code bits 8 B/chunk (and Q3_K's third bits 4 B/chunk)
+//         arranged for the kernel's byte spread; meta and dd as Q4_K.
 //   Q6_K: low 4 code bits 16 B/chunk; high 2 bits 8 B/chunk arranged for
 //         the kernel's byte spread; meta 8 u16 (u'(2p), u'(2p+1)); dd.
 //   Q8_0 / Q4_0: codes 32 / 16 B per 32-block; meta 8 f32 block scales.
@@ -116,11 +119,12 @@ struct RplOffsets {
 };
 void build_rpl(int fmt, const uint8_t* raw, int64_t rows, int64_t cols, Image& img, RplOffsets& o) {
     const int64_t rg = (rows + 63) / 64, nch = cols / 32, nsb = cols / 256;
-    const int cb = fmt == FMT_Q8_0 ? 32 : 16, mb = fmt == FMT_Q6_K ? 16 : 32;
-    const bool kq = fmt == FMT_Q4_K || fmt == FMT_Q5_K || fmt == FMT_Q6_K;
+    const bool low2 = fmt == FMT_Q2_K || fmt == FMT_Q3_K;  // 2-bit plane (+ third bits)
+    const int cb = fmt == FMT_Q8_0 ? 32 : low2 ? 8 : 16, mb = fmt == FMT_Q6_K ? 16 : 32;
+    const bool kq = low2 || fmt == FMT_Q4_K || fmt == FMT_Q5_K || fmt == FMT_Q6_K;
     o.codes = img.add(size_t(rg * nch * 64 * cb));
     if (fmt == FMT_Q6_K) o.hi = img.add(size_t(rg * nch * 64 * 8));
-    if (fmt == FMT_Q5_K) o.hi = img.add(size_t(rg * nch * 64 * 4));
+    if (fmt == FMT_Q5_K || fmt == FMT_Q3_K) o.hi = img.add(size_t(rg * nch * 64 * 4));
     o.meta = img.add(size_t(rg * nsb * 64 * mb));
     if (kq) o.dd = img.add(size_t(rg * nsb * 64 * 8));
     uint8_t* base = img.bytes.data();
@@ -152,26 +156,36 @@ void build_rpl(int fmt, const uint8_t* raw, int64_t rows, int64_t cols, Image& i
                                 m[4 * p + 2] = o8[24 + 2 * p];
                                 m[4 * p + 3] = o8[25 + 2 * p];
                                 std::memcpy(codes + ci * 16, o8 + 40 + 16 * p, 16);
-                            } else if (fmt == FMT_Q5_K) {
+                            } else if (fmt == FMT_Q5_K || low2) {
                                 m[4 * p] = u0;
                                 m[4 * p + 1] = u1;
                                 m[4 * p + 2] = o8[24 + 2 * p];
                                 m[4 * p + 3] = o8[25 + 2 * p];
-                                const uint8_t* q = o8 + 40;  // 160 B of 5-bit codes
+                                const int bits = ks.bits, qbytes = 32 * bits;  // 256*bits/8 bytes of codes
+                                const uint8_t* q = o8 + 40;
                                 uint8_t qv[32];
                                 for (int k = 0; k < 32; ++k) {  // LSB-first stream (helpers.go:140-149)
-                                    const int bit = (p * 32 + k) * 5;
-                                    const uint32_t v = q[bit >> 3] | ((bit >> 3) + 1 < 160 ? uint32_t(q[(bit >> 3) + 1]) << 8 : 0u);
-                                    qv[k] = uint8_t((v >> (bit & 7)) & 31u);
+                                    const int bit = (p * 32 + k) * bits;
+                                    const uint32_t v = q[bit >> 3] | ((bit >> 3) + 1 < qbytes ? uint32_t(q[(bit >> 3) + 1]) << 8 : 0u);
+                                    qv[k] = uint8_t((v >> (bit & 7)) & ((1u << bits) - 1));
                                 }
-                                uint8_t* c = codes + ci * 16;
-                                for (int k = 0; k < 16; ++k) c[k] = uint8_t((qv[2 * k] & 15) | ((qv[2 * k + 1] & 15) << 4));
-                                // byte b, bit s of the fifth-bit word: code 8w + 2b + half, s = 2w + half
-                                uint8_t* h = hi + ci * 4;
-                                std::memset(h, 0, 4);
-                                for (int sw = 0; sw < 8; ++sw)
-                                    for (int b = 0; b < 4; ++b)
-                                        h[b] |= uint8_t(((qv[8 * (sw >> 1) + 2 * b + (sw & 1)] >> 4) & 1) << sw);
+                                // spread word s holds, in byte b, the code of column 8(s/2) + 2b + s%2
+                                auto code = [&](int sw, int b) { return qv[8 * (sw >> 1) + 2 * b + (sw & 1)]; };
+                                uint8_t* c = codes + ci * cb;
+                                if (fmt == FMT_Q5_K) {
+                                    for (int k = 0; k < 16; ++k) c[k] = uint8_t((qv[2 * k] & 15) | ((qv[2 * k + 1] & 15) << 4));
+                                } else {  // dword s/4, byte b, bits 2(s%4): the low two bits
+                                    std::memset(c, 0, 8);
+                                    for (int sw = 0; sw < 8; ++sw)
+                                        for (int b = 0; b < 4; ++b) c[4 * (sw >> 2) + b] |= uint8_t((code(sw, b) & 3) << (2 * (sw & 3)));
+                                }
+                                if (fmt != FMT_Q2_K) {  // byte b, bit s: the top bit (bit 4 of Q5_K, bit 2 of Q3_K)
+                                    const int top = fmt == FMT_Q5_K ? 4 : 2;
+                                    uint8_t* h = hi + ci * 4;
+                                    std::memset(h, 0, 4);
+                                    for (int sw = 0; sw < 8; ++sw)
+                                        for (int b = 0; b < 4; ++b) h[b] |= uint8_t(((code(sw, b) >> top) & 1) << sw);
+                                }
                             } else {
                                 m[2 * p] = u0;
                                 m[2 * p + 1] = u1;
@@ -409,7 +423,8 @@ int wv_blob_upload(int format, int64_t rows, int64_t cols, int32_t block_weights
         o_codes = img.add(size_t(need));
         std::memcpy(img.bytes.data() + o_codes, raw, size_t(need));
     } else if (!raw_only &&
-               (format == FMT_Q4_K || format == FMT_Q5_K || format == FMT_Q6_K || format == FMT_Q8_0 || format == FMT_Q4_0) &&
+               (format == FMT_Q2_K || format == FMT_Q3_K || format == FMT_Q4_K || format == FMT_Q5_K ||
+                format == FMT_Q6_K || format == FMT_Q8_0 || format == FMT_Q4_0) &&
                cols % 256 == 0) {
         b.layout = LAYOUT_RPL;
         build_rpl(format, raw, rows, cols, img, ro);
