@@ -94,6 +94,7 @@ __device__ __forceinline__ float dot4_u8(uint32_t w, const float* x, float a) {
 // chunk j (0..7) of the super-block, given x[32] and the two 16-column sums.
 struct RplQ4K {  // w = dmin*m/127 + (d*u/255)*q  (quant/kquant.go:178-188)
     static constexpr bool kIntX = false;
+    static constexpr bool kWords2 = false;  // a second metadata word per chunk (block min)
     struct Ch { uint4 c; };
     struct Sb { uint4 g0, g1; float d255, dm127; };
     static __device__ __forceinline__ Ch load_ch(const RplArgs& a, int64_t ci, int lane) {
@@ -221,8 +222,89 @@ struct RplKxI : RplQ4KI {
     }
 };
 
+// The 32-weight block formats with the int-dot x planes: Q4_0 (XR = 0x8...8:
+// the signed nibble q becomes q + 8, OFF = 8), Q5_0 (stored q + 16, OFF =
+// 16), Q4_1 and Q5_1 (MIN: w = min + scale*q). Per chunk (one block) the
+// metadata holds the f32 scale and, with MIN, the f32 min: words j and 8 + j
+// of the lane's 16-word super-block record. Codes are spread as in RplKxI
+// (B = 5 adds the fifth-bit plane); the two 16-column group sums stay exact
+// in int32 and are added as floats.
+template <int B, bool MIN, int OFF, uint32_t XR>
+struct RplB32I {
+    static constexpr bool kIntX = true;
+    static constexpr bool kWords2 = MIN;
+    struct Ch { uint4 c; uint32_t h; };
+    struct Sb { uint4 s0, s1, m0, m1; };
+    static __device__ __forceinline__ Ch load_ch(const RplArgs& a, int64_t ci, int lane) {
+        Ch r;
+        r.c = ld_stream(reinterpret_cast<const uint4*>(a.codes) + ci * 64 + lane);
+        r.h = B == 5 ? ld_stream(reinterpret_cast<const uint32_t*>(a.hi) + ci * 64 + lane) : 0u;
+        return r;
+    }
+    static __device__ __forceinline__ Sb load_sb(const RplArgs& a, int64_t si, int lane) {
+        const uint4* m = reinterpret_cast<const uint4*>(a.meta) + (si * 64 + lane) * (MIN ? 4 : 2);
+        Sb r;
+        r.s0 = ld_stream(m);
+        r.s1 = ld_stream(m + 1);
+        if constexpr (MIN) {
+            r.m0 = ld_stream(m + 2);
+            r.m1 = ld_stream(m + 3);
+        } else {
+            r.m0 = r.m1 = make_uint4(0u, 0u, 0u, 0u);
+        }
+        return r;
+    }
+    static __device__ __forceinline__ uint32_t word(const Sb& sb, int j) {
+        const uint32_t sw[8] = {sb.s0.x, sb.s0.y, sb.s0.z, sb.s0.w, sb.s1.x, sb.s1.y, sb.s1.z, sb.s1.w};
+        return sw[j];
+    }
+    static __device__ __forceinline__ uint32_t word2(const Sb& sb, int j) {
+        const uint32_t mw[8] = {sb.m0.x, sb.m0.y, sb.m0.z, sb.m0.w, sb.m1.x, sb.m1.y, sb.m1.z, sb.m1.w};
+        return mw[j];
+    }
+    static __device__ __forceinline__ Sb with_word(Sb sb, uint32_t w) {
+        sb.s0.x = w;
+        return sb;
+    }
+    static __device__ __forceinline__ Sb with_word2(Sb sb, uint32_t w) {
+        sb.m0.x = w;
+        return sb;
+    }
+    static __device__ __forceinline__ uint32_t spread(const Ch& ch, int s) {
+        const uint32_t wd[4] = {ch.c.x ^ XR, ch.c.y ^ XR, ch.c.z ^ XR, ch.c.w ^ XR};
+        const uint32_t nib = (s & 1) ? (wd[s >> 1] >> 4) & 0x0F0F0F0Fu : wd[s >> 1] & 0x0F0F0F0Fu;
+        if constexpr (B == 5) return nib | (((ch.h >> s) & 0x01010101u) << 4);
+        else return nib;
+    }
+    static __device__ __forceinline__ float dot_i(const Ch& ch, const Sb& sb, int j, const uint32_t* xi, float4 xm) {
+        int A[2][3] = {{0, 0, 0}, {0, 0, 0}};
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const int gi = w >> 1;
+            const uint32_t lo = spread(ch, 2 * w), hi = spread(ch, 2 * w + 1);
+            A[gi][0] = int(__builtin_amdgcn_udot4(lo, xi[w], uint32_t(A[gi][0]), false));
+            A[gi][0] = int(__builtin_amdgcn_udot4(hi, xi[4 + w], uint32_t(A[gi][0]), false));
+            A[gi][1] = int(__builtin_amdgcn_udot4(lo, xi[8 + w], uint32_t(A[gi][1]), false));
+            A[gi][1] = int(__builtin_amdgcn_udot4(hi, xi[12 + w], uint32_t(A[gi][1]), false));
+            A[gi][2] = __builtin_amdgcn_sdot4(int(lo), int(xi[16 + w]), A[gi][2], false);
+            A[gi][2] = __builtin_amdgcn_sdot4(int(hi), int(xi[20 + w]), A[gi][2], false);
+        }
+        const int T0 = A[0][0] + (A[0][1] << 8) + (A[0][2] << 16);
+        const int T1 = A[1][0] + (A[1][1] << 8) + (A[1][2] << 16);
+        const float scale = __uint_as_float(word(sb, j));
+        const float S = xm.y + xm.z;  // sum of the chunk's 32 x
+        const float bias = MIN ? __uint_as_float(word2(sb, j)) : -float(OFF) * scale;
+        return fmaf(scale * (xm.x * 255.0f), float(T0) + float(T1), bias * S);
+    }
+};
+using RplQ4I = RplB32I<4, false, 8, 0x88888888u>;
+using RplQ41I = RplB32I<4, true, 0, 0u>;
+using RplQ50I = RplB32I<5, false, 16, 0u>;
+using RplQ51I = RplB32I<5, true, 0, 0u>;
+
 struct RplQ6K {  // q = lo4 | hi2 << 4, w = (d*u/255)*(q - 32)
     static constexpr bool kIntX = false;
+    static constexpr bool kWords2 = false;  // a second metadata word per chunk (block min)
     struct Ch { uint4 c; uint2 h; };
     struct Sb { uint4 g; float d255; };
     static __device__ __forceinline__ Ch load_ch(const RplArgs& a, int64_t ci, int lane) {
@@ -268,6 +350,7 @@ struct RplQ6K {  // q = lo4 | hi2 << 4, w = (d*u/255)*(q - 32)
 
 struct RplQ8 {  // w = scale * q, q int8; q + 128 converts as an unsigned byte
     static constexpr bool kIntX = false;
+    static constexpr bool kWords2 = false;  // a second metadata word per chunk (block min)
     struct Ch { uint4 c0, c1; };
     struct Sb { uint4 s0, s1; };
     static __device__ __forceinline__ Ch load_ch(const RplArgs& a, int64_t ci, int lane) {
@@ -299,6 +382,7 @@ struct RplQ8 {  // w = scale * q, q int8; q + 128 converts as an unsigned byte
 
 struct RplQ4 {  // w = scale * q, q signed nibble; q ^ 8 = q + 8
     static constexpr bool kIntX = false;
+    static constexpr bool kWords2 = false;  // a second metadata word per chunk (block min)
     struct Ch { uint4 c; };
     struct Sb { uint4 s0, s1; };
     static __device__ __forceinline__ Ch load_ch(const RplArgs& a, int64_t ci, int lane) {
@@ -519,6 +603,12 @@ __global__ void __launch_bounds__(1024) k_gemv_rpl(RplArgs a, const float* __res
 #pragma unroll
                 for (int i = 0; i < L; ++i) cand[i] = P::word(sbm[s], jb + i);
                 mv = P::with_word(sbm[s], pick<L>(cand, lg));
+                if constexpr (P::kWords2) {
+                    uint32_t cand2[L];
+#pragma unroll
+                    for (int i = 0; i < L; ++i) cand2[i] = P::word2(sbm[s], jb + i);
+                    mv = P::with_word2(mv, pick<L>(cand2, lg));
+                }
                 jsel = 0;
             }
             const float* xs = xw + s * kSlice;
@@ -636,15 +726,18 @@ int lds_floor() {
 struct RplPlan {
     int L, S, W, ksplit;
 };
-RplPlan rpl_plan(const DevBlob& bl) {
+// max_s: the most super-blocks per wave whose metadata fits the registers
+// (2 for the policies with a second metadata word: 4 spill at 128 VGPRs).
+RplPlan rpl_plan(const DevBlob& bl, int max_s = 4) {
     const RplArgs& a = bl.rpl;
     RplPlan p{1, 1, 1, 1};
-    static const int fl = env_int("WV_RPL_L", 0), fs = env_int("WV_RPL_S", 0);
+    static const int fl = env_int("WV_RPL_L", 0), fs0 = env_int("WV_RPL_S", 0);
+    const int fs = std::min(fs0, max_s);
     if (a.nsb <= 16) {
         while (p.L < 4 && int64_t(a.rg_count) * p.L < 180) p.L *= 2;
         if (p.L == 4 && a.nsb >= 2) p.S = 2;
     } else if (const int w4 = (a.nsb + 3) / 4;
-               w4 <= 16 && int64_t(a.rg_count) * 4 >= 180 && int64_t(a.rg_count) * 4 <= 256 * (16 / w4)) {
+               max_s >= 4 && w4 <= 16 && int64_t(a.rg_count) * 4 >= 180 && int64_t(a.rg_count) * 4 <= 256 * (16 / w4)) {
         // No K split: L = 4, S = 4, one block per 16-row subgroup covering
         // all of K, when those blocks fill the GPU in one resident pass.
         p.L = 4;
@@ -697,7 +790,7 @@ int launch_rpl_t(const DevBlob& bl, const float* x, float* y, int batch, hipStre
     a.nrm_n = ex.nrm_n;
     a.nrm_eps = ex.nrm_eps;
     a.ss_out = ex.ss_out;
-    const RplPlan p = rpl_plan(bl);
+    const RplPlan p = rpl_plan(bl, P::kWords2 ? 2 : 4);
     a.ksplit = p.ksplit;
     size_t lds = size_t(p.W) * (p.S * (256 + 16) + 64) * sizeof(float);  // x slices + partial row sums
     lds = std::max(lds, size_t(lds_floor()));
@@ -821,6 +914,40 @@ struct TKx : RplKxI<B> {
         tacc_w(ch, 1, c0, acc + 8);
         tacc_w(ch, 2, c1, acc + 16);
         tacc_w(ch, 3, c1, acc + 24);
+    }
+};
+
+template <int B, bool MIN, int OFF, uint32_t XR>
+struct TB32 : RplB32I<B, MIN, OFF, XR> {
+    using P = RplB32I<B, MIN, OFF, XR>;
+    using Ch = typename P::Ch;
+    struct TM { uint2 s, m; };  // scales (and mins) of chunks 2jp, 2jp+1
+    static __device__ __forceinline__ TM load_tm(const RplArgs& a, int64_t si, int lane, int jp) {
+        const uint2* m = reinterpret_cast<const uint2*>(a.meta) + (si * 64 + lane) * (MIN ? 8 : 4);
+        return {ld_stream(m + jp), MIN ? ld_stream(m + 4 + jp) : make_uint2(0u, 0u)};
+    }
+    static __device__ __forceinline__ void tacc_w(const Ch& ch, int w, float coef, float* acc) {
+        uint32_t lo = P::spread(ch, 2 * w), hi = P::spread(ch, 2 * w + 1);
+        asm("" : "+v"(lo), "+v"(hi));
+        acc[0] = fmaf(ub0(lo), coef, acc[0]);
+        acc[1] = fmaf(ub0(hi), coef, acc[1]);
+        acc[2] = fmaf(ub1(lo), coef, acc[2]);
+        acc[3] = fmaf(ub1(hi), coef, acc[3]);
+        acc[4] = fmaf(ub2(lo), coef, acc[4]);
+        acc[5] = fmaf(ub2(hi), coef, acc[5]);
+        acc[6] = fmaf(ub3(lo), coef, acc[6]);
+        acc[7] = fmaf(ub3(hi), coef, acc[7]);
+    }
+    template <int jj>
+    static __device__ __forceinline__ void tacc(const Ch& ch, const TM& t, float gy, float* acc, float* off) {
+        const float c = gy * __uint_as_float(jj ? t.s.y : t.s.x);
+        const float b = MIN ? gy * __uint_as_float(jj ? t.m.y : t.m.x) : -float(OFF) * c;
+        off[0] += b;
+        off[1] += b;
+        tacc_w(ch, 0, c, acc);
+        tacc_w(ch, 1, c, acc + 8);
+        tacc_w(ch, 2, c, acc + 16);
+        tacc_w(ch, 3, c, acc + 24);
     }
 };
 
@@ -1049,7 +1176,10 @@ int launch_rpl_ex(const DevBlob& b, const float* d_x, float* d_y, int batch, voi
     case FMT_Q5_K: return launch_rpl_t<RplKxI<5>>(b, d_x, d_y, batch, s, ex);
     case FMT_Q6_K: return launch_rpl_t<RplQ6K>(b, d_x, d_y, batch, s, ex);
     case FMT_Q8_0: return launch_rpl_t<RplQ8>(b, d_x, d_y, batch, s, ex);
-    case FMT_Q4_0: return launch_rpl_t<RplQ4>(b, d_x, d_y, batch, s, ex);
+    case FMT_Q4_0: return launch_rpl_t<RplQ4I>(b, d_x, d_y, batch, s, ex);
+    case FMT_Q4_1: return launch_rpl_t<RplQ41I>(b, d_x, d_y, batch, s, ex);
+    case FMT_Q5_0: return launch_rpl_t<RplQ50I>(b, d_x, d_y, batch, s, ex);
+    case FMT_Q5_1: return launch_rpl_t<RplQ51I>(b, d_x, d_y, batch, s, ex);
     default: return int(hipErrorInvalidValue);
     }
 }
@@ -1076,6 +1206,9 @@ bool rpl_items(int fmt, RplItems& it) {
     case FMT_Q6_K: it = {16, 8, 16, 8}; return true;
     case FMT_Q8_0: it = {32, 0, 32, 0}; return true;
     case FMT_Q4_0: it = {16, 0, 32, 0}; return true;
+    case FMT_Q4_1: it = {16, 0, 64, 0}; return true;
+    case FMT_Q5_0: it = {16, 4, 32, 0}; return true;
+    case FMT_Q5_1: it = {16, 4, 64, 0}; return true;
     default: return false;
     }
 }
@@ -1244,6 +1377,9 @@ int launch_rpl_matvec_t(const DevBlob& b, const float* d_gy, float* d_gx, int ba
     case FMT_Q6_K: return launch_rpl_tr<TQ6K>(b, d_gy, d_gx, batch, s);
     case FMT_Q8_0: return launch_rpl_tr<TQ8>(b, d_gy, d_gx, batch, s);
     case FMT_Q4_0: return launch_rpl_tr<TQ4>(b, d_gy, d_gx, batch, s);
+    case FMT_Q4_1: return launch_rpl_tr<TB32<4, true, 0, 0u>>(b, d_gy, d_gx, batch, s);
+    case FMT_Q5_0: return launch_rpl_tr<TB32<5, false, 16, 0u>>(b, d_gy, d_gx, batch, s);
+    case FMT_Q5_1: return launch_rpl_tr<TB32<5, true, 0, 0u>>(b, d_gy, d_gx, batch, s);
     default: return int(hipErrorInvalidValue);
     }
 }

@@ -94,12 +94,12 @@ struct Image {
     }
 };
 
-// Row-interleaved layout for the k-quants, Q8_0 and Q4_0 (requires cols % 256
+// Row-interleaved layout for the k-quants and the 32-block formats (requires cols % 256
 // == 0): rows are grouped 64 at a time, one per lane of a wave, and every
 // plane is stored [row group][chunk or super-block][lane][bytes] so that one
 // wave-wide load reads contiguous memory. Byte count per 256 weights equals
 // the reference blob's (Q2_K 104, Q3_K 136, Q4_K 168, Q5_K 200, Q6_K 216, Q8_0
-// 288, Q4_0 160); rows past
+// 288, Q4_0 160, Q4_1 / Q5_0 192, Q5_1 224); rows past
 // `rows` in the last group are zero (d = 0 / scale = 0, contributing 0).
 //   Q4_K: codes 16 B/chunk (LSB-first nibbles, as in the blob); meta per
 //         super-block 8 words (u'(2p), u'(2p+1), m(2p), m(2p+1)); dd (d, dmin).
@@ -112,6 +112,8 @@ struct Image {
 //   Q6_K: low 4 code bits 16 B/chunk; high 2 bits 8 B/chunk arranged for
 //         the kernel's byte spread; meta 8 u16 (u'(2p), u'(2p+1)); dd.
 //   Q8_0 / Q4_0: codes 32 / 16 B per 32-block; meta 8 f32 block scales.
+//   Q4_1 / Q5_0 / Q5_1: codes as Q4_0 (Q5_x: low 4 bits, plus the fifth
+//         bits as Q5_K's); meta 8 f32 scales, then (Q4_1, Q5_1) 8 f32 mins.
 // Code (and Q6_K high-bit) planes are chunk-step-major, [j][rg][sb][lane],
 // j = chunk index inside the super-block; meta/dd are [rg][sb][lane].
 struct RplOffsets {
@@ -120,11 +122,13 @@ struct RplOffsets {
 void build_rpl(int fmt, const uint8_t* raw, int64_t rows, int64_t cols, Image& img, RplOffsets& o) {
     const int64_t rg = (rows + 63) / 64, nch = cols / 32, nsb = cols / 256;
     const bool low2 = fmt == FMT_Q2_K || fmt == FMT_Q3_K;  // 2-bit plane (+ third bits)
-    const int cb = fmt == FMT_Q8_0 ? 32 : low2 ? 8 : 16, mb = fmt == FMT_Q6_K ? 16 : 32;
+    const bool bmin = fmt == FMT_Q4_1 || fmt == FMT_Q5_1;  // 32-blocks with a min
+    const bool five = fmt == FMT_Q5_K || fmt == FMT_Q5_0 || fmt == FMT_Q5_1;
+    const int cb = fmt == FMT_Q8_0 ? 32 : low2 ? 8 : 16, mb = fmt == FMT_Q6_K ? 16 : bmin ? 64 : 32;
     const bool kq = low2 || fmt == FMT_Q4_K || fmt == FMT_Q5_K || fmt == FMT_Q6_K;
     o.codes = img.add(size_t(rg * nch * 64 * cb));
     if (fmt == FMT_Q6_K) o.hi = img.add(size_t(rg * nch * 64 * 8));
-    if (fmt == FMT_Q5_K || fmt == FMT_Q3_K) o.hi = img.add(size_t(rg * nch * 64 * 4));
+    if (five || fmt == FMT_Q3_K) o.hi = img.add(size_t(rg * nch * 64 * 4));
     o.meta = img.add(size_t(rg * nsb * 64 * mb));
     if (kq) o.dd = img.add(size_t(rg * nsb * 64 * 8));
     uint8_t* base = img.bytes.data();
@@ -208,11 +212,30 @@ void build_rpl(int fmt, const uint8_t* raw, int64_t rows, int64_t cols, Image& i
                             }
                         }
                     } else {
-                        const int bb = fmt == FMT_Q8_0 ? 36 : 20;
+                        // 32-blocks: [scale][min (Q4_1, Q5_1)][codes]; meta = 8 scales, then 8 mins
+                        const int bb = fmt == FMT_Q8_0 ? 36 : fmt == FMT_Q4_0 ? 20 : fmt == FMT_Q5_1 ? 28 : 24;
+                        const int hdr = bmin ? 8 : 4;
                         for (int p = 0; p < 8; ++p) {
                             const uint8_t* blk = raw + (row * nch + sb * 8 + p) * bb;
+                            const int64_t ci = ((p * rg + g) * nsb + sb) * 64 + lane;
                             std::memcpy(m + 4 * p, blk, 4);
-                            std::memcpy(codes + (((p * rg + g) * nsb + sb) * 64 + lane) * cb, blk + 4, size_t(cb));
+                            if (bmin) std::memcpy(m + 32 + 4 * p, blk + 4, 4);
+                            if (!five) {
+                                std::memcpy(codes + ci * cb, blk + hdr, size_t(cb));
+                                continue;
+                            }
+                            uint8_t qv[32];
+                            for (int k = 0; k < 32; ++k) {  // 20 B LSB-first stream of 5-bit codes
+                                const int bit = k * 5;
+                                const uint32_t v = blk[hdr + (bit >> 3)] | ((bit >> 3) + 1 < 20 ? uint32_t(blk[hdr + (bit >> 3) + 1]) << 8 : 0u);
+                                qv[k] = uint8_t((v >> (bit & 7)) & 31u);
+                            }
+                            uint8_t* c = codes + ci * 16;
+                            for (int k = 0; k < 16; ++k) c[k] = uint8_t((qv[2 * k] & 15) | ((qv[2 * k + 1] & 15) << 4));
+                            uint8_t* h = hi + ci * 4;
+                            std::memset(h, 0, 4);
+                            for (int sw = 0; sw < 8; ++sw)
+                                for (int b = 0; b < 4; ++b) h[b] |= uint8_t(((qv[8 * (sw >> 1) + 2 * b + (sw & 1)] >> 4) & 1) << sw);
                         }
                     }
                 }
@@ -424,7 +447,8 @@ int wv_blob_upload(int format, int64_t rows, int64_t cols, int32_t block_weights
         std::memcpy(img.bytes.data() + o_codes, raw, size_t(need));
     } else if (!raw_only &&
                (format == FMT_Q2_K || format == FMT_Q3_K || format == FMT_Q4_K || format == FMT_Q5_K ||
-                format == FMT_Q6_K || format == FMT_Q8_0 || format == FMT_Q4_0) &&
+                format == FMT_Q6_K || format == FMT_Q8_0 || format == FMT_Q4_0 || format == FMT_Q4_1 ||
+                format == FMT_Q5_0 || format == FMT_Q5_1) &&
                cols % 256 == 0) {
         b.layout = LAYOUT_RPL;
         build_rpl(format, raw, rows, cols, img, ro);
