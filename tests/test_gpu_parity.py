@@ -18,7 +18,8 @@ TOL = 1e-5
 ALL = ["Q4_0", "Q8_0", "Q4_1", "Q5_0", "Q5_1", "Q2_K", "Q3_K", "Q4_K", "Q5_K", "Q6_K",
        "IQ1_S", "IQ2_XXS", "IQ2_XS", "IQ3_XXS", "IQ3_S", "IQ4_NL", "IQ4_XS",
        "TernaryPacked", "BinaryPacked"]
-PLANAR = {f: "row-interleaved" for f in ("Q2_K", "Q3_K", "Q4_K", "Q5_K", "Q6_K", "Q8_0", "Q4_0", "Q4_1", "Q5_0", "Q5_1")}
+PLANAR = {f: "row-interleaved" for f in ("Q2_K", "Q3_K", "Q4_K", "Q5_K", "Q6_K", "Q8_0", "Q4_0", "Q4_1", "Q5_0", "Q5_1",
+                                          "IQ1_S", "IQ2_XXS", "IQ2_XS", "IQ3_XXS", "IQ3_S", "IQ4_XS")}
 
 
 @pytest.fixture(scope="module", autouse=True)
@@ -124,11 +125,12 @@ def test_row_interleaved_split_and_batch(fmt, shape, batch):
 # fill the GPU in one pass, else a K split across blocks.
 PLAN_SHAPES = [
     ((12800, 1024), ["Q2_K", "Q3_K", "Q4_K", "Q5_K", "Q6_K", "Q8_0", "Q4_0"]),  # L=1 S=1
-    ((8192, 1024), ["Q2_K", "Q3_K", "Q4_K", "Q5_K", "Q6_K", "Q8_0", "Q4_0", "Q4_1", "Q5_1"]),   # L=2 S=1
+    ((8192, 1024), ["Q2_K", "Q3_K", "Q4_K", "Q5_K", "Q6_K", "Q8_0", "Q4_0", "Q4_1", "Q5_1", "IQ1_S", "IQ3_S"]),   # L=2 S=1
     ((1000, 2048), ["Q2_K", "Q3_K", "Q4_K", "Q5_K", "Q6_K", "Q8_0", "Q4_0", "Q4_1", "Q5_0", "Q5_1"]),   # L=4 S=2
     ((8192, 8192), ["Q4_K", "Q8_0"]),                           # L=4 S=4, 8-wave blocks, no split
     ((3000, 13312), ["Q3_K", "Q4_K", "Q5_K", "Q6_K", "Q8_0", "Q4_0", "Q5_0"]),  # L=4 S=4, 13 waves, padded last row group
-    ((3000, 13312), ["Q4_1", "Q5_1"]),  # two metadata words per block: at most 2 super-blocks per wave, K split
+    ((3000, 13312), ["Q4_1", "Q5_1", "IQ2_XS", "IQ3_S", "IQ4_XS"]),  # two metadata words per chunk: at most 2 super-blocks per wave, K split
+    ((3000, 13312), ["IQ1_S", "IQ2_XXS", "IQ3_XXS"]),  # L=4 S=4
     ((4096, 11008), ["Q4_K", "Q5_K", "Q6_K"]),                  # L=4 S=4, 43 super-blocks: last wave has 3
     ((2048, 16640), ["Q2_K", "Q3_K", "Q4_K", "Q5_K", "Q6_K", "Q8_0", "Q4_0"]),  # K split 5 over 13-wave blocks
     ((6400, 16640), ["Q4_K"]),                          # K split 2, 65 super-blocks

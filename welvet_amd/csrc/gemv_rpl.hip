@@ -302,6 +302,106 @@ using RplQ41I = RplB32I<4, true, 0, 0u>;
 using RplQ50I = RplB32I<5, false, 16, 0u>;
 using RplQ51I = RplB32I<5, true, 0, 0u>;
 
+// The linear IQ formats at their default code width and scale group
+// (quant/iq.go:49-68, 169-180): w = scale*(q - mid), and for one-bit codes
+// w = +-scale = (2*scale)*(q - 1/2). Planes as RplKxI (B = 2, 3) or Q4_K's
+// nibbles (B = 4); one-bit codes sit in a 32-bit plane arranged as the
+// fifth bits of Q5_K. Scales come from the blob's Scales array: one f32 per
+// chunk (scale group 32) or two (group 16, words 2j and 2j + 1).
+template <int B, bool SG16, int MID2>
+struct RplIQI {
+    static constexpr bool kIntX = true;
+    static constexpr bool kWords2 = SG16;
+    static constexpr float kMid = 0.5f * MID2;
+    static constexpr float kScaleMul = B == 1 ? 2.0f : 1.0f;  // +-scale = (2*scale)*(q - 1/2)
+    struct Ch { uint4 c; uint32_t h; };
+    struct Sb { uint4 s0, s1, m0, m1; };
+    static __device__ __forceinline__ Ch load_ch(const RplArgs& a, int64_t ci, int lane) {
+        Ch r{};
+        if constexpr (B == 4) {
+            r.c = ld_stream(reinterpret_cast<const uint4*>(a.codes) + ci * 64 + lane);
+        } else if constexpr (B >= 2) {
+            const uint2 v = ld_stream(reinterpret_cast<const uint2*>(a.codes) + ci * 64 + lane);
+            r.c = make_uint4(v.x, v.y, 0u, 0u);
+        } else {
+            r.c = make_uint4(ld_stream(reinterpret_cast<const uint32_t*>(a.codes) + ci * 64 + lane), 0u, 0u, 0u);
+        }
+        r.h = B == 3 ? ld_stream(reinterpret_cast<const uint32_t*>(a.hi) + ci * 64 + lane) : 0u;
+        return r;
+    }
+    static __device__ __forceinline__ Sb load_sb(const RplArgs& a, int64_t si, int lane) {
+        const uint4* m = reinterpret_cast<const uint4*>(a.meta) + (si * 64 + lane) * (SG16 ? 4 : 2);
+        Sb r;
+        r.s0 = ld_stream(m);
+        r.s1 = ld_stream(m + 1);
+        if constexpr (SG16) {
+            r.m0 = ld_stream(m + 2);
+            r.m1 = ld_stream(m + 3);
+        } else {
+            r.m0 = r.m1 = make_uint4(0u, 0u, 0u, 0u);
+        }
+        return r;
+    }
+    static __device__ __forceinline__ uint32_t sw(const Sb& sb, int k) {
+        const uint32_t w[16] = {sb.s0.x, sb.s0.y, sb.s0.z, sb.s0.w, sb.s1.x, sb.s1.y, sb.s1.z, sb.s1.w,
+                                sb.m0.x, sb.m0.y, sb.m0.z, sb.m0.w, sb.m1.x, sb.m1.y, sb.m1.z, sb.m1.w};
+        return w[k];
+    }
+    static __device__ __forceinline__ uint32_t word(const Sb& sb, int j) { return sw(sb, SG16 ? 2 * j : j); }
+    static __device__ __forceinline__ uint32_t word2(const Sb& sb, int j) { return sw(sb, 2 * j + 1); }
+    static __device__ __forceinline__ Sb with_word(Sb sb, uint32_t w) {
+        sb.s0.x = w;
+        return sb;
+    }
+    static __device__ __forceinline__ Sb with_word2(Sb sb, uint32_t w) {
+        sb.s0.y = w;
+        return sb;
+    }
+    static __device__ __forceinline__ uint32_t spread(const Ch& ch, int s) {
+        const uint32_t wd[4] = {ch.c.x, ch.c.y, ch.c.z, ch.c.w};
+        if constexpr (B == 4) {
+            return (s & 1) ? (wd[s >> 1] >> 4) & 0x0F0F0F0Fu : wd[s >> 1] & 0x0F0F0F0Fu;
+        } else if constexpr (B == 1) {
+            return (ch.c.x >> s) & 0x01010101u;
+        } else {
+            const uint32_t lo2 = (wd[s >> 2] >> (2 * (s & 3))) & 0x03030303u;
+            if constexpr (B == 2) return lo2;
+            else return lo2 | (((ch.h >> s) & 0x01010101u) << 2);
+        }
+    }
+    // the chunk's group scales (doubled for one-bit codes)
+    static __device__ __forceinline__ float2 scales(const Sb& sb, int j) {
+        const float s0 = __uint_as_float(word(sb, j)) * kScaleMul;
+        const float s1 = SG16 ? __uint_as_float(word2(sb, j)) * kScaleMul : s0;
+        return make_float2(s0, s1);
+    }
+    static __device__ __forceinline__ float dot_i(const Ch& ch, const Sb& sb, int j, const uint32_t* xi, float4 xm) {
+        int A[2][3] = {{0, 0, 0}, {0, 0, 0}};
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const int gi = w >> 1;
+            const uint32_t lo = spread(ch, 2 * w), hi = spread(ch, 2 * w + 1);
+            A[gi][0] = int(__builtin_amdgcn_udot4(lo, xi[w], uint32_t(A[gi][0]), false));
+            A[gi][0] = int(__builtin_amdgcn_udot4(hi, xi[4 + w], uint32_t(A[gi][0]), false));
+            A[gi][1] = int(__builtin_amdgcn_udot4(lo, xi[8 + w], uint32_t(A[gi][1]), false));
+            A[gi][1] = int(__builtin_amdgcn_udot4(hi, xi[12 + w], uint32_t(A[gi][1]), false));
+            A[gi][2] = __builtin_amdgcn_sdot4(int(lo), int(xi[16 + w]), A[gi][2], false);
+            A[gi][2] = __builtin_amdgcn_sdot4(int(hi), int(xi[20 + w]), A[gi][2], false);
+        }
+        const int T0 = A[0][0] + (A[0][1] << 8) + (A[0][2] << 16);
+        const int T1 = A[1][0] + (A[1][1] << 8) + (A[1][2] << 16);
+        const float2 sc = scales(sb, j);
+        const float sx = xm.x * 255.0f;
+        return fmaf(sx * sc.x, float(T0), fmaf(sx * sc.y, float(T1), -kMid * fmaf(sc.x, xm.y, sc.y * xm.z)));
+    }
+};
+using RplIQ1S = RplIQI<1, false, 1>;
+using RplIQ2XXS = RplIQI<2, false, 3>;
+using RplIQ2XS = RplIQI<2, true, 3>;
+using RplIQ3XXS = RplIQI<3, false, 7>;
+using RplIQ3S = RplIQI<3, true, 7>;
+using RplIQ4XS = RplIQI<4, true, 15>;
+
 struct RplQ6K {  // q = lo4 | hi2 << 4, w = (d*u/255)*(q - 32)
     static constexpr bool kIntX = false;
     static constexpr bool kWords2 = false;  // a second metadata word per chunk (block min)
@@ -951,6 +1051,46 @@ struct TB32 : RplB32I<B, MIN, OFF, XR> {
     }
 };
 
+template <class PQ>
+struct TIQ : PQ {
+    using Ch = typename PQ::Ch;
+    struct TM { uint4 s; };  // scales of chunks 2jp, 2jp+1 (group 32: .xy; group 16: .xyzw)
+    static __device__ __forceinline__ TM load_tm(const RplArgs& a, int64_t si, int lane, int jp) {
+        if constexpr (PQ::kWords2) {
+            return {ld_stream(reinterpret_cast<const uint4*>(a.meta) + (si * 64 + lane) * 4 + jp)};
+        } else {
+            const uint2 v = ld_stream(reinterpret_cast<const uint2*>(a.meta) + (si * 64 + lane) * 4 + jp);
+            return {make_uint4(v.x, v.y, 0u, 0u)};
+        }
+    }
+    static __device__ __forceinline__ void tacc_w(const Ch& ch, int w, float coef, float* acc) {
+        uint32_t lo = PQ::spread(ch, 2 * w), hi = PQ::spread(ch, 2 * w + 1);
+        asm("" : "+v"(lo), "+v"(hi));
+        acc[0] = fmaf(ub0(lo), coef, acc[0]);
+        acc[1] = fmaf(ub0(hi), coef, acc[1]);
+        acc[2] = fmaf(ub1(lo), coef, acc[2]);
+        acc[3] = fmaf(ub1(hi), coef, acc[3]);
+        acc[4] = fmaf(ub2(lo), coef, acc[4]);
+        acc[5] = fmaf(ub2(hi), coef, acc[5]);
+        acc[6] = fmaf(ub3(lo), coef, acc[6]);
+        acc[7] = fmaf(ub3(hi), coef, acc[7]);
+    }
+    template <int jj>
+    static __device__ __forceinline__ void tacc(const Ch& ch, const TM& t, float gy, float* acc, float* off) {
+        const float k = PQ::kMid;
+        const uint32_t w[4] = {t.s.x, t.s.y, t.s.z, t.s.w};
+        const float s0 = __uint_as_float(PQ::kWords2 ? w[2 * jj] : w[jj]) * PQ::kScaleMul;
+        const float s1 = PQ::kWords2 ? __uint_as_float(w[2 * jj + 1]) * PQ::kScaleMul : s0;
+        const float c0 = gy * s0, c1 = gy * s1;
+        off[0] = fmaf(-k, c0, off[0]);
+        off[1] = fmaf(-k, c1, off[1]);
+        tacc_w(ch, 0, c0, acc);
+        tacc_w(ch, 1, c0, acc + 8);
+        tacc_w(ch, 2, c1, acc + 16);
+        tacc_w(ch, 3, c1, acc + 24);
+    }
+};
+
 struct TQ6K : RplQ6K {
     struct TM { uint32_t g; float d; };  // (u'0,u'1) of chunk 2jp | (u'0,u'1) of 2jp+1 << 16
     static __device__ __forceinline__ TM load_tm(const RplArgs& a, int64_t si, int lane, int jp) {
@@ -1180,6 +1320,12 @@ int launch_rpl_ex(const DevBlob& b, const float* d_x, float* d_y, int batch, voi
     case FMT_Q4_1: return launch_rpl_t<RplQ41I>(b, d_x, d_y, batch, s, ex);
     case FMT_Q5_0: return launch_rpl_t<RplQ50I>(b, d_x, d_y, batch, s, ex);
     case FMT_Q5_1: return launch_rpl_t<RplQ51I>(b, d_x, d_y, batch, s, ex);
+    case FMT_IQ1_S: return launch_rpl_t<RplIQ1S>(b, d_x, d_y, batch, s, ex);
+    case FMT_IQ2_XXS: return launch_rpl_t<RplIQ2XXS>(b, d_x, d_y, batch, s, ex);
+    case FMT_IQ2_XS: return launch_rpl_t<RplIQ2XS>(b, d_x, d_y, batch, s, ex);
+    case FMT_IQ3_XXS: return launch_rpl_t<RplIQ3XXS>(b, d_x, d_y, batch, s, ex);
+    case FMT_IQ3_S: return launch_rpl_t<RplIQ3S>(b, d_x, d_y, batch, s, ex);
+    case FMT_IQ4_XS: return launch_rpl_t<RplIQ4XS>(b, d_x, d_y, batch, s, ex);
     default: return int(hipErrorInvalidValue);
     }
 }
@@ -1197,8 +1343,15 @@ namespace {
 struct RplItems {
     int cb, hb, mb, db;  // code chunk (x8 planes), high-bit chunk (x8), metadata, (d, dmin)
 };
-bool rpl_items(int fmt, RplItems& it) {
-    switch (fmt) {
+bool rpl_items(const DevBlob& b, RplItems& it) {
+    IQSpec is;
+    if (iq_rpl_spec(b.fmt, b.iq_bits, b.iq_sg)) {
+        iq_spec(b.fmt, is);
+        const int cb = is.bits == 4 ? 16 : is.bits >= 2 ? 8 : 4;
+        it = {cb, is.bits == 3 ? 4 : 0, is.sg == 16 ? 64 : 32, 0};
+        return true;
+    }
+    switch (b.fmt) {
     case FMT_Q4_K: it = {16, 0, 32, 8}; return true;
     case FMT_Q2_K: it = {8, 0, 32, 8}; return true;
     case FMT_Q3_K: it = {8, 4, 32, 8}; return true;
@@ -1258,6 +1411,8 @@ int finish_fused(const DevBlob& proto, int64_t rows, int64_t rg, const FusedLayo
                  hipStream_t s) {
     out = DevBlob{};
     out.fmt = proto.fmt;
+    out.iq_bits = proto.iq_bits;
+    out.iq_sg = proto.iq_sg;
     out.rows = rows;
     out.cols = proto.cols;
     out.layout = LAYOUT_RPL;
@@ -1284,11 +1439,12 @@ int finish_fused(const DevBlob& proto, int64_t rows, int64_t rg, const FusedLayo
 int rpl_fuse_rows(const DevBlob* parts, int n, DevBlob& out, void* stream) {
     hipStream_t s = static_cast<hipStream_t>(stream);
     RplItems it{};
-    if (n <= 0 || !rpl_items(parts[0].fmt, it)) return int(hipErrorInvalidValue);
+    if (n <= 0 || !rpl_items(parts[0], it)) return int(hipErrorInvalidValue);
     int64_t rg = 0, rows = 0;
     for (int i = 0; i < n; ++i) {
         const DevBlob& b = parts[i];
-        if (b.layout != LAYOUT_RPL || b.fmt != parts[0].fmt || b.cols != parts[0].cols || b.rows % 64)
+        if (b.layout != LAYOUT_RPL || b.fmt != parts[0].fmt || b.cols != parts[0].cols || b.rows % 64 ||
+            b.iq_bits != parts[0].iq_bits || b.iq_sg != parts[0].iq_sg)
             return int(hipErrorInvalidValue);
         rg += b.rpl.rg_count;
         rows += b.rows;
@@ -1328,7 +1484,8 @@ int rpl_fuse_rows(const DevBlob* parts, int n, DevBlob& out, void* stream) {
 int rpl_fuse_pairs(const DevBlob& a, const DevBlob& b, DevBlob& out, void* stream) {
     hipStream_t s = static_cast<hipStream_t>(stream);
     RplItems it{};
-    if (!rpl_items(a.fmt, it) || a.layout != LAYOUT_RPL || b.layout != LAYOUT_RPL || a.fmt != b.fmt ||
+    if (!rpl_items(a, it) || a.layout != LAYOUT_RPL || b.layout != LAYOUT_RPL || a.fmt != b.fmt ||
+        a.iq_bits != b.iq_bits || a.iq_sg != b.iq_sg ||
         a.rows != b.rows || a.cols != b.cols || a.rows % 32)
         return int(hipErrorInvalidValue);
     const int64_t rg_in = a.rpl.rg_count, rg = 2 * rg_in, nsb = a.rpl.nsb;
@@ -1380,6 +1537,12 @@ int launch_rpl_matvec_t(const DevBlob& b, const float* d_gy, float* d_gx, int ba
     case FMT_Q4_1: return launch_rpl_tr<TB32<4, true, 0, 0u>>(b, d_gy, d_gx, batch, s);
     case FMT_Q5_0: return launch_rpl_tr<TB32<5, false, 16, 0u>>(b, d_gy, d_gx, batch, s);
     case FMT_Q5_1: return launch_rpl_tr<TB32<5, true, 0, 0u>>(b, d_gy, d_gx, batch, s);
+    case FMT_IQ1_S: return launch_rpl_tr<TIQ<RplIQ1S>>(b, d_gy, d_gx, batch, s);
+    case FMT_IQ2_XXS: return launch_rpl_tr<TIQ<RplIQ2XXS>>(b, d_gy, d_gx, batch, s);
+    case FMT_IQ2_XS: return launch_rpl_tr<TIQ<RplIQ2XS>>(b, d_gy, d_gx, batch, s);
+    case FMT_IQ3_XXS: return launch_rpl_tr<TIQ<RplIQ3XXS>>(b, d_gy, d_gx, batch, s);
+    case FMT_IQ3_S: return launch_rpl_tr<TIQ<RplIQ3S>>(b, d_gy, d_gx, batch, s);
+    case FMT_IQ4_XS: return launch_rpl_tr<TIQ<RplIQ4XS>>(b, d_gy, d_gx, batch, s);
     default: return int(hipErrorInvalidValue);
     }
 }

@@ -251,6 +251,83 @@ void build_rpl(int fmt, const uint8_t* raw, int64_t rows, int64_t cols, Image& i
     for (auto& t : th) t.join();
 }
 
+// Row-interleaved layout for the linear IQ formats (iq_rpl_spec): the codes
+// come from Raw, one flat LSB-first stream over the whole matrix (element
+// r*cols + c at bit (r*cols + c)*bits, quant/iq.go:182-207), and the group
+// scales from Scales. Planes per 32-column chunk and lane: 4-bit codes as
+// nibbles (16 B); 2- and 3-bit codes as Q2_K / Q3_K (8 B + 4 B of third
+// bits); 1-bit codes as one 32-bit word holding at bit s of byte b the code
+// of column 8(s/2) + 2b + s%2. Meta: per super-block 8 (group 32) or 16
+// (group 16) f32 scales.
+void build_rpl_iq(int fmt, const uint8_t* raw, size_t raw_len, const float* scales, int64_t rows, int64_t cols,
+                  Image& img, RplOffsets& o) {
+    IQSpec is;
+    iq_spec(fmt, is);
+    const int bits = is.bits, sg = is.sg;
+    const int64_t rg = (rows + 63) / 64, nch = cols / 32, nsb = cols / 256;
+    const int cb = bits == 4 ? 16 : bits >= 2 ? 8 : 4, mb = sg == 16 ? 64 : 32;
+    o.codes = img.add(size_t(rg * nch * 64 * cb));
+    if (bits == 3) o.hi = img.add(size_t(rg * nch * 64 * 4));
+    o.meta = img.add(size_t(rg * nsb * 64 * mb));
+    uint8_t* base = img.bytes.data();
+    uint8_t* codes = base + o.codes;
+    uint8_t* hi = base + o.hi;
+    uint8_t* meta = base + o.meta;
+    auto work = [&](int64_t g0, int64_t g1) {
+        for (int64_t g = g0; g < g1; ++g)
+            for (int lane = 0; lane < 64; ++lane) {
+                const int64_t row = g * 64 + lane;
+                if (row >= rows) continue;
+                for (int64_t sb = 0; sb < nsb; ++sb) {
+                    float* m = reinterpret_cast<float*>(meta + ((g * nsb + sb) * 64 + lane) * mb);
+                    for (int p = 0; p < 8; ++p) {
+                        const int64_t i0 = row * cols + sb * 256 + p * 32;
+                        if (sg == 16) {
+                            m[2 * p] = scales[i0 / 16];
+                            m[2 * p + 1] = scales[i0 / 16 + 1];
+                        } else {
+                            m[p] = scales[i0 / 32];
+                        }
+                        uint8_t qv[32];
+                        for (int k = 0; k < 32; ++k) {
+                            const int64_t bit = (i0 + k) * bits;
+                            const int64_t by = bit >> 3;
+                            const uint32_t v = raw[by] | (size_t(by + 1) < raw_len ? uint32_t(raw[by + 1]) << 8 : 0u);
+                            qv[k] = uint8_t((v >> (bit & 7)) & ((1u << bits) - 1));
+                        }
+                        auto code = [&](int sw, int b) { return qv[8 * (sw >> 1) + 2 * b + (sw & 1)]; };
+                        const int64_t ci = ((p * rg + g) * nsb + sb) * 64 + lane;
+                        uint8_t* c = codes + ci * cb;
+                        std::memset(c, 0, size_t(cb));
+                        if (bits == 4) {
+                            for (int k = 0; k < 16; ++k) c[k] = uint8_t(qv[2 * k] | (qv[2 * k + 1] << 4));
+                        } else if (bits == 1) {
+                            for (int sw = 0; sw < 8; ++sw)
+                                for (int b = 0; b < 4; ++b) c[b] |= uint8_t((code(sw, b) & 1) << sw);
+                        } else {
+                            for (int sw = 0; sw < 8; ++sw)
+                                for (int b = 0; b < 4; ++b) c[4 * (sw >> 2) + b] |= uint8_t((code(sw, b) & 3) << (2 * (sw & 3)));
+                            if (bits == 3) {
+                                uint8_t* h = hi + ci * 4;
+                                std::memset(h, 0, 4);
+                                for (int sw = 0; sw < 8; ++sw)
+                                    for (int b = 0; b < 4; ++b) h[b] |= uint8_t(((code(sw, b) >> 2) & 1) << sw);
+                            }
+                        }
+                    }
+                }
+            }
+    };
+    const int64_t nthreads = std::min<int64_t>(std::max(1u, std::thread::hardware_concurrency()), std::max<int64_t>(1, rg / 4));
+    std::vector<std::thread> th;
+    const int64_t per = (rg + nthreads - 1) / nthreads;
+    for (int64_t t = 0; t < nthreads; ++t) {
+        const int64_t g0 = t * per, g1 = std::min(rg, g0 + per);
+        if (g0 < g1) th.emplace_back(work, g0, g1);
+    }
+    for (auto& t : th) t.join();
+}
+
 int upload_image(const Image& img, DevBlob& b) {
     void* d = nullptr;
     hipError_t e = hipMalloc(&d, std::max<size_t>(img.bytes.size(), 256));
@@ -439,6 +516,12 @@ int wv_blob_upload(int format, int64_t rows, int64_t cols, int32_t block_weights
     Image img;
     const bool raw_only = force_raw();
     RplOffsets ro;
+    IQSpec iqs;
+    if (iq_spec(format, iqs)) {
+        if (n_meta >= 2) { iqs.bits = meta[0]; iqs.sg = meta[1]; }
+        b.iq_bits = iqs.bits;
+        b.iq_sg = iqs.sg;
+    }
     size_t o_codes = 0, o_raw = 0, o_sc = 0, o_mn = 0;
     if (format == FMT_NATIVE_TERNARY) {
         b.layout = LAYOUT_TERNARY_I8;
@@ -452,6 +535,9 @@ int wv_blob_upload(int format, int64_t rows, int64_t cols, int32_t block_weights
                cols % 256 == 0) {
         b.layout = LAYOUT_RPL;
         build_rpl(format, raw, rows, cols, img, ro);
+    } else if (!raw_only && iq_rpl_spec(format, b.iq_bits, b.iq_sg) && cols % 256 == 0) {
+        b.layout = LAYOUT_RPL;
+        build_rpl_iq(format, raw, raw_len, scales, rows, cols, img, ro);
     } else {
         b.layout = LAYOUT_RAW;
         // 16 bytes of padding: the vectorized decoder reads whole aligned
@@ -459,12 +545,6 @@ int wv_blob_upload(int format, int64_t rows, int64_t cols, int32_t block_weights
         o_raw = img.add(size_t(need) + 16);
         std::memcpy(img.bytes.data() + o_raw, raw, size_t(need));
         b.raw_len = need;
-        IQSpec is;
-        if (iq_spec(format, is)) {
-            if (n_meta >= 2) { is.bits = meta[0]; is.sg = meta[1]; }
-            b.iq_bits = is.bits;
-            b.iq_sg = is.sg;
-        }
         if (format == FMT_AFFINE) {
             b.n_mins = rows * (cols / block_weights);
             o_mn = img.add(size_t(b.n_mins) * 4);

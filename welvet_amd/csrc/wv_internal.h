@@ -59,6 +59,13 @@ inline bool iq_spec(int fmt, IQSpec& s) {
     }
 }
 
+// An IQ blob goes to the row-interleaved layout when it is linear and keeps its
+// format's default code width and scale group (the kernels are built for those).
+inline bool iq_rpl_spec(int fmt, int bits, int sg) {
+    IQSpec s;
+    return iq_spec(fmt, s) && !s.nonlinear && bits == s.bits && sg == s.sg;
+}
+
 // IQ4_NL grid: a data table whose values must equal quant/iq.go:23-40.
 constexpr float kIQ4NLGrid[16] = {
     -1.0f, -0.6961928f, -0.52507305f, -0.3949175f, -0.28444138f, -0.18477343f,
