@@ -49,7 +49,7 @@ WORKLOADS = {
     "ternary_2560x6912": ("NativeTernary", 6912, 2560, "DTypeTernary int8 GEMV 2560->6912 b=1"),
     "ternary_6912x2560": ("NativeTernary", 2560, 6912, "DTypeTernary int8 GEMV 6912->2560 b=1"),
 }
-# Every other packed format at the headline shape (reference-layout kernels).
+# Every other packed format at the headline shape (row-interleaved where the format has it, else the reference layout).
 WORKLOADS.update({
     f"{f.lower()}_4096x14336": (f, 14336, 4096, f"{f} dequant-GEMV 4096->14336 b=1")
     for f in ("Q4_0", "Q4_1", "Q5_0", "Q5_1", "Q2_K", "Q3_K", "Q5_K", "IQ1_S", "IQ2_XXS", "IQ2_XS", "IQ3_XXS",

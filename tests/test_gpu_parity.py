@@ -19,7 +19,8 @@ ALL = ["Q4_0", "Q8_0", "Q4_1", "Q5_0", "Q5_1", "Q2_K", "Q3_K", "Q4_K", "Q5_K", "
        "IQ1_S", "IQ2_XXS", "IQ2_XS", "IQ3_XXS", "IQ3_S", "IQ4_NL", "IQ4_XS",
        "TernaryPacked", "BinaryPacked"]
 PLANAR = {f: "row-interleaved" for f in ("Q2_K", "Q3_K", "Q4_K", "Q5_K", "Q6_K", "Q8_0", "Q4_0", "Q4_1", "Q5_0", "Q5_1",
-                                          "IQ1_S", "IQ2_XXS", "IQ2_XS", "IQ3_XXS", "IQ3_S", "IQ4_XS")}
+                                          "IQ1_S", "IQ2_XXS", "IQ2_XS", "IQ3_XXS", "IQ3_S", "IQ4_XS",
+                                          "TernaryPacked", "BinaryPacked", "AffinePacked")}
 
 
 @pytest.fixture(scope="module", autouse=True)
@@ -268,6 +269,29 @@ def test_device_pointer_path_on_torch_stream():
     s.synchronize()
     ref = oracle.reference_y(oracle_packed(p), x)[0]
     assert normwise(ty.cpu().numpy(), ref) <= TOL
+
+
+@pytest.mark.parametrize("rows,cols", [(70, 512), (130, 2048)])
+def test_ternary_code3_and_missing_scales(rows, cols):
+    """TernaryPacked words holding code 3 (which decodes as 0, ternary.go:53-62)
+    and fewer scales than groups (missing ones read as 1, ternary.go:69-72),
+    on the row-interleaved layout and the reference one."""
+    rng = np.random.default_rng(rows)
+    words = rng.integers(0, 2**32, size=rows * cols // 16, dtype=np.uint64).astype(np.uint32)
+    scales = (np.abs(rng.standard_normal(rows * cols // 16 - 37)) * 0.02 + 1e-3).astype(np.float32)
+    p = wv.PackedBlob("TernaryPacked", rows, cols, words.view(np.uint8), scales, None, 16)
+    x = rng.standard_normal(cols).astype(np.float32)
+    op = oracle.Packed(p.fmt, rows, cols, p.raw, scales, None, 16)
+    ref = oracle.reference_y(op, x)[0]
+    for force_raw in (False, True):
+        os.environ["WV_FORCE_RAW"] = "1" if force_raw else "0"
+        try:
+            d = wv.upload(p)
+        finally:
+            os.environ.pop("WV_FORCE_RAW")
+        assert d.info()["layout"] == ("raw" if force_raw else "row-interleaved")
+        assert normwise(d.matvec(x), ref) <= TOL
+        d.free()
 
 
 def test_binary_g128_layout():

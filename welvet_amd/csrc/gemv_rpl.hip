@@ -229,8 +229,11 @@ struct RplKxI : RplQ4KI {
 // of the lane's 16-word super-block record. Codes are spread as in RplKxI
 // (B = 5 adds the fifth-bit plane); the two 16-column group sums stay exact
 // in int32 and are added as floats.
-template <int B, bool MIN, int OFF, uint32_t XR>
+template <int B, bool MIN, int OFF, uint32_t XR, int GSH = 0>
 struct RplB32I {
+    // GSH: chunk j's scale (and min) is group j >> GSH of the super-block
+    // (AffinePacked with 64-column groups: GSH = 1); NG groups, the mins follow the scales.
+    static constexpr int NG = 8 >> GSH, NW = MIN ? 2 * NG : NG;
     static constexpr bool kIntX = true;
     static constexpr bool kWords2 = MIN;
     struct Ch { uint4 c; uint32_t h; };
@@ -242,32 +245,29 @@ struct RplB32I {
         return r;
     }
     static __device__ __forceinline__ Sb load_sb(const RplArgs& a, int64_t si, int lane) {
-        const uint4* m = reinterpret_cast<const uint4*>(a.meta) + (si * 64 + lane) * (MIN ? 4 : 2);
+        const uint4* m = reinterpret_cast<const uint4*>(a.meta) + (si * 64 + lane) * (NW / 4);
         Sb r;
+        const uint4 z = make_uint4(0u, 0u, 0u, 0u);
         r.s0 = ld_stream(m);
-        r.s1 = ld_stream(m + 1);
-        if constexpr (MIN) {
-            r.m0 = ld_stream(m + 2);
-            r.m1 = ld_stream(m + 3);
-        } else {
-            r.m0 = r.m1 = make_uint4(0u, 0u, 0u, 0u);
-        }
+        r.s1 = NW >= 8 ? ld_stream(m + 1) : z;
+        r.m0 = NW >= 12 ? ld_stream(m + 2) : z;
+        r.m1 = NW >= 16 ? ld_stream(m + 3) : z;
         return r;
     }
-    static __device__ __forceinline__ uint32_t word(const Sb& sb, int j) {
-        const uint32_t sw[8] = {sb.s0.x, sb.s0.y, sb.s0.z, sb.s0.w, sb.s1.x, sb.s1.y, sb.s1.z, sb.s1.w};
-        return sw[j];
+    static __device__ __forceinline__ uint32_t sw(const Sb& sb, int k) {
+        const uint32_t w[16] = {sb.s0.x, sb.s0.y, sb.s0.z, sb.s0.w, sb.s1.x, sb.s1.y, sb.s1.z, sb.s1.w,
+                                sb.m0.x, sb.m0.y, sb.m0.z, sb.m0.w, sb.m1.x, sb.m1.y, sb.m1.z, sb.m1.w};
+        return w[k];
     }
-    static __device__ __forceinline__ uint32_t word2(const Sb& sb, int j) {
-        const uint32_t mw[8] = {sb.m0.x, sb.m0.y, sb.m0.z, sb.m0.w, sb.m1.x, sb.m1.y, sb.m1.z, sb.m1.w};
-        return mw[j];
-    }
+    static __device__ __forceinline__ uint32_t word(const Sb& sb, int j) { return sw(sb, j >> GSH); }
+    static __device__ __forceinline__ uint32_t word2(const Sb& sb, int j) { return sw(sb, NG + (j >> GSH)); }
     static __device__ __forceinline__ Sb with_word(Sb sb, uint32_t w) {
         sb.s0.x = w;
         return sb;
     }
-    static __device__ __forceinline__ Sb with_word2(Sb sb, uint32_t w) {
-        sb.m0.x = w;
+    static __device__ __forceinline__ Sb with_word2(Sb sb, uint32_t w) {  // the slot word2(sb, 0) reads
+        if constexpr (NG == 8) sb.m0.x = w;
+        else sb.s1.x = w;
         return sb;
     }
     static __device__ __forceinline__ uint32_t spread(const Ch& ch, int s) {
@@ -301,6 +301,7 @@ using RplQ4I = RplB32I<4, false, 8, 0x88888888u>;
 using RplQ41I = RplB32I<4, true, 0, 0u>;
 using RplQ50I = RplB32I<5, false, 16, 0u>;
 using RplQ51I = RplB32I<5, true, 0, 0u>;
+using RplAff64I = RplB32I<4, true, 0, 0u, 1>;  // AffinePacked, 64-column groups: w = scale*code + min
 
 // The linear IQ formats at their default code width and scale group
 // (quant/iq.go:49-68, 169-180): w = scale*(q - mid), and for one-bit codes
@@ -401,6 +402,9 @@ using RplIQ2XS = RplIQI<2, true, 3>;
 using RplIQ3XXS = RplIQI<3, false, 7>;
 using RplIQ3S = RplIQI<3, true, 7>;
 using RplIQ4XS = RplIQI<4, true, 15>;
+// TernaryPacked (quant/ternary.go:53-62): codes 0/1/2 -> -s/0/+s per 16 weights,
+// i.e. s*(q - 1); the layout stores code 3 (also 0) as 1.
+using RplTernI = RplIQI<2, true, 2>;
 
 struct RplQ6K {  // q = lo4 | hi2 << 4, w = (d*u/255)*(q - 32)
     static constexpr bool kIntX = false;
@@ -1017,14 +1021,20 @@ struct TKx : RplKxI<B> {
     }
 };
 
-template <int B, bool MIN, int OFF, uint32_t XR>
-struct TB32 : RplB32I<B, MIN, OFF, XR> {
-    using P = RplB32I<B, MIN, OFF, XR>;
+template <int B, bool MIN, int OFF, uint32_t XR, int GSH = 0>
+struct TB32 : RplB32I<B, MIN, OFF, XR, GSH> {
+    using P = RplB32I<B, MIN, OFF, XR, GSH>;
     using Ch = typename P::Ch;
     struct TM { uint2 s, m; };  // scales (and mins) of chunks 2jp, 2jp+1
     static __device__ __forceinline__ TM load_tm(const RplArgs& a, int64_t si, int lane, int jp) {
-        const uint2* m = reinterpret_cast<const uint2*>(a.meta) + (si * 64 + lane) * (MIN ? 8 : 4);
-        return {ld_stream(m + jp), MIN ? ld_stream(m + 4 + jp) : make_uint2(0u, 0u)};
+        const uint32_t* m = reinterpret_cast<const uint32_t*>(a.meta) + (si * 64 + lane) * P::NW;
+        if constexpr (GSH == 0) {
+            const uint2* m2 = reinterpret_cast<const uint2*>(m);
+            return {ld_stream(m2 + jp), MIN ? ld_stream(m2 + 4 + jp) : make_uint2(0u, 0u)};
+        } else {  // both chunks in group jp
+            const uint32_t sc = m[jp], mn = MIN ? m[P::NG + jp] : 0u;
+            return {make_uint2(sc, sc), make_uint2(mn, mn)};
+        }
     }
     static __device__ __forceinline__ void tacc_w(const Ch& ch, int w, float coef, float* acc) {
         uint32_t lo = P::spread(ch, 2 * w), hi = P::spread(ch, 2 * w + 1);
@@ -1320,6 +1330,9 @@ int launch_rpl_ex(const DevBlob& b, const float* d_x, float* d_y, int batch, voi
     case FMT_Q4_1: return launch_rpl_t<RplQ41I>(b, d_x, d_y, batch, s, ex);
     case FMT_Q5_0: return launch_rpl_t<RplQ50I>(b, d_x, d_y, batch, s, ex);
     case FMT_Q5_1: return launch_rpl_t<RplQ51I>(b, d_x, d_y, batch, s, ex);
+    case FMT_AFFINE: return launch_rpl_t<RplAff64I>(b, d_x, d_y, batch, s, ex);
+    case FMT_TERNARY: return launch_rpl_t<RplTernI>(b, d_x, d_y, batch, s, ex);
+    case FMT_BINARY: return launch_rpl_t<RplIQ1S>(b, d_x, d_y, batch, s, ex);  // +-scale per 32, as IQ1_S
     case FMT_IQ1_S: return launch_rpl_t<RplIQ1S>(b, d_x, d_y, batch, s, ex);
     case FMT_IQ2_XXS: return launch_rpl_t<RplIQ2XXS>(b, d_x, d_y, batch, s, ex);
     case FMT_IQ2_XS: return launch_rpl_t<RplIQ2XS>(b, d_x, d_y, batch, s, ex);
@@ -1344,11 +1357,14 @@ struct RplItems {
     int cb, hb, mb, db;  // code chunk (x8 planes), high-bit chunk (x8), metadata, (d, dmin)
 };
 bool rpl_items(const DevBlob& b, RplItems& it) {
-    IQSpec is;
-    if (iq_rpl_spec(b.fmt, b.iq_bits, b.iq_sg)) {
-        iq_spec(b.fmt, is);
-        const int cb = is.bits == 4 ? 16 : is.bits >= 2 ? 8 : 4;
-        it = {cb, is.bits == 3 ? 4 : 0, is.sg == 16 ? 64 : 32, 0};
+    LinCodes lc;
+    if (rpl_lin_spec(b.fmt, b.block_weights, b.iq_bits, b.iq_sg, lc)) {
+        const int cb = lc.bits == 4 ? 16 : lc.bits >= 2 ? 8 : 4;
+        it = {cb, lc.bits == 3 ? 4 : 0, lc.sg == 16 ? 64 : 32, 0};
+        return true;
+    }
+    if (b.fmt == FMT_AFFINE && b.block_weights == 64) {
+        it = {16, 0, 32, 0};
         return true;
     }
     switch (b.fmt) {
@@ -1413,6 +1429,7 @@ int finish_fused(const DevBlob& proto, int64_t rows, int64_t rg, const FusedLayo
     out.fmt = proto.fmt;
     out.iq_bits = proto.iq_bits;
     out.iq_sg = proto.iq_sg;
+    out.block_weights = proto.block_weights;
     out.rows = rows;
     out.cols = proto.cols;
     out.layout = LAYOUT_RPL;
@@ -1444,7 +1461,7 @@ int rpl_fuse_rows(const DevBlob* parts, int n, DevBlob& out, void* stream) {
     for (int i = 0; i < n; ++i) {
         const DevBlob& b = parts[i];
         if (b.layout != LAYOUT_RPL || b.fmt != parts[0].fmt || b.cols != parts[0].cols || b.rows % 64 ||
-            b.iq_bits != parts[0].iq_bits || b.iq_sg != parts[0].iq_sg)
+            b.iq_bits != parts[0].iq_bits || b.iq_sg != parts[0].iq_sg || b.block_weights != parts[0].block_weights)
             return int(hipErrorInvalidValue);
         rg += b.rpl.rg_count;
         rows += b.rows;
@@ -1485,7 +1502,7 @@ int rpl_fuse_pairs(const DevBlob& a, const DevBlob& b, DevBlob& out, void* strea
     hipStream_t s = static_cast<hipStream_t>(stream);
     RplItems it{};
     if (!rpl_items(a, it) || a.layout != LAYOUT_RPL || b.layout != LAYOUT_RPL || a.fmt != b.fmt ||
-        a.iq_bits != b.iq_bits || a.iq_sg != b.iq_sg ||
+        a.iq_bits != b.iq_bits || a.iq_sg != b.iq_sg || a.block_weights != b.block_weights ||
         a.rows != b.rows || a.cols != b.cols || a.rows % 32)
         return int(hipErrorInvalidValue);
     const int64_t rg_in = a.rpl.rg_count, rg = 2 * rg_in, nsb = a.rpl.nsb;
@@ -1537,6 +1554,9 @@ int launch_rpl_matvec_t(const DevBlob& b, const float* d_gy, float* d_gx, int ba
     case FMT_Q4_1: return launch_rpl_tr<TB32<4, true, 0, 0u>>(b, d_gy, d_gx, batch, s);
     case FMT_Q5_0: return launch_rpl_tr<TB32<5, false, 16, 0u>>(b, d_gy, d_gx, batch, s);
     case FMT_Q5_1: return launch_rpl_tr<TB32<5, true, 0, 0u>>(b, d_gy, d_gx, batch, s);
+    case FMT_AFFINE: return launch_rpl_tr<TB32<4, true, 0, 0u, 1>>(b, d_gy, d_gx, batch, s);
+    case FMT_TERNARY: return launch_rpl_tr<TIQ<RplTernI>>(b, d_gy, d_gx, batch, s);
+    case FMT_BINARY: return launch_rpl_tr<TIQ<RplIQ1S>>(b, d_gy, d_gx, batch, s);
     case FMT_IQ1_S: return launch_rpl_tr<TIQ<RplIQ1S>>(b, d_gy, d_gx, batch, s);
     case FMT_IQ2_XXS: return launch_rpl_tr<TIQ<RplIQ2XXS>>(b, d_gy, d_gx, batch, s);
     case FMT_IQ2_XS: return launch_rpl_tr<TIQ<RplIQ2XS>>(b, d_gy, d_gx, batch, s);

@@ -259,11 +259,10 @@ void build_rpl(int fmt, const uint8_t* raw, int64_t rows, int64_t cols, Image& i
 // bits); 1-bit codes as one 32-bit word holding at bit s of byte b the code
 // of column 8(s/2) + 2b + s%2. Meta: per super-block 8 (group 32) or 16
 // (group 16) f32 scales.
-void build_rpl_iq(int fmt, const uint8_t* raw, size_t raw_len, const float* scales, int64_t rows, int64_t cols,
-                  Image& img, RplOffsets& o) {
-    IQSpec is;
-    iq_spec(fmt, is);
-    const int bits = is.bits, sg = is.sg;
+void build_rpl_lin(const LinCodes& lc, const uint8_t* raw, size_t raw_len, const float* scales, size_t n_scales,
+                   int64_t rows, int64_t cols, Image& img, RplOffsets& o) {
+    const int bits = lc.bits, sg = lc.sg;
+    auto scale_at = [&](int64_t g) { return size_t(g) < n_scales && scales ? scales[g] : 1.0f; };
     const int64_t rg = (rows + 63) / 64, nch = cols / 32, nsb = cols / 256;
     const int cb = bits == 4 ? 16 : bits >= 2 ? 8 : 4, mb = sg == 16 ? 64 : 32;
     o.codes = img.add(size_t(rg * nch * 64 * cb));
@@ -283,10 +282,10 @@ void build_rpl_iq(int fmt, const uint8_t* raw, size_t raw_len, const float* scal
                     for (int p = 0; p < 8; ++p) {
                         const int64_t i0 = row * cols + sb * 256 + p * 32;
                         if (sg == 16) {
-                            m[2 * p] = scales[i0 / 16];
-                            m[2 * p + 1] = scales[i0 / 16 + 1];
+                            m[2 * p] = scale_at(i0 / 16);
+                            m[2 * p + 1] = scale_at(i0 / 16 + 1);
                         } else {
-                            m[p] = scales[i0 / 32];
+                            m[p] = scale_at(i0 / 32);
                         }
                         uint8_t qv[32];
                         for (int k = 0; k < 32; ++k) {
@@ -294,6 +293,7 @@ void build_rpl_iq(int fmt, const uint8_t* raw, size_t raw_len, const float* scal
                             const int64_t by = bit >> 3;
                             const uint32_t v = raw[by] | (size_t(by + 1) < raw_len ? uint32_t(raw[by + 1]) << 8 : 0u);
                             qv[k] = uint8_t((v >> (bit & 7)) & ((1u << bits) - 1));
+                            if (lc.remap3 && qv[k] == 3) qv[k] = 1;  // TernaryPacked: code 3 decodes as 0
                         }
                         auto code = [&](int sw, int b) { return qv[8 * (sw >> 1) + 2 * b + (sw & 1)]; };
                         const int64_t ci = ((p * rg + g) * nsb + sb) * 64 + lane;
@@ -326,6 +326,33 @@ void build_rpl_iq(int fmt, const uint8_t* raw, size_t raw_len, const float* scal
         if (g0 < g1) th.emplace_back(work, g0, g1);
     }
     for (auto& t : th) t.join();
+}
+
+// AffinePacked with 64-column groups (affine_g64.go:124-161): 4-bit codes,
+// element i at nibble i of Raw (low nibble first), as Q4_K's planes; meta per
+// super-block and lane: the 4 group scales, then the 4 group mins (f32).
+void build_rpl_affine(const uint8_t* raw, const float* scales, const float* mins, int64_t rows, int64_t cols, Image& img,
+                      RplOffsets& o) {
+    const int64_t rg = (rows + 63) / 64, nch = cols / 32, nsb = cols / 256, gpr = cols / 64;
+    o.codes = img.add(size_t(rg * nch * 64 * 16));
+    o.meta = img.add(size_t(rg * nsb * 64 * 32));
+    uint8_t* base = img.bytes.data();
+    uint8_t* codes = base + o.codes;
+    uint8_t* meta = base + o.meta;
+    for (int64_t g = 0; g < rg; ++g)
+        for (int lane = 0; lane < 64; ++lane) {
+            const int64_t row = g * 64 + lane;
+            if (row >= rows) continue;
+            for (int64_t sb = 0; sb < nsb; ++sb) {
+                float* m = reinterpret_cast<float*>(meta + ((g * nsb + sb) * 64 + lane) * 32);
+                for (int q = 0; q < 4; ++q) {
+                    m[q] = scales[row * gpr + sb * 4 + q];
+                    m[4 + q] = mins[row * gpr + sb * 4 + q];
+                }
+                for (int p = 0; p < 8; ++p)
+                    std::memcpy(codes + (((p * rg + g) * nsb + sb) * 64 + lane) * 16, raw + (row * cols + sb * 256 + p * 32) / 2, 16);
+            }
+        }
 }
 
 int upload_image(const Image& img, DevBlob& b) {
@@ -535,9 +562,12 @@ int wv_blob_upload(int format, int64_t rows, int64_t cols, int32_t block_weights
                cols % 256 == 0) {
         b.layout = LAYOUT_RPL;
         build_rpl(format, raw, rows, cols, img, ro);
-    } else if (!raw_only && iq_rpl_spec(format, b.iq_bits, b.iq_sg) && cols % 256 == 0) {
+    } else if (LinCodes lc; !raw_only && rpl_lin_spec(format, block_weights, b.iq_bits, b.iq_sg, lc) && cols % 256 == 0) {
         b.layout = LAYOUT_RPL;
-        build_rpl_iq(format, raw, raw_len, scales, rows, cols, img, ro);
+        build_rpl_lin(lc, raw, raw_len, scales, n_scales, rows, cols, img, ro);
+    } else if (!raw_only && format == FMT_AFFINE && block_weights == 64 && cols % 256 == 0) {
+        b.layout = LAYOUT_RPL;
+        build_rpl_affine(raw, scales, mins, rows, cols, img, ro);
     } else {
         b.layout = LAYOUT_RAW;
         // 16 bytes of padding: the vectorized decoder reads whole aligned

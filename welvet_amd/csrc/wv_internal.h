@@ -65,6 +65,29 @@ inline bool iq_rpl_spec(int fmt, int bits, int sg) {
     IQSpec s;
     return iq_spec(fmt, s) && !s.nonlinear && bits == s.bits && sg == s.sg;
 }
+// Formats whose codes form one matrix-wide LSB-first stream of `bits`-bit
+// codes with one f32 scale per `sg` weights: the linear IQ formats,
+// TernaryPacked (2 bits, 16 weights; code 3 reads as 1) and BinaryPacked with
+// 32-weight groups (1 bit). Missing Ternary / Binary scales read as 1.
+struct LinCodes {
+    int bits = 0, sg = 0;
+    bool remap3 = false;
+};
+inline bool rpl_lin_spec(int fmt, int block_weights, int iq_bits, int iq_sg, LinCodes& lc) {
+    if (iq_rpl_spec(fmt, iq_bits, iq_sg)) {
+        lc = {iq_bits, iq_sg, false};
+        return true;
+    }
+    if (fmt == FMT_TERNARY) {
+        lc = {2, 16, true};
+        return true;
+    }
+    if (fmt == FMT_BINARY && block_weights != 128) {
+        lc = {1, 32, false};
+        return true;
+    }
+    return false;
+}
 
 // IQ4_NL grid: a data table whose values must equal quant/iq.go:23-40.
 constexpr float kIQ4NLGrid[16] = {
