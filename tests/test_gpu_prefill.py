@@ -81,6 +81,29 @@ def test_prefill_q4k_wide(shape, m):
     d.free()
 
 
+@pytest.mark.parametrize("fmt", ["Q2_K", "Q3_K", "Q5_K", "Q6_K", "Q8_0"])
+@pytest.mark.parametrize("shape,m", [((256, 1024), 128), ((448, 2048), 300), ((1000, 4096), 130)])
+def test_prefill_other_kquants_mfma(fmt, shape, m):
+    """Token blocks over 64 of Q2_K, Q3_K, Q5_K (Q4_K's metadata with other
+    code planes), Q6_K and Q8_0 take the packed-W MFMA GEMM."""
+    rows, cols = shape
+    print(f"[gpu] prefill {fmt} {cols}->{rows} M={m}", flush=True)
+    rng = np.random.default_rng(rows + m)
+    w = (rng.standard_normal(rows * cols, dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+    p = wv.pack(fmt, w, rows, cols)
+    wd = oracle.unpack(oracle.Packed(p.fmt, rows, cols, p.raw, p.scales, p.meta, p.block_weights))
+    wd = wd.reshape(rows, cols).astype(np.float64)
+    d = wv.upload(p)
+    assert d.info()["layout"] == "row-interleaved"
+    x = rng.standard_normal((m, cols)).astype(np.float32)
+    ref = x.astype(np.float64) @ wd.T
+    for _ in range(2):
+        y = d.matmul(x)
+        assert normwise(y, ref) <= TOL_MFMA
+        assert rowwise(y, ref) <= 4 * TOL_MFMA
+    d.free()
+
+
 _BASE = {}
 
 

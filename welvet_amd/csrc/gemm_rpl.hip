@@ -26,7 +26,8 @@
 //
 // Token blocks of more than 64 use k_gemm_q4k_pw instead: W goes from the
 // planes straight into MFMA B operands (a lane swap puts the row-interleaved
-// chunks into the 32x32x16 operand layout) and only X passes through LDS.
+// chunks into the 32x32x16 operand layout) and only X passes through LDS. It
+// also serves Q2_K, Q3_K, Q5_K, Q6_K and Q8_0 (per-format B-operand builders).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -88,6 +89,183 @@ __device__ __forceinline__ uint4 dequant8p(uint32_t v, half2v sc, half2v mn) {
     }
     return make_uint4(p[0], p[1], p[2], p[3]);
 }
+
+// The same from two spread words (byte b of `se` / `so` = the code of column
+// 2b / 2b + 1 of an 8-column run, any width up to 5 bits): k order
+// [0,2,4,6,1,3,5,7] as dequant8p.
+__device__ __forceinline__ uint4 dequant8s(uint32_t se, uint32_t so, half2v sc, half2v mn) {
+    const half2v k1024 = {_Float16(1024.0f), _Float16(1024.0f)};
+    const uint32_t e = 0x64646464u;
+    const uint32_t hb[4] = {__builtin_amdgcn_perm(e, se, 0x04010400u), __builtin_amdgcn_perm(e, se, 0x04030402u),
+                            __builtin_amdgcn_perm(e, so, 0x04010400u), __builtin_amdgcn_perm(e, so, 0x04030402u)};
+    uint32_t p[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const half2v q = __builtin_bit_cast(half2v, hb[i]) - k1024;
+        p[i] = __builtin_bit_cast(uint32_t, q * sc + mn);
+    }
+    return make_uint4(p[0], p[1], p[2], p[3]);
+}
+
+// Code planes of one 32-column chunk of a k-quant row (lane = row) and, after
+// the lane swaps, the spread words of the MFMA B operands: for 32-row tile T
+// and k16 step kk, lanes 0-31 take columns 16kk + 0..7 of rows 32T + lane and
+// lanes 32-63 columns 16kk + 8..15 of the same rows. FB = code bits (2, 3, 4,
+// 5); the planes are those of the forward kernels (Q4_K nibbles; Q5_K fifth
+// bits; Q2_K / Q3_K two-bit plane and third bits).
+template <int FB>
+struct GemmCodes {
+    struct C { uint4 c; uint32_t h; };
+    static __device__ __forceinline__ C load(const RplArgs& a, int64_t ci, int lane) {
+        C r;
+        if constexpr (FB >= 4) {
+            r.c = ld_nt(reinterpret_cast<const uint4*>(a.codes) + ci * 64 + lane);
+        } else {
+            const uint2 v = reinterpret_cast<const uint2*>(a.codes)[ci * 64 + lane];
+            r.c = make_uint4(v.x, v.y, 0u, 0u);
+        }
+        r.h = (FB == 5 || FB == 3) ? reinterpret_cast<const uint32_t*>(a.hi)[ci * 64 + lane] : 0u;
+        return r;
+    }
+    // se/so[T][kk]: even / odd columns of the lane's 8-column run
+    static __device__ __forceinline__ void spread(const C& c, int lane, uint32_t (&se)[2][2], uint32_t (&so)[2][2]) {
+        const int up = lane >> 5;
+        if constexpr (FB >= 4) {
+            const auto k0 = __builtin_amdgcn_permlane32_swap(c.c.x, c.c.y, false, false);  // columns 0-15
+            const auto k1 = __builtin_amdgcn_permlane32_swap(c.c.z, c.c.w, false, false);  // columns 16-31
+#pragma unroll
+            for (int T = 0; T < 2; ++T) {
+                se[T][0] = k0[T] & 0x0F0F0F0Fu;
+                so[T][0] = (k0[T] >> 4) & 0x0F0F0F0Fu;
+                se[T][1] = k1[T] & 0x0F0F0F0Fu;
+                so[T][1] = (k1[T] >> 4) & 0x0F0F0F0Fu;
+            }
+        } else {  // dword kk holds spread words 4kk..4kk+3; this lane's are 4kk + 2up (+1)
+            const auto p0 = __builtin_amdgcn_permlane32_swap(c.c.x, c.c.x, false, false);
+            const auto p1 = __builtin_amdgcn_permlane32_swap(c.c.y, c.c.y, false, false);
+            const int sh = 4 * up;
+#pragma unroll
+            for (int T = 0; T < 2; ++T) {
+                se[T][0] = (p0[T] >> sh) & 0x03030303u;
+                so[T][0] = (p0[T] >> (sh + 2)) & 0x03030303u;
+                se[T][1] = (p1[T] >> sh) & 0x03030303u;
+                so[T][1] = (p1[T] >> (sh + 2)) & 0x03030303u;
+            }
+        }
+        if constexpr (FB == 5 || FB == 3) {  // top bit of spread word s at bit s of each byte
+            constexpr int top = FB == 5 ? 4 : 2;
+            const auto hh = __builtin_amdgcn_permlane32_swap(c.h, c.h, false, false);
+#pragma unroll
+            for (int T = 0; T < 2; ++T)
+#pragma unroll
+                for (int kk = 0; kk < 2; ++kk) {
+                    const int sb = 4 * kk + 2 * up;
+                    se[T][kk] |= ((hh[T] >> sb) & 0x01010101u) << top;
+                    so[T][kk] |= ((hh[T] >> (sb + 1)) & 0x01010101u) << top;
+                }
+        }
+    }
+};
+
+// Per-format B-operand builders of k_gemm_q4k_pw. Ch holds one 32-column
+// chunk of the lane's row (codes, the chunk's metadata, the super-block's
+// scales); bops() returns the fp16 B operands bf[T][kk] of 32-row tile T and
+// k16 step kk, in X's k order [0,2,4,6,1,3,5,7].
+template <int FB>
+struct GemmKQ {  // Q2_K, Q3_K, Q4_K, Q5_K: w = (d/255)*u*q + (dmin/127)*m
+    struct Ch { typename GemmCodes<FB>::C c; uint32_t mw; float2 dd; };
+    static __device__ __forceinline__ Ch load(const RplArgs& a, int64_t ci, int64_t si, int j, int lane) {
+        return {GemmCodes<FB>::load(a, ci, lane), reinterpret_cast<const uint32_t*>(a.meta)[(si * 64 + lane) * 8 + j],
+                reinterpret_cast<const float2*>(a.dd)[si * 64 + lane]};
+    }
+    static __device__ __forceinline__ void bops(const Ch& c, int lane, half8 (&bf)[2][2]) {
+        const auto d2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(c.dd.x), __float_as_uint(c.dd.x), false, false);
+        const auto m2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(c.dd.y), __float_as_uint(c.dd.y), false, false);
+        const auto mt = __builtin_amdgcn_permlane32_swap(c.mw, c.mw, false, false);
+        uint32_t se[2][2], so[2][2];
+        GemmCodes<FB>::spread(c.c, lane, se, so);
+#pragma unroll
+        for (int T = 0; T < 2; ++T) {
+            const float d255 = __uint_as_float(d2[T]) * (1.0f / 255.0f);
+            const float dm127 = __uint_as_float(m2[T]) * (1.0f / 127.0f);
+            const uint32_t gm = mt[T];
+            const _Float16 sc0 = _Float16(d255 * float(gm & 0xFFu));
+            const _Float16 sc1 = _Float16(d255 * float((gm >> 8) & 0xFFu));
+            const _Float16 mn0 = _Float16(dm127 * float(int8_t(gm >> 16)));
+            const _Float16 mn1 = _Float16(dm127 * float(int32_t(gm) >> 24));
+            const half2v s0 = {sc0, sc0}, s1 = {sc1, sc1}, n0 = {mn0, mn0}, n1 = {mn1, mn1};
+            bf[T][0] = __builtin_bit_cast(half8, dequant8s(se[T][0], so[T][0], s0, n0));
+            bf[T][1] = __builtin_bit_cast(half8, dequant8s(se[T][1], so[T][1], s1, n1));
+        }
+    }
+};
+
+struct GemmQ6 {  // Q6_K: q = lo4 | hi2 << 4, w = (d/255)*u*(q - 32)
+    struct Ch { uint4 c; uint2 h; uint32_t mw; float d; };
+    static __device__ __forceinline__ Ch load(const RplArgs& a, int64_t ci, int64_t si, int j, int lane) {
+        const uint32_t m = reinterpret_cast<const uint32_t*>(a.meta)[(si * 64 + lane) * 4 + (j >> 1)];
+        return {ld_nt(reinterpret_cast<const uint4*>(a.codes) + ci * 64 + lane),
+                reinterpret_cast<const uint2*>(a.hi)[ci * 64 + lane], m >> (16 * (j & 1)),
+                reinterpret_cast<const float*>(a.dd)[(si * 64 + lane) * 2]};
+    }
+    static __device__ __forceinline__ void bops(const Ch& c, int lane, half8 (&bf)[2][2]) {
+        typename GemmCodes<4>::C nib{c.c, 0u};
+        uint32_t se[2][2], so[2][2];
+        GemmCodes<4>::spread(nib, lane, se, so);
+        // high-bit dword kk holds spread words 4kk..4kk+3 at bits 2f; this lane's are 4kk + 2up (+1)
+        const int sh = 4 * (lane >> 5);
+        const auto h0 = __builtin_amdgcn_permlane32_swap(c.h.x, c.h.x, false, false);
+        const auto h1 = __builtin_amdgcn_permlane32_swap(c.h.y, c.h.y, false, false);
+        const auto dt = __builtin_amdgcn_permlane32_swap(__float_as_uint(c.d), __float_as_uint(c.d), false, false);
+        const auto mt = __builtin_amdgcn_permlane32_swap(c.mw, c.mw, false, false);
+#pragma unroll
+        for (int T = 0; T < 2; ++T) {
+            se[T][0] |= ((h0[T] >> sh) & 0x03030303u) << 4;
+            so[T][0] |= ((h0[T] >> (sh + 2)) & 0x03030303u) << 4;
+            se[T][1] |= ((h1[T] >> sh) & 0x03030303u) << 4;
+            so[T][1] |= ((h1[T] >> (sh + 2)) & 0x03030303u) << 4;
+            const float d255 = __uint_as_float(dt[T]) * (1.0f / 255.0f);
+            const _Float16 sc0 = _Float16(d255 * float(mt[T] & 0xFFu)), sc1 = _Float16(d255 * float((mt[T] >> 8) & 0xFFu));
+            const _Float16 mn0 = _Float16(-32.0f) * sc0, mn1 = _Float16(-32.0f) * sc1;
+            const half2v s0 = {sc0, sc0}, s1 = {sc1, sc1}, n0 = {mn0, mn0}, n1 = {mn1, mn1};
+            bf[T][0] = __builtin_bit_cast(half8, dequant8s(se[T][0], so[T][0], s0, n0));
+            bf[T][1] = __builtin_bit_cast(half8, dequant8s(se[T][1], so[T][1], s1, n1));
+        }
+    }
+};
+
+struct GemmQ8 {  // Q8_0: w = scale*q, q int8, 32 bytes per chunk (consecutive columns)
+    struct Ch { uint4 c0, c1; uint32_t sc; };
+    static __device__ __forceinline__ Ch load(const RplArgs& a, int64_t ci, int64_t si, int j, int lane) {
+        const uint4* p = reinterpret_cast<const uint4*>(a.codes) + (ci * 64 + lane) * 2;
+        return {ld_nt(p), ld_nt(p + 1), reinterpret_cast<const uint32_t*>(a.meta)[(si * 64 + lane) * 8 + j]};
+    }
+    static __device__ __forceinline__ void bops(const Ch& c, int lane, half8 (&bf)[2][2]) {
+        (void)lane;
+        const uint32_t dw[8] = {c.c0.x, c.c0.y, c.c0.z, c.c0.w, c.c1.x, c.c1.y, c.c1.z, c.c1.w};
+        const auto st = __builtin_amdgcn_permlane32_swap(c.sc, c.sc, false, false);
+        const half2v k1152 = {_Float16(1152.0f), _Float16(1152.0f)};
+        const uint32_t e = 0x64646464u;
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            // lanes 0-31: columns 16kk + 0..7 (dwords 4kk, 4kk+1); lanes 32-63: + 8..15
+            const auto A = __builtin_amdgcn_permlane32_swap(dw[4 * kk], dw[4 * kk + 2], false, false);
+            const auto B = __builtin_amdgcn_permlane32_swap(dw[4 * kk + 1], dw[4 * kk + 3], false, false);
+#pragma unroll
+            for (int T = 0; T < 2; ++T) {
+                const uint32_t lo = A[T] ^ 0x80808080u, hi = B[T] ^ 0x80808080u;  // q + 128 as unsigned bytes
+                const uint32_t hb[4] = {__builtin_amdgcn_perm(e, lo, 0x04020400u), __builtin_amdgcn_perm(e, hi, 0x04020400u),
+                                        __builtin_amdgcn_perm(e, lo, 0x04030401u), __builtin_amdgcn_perm(e, hi, 0x04030401u)};
+                const _Float16 sh = _Float16(__uint_as_float(st[T]));
+                const half2v s2 = {sh, sh};
+                uint32_t p[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) p[i] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(half2v, hb[i]) - k1152) * s2);
+                bf[T][kk] = __builtin_bit_cast(half8, make_uint4(p[0], p[1], p[2], p[3]));
+            }
+        }
+    }
+};
 
 struct GemmArgs {
     RplArgs w;
@@ -264,7 +442,7 @@ __global__ void __launch_bounds__(256) k_gemm_q4k(GemmArgs ga) {
 // LDS carries X alone: per K-step a block writes 16 KB of fp16 X and each
 // wave reads 16 KB back for 32 MFMAs (128 tokens x 64 rows x 64 columns),
 // against 96 KB per 16 MFMAs per wave with fp16 W tiles.
-template <int TM, int D>
+template <class GP, int TM, int D>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) k_gemm_q4k_pw(GemmArgs ga) {
     constexpr int BM = 32 * TM;
     constexpr int BNW = 256;                 // output rows per block: 4 waves x 64
@@ -283,10 +461,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
     const int g = min(nblk * 4 + wave, a.rg_count - 1);  // this wave's row group
 
     struct Regs {
-        uint4 c[2];      // codes of the step's two chunks (this lane's row)
-        uint32_t mw[2];  // their metadata words (u'0, u'1, m0, m1)
-        float2 dd;       // (d, dmin) of the super-block
-        uint4 xv[XB];    // fp16 X blocks
+        typename GP::Ch c[2];  // the step's two chunks of this lane's row
+        uint4 xv[XB];          // fp16 X blocks
     };
     auto load = [&](int s, Regs& r) {
         const int sb = sb0 + s / 4;
@@ -294,10 +470,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
 #pragma unroll
         for (int jj = 0; jj < 2; ++jj) {
             const int j = 2 * (s & 3) + jj;
-            r.c[jj] = ld_nt(reinterpret_cast<const uint4*>(a.codes) + (int64_t(j) * nsb_total + si) * 64 + lane);
-            r.mw[jj] = reinterpret_cast<const uint32_t*>(a.meta)[(si * 64 + lane) * 8 + j];
+            r.c[jj] = GP::load(a, int64_t(j) * nsb_total + si, si, j, lane);
         }
-        r.dd = reinterpret_cast<const float2*>(a.dd)[si * 64 + lane];
         const int k8 = sb * 32 + (s & 3) * 8;
 #pragma unroll
         for (int i = 0; i < XB; ++i) {
@@ -329,39 +503,14 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
                 const int f = t + 256 * i;
                 *reinterpret_cast<uint4*>(&xs[buf][(f / 8) * LDK + 8 * (f % 8)]) = ring[d].xv[i];
             }
-            const uint4 c0 = ring[d].c[0], c1 = ring[d].c[1];
-            const uint32_t mw0 = ring[d].mw[0], mw1 = ring[d].mw[1];
-            const float2 dd = ring[d].dd;
+            const typename GP::Ch c0 = ring[d].c[0], c1 = ring[d].c[1];
             __builtin_amdgcn_sched_barrier(0);
             load(min(s + D, steps - 1), ring[d]);
             __builtin_amdgcn_sched_barrier(0);
             // B operands: [chunk][tile][k16 step] as fp16 in k order [0,2,4,6,1,3,5,7]
             half8 bf[2][2][2];
-            {
-                const auto d2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(dd.x), __float_as_uint(dd.x), false, false);
-                const auto m2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(dd.y), __float_as_uint(dd.y), false, false);
-#pragma unroll
-                for (int jj = 0; jj < 2; ++jj) {
-                    const uint4 c = jj ? c1 : c0;
-                    const uint32_t w = jj ? mw1 : mw0;
-                    const auto k0 = __builtin_amdgcn_permlane32_swap(c.x, c.y, false, false);  // columns 0-15
-                    const auto k1 = __builtin_amdgcn_permlane32_swap(c.z, c.w, false, false);  // columns 16-31
-                    const auto mt = __builtin_amdgcn_permlane32_swap(w, w, false, false);
-#pragma unroll
-                    for (int T = 0; T < 2; ++T) {
-                        const float d255 = __uint_as_float(d2[T]) * (1.0f / 255.0f);
-                        const float dm127 = __uint_as_float(m2[T]) * (1.0f / 127.0f);
-                        const uint32_t gm = mt[T];
-                        const _Float16 sc0 = _Float16(d255 * float(gm & 0xFFu));
-                        const _Float16 sc1 = _Float16(d255 * float((gm >> 8) & 0xFFu));
-                        const _Float16 mn0 = _Float16(dm127 * float(int8_t(gm >> 16)));
-                        const _Float16 mn1 = _Float16(dm127 * float(int32_t(gm) >> 24));
-                        const half2v s0 = {sc0, sc0}, s1 = {sc1, sc1}, n0 = {mn0, mn0}, n1 = {mn1, mn1};
-                        bf[jj][T][0] = __builtin_bit_cast(half8, dequant8p(k0[T], s0, n0));
-                        bf[jj][T][1] = __builtin_bit_cast(half8, dequant8p(k1[T], s1, n1));
-                    }
-                }
-            }
+            GP::bops(c0, lane, bf[0]);
+            GP::bops(c1, lane, bf[1]);
             __syncthreads();
 #pragma unroll
             for (int jj = 0; jj < 2; ++jj)
@@ -446,7 +595,14 @@ void launch_bm(const GemmArgs& ga, dim3 grid, hipStream_t s) {
 
 }  // namespace
 
-bool gemm_supported(const DevBlob& b) { return b.layout == LAYOUT_RPL && b.fmt == FMT_Q4_K; }
+// Q4_K at every M; Q2_K, Q3_K, Q5_K, Q6_K and Q8_0 from the packed-W
+// kernel's token tiles up.
+bool gemm_supported(const DevBlob& b, int M) {
+    if (b.layout != LAYOUT_RPL) return false;
+    if (b.fmt == FMT_Q4_K) return true;
+    return (b.fmt == FMT_Q2_K || b.fmt == FMT_Q3_K || b.fmt == FMT_Q5_K || b.fmt == FMT_Q6_K || b.fmt == FMT_Q8_0) &&
+           M > 64;
+}
 
 // Token tiles from kPwMin up run k_gemm_q4k_pw (256-row tiles, one block per
 // CU); smaller ones k_gemm_q4k (128-row tiles). At M = 32 both kernels take
@@ -482,7 +638,7 @@ size_t gemm_scratch_floats(const DevBlob& b, int M) {
 
 int launch_gemm(const DevBlob& b, const float* d_x, float* d_y, int M, void* stream, float* d_scratch) {
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if (!gemm_supported(b)) return int(hipErrorInvalidValue);
+    if (!gemm_supported(b, M)) return int(hipErrorInvalidValue);
     int bm = 0, splits = 1, per = 0;
     gemm_plan(b, M, bm, splits, per);
     if (gemm_scratch_floats(b, M) && !d_scratch) return int(hipErrorInvalidValue);
@@ -510,8 +666,15 @@ int launch_gemm(const DevBlob& b, const float* d_x, float* d_y, int M, void* str
     ga.sb_per_split = per;
     if (pw) {
         const dim3 grid(unsigned((b.rows + 255) / 256), unsigned((M + bm - 1) / bm), unsigned(splits));
-        static_assert(kPwMin == 128, "token tiles below 128 would need k_gemm_q4k_pw<bm / 32, 4>");
-        hipLaunchKernelGGL((k_gemm_q4k_pw<4, 4>), grid, dim3(256), 0, s, ga);
+        static_assert(kPwMin == 128, "token tiles below 128 would need k_gemm_q4k_pw<FB, bm / 32, 4>");
+        switch (b.fmt) {
+        case FMT_Q2_K: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmKQ<2>, 4, 4>), grid, dim3(256), 0, s, ga); break;
+        case FMT_Q3_K: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmKQ<3>, 4, 4>), grid, dim3(256), 0, s, ga); break;
+        case FMT_Q5_K: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmKQ<5>, 4, 4>), grid, dim3(256), 0, s, ga); break;
+        case FMT_Q6_K: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmQ6, 4, 4>), grid, dim3(256), 0, s, ga); break;
+        case FMT_Q8_0: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmQ8, 4, 4>), grid, dim3(256), 0, s, ga); break;
+        default: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmKQ<4>, 4, 4>), grid, dim3(256), 0, s, ga); break;
+        }
     } else {
         const dim3 grid(unsigned((b.rows + BN - 1) / BN), unsigned((M + bm - 1) / bm), unsigned(splits));
         if (bm == 32) launch_bm<32, 1>(ga, grid, s);

@@ -743,7 +743,7 @@ int wv_matmul_dev(uint64_t handle, const float* d_x, float* d_y, int32_t m, void
     if (m == 0) return WV_OK;
     hipSetDevice(b.device);
     hipStream_t s = stream_or_default(stream, b.device);
-    if (!gemm_supported(b)) {
+    if (!gemm_supported(b, m)) {
         const int k = launch_matvec(b, d_x, d_y, m, s);
         if (k != hipSuccess) return hip_fail(hipError_t(k), "MatMul: kernel launch");
         return WV_OK;

@@ -200,7 +200,7 @@ int launch_matvec_t(const DevBlob& b, const float* d_gy, float* d_gx, int batch,
 int rpl_fuse_rows(const DevBlob* parts, int n, DevBlob& out, void* stream);
 int rpl_fuse_pairs(const DevBlob& a, const DevBlob& b, DevBlob& out, void* stream);
 // Batched prefill GEMM (gemm_rpl.hip): fp16 MFMA on the row-interleaved Q4_K layout.
-bool gemm_supported(const DevBlob& b);
+bool gemm_supported(const DevBlob& b, int M);
 size_t gemm_scratch_floats(const DevBlob& b, int M);
 int launch_gemm(const DevBlob& b, const float* d_x, float* d_y, int M, void* stream, float* d_scratch);
 // MatVecT on LAYOUT_RPL uses the blob's own scratch (rpl_t_partial).
