@@ -81,17 +81,19 @@ def test_prefill_q4k_wide(shape, m):
     d.free()
 
 
-@pytest.mark.parametrize("fmt", ["Q2_K", "Q3_K", "Q5_K", "Q6_K", "Q8_0"])
+@pytest.mark.parametrize("fmt", ["Q2_K", "Q3_K", "Q5_K", "Q6_K", "Q8_0", "Q4_0", "Q4_1", "Q5_0", "Q5_1",
+                                 "IQ1_S", "IQ2_XXS", "IQ2_XS", "IQ3_XXS", "IQ3_S", "IQ4_XS",
+                                 "TernaryPacked", "BinaryPacked", "AffinePacked"])
 @pytest.mark.parametrize("shape,m", [((256, 1024), 128), ((448, 2048), 300), ((1000, 4096), 130)])
-def test_prefill_other_kquants_mfma(fmt, shape, m):
-    """Token blocks over 64 of Q2_K, Q3_K, Q5_K (Q4_K's metadata with other
-    code planes), Q6_K and Q8_0 take the packed-W MFMA GEMM."""
+def test_prefill_other_formats_mfma(fmt, shape, m):
+    """Token blocks over 64 of every other row-interleaved format take the
+    packed-W MFMA GEMM, each with its own B-operand builder."""
     rows, cols = shape
     print(f"[gpu] prefill {fmt} {cols}->{rows} M={m}", flush=True)
     rng = np.random.default_rng(rows + m)
     w = (rng.standard_normal(rows * cols, dtype=np.float32) * np.float32(0.02)).astype(np.float32)
     p = wv.pack(fmt, w, rows, cols)
-    wd = oracle.unpack(oracle.Packed(p.fmt, rows, cols, p.raw, p.scales, p.meta, p.block_weights))
+    wd = oracle.unpack(oracle.Packed(p.fmt, rows, cols, p.raw, p.scales, p.meta, p.block_weights, p.mins))
     wd = wd.reshape(rows, cols).astype(np.float64)
     d = wv.upload(p)
     assert d.info()["layout"] == "row-interleaved"

@@ -27,11 +27,12 @@
 // Token blocks of more than 64 use k_gemm_q4k_pw instead: W goes from the
 // planes straight into MFMA B operands (a lane swap puts the row-interleaved
 // chunks into the 32x32x16 operand layout) and only X passes through LDS. It
-// also serves Q2_K, Q3_K, Q5_K, Q6_K and Q8_0 (per-format B-operand builders).
+// serves every row-interleaved format (per-format B-operand builders).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
 #include <cstdint>
+#include <type_traits>
 
 #include "wv_internal.h"
 
@@ -264,6 +265,93 @@ struct GemmQ8 {  // Q8_0: w = scale*q, q int8, 32 bytes per chunk (consecutive c
                 bf[T][kk] = __builtin_bit_cast(half8, make_uint4(p[0], p[1], p[2], p[3]));
             }
         }
+    }
+};
+
+// The 32-weight block formats (Q4_0 with its nibble xor 8, Q4_1, Q5_0, Q5_1)
+// and AffinePacked g64 (GSH = 1: chunks 2g, 2g+1 share group g): one scale
+// (and min) per chunk from the lane's 8 (16) metadata words per super-block;
+// w = scale*q + min, or scale*(q - OFF).
+template <int FB, bool MIN, int OFF, uint32_t XR, int GSH = 0>
+struct GemmB32 {
+    static constexpr int NG = 8 >> GSH, NW = MIN ? 2 * NG : NG;
+    struct Ch { typename GemmCodes<FB>::C c; uint32_t sc, mn; };
+    static __device__ __forceinline__ Ch load(const RplArgs& a, int64_t ci, int64_t si, int j, int lane) {
+        Ch r;
+        r.c = GemmCodes<FB>::load(a, ci, lane);
+        r.c.c.x ^= XR;
+        r.c.c.y ^= XR;
+        r.c.c.z ^= XR;
+        r.c.c.w ^= XR;
+        const uint32_t* m = reinterpret_cast<const uint32_t*>(a.meta) + (si * 64 + lane) * NW;
+        r.sc = m[j >> GSH];
+        r.mn = MIN ? m[NG + (j >> GSH)] : 0u;
+        return r;
+    }
+    static __device__ __forceinline__ void bops(const Ch& c, int lane, half8 (&bf)[2][2]) {
+        uint32_t se[2][2], so[2][2];
+        GemmCodes<FB>::spread(c.c, lane, se, so);
+        const auto st = __builtin_amdgcn_permlane32_swap(c.sc, c.sc, false, false);
+        const auto mt = __builtin_amdgcn_permlane32_swap(c.mn, c.mn, false, false);
+#pragma unroll
+        for (int T = 0; T < 2; ++T) {
+            const float scf = __uint_as_float(st[T]);
+            const _Float16 sc = _Float16(scf), mn = _Float16(MIN ? __uint_as_float(mt[T]) : -float(OFF) * scf);
+            const half2v s2 = {sc, sc}, n2 = {mn, mn};
+            bf[T][0] = __builtin_bit_cast(half8, dequant8s(se[T][0], so[T][0], s2, n2));
+            bf[T][1] = __builtin_bit_cast(half8, dequant8s(se[T][1], so[T][1], s2, n2));
+        }
+    }
+};
+
+// Codes of one bit (BinaryPacked g32, IQ1_S): one word per chunk whose byte b
+// holds at bit s the code of column 8(s/2) + 2b + s%2.
+struct GemmCodes1 {
+    struct C { uint32_t c; };
+    static __device__ __forceinline__ C load(const RplArgs& a, int64_t ci, int lane) {
+        return {reinterpret_cast<const uint32_t*>(a.codes)[ci * 64 + lane]};
+    }
+    static __device__ __forceinline__ void spread(const C& c, int lane, uint32_t (&se)[2][2], uint32_t (&so)[2][2]) {
+        const auto hh = __builtin_amdgcn_permlane32_swap(c.c, c.c, false, false);
+        const int up = lane >> 5;
+#pragma unroll
+        for (int T = 0; T < 2; ++T)
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk) {
+                const int sb = 4 * kk + 2 * up;
+                se[T][kk] = (hh[T] >> sb) & 0x01010101u;
+                so[T][kk] = (hh[T] >> (sb + 1)) & 0x01010101u;
+            }
+    }
+};
+
+// The linear-code formats (the linear IQ formats, TernaryPacked, BinaryPacked
+// g32): w = scale*(q - MID2/2), one scale per 32 columns or two (SG16, one
+// per k16 step); one-bit codes read +-scale = (2*scale)*(q - 1/2).
+template <int FB, bool SG16, int MID2>
+struct GemmLin {
+    using Codes = std::conditional_t<FB == 1, GemmCodes1, GemmCodes<FB>>;
+    struct Ch { typename Codes::C c; uint32_t s0, s1; };
+    static __device__ __forceinline__ Ch load(const RplArgs& a, int64_t ci, int64_t si, int j, int lane) {
+        const uint32_t* m = reinterpret_cast<const uint32_t*>(a.meta) + (si * 64 + lane) * (SG16 ? 16 : 8);
+        const uint32_t s0 = m[SG16 ? 2 * j : j];
+        return {Codes::load(a, ci, lane), s0, SG16 ? m[2 * j + 1] : s0};
+    }
+    static __device__ __forceinline__ void bops(const Ch& c, int lane, half8 (&bf)[2][2]) {
+        uint32_t se[2][2], so[2][2];
+        Codes::spread(c.c, lane, se, so);
+        const auto t0 = __builtin_amdgcn_permlane32_swap(c.s0, c.s0, false, false);
+        const auto t1 = __builtin_amdgcn_permlane32_swap(c.s1, c.s1, false, false);
+        constexpr float mul = FB == 1 ? 2.0f : 1.0f, mid = 0.5f * MID2;
+#pragma unroll
+        for (int T = 0; T < 2; ++T)
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk) {
+                const float scf = __uint_as_float(kk ? t1[T] : t0[T]) * mul;
+                const _Float16 sc = _Float16(scf), mn = _Float16(-mid * scf);
+                const half2v s2 = {sc, sc}, n2 = {mn, mn};
+                bf[T][kk] = __builtin_bit_cast(half8, dequant8s(se[T][kk], so[T][kk], s2, n2));
+            }
     }
 };
 
@@ -595,13 +683,11 @@ void launch_bm(const GemmArgs& ga, dim3 grid, hipStream_t s) {
 
 }  // namespace
 
-// Q4_K at every M; Q2_K, Q3_K, Q5_K, Q6_K and Q8_0 from the packed-W
+// Q4_K at every M; every other row-interleaved format from the packed-W
 // kernel's token tiles up.
 bool gemm_supported(const DevBlob& b, int M) {
     if (b.layout != LAYOUT_RPL) return false;
-    if (b.fmt == FMT_Q4_K) return true;
-    return (b.fmt == FMT_Q2_K || b.fmt == FMT_Q3_K || b.fmt == FMT_Q5_K || b.fmt == FMT_Q6_K || b.fmt == FMT_Q8_0) &&
-           M > 64;
+    return b.fmt == FMT_Q4_K || M > 64;
 }
 
 // Token tiles from kPwMin up run k_gemm_q4k_pw (256-row tiles, one block per
@@ -673,7 +759,21 @@ int launch_gemm(const DevBlob& b, const float* d_x, float* d_y, int M, void* str
         case FMT_Q5_K: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmKQ<5>, 4, 4>), grid, dim3(256), 0, s, ga); break;
         case FMT_Q6_K: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmQ6, 4, 4>), grid, dim3(256), 0, s, ga); break;
         case FMT_Q8_0: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmQ8, 4, 4>), grid, dim3(256), 0, s, ga); break;
-        default: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmKQ<4>, 4, 4>), grid, dim3(256), 0, s, ga); break;
+        case FMT_Q4_0: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmB32<4, false, 8, 0x88888888u>, 4, 4>), grid, dim3(256), 0, s, ga); break;
+        case FMT_Q4_1: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmB32<4, true, 0, 0u>, 4, 4>), grid, dim3(256), 0, s, ga); break;
+        case FMT_Q5_0: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmB32<5, false, 16, 0u>, 4, 4>), grid, dim3(256), 0, s, ga); break;
+        case FMT_Q5_1: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmB32<5, true, 0, 0u>, 4, 4>), grid, dim3(256), 0, s, ga); break;
+        case FMT_AFFINE: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmB32<4, true, 0, 0u, 1>, 4, 4>), grid, dim3(256), 0, s, ga); break;
+        case FMT_IQ1_S:
+        case FMT_BINARY: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmLin<1, false, 1>, 4, 4>), grid, dim3(256), 0, s, ga); break;
+        case FMT_IQ2_XXS: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmLin<2, false, 3>, 4, 4>), grid, dim3(256), 0, s, ga); break;
+        case FMT_IQ2_XS: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmLin<2, true, 3>, 4, 4>), grid, dim3(256), 0, s, ga); break;
+        case FMT_IQ3_XXS: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmLin<3, false, 7>, 4, 4>), grid, dim3(256), 0, s, ga); break;
+        case FMT_IQ3_S: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmLin<3, true, 7>, 4, 4>), grid, dim3(256), 0, s, ga); break;
+        case FMT_IQ4_XS: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmLin<4, true, 15>, 4, 4>), grid, dim3(256), 0, s, ga); break;
+        case FMT_TERNARY: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmLin<2, true, 2>, 4, 4>), grid, dim3(256), 0, s, ga); break;
+        case FMT_Q4_K: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmKQ<4>, 4, 4>), grid, dim3(256), 0, s, ga); break;
+        default: return int(hipErrorInvalidValue);
         }
     } else {
         const dim3 grid(unsigned((b.rows + BN - 1) / BN), unsigned((M + bm - 1) / bm), unsigned(splits));
