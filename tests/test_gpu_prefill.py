@@ -84,10 +84,12 @@ def test_prefill_q4k_wide(shape, m):
 @pytest.mark.parametrize("fmt", ["Q2_K", "Q3_K", "Q5_K", "Q6_K", "Q8_0", "Q4_0", "Q4_1", "Q5_0", "Q5_1",
                                  "IQ1_S", "IQ2_XXS", "IQ2_XS", "IQ3_XXS", "IQ3_S", "IQ4_XS",
                                  "TernaryPacked", "BinaryPacked", "AffinePacked"])
-@pytest.mark.parametrize("shape,m", [((256, 1024), 128), ((448, 2048), 300), ((1000, 4096), 130)])
+@pytest.mark.parametrize("shape,m", [((256, 1024), 128), ((448, 2048), 300), ((1000, 4096), 130), ((300, 1024), 9),
+                                     ((520, 2048), 33), ((256, 1024), 64)])
 def test_prefill_other_formats_mfma(fmt, shape, m):
-    """Token blocks over 64 of every other row-interleaved format take the
-    packed-W MFMA GEMM, each with its own B-operand builder."""
+    """Token blocks over 8 of every other row-interleaved format take the
+    packed-W MFMA GEMM (32-, 64- and 128-token tiles), each with its own
+    B-operand builder."""
     rows, cols = shape
     print(f"[gpu] prefill {fmt} {cols}->{rows} M={m}", flush=True)
     rng = np.random.default_rng(rows + m)
@@ -135,10 +137,12 @@ def test_prefill_q4k_baseline(shape, m):
     assert err <= TOL_MFMA
 
 
-@pytest.mark.parametrize("fmt", ["Q8_0", "Q6_K", "Q5_K", "IQ4_NL"])
-def test_prefill_other_formats_use_batched_gemv(fmt):
-    rows, cols, m = 300, 1024, 9
-    print(f"[gpu] prefill {fmt} via batched gemv", flush=True)
+@pytest.mark.parametrize("fmt,m", [("Q8_0", 8), ("Q6_K", 8), ("Q5_K", 3), ("IQ4_NL", 9), ("IQ4_NL", 40)])
+def test_prefill_other_formats_use_batched_gemv(fmt, m):
+    """Up to 8 token rows (and IQ4_NL, on the reference layout, at any M) run
+    the batched GEMVs, with the GEMV bar."""
+    rows, cols = 300, 1024
+    print(f"[gpu] prefill {fmt} M={m} via batched gemv", flush=True)
     rng = np.random.default_rng(5)
     w = (rng.standard_normal(rows * cols) * 0.02).astype(np.float32)
     p = wv.pack(fmt, w, rows, cols)

@@ -683,22 +683,23 @@ void launch_bm(const GemmArgs& ga, dim3 grid, hipStream_t s) {
 
 }  // namespace
 
-// Q4_K at every M; every other row-interleaved format from the packed-W
-// kernel's token tiles up.
+// Q4_K at every M; every other row-interleaved format from 9 token rows up
+// (up to 8 rows, one batched GEMV launch reads the weights once).
 bool gemm_supported(const DevBlob& b, int M) {
     if (b.layout != LAYOUT_RPL) return false;
-    return b.fmt == FMT_Q4_K || M > 64;
+    return b.fmt == FMT_Q4_K || M > 8;
 }
 
 // Token tiles from kPwMin up run k_gemm_q4k_pw (256-row tiles, one block per
 // CU); smaller ones k_gemm_q4k (128-row tiles). At M = 32 both kernels take
 // 20.5 us, and k_gemm_q4k needs no fp16 copy of X.
 constexpr int kPwMin = 128;
+bool use_pw(const DevBlob& b, int bm) { return bm >= kPwMin || b.fmt != FMT_Q4_K; }
 void gemm_plan(const DevBlob& b, int M, int& bm, int& splits, int& sb_per_split) {
     const RplArgs& a = b.rpl;
     bm = M <= 32 ? 32 : M <= 64 ? 64 : 128;
     int want = 1;
-    if (bm >= kPwMin) {
+    if (use_pw(b, bm)) {
         // Split K while whole tiles leave CUs idle, never past one block per CU.
         const int64_t tiles = int64_t((a.rows + 255) / 256) * ((M + bm - 1) / bm);
         want = int(std::max<int64_t>(1, 256 / tiles));
@@ -718,8 +719,35 @@ void gemm_plan(const DevBlob& b, int M, int& bm, int& splits, int& sb_per_split)
 size_t gemm_scratch_floats(const DevBlob& b, int M) {
     int bm = 0, splits = 1, per = 0;
     gemm_plan(b, M, bm, splits, per);
-    const size_t xh = bm == 32 && bm < kPwMin ? 0 : (size_t(M) * size_t(b.cols) / 2 + 63) / 64 * 64;
+    const size_t xh = bm == 32 && !use_pw(b, bm) ? 0 : (size_t(M) * size_t(b.cols) / 2 + 63) / 64 * 64;
     return xh + (splits > 1 ? size_t(splits) * size_t(M) * size_t(b.rows) : 0);
+}
+
+// The packed-W GEMM for b's format with TM 32-token tiles per wave.
+template <int TM>
+int launch_pw(const DevBlob& b, dim3 grid, hipStream_t s, const GemmArgs& ga) {
+    switch (b.fmt) {
+    case FMT_Q2_K: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmKQ<2>, TM, 4>), grid, dim3(256), 0, s, ga); return 0;
+    case FMT_Q3_K: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmKQ<3>, TM, 4>), grid, dim3(256), 0, s, ga); return 0;
+    case FMT_Q5_K: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmKQ<5>, TM, 4>), grid, dim3(256), 0, s, ga); return 0;
+    case FMT_Q6_K: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmQ6, TM, 4>), grid, dim3(256), 0, s, ga); return 0;
+    case FMT_Q8_0: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmQ8, TM, 4>), grid, dim3(256), 0, s, ga); return 0;
+    case FMT_Q4_0: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmB32<4, false, 8, 0x88888888u>, TM, 4>), grid, dim3(256), 0, s, ga); return 0;
+    case FMT_Q4_1: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmB32<4, true, 0, 0u>, TM, 4>), grid, dim3(256), 0, s, ga); return 0;
+    case FMT_Q5_0: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmB32<5, false, 16, 0u>, TM, 4>), grid, dim3(256), 0, s, ga); return 0;
+    case FMT_Q5_1: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmB32<5, true, 0, 0u>, TM, 4>), grid, dim3(256), 0, s, ga); return 0;
+    case FMT_AFFINE: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmB32<4, true, 0, 0u, 1>, TM, 4>), grid, dim3(256), 0, s, ga); return 0;
+    case FMT_IQ1_S:
+    case FMT_BINARY: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmLin<1, false, 1>, TM, 4>), grid, dim3(256), 0, s, ga); return 0;
+    case FMT_IQ2_XXS: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmLin<2, false, 3>, TM, 4>), grid, dim3(256), 0, s, ga); return 0;
+    case FMT_IQ2_XS: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmLin<2, true, 3>, TM, 4>), grid, dim3(256), 0, s, ga); return 0;
+    case FMT_IQ3_XXS: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmLin<3, false, 7>, TM, 4>), grid, dim3(256), 0, s, ga); return 0;
+    case FMT_IQ3_S: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmLin<3, true, 7>, TM, 4>), grid, dim3(256), 0, s, ga); return 0;
+    case FMT_IQ4_XS: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmLin<4, true, 15>, TM, 4>), grid, dim3(256), 0, s, ga); return 0;
+    case FMT_TERNARY: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmLin<2, true, 2>, TM, 4>), grid, dim3(256), 0, s, ga); return 0;
+    case FMT_Q4_K: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmKQ<4>, TM, 4>), grid, dim3(256), 0, s, ga); return 0;
+    default: return int(hipErrorInvalidValue);
+    }
 }
 
 int launch_gemm(const DevBlob& b, const float* d_x, float* d_y, int M, void* stream, float* d_scratch) {
@@ -730,7 +758,7 @@ int launch_gemm(const DevBlob& b, const float* d_x, float* d_y, int M, void* str
     if (gemm_scratch_floats(b, M) && !d_scratch) return int(hipErrorInvalidValue);
     uint4* xh = nullptr;
     float* part = d_scratch;
-    const bool pw = bm >= kPwMin;
+    const bool pw = use_pw(b, bm);
     if (bm != 32 || pw) {
         const int64_t n8 = int64_t(M) * b.cols / 8;
         xh = reinterpret_cast<uint4*>(d_scratch);
@@ -752,29 +780,8 @@ int launch_gemm(const DevBlob& b, const float* d_x, float* d_y, int M, void* str
     ga.sb_per_split = per;
     if (pw) {
         const dim3 grid(unsigned((b.rows + 255) / 256), unsigned((M + bm - 1) / bm), unsigned(splits));
-        static_assert(kPwMin == 128, "token tiles below 128 would need k_gemm_q4k_pw<FB, bm / 32, 4>");
-        switch (b.fmt) {
-        case FMT_Q2_K: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmKQ<2>, 4, 4>), grid, dim3(256), 0, s, ga); break;
-        case FMT_Q3_K: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmKQ<3>, 4, 4>), grid, dim3(256), 0, s, ga); break;
-        case FMT_Q5_K: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmKQ<5>, 4, 4>), grid, dim3(256), 0, s, ga); break;
-        case FMT_Q6_K: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmQ6, 4, 4>), grid, dim3(256), 0, s, ga); break;
-        case FMT_Q8_0: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmQ8, 4, 4>), grid, dim3(256), 0, s, ga); break;
-        case FMT_Q4_0: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmB32<4, false, 8, 0x88888888u>, 4, 4>), grid, dim3(256), 0, s, ga); break;
-        case FMT_Q4_1: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmB32<4, true, 0, 0u>, 4, 4>), grid, dim3(256), 0, s, ga); break;
-        case FMT_Q5_0: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmB32<5, false, 16, 0u>, 4, 4>), grid, dim3(256), 0, s, ga); break;
-        case FMT_Q5_1: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmB32<5, true, 0, 0u>, 4, 4>), grid, dim3(256), 0, s, ga); break;
-        case FMT_AFFINE: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmB32<4, true, 0, 0u, 1>, 4, 4>), grid, dim3(256), 0, s, ga); break;
-        case FMT_IQ1_S:
-        case FMT_BINARY: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmLin<1, false, 1>, 4, 4>), grid, dim3(256), 0, s, ga); break;
-        case FMT_IQ2_XXS: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmLin<2, false, 3>, 4, 4>), grid, dim3(256), 0, s, ga); break;
-        case FMT_IQ2_XS: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmLin<2, true, 3>, 4, 4>), grid, dim3(256), 0, s, ga); break;
-        case FMT_IQ3_XXS: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmLin<3, false, 7>, 4, 4>), grid, dim3(256), 0, s, ga); break;
-        case FMT_IQ3_S: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmLin<3, true, 7>, 4, 4>), grid, dim3(256), 0, s, ga); break;
-        case FMT_IQ4_XS: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmLin<4, true, 15>, 4, 4>), grid, dim3(256), 0, s, ga); break;
-        case FMT_TERNARY: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmLin<2, true, 2>, 4, 4>), grid, dim3(256), 0, s, ga); break;
-        case FMT_Q4_K: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmKQ<4>, 4, 4>), grid, dim3(256), 0, s, ga); break;
-        default: return int(hipErrorInvalidValue);
-        }
+        const int e = bm == 32 ? launch_pw<1>(b, grid, s, ga) : bm == 64 ? launch_pw<2>(b, grid, s, ga) : launch_pw<4>(b, grid, s, ga);
+        if (e) return e;
     } else {
         const dim3 grid(unsigned((b.rows + BN - 1) / BN), unsigned((M + bm - 1) / bm), unsigned(splits));
         if (bm == 32) launch_bm<32, 1>(ga, grid, s);
