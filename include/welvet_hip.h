@@ -143,10 +143,12 @@ int wv_ternary_acc_dev(uint64_t handle, const float *d_x, int32_t *d_acc, float 
 /* Y[M*rows] = X[M*cols] W^T for a block of M token rows (Y overwritten).
  * Replaces forwardSIMDBlockFused (layers/dense/simd_block.go:17-39) and the
  * batch loop of forwardSIMDQ4_0 (layers/dense/simd.go:294-299), which run M
- * independent GEMVs. Row-interleaved Q4_K blobs use fp16 MFMA with f32
+ * independent GEMVs. Row-interleaved blobs use fp16 MFMA with f32
  * accumulation (results within 2e-3 normwise of the f64 reference, not the
- * 1e-5 of wv_matvec); every other blob runs the batched GEMV kernels of
- * wv_matvec_dev. Device pointers, enqueued on `stream`. */
+ * 1e-5 of wv_matvec): Q4_K at every m, the other row-interleaved formats
+ * (wv_blob_info layout "row-interleaved") from m = 9. Every other case runs
+ * the batched GEMV kernels of wv_matvec_dev. Device pointers, enqueued on
+ * `stream`. */
 int wv_matmul_dev(uint64_t handle, const float *d_x, float *d_y, int32_t m, void *stream);
 
 /* Host-pointer form of wv_matmul_dev; synchronous. */
