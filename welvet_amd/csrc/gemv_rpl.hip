@@ -671,9 +671,10 @@ __global__ void __launch_bounds__(1024) k_gemv_rpl(RplArgs a, const float* __res
             const int w = q >> 1, half = q & 1;
 #pragma unroll
             for (int pl = 0; pl < 3; ++pl) {
-                const int sb8 = 8 * pl;
-                const uint32_t blo = (uint32_t(X0 >> sb8) & 255u) | ((uint32_t(X2 >> sb8) & 255u) << 8);
-                const uint32_t bhi = (uint32_t(X1 >> sb8) & 255u) | ((uint32_t(X3 >> sb8) & 255u) << 8);
+                // byte pl of X0 (X1) and of X2 (X3) in one v_perm_b32 each
+                const uint32_t sel = uint32_t(pl) | (uint32_t(4 + pl) << 8) | 0x0C0C0000u;
+                const uint32_t blo = __builtin_amdgcn_perm(uint32_t(X2), uint32_t(X0), sel);
+                const uint32_t bhi = __builtin_amdgcn_perm(uint32_t(X3), uint32_t(X1), sel);
                 h16[(pl * 8 + w) * 2 + half] = uint16_t(blo);
                 h16[(pl * 8 + 4 + w) * 2 + half] = uint16_t(bhi);
             }
