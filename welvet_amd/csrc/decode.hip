@@ -553,22 +553,31 @@ __global__ void __launch_bounds__(256) k_attn_combine(const float* __restrict__ 
     constexpr int ND = HD / 64, PW = 16 * NCL;
     __shared__ float red[4][HD];
     const int h = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int kv_len = min(*d_pos + 1, max_seq);
-    const int nc = min(n_chunks, (kv_len + kChunk - 1) / kChunk);
     const float* ph = part + int64_t(h) * n_chunks * (HD + 2);
+    // The loads are clamped to the allocated chunks, not to the live count,
+    // so they issue together with the position's load instead of after it;
+    // chunks past the live count (stale or never written) are selected away.
     float mc[NCL], lc[NCL];
 #pragma unroll
     for (int j = 0; j < NCL; ++j) {
-        const int cc = lane + 64 * j, cl = min(cc, nc - 1);
-        mc[j] = cc < nc ? ph[cl * (HD + 2) + HD] : -INFINITY;
+        const int cl = min(lane + 64 * j, n_chunks - 1);
+        mc[j] = ph[cl * (HD + 2) + HD];
         lc[j] = ph[cl * (HD + 2) + HD + 1];
     }
     float ov[PW][ND];
 #pragma unroll
     for (int k = 0; k < PW; ++k) {
-        const int cc = min(wave + 4 * k, nc - 1);
+        const int cc = min(wave + 4 * k, n_chunks - 1);
 #pragma unroll
         for (int j = 0; j < ND; ++j) ov[k][j] = ph[cc * (HD + 2) + lane + 64 * j];
+    }
+    const int kv_len = min(*d_pos + 1, max_seq);
+    const int nc = min(n_chunks, (kv_len + kChunk - 1) / kChunk);
+#pragma unroll
+    for (int j = 0; j < NCL; ++j) {
+        const bool live = lane + 64 * j < nc;
+        mc[j] = live ? mc[j] : -INFINITY;
+        lc[j] = live ? lc[j] : 0.f;
     }
     float m = mc[0];
 #pragma unroll
@@ -587,9 +596,11 @@ __global__ void __launch_bounds__(256) k_attn_combine(const float* __restrict__ 
 #pragma unroll
     for (int k = 0; k < PW; ++k) {
         const int cc = wave + 4 * k;  // weight register (4k)/64, lane cc % 64
-        const float wk = cc < nc ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w[(4 * k) / 64]), cc % 64)) : 0.f;
+        if (cc < nc) {  // uniform over the wave
+            const float wk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w[(4 * k) / 64]), cc % 64));
 #pragma unroll
-        for (int j = 0; j < ND; ++j) acc[j] = fmaf(ov[k][j], wk, acc[j]);
+            for (int j = 0; j < ND; ++j) acc[j] = fmaf(ov[k][j], wk, acc[j]);
+        }
     }
 #pragma unroll
     for (int j = 0; j < ND; ++j) red[wave][lane + 64 * j] = acc[j];
