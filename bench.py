@@ -39,6 +39,7 @@ WORKLOADS = {
     "q4k_4096x14336": ("Q4_K", 14336, 4096, "Q4_K dequant-GEMV 4096->14336 b=1"),
     "q4k_4096x4096": ("Q4_K", 4096, 4096, "Q4_K dequant-GEMV 4096->4096 b=1"),
     "q4k_14336x4096": ("Q4_K", 4096, 14336, "Q4_K dequant-GEMV 14336->4096 b=1"),
+    "q4k_4096x6144": ("Q4_K", 6144, 4096, "Q4_K dequant-GEMV 4096->6144 b=1 (a decoder's fused Q|K|V shape)"),
     "q6k_4096x14336": ("Q6_K", 14336, 4096, "Q6_K dequant-GEMV 4096->14336 b=1"),
     "q6k_4096x4096": ("Q6_K", 4096, 4096, "Q6_K dequant-GEMV 4096->4096 b=1"),
     "q6k_14336x4096": ("Q6_K", 4096, 14336, "Q6_K dequant-GEMV 14336->4096 b=1"),
