@@ -607,18 +607,25 @@ __global__ void __launch_bounds__(1024) k_gemv_rpl(RplArgs a, const float* __res
     // The producer's sum-of-squares partials: the first kSsU per lane are
     // loaded together here (clamped, masked to 0) and added after the weight
     // loads are issued, in the same order as one pass i = lane, lane+64, ...
-    constexpr int kSsU = 8;
-    float ssv[kSsU];
+    // S = 4 (wide K, never behind a norm in the decoder) sums them in one
+    // loop here: eight more live registers would spill there.
+    constexpr int kSsU = S >= 4 ? 0 : 8;
+    float ssv[kSsU > 0 ? kSsU : 1];
+    double ssp = 0.0;
     const float* ssb = a.nrm_ss + int64_t(b) * a.nrm_n;
     if (a.nrm_gamma) {
 #pragma unroll
         for (int s = 0; s < S; ++s)
             gv4[s] = reinterpret_cast<const float4*>(a.nrm_gamma + (si[s] - int64_t(rg) * a.nsb) * 256)[lane];
+        if constexpr (kSsU == 0) {
+            for (int i = lane; i < a.nrm_n; i += 64) ssp += ssb[i];
+        } else {
 #pragma unroll
-        for (int k = 0; k < kSsU; ++k) {
-            const int i = lane + 64 * k;
-            const float v = ssb[min(i, a.nrm_n - 1)];
-            ssv[k] = i < a.nrm_n ? v : 0.f;
+            for (int k = 0; k < kSsU; ++k) {
+                const int i = lane + 64 * k;
+                const float v = ssb[min(i, a.nrm_n - 1)];
+                ssv[k] = i < a.nrm_n ? v : 0.f;
+            }
         }
     }
     typename P::Sb sbm[S];
@@ -634,10 +641,11 @@ __global__ void __launch_bounds__(1024) k_gemv_rpl(RplArgs a, const float* __res
     if (a.nrm_gamma) {
         // RMSNorm of x folded in (layers/rmsnorm/cpu.go:70-85): f64 total of
         // the producer's partial sums, y = f32((x * inv) * gamma).
-        double ssp = 0.0;
+        if constexpr (kSsU > 0) {
 #pragma unroll
-        for (int k = 0; k < kSsU; ++k) ssp += ssv[k];
-        for (int i = lane + 64 * kSsU; i < a.nrm_n; i += 64) ssp += ssb[i];
+            for (int k = 0; k < kSsU; ++k) ssp += ssv[k];
+            for (int i = lane + 64 * kSsU; i < a.nrm_n; i += 64) ssp += ssb[i];
+        }
         ssp = wave_total_f64(ssp);
         const double inv = 1.0 / sqrt(ssp / double(a.nsb * 256) + a.nrm_eps);
 #pragma unroll
