@@ -900,9 +900,12 @@ RplPlan rpl_plan(const DevBlob& bl, int max_s = 4) {
     return p;
 }
 
+// Policies with a second metadata word are planned with S <= 2 (rpl_plan's
+// max_s; launch_rpl_t checks it), so their S = 4 kernels are not built.
 template <class P, int L, int S>
 void launch_rpl_ls(const RplArgs& a, const RplPlan& p, dim3 grid, size_t lds, hipStream_t s, const float* x, float* y) {
-    hipLaunchKernelGGL((k_gemv_rpl<P, L, S, 4>), grid, dim3(unsigned(64 * p.W)), lds, s, a, x, y);
+    if constexpr (!(P::kWords2 && S > 2))
+        hipLaunchKernelGGL((k_gemv_rpl<P, L, S, 4>), grid, dim3(unsigned(64 * p.W)), lds, s, a, x, y);
 }
 
 template <class P>
@@ -918,6 +921,7 @@ int launch_rpl_t(const DevBlob& bl, const float* x, float* y, int batch, hipStre
     a.nrm_eps = ex.nrm_eps;
     a.ss_out = ex.ss_out;
     const RplPlan p = rpl_plan(bl, P::kWords2 ? 2 : 4);
+    if (P::kWords2 && p.S > 2) return int(hipErrorInvalidValue);  // not reachable: the plan caps S
     a.ksplit = p.ksplit;
     size_t lds = size_t(p.W) * (p.S * (256 + 16) + 64) * sizeof(float);  // x slices + partial row sums
     lds = std::max(lds, size_t(lds_floor()));
