@@ -89,6 +89,10 @@ COPY_WRITE_SCALE = 65536.0 / 65536.0
 PMC_KIB = {
     "q4k_4096x14336": (18951.5, 56.0),
 }
+# Where each PMC_KIB entry comes from (the profile summary under profiles/).
+PMC_SOURCE = {
+    "q4k_4096x14336": "profiles/k_gemv_rpl_q4k_4096x14336_pmc_traffic.txt",
+}
 METRIC = "dequant-GEMV HBM GB/s (% of peak) at 4096->14336 Q4_K b=1; decode tokens/s"
 
 
@@ -107,40 +111,66 @@ def make_weights(fmt, rows, cols, seed=1234):
     return (rng.standard_normal(rows * cols, dtype=np.float32) * np.float32(0.02)).astype(np.float32), rng
 
 
+def host_info():
+    """nproc, the cores this process may run on, the CPU model, and the threads
+    the CPU baseline uses: every core available to the process, capped by the
+    host's CPU share for one GPU (OMP_NUM_THREADS, set on the GPU boxes)."""
+    nproc = os.cpu_count() or 1
+    avail = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else nproc
+    share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    threads = avail if share <= 0 else max(1, min(avail, share))
+    return dict(nproc=nproc, cores_available=avail, cpu_model=model, threads=threads)
+
+
 def cpu_baseline(packed, x, rows, cols, ternary, nbytes, budget_s, threads):
-    """CPU restatement of welvet's Go/SIMD Dense path (oracle/), timed here."""
+    """CPU restatement of welvet's Go/SIMD Dense path (oracle/), timed here on
+    `threads` row-shard threads and on one thread."""
     import oracle
+    info = host_info()
     op = oracle.Packed(packed.fmt if not ternary else 0, rows, cols, packed.raw, packed.scales, packed.meta,
                        packed.block_weights, packed.mins)
-    if ternary:
+
+    def timed(fn, budget):
         t0 = time.perf_counter()
-        oracle.ternary_i8_forward(packed.raw, np.float32(packed.tensor_scale), rows, cols, x)
+        fn()
         one = time.perf_counter() - t0
-        n = max(1, min(200, int(budget_s / max(one, 1e-6))))
+        n = max(2, min(500, int(budget / max(one, 1e-6))))
         t0 = time.perf_counter()
         for _ in range(n):
-            oracle.ternary_i8_forward(packed.raw, np.float32(packed.tensor_scale), rows, cols, x)
-        dt = (time.perf_counter() - t0) / n
-        return dict(value=round(nbytes / dt / 1e9, 3), unit="GB/s", cores=1, kind="port",
-                    sample=f"{n} full calls of forwardSIMDNarrowI8 restated (serial, re-expands codes per call, "
-                           f"as the reference), {dt * 1e3:.3f} ms/call")
+            fn()
+        return n, (time.perf_counter() - t0) / n
+
+    if ternary:
+        dt = oracle.DTYPES[packed.name]
+        n, sec = timed(lambda: oracle.narrow_i8_forward(dt, packed.raw, np.float32(packed.tensor_scale), rows, cols, x),
+                       budget_s)
+        return dict(value=round(nbytes / sec / 1e9, 3), unit="GB/s", cores=1, kind="port",
+                    one_thread_value=round(nbytes / sec / 1e9, 3), nproc=info["nproc"],
+                    cores_available=info["cores_available"], cpu_model=info["cpu_model"],
+                    sample=f"{n} full calls of forwardSIMDNarrowI8 restated (serial, re-expands codes every call, "
+                           f"as the reference), {sec * 1e3:.3f} ms/call; the reference path has no threads")
     t0 = time.perf_counter()
     simd = oracle.SimdPath(op)
     cache_s = time.perf_counter() - t0
     simd.matvec(x, nthreads=threads)  # warm
-    t0 = time.perf_counter()
-    simd.matvec(x, nthreads=threads)
-    one = time.perf_counter() - t0
-    n = max(2, min(500, int(budget_s / max(one, 1e-6))))
-    t0 = time.perf_counter()
-    for _ in range(n):
-        simd.matvec(x, nthreads=threads)
-    dt = (time.perf_counter() - t0) / n
+    n, sec = timed(lambda: simd.matvec(x, nthreads=threads), budget_s)
+    n1, sec1 = timed(lambda: simd.matvec(x, nthreads=1), budget_s / 3)
     simd.close()
-    return dict(value=round(nbytes / dt / 1e9, 3), unit="GB/s", cores=threads, kind="port",
-                sample=f"{n} full GEMVs of the restated fused SIMD path (Ensure*SIMDCache projection built once in "
-                       f"{cache_s:.2f} s, not timed; f64 Dot*Row kernels, {threads} row-shard threads), "
-                       f"{dt * 1e3:.3f} ms/call")
+    return dict(value=round(nbytes / sec / 1e9, 3), unit="GB/s", cores=threads, kind="port",
+                one_thread_value=round(nbytes / sec1 / 1e9, 3), nproc=info["nproc"],
+                cores_available=info["cores_available"], cpu_model=info["cpu_model"],
+                sample=f"{n} full GEMVs of the restated fused SIMD path on {threads} row-shard threads "
+                       f"({sec * 1e3:.3f} ms/call) and {n1} on one thread ({sec1 * 1e3:.3f} ms/call); "
+                       f"Ensure*SIMDCache projection built once in {cache_s:.2f} s, not timed")
 
 
 def main():
@@ -150,15 +180,19 @@ def main():
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--workload", default="q4k_4096x14336",
                     choices=sorted(WORKLOADS) + sorted(PREFILL) + sorted(MATVECT) + sorted(DECODE))
-    ap.add_argument("--cpu-budget-s", type=float, default=12.0)
+    ap.add_argument("--cpu-budget-s", type=float, default=10.0)
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-decode", action="store_true",
+                    help="leave out the decode_32l tokens/s run the headline workload's line carries")
+    ap.add_argument("--decode-steps", type=int, default=40)
     ap.add_argument("--traffic-kib", type=float, nargs=2, metavar=("FETCH_KIB", "WRITE_KIB"),
                     help="override the per-dispatch FETCH_SIZE and WRITE_SIZE (KiB) of the GEMV kernel "
                          "(rocprofv3 --pmc of this command) used for roofline.traffic")
-    ap.add_argument("--graph", action="store_true",
-                    help="replay the timed launches from a captured HIP graph (for kernels shorter than the "
-                         "host's per-launch cost, where stream launches would time the host)")
+    ap.add_argument("--launch", choices=("stream", "graph"), default="stream",
+                    help="timed region: K stream launches from the host behind a queue primed with the warmup "
+                         "launches (default), or one HIP graph holding the K launches (measured slower per "
+                         "launch on MI355X: 12.5 against 9.0 us at the headline shape)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="also run plain device-to-device copies of MIB MiB (torch copy_) for counter calibration")
     args = ap.parse_args()
@@ -176,9 +210,10 @@ def main():
     if args.workload in MATVECT:
         return matvect_main(args, torch, wv)
     if args.workload in DECODE:
-        return decode_main(args, wv)
+        print(json.dumps(decode_run(args, wv, args.workload, args.steps, args.warmup, not args.no_cpu)), flush=True)
+        return
     fmt, rows, cols, desc = WORKLOADS[args.workload]
-    ternary = fmt == "NativeTernary"
+    ternary = fmt in wv.NATIVE
     print(f"[bench] {desc}: packing", file=sys.stderr, flush=True)
     w, rng = make_weights(fmt, rows, cols)
     packed = wv.pack(fmt, w, rows, cols)
@@ -197,9 +232,8 @@ def main():
     ty = torch.empty(rows, device="cuda")
     torch.cuda.synchronize()
 
-    # correctness gate on the benchmarked blob (full f64 reference is in tests/)
-    with torch.cuda.stream(stream):
-        blobs[0].matvec_dev(tx.data_ptr(), ty.data_ptr(), 1, sh)
+    # correctness gate on the benchmarked blob (full parity is in tests/)
+    blobs[0].matvec_dev(tx.data_ptr(), ty.data_ptr(), 1, sh)
     stream.synchronize()
     assert torch.isfinite(ty).all().item(), "non-finite output"
 
@@ -215,47 +249,51 @@ def main():
             rc |= launch(handles[(first + i) % copies], xp, yp, 1, sh)
         wv.check(rc)
 
-    with torch.cuda.stream(stream):
-        run(args.warmup)
-    stream.synchronize()
-
-    graph = None
-    if args.graph:
-        # one graph of `copies` launches (one per weight copy), replayed
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph, stream=stream):
-            run(copies)
+    def timed_stream():
+        # The warmup launches are enqueued and e0 is recorded behind them with
+        # no synchronisation, so the GPU is busy when the timed region starts
+        # and the host stays ahead of it (a launch costs less host time than
+        # the kernel takes).
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         stream.synchronize()
-        for _ in range(2):
-            graph.replay()
-        stream.synchronize()
-        reps = max(1, args.steps // copies)
-        args.steps = reps * copies
+        with torch.cuda.stream(stream):
+            run(args.warmup)
+            e0.record(stream)
+            run(args.steps, args.warmup)
+            e1.record(stream)
+        e1.synchronize()
+        return e0.elapsed_time(e1) / args.steps
 
-    # timed region: K back-to-back launches, events on the kernels' stream
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    def timed_graph():
+        # One graph holds exactly the K timed launches (weight copies in
+        # rotation); it is replayed once untimed (upload), then the warmup runs
+        # as stream launches and the timed replay follows on the primed queue.
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            run(args.steps, args.warmup)
+        g.replay()
+        stream.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(stream):
+            run(args.warmup)
+            e0.record(stream)
+            g.replay()
+            e1.record(stream)
+        e1.synchronize()
+        return e0.elapsed_time(e1) / args.steps
+
+    ms_stream = timed_stream()
+    ms_graph = timed_graph() if args.launch == "graph" else None
+    ms_per_step = ms_graph if ms_graph is not None else ms_stream
     torch.cuda.synchronize()
-    e0.record(stream)
-    with torch.cuda.stream(stream):
-        if graph is not None:
-            for _ in range(args.steps // copies):
-                graph.replay()
-        else:
-            run(args.steps)
-    e1.record(stream)
-    e1.synchronize()
-    torch.cuda.synchronize()
-    ms_total = e0.elapsed_time(e1)
-    ms_per_step = ms_total / args.steps
     value = nbytes / (ms_per_step * 1e-3) / 1e9
 
-    # The timed region is K back-to-back launches on one stream with no host
-    # work in between; at this size the launches are GPU-bound (a kernel
-    # trace shows no gap between consecutive dispatches), so the region's
-    # average is the kernel's average duration. profiles/ holds the
-    # rocprofv3 --kernel-trace --stats summary of this same command.
-    kern_us = ms_per_step * 1e3
-    achieved = nbytes / (kern_us * 1e-6) / 1e9
+    # The timed region is K back-to-back launches of one kernel on one
+    # stream; the events bracket them on that stream, so the region's average
+    # is the kernel's average duration plus the dispatcher's gap between
+    # consecutive launches. profiles/ holds the rocprofv3 --kernel-trace
+    # --stats summary of this same command.
+    event_us = ms_per_step * 1e3
     traffic = None
     pmc = tuple(args.traffic_kib) if args.traffic_kib else PMC_KIB.get(args.workload)
     if pmc:
@@ -277,18 +315,21 @@ def main():
         "config": {
             "workload": desc, "format": fmt, "in": cols, "out": rows, "batch": 1,
             "weight_copies_rotated": copies, "packed_bytes": int(packed.nbytes),
-            "launch": "HIP graph replay" if args.graph else "stream launches",
+            "launch": "one HIP graph of the K launches" if ms_graph is not None else "K stream launches",
             "device_bytes": int(dev_bytes), "algorithmic_bytes_per_step": int(nbytes),
         },
         "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
         "roofline": {
-            "bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-            "kernel_us": round(kern_us, 3),
+            "bound": "hbm", "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(value / HBM_PEAK_GBS, 4), "traffic": traffic,
+            "event_us_per_launch": round(event_us, 3),
+            "event_us_per_launch_graph": None if ms_graph is None else round(ms_graph * 1e3, 3),
+            "traffic_source": PMC_SOURCE.get(args.workload) if pmc and not args.traffic_kib else None,
         },
     }
     if not args.no_cpu:
-        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        info = host_info()
+        threads = args.cpu_threads or info["threads"]
         print(f"[bench] cpu baseline ({threads} threads, ~{args.cpu_budget_s:.0f} s)", file=sys.stderr, flush=True)
         result["cpu_baseline"] = cpu_baseline(packed, x, rows, cols, ternary, nbytes, args.cpu_budget_s, threads)
     if args.copy_probe:
@@ -300,6 +341,16 @@ def main():
         result["copy_probe_bytes"] = args.copy_probe << 20
     for b in blobs:
         b.free()
+    del blobs
+    if args.workload == "q4k_4096x14336" and not args.no_decode:
+        # The metric's second half: decode tokens/s of BASELINE config 5.
+        d = decode_run(args, wv, "decode_32l", args.decode_steps, 4, with_cpu=not args.no_cpu)
+        result["decode_tokens_per_s"] = d["value"]
+        result["decode_ms_per_token"] = d["ms_per_step"]
+        result["decode_roofline"] = d["roofline"]
+        result["decode_config"] = d["config"]["workload"]
+        if "cpu_baseline" in d:
+            result["decode_cpu_baseline"] = d["cpu_baseline"]
     print(json.dumps(result), flush=True)
 
 
@@ -458,10 +509,10 @@ def matvect_main(args, torch, wv):
     print(json.dumps(result), flush=True)
 
 
-def decode_main(args, wv):
+def decode_run(args, wv, workload, steps, warmup, with_cpu):
     """One step = one greedy decode token of the whole 32-layer model at KV length 2048."""
     from welvet_amd.decode import Config, Decoder
-    spec = DECODE[args.workload]
+    spec = DECODE[workload]
     kv = spec["kv"]
     cfg = Config(n_layers=spec["n_layers"], hidden=spec["hidden"], n_heads=spec["n_heads"],
                  n_kv_heads=spec["n_kv_heads"], head_dim=spec["head_dim"], ffn=spec["ffn"], vocab=spec["vocab"],
@@ -499,8 +550,8 @@ def decode_main(args, wv):
     print(f"[bench] model resident ({time.perf_counter() - t0:.1f} s)", file=sys.stderr, flush=True)
     dec.use_graph(True)
     pos, tok = kv - 1, 1
-    steps = max(8, min(args.steps, 200))
-    warmup = max(2, min(args.warmup, 10))
+    steps = max(8, min(steps, 200))
+    warmup = max(2, min(warmup, 10))
     dec.generate(tok, pos, warmup, advance_pos=False)
     t1 = time.perf_counter()
     toks = dec.generate(tok, pos, steps, advance_pos=False)
@@ -524,9 +575,9 @@ def decode_main(args, wv):
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
     }
-    if not args.no_cpu:
+    if with_cpu:
         import oracle
-        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        threads = args.cpu_threads or host_info()["threads"]
         per_layer = 0.0
         for p in packed_sets[0]:
             op = oracle.Packed(p.fmt, p.rows, p.cols, p.raw, p.scales, p.meta, p.block_weights)
@@ -555,15 +606,17 @@ def decode_main(args, wv):
         lm_t = time.perf_counter() - t2
         simd.close()
         tok_s = cfg.n_layers * per_layer + lm_t
+        info = host_info()
         result["cpu_baseline"] = {
             "value": round(1.0 / tok_s, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "nproc": info["nproc"], "cpu_model": info["cpu_model"],
             "sample": f"one layer's 7 projections (restated fused SIMD path, {threads} row-shard threads) and its "
                       f"f64 attention over {kv} positions, x{cfg.n_layers} layers, plus the LM head: "
                       f"{tok_s * 1e3:.1f} ms per token"}
     dec.free()
     for b in blobs + [lm]:
         b.free()
-    print(json.dumps(result), flush=True)
+    return result
 
 
 if __name__ == "__main__":

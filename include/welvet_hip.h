@@ -19,7 +19,11 @@
  *     enqueue work and return without synchronising. Host-pointer entry
  *     points copy in, compute and copy out synchronously.
  *   - All entry points are thread-safe (handle table under a mutex,
- *     thread-local error text).
+ *     thread-local error text). A blob holds weights only: the scratch a call
+ *     needs (K-split or slice partials) is allocated per call on the call's
+ *     stream, so concurrent calls on one blob, from several threads or on
+ *     several streams, do not share memory. Blob and decoder handles must
+ *     not be freed while another thread still calls with them.
  */
 #ifndef WELVET_HIP_H
 #define WELVET_HIP_H
@@ -50,9 +54,26 @@ enum wv_format {
     WV_FMT_IQ3_S = 15, WV_FMT_IQ4_NL = 16, WV_FMT_IQ4_XS = 17,
     WV_FMT_TERNARY_PACKED = 18, WV_FMT_BINARY_PACKED = 19, WV_FMT_AFFINE_PACKED = 20
 };
-/* FormatNone stores: weights.Store{DType, Native, Scale} (weights/store.go:14-32). */
+/* WV_FMT_NONE blobs hold f32 weights (rows*cols*4 bytes of Raw, quant/none.go:3-21;
+ * also a weights.Store FormatNone + DTypeFloat32 master, weights/store.go:19-22).
+ * FormatNone stores of a narrow DType: weights.Store{DType, Native, Scale}
+ * (weights/store.go:14-32) uploaded as raw = Native, tensor_scale = Scale. */
 #define WV_NATIVE_BASE 1000
+#define WV_NATIVE_INT8 (WV_NATIVE_BASE + 9)     /* core.DTypeInt8 */
+#define WV_NATIVE_INT4 (WV_NATIVE_BASE + 14)    /* core.DTypeInt4 */
+#define WV_NATIVE_INT2 (WV_NATIVE_BASE + 17)    /* core.DTypeInt2 */
 #define WV_NATIVE_TERNARY (WV_NATIVE_BASE + 19) /* core.DTypeTernary */
+#define WV_NATIVE_BINARY (WV_NATIVE_BASE + 20)  /* core.DTypeBinary */
+
+/* core.ActivationType values (core/layer.go:88-99). */
+#define WV_ACT_LINEAR (-1)
+#define WV_ACT_RELU 0
+#define WV_ACT_SILU 1
+#define WV_ACT_GELU 2
+#define WV_ACT_TANH 3
+#define WV_ACT_SIGMOID 4
+#define WV_ACT_LEAKY_RELU 5
+#define WV_ACT_RELU2 6
 
 /* ---- library ---- */
 
@@ -80,17 +101,21 @@ int wv_pack_sizes(int format, int64_t rows, int64_t cols, size_t *raw_len,
 int wv_pack(int format, const float *weights, int64_t rows, int64_t cols,
             uint8_t *raw, float *scales, float *mins, uint8_t *meta);
 
-/* weights.Store packing for FormatNone DTypeTernary (weights/native.go:249-267):
- * codes[(n+3)/4] (4 codes per byte, LSB-first) and the absMax scale. */
-int wv_pack_native_ternary(const float *weights, int64_t n, uint8_t *codes, float *scale);
+/* weights.Store packing of a narrow DType (SetDType -> packNative,
+ * weights/native.go:88-97 Int8, 180-194 packInt4, 218-230 packInt2,
+ * 249-269 packTernary, 271-283 packBinary): format is WV_NATIVE_INT8 / INT4 /
+ * INT2 / TERNARY / BINARY; codes receive (n*bits+7)/8 bytes (LSB-first) and
+ * *scale the Store.Scale. */
+int wv_pack_native(int format, const float *weights, int64_t n, uint8_t *codes, float *scale);
 
 /* ---- resident blobs ---- */
 
 /* Uploads a packed quant.Blob (quant/format.go:110-131) into HBM once.
  * Replaces the per-call CreateBufferInit uploads of the WebGPU path
  * (webgpu/dense.go:570-617) and the lazily built host SIMD caches
- * (quant.EnsureFusedSIMDCache, quant/qx_simd.go:150). For WV_NATIVE_TERNARY,
- * raw = Store.Native codes and tensor_scale = Store.Scale. */
+ * (quant.EnsureFusedSIMDCache, quant/qx_simd.go:150). For the WV_NATIVE_*
+ * DTypes raw = Store.Native codes and tensor_scale = Store.Scale; for
+ * WV_FMT_NONE raw = the f32 weights. */
 int wv_blob_upload(int format, int64_t rows, int64_t cols, int32_t block_weights,
                    const uint8_t *raw, size_t raw_len,
                    const float *scales, size_t n_scales,
@@ -122,21 +147,54 @@ int wv_blob_info(uint64_t handle, int *format, int64_t *rows, int64_t *cols,
 /* ---- forward: quant.MatVec / dense.MatVecPackedBlob / dense.Forward ---- */
 
 /* y[batch*rows] = W x[batch*cols] for each of `batch` rows (y overwritten).
- * Host pointers; synchronous. Replaces quant.MatVec (quant/matvec.go:5),
- * dense.MatVecPackedBlob (layers/dense/simd.go:571) and the packed branch of
- * dense.ForwardSIMD (layers/dense/simd.go:42-45) for linear, bias-free layers.
- * For WV_NATIVE_TERNARY it is forwardSIMDNarrowI8 (layers/dense/simd.go:130-147):
- * activations absmax-quantized to int8, exact int32 accumulators,
- * y = f32(acc) * actScale * scale. */
+ * Host pointers; synchronous. The batched form behind Dense's forward
+ * (layers/dense/simd.go:23-77 packed branch, forwardSIMDBlockFused
+ * simd_block.go:17-39) and dense.MatVecPackedBlob (simd.go:571-614); the
+ * single-vector quant.MatVec contract is wv_quant_matvec. On the WV_NATIVE_*
+ * DTypes it is Dense's int8 path (forwardSIMDNarrowI8 / forwardSIMDInt8,
+ * simd.go:130-195, 303-326): activations absmax-quantized to int8
+ * (quantizeActsI8, simd.go:526-549), exact int32 accumulators,
+ * y = f32(acc) * actScale * scale. On WV_FMT_NONE it is forwardSIMDMasterF32
+ * (simd.go:201-214): f32 weights, f64 sums. */
 int wv_matvec(uint64_t handle, const float *x, float *y, int32_t batch);
 
 /* Device-pointer form of wv_matvec, enqueued on `stream`. */
 int wv_matvec_dev(uint64_t handle, const float *d_x, float *d_y, int32_t batch, void *stream);
 
-/* WV_NATIVE_TERNARY only: the exact int32 accumulators (batch*rows) and the
+/* quant.MatVec (quant/matvec.go:5-35) for one vector, with its argument check
+ * checkBlobYX (quant/helpers.go:94-103): len_x >= cols and len_y >= rows, else
+ * WV_E_SHAPE "MatVec: size mismatch rows=R cols=C len(x)=X len(y)=Y"; x past
+ * cols is not read and y past rows is not written. Host pointers; synchronous.
+ * WV_NATIVE_* blobs are not quant blobs (WV_E_FORMAT). */
+int wv_quant_matvec(uint64_t handle, const float *x, size_t len_x, float *y, size_t len_y);
+
+/* dense.Forward for a linear map with bias and activation (layers/dense/
+ * dense.go:100-112 -> ForwardSIMD simd.go:23-77, applyBiasAct dense.go:145-167):
+ * pre[batch*rows] = W x (+ bias), post = act(pre). bias: f64[rows] or NULL
+ * (weights.Store.Bias); act: a WV_ACT_* value. With a bias, pre holds
+ * f32(f64(Wx) + bias); post = f32(act(f64(pre))). post may be NULL only when
+ * act is WV_ACT_LINEAR and bias is NULL (linearNoBias: post is pre). Every
+ * blob kind, including the WV_NATIVE_* DTypes and WV_FMT_NONE. */
+int wv_dense_forward(uint64_t handle, const float *x, float *pre, float *post, int32_t batch,
+                     const double *bias, int32_t act);
+
+/* Device-pointer form of wv_dense_forward (d_bias a device pointer), enqueued on `stream`. */
+int wv_dense_forward_dev(uint64_t handle, const float *d_x, float *d_pre, float *d_post, int32_t batch,
+                         const double *d_bias, int32_t act, void *stream);
+
+/* WV_NATIVE_* DTypes only: the exact int32 accumulators (batch*rows) and the
  * per-batch-row activation scales (batch) of the int8 path, device pointers. */
-int wv_ternary_acc_dev(uint64_t handle, const float *d_x, int32_t *d_acc, float *d_act_scale,
-                       int32_t batch, void *stream);
+int wv_native_acc_dev(uint64_t handle, const float *d_x, int32_t *d_acc, float *d_act_scale,
+                      int32_t batch, void *stream);
+
+/* weights.Store.MatVec with f64 activations (weights/store.go:133-145,
+ * 162-180): packed blobs run quant.MatVec on f32(x) and widen y (its check and
+ * wording); WV_FMT_NONE and WV_NATIVE_* stores run matVecNativeF64
+ * (weights/native.go:1120-1137): y = sum_c f64(w_rc) * x_c in f64 over the
+ * decoded weights (weightAt, weights/decode.go:50-215), WV_E_SHAPE
+ * "weights: matvecF64 shape" if len_x < cols or len_y < rows. y entries past
+ * rows are set to 0, as MatVec's zeroed result buffer. Host pointers. */
+int wv_store_matvec(uint64_t handle, const double *x, size_t len_x, double *y, size_t len_y);
 
 /* ---- batched prefill: M token rows through the same Dense layer ---- */
 
@@ -157,12 +215,26 @@ int wv_matmul(uint64_t handle, const float *x, float *y, int32_t m);
 /* ---- backward: quant.MatVecT ---- */
 
 /* gx[batch*cols] += W^T gy[batch*rows] (gx NOT zeroed, quant/matvec_t.go:3-5).
- * Host pointers; synchronous. Replaces quant.MatVecT (quant/matvec_t.go:5)
- * as called from backwardSIMDPacked (layers/dense/simd_quant.go:103-126). */
+ * Host pointers; synchronous. The batched form of quant.MatVecT
+ * (quant/matvec_t.go:5) as backwardSIMDPacked calls it (layers/dense/
+ * simd_quant.go:103-126); on WV_NATIVE_* and WV_FMT_NONE blobs the input
+ * gradient of BackwardSIMD (simd.go:412-504): f64 sums of gy * w added to gx. */
 int wv_matvec_t(uint64_t handle, const float *gy, float *gx, int32_t batch);
 
 /* Device-pointer form of wv_matvec_t. */
 int wv_matvec_t_dev(uint64_t handle, const float *d_gy, float *d_gx, int32_t batch, void *stream);
+
+/* quant.MatVecT (quant/matvec_t.go:5-35) for one vector, with checkBlobGYGX
+ * (quant/helpers.go:105-114): len_gy >= rows and len_gx >= cols, else WV_E_SHAPE
+ * "MatVecT: size mismatch rows=R cols=C len(gy)=G len(gx)=X"; gx[:cols] += W^T gy[:rows]. */
+int wv_quant_matvec_t(uint64_t handle, const float *gy, size_t len_gy, float *gx, size_t len_gx);
+
+/* weights.Store.MatVecT with f64 activations (weights/store.go:147-160,
+ * 182-206): packed blobs run quant.MatVecT on f32 copies of gy and gx (every
+ * gx entry comes back through f32); WV_FMT_NONE and WV_NATIVE_* stores run
+ * matVecTNativeF64 (weights/native.go:1139-1158): gx[c] += sum_r w_rc * gy_r
+ * in f64, rows with gy_r == 0 skipped; WV_E_SHAPE "weights: matvecTF64 shape". */
+int wv_store_matvec_t(uint64_t handle, const double *gy, size_t len_gy, double *gx, size_t len_gx);
 
 /* ---- device decode step (greedy), for a decoder whose projections are resident blobs ---- */
 

@@ -49,6 +49,10 @@ def lib():
         L.or_simd_matvec.argtypes = [_P, _P, _P, ctypes.c_int, ctypes.c_int]
         L.or_pack_native_ternary.argtypes = [_P, _I64, _P, _P]
         L.or_pack_native_ternary.restype = None
+        L.or_pack_native.argtypes = [ctypes.c_int, _P, _I64, _P, _P]
+        L.or_expand_narrow_i8.argtypes = [ctypes.c_int, _P, _I64, _P]
+        L.or_narrow_i8_forward.argtypes = [ctypes.c_int, _P, ctypes.c_float, _I64, _I64, _P, _P, _P, _P, ctypes.c_int]
+        L.or_native_decode.argtypes = [ctypes.c_int, _P, ctypes.c_float, _I64, _P]
         L.or_quantize_acts_i8.argtypes = [_P, _I64, _P]
         L.or_quantize_acts_i8.restype = ctypes.c_float
         L.or_ternary_i8_forward.argtypes = [_P, ctypes.c_float, _I64, _I64, _P, _P, _P, _P, ctypes.c_int]
@@ -196,6 +200,56 @@ def ternary_i8_forward(codes, scale, rows, cols, x):
     lib().or_ternary_i8_forward(codes.ctypes.data, ctypes.c_float(scale), rows, cols, x.ctypes.data,
                                 y.ctypes.data, acc.ctypes.data, asc.ctypes.data, batch)
     return y, acc, asc
+
+
+# core.DType values of the narrow weights.Store DTypes (core/dtype.go:23-34).
+DTYPES = {"NativeInt8": 9, "NativeInt4": 14, "NativeInt2": 17, "NativeTernary": 19, "NativeBinary": 20}
+
+
+def _dt(dt) -> int:
+    return DTYPES[dt] if isinstance(dt, str) else int(dt)
+
+
+def pack_native(dt, w: np.ndarray):
+    """weights.Store packNative of a narrow DType -> (codes, scale)."""
+    w = np.ascontiguousarray(w, np.float32).reshape(-1)
+    bits = {9: 8, 14: 4, 17: 2, 19: 2, 20: 1}[_dt(dt)]
+    codes = np.zeros((w.size * bits + 7) // 8, np.uint8)
+    scale = np.zeros(1, np.float32)
+    if lib().or_pack_native(_dt(dt), w.ctypes.data, w.size, codes.ctypes.data, scale.ctypes.data) != bits:
+        raise ValueError(f"oracle: no native pack for {dt}")
+    return codes, np.float32(scale[0])
+
+
+def expand_narrow_i8(dt, codes, n: int) -> np.ndarray:
+    codes = np.ascontiguousarray(codes, np.uint8)
+    out = np.zeros(n, np.int8)
+    if lib().or_expand_narrow_i8(_dt(dt), codes.ctypes.data, n, out.ctypes.data):
+        raise ValueError(f"oracle: no int8 expansion for {dt}")
+    return out
+
+
+def narrow_i8_forward(dt, codes, scale, rows, cols, x):
+    """Dense's int8 path for a narrow DType -> (y, acc, act_scale)."""
+    x = np.ascontiguousarray(x, np.float32).reshape(-1)
+    batch = x.size // cols
+    y = np.zeros(batch * rows, np.float32)
+    acc = np.zeros(batch * rows, np.int32)
+    asc = np.zeros(batch, np.float32)
+    codes = np.ascontiguousarray(codes, np.uint8)
+    if lib().or_narrow_i8_forward(_dt(dt), codes.ctypes.data, ctypes.c_float(scale), rows, cols, x.ctypes.data,
+                                  y.ctypes.data, acc.ctypes.data, asc.ctypes.data, batch):
+        raise ValueError(f"oracle: no int8 path for {dt}")
+    return y, acc, asc
+
+
+def native_decode(dt, codes, scale, n: int) -> np.ndarray:
+    """weightAt: the f32 weights a narrow-DType weights.Store decodes to."""
+    codes = np.ascontiguousarray(codes, np.uint8)
+    out = np.zeros(n, np.float32)
+    if lib().or_native_decode(_dt(dt), codes.ctypes.data, ctypes.c_float(scale), n, out.ctypes.data):
+        raise ValueError(f"oracle: no decode for {dt}")
+    return out
 
 
 def num_cpus() -> int:

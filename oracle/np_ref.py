@@ -373,3 +373,91 @@ def quantize_acts_i8(x: np.ndarray):
         scale = F32(1)
     q = np.clip(round_half_away((x / scale).astype(F32).astype(np.float64)), -128, 127).astype(np.int8)
     return q, scale
+
+
+# ---- narrow weights.Store DTypes (core.DType: 9 Int8, 14 Int4, 17 Int2, 19 Ternary, 20 Binary) ----
+
+NATIVE_BITS = {9: 8, 14: 4, 17: 2, 19: 2, 20: 1}
+
+
+def _pack_bits(codes: np.ndarray, bits: int) -> np.ndarray:
+    """LSB-first packing of `bits`-bit codes, element i at bit i*bits."""
+    per = 8 // bits
+    padn = -(-codes.size // per) * per
+    c = np.zeros(padn, np.uint16)
+    c[: codes.size] = codes
+    c = c.reshape(-1, per)
+    out = np.zeros(c.shape[0], np.uint16)
+    for k in range(per):
+        out |= c[:, k] << (bits * k)
+    return out.astype(np.uint8)
+
+
+def pack_native(dt: int, w: np.ndarray):
+    """packNative for the narrow DTypes (weights/native.go:88-97, 180-283)."""
+    w = np.asarray(w, F32).reshape(-1)
+    amax = F32(np.abs(w).max()) if w.size else F32(0)
+    scale = {9: F32(amax / F32(127)), 14: F32(amax / F32(7))}.get(dt, amax)
+    if scale == 0:
+        scale = F32(1)
+    r = (w / scale).astype(F32)
+    q = round_half_away(r.astype(np.float64))
+    if dt == 9:
+        codes = np.clip(q, -128, 127).astype(np.int64) & 0xFF
+    elif dt == 14:
+        codes = np.clip(q, -8, 7).astype(np.int64) & 0xF
+    elif dt == 17:
+        codes = (np.clip(q, -2, 1).astype(np.int64) + 2) & 3
+    elif dt == 19:
+        codes = np.where(r > F32(0.5), 2, np.where(r < F32(-0.5), 0, 1))
+    else:
+        codes = (w >= 0).astype(np.int64)
+    return _pack_bits(codes.astype(np.uint16), NATIVE_BITS[dt]), scale
+
+
+def unpack_codes(dt: int, codes: np.ndarray, n: int) -> np.ndarray:
+    """The unsigned codes of elements 0..n-1 (LSB-first)."""
+    bits = NATIVE_BITS[dt]
+    b = np.asarray(codes, np.uint8)
+    idx = np.arange(n, dtype=np.int64) * bits
+    return ((b[idx >> 3].astype(np.uint16) >> (idx & 7)) & ((1 << bits) - 1)).astype(np.int64)
+
+
+def expand_narrow_i8(dt: int, codes: np.ndarray, n: int) -> np.ndarray:
+    """expandNarrowToI8 (layers/dense/simd.go:149-195); Int8 bytes as signed."""
+    u = unpack_codes(dt, codes, n)
+    if dt == 9:
+        return u.astype(np.uint8).view(np.int8).astype(np.int8)
+    if dt == 14:
+        return np.where(u > 7, u - 16, u).astype(np.int8)
+    if dt == 17:
+        return (u - 2).astype(np.int8)
+    if dt == 19:
+        return (u - 1).astype(np.int8)
+    return (2 * u - 1).astype(np.int8)
+
+
+def native_decode(dt: int, codes: np.ndarray, scale, n: int) -> np.ndarray:
+    """weightAt (weights/decode.go:50-215): f32(q) * scale; Ternary 0/2 -> -s/+s, 1/3 -> 0."""
+    scale = F32(scale) if F32(scale) != 0 else F32(1)
+    u = unpack_codes(dt, codes, n)
+    if dt == 19:
+        return np.where(u == 0, -scale, np.where(u == 2, scale, F32(0))).astype(F32)
+    if dt == 20:
+        return np.where(u == 1, scale, -scale).astype(F32)
+    return (expand_narrow_i8(dt, codes, n).astype(F32) * scale).astype(F32)
+
+
+def narrow_i8_forward(dt: int, codes: np.ndarray, scale, rows: int, cols: int, x: np.ndarray):
+    """Dense's int8 path (simd.go:130-147, 303-326) with exact int64 sums."""
+    scale = F32(scale) if F32(scale) != 0 else F32(1)
+    wi8 = expand_narrow_i8(dt, codes, rows * cols).reshape(rows, cols).astype(np.int64)
+    x = np.asarray(x, F32).reshape(-1, cols)
+    ys, accs, acts = [], [], []
+    for xb in x:
+        q, a = quantize_acts_i8(xb)
+        acc = wi8 @ q.astype(np.int64)
+        ys.append(((acc.astype(np.int32).astype(F32) * a).astype(F32) * scale).astype(F32))
+        accs.append(acc.astype(np.int32))
+        acts.append(a)
+    return np.concatenate(ys), np.concatenate(accs), np.array(acts, F32)

@@ -1270,4 +1270,121 @@ int or_ternary_i8_forward(const uint8_t *codes, float scale, int64_t rows, int64
     return 0;
 }
 
+/* ------------------------------------------------------------------ */
+/* Narrow weights.Store DTypes: Int8 (9), Int4 (14), Int2 (17),         */
+/* Ternary (19), Binary (20) — core.DType values (core/dtype.go:23-34). */
+/* ------------------------------------------------------------------ */
+
+static int narrow_bits_of(int dt) {
+    switch (dt) {
+    case 9: return 8;
+    case 14: return 4;
+    case 17: case 19: return 2;
+    case 20: return 1;
+    default: return 0;
+    }
+}
+
+/* clampI(math.Round(float64(f32)), lo, hi) (weights/native.go:1184-1192). */
+static int round_clamp(float v, double lo, double hi) {
+    double r = round((double)v);
+    if (r < lo) r = lo;
+    if (r > hi) r = hi;
+    return (int)r;
+}
+
+/* packNative for the narrow DTypes: Int8 (weights/native.go:88-97),
+ * packInt4 (:180-194), packInt2 (:218-230), packTernary (:249-269),
+ * packBinary (:271-283). Returns the bits per code, 0 for other DTypes. */
+int or_pack_native(int dt, const float *w, int64_t n, uint8_t *codes, float *scale_out) {
+    const int bits = narrow_bits_of(dt);
+    if (!bits || n <= 0) return 0;
+    float amax = 0;
+    for (int64_t i = 0; i < n; i++) { float a = (float)fabs((double)w[i]); if (a > amax) amax = a; }
+    float scale = dt == 9 ? amax / 127 : (dt == 14 ? amax / 7 : amax);
+    if (scale == 0) scale = 1;
+    memset(codes, 0, (size_t)((n * bits + 7) / 8));
+    for (int64_t i = 0; i < n; i++) {
+        unsigned code;
+        switch (dt) {
+        case 9: code = (uint8_t)(int8_t)round_clamp(w[i] / scale, -128, 127); break;
+        case 14: code = (unsigned)round_clamp(w[i] / scale, -8, 7) & 0xF; break;
+        case 17: code = (unsigned)(round_clamp(w[i] / scale, -2, 1) + 2) & 3; break;
+        case 19: { float r = w[i] / scale; code = r > 0.5f ? 2 : (r < -0.5f ? 0 : 1); break; }
+        default: code = w[i] >= 0 ? 1 : 0; break;
+        }
+        const int64_t bit = i * bits;
+        codes[bit >> 3] |= (uint8_t)(code << (bit & 7));
+    }
+    *scale_out = scale;
+    return bits;
+}
+
+/* expandNarrowToI8 (layers/dense/simd.go:149-195); Int8 bytes as they are
+ * (nativeInt8Weights, simd.go:506-511). */
+int or_expand_narrow_i8(int dt, const uint8_t *codes, int64_t n, int8_t *out) {
+    for (int64_t i = 0; i < n; i++) {
+        int v;
+        switch (dt) {
+        case 9: v = (int8_t)codes[i]; break;
+        case 14: { int q = (i % 2 == 0) ? (codes[i / 2] & 0xF) : (codes[i / 2] >> 4); v = q > 7 ? q - 16 : q; break; }
+        case 17: v = ((codes[i / 4] >> ((i % 4) * 2)) & 3) - 2; break;
+        case 19: v = ((codes[i / 4] >> ((i % 4) * 2)) & 3) - 1; break;
+        case 20: v = (codes[i / 8] & (1 << (i % 8))) ? 1 : -1; break;
+        default: return -1;
+        }
+        out[i] = (int8_t)v;
+    }
+    return 0;
+}
+
+/* forwardSIMDNarrowI8 / forwardSIMDInt8 (layers/dense/simd.go:130-147,
+ * 303-326): expand (every call, as the reference), quantizeActsI8, DotI8Tile
+ * per row, y = f32(acc) * actScale * scale. acc / act_scale may be NULL. */
+int or_narrow_i8_forward(int dt, const uint8_t *codes, float scale, int64_t rows, int64_t cols,
+                         const float *x, float *y, int32_t *acc, float *act_scale, int batch) {
+    int64_t n = rows * cols;
+    if (scale == 0) scale = 1;
+    int8_t *wi8 = (int8_t *)malloc((size_t)n);
+    if (or_expand_narrow_i8(dt, codes, n, wi8)) { free(wi8); return -1; }
+    int8_t *xq = (int8_t *)malloc((size_t)cols);
+    for (int bt = 0; bt < batch; bt++) {
+        float as = or_quantize_acts_i8(x + (int64_t)bt * cols, cols, xq);
+        if (act_scale) act_scale[bt] = as;
+        for (int64_t o = 0; o < rows; o++) {
+            int32_t a = dot_i8(xq, wi8 + o * cols, cols);
+            if (acc) acc[(int64_t)bt * rows + o] = a;
+            y[(int64_t)bt * rows + o] = (float)a * as * scale;
+        }
+    }
+    free(xq); free(wi8);
+    return 0;
+}
+
+/* weightAt (weights/decode.go:50-215) for the narrow DTypes: f32(q) * scale;
+ * Ternary codes 0 / 2 -> -scale / +scale, 1 and 3 -> 0; Binary +-scale. */
+int or_native_decode(int dt, const uint8_t *codes, float scale, int64_t n, float *out) {
+    if (scale == 0) scale = 1;
+    for (int64_t i = 0; i < n; i++) {
+        switch (dt) {
+        case 19: {
+            int c = (codes[i / 4] >> ((i % 4) * 2)) & 3;
+            out[i] = c == 0 ? -scale : (c == 2 ? scale : 0.0f);
+            break;
+        }
+        case 20: out[i] = (codes[i / 8] & (1 << (i % 8))) ? scale : -scale; break;
+        case 9: case 14: case 17: {
+            int8_t q;
+            if (dt == 9) q = (int8_t)codes[i];
+            else if (dt == 14) { int v = (i % 2 == 0) ? (codes[i / 2] & 0xF) : (codes[i / 2] >> 4); q = (int8_t)(v > 7 ? v - 16 : v); }
+            else q = (int8_t)(((codes[i / 4] >> ((i % 4) * 2)) & 3) - 2);
+            out[i] = (float)q * scale;
+            break;
+        }
+        default: return -1;
+        }
+    }
+    return 0;
+}
+
 int or_num_cpus(void) { return (int)sysconf(_SC_NPROCESSORS_ONLN); }

@@ -8,7 +8,8 @@
  *   - the scalar quant.MatVec / quant.MatVecT (flat f32 walk),
  *   - the fused SIMD path of layers/dense (Ensure*SIMDCache projections,
  *     simd.Dot*Row kernels with f64 accumulation, row-sharded threads),
- *   - the DTypeTernary int8 path (quantizeActsI8 + DotI8Tile).
+ *   - the narrow-DType int8 path (quantizeActsI8 + DotI8Tile) and the
+ *     weights.Store packers / decoders of those DTypes.
  *
  * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg load
  * this library, and only as the checker / the reported CPU baseline. The HIP
@@ -96,6 +97,20 @@ float or_quantize_acts_i8(const float *x, int64_t n, int8_t *xq);
  * (batch floats) may be NULL. */
 int or_ternary_i8_forward(const uint8_t *codes, float scale, int64_t rows, int64_t cols,
                           const float *x, float *y, int32_t *acc, float *act_scale, int batch);
+
+/* ---- narrow weights.Store DTypes (dt = core.DType: 9 Int8, 14 Int4, 17 Int2,
+ * 19 Ternary, 20 Binary) ---- */
+
+/* packNative (weights/native.go:88-283): codes (n*bits+7)/8 bytes LSB-first,
+ * Store.Scale; returns bits per code (0: not a narrow DType). */
+int or_pack_native(int dt, const float *w, int64_t n, uint8_t *codes, float *scale);
+/* expandNarrowToI8 (layers/dense/simd.go:149-195). */
+int or_expand_narrow_i8(int dt, const uint8_t *codes, int64_t n, int8_t *out);
+/* Dense's int8 path for any narrow DType (simd.go:130-147, 303-326). */
+int or_narrow_i8_forward(int dt, const uint8_t *codes, float scale, int64_t rows, int64_t cols,
+                         const float *x, float *y, int32_t *acc, float *act_scale, int batch);
+/* weightAt (weights/decode.go:50-215): the f32 weights weights.Store decodes. */
+int or_native_decode(int dt, const uint8_t *codes, float scale, int64_t n, float *out);
 
 /* One-time cost helpers for the baseline report. */
 int or_num_cpus(void);

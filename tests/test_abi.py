@@ -115,3 +115,36 @@ def test_affine_pack_and_upload_errors():
     p = wv.PackedBlob("AffinePacked", rows, cols, words, scales, np.array([4], np.uint8), 64)
     with pytest.raises(wv.WelvetError, match="mins"):
         wv.upload(p)
+
+
+@pytest.mark.parametrize("dt", ["NativeInt8", "NativeInt4", "NativeInt2", "NativeTernary", "NativeBinary"])
+def test_native_packers_match_oracle(dt):
+    """The library's weights.Store packers (C++) against the C oracle's, byte for
+    byte, on weights with exact ties and clamp edges mixed in."""
+    rng = np.random.default_rng(11)
+    n = 4096 * 3 + 5
+    w = (rng.standard_normal(n) * 0.02).astype(np.float32)
+    amax = np.float32(0.05)
+    w[:8] = [amax, -amax, 0, amax / 2, -amax / 2, amax * 0.25, -0.0, amax * 0.75]
+    p = wv.pack_native(dt, w, 1, n)
+    codes, scale = oracle.pack_native(dt, w)
+    assert np.array_equal(p.raw, codes)
+    assert np.float32(p.tensor_scale) == scale
+
+
+def test_quant_contract_errors_without_device():
+    """quant.MatVec / MatVecT and weights.Store entry points on an unknown
+    handle fail with the reference's nil-blob wording before touching a device."""
+    L = wv.lib()
+    x = np.zeros(4, np.float32)
+    rc = L.wv_quant_matvec(987654321, x.ctypes.data, 4, x.ctypes.data, 4)
+    assert rc == -7 and L.wv_last_error().decode() == "MatVec: nil blob"
+    rc = L.wv_quant_matvec_t(987654321, x.ctypes.data, 4, x.ctypes.data, 4)
+    assert rc == -7 and L.wv_last_error().decode() == "MatVecT: nil blob"
+    xd = np.zeros(4, np.float64)
+    assert L.wv_store_matvec(987654321, xd.ctypes.data, 4, xd.ctypes.data, 4) == -7
+    assert L.wv_last_error().decode() == "weights: nil"
+    assert L.wv_dense_forward(987654321, x.ctypes.data, x.ctypes.data, None, 1, None, -1) == -7
+    with pytest.raises(wv.WelvetError) as e:
+        wv.pack_native("Q4_K", np.zeros(8, np.float32), 1, 8)
+    assert e.value.code != 0

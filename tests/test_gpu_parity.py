@@ -177,14 +177,14 @@ def test_native_ternary_bit_exact(shape):
     x = rng.standard_normal((2, cols)).astype(np.float32)
     p = wv.pack_native_ternary(w, rows, cols)
     d = wv.upload(p)
-    assert d.info()["layout"] == "ternary-i8"
+    assert d.info()["layout"] == "narrow"
     y_ref, acc_ref, as_ref = oracle.ternary_i8_forward(p.raw, np.float32(p.tensor_scale), rows, cols, x)
     tx = torch.from_numpy(x).cuda()
     acc = torch.zeros(2 * rows, dtype=torch.int32, device="cuda")
     act = torch.zeros(2, dtype=torch.float32, device="cuda")
     y = torch.zeros(2 * rows, dtype=torch.float32, device="cuda")
     torch.cuda.synchronize()  # the library's stream does not wait for torch's
-    d.ternary_acc_dev(tx.data_ptr(), acc.data_ptr(), act.data_ptr(), 2)
+    d.native_acc_dev(tx.data_ptr(), acc.data_ptr(), act.data_ptr(), 2)
     d.matvec_dev(tx.data_ptr(), y.data_ptr(), 2)
     wv.sync()
     assert np.array_equal(acc.cpu().numpy(), acc_ref)

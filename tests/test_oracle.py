@@ -376,3 +376,117 @@ def test_affine_matvec_t_skips_zero_rows():
     neg = np.full(cols, -0.0, np.float32)  # a skipped row leaves -0.0 untouched
     gz = np.zeros(rows, np.float32)
     assert np.signbit(oracle.matvec_t_scalar(p, gz, neg)).all()
+
+
+# ---- narrow weights.Store DTypes, Dense's bias/activation epilogue, Store f64 products ----
+
+from oracle import dense_ref  # noqa: E402
+
+NARROW = {"NativeInt8": 9, "NativeInt4": 14, "NativeInt2": 17, "NativeTernary": 19, "NativeBinary": 20}
+
+
+def test_native_pack_known_answers():
+    """Hand-computed packs (weights/native.go): Int4 scale = absMax/7, half-away
+    ties and clamps; Int2 clamps to [-2, 1]; Binary sign bit (0 -> +1)."""
+    w = np.array([0.7, -0.7, 0.05, -0.15, 0.35, 0.0, -0.0, 0.1], np.float32)
+    codes, scale = oracle.pack_native("NativeInt4", w)
+    assert scale == np.float32(np.float32(0.7) / np.float32(7))
+    # q = round(w/s): 7, -7, 0.5 -> 1 (half away), -1.5 -> -2, 3.5 -> 4, 0, 0, 1
+    q = [7, -7, 1, -2, 4, 0, 0, 1]
+    assert list(codes) == [(q[0] & 15) | ((q[1] & 15) << 4), (q[2] & 15) | ((q[3] & 15) << 4),
+                           (q[4] & 15) | ((q[5] & 15) << 4), (q[6] & 15) | ((q[7] & 15) << 4)]
+    codes, scale = oracle.pack_native("NativeInt2", np.array([1.0, -1.0, 0.4, -0.6], np.float32))
+    # scale = absMax, so q = round(w/s) is 1, -1, 0, -1 (-2 is never reached) -> codes q + 2
+    assert scale == 1.0 and codes[0] == (3 | (1 << 2) | (2 << 4) | (1 << 6))
+    codes, scale = oracle.pack_native("NativeBinary", np.array([0.5, -0.25, 0.0, -0.0, 1, -1, 2, -2, 3], np.float32))
+    assert scale == 3.0 and list(codes) == [0b01011101, 0b1]  # -0.0 >= 0 holds: bit set
+    codes, scale = oracle.pack_native("NativeInt8", np.array([127.0, -127.0, 0.5, -63.5], np.float32))
+    assert scale == 1.0 and list(codes.view(np.int8)) == [127, -127, 1, -64]
+    codes, scale = oracle.pack_native("NativeTernary", np.zeros(5, np.float32))
+    assert scale == 1.0 and list(codes) == [0b01010101, 0b01]  # all-zero tensor: scale 1, codes "0"
+
+
+@pytest.mark.parametrize("dt", sorted(NARROW))
+def test_native_oracle_two_restatements(dt):
+    """C oracle vs the numpy restatement: packs, int8 expansion and decode."""
+    rng = np.random.default_rng(NARROW[dt])
+    n = 1237
+    w = (rng.standard_normal(n) * 0.03).astype(np.float32)
+    codes, scale = oracle.pack_native(dt, w)
+    nc, ns = np_ref.pack_native(NARROW[dt], w)
+    assert np.array_equal(codes, nc) and scale == ns
+    assert np.array_equal(oracle.expand_narrow_i8(dt, codes, n), np_ref.expand_narrow_i8(NARROW[dt], codes, n))
+    assert np.array_equal(oracle.native_decode(dt, codes, scale, n), np_ref.native_decode(NARROW[dt], codes, scale, n))
+
+
+def test_native_expand_closed_forms():
+    """Every code of every DType maps as expandNarrowToI8 / weightAt state,
+    including Ternary code 3 (+2 on the int8 path, 0 when decoded)."""
+    allc = np.array([0b11100100], np.uint8)  # 2-bit codes 0, 1, 2, 3
+    assert list(oracle.expand_narrow_i8("NativeTernary", allc, 4)) == [-1, 0, 1, 2]
+    assert list(oracle.expand_narrow_i8("NativeInt2", allc, 4)) == [-2, -1, 0, 1]
+    assert list(oracle.native_decode("NativeTernary", allc, 0.5, 4)) == [-0.5, 0, 0.5, 0]
+    nib = np.array([0x87, 0xF0], np.uint8)  # nibbles 7, 8, 0, 15
+    assert list(oracle.expand_narrow_i8("NativeInt4", nib, 4)) == [7, -8, 0, -1]
+    assert list(oracle.expand_narrow_i8("NativeBinary", np.array([0b10100101], np.uint8), 8)) == [1, -1, 1, -1, -1, 1, -1, 1]
+    assert list(oracle.expand_narrow_i8("NativeInt8", np.array([0x80, 0x7F, 0xFF], np.uint8), 3)) == [-128, 127, -1]
+    assert list(oracle.native_decode("NativeInt4", nib, 0, 4)) == [7, -8, 0, -1]  # scale 0 reads as 1
+
+
+@pytest.mark.parametrize("dt", sorted(NARROW))
+def test_narrow_forward_brute_force(dt):
+    """The C oracle's int8 path equals an exact int64 brute force over the numpy
+    expansion and quantization (int32 accumulators bit for bit, y as f32)."""
+    rng = np.random.default_rng(3 + NARROW[dt])
+    rows, cols = 23, 200
+    w = (rng.standard_normal(rows * cols) * 0.02).astype(np.float32)
+    x = rng.standard_normal((2, cols)).astype(np.float32)
+    codes, scale = oracle.pack_native(dt, w)
+    y, acc, asc = oracle.narrow_i8_forward(dt, codes, scale, rows, cols, x)
+    y2, acc2, asc2 = np_ref.narrow_i8_forward(NARROW[dt], codes, scale, rows, cols, x)
+    assert np.array_equal(acc, acc2) and np.array_equal(asc, asc2) and np.array_equal(y, y2)
+
+
+def test_activation_closed_forms():
+    """core.Activate (core/activate.go:6-37) at points with known values."""
+    x = np.array([-2.0, 0.0, 3.0])
+    assert list(dense_ref.activate(x, "relu")) == [0.0, 0.0, 3.0]
+    assert list(dense_ref.activate(x, "relu2")) == [0.0, 0.0, 9.0]
+    assert list(dense_ref.activate(x, "leaky_relu")) == [-0.02, 0.0, 3.0]
+    assert list(dense_ref.activate(x, "linear")) == [-2.0, 0.0, 3.0]
+    assert dense_ref.activate(np.array([0.0]), "sigmoid")[0] == 0.5
+    assert dense_ref.activate(np.array([0.0]), "tanh")[0] == 0.0
+    assert dense_ref.activate(np.array([0.0]), "silu")[0] == 0.0
+    # silu(x) = x * sigmoid(x); sigmoid(ln 3) = 3/4
+    assert abs(dense_ref.activate(np.array([np.log(3.0)]), "silu")[0] - 0.75 * np.log(3.0)) < 1e-15
+    # GELU tanh form at 1: 0.5 * (1 + tanh(sqrt(2/pi) * 1.044715))
+    g = 0.5 * (1 + np.tanh(np.sqrt(2 / np.pi) * 1.044715))
+    assert abs(dense_ref.activate(np.array([1.0]), "gelu")[0] - g) < 1e-15
+    assert abs(g - 0.8411919906082768) < 1e-15
+
+
+def test_apply_bias_act_rules():
+    """applyBiasAct (layers/dense/dense.go:145-167): the bias is added in f64 and
+    rounded into pre; without a bias pre stays; post = act(f32 pre); linear with
+    no bias copies pre; a bias shorter than the row leaves the tail unbiased."""
+    pre = np.array([[1.0, -2.0, 0.5]], np.float32)
+    p, q = dense_ref.apply_bias_act(pre, None, "linear")
+    assert np.array_equal(p, pre) and np.array_equal(q, pre)
+    p, q = dense_ref.apply_bias_act(pre, np.array([0.25, 1.0]), "relu")
+    assert list(p[0]) == [1.25, -1.0, 0.5] and list(q[0]) == [1.25, 0.0, 0.5]
+    b = np.array([1e-9, 0, 0])  # below f32 resolution at 1.0: pre unchanged after rounding
+    p, _ = dense_ref.apply_bias_act(pre, b, "linear")
+    assert p[0, 0] == np.float32(1.0)
+    p, q = dense_ref.apply_bias_act(pre, None, "sigmoid")
+    assert np.array_equal(p, pre) and q[0, 0] == np.float32(1 / (1 + np.exp(-1.0)))
+
+
+def test_store_f64_closed_forms():
+    """matVecNativeF64 / matVecTNativeF64 on matrices whose products are exact."""
+    w = np.array([1, 2, 3, 4, 5, 6], np.float32)  # 2 x 3
+    y = dense_ref.store_matvec_f64(w, 2, 3, np.array([1.0, 0.5, 0.25, 99.0]))  # x longer than cols
+    assert list(y) == [1 + 1 + 0.75, 4 + 2.5 + 1.5]
+    gx = dense_ref.store_matvec_t_f64(w, 2, 3, np.array([1.0, 0.0]), np.array([0.5, 0.5, 0.5]))
+    assert list(gx) == [1.5, 2.5, 3.5]
+    wi = np.array([np.inf, 1, 1, 1, 1, 1], np.float32)  # a zero gy row is skipped, so inf never meets 0
+    assert np.isfinite(dense_ref.store_matvec_t_f64(wi, 2, 3, np.array([0.0, 1.0]), np.zeros(3))).all()

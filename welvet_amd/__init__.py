@@ -15,25 +15,31 @@ import numpy as np
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libwelvet_hip.so")
 
-# quant.Format numbering (quant/format.go:9-39) + FormatNone DTypeTernary.
+# quant.Format numbering (quant/format.go:9-39; "none" = f32 weights) and the
+# FormatNone weights.Store DTypes (1000 + core.DType, core/dtype.go:11-52).
 FORMATS = {
-    "Q8_0": 1, "Q4_0": 2, "Q4_1": 3, "Q5_0": 4, "Q5_1": 5,
+    "none": 0, "Q8_0": 1, "Q4_0": 2, "Q4_1": 3, "Q5_0": 4, "Q5_1": 5,
     "Q2_K": 6, "Q3_K": 7, "Q4_K": 8, "Q5_K": 9, "Q6_K": 10,
     "IQ1_S": 11, "IQ2_XXS": 12, "IQ2_XS": 13, "IQ3_XXS": 14, "IQ3_S": 15,
     "IQ4_NL": 16, "IQ4_XS": 17, "TernaryPacked": 18, "BinaryPacked": 19, "AffinePacked": 20,
-    "NativeTernary": 1019,
+    "NativeInt8": 1009, "NativeInt4": 1014, "NativeInt2": 1017, "NativeTernary": 1019, "NativeBinary": 1020,
 }
+NATIVE = ("NativeInt8", "NativeInt4", "NativeInt2", "NativeTernary", "NativeBinary")
+NATIVE_BITS = {"NativeInt8": 8, "NativeInt4": 4, "NativeInt2": 2, "NativeTernary": 2, "NativeBinary": 1}
+# core.ActivationType (core/layer.go:88-99)
+ACT = {"linear": -1, "relu": 0, "silu": 1, "gelu": 2, "tanh": 3, "sigmoid": 4, "leaky_relu": 5, "relu2": 6}
 FORMAT_NAMES = {v: k for k, v in FORMATS.items()}
-LAYOUTS = {0: "raw", 1: "row-interleaved", 4: "ternary-i8"}
+LAYOUTS = {0: "raw", 1: "row-interleaved", 4: "narrow", 5: "f32"}
 
 WV_E = {-1: "ARG", -2: "SHAPE", -3: "FORMAT", -4: "OOM", -5: "HIP", -6: "NODEV", -7: "HANDLE"}
 
 # Every symbol include/welvet_hip.h declares.
 EXPORTS = (
     "wv_init", "wv_last_error", "wv_version", "wv_pack_sizes", "wv_pack",
-    "wv_pack_native_ternary", "wv_blob_upload", "wv_blob_upload_wire", "wv_blob_free", "wv_blob_info",
-    "wv_matvec", "wv_matvec_dev", "wv_ternary_acc_dev", "wv_matvec_t",
-    "wv_matvec_t_dev", "wv_matmul", "wv_matmul_dev", "wv_sync",
+    "wv_pack_native", "wv_blob_upload", "wv_blob_upload_wire", "wv_blob_free", "wv_blob_info",
+    "wv_matvec", "wv_matvec_dev", "wv_quant_matvec", "wv_dense_forward", "wv_dense_forward_dev",
+    "wv_native_acc_dev", "wv_store_matvec", "wv_matvec_t", "wv_matvec_t_dev", "wv_quant_matvec_t",
+    "wv_store_matvec_t", "wv_matmul", "wv_matmul_dev", "wv_sync",
     "wv_decoder_create", "wv_decoder_set_layer", "wv_decoder_set_output", "wv_decoder_set_kv",
     "wv_decoder_use_graph", "wv_decoder_generate", "wv_decoder_free",
 )
@@ -64,7 +70,7 @@ def lib():
     L.wv_version.restype = ctypes.c_char_p
     L.wv_pack_sizes.argtypes = [ctypes.c_int, _I64, _I64, _P, _P, _P, _P, _P]
     L.wv_pack.argtypes = [ctypes.c_int, _P, _I64, _I64, _P, _P, _P, _P]
-    L.wv_pack_native_ternary.argtypes = [_P, _I64, _P, _P]
+    L.wv_pack_native.argtypes = [ctypes.c_int, _P, _I64, _P, _P]
     L.wv_blob_upload.argtypes = [ctypes.c_int, _I64, _I64, ctypes.c_int32, _P, _SZ, _P, _SZ, _P, _SZ, _P, _SZ,
                                  ctypes.c_float, _P]
     L.wv_blob_upload_wire.argtypes = [ctypes.c_int, _I64, _I64, _P, _SZ, _P]
@@ -72,7 +78,13 @@ def lib():
     L.wv_blob_info.argtypes = [ctypes.c_uint64, _P, _P, _P, _P, _P]
     L.wv_matvec.argtypes = [ctypes.c_uint64, _P, _P, ctypes.c_int32]
     L.wv_matvec_dev.argtypes = [ctypes.c_uint64, _P, _P, ctypes.c_int32, _P]
-    L.wv_ternary_acc_dev.argtypes = [ctypes.c_uint64, _P, _P, _P, ctypes.c_int32, _P]
+    L.wv_native_acc_dev.argtypes = [ctypes.c_uint64, _P, _P, _P, ctypes.c_int32, _P]
+    L.wv_quant_matvec.argtypes = [ctypes.c_uint64, _P, _SZ, _P, _SZ]
+    L.wv_quant_matvec_t.argtypes = [ctypes.c_uint64, _P, _SZ, _P, _SZ]
+    L.wv_dense_forward.argtypes = [ctypes.c_uint64, _P, _P, _P, ctypes.c_int32, _P, ctypes.c_int32]
+    L.wv_dense_forward_dev.argtypes = [ctypes.c_uint64, _P, _P, _P, ctypes.c_int32, _P, ctypes.c_int32, _P]
+    L.wv_store_matvec.argtypes = [ctypes.c_uint64, _P, _SZ, _P, _SZ]
+    L.wv_store_matvec_t.argtypes = [ctypes.c_uint64, _P, _SZ, _P, _SZ]
     L.wv_matvec_t.argtypes = [ctypes.c_uint64, _P, _P, ctypes.c_int32]
     L.wv_matvec_t_dev.argtypes = [ctypes.c_uint64, _P, _P, ctypes.c_int32, _P]
     L.wv_matmul.argtypes = [ctypes.c_uint64, _P, _P, ctypes.c_int32]
@@ -136,9 +148,13 @@ def pack_sizes(fmt, rows: int, cols: int):
 
 
 def pack(fmt, w: np.ndarray, rows: int, cols: int) -> PackedBlob:
-    """quant.Pack (quant/pack.go:4) through the library's host packer."""
-    if _fmt(fmt) == FORMATS["NativeTernary"]:
-        return pack_native_ternary(w, rows, cols)
+    """quant.Pack (quant/pack.go:4) through the library's host packer; the
+    WV_NATIVE_* DTypes through the weights.Store packers; "none" keeps f32."""
+    if _fmt(fmt) in (FORMATS[n] for n in NATIVE):
+        return pack_native(fmt, w, rows, cols)
+    if _fmt(fmt) == 0:
+        w = np.ascontiguousarray(w, np.float32).reshape(-1)[: rows * cols]
+        return PackedBlob(0, rows, cols, w.view(np.uint8).copy())
     raw_n, ns, nmins, nmeta, bw = pack_sizes(fmt, rows, cols)
     w = np.ascontiguousarray(w, np.float32).reshape(-1)
     if w.size < rows * cols:
@@ -151,13 +167,19 @@ def pack(fmt, w: np.ndarray, rows: int, cols: int) -> PackedBlob:
     return PackedBlob(fmt, rows, cols, raw, scales, meta, bw, mins=mins)
 
 
-def pack_native_ternary(w: np.ndarray, rows: int, cols: int) -> PackedBlob:
-    """weights.Store DTypeTernary pack (weights/native.go:249-267)."""
+def pack_native(fmt, w: np.ndarray, rows: int, cols: int) -> PackedBlob:
+    """weights.Store pack of a narrow DType (weights/native.go:88-283): codes + Store.Scale."""
+    f = _fmt(fmt)
     w = np.ascontiguousarray(w, np.float32).reshape(-1)[: rows * cols]
-    codes = np.zeros((w.size + 3) // 4, np.uint8)
+    codes = np.zeros((w.size * NATIVE_BITS.get(FORMAT_NAMES.get(f), 8) + 7) // 8, np.uint8)
     scale = ctypes.c_float()
-    check(lib().wv_pack_native_ternary(w.ctypes.data, w.size, codes.ctypes.data, ctypes.byref(scale)))
-    return PackedBlob("NativeTernary", rows, cols, codes, None, None, 0, scale.value)
+    check(lib().wv_pack_native(f, w.ctypes.data, w.size, codes.ctypes.data, ctypes.byref(scale)))
+    return PackedBlob(f, rows, cols, codes, None, None, 0, scale.value)
+
+
+def pack_native_ternary(w: np.ndarray, rows: int, cols: int) -> PackedBlob:
+    """weights.Store DTypeTernary pack (weights/native.go:249-269)."""
+    return pack_native("NativeTernary", w, rows, cols)
 
 
 def _p(a):
@@ -240,8 +262,56 @@ class DeviceBlob:
     def matvec_t_dev(self, gy_ptr: int, gx_ptr: int, batch: int = 1, stream: int | None = None) -> None:
         check(lib().wv_matvec_t_dev(self.handle, gy_ptr, gx_ptr, batch, stream))
 
-    def ternary_acc_dev(self, x_ptr: int, acc_ptr: int, act_ptr: int, batch: int = 1, stream: int | None = None) -> None:
-        check(lib().wv_ternary_acc_dev(self.handle, x_ptr, acc_ptr, act_ptr, batch, stream))
+    def native_acc_dev(self, x_ptr: int, acc_ptr: int, act_ptr: int, batch: int = 1, stream: int | None = None) -> None:
+        check(lib().wv_native_acc_dev(self.handle, x_ptr, acc_ptr, act_ptr, batch, stream))
+
+    ternary_acc_dev = native_acc_dev
+
+    def quant_matvec(self, x: np.ndarray, y: np.ndarray) -> None:
+        """quant.MatVec(b, x, y) (quant/matvec.go:5): one vector, checkBlobYX, y[:rows] overwritten."""
+        x = np.ascontiguousarray(x, np.float32)
+        assert y.dtype == np.float32 and y.flags.c_contiguous
+        check(lib().wv_quant_matvec(self.handle, x.ctypes.data if x.size else None, x.size,
+                                    y.ctypes.data if y.size else None, y.size))
+
+    def quant_matvec_t(self, gy: np.ndarray, gx: np.ndarray) -> None:
+        """quant.MatVecT(b, gy, gx) (quant/matvec_t.go:5): gx[:cols] += W^T gy[:rows], checkBlobGYGX."""
+        gy = np.ascontiguousarray(gy, np.float32)
+        assert gx.dtype == np.float32 and gx.flags.c_contiguous
+        check(lib().wv_quant_matvec_t(self.handle, gy.ctypes.data if gy.size else None, gy.size,
+                                      gx.ctypes.data if gx.size else None, gx.size))
+
+    def dense_forward(self, x: np.ndarray, bias: np.ndarray | None = None, act="linear"):
+        """dense.Forward (layers/dense/dense.go:100): (pre, post) with applyBiasAct (dense.go:145-167)."""
+        x = np.ascontiguousarray(x, np.float32)
+        batch = x.size // self.cols
+        pre = np.zeros((batch, self.rows), np.float32)
+        post = np.zeros((batch, self.rows), np.float32)
+        b = None if bias is None else np.ascontiguousarray(bias, np.float64)
+        a = ACT[act] if isinstance(act, str) else int(act)
+        check(lib().wv_dense_forward(self.handle, x.ctypes.data, pre.ctypes.data, post.ctypes.data, batch, _p(b), a))
+        if x.ndim == 1:
+            return pre.reshape(self.rows), post.reshape(self.rows)
+        return pre, post
+
+    def dense_forward_dev(self, x_ptr: int, pre_ptr: int, post_ptr: int | None, batch: int = 1,
+                          bias_ptr: int | None = None, act=-1, stream: int | None = None) -> None:
+        a = ACT[act] if isinstance(act, str) else int(act)
+        check(lib().wv_dense_forward_dev(self.handle, x_ptr, pre_ptr, post_ptr, batch, bias_ptr, a, stream))
+
+    def store_matvec(self, x: np.ndarray, y: np.ndarray) -> None:
+        """weights.Store.MatVec with f64 x / y (weights/store.go:133-145)."""
+        x = np.ascontiguousarray(x, np.float64)
+        assert y.dtype == np.float64 and y.flags.c_contiguous
+        check(lib().wv_store_matvec(self.handle, x.ctypes.data if x.size else None, x.size,
+                                    y.ctypes.data if y.size else None, y.size))
+
+    def store_matvec_t(self, gy: np.ndarray, gx: np.ndarray) -> None:
+        """weights.Store.MatVecT with f64 gy / gx (weights/store.go:147-160): gx += W^T gy."""
+        gy = np.ascontiguousarray(gy, np.float64)
+        assert gx.dtype == np.float64 and gx.flags.c_contiguous
+        check(lib().wv_store_matvec_t(self.handle, gy.ctypes.data if gy.size else None, gy.size,
+                                      gx.ctypes.data if gx.size else None, gx.size))
 
     def free(self) -> None:
         if self.handle:

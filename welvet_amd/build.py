@@ -12,6 +12,7 @@ import os
 import shutil
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
@@ -27,7 +28,7 @@ HIP_FLAGS = [
 ]
 CXX_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-pthread", "-ffp-contract=off", "-Wall"]
 
-HIP_SOURCES = ["runtime.hip", "gemv.hip", "gemv_rpl.hip", "gemm_rpl.hip", "decode.hip"]
+HIP_SOURCES = ["runtime.hip", "gemv.hip", "gemv_rpl.hip", "gemm_rpl.hip", "decode.hip", "native.hip"]
 CXX_SOURCES = ["pack.cpp"]
 
 
@@ -41,15 +42,14 @@ def _run(cmd):
 
 def build(verbose: bool = False) -> str:
     os.makedirs(OBJ, exist_ok=True)
-    objs = []
-    for src in HIP_SOURCES:
-        o = os.path.join(OBJ, src + ".o")
-        _run([HIPCC, *HIP_FLAGS, "-c", os.path.join(CSRC, src), "-o", o])
-        objs.append(o)
-    for src in CXX_SOURCES:
-        o = os.path.join(OBJ, src + ".o")
-        _run(["g++", *CXX_FLAGS, "-c", os.path.join(CSRC, src), "-o", o])
-        objs.append(o)
+    jobs = [[HIPCC, *HIP_FLAGS, "-c", os.path.join(CSRC, src), "-o", os.path.join(OBJ, src + ".o")]
+            for src in HIP_SOURCES]
+    jobs += [["g++", *CXX_FLAGS, "-c", os.path.join(CSRC, src), "-o", os.path.join(OBJ, src + ".o")]
+             for src in CXX_SOURCES]
+    workers = max(1, min(len(jobs), int(os.environ.get("MAX_JOBS", "0")) or (os.cpu_count() or 1)))
+    with ThreadPoolExecutor(workers) as pool:
+        list(pool.map(_run, jobs))
+    objs = [j[-1] for j in jobs]
     tmp = LIB + ".tmp"
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs, "-pthread"])
     os.replace(tmp, LIB)

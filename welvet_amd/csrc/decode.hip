@@ -770,8 +770,11 @@ struct Decoder {
     std::vector<Layer> layers;
     DevBlob lm{};
     bool lm_set = false;
-    float* final_norm = nullptr;
+    float* final_norm = nullptr;  // allocated once; used while has_final_norm
+    bool has_final_norm = false;
     float* embed = nullptr;
+    float* gemv_scratch = nullptr;  // K-split partials of the projections (decoder-owned)
+    size_t gemv_scratch_floats = 0;
     // activations and state
     float *h = nullptr, *n = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr;
     float *g = nullptr, *u = nullptr, *logits = nullptr, *part = nullptr;
@@ -791,15 +794,6 @@ struct Decoder {
     hipGraphExec_t exec = nullptr;
     hipGraph_t graph = nullptr;
 };
-
-// WV_DECODER_FUSE=0 keeps every projection as its own launch (for comparisons).
-bool fusion_off() {
-    static const bool off = [] {
-        const char* v = std::getenv("WV_DECODER_FUSE");
-        return v && v[0] == '0';
-    }();
-    return off;
-}
 
 std::mutex g_dmu;
 std::unordered_map<uint64_t, Decoder*> g_decs;
@@ -824,9 +818,16 @@ void drop_fused(Layer& ly) {
     ly.has_qkv = ly.has_gu = false;
 }
 
+void drop_graph(Decoder& d) {
+    if (d.exec) hipGraphExecDestroy(d.exec);
+    if (d.graph) hipGraphDestroy(d.graph);
+    d.exec = nullptr;
+    d.graph = nullptr;
+}
+
 void release(Decoder* d) {
-    if (d->exec) hipGraphExecDestroy(d->exec);
-    if (d->graph) hipGraphDestroy(d->graph);
+    drop_graph(*d);
+    if (d->gemv_scratch) hipFree(d->gemv_scratch);
     for (Layer& ly : d->layers) drop_fused(ly);
     for (void* p : d->allocs) hipFree(p);
     if (d->stream) hipStreamDestroy(d->stream);
@@ -836,10 +837,10 @@ void release(Decoder* d) {
 // y (op)= W x for one projection: fused epilogue on the row-interleaved layout,
 // separate elementwise kernels otherwise.
 int proj(Decoder& d, const DevBlob& w, const float* x, float* y, int mode, const float* aux, float* tmp) {
-    if (w.layout == LAYOUT_RPL) return launch_rpl(w, x, y, 1, d.stream, mode, aux);
+    if (w.layout == LAYOUT_RPL) return launch_rpl(w, x, y, 1, d.stream, mode, aux, d.gemv_scratch);
     const int rows = int(w.rows);
     float* out = mode == RPL_STORE ? y : tmp;
-    int e = launch_matvec(w, x, out, 1, d.stream);
+    int e = launch_matvec(w, x, out, 1, d.stream, d.gemv_scratch);
     if (e) return e;
     if (mode == RPL_ADD) hipLaunchKernelGGL(k_add, dim3((rows + 255) / 256), dim3(256), 0, d.stream, y, tmp, rows);
     if (mode == RPL_SILU_MUL)
@@ -915,6 +916,7 @@ int enqueue_step(Decoder& d, int advance) {
         ex.nrm_n = nss;
         ex.nrm_eps = c.rms_eps;
         ex.ss_out = ss_out;
+        ex.partial = d.gemv_scratch;
         return ex;
     };
     for (int L = 0; L < c.n_layers; ++L) {
@@ -925,7 +927,7 @@ int enqueue_step(Decoder& d, int advance) {
         } else {
             hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(1024), 0, d.stream, d.h, ly.attn_norm, d.n, c.hidden, c.rms_eps);
             if (ly.has_qkv) {
-                e = launch_rpl(ly.qkv, d.n, d.q, 1, d.stream);  // q, k, v are contiguous
+                e = launch_rpl(ly.qkv, d.n, d.q, 1, d.stream, RPL_STORE, nullptr, d.gemv_scratch);  // q, k, v are contiguous
             } else {
                 e = proj(d, ly.w[0], d.n, d.q, RPL_STORE, nullptr, tmp);
                 if (!e) e = proj(d, ly.w[1], d.n, d.k, RPL_STORE, nullptr, tmp);
@@ -946,7 +948,7 @@ int enqueue_step(Decoder& d, int advance) {
         if (e) return e;
         hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(1024), 0, d.stream, d.h, ly.ffn_norm, d.n, c.hidden, c.rms_eps);
         if (ly.has_gu) {
-            e = launch_rpl(ly.gu, d.n, d.u, 1, d.stream, RPL_SWIGLU);
+            e = launch_rpl(ly.gu, d.n, d.u, 1, d.stream, RPL_SWIGLU, nullptr, d.gemv_scratch);
         } else {
             e = proj(d, ly.w[4], d.n, d.g, RPL_STORE, nullptr, tmp);
             if (!e) e = proj(d, ly.w[5], d.n, d.u, RPL_SILU_MUL, d.g, tmp);
@@ -955,11 +957,11 @@ int enqueue_step(Decoder& d, int advance) {
         if (e) return e;
     }
     int e = 0;
-    if (fn && d.final_norm) {
+    if (fn && d.has_final_norm) {
         e = launch_rpl_ex(d.lm, d.h, d.logits, 1, d.stream, normed(d.final_norm, d.ss_a, RPL_STORE, nullptr));
     } else {
         const float* fin = d.h;
-        if (d.final_norm) {
+        if (d.has_final_norm) {
             hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(1024), 0, d.stream, d.h, d.final_norm, d.n, c.hidden,
                                c.rms_eps);
             fin = d.n;
@@ -976,7 +978,7 @@ int enqueue_step(Decoder& d, int advance) {
 // row-interleaved layout with Q|K|V and gate/up fused (the residual GEMVs then
 // produce the sums of squares the next norm needs).
 bool can_fuse_norms(const Decoder& d) {
-    if (fusion_off() || d.c.hidden % 256) return false;
+    if (d.c.hidden % 256) return false;
     for (const Layer& ly : d.layers)
         if (!ly.has_qkv || !ly.has_gu || ly.w[3].layout != LAYOUT_RPL || ly.w[6].layout != LAYOUT_RPL) return false;
     return d.lm.layout == LAYOUT_RPL;
@@ -987,13 +989,28 @@ int ready(Decoder& d) {
         if (!d.layers[L].set) return rt_fail(WV_E_ARG, "decoder: layer %d has no weights (wv_decoder_set_layer)", L);
     if (!d.lm_set || !d.embed) return rt_fail(WV_E_ARG, "decoder: no LM head / embedding (wv_decoder_set_output)");
     const bool fn = can_fuse_norms(d);
-    if (fn != d.fused_norm && d.exec) {
-        hipGraphExecDestroy(d.exec);
-        hipGraphDestroy(d.graph);
-        d.exec = nullptr;
-        d.graph = nullptr;
-    }
+    if (fn != d.fused_norm) drop_graph(d);
     d.fused_norm = fn;
+    // K-split scratch of the widest projection plan; a captured graph holds
+    // its address, so growing it means capturing again.
+    size_t need = matvec_scratch_floats(d.lm, 1);
+    for (const Layer& ly : d.layers) {
+        for (const DevBlob& w : ly.w) need = std::max(need, matvec_scratch_floats(w, 1));
+        if (ly.has_qkv) need = std::max(need, matvec_scratch_floats(ly.qkv, 1));
+        if (ly.has_gu) need = std::max(need, matvec_scratch_floats(ly.gu, 1));
+    }
+    if (need > d.gemv_scratch_floats) {
+        drop_graph(d);
+        if (d.gemv_scratch) hipFree(d.gemv_scratch);
+        d.gemv_scratch = nullptr;
+        d.gemv_scratch_floats = 0;
+        const hipError_t e = hipMalloc(&d.gemv_scratch, need * sizeof(float));
+        if (e != hipSuccess) {
+            d.gemv_scratch = nullptr;
+            return rt_hip_fail(e, "decoder: projection scratch");
+        }
+        d.gemv_scratch_floats = need;
+    }
     return WV_OK;
 }
 
@@ -1006,12 +1023,7 @@ int run_steps(Decoder& d, int n_steps, int advance) {
         return WV_OK;
     }
     if (!d.exec || d.graph_advance != advance) {
-        if (d.exec) {
-            hipGraphExecDestroy(d.exec);
-            hipGraphDestroy(d.graph);
-            d.exec = nullptr;
-            d.graph = nullptr;
-        }
+        drop_graph(d);
         hipError_t e = hipStreamBeginCapture(d.stream, hipStreamCaptureModeThreadLocal);
         if (e != hipSuccess) return rt_hip_fail(e, "decoder: begin capture");
         const int k = enqueue_step(d, advance);
@@ -1151,40 +1163,41 @@ int wv_decoder_set_layer(uint64_t dec, int32_t layer, const uint64_t* blobs, con
                                 {c.ffn, c.hidden}, {c.ffn, c.hidden}, {c.hidden, c.ffn}};
     static const char* names[7] = {"Q", "K", "V", "O", "gate", "up", "down"};
     Layer& ly = d->layers[layer];
+    DevBlob nw[7];
     for (int i = 0; i < 7; ++i) {
         DevBlob b;
         if (!rt_lookup(blobs[i], b)) return rt_fail(WV_E_HANDLE, "wv_decoder_set_layer: %s blob %llu unknown", names[i], (unsigned long long)blobs[i]);
         if (b.rows != want[i][0] || b.cols != want[i][1])
             return rt_fail(WV_E_SHAPE, "wv_decoder_set_layer: %s is %lldx%lld, want %lldx%lld", names[i], (long long)b.rows,
                            (long long)b.cols, (long long)want[i][0], (long long)want[i][1]);
-        ly.w[i] = b;
+        nw[i] = b;
     }
     hipSetDevice(d->device);
-    hipError_t e = hipMemcpy(ly.attn_norm, attn_norm, size_t(c.hidden) * 4, hipMemcpyHostToDevice);
+    // A captured step reads this layer's old weights and fused copies: drop
+    // it, and keep the layer unusable until every part below succeeded.
+    drop_graph(*d);
+    ly.set = false;
+    hipError_t e = hipStreamSynchronize(d->stream);
+    if (e == hipSuccess) e = hipMemcpy(ly.attn_norm, attn_norm, size_t(c.hidden) * 4, hipMemcpyHostToDevice);
     if (e == hipSuccess) e = hipMemcpy(ly.ffn_norm, ffn_norm, size_t(c.hidden) * 4, hipMemcpyHostToDevice);
     if (e != hipSuccess) return rt_hip_fail(e, "wv_decoder_set_layer: norms");
     drop_fused(ly);
+    for (int i = 0; i < 7; ++i) ly.w[i] = nw[i];
     const DevBlob* w = ly.w;
     auto rpl_same = [&](int i, int j) {
         return w[i].layout == LAYOUT_RPL && w[j].layout == LAYOUT_RPL && w[i].fmt == w[j].fmt;
     };
-    if (!fusion_off() && rpl_same(0, 1) && rpl_same(0, 2) && w[0].rows % 64 == 0 && w[1].rows % 64 == 0) {
+    if (rpl_same(0, 1) && rpl_same(0, 2) && w[0].rows % 64 == 0 && w[1].rows % 64 == 0) {
         const int k = rpl_fuse_rows(w, 3, ly.qkv, d->stream);
         if (k != hipSuccess) return rt_hip_fail(hipError_t(k), "wv_decoder_set_layer: fuse Q|K|V");
         ly.has_qkv = true;
     }
-    if (!fusion_off() && rpl_same(4, 5) && w[4].rows % 32 == 0) {
+    if (rpl_same(4, 5) && w[4].rows % 32 == 0) {
         const int k = rpl_fuse_pairs(w[4], w[5], ly.gu, d->stream);
         if (k != hipSuccess) return rt_hip_fail(hipError_t(k), "wv_decoder_set_layer: fuse gate/up");
         ly.has_gu = true;
     }
     ly.set = true;
-    if (d->exec) {  // weights changed: capture again on the next graph run
-        hipGraphExecDestroy(d->exec);
-        hipGraphDestroy(d->graph);
-        d->exec = nullptr;
-        d->graph = nullptr;
-    }
     return WV_OK;
 }
 
@@ -1199,14 +1212,19 @@ int wv_decoder_set_output(uint64_t dec, uint64_t lm_head, const float* final_nor
         return rt_fail(WV_E_SHAPE, "wv_decoder_set_output: LM head is %lldx%lld, want %dx%d", (long long)b.rows,
                        (long long)b.cols, c.vocab, c.hidden);
     hipSetDevice(d->device);
+    // A captured step holds the old head, norm and table: capture again, and
+    // keep the output unusable until the copies below succeeded.
+    drop_graph(*d);
+    d->lm_set = false;
     int rc = WV_OK;
     if (final_norm && !d->final_norm) rc = dalloc(*d, reinterpret_cast<void**>(&d->final_norm), size_t(c.hidden) * 4, "final norm");
     if (!rc && !d->embed) rc = dalloc(*d, reinterpret_cast<void**>(&d->embed), size_t(c.vocab) * c.hidden * 4, "embedding");
     if (rc) return rc;
-    hipError_t e = hipSuccess;
-    if (final_norm) e = hipMemcpy(d->final_norm, final_norm, size_t(c.hidden) * 4, hipMemcpyHostToDevice);
+    hipError_t e = hipStreamSynchronize(d->stream);
+    if (e == hipSuccess && final_norm) e = hipMemcpy(d->final_norm, final_norm, size_t(c.hidden) * 4, hipMemcpyHostToDevice);
     if (e == hipSuccess) e = hipMemcpy(d->embed, embedding, size_t(c.vocab) * c.hidden * 4, hipMemcpyHostToDevice);
     if (e != hipSuccess) return rt_hip_fail(e, "wv_decoder_set_output: copy");
+    d->has_final_norm = final_norm != nullptr;  // NULL: no final norm (forward.go:80-86)
     d->lm = b;
     d->lm_set = true;
     return WV_OK;

@@ -5,17 +5,17 @@
 //     including blocks that straddle rows): the reference layout as uploaded
 //     (LAYOUT_RAW), every format; semantics follow the reference decoders
 //     (quant/*.go forEach* / unpack*), accumulating in f32.
-//   * the row-interleaved fast path for Q4_K/Q6_K/Q8_0/Q4_0 lives in
-//     gemv_rpl.hip;
-//   * k_ternary_i8: the DTypeTernary int8 path (layers/dense/simd.go:130-147):
-//     activations absmax-quantized to int8 in LDS, codes unpacked to bytes in
-//     registers and multiplied with packed-dot v_dot4_i32_i8; exact int32.
+//   * the row-interleaved fast path lives in gemv_rpl.hip, the weights.Store
+//     DTypes (int8 path, f32 and f64 products) in native.hip;
+//   * k_bias_act: Dense's bias + activation epilogue for the layouts whose
+//     GEMV has no fused one.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
 #include <cstdint>
 #include <cstdlib>
 
+#include "epilogue.h"
 #include "wave_ops.h"
 #include "wv_internal.h"
 
@@ -23,24 +23,6 @@ namespace wv {
 namespace {
 
 constexpr int kWave = 64;
-
-// WV_RAW16_KW=1|2|4 fixes the K parts of the run-vectorized kernel (tuning sweeps).
-int raw16_kw() {
-    static const int v = [] {
-        const char* e = std::getenv("WV_RAW16_KW");
-        return e && *e ? std::atoi(e) : 0;
-    }();
-    return v == 1 || v == 2 || v == 4 ? v : 0;
-}
-
-// WV_RAW16=0 forces the per-weight decoder on the reference layout (for comparisons).
-bool raw16_off() {
-    static const bool off = [] {
-        const char* v = std::getenv("WV_RAW16");
-        return v && v[0] == '0';
-    }();
-    return off;
-}
 
 __device__ __forceinline__ float wave_sum(float v) { return wave_total(v); }
 __device__ __forceinline__ int wave_sum_i(int v) { return wave_total_i(v); }
@@ -577,187 +559,14 @@ __global__ void __launch_bounds__(64) k_gemvt_reduce(const float* __restrict__ p
     gx[int64_t(b) * cols + c] += s;
 }
 
-// ---------------------------------------------------------------------------
-// DTypeTernary int8 path
-// ---------------------------------------------------------------------------
-
-// One block computes rows [blockIdx.x*rows_per_block, ...) for batch row blockIdx.y.
-// LDS: xq permuted so that byte b of word (g*4+k) is xq[16g + 4b + k], matching
-// the byte spread (codes >> 2k) & 0x03030303 of a 16-code dword.
-__global__ void __launch_bounds__(256) k_ternary_i8(const uint8_t* __restrict__ codes, float scale, int rows, int K,
-                                                   const float* __restrict__ x, float* __restrict__ y,
-                                                   int32_t* __restrict__ acc_out, float* __restrict__ act_out,
-                                                   int rows_per_block) {
-    extern __shared__ uint32_t lds[];  // K/4 words of permuted xq (K%16==0) or K plain bytes
-    __shared__ float red_f[4];
-    __shared__ int red_i[4];
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int b = blockIdx.y;
-    const float* xb = x + int64_t(b) * K;
-
-    // quantizeActsI8 (layers/dense/simd.go:526-549): absmax, f32 scale, round half away.
-    float m = 0.f;
-    for (int j = tid; j < K; j += 256) m = fmaxf(m, fabsf(xb[j]));
-    m = wave_max(m);
-    if (lane == 0) red_f[wave] = m;
-    __syncthreads();
-    m = fmaxf(fmaxf(red_f[0], red_f[1]), fmaxf(red_f[2], red_f[3]));
-    float act = m / 127.0f;
-    if (act == 0.0f) act = 1.0f;
-    const bool fast = (K % 64) == 0;
-    uint8_t* l8 = reinterpret_cast<uint8_t*>(lds);
-    int sq = 0;
-    for (int j = tid; j < K; j += 256) {
-        float t = xb[j] / act;
-        int q = int(roundf(t));
-        q = q > 127 ? 127 : (q < -128 ? -128 : q);
-        sq += q;
-        const int pos = fast ? ((j >> 4) * 16 + (j & 3) * 4 + ((j & 15) >> 2)) : j;
-        l8[pos] = uint8_t(int8_t(q));
-    }
-    sq = wave_sum_i(sq);
-    if (lane == 0) red_i[wave] = sq;
-    __syncthreads();
-    sq = red_i[0] + red_i[1] + red_i[2] + red_i[3];
-    if (act_out && blockIdx.x == 0 && tid == 0) act_out[b] = act;
-
-    const int r0 = blockIdx.x * rows_per_block;
-    const int r1 = min(rows, r0 + rows_per_block);
-    const int64_t row_bytes = K / 4;
-    for (int r = r0 + wave; r < r1; r += 4) {
-        int acc = 0;
-        if (fast) {
-            const uint4* rowp = reinterpret_cast<const uint4*>(codes + int64_t(r) * row_bytes);
-            for (int c = lane; c < K / 64; c += kWave) {
-                const uint4 v = rowp[c];
-                const uint32_t wd[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-                for (int d = 0; d < 4; ++d) {
-                    const uint32_t* xw = lds + (c * 4 + d) * 4;
-#pragma unroll
-                    for (int k = 0; k < 4; ++k)
-                        acc = __builtin_amdgcn_sdot4(int((wd[d] >> (2 * k)) & 0x03030303u), int(xw[k]), acc, false);
-                }
-            }
-            acc = wave_sum_i(acc) - sq;  // codes are t+1: sum (t+1)*xq - sum xq
-        } else {
-            const int64_t base = int64_t(r) * K;
-            for (int j = lane; j < K; j += kWave) {
-                const int64_t i = base + j;
-                const int t = int((codes[i >> 2] >> ((i & 3) * 2)) & 3u) - 1;
-                acc += t * int(int8_t(l8[j]));
-            }
-            acc = wave_sum_i(acc);
-        }
-        if (lane == 0) {
-            if (acc_out) acc_out[int64_t(b) * rows + r] = acc;
-            if (y) y[int64_t(b) * rows + r] = float(acc) * act * scale;  // simd.go:142
-        }
-    }
-}
-
-// DTypeTernary int8 GEMV for K % 64 == 0 and K <= 8192 (layers/dense/
-// simd.go:130-147 with quantizeActsI8, simd.go:526-549). A block of four
-// waves covers 4*RW rows of one batch row:
-//  * x is requested first (NX float4 per thread), then the block's codes (NC
-//    uint4 per lane per row), so the activation quantization overlaps the
-//    codes' arrival;
-//  * absmax over x, act = max/127 (1 if 0), q = round-half-away(f32(x / act))
-//    clamped to [-128, 127], with the exact f32 division of the reference;
-//  * xq is stored in LDS laid out for the dot: dword (d*C + c)*4 + k, C = K/64,
-//    holds in byte b the value xq[64c + 16d + 4b + k], which is what byte b of
-//    code word d of uint4 c meets after >> 2k & 0x03030303. Lane c reads its
-//    four uint4 (d = 0..3) once for all its rows, and consecutive lanes read
-//    consecutive uint4 (no bank conflicts). A thread quantizes four
-//    consecutive x (byte b of four dwords k); a DPP quad transpose gives each
-//    lane of the quad one whole dword to store;
-//  * codes are t+1 in {0,1,2}: sum (t+1)*xq - sum xq on v_dot4_i32_i8, exact.
-template <int NC, int NX, int RW>
-__global__ void __launch_bounds__(256) k_ternary_i8v(const uint8_t* __restrict__ codes, float scale, int rows, int K,
-                                                    const float* __restrict__ x, float* __restrict__ y,
-                                                    int32_t* __restrict__ acc_out, float* __restrict__ act_out) {
-    extern __shared__ uint32_t lds[];  // K/4 dwords of xq in the dot layout
-    __shared__ float red_f[4];
-    __shared__ int red_i[4];
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int b = blockIdx.y;
-    const int r0 = blockIdx.x * (4 * RW) + wave * RW;
-    const int c64 = K / 64, k4 = K / 4;
-    const float4* xb = reinterpret_cast<const float4*>(x + int64_t(b) * K);
-    float4 xv[NX];
-#pragma unroll
-    for (int n = 0; n < NX; ++n) xv[n] = xb[min(tid + 256 * n, k4 - 1)];
-    __builtin_amdgcn_sched_barrier(0);  // keep the x requests ahead of the codes
-    uint4 cv[RW][NC];
-#pragma unroll
-    for (int rw = 0; rw < RW; ++rw) {
-        const uint4* rowp = reinterpret_cast<const uint4*>(codes + int64_t(min(r0 + rw, rows - 1)) * k4);
-#pragma unroll
-        for (int c = 0; c < NC; ++c) cv[rw][c] = rowp[min(lane + 64 * c, c64 - 1)];
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    float m = 0.f;
-#pragma unroll
-    for (int n = 0; n < NX; ++n) {
-        if (tid + 256 * n >= k4) xv[n] = make_float4(0.f, 0.f, 0.f, 0.f);
-        m = fmaxf(m, fmaxf(fmaxf(fabsf(xv[n].x), fabsf(xv[n].y)), fmaxf(fabsf(xv[n].z), fabsf(xv[n].w))));
-    }
-    m = wave_max(m);
-    if (lane == 0) red_f[wave] = m;
-    __syncthreads();
-    m = fmaxf(fmaxf(red_f[0], red_f[1]), fmaxf(red_f[2], red_f[3]));
-    float act = m / 127.0f;
-    if (act == 0.0f) act = 1.0f;
-    int sq = 0;
-    const int qd = lane & 3;
-#pragma unroll
-    for (int n = 0; n < NX; ++n) {
-        const int i = tid + 256 * n;  // float4 index: x[4i + e] = xq[64c + 16d + 4b + k], c = i>>4, d = (i>>2)&3, b = i&3, k = e
-        const float e4[4] = {xv[n].x, xv[n].y, xv[n].z, xv[n].w};
-        uint32_t pk = 0;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            int q = int(roundf(e4[e] / act));
-            q = q > 127 ? 127 : (q < -128 ? -128 : q);
-            sq += q;
-            pk |= (uint32_t(q) & 0xffu) << (8 * e);
-        }
-        const uint32_t dw = quad_byte_transpose(pk, qd);  // bytes b = 0..3 of dword k = qd
-        if (i < k4) lds[(((i >> 2) & 3) * c64 + (i >> 4)) * 4 + qd] = dw;
-    }
-    sq = wave_sum_i(sq);
-    if (lane == 0) red_i[wave] = sq;
-    __syncthreads();
-    sq = red_i[0] + red_i[1] + red_i[2] + red_i[3];
-    if (act_out && blockIdx.x == 0 && tid == 0) act_out[b] = act;
-    uint4 xw[NC][4];
-#pragma unroll
-    for (int c = 0; c < NC; ++c)
-#pragma unroll
-        for (int d = 0; d < 4; ++d) xw[c][d] = reinterpret_cast<const uint4*>(lds)[d * c64 + min(lane + 64 * c, c64 - 1)];
-#pragma unroll
-    for (int rw = 0; rw < RW; ++rw) {
-        int acc = 0;
-#pragma unroll
-        for (int c = 0; c < NC; ++c) {
-            if (lane + 64 * c < c64) {
-                const uint32_t wd[4] = {cv[rw][c].x, cv[rw][c].y, cv[rw][c].z, cv[rw][c].w};
-#pragma unroll
-                for (int d = 0; d < 4; ++d) {
-                    const uint32_t xk[4] = {xw[c][d].x, xw[c][d].y, xw[c][d].z, xw[c][d].w};
-#pragma unroll
-                    for (int k = 0; k < 4; ++k)
-                        acc = __builtin_amdgcn_sdot4(int((wd[d] >> (2 * k)) & 0x03030303u), int(xk[k]), acc, false);
-                }
-            }
-        }
-        acc = wave_sum_i(acc) - sq;  // codes are t+1: sum (t+1)*xq - sum xq
-        const int r = r0 + rw;
-        if (lane == 0 && r < rows) {
-            if (acc_out) acc_out[int64_t(b) * rows + r] = acc;
-            if (y) y[int64_t(b) * rows + r] = float(acc) * act * scale;  // simd.go:142
-        }
-    }
+// applyBiasAct (layers/dense/dense.go:145-167) over y[batch][rows]: pre =
+// f32(y + bias) written to `pre`, post = f32(act(f64(pre))) to `post`.
+__global__ void __launch_bounds__(256) k_bias_act(const float* __restrict__ y, float* __restrict__ pre,
+                                                  float* __restrict__ post, const double* __restrict__ bias, int act,
+                                                  int64_t rows, int64_t n) {
+    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (i >= n) return;
+    store_bias_act(pre, post, i, y[i], bias, i % rows, act);
 }
 
 RawArgs raw_args(const DevBlob& b) {
@@ -780,7 +589,7 @@ RawArgs raw_args(const DevBlob& b) {
 // format's standard IQ bit width and scale group (Meta may override them).
 template <int F>
 bool raw16_ok(const DevBlob& b) {
-    if (b.cols % 256 != 0 || raw16_off()) return false;
+    if (b.cols % 256 != 0) return false;
     if constexpr (F >= FMT_IQ1_S && F <= FMT_IQ4_XS) {
         IQSpec sp;
         iq_spec(F, sp);
@@ -801,8 +610,7 @@ int launch_raw(const DevBlob& b, const float* x, float* y, int batch, hipStream_
         // about 4 waves per SIMD, never more parts than the row has runs of 64;
         // IQ4_NL's 4-run ring already holds as many registers as a SIMD has.
         const int64_t quads = (b.rows + 3) / 4, nsg = b.cols / 16;
-        int kw = raw16_kw();
-        if (kw <= 0) kw = U > 1 || quads >= 4096 ? 1 : (quads * 2 >= 4096 ? 2 : 4);
+        int kw = U > 1 || quads >= 4096 ? 1 : (quads * 2 >= 4096 ? 2 : 4);
         while (kw > 1 && nsg < 64 * kw) kw /= 2;
         const dim3 g(unsigned((quads * kw + 3) / 4), unsigned(batch));
         if (kw == 4)
@@ -818,19 +626,13 @@ int launch_raw(const DevBlob& b, const float* x, float* y, int batch, hipStream_
     return int(hipGetLastError());
 }
 
-// Row slices of the run-vectorized MatVecT: about rawt_blocks() (1024) blocks over
-// the column tiles, at most 128 slices and at least 64 rows per slice (so
-// the partials stay small next to the weights).
-int rawt_blocks() {
-    static const int v = [] {
-        const char* e = std::getenv("WV_RAWT_BLOCKS");
-        return e && *e ? std::atoi(e) : 1024;
-    }();
-    return v;
-}
+// Row slices of the run-vectorized MatVecT: about kRawTBlocks blocks over the
+// column tiles (measured on MI355X), at most 128 slices and at least 64 rows
+// per slice (so the partials stay small next to the weights).
+constexpr int kRawTBlocks = 1024;
 int raw_t16_slices(const DevBlob& b) {
     const int64_t tiles = (b.cols / 16 + 63) / 64;
-    const int64_t want = (rawt_blocks() + tiles - 1) / tiles;
+    const int64_t want = (kRawTBlocks + tiles - 1) / tiles;
     return int(std::max<int64_t>(1, std::min<int64_t>({want, 128, b.rows / 64})));
 }
 // Row splits of the per-weight MatVecT.
@@ -911,63 +713,44 @@ RawTFn pick_raw_t(int fmt) {
     }
 }
 
-template <int NC, int NX>
-void launch_ternary_v(const DevBlob& b, const float* x, float* y, int32_t* acc, float* act, int batch, hipStream_t s) {
-    const int rows = int(b.rows), K = int(b.cols);
-    // 8 rows per wave while that still leaves ~200 blocks (measured on 2560/4096/6912 shapes)
-    if constexpr (NC == 1) {
-        if ((rows + 31) / 32 >= 192) {
-            hipLaunchKernelGGL((k_ternary_i8v<NC, NX, 8>), dim3(unsigned((rows + 31) / 32), unsigned(batch)), dim3(256),
-                               size_t(K), s, b.codes, b.tensor_scale, rows, K, x, y, acc, act);
-            return;
-        }
-    }
-    hipLaunchKernelGGL((k_ternary_i8v<NC, NX, 4>), dim3(unsigned((rows + 15) / 16), unsigned(batch)), dim3(256), size_t(K),
-                       s, b.codes, b.tensor_scale, rows, K, x, y, acc, act);
-}
-
-int launch_ternary(const DevBlob& b, const float* x, float* y, int32_t* acc, float* act, int batch, hipStream_t s) {
-    const int rows = int(b.rows), K = int(b.cols);
-    if (K % 64 == 0 && K <= 8192) {  // NC = ceil(K/4096) uint4 per lane per row, NX = ceil(K/1024) float4 of x
-        const int nc = (K + 4095) / 4096, nx = (K + 1023) / 1024;
-        if (nc == 1) {
-            switch (nx) {
-            case 1: launch_ternary_v<1, 1>(b, x, y, acc, act, batch, s); break;
-            case 2: launch_ternary_v<1, 2>(b, x, y, acc, act, batch, s); break;
-            case 3: launch_ternary_v<1, 3>(b, x, y, acc, act, batch, s); break;
-            default: launch_ternary_v<1, 4>(b, x, y, acc, act, batch, s); break;
-            }
-        } else {
-            switch (nx) {
-            case 5: launch_ternary_v<2, 5>(b, x, y, acc, act, batch, s); break;
-            case 6: launch_ternary_v<2, 6>(b, x, y, acc, act, batch, s); break;
-            case 7: launch_ternary_v<2, 7>(b, x, y, acc, act, batch, s); break;
-            default: launch_ternary_v<2, 8>(b, x, y, acc, act, batch, s); break;
-            }
-        }
-        return int(hipGetLastError());
-    }
-    const int rpb = 16;
-    dim3 grid(unsigned((rows + rpb - 1) / rpb), unsigned(batch));
-    const size_t lds = size_t((K + 3) / 4) * 4;
-    hipLaunchKernelGGL(k_ternary_i8, grid, dim3(256), lds, s, b.codes, b.tensor_scale, rows, K, x, y, acc, act, rpb);
-    return int(hipGetLastError());
-}
-
 }  // namespace
 
-int launch_matvec(const DevBlob& b, const float* d_x, float* d_y, int batch, void* stream) {
+size_t matvec_scratch_floats(const DevBlob& b, int batch) { return rpl_scratch_floats(b, batch); }
+
+int launch_matvec(const DevBlob& b, const float* d_x, float* d_y, int batch, void* stream, float* d_scratch,
+                  const BiasAct* ba) {
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (b.rows == 0 || batch == 0) return 0;
-    switch (b.layout) {
-    case LAYOUT_RPL: return launch_rpl(b, d_x, d_y, batch, s);
-    case LAYOUT_TERNARY_I8: return launch_ternary(b, d_x, d_y, nullptr, nullptr, batch, s);
-    default: {
+    const bool epi = ba && ba->post;
+    if (b.layout == LAYOUT_RPL) {  // the epilogue is fused into the GEMV's store
+        RplExtra ex;
+        ex.partial = d_scratch;
+        if (epi) {
+            ex.bias = ba->bias;
+            ex.act = ba->act;
+            ex.post = ba->post;
+        }
+        return launch_rpl_ex(b, d_x, d_y, batch, s, ex);
+    }
+    int e = 0;
+    if (b.layout == LAYOUT_NARROW || b.layout == LAYOUT_F32) {
+        e = launch_native_fwd(b, d_x, d_y, batch, s);
+    } else {
         RawFn f = pick_raw(b.fmt);
         if (!f) return int(hipErrorInvalidValue);
-        return f(b, d_x, d_y, batch, s);
+        e = f(b, d_x, d_y, batch, s);
     }
-    }
+    if (e || !epi) return e;
+    return launch_bias_act(d_y, d_y, ba->post, ba->bias, ba->act, b.rows, batch, s);
+}
+
+int launch_bias_act(const float* d_y, float* d_pre, float* d_post, const double* d_bias, int act, int64_t rows,
+                    int batch, void* stream) {
+    const int64_t n = rows * int64_t(batch);
+    if (n == 0) return 0;
+    hipLaunchKernelGGL(k_bias_act, dim3(unsigned((n + 255) / 256)), dim3(256), 0, static_cast<hipStream_t>(stream), d_y,
+                       d_pre, d_post, d_bias, act, rows, n);
+    return int(hipGetLastError());
 }
 
 void launch_gemvt_reduce(const float* part, float* gx, int64_t cols, int nsplit, int batch, void* stream) {
@@ -976,7 +759,9 @@ void launch_gemvt_reduce(const float* part, float* gx, int64_t cols, int nsplit,
 }
 
 size_t matvec_t_scratch_floats(const DevBlob& b, int batch) {
-    if (b.layout == LAYOUT_RPL) return 0;
+    if (batch <= 0) return 0;
+    if (b.layout == LAYOUT_RPL) return rpl_t_scratch_floats(b.rpl, batch);
+    if (b.layout == LAYOUT_NARROW || b.layout == LAYOUT_F32) return native_t_scratch_floats(b, batch);
     const int64_t n = std::max(raw_t_splits(b), raw_t16_slices(b));  // covers either kernel
     return size_t(n) * size_t(b.cols) * size_t(batch);
 }
@@ -984,16 +769,13 @@ size_t matvec_t_scratch_floats(const DevBlob& b, int batch) {
 int launch_matvec_t(const DevBlob& b, const float* d_gy, float* d_gx, int batch, void* stream, float* d_scratch) {
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (b.rows == 0 || batch == 0) return 0;
-    if (b.layout == LAYOUT_RPL) return launch_rpl_matvec_t(b, d_gy, d_gx, batch, stream);
+    if (b.layout == LAYOUT_RPL) return launch_rpl_matvec_t(b, d_gy, d_gx, batch, stream, d_scratch);
+    if (b.layout == LAYOUT_NARROW || b.layout == LAYOUT_F32)
+        return launch_native_t(b, d_gy, d_gx, batch, stream, reinterpret_cast<double*>(d_scratch));
     if (b.layout != LAYOUT_RAW) return int(hipErrorInvalidValue);
     RawTFn f = pick_raw_t(b.fmt);
-    if (!f) return int(hipErrorInvalidValue);
+    if (!f || !d_scratch) return int(hipErrorInvalidValue);
     return f(b, d_gy, d_gx, batch, s, d_scratch);
-}
-
-int launch_ternary_acc(const DevBlob& b, const float* d_x, int32_t* d_acc, float* d_act, int batch, void* stream) {
-    if (b.layout != LAYOUT_TERNARY_I8) return int(hipErrorInvalidValue);
-    return launch_ternary(b, d_x, nullptr, d_acc, d_act, batch, static_cast<hipStream_t>(stream));
 }
 
 }  // namespace wv

@@ -28,6 +28,7 @@
 #include <cstdint>
 #include <cstdlib>
 
+#include "epilogue.h"
 #include "wave_ops.h"
 #include "wv_internal.h"
 
@@ -535,7 +536,10 @@ __device__ __forceinline__ void finish_rows(const RplArgs& a, float* y, int b, i
         return;
     }
     float v = 0.f;
-    if (valid && row < a.rows) v = store_y(a, y, int64_t(b) * a.rows + row, s);
+    if (valid && row < a.rows) {
+        const int64_t idx = int64_t(b) * a.rows + row;
+        v = a.post ? store_bias_act(y, a.post, idx, s, a.bias, row, a.act) : store_y(a, y, idx, s);
+    }
     if (a.ss_out) {
         const float q = row_sum16(v * v);
         if (valid && (lane & 15) == 0) a.ss_out[int64_t(b) * a.rg_count * 4 + row / 16] = q;
@@ -813,27 +817,8 @@ __global__ void __launch_bounds__(64) k_rpl_ksum(RplArgs a, float* __restrict__ 
     finish_rows(a, y, b, row, true, lane, s);
 }
 
-// Launch-geometry overrides for tuning sweeps, read once per process.
-int env_int(const char* name, int dflt) {
-    const char* v = std::getenv(name);
-    return v && *v ? std::atoi(v) : dflt;
-}
-int min_blocks() {
-    static const int v = env_int("WV_RPL_MIN_BLOCKS", 200);
-    return v;
-}
-int forced_waves() {
-    static const int v = env_int("WV_RPL_WAVES", 0);
-    return v;
-}
-int int_x() {
-    static const int v = env_int("WV_RPL_INT", 1);
-    return v;
-}
-int lds_floor() {
-    static const int v = env_int("WV_RPL_LDS_MIN", 0);
-    return v;
-}
+// Blocks a K-split plan aims for (measured on MI355X: fewer leave CUs idle).
+constexpr int kRplMinBlocks = 200;
 
 // Launch plan of the forward kernel: lanes per row L, super-blocks per wave
 // S, waves per block W and K split (measured on MI355X):
@@ -858,8 +843,7 @@ struct RplPlan {
 RplPlan rpl_plan(const DevBlob& bl, int max_s = 4) {
     const RplArgs& a = bl.rpl;
     RplPlan p{1, 1, 1, 1};
-    static const int fl = env_int("WV_RPL_L", 0), fs0 = env_int("WV_RPL_S", 0);
-    const int fs = std::min(fs0, max_s);
+    const int max_split = std::max(1, (a.nsb + 3) / 4);  // K-split partials per row at most
     if (a.nsb <= 16) {
         while (p.L < 4 && int64_t(a.rg_count) * p.L < 180) p.L *= 2;
         if (p.L == 4 && a.nsb >= 2) p.S = 2;
@@ -871,11 +855,11 @@ RplPlan rpl_plan(const DevBlob& bl, int max_s = 4) {
         p.S = 4;
         p.W = w4;
     } else {
-        const int target = min_blocks();
+        const int target = kRplMinBlocks;
         int best = -1;
         for (int w = 16; w >= 4; --w) {
             const int k = (a.nsb + w - 1) / w;
-            if (k > bl.rpl_max_split) continue;
+            if (k > max_split) continue;
             const bool fills = int64_t(a.rg_count) * k >= target;
             const int idle = k * w - a.nsb;
             const int score = (fills ? 1 << 20 : 0) + (1 << 10) * (64 - std::min(idle, 63)) + w;
@@ -885,18 +869,10 @@ RplPlan rpl_plan(const DevBlob& bl, int max_s = 4) {
             }
         }
     }
-    if (fl == 1 || fl == 2 || fl == 4) p.L = fl;
-    if (fs == 1 || fs == 2 || fs == 4) p.S = fs;
     const int waves = (a.nsb + p.S - 1) / p.S;
-    if (a.nsb <= 16 || fl || fs) p.W = std::min(16, waves);
-    const int fw = forced_waves();
-    if (fw > 0 && fw <= 16) p.W = fw;
+    if (a.nsb <= 16) p.W = std::min(16, waves);
     p.W = std::min(p.W, waves);
     p.ksplit = (waves + p.W - 1) / p.W;
-    if (p.ksplit > bl.rpl_max_split) {  // overrides beyond the scratch: fall back to the widest blocks
-        p.W = std::min(16, waves);
-        p.ksplit = (waves + p.W - 1) / p.W;
-    }
     return p;
 }
 
@@ -920,18 +896,26 @@ int launch_rpl_t(const DevBlob& bl, const float* x, float* y, int batch, hipStre
     a.nrm_n = ex.nrm_n;
     a.nrm_eps = ex.nrm_eps;
     a.ss_out = ex.ss_out;
+    a.bias = ex.bias;
+    a.act = ex.act;
+    a.post = ex.post;
+    a.partial = ex.partial;
     const RplPlan p = rpl_plan(bl, P::kWords2 ? 2 : 4);
     if (P::kWords2 && p.S > 2) return int(hipErrorInvalidValue);  // not reachable: the plan caps S
+    if (p.ksplit > 1 && !a.partial) return int(hipErrorInvalidValue);  // the caller owes the split scratch
     a.ksplit = p.ksplit;
-    size_t lds = size_t(p.W) * (p.S * (256 + 16) + 64) * sizeof(float);  // x slices + partial row sums
-    lds = std::max(lds, size_t(lds_floor()));
-    for (int b0 = 0; b0 < batch; b0 += bl.rpl_max_batch) {
-        const int nb = std::min(bl.rpl_max_batch, batch - b0);
-        dim3 grid(unsigned(a.rg_count * p.L), unsigned(p.ksplit), unsigned(p.ksplit > 1 ? nb : batch - b0));
+    const size_t lds = size_t(p.W) * (p.S * (256 + 16) + 64) * sizeof(float);  // x slices + partial row sums
+    // A K-split launch carries kRplFwdBatch batch rows (the scratch holds their
+    // partials; chunks run in stream order and reuse it); otherwise one launch.
+    const int chunk = p.ksplit > 1 ? kRplFwdBatch : std::min(batch, 65535);
+    for (int b0 = 0; b0 < batch; b0 += chunk) {
+        const int nb = std::min(chunk, batch - b0);
+        dim3 grid(unsigned(a.rg_count * p.L), unsigned(p.ksplit), unsigned(nb));
         RplArgs ab = a;
         if (aux) ab.aux = aux + int64_t(b0) * a.rows;
         if (ab.nrm_ss) ab.nrm_ss += int64_t(b0) * a.nrm_n;
         if (ab.ss_out) ab.ss_out += int64_t(b0) * a.rg_count * 4;
+        if (ab.post) ab.post += int64_t(b0) * a.rows;
         const int64_t ystride = mode == RPL_SWIGLU ? a.rows / 2 : a.rows;
         const float* xb = x + int64_t(b0) * a.nsb * 256;
         float* yb = y + int64_t(b0) * ystride;
@@ -946,8 +930,7 @@ int launch_rpl_t(const DevBlob& bl, const float* x, float* y, int batch, hipStre
         case 34: launch_rpl_ls<P, 4, 2>(ab, p, grid, lds, s, xb, yb); break;
         default: launch_rpl_ls<P, 4, 4>(ab, p, grid, lds, s, xb, yb); break;
         }
-        if (p.ksplit == 1) break;  // one launch covers every batch row
-        hipLaunchKernelGGL(k_rpl_ksum, dim3(unsigned(a.rg_count), unsigned(nb)), dim3(64), 0, s, ab, yb);
+        if (p.ksplit > 1) hipLaunchKernelGGL(k_rpl_ksum, dim3(unsigned(a.rg_count), unsigned(nb)), dim3(64), 0, s, ab, yb);
     }
     return int(hipGetLastError());
 }
@@ -1308,16 +1291,13 @@ __global__ void __launch_bounds__(256) k_gemvt_rpl(RplArgs a, const float* __res
     part[(int64_t(b) * nslices + slice) * cols + col] = total;
 }
 
-// Row-group slices for `batch` rows: about 512 blocks; each slice takes GP
-// (1, 2, 4 or 8) row groups.
-int rplt_blocks() {
-    static const int v = env_int("WV_RPLT_BLOCKS", 512);
-    return v;
-}
+// Row-group slices for `batch` rows: about kRplTBlocks blocks (measured on
+// MI355X); each slice takes GP (1, 2, 4 or 8) row groups.
+constexpr int kRplTBlocks = 512;
 
 void rpl_t_plan(const RplArgs& a, int batch, int& slices, int& g_per) {
     const int64_t per_slice = int64_t(a.nsb) * std::max(1, batch);
-    const int64_t target = rplt_blocks();
+    const int64_t target = kRplTBlocks;
     const int64_t s = std::min<int64_t>(a.rg_count, std::max<int64_t>(1, (target + per_slice - 1) / per_slice));
     const int64_t need = (a.rg_count + s - 1) / s;
     g_per = need <= 1 ? 1 : need <= 2 ? 2 : need <= 4 ? 4 : 8;
@@ -1325,7 +1305,7 @@ void rpl_t_plan(const RplArgs& a, int batch, int& slices, int& g_per) {
 }
 
 template <class P>
-int launch_rpl_tr(const DevBlob& bl, const float* gy, float* gx, int batch, hipStream_t s) {
+int launch_rpl_tr(const DevBlob& bl, const float* gy, float* gx, int batch, hipStream_t s, float* part) {
     const RplArgs& a = bl.rpl;
     const int64_t cols = int64_t(a.nsb) * 256;
     for (int b0 = 0; b0 < batch; b0 += kRplTMaxBatch) {
@@ -1333,10 +1313,10 @@ int launch_rpl_tr(const DevBlob& bl, const float* gy, float* gx, int batch, hipS
         int slices = 1, g_per = 1;
         rpl_t_plan(a, nb, slices, g_per);
         auto kern = g_per == 1 ? k_gemvt_rpl<P, 1> : g_per == 2 ? k_gemvt_rpl<P, 2> : g_per == 4 ? k_gemvt_rpl<P, 4> : k_gemvt_rpl<P, 8>;
+        if (slices > 1 && !part) return int(hipErrorInvalidValue);  // the caller owes the slice scratch
         dim3 grid(unsigned(a.nsb), unsigned(slices), unsigned(nb));
-        hipLaunchKernelGGL(kern, grid, dim3(256), 0, s, a, gy + int64_t(b0) * a.rows, gx + int64_t(b0) * cols,
-                           bl.rpl_t_partial);
-        if (slices > 1) launch_gemvt_reduce(bl.rpl_t_partial, gx + int64_t(b0) * cols, cols, slices, nb, s);
+        hipLaunchKernelGGL(kern, grid, dim3(256), 0, s, a, gy + int64_t(b0) * a.rows, gx + int64_t(b0) * cols, part);
+        if (slices > 1) launch_gemvt_reduce(part, gx + int64_t(b0) * cols, cols, slices, nb, s);
     }
     return int(hipGetLastError());
 }
@@ -1347,7 +1327,7 @@ int launch_rpl_ex(const DevBlob& b, const float* d_x, float* d_y, int batch, voi
     hipStream_t s = static_cast<hipStream_t>(stream);
     switch (b.fmt) {
     case FMT_Q4_K:
-        return int_x() ? launch_rpl_t<RplQ4KI>(b, d_x, d_y, batch, s, ex) : launch_rpl_t<RplQ4K>(b, d_x, d_y, batch, s, ex);
+        return launch_rpl_t<RplQ4KI>(b, d_x, d_y, batch, s, ex);
     case FMT_Q2_K: return launch_rpl_t<RplKxI<2>>(b, d_x, d_y, batch, s, ex);
     case FMT_Q3_K: return launch_rpl_t<RplKxI<3>>(b, d_x, d_y, batch, s, ex);
     case FMT_Q5_K: return launch_rpl_t<RplKxI<5>>(b, d_x, d_y, batch, s, ex);
@@ -1370,10 +1350,12 @@ int launch_rpl_ex(const DevBlob& b, const float* d_x, float* d_y, int batch, voi
     }
 }
 
-int launch_rpl(const DevBlob& b, const float* d_x, float* d_y, int batch, void* stream, int mode, const float* aux) {
+int launch_rpl(const DevBlob& b, const float* d_x, float* d_y, int batch, void* stream, int mode, const float* aux,
+               float* d_scratch) {
     RplExtra ex;
     ex.mode = mode;
     ex.aux = aux;
+    ex.partial = d_scratch;
     return launch_rpl_ex(b, d_x, d_y, batch, stream, ex);
 }
 
@@ -1431,9 +1413,9 @@ __global__ void __launch_bounds__(256) k_rpl_pairs(uint8_t* __restrict__ dst, co
 }
 
 struct FusedLayout {
-    size_t codes, hi, meta, dd, part, total, weights;
+    size_t codes, hi, meta, dd, total;
 };
-FusedLayout fused_layout(const RplItems& it, int64_t rg, int64_t nsb, int max_batch, int max_split) {
+FusedLayout fused_layout(const RplItems& it, int64_t rg, int64_t nsb) {
     FusedLayout f{};
     auto add = [&](size_t n) {
         const size_t off = (f.total + 255) & ~size_t(255);
@@ -1445,13 +1427,10 @@ FusedLayout fused_layout(const RplItems& it, int64_t rg, int64_t nsb, int max_ba
     f.hi = it.hb ? add(per * 8 * it.hb) : 0;
     f.meta = add(per * it.mb);
     f.dd = it.db ? add(per * it.db) : 0;
-    f.weights = f.total;
-    f.part = add(size_t(max_batch) * max_split * rg * 64 * sizeof(float));
     return f;
 }
 
-int finish_fused(const DevBlob& proto, int64_t rows, int64_t rg, const FusedLayout& f, uint8_t* base, DevBlob& out,
-                 hipStream_t s) {
+void finish_fused(const DevBlob& proto, int64_t rows, int64_t rg, const FusedLayout& f, uint8_t* base, DevBlob& out) {
     out = DevBlob{};
     out.fmt = proto.fmt;
     out.iq_bits = proto.iq_bits;
@@ -1462,20 +1441,17 @@ int finish_fused(const DevBlob& proto, int64_t rows, int64_t rg, const FusedLayo
     out.layout = LAYOUT_RPL;
     out.device = proto.device;
     out.base = base;
-    out.device_bytes = f.weights;
-    out.rpl_max_batch = 8;
-    out.rpl_max_split = int(std::max<int64_t>(1, (proto.rpl.nsb + 3) / 4));
+    out.device_bytes = f.total;
     RplArgs& r = out.rpl;
     r.codes = base + f.codes;
     r.hi = f.hi ? base + f.hi : nullptr;
     r.meta = base + f.meta;
     r.dd = f.dd ? reinterpret_cast<const float2_t*>(base + f.dd) : nullptr;
-    r.partial = reinterpret_cast<float*>(base + f.part);
+    r.partial = nullptr;
     r.rows = int(rows);
     r.nsb = proto.rpl.nsb;
     r.rg_count = int(rg);
     r.ksplit = 1;
-    return int(hipMemsetAsync(base + f.part, 0, f.total - f.part, s));
 }
 
 }  // namespace
@@ -1494,7 +1470,7 @@ int rpl_fuse_rows(const DevBlob* parts, int n, DevBlob& out, void* stream) {
         rows += b.rows;
     }
     const int64_t nsb = parts[0].rpl.nsb;
-    const FusedLayout f = fused_layout(it, rg, nsb, 8, int(std::max<int64_t>(1, (nsb + 3) / 4)));
+    const FusedLayout f = fused_layout(it, rg, nsb);
     void* base = nullptr;
     hipError_t e = hipMalloc(&base, f.total);
     if (e != hipSuccess) return int(e);
@@ -1516,7 +1492,7 @@ int rpl_fuse_rows(const DevBlob* parts, int n, DevBlob& out, void* stream) {
             e = hipMemcpyAsync(b8 + f.dd + off * it.db, r.dd, per * it.db, hipMemcpyDeviceToDevice, s);
         g0 += r.rg_count;
     }
-    if (e == hipSuccess) e = hipError_t(finish_fused(parts[0], rows, rg, f, b8, out, s));
+    if (e == hipSuccess) finish_fused(parts[0], rows, rg, f, b8, out);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
     if (e != hipSuccess) {
         (void)hipFree(base);  // cleanup after the error being returned
@@ -1533,7 +1509,7 @@ int rpl_fuse_pairs(const DevBlob& a, const DevBlob& b, DevBlob& out, void* strea
         a.rows != b.rows || a.cols != b.cols || a.rows % 32)
         return int(hipErrorInvalidValue);
     const int64_t rg_in = a.rpl.rg_count, rg = 2 * rg_in, nsb = a.rpl.nsb;
-    const FusedLayout f = fused_layout(it, rg, nsb, 8, int(std::max<int64_t>(1, (nsb + 3) / 4)));
+    const FusedLayout f = fused_layout(it, rg, nsb);
     void* base = nullptr;
     hipError_t e = hipMalloc(&base, f.total);
     if (e != hipSuccess) return int(e);
@@ -1549,7 +1525,7 @@ int rpl_fuse_pairs(const DevBlob& a, const DevBlob& b, DevBlob& out, void* strea
     if (it.db)
         run(f.dd, reinterpret_cast<const uint8_t*>(a.rpl.dd), reinterpret_cast<const uint8_t*>(b.rpl.dd), it.db, 1);
     e = hipGetLastError();
-    if (e == hipSuccess) e = hipError_t(finish_fused(a, 2 * a.rows, rg, f, b8, out, s));
+    if (e == hipSuccess) finish_fused(a, 2 * a.rows, rg, f, b8, out);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
     if (e != hipSuccess) {
         (void)hipFree(base);  // cleanup after the error being returned
@@ -1558,9 +1534,12 @@ int rpl_fuse_pairs(const DevBlob& a, const DevBlob& b, DevBlob& out, void* strea
     return int(e);
 }
 
-size_t rpl_t_scratch_floats(const RplArgs& a) {
+size_t rpl_t_scratch_floats(const RplArgs& a, int batch) {
+    // batch rows go kRplTMaxBatch per launch (the last launch may take fewer)
     size_t most = 0;
-    for (int nb = 1; nb <= kRplTMaxBatch; ++nb) {
+    const int full = std::min(batch, kRplTMaxBatch), rest = batch % kRplTMaxBatch;
+    for (int nb : {full, rest}) {
+        if (nb <= 0) continue;
         int slices = 1, g_per = 1;
         rpl_t_plan(a, nb, slices, g_per);
         if (slices > 1) most = std::max(most, size_t(slices) * size_t(nb) * size_t(a.nsb) * 256);
@@ -1568,28 +1547,39 @@ size_t rpl_t_scratch_floats(const RplArgs& a) {
     return most;
 }
 
-int launch_rpl_matvec_t(const DevBlob& b, const float* d_gy, float* d_gx, int batch, void* stream) {
+size_t rpl_scratch_floats(const DevBlob& b, int batch) {
+    if (b.layout != LAYOUT_RPL || batch <= 0) return 0;
+    size_t most = 0;
+    for (int max_s : {2, 4}) {  // the plan of either policy family
+        const RplPlan p = rpl_plan(b, max_s);
+        if (p.ksplit > 1)
+            most = std::max(most, size_t(std::min(batch, kRplFwdBatch)) * size_t(p.ksplit) * size_t(b.rpl.rg_count) * 64);
+    }
+    return most;
+}
+
+int launch_rpl_matvec_t(const DevBlob& b, const float* d_gy, float* d_gx, int batch, void* stream, float* d_scratch) {
     hipStream_t s = static_cast<hipStream_t>(stream);
     switch (b.fmt) {
-    case FMT_Q4_K: return launch_rpl_tr<TQ4K>(b, d_gy, d_gx, batch, s);
-    case FMT_Q2_K: return launch_rpl_tr<TKx<2>>(b, d_gy, d_gx, batch, s);
-    case FMT_Q3_K: return launch_rpl_tr<TKx<3>>(b, d_gy, d_gx, batch, s);
-    case FMT_Q5_K: return launch_rpl_tr<TKx<5>>(b, d_gy, d_gx, batch, s);
-    case FMT_Q6_K: return launch_rpl_tr<TQ6K>(b, d_gy, d_gx, batch, s);
-    case FMT_Q8_0: return launch_rpl_tr<TQ8>(b, d_gy, d_gx, batch, s);
-    case FMT_Q4_0: return launch_rpl_tr<TQ4>(b, d_gy, d_gx, batch, s);
-    case FMT_Q4_1: return launch_rpl_tr<TB32<4, true, 0, 0u>>(b, d_gy, d_gx, batch, s);
-    case FMT_Q5_0: return launch_rpl_tr<TB32<5, false, 16, 0u>>(b, d_gy, d_gx, batch, s);
-    case FMT_Q5_1: return launch_rpl_tr<TB32<5, true, 0, 0u>>(b, d_gy, d_gx, batch, s);
-    case FMT_AFFINE: return launch_rpl_tr<TB32<4, true, 0, 0u, 1>>(b, d_gy, d_gx, batch, s);
-    case FMT_TERNARY: return launch_rpl_tr<TIQ<RplTernI>>(b, d_gy, d_gx, batch, s);
-    case FMT_BINARY: return launch_rpl_tr<TIQ<RplIQ1S>>(b, d_gy, d_gx, batch, s);
-    case FMT_IQ1_S: return launch_rpl_tr<TIQ<RplIQ1S>>(b, d_gy, d_gx, batch, s);
-    case FMT_IQ2_XXS: return launch_rpl_tr<TIQ<RplIQ2XXS>>(b, d_gy, d_gx, batch, s);
-    case FMT_IQ2_XS: return launch_rpl_tr<TIQ<RplIQ2XS>>(b, d_gy, d_gx, batch, s);
-    case FMT_IQ3_XXS: return launch_rpl_tr<TIQ<RplIQ3XXS>>(b, d_gy, d_gx, batch, s);
-    case FMT_IQ3_S: return launch_rpl_tr<TIQ<RplIQ3S>>(b, d_gy, d_gx, batch, s);
-    case FMT_IQ4_XS: return launch_rpl_tr<TIQ<RplIQ4XS>>(b, d_gy, d_gx, batch, s);
+    case FMT_Q4_K: return launch_rpl_tr<TQ4K>(b, d_gy, d_gx, batch, s, d_scratch);
+    case FMT_Q2_K: return launch_rpl_tr<TKx<2>>(b, d_gy, d_gx, batch, s, d_scratch);
+    case FMT_Q3_K: return launch_rpl_tr<TKx<3>>(b, d_gy, d_gx, batch, s, d_scratch);
+    case FMT_Q5_K: return launch_rpl_tr<TKx<5>>(b, d_gy, d_gx, batch, s, d_scratch);
+    case FMT_Q6_K: return launch_rpl_tr<TQ6K>(b, d_gy, d_gx, batch, s, d_scratch);
+    case FMT_Q8_0: return launch_rpl_tr<TQ8>(b, d_gy, d_gx, batch, s, d_scratch);
+    case FMT_Q4_0: return launch_rpl_tr<TQ4>(b, d_gy, d_gx, batch, s, d_scratch);
+    case FMT_Q4_1: return launch_rpl_tr<TB32<4, true, 0, 0u>>(b, d_gy, d_gx, batch, s, d_scratch);
+    case FMT_Q5_0: return launch_rpl_tr<TB32<5, false, 16, 0u>>(b, d_gy, d_gx, batch, s, d_scratch);
+    case FMT_Q5_1: return launch_rpl_tr<TB32<5, true, 0, 0u>>(b, d_gy, d_gx, batch, s, d_scratch);
+    case FMT_AFFINE: return launch_rpl_tr<TB32<4, true, 0, 0u, 1>>(b, d_gy, d_gx, batch, s, d_scratch);
+    case FMT_TERNARY: return launch_rpl_tr<TIQ<RplTernI>>(b, d_gy, d_gx, batch, s, d_scratch);
+    case FMT_BINARY: return launch_rpl_tr<TIQ<RplIQ1S>>(b, d_gy, d_gx, batch, s, d_scratch);
+    case FMT_IQ1_S: return launch_rpl_tr<TIQ<RplIQ1S>>(b, d_gy, d_gx, batch, s, d_scratch);
+    case FMT_IQ2_XXS: return launch_rpl_tr<TIQ<RplIQ2XXS>>(b, d_gy, d_gx, batch, s, d_scratch);
+    case FMT_IQ2_XS: return launch_rpl_tr<TIQ<RplIQ2XS>>(b, d_gy, d_gx, batch, s, d_scratch);
+    case FMT_IQ3_XXS: return launch_rpl_tr<TIQ<RplIQ3XXS>>(b, d_gy, d_gx, batch, s, d_scratch);
+    case FMT_IQ3_S: return launch_rpl_tr<TIQ<RplIQ3S>>(b, d_gy, d_gx, batch, s, d_scratch);
+    case FMT_IQ4_XS: return launch_rpl_tr<TIQ<RplIQ4XS>>(b, d_gy, d_gx, batch, s, d_scratch);
     default: return int(hipErrorInvalidValue);
     }
 }

@@ -1,0 +1,457 @@
+// native.hip — weights.Store payloads (FormatNone + DType) on the device.
+//
+// Three computations over the same resident codes:
+//   * Dense's int8 path for the narrow DTypes (forwardSIMDNarrowI8 and
+//     forwardSIMDInt8, layers/dense/simd.go:130-195, 303-326): activations
+//     absmax-quantized to int8 (quantizeActsI8, simd.go:526-549), codes
+//     expanded to int8 (expandNarrowToI8, simd.go:149-195), exact int32 dot
+//     on v_dot4_i32_i8, y = f32(acc) * actScale * scale;
+//   * the f32 FormatNone product (quant/none.go:37-51, Dense's
+//     forwardSIMDMasterF32, simd.go:201-214) with f64 accumulation;
+//   * weights.Store.MatVec / MatVecT on FormatNone stores
+//     (weights/store.go:133-206 -> matVecNativeF64 / matVecTNativeF64,
+//     weights/native.go:1120-1158): f64 sums over the decoded weights.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+
+#include "wave_ops.h"
+#include "wv_internal.h"
+
+namespace wv {
+namespace {
+
+// Code width and int8 expansion of each narrow DType (expandNarrowToI8,
+// layers/dense/simd.go:149-195): value = MUL * u - OFF with u the unsigned
+// code after xor XR; Int8 bytes are used as signed values directly.
+template <int F>
+struct Narrow;
+template <> struct Narrow<FMT_NATIVE_INT8> {  // nativeInt8Weights (simd.go:506-511)
+    static constexpr int B = 8, MUL = 1, OFF = 0;
+    static constexpr uint32_t XR = 0u, MASK = 0xFFFFFFFFu;
+};
+template <> struct Narrow<FMT_NATIVE_INT4> {  // nibble, q > 7 -> q - 16: (q ^ 8) - 8
+    static constexpr int B = 4, MUL = 1, OFF = 8;
+    static constexpr uint32_t XR = 0x88888888u, MASK = 0x0F0F0F0Fu;
+};
+template <> struct Narrow<FMT_NATIVE_INT2> {  // code - 2
+    static constexpr int B = 2, MUL = 1, OFF = 2;
+    static constexpr uint32_t XR = 0u, MASK = 0x03030303u;
+};
+template <> struct Narrow<FMT_NATIVE_TERNARY> {  // code - 1 (code 3 -> +2, as expandNarrowToI8)
+    static constexpr int B = 2, MUL = 1, OFF = 1;
+    static constexpr uint32_t XR = 0u, MASK = 0x03030303u;
+};
+template <> struct Narrow<FMT_NATIVE_BINARY> {  // bit set -> +1, clear -> -1: 2u - 1
+    static constexpr int B = 1, MUL = 2, OFF = 1;
+    static constexpr uint32_t XR = 0u, MASK = 0x01010101u;
+};
+
+// int8 value of flat element i (expandNarrowToI8).
+template <int F>
+__device__ __forceinline__ int narrow_i8(const uint8_t* codes, int64_t i) {
+    using N = Narrow<F>;
+    if constexpr (N::B == 8) {
+        return int(int8_t(codes[i]));
+    } else {
+        const int per = 8 / N::B;
+        const uint32_t u = (uint32_t(codes[i / per]) >> (N::B * int(i % per))) & ((1u << N::B) - 1u);
+        return N::MUL * int(u ^ (N::XR & ((1u << N::B) - 1u))) - N::OFF;
+    }
+}
+
+// quantizeActsI8's q = round-half-away(f32(x / act)) clamped to [-128, 127].
+// x * (1/act) is within 2 ulp of the exact quotient, so its rounding agrees
+// whenever its fraction is not within 2^-13 of one half; only those rare
+// elements pay for the exact f32 division.
+__device__ __forceinline__ int quant_act(float x, float act, float inv) {
+    float t = x * inv;
+    const float f = fabsf(t - truncf(t));
+    if (fabsf(f - 0.5f) < 1.2e-4f) t = x / act;
+    int q = int(roundf(t));
+    return q > 127 ? 127 : (q < -128 ? -128 : q);
+}
+
+// The narrow int8 GEMV when each row is a whole number of 16-byte code
+// vectors (K % (128/B) == 0) and K <= 8192. A block of four waves covers
+// 4*RW rows of one batch row:
+//  * x is requested first (NX float4 per thread), then the block's codes (NC
+//    uint4 per lane per row), so the activation quantization overlaps the
+//    codes' arrival;
+//  * absmax over x, act = max/127 (1 if 0), q as quant_act;
+//  * xq goes to LDS laid out for the dot: code vector c holds E = 32/B codes
+//    per dword; dword d, shifted by k*B (k < KS = 8/B) and masked, offers in
+//    byte b the code of element c*(128/B) + d*E + KS*b + k, so LDS dword
+//    (d*nU + c)*KS + k holds those four xq bytes. Lane c reads its KS dwords
+//    per d once for all its rows;
+//  * acc = MUL * sum u*xq - OFF * sum xq on v_dot4_i32_i8: exact.
+template <int F, int NC, int NX, int RW>
+__global__ void __launch_bounds__(256) k_narrow_i8v(const uint8_t* __restrict__ codes, float scale, int rows, int K,
+                                                   const float* __restrict__ x, float* __restrict__ y,
+                                                   int32_t* __restrict__ acc_out, float* __restrict__ act_out) {
+    using N = Narrow<F>;
+    constexpr int B = N::B, KS = 8 / B, E = 32 / B, EU = 128 / B;
+    extern __shared__ uint32_t lds[];  // K/4 dwords of xq in the dot layout
+    __shared__ float red_f[4];
+    __shared__ int red_i[4];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int b = blockIdx.y;
+    const int r0 = blockIdx.x * (4 * RW) + wave * RW;
+    const int nU = K / EU, k4 = K / 4;
+    const float4* xb = reinterpret_cast<const float4*>(x + int64_t(b) * K);
+    float4 xv[NX];
+#pragma unroll
+    for (int n = 0; n < NX; ++n) xv[n] = xb[min(tid + 256 * n, k4 - 1)];
+    __builtin_amdgcn_sched_barrier(0);  // keep the x requests ahead of the codes
+    uint4 cv[RW][NC];
+#pragma unroll
+    for (int rw = 0; rw < RW; ++rw) {
+        const uint4* rowp = reinterpret_cast<const uint4*>(codes + int64_t(min(r0 + rw, rows - 1)) * (K / 8 * B));
+#pragma unroll
+        for (int c = 0; c < NC; ++c) cv[rw][c] = rowp[min(lane + 64 * c, nU - 1)];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    float m = 0.f;
+#pragma unroll
+    for (int n = 0; n < NX; ++n) {
+        if (tid + 256 * n >= k4) xv[n] = make_float4(0.f, 0.f, 0.f, 0.f);
+        m = fmaxf(m, fmaxf(fmaxf(fabsf(xv[n].x), fabsf(xv[n].y)), fmaxf(fabsf(xv[n].z), fabsf(xv[n].w))));
+    }
+    m = wave_maximum(m);
+    if (lane == 0) red_f[wave] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red_f[0], red_f[1]), fmaxf(red_f[2], red_f[3]));
+    float act = m / 127.0f;
+    if (act == 0.0f) act = 1.0f;
+    const float inv = 1.0f / act;
+    int sq = 0;
+    uint8_t* l8 = reinterpret_cast<uint8_t*>(lds);
+#pragma unroll
+    for (int n = 0; n < NX; ++n) {
+        const int i = tid + 256 * n;
+        if (i >= k4) continue;
+        const float e4[4] = {xv[n].x, xv[n].y, xv[n].z, xv[n].w};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int q = quant_act(e4[t], act, inv);
+            sq += q;
+            const int e = 4 * i + t;
+            const int c = e / EU, r = e % EU, d = r / E, r2 = r % E, bb = r2 / KS, k = r2 % KS;
+            l8[4 * ((d * nU + c) * KS + k) + bb] = uint8_t(int8_t(q));
+        }
+    }
+    sq = wave_total_i(sq);
+    if (lane == 0) red_i[wave] = sq;
+    __syncthreads();
+    sq = red_i[0] + red_i[1] + red_i[2] + red_i[3];
+    if (act_out && blockIdx.x == 0 && tid == 0) act_out[b] = act;
+    uint32_t xw[NC][4][KS];
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int d = 0; d < 4; ++d)
+#pragma unroll
+            for (int k = 0; k < KS; ++k) xw[c][d][k] = lds[(d * nU + min(lane + 64 * c, nU - 1)) * KS + k];
+#pragma unroll
+    for (int rw = 0; rw < RW; ++rw) {
+        int acc = 0;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            if (lane + 64 * c < nU) {
+                const uint32_t wd[4] = {cv[rw][c].x ^ N::XR, cv[rw][c].y ^ N::XR, cv[rw][c].z ^ N::XR,
+                                        cv[rw][c].w ^ N::XR};
+#pragma unroll
+                for (int d = 0; d < 4; ++d)
+#pragma unroll
+                    for (int k = 0; k < KS; ++k)
+                        acc = __builtin_amdgcn_sdot4(int((wd[d] >> (B * k)) & N::MASK), int(xw[c][d][k]), acc, false);
+            }
+        }
+        acc = N::MUL * wave_total_i(acc) - N::OFF * sq;
+        const int r = r0 + rw;
+        if (lane == 0 && r < rows) {
+            if (acc_out) acc_out[int64_t(b) * rows + r] = acc;
+            if (y) y[int64_t(b) * rows + r] = float(acc) * act * scale;  // simd.go:142
+        }
+    }
+}
+
+// Any shape (K <= 32768): xq in LDS in plain order, one wave per row, codes
+// read per element by flat index (rows need not start on a byte).
+template <int F>
+__global__ void __launch_bounds__(256) k_narrow_i8(const uint8_t* __restrict__ codes, float scale, int rows, int K,
+                                                  const float* __restrict__ x, float* __restrict__ y,
+                                                  int32_t* __restrict__ acc_out, float* __restrict__ act_out,
+                                                  int rows_per_block) {
+    extern __shared__ uint32_t lds[];
+    __shared__ float red_f[4];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int b = blockIdx.y;
+    const float* xb = x + int64_t(b) * K;
+    float m = 0.f;
+    for (int j = tid; j < K; j += 256) m = fmaxf(m, fabsf(xb[j]));
+    m = wave_maximum(m);
+    if (lane == 0) red_f[wave] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red_f[0], red_f[1]), fmaxf(red_f[2], red_f[3]));
+    float act = m / 127.0f;
+    if (act == 0.0f) act = 1.0f;
+    const float inv = 1.0f / act;
+    int8_t* l8 = reinterpret_cast<int8_t*>(lds);
+    for (int j = tid; j < K; j += 256) l8[j] = int8_t(quant_act(xb[j], act, inv));
+    __syncthreads();
+    if (act_out && blockIdx.x == 0 && tid == 0) act_out[b] = act;
+    const int r0 = blockIdx.x * rows_per_block, r1 = min(rows, r0 + rows_per_block);
+    for (int r = r0 + wave; r < r1; r += 4) {
+        int acc = 0;
+        const int64_t base = int64_t(r) * K;
+        for (int j = lane; j < K; j += 64) acc += narrow_i8<F>(codes, base + j) * int(l8[j]);
+        acc = wave_total_i(acc);
+        if (lane == 0) {
+            if (acc_out) acc_out[int64_t(b) * rows + r] = acc;
+            if (y) y[int64_t(b) * rows + r] = float(acc) * act * scale;
+        }
+    }
+}
+
+// f32 weight of flat element i, as the Store decoders give it (weightAt,
+// weights/decode.go:150-215): f32(q) * scale for the narrow DTypes, Ternary
+// codes 0 / 2 -> -scale / +scale and 1, 3 -> 0; the f32 value for LAYOUT_F32.
+template <int F>
+__device__ __forceinline__ float store_w(const uint8_t* codes, int64_t i, float scale) {
+    if constexpr (F == FMT_NONE) {
+        return reinterpret_cast<const float*>(codes)[i];
+    } else if constexpr (F == FMT_NATIVE_TERNARY) {
+        const uint32_t u = (uint32_t(codes[i >> 2]) >> (2 * int(i & 3))) & 3u;
+        return u == 0 ? -scale : (u == 2 ? scale : 0.0f);
+    } else if constexpr (F == FMT_NATIVE_BINARY) {
+        return (codes[i >> 3] >> int(i & 7)) & 1 ? scale : -scale;
+    } else {
+        return float(narrow_i8<F>(codes, i)) * scale;
+    }
+}
+
+// y = W x with f64 sums (one wave per row, 4 rows per block): the f32
+// FormatNone product (TX = TY = float) and Store.MatVec (TX = TY = double).
+template <int F, class TX, class TY>
+__global__ void __launch_bounds__(256) k_native_fwd(const uint8_t* __restrict__ codes, float scale, int64_t rows,
+                                                   int64_t K, const TX* __restrict__ x, TY* __restrict__ y) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int64_t r = int64_t(blockIdx.x) * 4 + wave;
+    const int b = blockIdx.y;
+    if (r >= rows) return;
+    const TX* xb = x + int64_t(b) * K;
+    const int64_t base = r * K;
+    double acc = 0.0;
+    if constexpr (F == FMT_NONE && sizeof(TX) == 4) {
+        if (K % 4 == 0) {  // rows start 16-byte aligned
+            typedef float f32x4 __attribute__((ext_vector_type(4)));
+            const f32x4* w4 = reinterpret_cast<const f32x4*>(codes) + base / 4;
+            const float4* x4 = reinterpret_cast<const float4*>(xb);
+            for (int64_t j = lane; j < K / 4; j += 64) {
+                const f32x4 w = __builtin_nontemporal_load(w4 + j);
+                const float4 v = x4[j];
+                acc = fma(double(w.x), double(v.x), acc);
+                acc = fma(double(w.y), double(v.y), acc);
+                acc = fma(double(w.z), double(v.z), acc);
+                acc = fma(double(w.w), double(v.w), acc);
+            }
+        } else {
+            for (int64_t j = lane; j < K; j += 64) acc = fma(double(store_w<F>(codes, base + j, scale)), double(xb[j]), acc);
+        }
+    } else {
+        for (int64_t j = lane; j < K; j += 64) acc = fma(double(store_w<F>(codes, base + j, scale)), double(xb[j]), acc);
+    }
+    acc = wave_total_f64(acc);
+    if (lane == 0) y[int64_t(b) * rows + r] = TY(acc);
+}
+
+// Column partials of W^T gy over row slices (f64): thread = column, slice =
+// blockIdx.y (rows_per_slice rows in row order), batch = blockIdx.z. Rows
+// with gy == 0 are skipped, as matVecTNativeF64 does (weights/native.go:1147).
+template <int F, class TG>
+__global__ void __launch_bounds__(256) k_native_t(const uint8_t* __restrict__ codes, float scale, int64_t rows,
+                                                 int64_t K, const TG* __restrict__ gy, double* __restrict__ part,
+                                                 int64_t rows_per_slice) {
+    const int64_t c = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    const int slice = blockIdx.y, b = blockIdx.z, nslices = gridDim.y;
+    if (c >= K) return;
+    const int64_t r0 = int64_t(slice) * rows_per_slice, r1 = min(rows, r0 + rows_per_slice);
+    const TG* g = gy + int64_t(b) * rows;
+    double acc = 0.0;
+    for (int64_t r = r0; r < r1; ++r) {
+        const double gv = double(g[r]);
+        if (gv == 0.0) continue;
+        acc = fma(double(store_w<F>(codes, r * K + c, scale)), gv, acc);
+    }
+    part[(int64_t(b) * nslices + slice) * K + c] = acc;
+}
+
+// gx[b][c] = TX(gx[b][c] + sum of the slices' partials in slice order), in f64.
+template <class TX>
+__global__ void __launch_bounds__(256) k_native_t_sum(const double* __restrict__ part, TX* __restrict__ gx, int64_t K,
+                                                     int nslices) {
+    const int64_t c = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    const int b = blockIdx.y;
+    if (c >= K) return;
+    const double* p = part + int64_t(b) * nslices * K + c;
+    double s = 0.0;
+    for (int k = 0; k < nslices; ++k) s += p[int64_t(k) * K];
+    TX* o = gx + int64_t(b) * K + c;
+    *o = TX(double(*o) + s);
+}
+
+template <int F, int NC, int NX>
+void launch_narrow_v(const DevBlob& b, const float* x, float* y, int32_t* acc, float* act, int batch, hipStream_t s) {
+    const int rows = int(b.rows), K = int(b.cols);
+    if constexpr (NC == 1) {  // 8 rows per wave while that still leaves ~200 blocks
+        if ((rows + 31) / 32 >= 192) {
+            hipLaunchKernelGGL((k_narrow_i8v<F, NC, NX, 8>), dim3(unsigned((rows + 31) / 32), unsigned(batch)),
+                               dim3(256), size_t(K), s, b.codes, b.tensor_scale, rows, K, x, y, acc, act);
+            return;
+        }
+    }
+    hipLaunchKernelGGL((k_narrow_i8v<F, NC, NX, 4>), dim3(unsigned((rows + 15) / 16), unsigned(batch)), dim3(256),
+                       size_t(K), s, b.codes, b.tensor_scale, rows, K, x, y, acc, act);
+}
+
+template <int F>
+int launch_narrow_f(const DevBlob& b, const float* x, float* y, int32_t* acc, float* act, int batch, hipStream_t s) {
+    const int rows = int(b.rows), K = int(b.cols);
+    constexpr int EU = 128 / Narrow<F>::B;  // codes per 16-byte vector
+    if (K % EU == 0 && K <= 8192 && K / EU <= 256) {
+        const int nu = K / EU, nx = (K + 1023) / 1024;  // NC = ceil(nu / 64) vectors per lane and row
+        if (nu <= 64) {
+            switch (nx) {
+            case 1: launch_narrow_v<F, 1, 1>(b, x, y, acc, act, batch, s); break;
+            case 2: launch_narrow_v<F, 1, 2>(b, x, y, acc, act, batch, s); break;
+            case 3: launch_narrow_v<F, 1, 3>(b, x, y, acc, act, batch, s); break;
+            case 4: launch_narrow_v<F, 1, 4>(b, x, y, acc, act, batch, s); break;
+            case 5: launch_narrow_v<F, 1, 5>(b, x, y, acc, act, batch, s); break;
+            case 6: launch_narrow_v<F, 1, 6>(b, x, y, acc, act, batch, s); break;
+            case 7: launch_narrow_v<F, 1, 7>(b, x, y, acc, act, batch, s); break;
+            default: launch_narrow_v<F, 1, 8>(b, x, y, acc, act, batch, s); break;
+            }
+        } else if (nu <= 128) {
+            switch (nx) {
+            case 1: case 2: launch_narrow_v<F, 2, 2>(b, x, y, acc, act, batch, s); break;
+            case 3: launch_narrow_v<F, 2, 3>(b, x, y, acc, act, batch, s); break;
+            case 4: launch_narrow_v<F, 2, 4>(b, x, y, acc, act, batch, s); break;
+            case 5: launch_narrow_v<F, 2, 5>(b, x, y, acc, act, batch, s); break;
+            case 6: launch_narrow_v<F, 2, 6>(b, x, y, acc, act, batch, s); break;
+            case 7: launch_narrow_v<F, 2, 7>(b, x, y, acc, act, batch, s); break;
+            default: launch_narrow_v<F, 2, 8>(b, x, y, acc, act, batch, s); break;
+            }
+        } else {  // Int8 rows of more than 2048 columns
+            switch (nx) {
+            case 3: launch_narrow_v<F, 4, 3>(b, x, y, acc, act, batch, s); break;
+            case 4: launch_narrow_v<F, 4, 4>(b, x, y, acc, act, batch, s); break;
+            case 5: launch_narrow_v<F, 4, 5>(b, x, y, acc, act, batch, s); break;
+            case 6: launch_narrow_v<F, 4, 6>(b, x, y, acc, act, batch, s); break;
+            case 7: launch_narrow_v<F, 4, 7>(b, x, y, acc, act, batch, s); break;
+            default: launch_narrow_v<F, 4, 8>(b, x, y, acc, act, batch, s); break;
+            }
+        }
+        return int(hipGetLastError());
+    }
+    const int rpb = 16;
+    const size_t lds = size_t((K + 3) / 4) * 4;
+    hipLaunchKernelGGL(k_narrow_i8<F>, dim3(unsigned((rows + rpb - 1) / rpb), unsigned(batch)), dim3(256), lds, s,
+                       b.codes, b.tensor_scale, rows, K, x, y, acc, act, rpb);
+    return int(hipGetLastError());
+}
+
+int launch_narrow(const DevBlob& b, const float* x, float* y, int32_t* acc, float* act, int batch, hipStream_t s) {
+    switch (b.fmt) {
+    case FMT_NATIVE_INT8: return launch_narrow_f<FMT_NATIVE_INT8>(b, x, y, acc, act, batch, s);
+    case FMT_NATIVE_INT4: return launch_narrow_f<FMT_NATIVE_INT4>(b, x, y, acc, act, batch, s);
+    case FMT_NATIVE_INT2: return launch_narrow_f<FMT_NATIVE_INT2>(b, x, y, acc, act, batch, s);
+    case FMT_NATIVE_TERNARY: return launch_narrow_f<FMT_NATIVE_TERNARY>(b, x, y, acc, act, batch, s);
+    case FMT_NATIVE_BINARY: return launch_narrow_f<FMT_NATIVE_BINARY>(b, x, y, acc, act, batch, s);
+    default: return int(hipErrorInvalidValue);
+    }
+}
+
+template <class TX, class TY>
+int launch_fwd_t(const DevBlob& b, const TX* x, TY* y, int batch, hipStream_t s) {
+    const dim3 g(unsigned((b.rows + 3) / 4), unsigned(batch));
+    const float sc = b.tensor_scale;
+    switch (b.fmt) {
+    case FMT_NONE: hipLaunchKernelGGL((k_native_fwd<FMT_NONE, TX, TY>), g, dim3(256), 0, s, b.codes, sc, b.rows, b.cols, x, y); break;
+    case FMT_NATIVE_INT8: hipLaunchKernelGGL((k_native_fwd<FMT_NATIVE_INT8, TX, TY>), g, dim3(256), 0, s, b.codes, sc, b.rows, b.cols, x, y); break;
+    case FMT_NATIVE_INT4: hipLaunchKernelGGL((k_native_fwd<FMT_NATIVE_INT4, TX, TY>), g, dim3(256), 0, s, b.codes, sc, b.rows, b.cols, x, y); break;
+    case FMT_NATIVE_INT2: hipLaunchKernelGGL((k_native_fwd<FMT_NATIVE_INT2, TX, TY>), g, dim3(256), 0, s, b.codes, sc, b.rows, b.cols, x, y); break;
+    case FMT_NATIVE_TERNARY: hipLaunchKernelGGL((k_native_fwd<FMT_NATIVE_TERNARY, TX, TY>), g, dim3(256), 0, s, b.codes, sc, b.rows, b.cols, x, y); break;
+    case FMT_NATIVE_BINARY: hipLaunchKernelGGL((k_native_fwd<FMT_NATIVE_BINARY, TX, TY>), g, dim3(256), 0, s, b.codes, sc, b.rows, b.cols, x, y); break;
+    default: return int(hipErrorInvalidValue);
+    }
+    return int(hipGetLastError());
+}
+
+// Row slices of the transposed products: about 1024 blocks, at least 64 rows each.
+int native_t_slices(const DevBlob& b, int batch) {
+    const int64_t colb = (b.cols + 255) / 256;
+    const int64_t want = (1024 + colb * batch - 1) / (colb * std::max(1, batch));
+    return int(std::max<int64_t>(1, std::min<int64_t>({want, 256, b.rows / 64})));
+}
+
+template <class TG, class TX>
+int launch_t_t(const DevBlob& b, const TG* gy, TX* gx, int batch, hipStream_t s, double* part) {
+    if (!part) return int(hipErrorInvalidValue);
+    const int ns = native_t_slices(b, batch);
+    const int64_t rps = (b.rows + ns - 1) / ns;
+    const dim3 g(unsigned((b.cols + 255) / 256), unsigned(ns), unsigned(batch));
+    const float sc = b.tensor_scale;
+    switch (b.fmt) {
+    case FMT_NONE: hipLaunchKernelGGL((k_native_t<FMT_NONE, TG>), g, dim3(256), 0, s, b.codes, sc, b.rows, b.cols, gy, part, rps); break;
+    case FMT_NATIVE_INT8: hipLaunchKernelGGL((k_native_t<FMT_NATIVE_INT8, TG>), g, dim3(256), 0, s, b.codes, sc, b.rows, b.cols, gy, part, rps); break;
+    case FMT_NATIVE_INT4: hipLaunchKernelGGL((k_native_t<FMT_NATIVE_INT4, TG>), g, dim3(256), 0, s, b.codes, sc, b.rows, b.cols, gy, part, rps); break;
+    case FMT_NATIVE_INT2: hipLaunchKernelGGL((k_native_t<FMT_NATIVE_INT2, TG>), g, dim3(256), 0, s, b.codes, sc, b.rows, b.cols, gy, part, rps); break;
+    case FMT_NATIVE_TERNARY: hipLaunchKernelGGL((k_native_t<FMT_NATIVE_TERNARY, TG>), g, dim3(256), 0, s, b.codes, sc, b.rows, b.cols, gy, part, rps); break;
+    case FMT_NATIVE_BINARY: hipLaunchKernelGGL((k_native_t<FMT_NATIVE_BINARY, TG>), g, dim3(256), 0, s, b.codes, sc, b.rows, b.cols, gy, part, rps); break;
+    default: return int(hipErrorInvalidValue);
+    }
+    hipLaunchKernelGGL(k_native_t_sum<TX>, dim3(unsigned((b.cols + 255) / 256), unsigned(batch)), dim3(256), 0, s, part,
+                       gx, b.cols, ns);
+    return int(hipGetLastError());
+}
+
+}  // namespace
+
+int launch_narrow_acc(const DevBlob& b, const float* d_x, int32_t* d_acc, float* d_act_scale, int batch, void* stream) {
+    if (b.layout != LAYOUT_NARROW) return int(hipErrorInvalidValue);
+    return launch_narrow(b, d_x, nullptr, d_acc, d_act_scale, batch, static_cast<hipStream_t>(stream));
+}
+
+int launch_native_fwd(const DevBlob& b, const float* d_x, float* d_y, int batch, void* stream) {
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (b.layout == LAYOUT_NARROW) return launch_narrow(b, d_x, d_y, nullptr, nullptr, batch, s);
+    if (b.layout == LAYOUT_F32) return launch_fwd_t<float, float>(b, d_x, d_y, batch, s);
+    return int(hipErrorInvalidValue);
+}
+
+int launch_store_f64(const DevBlob& b, const double* d_x, double* d_y, void* stream) {
+    if (b.layout != LAYOUT_NARROW && b.layout != LAYOUT_F32) return int(hipErrorInvalidValue);
+    return launch_fwd_t<double, double>(b, d_x, d_y, 1, static_cast<hipStream_t>(stream));
+}
+
+size_t store_t_scratch_floats(const DevBlob& b) { return native_t_scratch_floats(b, 1); }
+
+int launch_store_t_f64(const DevBlob& b, const double* d_gy, double* d_gx, void* stream, double* d_scratch) {
+    if (b.layout != LAYOUT_NARROW && b.layout != LAYOUT_F32) return int(hipErrorInvalidValue);
+    return launch_t_t<double, double>(b, d_gy, d_gx, 1, static_cast<hipStream_t>(stream), d_scratch);
+}
+
+// f64 partials: two floats of scratch each.
+size_t native_t_scratch_floats(const DevBlob& b, int batch) {
+    if (batch <= 0) return 0;
+    return 2 * size_t(native_t_slices(b, batch)) * size_t(b.cols) * size_t(batch);
+}
+
+int launch_native_t(const DevBlob& b, const float* d_gy, float* d_gx, int batch, void* stream, double* d_scratch) {
+    if (b.layout != LAYOUT_NARROW && b.layout != LAYOUT_F32) return int(hipErrorInvalidValue);
+    return launch_t_t<float, float>(b, d_gy, d_gx, batch, static_cast<hipStream_t>(stream), d_scratch);
+}
+
+}  // namespace wv

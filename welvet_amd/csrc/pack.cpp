@@ -409,23 +409,47 @@ bool pack(int fmt, const float* w, int64_t rows, int64_t cols, uint8_t* raw, flo
 }
 
 // weights/native.go:249-267 (absMax, weights/native.go:1160-1169).
-void pack_native_ternary(const float* w, int64_t n, uint8_t* codes, float* scale_out) {
-    float scale = 0;
-    for (int64_t i = 0; i < n; ++i) scale = std::max(scale, float(std::fabs(double(w[i]))));
+// weights.Store packers of the narrow DTypes (weights/native.go:88-97 Int8,
+// 180-194 packInt4, 218-230 packInt2, 249-269 packTernary, 271-283
+// packBinary): scale = absMax (/127 Int8, /7 Int4), 1 when zero; codes
+// LSB-first within bytes. `fmt` is FMT_NATIVE_*; false for other formats.
+bool pack_native(int fmt, const float* w, int64_t n, uint8_t* codes, float* scale_out) {
+    const int bits = narrow_bits(fmt);
+    if (!bits) return false;
+    float amax = 0;
+    for (int64_t i = 0; i < n; ++i) amax = std::max(amax, float(std::fabs(double(w[i]))));
+    float scale = fmt == FMT_NATIVE_INT8 ? amax / 127.0f : fmt == FMT_NATIVE_INT4 ? amax / 7.0f : amax;
     if (scale == 0) scale = 1;
-    std::memset(codes, 0, size_t((n + 3) / 4));
-    parallel_blocks((n + 3) / 4, [&](int64_t lo, int64_t hi) {
+    const int per = 8 / bits;
+    // round-half-away(f64(f32(w / scale))) clamped (clampI, weights/native.go:1184-1192)
+    auto qround = [&](float v, double lo, double hi) {
+        const double r = std::round(double(v / scale));
+        return int(r < lo ? lo : (r > hi ? hi : r));
+    };
+    parallel_blocks((n + per - 1) / per, [&](int64_t lo, int64_t hi) {
         for (int64_t b = lo; b < hi; ++b) {
-            uint8_t v = 0;
-            for (int k = 0; k < 4 && b * 4 + k < n; ++k) {
-                float r = w[b * 4 + k] / scale;
-                int code = r > 0.5f ? 2 : (r < -0.5f ? 0 : 1);
-                v |= uint8_t(code << (2 * k));
+            uint32_t v = 0;
+            for (int k = 0; k < per && b * per + k < n; ++k) {
+                const float x = w[b * per + k];
+                uint32_t code = 0;
+                switch (fmt) {
+                case FMT_NATIVE_INT8: code = uint32_t(uint8_t(int8_t(qround(x, -128, 127)))); break;
+                case FMT_NATIVE_INT4: code = uint32_t(qround(x, -8, 7)) & 0xFu; break;
+                case FMT_NATIVE_INT2: code = uint32_t(qround(x, -2, 1) + 2) & 3u; break;
+                case FMT_NATIVE_TERNARY: {
+                    const float r = x / scale;
+                    code = r > 0.5f ? 2u : (r < -0.5f ? 0u : 1u);
+                    break;
+                }
+                default: code = x >= 0 ? 1u : 0u; break;  // Binary
+                }
+                v |= code << (bits * k);
             }
-            codes[b] = v;
+            codes[b] = uint8_t(v);
         }
     });
     *scale_out = scale;
+    return true;
 }
 
 }  // namespace wv

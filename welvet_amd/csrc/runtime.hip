@@ -77,6 +77,67 @@ hipStream_t stream_or_default(void* s, int dev) {
     return g_dev[dev].stream;
 }
 
+
+// Scratch of one call (K-split or slice partials), stream-ordered: allocated
+// on the call's stream and released after its kernels, so concurrent calls on
+// one blob never share it.
+struct CallScratch {
+    void* p = nullptr;
+    hipStream_t s = nullptr;
+    int get(size_t floats, hipStream_t st, const char* what) {
+        if (!floats) return WV_OK;
+        s = st;
+        const hipError_t e = hipMallocAsync(&p, floats * sizeof(float), st);
+        if (e != hipSuccess) {
+            p = nullptr;
+            return hip_fail(e, what);
+        }
+        return WV_OK;
+    }
+    float* f() const { return static_cast<float*>(p); }
+    ~CallScratch() {
+        if (p) (void)hipFreeAsync(p, s);
+    }
+};
+
+// Device copies of a host call's buffers on stream s; finish() frees them in
+// stream order and waits for the stream.
+struct Staging {
+    hipStream_t s;
+    std::vector<void*> bufs;
+    hipError_t err = hipSuccess;
+    explicit Staging(hipStream_t st) : s(st) {}
+    template <class T = float>
+    T* out(size_t n) {
+        void* p = nullptr;
+        if (err == hipSuccess) err = hipMallocAsync(&p, std::max<size_t>(n, 1) * sizeof(T), s);
+        if (err == hipSuccess) bufs.push_back(p);
+        return static_cast<T*>(p);
+    }
+    template <class T>
+    T* in(const T* h, size_t n) {
+        T* p = out<T>(n);
+        if (err == hipSuccess && n) err = hipMemcpyAsync(p, h, n * sizeof(T), hipMemcpyHostToDevice, s);
+        return p;
+    }
+    int rc(const char* what) { return err == hipSuccess ? WV_OK : hip_fail(err, what); }
+    template <class T>
+    int back(T* h, const T* d, size_t n, const char* what) {
+        const hipError_t e = n ? hipMemcpyAsync(h, d, n * sizeof(T), hipMemcpyDeviceToHost, s) : hipSuccess;
+        return e == hipSuccess ? WV_OK : hip_fail(e, what);
+    }
+    int finish(int rc, const char* what) {
+        for (void* p : bufs) (void)hipFreeAsync(p, s);
+        bufs.clear();
+        const hipError_t e = hipStreamSynchronize(s);
+        if (!rc && e != hipSuccess) rc = hip_fail(e, what);
+        return rc;
+    }
+    ~Staging() {
+        for (void* p : bufs) (void)hipFreeAsync(p, s);
+    }
+};
+
 bool force_raw() {
     const char* v = std::getenv("WV_FORCE_RAW");
     return v && v[0] == '1';
@@ -377,9 +438,7 @@ bool lookup(uint64_t h, DevBlob& out) {
     return true;
 }
 
-bool supported_format(int fmt) {
-    return (fmt >= FMT_Q8_0 && fmt <= FMT_AFFINE) || fmt == FMT_NATIVE_TERNARY;
-}
+bool supported_format(int fmt) { return (fmt >= FMT_NONE && fmt <= FMT_AFFINE) || narrow_bits(fmt) > 0; }
 
 // InferAffineBlockWeights (affine_g64.go:99-122): keep BlockWeights when the
 // scales fit it, else 64 when they fit that, else cols / (scales per row).
@@ -398,8 +457,14 @@ const char* fmt_name(int f) {
                                   "Q4_K", "Q5_K", "Q6_K", "IQ1_S", "IQ2_XXS", "IQ2_XS", "IQ3_XXS",
                                   "IQ3_S", "IQ4_NL", "IQ4_XS", "TernaryPacked", "BinaryPacked", "AffinePacked"};
     if (f >= 0 && f <= 20) return names[f];
-    if (f == FMT_NATIVE_TERNARY) return "native-ternary";
-    return "unknown";
+    switch (f) {  // core.DType names (core/dtype.go:67-140)
+    case FMT_NATIVE_INT8: return "int8";
+    case FMT_NATIVE_INT4: return "int4";
+    case FMT_NATIVE_INT2: return "int2";
+    case FMT_NATIVE_TERNARY: return "ternary";
+    case FMT_NATIVE_BINARY: return "binary";
+    default: return "unknown";
+    }
 }
 
 // Raw bytes a blob must hold (quant.Pack sizes), or -1 if the format cannot
@@ -408,7 +473,8 @@ int64_t need_raw(int fmt, int64_t rows, int64_t cols, int32_t bw, const uint8_t*
                  int64_t* need_scales) {
     const int64_t n = rows * cols;
     *need_scales = 0;
-    if (fmt == FMT_NATIVE_TERNARY) return (n + 3) / 4;
+    if (fmt == FMT_NONE) return n * 4;  // f32 weights (quant/none.go:3-21)
+    if (const int nb = narrow_bits(fmt)) return (n * nb + 7) / 8;  // packInt4/Int2/Ternary/Binary, Int8 bytes
     if (fmt == FMT_AFFINE) {  // 4-bit codes, groups of bw along each row (affine_g64.go:34-47)
         if (bw <= 0 || bw % 8 || cols % bw) return -1;
         *need_scales = rows * (cols / bw);
@@ -494,10 +560,11 @@ int wv_pack(int format, const float* weights, int64_t rows, int64_t cols, uint8_
     return WV_OK;
 }
 
-int wv_pack_native_ternary(const float* weights, int64_t n, uint8_t* codes, float* scale) {
-    if (!weights || !codes || !scale) return fail(WV_E_ARG, "packTernary: nil buffer");
-    if (n <= 0) return fail(WV_E_SHAPE, "packTernary: empty tensor");
-    pack_native_ternary(weights, n, codes, scale);
+int wv_pack_native(int format, const float* weights, int64_t n, uint8_t* codes, float* scale) {
+    if (!weights || !codes || !scale) return fail(WV_E_ARG, "weights: nil buffer");
+    if (n <= 0) return fail(WV_E_SHAPE, "weights: empty tensor");
+    if (!pack_native(format, weights, n, codes, scale))
+        return fail(WV_E_FORMAT, "weights: native pack for %s not provided (Int8, Int4, Int2, Ternary, Binary)", fmt_name(format));
     return WV_OK;
 }
 
@@ -550,9 +617,10 @@ int wv_blob_upload(int format, int64_t rows, int64_t cols, int32_t block_weights
         b.iq_sg = iqs.sg;
     }
     size_t o_codes = 0, o_raw = 0, o_sc = 0, o_mn = 0;
-    if (format == FMT_NATIVE_TERNARY) {
-        b.layout = LAYOUT_TERNARY_I8;
-        if (cols > 32768) return fail(WV_E_SHAPE, "wv_blob_upload: native ternary cols %lld > 32768", (long long)cols);
+    if (narrow_bits(format) || format == FMT_NONE) {
+        b.layout = format == FMT_NONE ? LAYOUT_F32 : LAYOUT_NARROW;
+        if (b.layout == LAYOUT_NARROW && cols > 32768)
+            return fail(WV_E_SHAPE, "wv_blob_upload: %s cols %lld > 32768", fmt_name(format), (long long)cols);
         o_codes = img.add(size_t(need));
         std::memcpy(img.bytes.data() + o_codes, raw, size_t(need));
     } else if (!raw_only &&
@@ -586,32 +654,14 @@ int wv_blob_upload(int format, int64_t rows, int64_t cols, int32_t block_weights
             b.n_scales = int64_t(n_scales);
         }
     }
-    // K-split scratch for the row-interleaved path: forward partial sums
-    // [batch][split][rows] and MatVecT slice partials.
-    size_t o_part = 0, o_tpart = 0, weight_bytes = img.bytes.size();
-    if (b.layout == LAYOUT_RPL) {
-        const int64_t rg = (rows + 63) / 64, nsb = cols / 256;
-        b.rpl_max_batch = 8;
-        b.rpl_max_split = int(std::max<int64_t>(1, (nsb + 3) / 4));
-        o_part = img.add(size_t(b.rpl_max_batch) * b.rpl_max_split * rg * 64 * sizeof(float));
-        RplArgs shape{};
-        shape.rows = int(rows);
-        shape.nsb = int(nsb);
-        shape.rg_count = int(rg);
-        const size_t tf = rpl_t_scratch_floats(shape);
-        if (tf) {
-            o_tpart = img.add(tf * sizeof(float));
-        }
-    }
     rc = upload_image(img, b);
     if (rc) return rc;
-    b.device_bytes = weight_bytes;
     uint8_t* base = static_cast<uint8_t*>(b.base);
     if (b.layout == LAYOUT_RAW) {
         b.raw = base + o_raw;
         b.scales = b.n_scales ? reinterpret_cast<const float*>(base + o_sc) : nullptr;
         b.mins = b.n_mins ? reinterpret_cast<const float*>(base + o_mn) : nullptr;
-    } else if (b.layout == LAYOUT_TERNARY_I8) {
+    } else if (b.layout == LAYOUT_NARROW || b.layout == LAYOUT_F32) {
         b.codes = base + o_codes;
     } else {
         RplArgs& r = b.rpl;
@@ -619,14 +669,11 @@ int wv_blob_upload(int format, int64_t rows, int64_t cols, int32_t block_weights
         r.hi = ro.hi ? base + ro.hi : nullptr;
         r.meta = base + ro.meta;
         r.dd = ro.dd ? reinterpret_cast<const float2_t*>(base + ro.dd) : nullptr;
-        r.partial = reinterpret_cast<float*>(base + o_part);
+        r.partial = nullptr;
         r.rows = int(rows);
         r.nsb = int(cols / 256);
         r.rg_count = int((rows + 63) / 64);
         r.ksplit = 1;
-        if (o_tpart) {
-            b.rpl_t_partial = reinterpret_cast<float*>(base + o_tpart);
-        }
     }
     std::lock_guard<std::mutex> lk(g_mu);
     const uint64_t h = g_next++;
@@ -638,7 +685,7 @@ int wv_blob_upload(int format, int64_t rows, int64_t cols, int32_t block_weights
 int wv_blob_upload_wire(int format, int64_t rows, int64_t cols, const uint8_t* wire, size_t wire_len,
                         uint64_t* handle) {
     if (!handle || !wire) return fail(WV_E_ARG, "wv_blob_upload_wire: nil wire");
-    if (format == FMT_NONE || format == FMT_NATIVE_TERNARY)
+    if (format == FMT_NONE || narrow_bits(format))
         return fail(WV_E_FORMAT, "entity: not a packed quant blob (format=%s)", fmt_name(format));
     if (wire_len < 12) return fail(WV_E_SHAPE, "packed wire too short");
     uint32_t hdr[3];
@@ -694,20 +741,27 @@ int wv_matvec_dev(uint64_t handle, const float* d_x, float* d_y, int32_t batch, 
     if (!lookup(handle, b)) return fail(WV_E_HANDLE, "MatVec: unknown handle %llu", (unsigned long long)handle);
     if (!d_x || !d_y) return fail(WV_E_ARG, "MatVec: nil x/y");
     if (batch < 0) return fail(WV_E_SHAPE, "MatVec: negative batch %d", batch);
+    if (batch == 0) return WV_OK;
     hipSetDevice(b.device);
-    const int e = launch_matvec(b, d_x, d_y, batch, stream_or_default(stream, b.device));
+    hipStream_t s = stream_or_default(stream, b.device);
+    CallScratch sc;
+    int rc = sc.get(matvec_scratch_floats(b, batch), s, "MatVec: scratch");
+    if (rc) return rc;
+    const int e = launch_matvec(b, d_x, d_y, batch, s, sc.f());
     if (e != hipSuccess) return hip_fail(hipError_t(e), "MatVec: kernel launch");
     return WV_OK;
 }
 
-int wv_ternary_acc_dev(uint64_t handle, const float* d_x, int32_t* d_acc, float* d_act_scale, int32_t batch, void* stream) {
+int wv_native_acc_dev(uint64_t handle, const float* d_x, int32_t* d_acc, float* d_act_scale, int32_t batch, void* stream) {
     DevBlob b;
-    if (!lookup(handle, b)) return fail(WV_E_HANDLE, "ternary acc: unknown handle %llu", (unsigned long long)handle);
-    if (b.layout != LAYOUT_TERNARY_I8) return fail(WV_E_FORMAT, "ternary acc: blob is %s, not native ternary", fmt_name(b.fmt));
-    if (!d_x || !d_acc) return fail(WV_E_ARG, "ternary acc: nil x/acc");
+    if (!lookup(handle, b)) return fail(WV_E_HANDLE, "native acc: unknown handle %llu", (unsigned long long)handle);
+    if (b.layout != LAYOUT_NARROW)
+        return fail(WV_E_FORMAT, "native acc: blob is %s, not an Int8/Int4/Int2/Ternary/Binary store", fmt_name(b.fmt));
+    if (!d_x || !d_acc) return fail(WV_E_ARG, "native acc: nil x/acc");
+    if (batch <= 0) return batch < 0 ? fail(WV_E_SHAPE, "native acc: negative batch %d", batch) : WV_OK;
     hipSetDevice(b.device);
-    const int e = launch_ternary_acc(b, d_x, d_acc, d_act_scale, batch, stream_or_default(stream, b.device));
-    if (e != hipSuccess) return hip_fail(hipError_t(e), "ternary acc: kernel launch");
+    const int e = launch_narrow_acc(b, d_x, d_acc, d_act_scale, batch, stream_or_default(stream, b.device));
+    if (e != hipSuccess) return hip_fail(hipError_t(e), "native acc: kernel launch");
     return WV_OK;
 }
 
@@ -715,22 +769,13 @@ int wv_matvec_t_dev(uint64_t handle, const float* d_gy, float* d_gx, int32_t bat
     DevBlob b;
     if (!lookup(handle, b)) return fail(WV_E_HANDLE, "MatVecT: unknown handle %llu", (unsigned long long)handle);
     if (!d_gy || !d_gx) return fail(WV_E_ARG, "MatVecT: nil gy/gx");
-    if (b.layout == LAYOUT_TERNARY_I8)
-        return fail(WV_E_FORMAT, "quant: MatVecT not implemented for %s", fmt_name(b.fmt));
-    if (batch <= 0) return WV_OK;
+    if (batch <= 0) return batch < 0 ? fail(WV_E_SHAPE, "MatVecT: negative batch %d", batch) : WV_OK;
     hipSetDevice(b.device);
     hipStream_t s = stream_or_default(stream, b.device);
-    if (b.layout == LAYOUT_RPL) {
-        const int k = launch_matvec_t(b, d_gy, d_gx, batch, s, nullptr);
-        if (k != hipSuccess) return hip_fail(hipError_t(k), "MatVecT: kernel launch");
-        return WV_OK;
-    }
-    float* part = nullptr;
-    const size_t nf = matvec_t_scratch_floats(b, batch);
-    hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&part), std::max<size_t>(nf, 1) * sizeof(float), s);
-    if (e != hipSuccess) return hip_fail(e, "MatVecT: scratch");
-    const int k = launch_matvec_t(b, d_gy, d_gx, batch, s, part);
-    hipFreeAsync(part, s);
+    CallScratch sc;
+    int rc = sc.get(matvec_t_scratch_floats(b, batch), s, "MatVecT: scratch");
+    if (rc) return rc;
+    const int k = launch_matvec_t(b, d_gy, d_gx, batch, s, sc.f());
     if (k != hipSuccess) return hip_fail(hipError_t(k), "MatVecT: kernel launch");
     return WV_OK;
 }
@@ -743,19 +788,11 @@ int wv_matmul_dev(uint64_t handle, const float* d_x, float* d_y, int32_t m, void
     if (m == 0) return WV_OK;
     hipSetDevice(b.device);
     hipStream_t s = stream_or_default(stream, b.device);
-    if (!gemm_supported(b, m)) {
-        const int k = launch_matvec(b, d_x, d_y, m, s);
-        if (k != hipSuccess) return hip_fail(hipError_t(k), "MatMul: kernel launch");
-        return WV_OK;
-    }
-    float* part = nullptr;
-    const size_t nf = gemm_scratch_floats(b, m);
-    if (nf) {
-        hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&part), nf * sizeof(float), s);
-        if (e != hipSuccess) return hip_fail(e, "MatMul: split-K scratch");
-    }
-    const int k = launch_gemm(b, d_x, d_y, m, s, part);
-    if (part) hipFreeAsync(part, s);
+    const bool gemm = gemm_supported(b, m);
+    CallScratch sc;
+    int rc = sc.get(gemm ? gemm_scratch_floats(b, m) : matvec_scratch_floats(b, m), s, "MatMul: scratch");
+    if (rc) return rc;
+    const int k = gemm ? launch_gemm(b, d_x, d_y, m, s, sc.f()) : launch_matvec(b, d_x, d_y, m, s, sc.f());
     if (k != hipSuccess) return hip_fail(hipError_t(k), "MatMul: kernel launch");
     return WV_OK;
 }
@@ -767,82 +804,173 @@ int wv_matmul(uint64_t handle, const float* x, float* y, int32_t m) {
     if (m <= 0) return m < 0 ? fail(WV_E_ARG, "MatMul: negative row count %d", m) : WV_OK;
     hipSetDevice(b.device);
     hipStream_t s = g_dev[b.device].stream;
-    const size_t nx = size_t(m) * size_t(b.cols), ny = size_t(m) * size_t(b.rows);
-    float *dx = nullptr, *dy = nullptr;
-    hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&dx), nx * 4, s);
-    if (e == hipSuccess) e = hipMallocAsync(reinterpret_cast<void**>(&dy), ny * 4, s);
-    if (e != hipSuccess) return hip_fail(e, "MatMul: staging");
-    int rc = WV_OK;
-    e = hipMemcpyAsync(dx, x, nx * 4, hipMemcpyHostToDevice, s);
-    if (e != hipSuccess) rc = hip_fail(e, "MatMul: copy x");
+    Staging st(s);
+    float* dx = st.in(x, size_t(m) * size_t(b.cols));
+    float* dy = st.out(size_t(m) * size_t(b.rows));
+    int rc = st.rc("MatMul: staging");
     if (!rc) rc = wv_matmul_dev(handle, dx, dy, m, s);
-    if (!rc) {
-        e = hipMemcpyAsync(y, dy, ny * 4, hipMemcpyDeviceToHost, s);
-        if (e != hipSuccess) rc = hip_fail(e, "MatMul: copy y");
-    }
-    hipFreeAsync(dx, s);
-    hipFreeAsync(dy, s);
-    e = hipStreamSynchronize(s);
-    if (!rc && e != hipSuccess) rc = hip_fail(e, "MatMul: sync");
-    return rc;
+    if (!rc) rc = st.back(y, dy, size_t(m) * size_t(b.rows), "MatMul: copy y");
+    return st.finish(rc, "MatMul: sync");
 }
 
 int wv_matvec(uint64_t handle, const float* x, float* y, int32_t batch) {
     DevBlob b;
     if (!lookup(handle, b)) return fail(WV_E_HANDLE, "MatVec: unknown handle %llu", (unsigned long long)handle);
     if (!x || !y) return fail(WV_E_ARG, "MatVec: nil x/y");
-    if (batch <= 0) return WV_OK;
+    if (batch <= 0) return batch < 0 ? fail(WV_E_SHAPE, "MatVec: negative batch %d", batch) : WV_OK;
     hipSetDevice(b.device);
     hipStream_t s = g_dev[b.device].stream;
-    const size_t nx = size_t(batch) * size_t(b.cols), ny = size_t(batch) * size_t(b.rows);
-    float *dx = nullptr, *dy = nullptr;
-    hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&dx), nx * 4, s);
-    if (e == hipSuccess) e = hipMallocAsync(reinterpret_cast<void**>(&dy), ny * 4, s);
-    if (e != hipSuccess) return hip_fail(e, "MatVec: staging");
-    e = hipMemcpyAsync(dx, x, nx * 4, hipMemcpyHostToDevice, s);
-    int rc = WV_OK;
-    if (e != hipSuccess) rc = hip_fail(e, "MatVec: copy x");
-    if (!rc) {
-        const int k = launch_matvec(b, dx, dy, batch, s);
-        if (k != hipSuccess) rc = hip_fail(hipError_t(k), "MatVec: kernel launch");
-    }
-    if (!rc) {
-        e = hipMemcpyAsync(y, dy, ny * 4, hipMemcpyDeviceToHost, s);
-        if (e != hipSuccess) rc = hip_fail(e, "MatVec: copy y");
-    }
-    hipFreeAsync(dx, s);
-    hipFreeAsync(dy, s);
-    e = hipStreamSynchronize(s);
-    if (!rc && e != hipSuccess) rc = hip_fail(e, "MatVec: sync");
-    return rc;
+    Staging st(s);
+    float* dx = st.in(x, size_t(batch) * size_t(b.cols));
+    float* dy = st.out(size_t(batch) * size_t(b.rows));
+    int rc = st.rc("MatVec: staging");
+    if (!rc) rc = wv_matvec_dev(handle, dx, dy, batch, s);
+    if (!rc) rc = st.back(y, dy, size_t(batch) * size_t(b.rows), "MatVec: copy y");
+    return st.finish(rc, "MatVec: sync");
 }
 
 int wv_matvec_t(uint64_t handle, const float* gy, float* gx, int32_t batch) {
     DevBlob b;
     if (!lookup(handle, b)) return fail(WV_E_HANDLE, "MatVecT: unknown handle %llu", (unsigned long long)handle);
     if (!gy || !gx) return fail(WV_E_ARG, "MatVecT: nil gy/gx");
-    if (batch <= 0) return WV_OK;
+    if (batch <= 0) return batch < 0 ? fail(WV_E_SHAPE, "MatVecT: negative batch %d", batch) : WV_OK;
     hipSetDevice(b.device);
     hipStream_t s = g_dev[b.device].stream;
-    const size_t ng = size_t(batch) * size_t(b.rows), nx = size_t(batch) * size_t(b.cols);
-    float *dg = nullptr, *dx = nullptr;
-    hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&dg), ng * 4, s);
-    if (e == hipSuccess) e = hipMallocAsync(reinterpret_cast<void**>(&dx), nx * 4, s);
-    if (e != hipSuccess) return hip_fail(e, "MatVecT: staging");
-    int rc = WV_OK;
-    e = hipMemcpyAsync(dg, gy, ng * 4, hipMemcpyHostToDevice, s);
-    if (e == hipSuccess) e = hipMemcpyAsync(dx, gx, nx * 4, hipMemcpyHostToDevice, s);
-    if (e != hipSuccess) rc = hip_fail(e, "MatVecT: copy in");
+    Staging st(s);
+    float* dg = st.in(gy, size_t(batch) * size_t(b.rows));
+    float* dx = st.in(gx, size_t(batch) * size_t(b.cols));
+    int rc = st.rc("MatVecT: staging");
     if (!rc) rc = wv_matvec_t_dev(handle, dg, dx, batch, s);
-    if (!rc) {
-        e = hipMemcpyAsync(gx, dx, nx * 4, hipMemcpyDeviceToHost, s);
-        if (e != hipSuccess) rc = hip_fail(e, "MatVecT: copy out");
+    if (!rc) rc = st.back(gx, dx, size_t(batch) * size_t(b.cols), "MatVecT: copy out");
+    return st.finish(rc, "MatVecT: sync");
+}
+
+int wv_quant_matvec(uint64_t handle, const float* x, size_t len_x, float* y, size_t len_y) {
+    DevBlob b;
+    if (!lookup(handle, b)) return fail(WV_E_HANDLE, "MatVec: nil blob");
+    if (b.layout == LAYOUT_NARROW)
+        return fail(WV_E_FORMAT, "quant: MatVec not implemented for %s (native path TBD — no QAT fallback)", fmt_name(b.fmt));
+    if (int64_t(len_x) < b.cols || int64_t(len_y) < b.rows)  // checkBlobYX (quant/helpers.go:94-103)
+        return fail(WV_E_SHAPE, "MatVec: size mismatch rows=%lld cols=%lld len(x)=%zu len(y)=%zu", (long long)b.rows,
+                    (long long)b.cols, len_x, len_y);
+    if (!x || !y) return fail(WV_E_ARG, "MatVec: nil x/y");
+    return wv_matvec(handle, x, y, 1);
+}
+
+int wv_quant_matvec_t(uint64_t handle, const float* gy, size_t len_gy, float* gx, size_t len_gx) {
+    DevBlob b;
+    if (!lookup(handle, b)) return fail(WV_E_HANDLE, "MatVecT: nil blob");
+    if (b.layout == LAYOUT_NARROW)
+        return fail(WV_E_FORMAT, "quant: MatVecT not implemented for %s (native path TBD — no QAT fallback)", fmt_name(b.fmt));
+    if (int64_t(len_gy) < b.rows || int64_t(len_gx) < b.cols)  // checkBlobGYGX (quant/helpers.go:105-114)
+        return fail(WV_E_SHAPE, "MatVecT: size mismatch rows=%lld cols=%lld len(gy)=%zu len(gx)=%zu", (long long)b.rows,
+                    (long long)b.cols, len_gy, len_gx);
+    if (!gy || !gx) return fail(WV_E_ARG, "MatVecT: nil gy/gx");
+    return wv_matvec_t(handle, gy, gx, 1);
+}
+
+int wv_dense_forward_dev(uint64_t handle, const float* d_x, float* d_pre, float* d_post, int32_t batch,
+                         const double* d_bias, int32_t act, void* stream) {
+    DevBlob b;
+    if (!lookup(handle, b)) return fail(WV_E_HANDLE, "dense: unknown handle %llu", (unsigned long long)handle);
+    if (!d_x || !d_pre) return fail(WV_E_ARG, "dense: nil layer/input");
+    if (!act_valid(act)) return fail(WV_E_ARG, "dense: activation %d is not a core.ActivationType", act);
+    if (!d_post && (d_bias || act != ACT_LINEAR))
+        return fail(WV_E_ARG, "dense: a bias or a non-linear activation needs a post buffer");
+    if (batch <= 0) return batch < 0 ? fail(WV_E_SHAPE, "dense: negative batch %d", batch) : WV_OK;
+    hipSetDevice(b.device);
+    hipStream_t s = stream_or_default(stream, b.device);
+    CallScratch sc;
+    int rc = sc.get(matvec_scratch_floats(b, batch), s, "dense: scratch");
+    if (rc) return rc;
+    BiasAct ba;
+    ba.bias = d_bias;
+    ba.act = act;
+    ba.post = d_post;
+    const int e = launch_matvec(b, d_x, d_pre, batch, s, sc.f(), d_post ? &ba : nullptr);
+    if (e != hipSuccess) return hip_fail(hipError_t(e), "dense: kernel launch");
+    return WV_OK;
+}
+
+int wv_dense_forward(uint64_t handle, const float* x, float* pre, float* post, int32_t batch, const double* bias,
+                     int32_t act) {
+    DevBlob b;
+    if (!lookup(handle, b)) return fail(WV_E_HANDLE, "dense: unknown handle %llu", (unsigned long long)handle);
+    if (!x || !pre) return fail(WV_E_ARG, "dense: nil layer/input");
+    if (batch <= 0) return batch < 0 ? fail(WV_E_SHAPE, "dense: negative batch %d", batch) : WV_OK;
+    hipSetDevice(b.device);
+    hipStream_t s = g_dev[b.device].stream;
+    const size_t n = size_t(batch) * size_t(b.rows);
+    Staging st(s);
+    float* dx = st.in(x, size_t(batch) * size_t(b.cols));
+    float* dpre = st.out(n);
+    float* dpost = post ? st.out(n) : nullptr;
+    const double* dbias = bias ? st.in(bias, size_t(b.rows)) : nullptr;
+    int rc = st.rc("dense: staging");
+    if (!rc) rc = wv_dense_forward_dev(handle, dx, dpre, dpost, batch, dbias, act, s);
+    if (!rc) rc = st.back(pre, dpre, n, "dense: copy pre");
+    if (!rc && post) rc = st.back(post, dpost, n, "dense: copy post");
+    return st.finish(rc, "dense: sync");
+}
+
+int wv_store_matvec(uint64_t handle, const double* x, size_t len_x, double* y, size_t len_y) {
+    DevBlob b;
+    if (!lookup(handle, b)) return fail(WV_E_HANDLE, "weights: nil");
+    if ((len_x && !x) || (len_y && !y)) return fail(WV_E_ARG, "weights: nil x/y");
+    if (b.layout == LAYOUT_NARROW || b.layout == LAYOUT_F32) {
+        if (int64_t(len_x) < b.cols || int64_t(len_y) < b.rows) return fail(WV_E_SHAPE, "weights: matvecF64 shape");
+        hipSetDevice(b.device);
+        hipStream_t s = g_dev[b.device].stream;
+        Staging st(s);
+        double* dx = st.in(x, size_t(b.cols));
+        double* dy = st.out<double>(size_t(b.rows));
+        int rc = st.rc("weights: staging");
+        if (!rc) {
+            const int e = launch_store_f64(b, dx, dy, s);
+            if (e != hipSuccess) rc = hip_fail(hipError_t(e), "weights: kernel launch");
+        }
+        if (!rc) rc = st.back(y, dy, size_t(b.rows), "weights: copy y");
+        rc = st.finish(rc, "weights: sync");
+        if (!rc) std::fill(y + b.rows, y + len_y, 0.0);  // MatVec[T] returns its whole zeroed y buffer (store.go:133-145)
+        return rc;
     }
-    hipFreeAsync(dg, s);
-    hipFreeAsync(dx, s);
-    e = hipStreamSynchronize(s);
-    if (!rc && e != hipSuccess) rc = hip_fail(e, "MatVecT: sync");
-    return rc;
+    // Packed: quant.MatVec on f32 copies, then widen every entry (weights/store.go:162-180).
+    std::vector<float> xf(len_x), yf(len_y, 0.0f);
+    for (size_t i = 0; i < len_x; ++i) xf[i] = float(x[i]);
+    const int rc = wv_quant_matvec(handle, xf.data(), len_x, yf.data(), len_y);
+    if (rc) return rc;
+    for (size_t i = 0; i < len_y; ++i) y[i] = double(yf[i]);
+    return WV_OK;
+}
+
+int wv_store_matvec_t(uint64_t handle, const double* gy, size_t len_gy, double* gx, size_t len_gx) {
+    DevBlob b;
+    if (!lookup(handle, b)) return fail(WV_E_HANDLE, "weights: nil");
+    if ((len_gy && !gy) || (len_gx && !gx)) return fail(WV_E_ARG, "weights: nil gy/gx");
+    if (b.layout == LAYOUT_NARROW || b.layout == LAYOUT_F32) {
+        if (int64_t(len_gy) < b.rows || int64_t(len_gx) < b.cols) return fail(WV_E_SHAPE, "weights: matvecTF64 shape");
+        hipSetDevice(b.device);
+        hipStream_t s = g_dev[b.device].stream;
+        Staging st(s);
+        double* dg = st.in(gy, size_t(b.rows));
+        double* dx = st.in(gx, size_t(b.cols));
+        double* part = st.out<double>(std::max<size_t>(1, store_t_scratch_floats(b) / 2));
+        int rc = st.rc("weights: staging");
+        if (!rc) {
+            const int e = launch_store_t_f64(b, dg, dx, s, part);
+            if (e != hipSuccess) rc = hip_fail(hipError_t(e), "weights: kernel launch");
+        }
+        if (!rc) rc = st.back(gx, dx, size_t(b.cols), "weights: copy gx");
+        return st.finish(rc, "weights: sync");
+    }
+    // Packed: quant.MatVecT on f32 copies of gy and gx, then widen gx (weights/store.go:182-206).
+    std::vector<float> gyf(len_gy), gxf(len_gx);
+    for (size_t i = 0; i < len_gy; ++i) gyf[i] = float(gy[i]);
+    for (size_t i = 0; i < len_gx; ++i) gxf[i] = float(gx[i]);
+    const int rc = wv_quant_matvec_t(handle, gyf.data(), len_gy, gxf.data(), len_gx);
+    if (rc) return rc;
+    for (size_t i = 0; i < len_gx; ++i) gx[i] = double(gxf[i]);
+    return WV_OK;
 }
 
 int wv_sync(void* stream) {

@@ -16,8 +16,23 @@ enum Fmt : int {
     FMT_Q2_K = 6, FMT_Q3_K = 7, FMT_Q4_K = 8, FMT_Q5_K = 9, FMT_Q6_K = 10,
     FMT_IQ1_S = 11, FMT_IQ2_XXS = 12, FMT_IQ2_XS = 13, FMT_IQ3_XXS = 14, FMT_IQ3_S = 15,
     FMT_IQ4_NL = 16, FMT_IQ4_XS = 17, FMT_TERNARY = 18, FMT_BINARY = 19, FMT_AFFINE = 20,
-    FMT_NATIVE_TERNARY = 1019,  // FormatNone + core.DTypeTernary (core/dtype.go:31)
+    // FormatNone weights.Store payloads: WV_NATIVE_BASE + core.DType (core/dtype.go:11-52)
+    FMT_NATIVE_BASE = 1000,
+    FMT_NATIVE_INT8 = 1009, FMT_NATIVE_INT4 = 1014, FMT_NATIVE_INT2 = 1017, FMT_NATIVE_TERNARY = 1019,
+    FMT_NATIVE_BINARY = 1020,
 };
+// The narrow weights.Store DTypes that run Dense's int8 path
+// (forwardSIMDNarrowI8 / forwardSIMDInt8, layers/dense/simd.go:130-195, 303-326):
+// code bits per weight, or 0.
+inline int narrow_bits(int fmt) {
+    switch (fmt) {
+    case FMT_NATIVE_INT8: return 8;
+    case FMT_NATIVE_INT4: return 4;
+    case FMT_NATIVE_INT2: case FMT_NATIVE_TERNARY: return 2;
+    case FMT_NATIVE_BINARY: return 1;
+    default: return 0;
+    }
+}
 
 // k-quant super-block spec (quant/kquant.go:29-51).
 struct KSpec {
@@ -102,7 +117,7 @@ struct PackSizes {
 bool pack_sizes(int fmt, int64_t rows, int64_t cols, PackSizes& out);
 bool pack(int fmt, const float* w, int64_t rows, int64_t cols, uint8_t* raw, float* scales, float* mins,
           uint8_t* meta);
-void pack_native_ternary(const float* w, int64_t n, uint8_t* codes, float* scale);
+bool pack_native(int fmt, const float* w, int64_t n, uint8_t* codes, float* scale);
 
 // ---- device residency ----
 
@@ -110,7 +125,8 @@ void pack_native_ternary(const float* w, int64_t n, uint8_t* codes, float* scale
 enum Layout : int {
     LAYOUT_RAW = 0,        // uploaded bytes verbatim; decoded per element (any shape / format)
     LAYOUT_RPL = 1,        // Q4_K/Q6_K/Q8_0/Q4_0 with cols % 256 == 0: row-interleaved planes (gemv_rpl.hip)
-    LAYOUT_TERNARY_I8 = 4, // DTypeTernary: 2-bit codes rows (as uploaded)
+    LAYOUT_NARROW = 4,     // weights.Store Int8/Int4/Int2/Ternary/Binary codes (as uploaded) + Store.Scale
+    LAYOUT_F32 = 5,        // FormatNone f32 weights, row-major (quant/none.go, Store FormatNone+Float32)
 };
 
 // Device view of a row-interleaved blob. Rows are grouped 64 at a time (one
@@ -125,7 +141,10 @@ struct RplArgs {
     const uint8_t* hi;
     const uint8_t* meta;
     const float2_t* dd;
-    float* partial;       // [batch chunk][ksplit][rg*64] partial sums when K is split
+    // K-split partial sums [batch chunk][ksplit][rg*64], in scratch the caller
+    // of the launch provides (never stored with the blob: two launches on one
+    // blob may run at once).
+    float* partial;
     int rows, nsb, rg_count, ksplit;
     // Output epilogue of the forward kernel: RPL_STORE y = Wx;
     // RPL_ADD y += Wx (residual); RPL_SILU_MUL y = silu(aux) * Wx (SwiGLU up);
@@ -143,6 +162,12 @@ struct RplArgs {
     // With RPL_ADD: sums of the updated y^2 over each 16 rows
     // ([batch][rg*4]), the partials the next fused RMSNorm consumes.
     float* ss_out;
+    // RPL_STORE with post != nullptr: applyBiasAct (layers/dense/dense.go:
+    // 145-167). y = pre = f32(Wx + bias) (bias f64, may be null) and
+    // post = f32(act(f64(pre))).
+    const double* bias;
+    int act;
+    float* post;
 };
 
 // Options of one forward launch on the row-interleaved layout.
@@ -154,12 +179,32 @@ struct RplExtra {
     int nrm_n = 0;
     double nrm_eps = 0.0;
     float* ss_out = nullptr;
+    float* partial = nullptr;  // K-split scratch, rpl_scratch_floats() floats
+    const double* bias = nullptr;
+    int act = -1;
+    float* post = nullptr;
 };
 enum RplMode { RPL_STORE = 0, RPL_ADD = 1, RPL_SILU_MUL = 2, RPL_SWIGLU = 3 };
 
-constexpr int kRplTMaxBatch = 16;  // batch rows per MatVecT launch on LAYOUT_RPL
+// core.ActivationType values (core/layer.go:88-99).
+enum Act : int {
+    ACT_LINEAR = -1, ACT_RELU = 0, ACT_SILU = 1, ACT_GELU = 2, ACT_TANH = 3, ACT_SIGMOID = 4, ACT_LEAKY_RELU = 5,
+    ACT_RELU2 = 6,
+};
+inline bool act_valid(int a) { return a >= ACT_LINEAR && a <= ACT_RELU2; }
 
-// Device view of one blob. Pointers are into one hipMalloc'd allocation.
+// Forward epilogue of launch_matvec: applyBiasAct (layers/dense/dense.go:145-167).
+struct BiasAct {
+    const double* bias = nullptr;  // [rows] f64, or null
+    int act = ACT_LINEAR;
+    float* post = nullptr;  // [batch][rows]; null: no epilogue (y = W x only)
+};
+
+constexpr int kRplTMaxBatch = 16;  // batch rows per MatVecT launch on LAYOUT_RPL
+constexpr int kRplFwdBatch = 8;    // batch rows per K-split forward launch on LAYOUT_RPL
+
+// Device view of one blob. Pointers are into one hipMalloc'd allocation that
+// holds weights only: every launch that needs scratch takes it as an argument.
 struct DevBlob {
     int fmt = 0;
     int64_t rows = 0, cols = 0;
@@ -175,22 +220,26 @@ struct DevBlob {
     const float* mins = nullptr;  // AffinePacked biases (Blob.Mins), one per group of block_weights
     int64_t n_mins = 0;
     int iq_bits = 0, iq_sg = 0;  // Meta[0], Meta[1] for IQ (iq.go:187-190)
-    // LAYOUT_TERNARY_I8
+    // LAYOUT_NARROW (codes of a weights.Store DType) and LAYOUT_F32 (f32 weights)
     const uint8_t* codes = nullptr;
     // LAYOUT_RPL
     RplArgs rpl{};
-    int rpl_max_split = 1;  // capacity of rpl.partial per batch row
-    int rpl_max_batch = 1;  // batch rows one split launch can carry
-    float* rpl_t_partial = nullptr;    // MatVecT slice partials [batch][slice][cols]
     void* base = nullptr;   // allocation owner
-    size_t device_bytes = 0;  // weight bytes (excludes scratch)
+    size_t device_bytes = 0;  // bytes of the allocation
 };
 
-// Kernel launchers (gemv.hip, gemv_rpl.hip). Return a hipError_t as int.
+// Kernel launchers (gemv.hip, gemv_rpl.hip, native.hip). Return a hipError_t
+// as int. A launcher whose kernels need scratch takes it as `d_scratch` and
+// returns hipErrorInvalidValue when it is null; *_scratch_floats() give the
+// floats it needs (0: none).
 int launch_rpl(const DevBlob& b, const float* d_x, float* d_y, int batch, void* stream, int mode = RPL_STORE,
-               const float* aux = nullptr);
+               const float* aux = nullptr, float* d_scratch = nullptr);
 int launch_rpl_ex(const DevBlob& b, const float* d_x, float* d_y, int batch, void* stream, const RplExtra& ex);
-int launch_matvec(const DevBlob& b, const float* d_x, float* d_y, int batch, void* stream);
+size_t rpl_scratch_floats(const DevBlob& b, int batch);
+size_t matvec_scratch_floats(const DevBlob& b, int batch);
+int launch_matvec(const DevBlob& b, const float* d_x, float* d_y, int batch, void* stream, float* d_scratch,
+                  const BiasAct* ba = nullptr);
+size_t matvec_t_scratch_floats(const DevBlob& b, int batch);
 int launch_matvec_t(const DevBlob& b, const float* d_gy, float* d_gx, int batch, void* stream, float* d_scratch);
 // Fused row-interleaved images (gemv_rpl.hip), built on the device from
 // resident blobs of one format and width: rpl_fuse_rows stacks the parts'
@@ -203,13 +252,24 @@ int rpl_fuse_pairs(const DevBlob& a, const DevBlob& b, DevBlob& out, void* strea
 bool gemm_supported(const DevBlob& b, int M);
 size_t gemm_scratch_floats(const DevBlob& b, int M);
 int launch_gemm(const DevBlob& b, const float* d_x, float* d_y, int M, void* stream, float* d_scratch);
-// MatVecT on LAYOUT_RPL uses the blob's own scratch (rpl_t_partial).
-int launch_rpl_matvec_t(const DevBlob& b, const float* d_gy, float* d_gx, int batch, void* stream);
-// Partial floats that scratch needs (batch rows are taken kRplTMaxBatch per launch).
-size_t rpl_t_scratch_floats(const RplArgs& a);
+// MatVecT on LAYOUT_RPL (slice partials in d_scratch when the plan has several slices).
+int launch_rpl_matvec_t(const DevBlob& b, const float* d_gy, float* d_gx, int batch, void* stream, float* d_scratch);
+size_t rpl_t_scratch_floats(const RplArgs& a, int batch);
 // gx[b][c] += sum_k part[(b*nsplit + k)*cols + c], k ascending.
 void launch_gemvt_reduce(const float* part, float* gx, int64_t cols, int nsplit, int batch, void* stream);
-size_t matvec_t_scratch_floats(const DevBlob& b, int batch);
-int launch_ternary_acc(const DevBlob& b, const float* d_x, int32_t* d_acc, float* d_act_scale, int batch, void* stream);
+// The elementwise applyBiasAct epilogue over y[batch][rows] (layouts without a fused one).
+int launch_bias_act(const float* d_y, float* d_y_pre, float* d_post, const double* d_bias, int act, int64_t rows,
+                    int batch, void* stream);
+// weights.Store DTypes on LAYOUT_NARROW / LAYOUT_F32 (native.hip).
+int launch_narrow_acc(const DevBlob& b, const float* d_x, int32_t* d_acc, float* d_act_scale, int batch, void* stream);
+int launch_native_fwd(const DevBlob& b, const float* d_x, float* d_y, int batch, void* stream);
+// weights.Store.MatVec / MatVecT on FormatNone stores: f64 x / y, f64 sums
+// over the decoded weights (weights/native.go:1120-1158).
+int launch_store_f64(const DevBlob& b, const double* d_x, double* d_y, void* stream);
+size_t store_t_scratch_floats(const DevBlob& b);
+int launch_store_t_f64(const DevBlob& b, const double* d_gy, double* d_gx, void* stream, double* d_scratch);
+// MatVecT (gx += W^T gy, f32) on LAYOUT_NARROW / LAYOUT_F32.
+size_t native_t_scratch_floats(const DevBlob& b, int batch);
+int launch_native_t(const DevBlob& b, const float* d_gy, float* d_gx, int batch, void* stream, double* d_scratch);
 
 }  // namespace wv

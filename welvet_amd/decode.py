@@ -44,10 +44,16 @@ class Config:
 
 
 class Decoder:
-    """Owns a wv_decoder handle; layer blobs stay owned by the caller."""
+    """Owns a wv_decoder handle. The device blobs given to set_layer and
+    set_output are referenced by the decoder's kernels, so the Decoder keeps
+    those DeviceBlob objects alive until free() (or until a later set_layer /
+    set_output replaces them): a caller may pass freshly uploaded blobs
+    without holding them itself."""
 
     def __init__(self, cfg: Config):
         self.cfg = cfg
+        self._layer_blobs: dict[int, list[DeviceBlob]] = {}
+        self._lm: DeviceBlob | None = None
         h = ctypes.c_uint64()
         c = cfg.c()
         check(lib().wv_decoder_create(ctypes.byref(c), ctypes.byref(h)))
@@ -58,12 +64,14 @@ class Decoder:
         an = np.ascontiguousarray(attn_norm, np.float32)
         fn = np.ascontiguousarray(ffn_norm, np.float32)
         check(lib().wv_decoder_set_layer(self.handle, layer, hs, an.ctypes.data, fn.ctypes.data))
+        self._layer_blobs[layer] = list(blobs)
 
     def set_output(self, lm_head: DeviceBlob, final_norm: np.ndarray | None, embedding: np.ndarray) -> None:
         fn = None if final_norm is None else np.ascontiguousarray(final_norm, np.float32)
         emb = np.ascontiguousarray(embedding, np.float32)
         check(lib().wv_decoder_set_output(self.handle, lm_head.handle, None if fn is None else fn.ctypes.data,
                                           emb.ctypes.data))
+        self._lm = lm_head
 
     def set_kv(self, layer: int, first_pos: int, k: np.ndarray, v: np.ndarray) -> None:
         k = np.ascontiguousarray(k, np.float32)
@@ -85,6 +93,8 @@ class Decoder:
         if self.handle:
             check(lib().wv_decoder_free(self.handle))
             self.handle = 0
+        self._layer_blobs.clear()
+        self._lm = None
 
     def __del__(self):
         try:
