@@ -161,6 +161,19 @@ int wv_matvec(uint64_t handle, const float *x, float *y, int32_t batch);
 /* Device-pointer form of wv_matvec, enqueued on `stream`. */
 int wv_matvec_dev(uint64_t handle, const float *d_x, float *d_y, int32_t batch, void *stream);
 
+/* wv_matvec_dev that allocates nothing. It has no counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Kernels that need scratch (the K-split partials of large-K shapes) use one
+ * fixed 4 MiB device array per GPU, held until the process ends, instead of a
+ * per-call allocation; a shape whose partials (up to 8 batch rows x the K
+ * split x the rows padded to 64) exceed 2^20 floats fails with WV_E_SHAPE
+ * before anything is enqueued. Every call
+ * on a GPU shares that GPU's array: calls that overlap on one GPU (other
+ * threads or streams) race; callers must order them. Results equal
+ * wv_matvec_dev's. */
+int wv_matvec_dev_noalloc(uint64_t handle, const float *d_x, float *d_y, int32_t batch, void *stream);
+
 /* quant.MatVec (quant/matvec.go:5-35) for one vector, with its argument check
  * checkBlobYX (quant/helpers.go:94-103): len_x >= cols and len_y >= rows, else
  * WV_E_SHAPE "MatVec: size mismatch rows=R cols=C len(x)=X len(y)=Y"; x past

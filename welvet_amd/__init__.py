@@ -37,7 +37,7 @@ WV_E = {-1: "ARG", -2: "SHAPE", -3: "FORMAT", -4: "OOM", -5: "HIP", -6: "NODEV",
 EXPORTS = (
     "wv_init", "wv_last_error", "wv_version", "wv_pack_sizes", "wv_pack",
     "wv_pack_native", "wv_blob_upload", "wv_blob_upload_wire", "wv_blob_free", "wv_blob_info",
-    "wv_matvec", "wv_matvec_dev", "wv_quant_matvec", "wv_dense_forward", "wv_dense_forward_dev",
+    "wv_matvec", "wv_matvec_dev", "wv_matvec_dev_noalloc", "wv_quant_matvec", "wv_dense_forward", "wv_dense_forward_dev",
     "wv_native_acc_dev", "wv_store_matvec", "wv_matvec_t", "wv_matvec_t_dev", "wv_quant_matvec_t",
     "wv_store_matvec_t", "wv_matmul", "wv_matmul_dev", "wv_sync",
     "wv_decoder_create", "wv_decoder_set_layer", "wv_decoder_set_output", "wv_decoder_set_kv",
@@ -78,6 +78,7 @@ def lib():
     L.wv_blob_info.argtypes = [ctypes.c_uint64, _P, _P, _P, _P, _P]
     L.wv_matvec.argtypes = [ctypes.c_uint64, _P, _P, ctypes.c_int32]
     L.wv_matvec_dev.argtypes = [ctypes.c_uint64, _P, _P, ctypes.c_int32, _P]
+    L.wv_matvec_dev_noalloc.argtypes = [ctypes.c_uint64, _P, _P, ctypes.c_int32, _P]
     L.wv_native_acc_dev.argtypes = [ctypes.c_uint64, _P, _P, _P, ctypes.c_int32, _P]
     L.wv_quant_matvec.argtypes = [ctypes.c_uint64, _P, _SZ, _P, _SZ]
     L.wv_quant_matvec_t.argtypes = [ctypes.c_uint64, _P, _SZ, _P, _SZ]

@@ -17,6 +17,13 @@
 #include "../../include/welvet_hip.h"
 #include "wv_internal.h"
 
+// Scratch of wv_matvec_dev_noalloc: a fixed device array, one copy per GPU
+// the library runs on, held until the process ends. Host code never uses
+// this name as an address: each device's address comes from
+// hipGetSymbolAddress at initialisation (DeviceState::scratch).
+constexpr size_t kNoAllocScratchFloats = size_t(1) << 20;  // 4 MiB
+static __device__ __align__(256) float scratch[kNoAllocScratchFloats];
+
 namespace wv {
 namespace {
 
@@ -40,6 +47,7 @@ int hip_fail(hipError_t e, const char* what) {
 struct DeviceState {
     bool ready = false;
     hipStream_t stream = nullptr;
+    float* scratch = nullptr;  // this device's address of the file-scope `scratch` array
 };
 
 std::mutex g_mu;  // guards g_blobs, g_next, g_dev
@@ -55,8 +63,12 @@ int ensure_device_locked(int dev) {
     hipError_t e = hipSetDevice(dev);
     if (e != hipSuccess) return hip_fail(e, "wv_init: hipSetDevice");
     if (!g_dev[dev].ready) {
+        void* sp = nullptr;
+        e = hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_fail(e, "wv_init: hipGetSymbolAddress(scratch)");
         e = hipStreamCreateWithFlags(&g_dev[dev].stream, hipStreamNonBlocking);
         if (e != hipSuccess) return hip_fail(e, "wv_init: hipStreamCreate");
+        g_dev[dev].scratch = static_cast<float*>(sp);
         g_dev[dev].ready = true;
     }
     g_current = dev;
@@ -749,6 +761,30 @@ int wv_matvec_dev(uint64_t handle, const float* d_x, float* d_y, int32_t batch, 
     if (rc) return rc;
     const int e = launch_matvec(b, d_x, d_y, batch, s, sc.f());
     if (e != hipSuccess) return hip_fail(hipError_t(e), "MatVec: kernel launch");
+    return WV_OK;
+}
+
+int wv_matvec_dev_noalloc(uint64_t handle, const float* d_x, float* d_y, int32_t batch, void* stream) {
+    DevBlob b;
+    if (!lookup(handle, b)) return fail(WV_E_HANDLE, "MatVec: unknown handle %llu", (unsigned long long)handle);
+    if (!d_x || !d_y) return fail(WV_E_ARG, "MatVec: nil x/y");
+    if (batch < 0) return fail(WV_E_SHAPE, "MatVec: negative batch %d", batch);
+    if (batch == 0) return WV_OK;
+    float* sp = nullptr;
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        sp = g_dev[b.device].scratch;
+    }
+    if (!sp) return fail(WV_E_NODEV, "MatVec (no-alloc): device %d has no scratch (not initialised)", b.device);
+    // Every partial the split kernels read was written earlier in the same
+    // call, so the array needs no clearing between calls.
+    const size_t need = matvec_scratch_floats(b, batch);
+    if (need > kNoAllocScratchFloats)
+        return fail(WV_E_SHAPE, "MatVec (no-alloc): rows=%lld cols=%lld needs %zu floats of scratch, the fixed array holds %zu",
+                    (long long)b.rows, (long long)b.cols, need, kNoAllocScratchFloats);
+    hipSetDevice(b.device);
+    const int e = launch_matvec(b, d_x, d_y, batch, stream_or_default(stream, b.device), need ? sp : nullptr);
+    if (e != hipSuccess) return hip_fail(hipError_t(e), "MatVec (no-alloc): kernel launch");
     return WV_OK;
 }
 
