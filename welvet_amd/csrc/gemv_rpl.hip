@@ -28,7 +28,6 @@
 #include <cstdint>
 #include <cstdlib>
 
-#include "epilogue.h"
 #include "wave_ops.h"
 #include "wv_internal.h"
 
@@ -536,10 +535,7 @@ __device__ __forceinline__ void finish_rows(const RplArgs& a, float* y, int b, i
         return;
     }
     float v = 0.f;
-    if (valid && row < a.rows) {
-        const int64_t idx = int64_t(b) * a.rows + row;
-        v = a.post ? store_bias_act(y, a.post, idx, s, a.bias, row, a.act) : store_y(a, y, idx, s);
-    }
+    if (valid && row < a.rows) v = store_y(a, y, int64_t(b) * a.rows + row, s);
     if (a.ss_out) {
         const float q = row_sum16(v * v);
         if (valid && (lane & 15) == 0) a.ss_out[int64_t(b) * a.rg_count * 4 + row / 16] = q;
@@ -896,9 +892,6 @@ int launch_rpl_t(const DevBlob& bl, const float* x, float* y, int batch, hipStre
     a.nrm_n = ex.nrm_n;
     a.nrm_eps = ex.nrm_eps;
     a.ss_out = ex.ss_out;
-    a.bias = ex.bias;
-    a.act = ex.act;
-    a.post = ex.post;
     a.partial = ex.partial;
     const RplPlan p = rpl_plan(bl, P::kWords2 ? 2 : 4);
     if (P::kWords2 && p.S > 2) return int(hipErrorInvalidValue);  // not reachable: the plan caps S
@@ -915,7 +908,6 @@ int launch_rpl_t(const DevBlob& bl, const float* x, float* y, int batch, hipStre
         if (aux) ab.aux = aux + int64_t(b0) * a.rows;
         if (ab.nrm_ss) ab.nrm_ss += int64_t(b0) * a.nrm_n;
         if (ab.ss_out) ab.ss_out += int64_t(b0) * a.rg_count * 4;
-        if (ab.post) ab.post += int64_t(b0) * a.rows;
         const int64_t ystride = mode == RPL_SWIGLU ? a.rows / 2 : a.rows;
         const float* xb = x + int64_t(b0) * a.nsb * 256;
         float* yb = y + int64_t(b0) * ystride;
@@ -1323,6 +1315,21 @@ int launch_rpl_tr(const DevBlob& bl, const float* gy, float* gx, int batch, hipS
 
 }  // namespace
 
+// The forward policy of a row-interleaved blob has a second metadata word per
+// chunk (block min or second scale group), which caps its plan at S = 2.
+bool rpl_words2(const DevBlob& b) {
+    switch (b.fmt) {
+    case FMT_Q4_1: return RplQ41I::kWords2;
+    case FMT_Q5_1: return RplQ51I::kWords2;
+    case FMT_AFFINE: return RplAff64I::kWords2;
+    case FMT_TERNARY: return RplTernI::kWords2;
+    case FMT_IQ2_XS: return RplIQ2XS::kWords2;
+    case FMT_IQ3_S: return RplIQ3S::kWords2;
+    case FMT_IQ4_XS: return RplIQ4XS::kWords2;
+    default: return false;
+    }
+}
+
 int launch_rpl_ex(const DevBlob& b, const float* d_x, float* d_y, int batch, void* stream, const RplExtra& ex) {
     hipStream_t s = static_cast<hipStream_t>(stream);
     switch (b.fmt) {
@@ -1549,13 +1556,9 @@ size_t rpl_t_scratch_floats(const RplArgs& a, int batch) {
 
 size_t rpl_scratch_floats(const DevBlob& b, int batch) {
     if (b.layout != LAYOUT_RPL || batch <= 0) return 0;
-    size_t most = 0;
-    for (int max_s : {2, 4}) {  // the plan of either policy family
-        const RplPlan p = rpl_plan(b, max_s);
-        if (p.ksplit > 1)
-            most = std::max(most, size_t(std::min(batch, kRplFwdBatch)) * size_t(p.ksplit) * size_t(b.rpl.rg_count) * 64);
-    }
-    return most;
+    const RplPlan p = rpl_plan(b, rpl_words2(b) ? 2 : 4);  // the plan launch_rpl_t makes for this blob
+    if (p.ksplit <= 1) return 0;
+    return size_t(std::min(batch, kRplFwdBatch)) * size_t(p.ksplit) * size_t(b.rpl.rg_count) * 64;
 }
 
 int launch_rpl_matvec_t(const DevBlob& b, const float* d_gy, float* d_gx, int batch, void* stream, float* d_scratch) {

@@ -162,12 +162,6 @@ struct RplArgs {
     // With RPL_ADD: sums of the updated y^2 over each 16 rows
     // ([batch][rg*4]), the partials the next fused RMSNorm consumes.
     float* ss_out;
-    // RPL_STORE with post != nullptr: applyBiasAct (layers/dense/dense.go:
-    // 145-167). y = pre = f32(Wx + bias) (bias f64, may be null) and
-    // post = f32(act(f64(pre))).
-    const double* bias;
-    int act;
-    float* post;
 };
 
 // Options of one forward launch on the row-interleaved layout.
@@ -180,9 +174,6 @@ struct RplExtra {
     double nrm_eps = 0.0;
     float* ss_out = nullptr;
     float* partial = nullptr;  // K-split scratch, rpl_scratch_floats() floats
-    const double* bias = nullptr;
-    int act = -1;
-    float* post = nullptr;
 };
 enum RplMode { RPL_STORE = 0, RPL_ADD = 1, RPL_SILU_MUL = 2, RPL_SWIGLU = 3 };
 
