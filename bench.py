@@ -80,7 +80,8 @@ DECODE = {
 }
 # Per-dispatch TCC counters of the GEMV kernel (KiB), medians over the timed
 # launches of `rocprofv3 --pmc FETCH_SIZE` and `--pmc WRITE_SIZE` runs of
-# `bench.py --no-cpu --steps 200 --warmup 20 --copy-probe 64 --workload W`.
+# `bench.py --no-cpu --copy-probe 64 --workload W` (the commands are in the
+# PMC_SOURCE files).
 # On gfx950 FETCH_SIZE counts one half of the bytes a plain 64 MiB device copy
 # reads (32779.5 KiB for 65536 KiB) and WRITE_SIZE all the bytes it writes
 # (65536 KiB), so traffic = 1.9993 * FETCH + 1.0 * WRITE, in bytes.
@@ -88,18 +89,23 @@ COPY_FETCH_SCALE = 65536.0 / 32779.5
 COPY_WRITE_SCALE = 65536.0 / 65536.0
 PMC_KIB = {
     "q4k_4096x14336": (18951.5, 56.0),
+    "ternary_2560x6912": (2241.25, 30.84),
+    "ternary_6912x2560": (2308.0, 16.0),
 }
 # Where each PMC_KIB entry comes from (the profile summary under profiles/).
 PMC_SOURCE = {
     "q4k_4096x14336": "profiles/k_gemv_rpl_q4k_4096x14336_pmc_traffic.txt",
+    "ternary_2560x6912": "profiles/k_narrow_i8v_ternary_2560x6912.txt",
+    "ternary_6912x2560": "profiles/k_narrow_i8v_ternary_6912x2560.txt",
 }
 METRIC = "dequant-GEMV HBM GB/s (% of peak) at 4096->14336 Q4_K b=1; decode tokens/s"
 
 
 def algorithmic_bytes(packed, rows, cols, ternary):
-    """Packed weight bytes in the reference layout + x + y (int8 x for ternary)."""
-    x_bytes = cols if ternary else 4 * cols
-    return packed.nbytes + (4 if ternary else 0) + x_bytes + 4 * rows
+    """Packed weight bytes in the reference layout (+ the f32 tensor scale of
+    the native DTypes) + f32 x + f32 y. Every path reads x as f32: the int8
+    path quantizes it on chip."""
+    return packed.nbytes + (4 if ternary else 0) + 4 * cols + 4 * rows
 
 
 def make_weights(fmt, rows, cols, seed=1234):

@@ -46,11 +46,15 @@ def native_blob(dt, rows, cols, seed):
 
 
 @pytest.mark.parametrize("dt", NARROW)
-@pytest.mark.parametrize("shape", [(6912, 2560), (2560, 6912), (300, 1024), (37, 100), (5, 4104)])
+@pytest.mark.parametrize("shape", [(6912, 2560), (2560, 6912), (300, 1024), (4500, 1024), (9001, 768), (4200, 8192),
+                                   (37, 100), (5, 4104)])
 def test_narrow_int8_path_bit_exact(dt, shape):
-    """(6912, 2560) and (2560, 6912) are BASELINE config 3's shapes; 37x100 and
-    5x4104 leave the vector kernel (rows not whole code vectors, or a row of
-    Binary codes that is not 16-byte aligned) for the per-element one."""
+    """(6912, 2560) and (2560, 6912) are BASELINE config 3's shapes; 4500 and
+    9001 rows give each wave 4 rows (9001 leaves a ragged last block);
+    4200 x 8192 holds 4 code vectors per lane and row for Int4 (Int8 leaves
+    the vector kernel there: its rows exceed 256 code vectors);
+    37x100 and 5x4104 leave the vector kernel (rows not whole code vectors, or
+    a row of Binary codes that is not 16-byte aligned) for the per-element one."""
     import torch
     rows, cols = shape
     print(f"[gpu] narrow {dt} {cols}->{rows}", flush=True)
@@ -67,6 +71,21 @@ def test_narrow_int8_path_bit_exact(dt, shape):
     wv.sync()
     assert np.array_equal(acc.cpu().numpy(), acc_ref)
     assert np.array_equal(act.cpu().numpy(), as_ref)
+    assert np.array_equal(d.matvec(x).reshape(-1), y_ref)
+    d.free()
+
+
+@pytest.mark.parametrize("dt", ["NativeInt4", "NativeTernary"])
+@pytest.mark.parametrize("shape", [(2560, 6912), (37, 100)])
+@pytest.mark.parametrize("mag", [1e-38, 1e-42])
+def test_narrow_tiny_activations(dt, shape, mag):
+    """max|x| below 127 * 2^-128 makes 1/act overflow (and 1e-42 is all
+    subnormal): quantizeActsI8 still divides exactly, element by element."""
+    rows, cols = shape
+    p, d, rng = native_blob(dt, rows, cols, 7)
+    x = (rng.standard_normal((1, cols)) * mag).astype(np.float32)
+    y_ref, acc_ref, as_ref = oracle.narrow_i8_forward(dt, p.raw, p.tensor_scale, rows, cols, x)
+    assert as_ref[0] != 1.0 and np.count_nonzero(x) > cols // 2
     assert np.array_equal(d.matvec(x).reshape(-1), y_ref)
     d.free()
 

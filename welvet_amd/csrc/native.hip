@@ -62,20 +62,41 @@ __device__ __forceinline__ int narrow_i8(const uint8_t* codes, int64_t i) {
 }
 
 // quantizeActsI8's q = round-half-away(f32(x / act)) clamped to [-128, 127].
-// x * (1/act) is within 2 ulp of the exact quotient, so its rounding agrees
-// whenever its fraction is not within 2^-13 of one half; only those rare
-// elements pay for the exact f32 division.
-__device__ __forceinline__ int quant_act(float x, float act, float inv) {
-    float t = x * inv;
-    const float f = fabsf(t - truncf(t));
-    if (fabsf(f - 0.5f) < 1.2e-4f) t = x / act;
-    int q = int(roundf(t));
+// With inv = v_rcp(act) (1 ulp), t = x * inv is within 4e-5 of RN(x / act)
+// while |t| <= 128 (relative 2^-23 + 2^-24 on t, 2^-24 on the quotient), so
+// rint(t) is the reference's rounding unless t lies that close to a
+// half-integer. Those rare elements, and every element when 1/act overflows
+// (max|x| < 127 * 2^-128: thr = -1), are redone by the exact f32 division.
+constexpr float kTieWindow = 1.2e-4f;
+__device__ __forceinline__ float quant_inv(float act) { return __builtin_amdgcn_rcpf(act); }
+__device__ __forceinline__ float quant_thr(float inv) { return inv <= 3.4e38f ? 0.5f - kTieWindow : -1.0f; }
+// The rounding of t = x * inv when it is safe (returns false otherwise; NaN
+// from inf * 0 or inf - inf fails the test too).
+__device__ __forceinline__ bool quant_fast(float x, float inv, float thr, float& r) {
+    const float t = x * inv;
+    r = rintf(t);
+    return fabsf(t - r) <= thr;
+}
+__device__ __forceinline__ int quant_clamp(float r) {
+    const int q = int(r);
     return q > 127 ? 127 : (q < -128 ? -128 : q);
+}
+// One element, the exact division on a wave-uniform branch (a ballot), so it
+// is not if-converted into every element's path.
+__device__ __forceinline__ int quant_act(float x, float act, float inv, float thr) {
+    float r;
+    const bool exact = !quant_fast(x, inv, thr, r);
+    if (__builtin_amdgcn_ballot_w64(exact)) {
+        if (exact) r = roundf(x / act);
+    }
+    return quant_clamp(r);
 }
 
 // The narrow int8 GEMV when each row is a whole number of 16-byte code
-// vectors (K % (128/B) == 0) and K <= 8192. A block of four waves covers
-// 4*RW rows of one batch row:
+// vectors (K % (128/B) == 0) and K <= 8192. A block of WB = blockDim/64 waves
+// (up to 16, sized so the grid is about one block per CU) covers WB*RW rows of
+// one batch row; every block quantizes all of x, so more threads per block
+// shorten that serial prologue:
 //  * x is requested first (NX float4 per thread), then the block's codes (NC
 //    uint4 per lane per row), so the activation quantization overlaps the
 //    codes' arrival;
@@ -87,22 +108,22 @@ __device__ __forceinline__ int quant_act(float x, float act, float inv) {
 //    per d once for all its rows;
 //  * acc = MUL * sum u*xq - OFF * sum xq on v_dot4_i32_i8: exact.
 template <int F, int NC, int NX, int RW>
-__global__ void __launch_bounds__(256) k_narrow_i8v(const uint8_t* __restrict__ codes, float scale, int rows, int K,
-                                                   const float* __restrict__ x, float* __restrict__ y,
-                                                   int32_t* __restrict__ acc_out, float* __restrict__ act_out) {
+__global__ void __launch_bounds__(1024) k_narrow_i8v(const uint8_t* __restrict__ codes, float scale, int rows, int K,
+                                                    const float* __restrict__ x, float* __restrict__ y,
+                                                    int32_t* __restrict__ acc_out, float* __restrict__ act_out) {
     using N = Narrow<F>;
     constexpr int B = N::B, KS = 8 / B, E = 32 / B, EU = 128 / B;
     extern __shared__ uint32_t lds[];  // K/4 dwords of xq in the dot layout
-    __shared__ float red_f[4];
-    __shared__ int red_i[4];
+    __shared__ float red_f[16];
+    const int nt = blockDim.x, WB = nt >> 6;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int b = blockIdx.y;
-    const int r0 = blockIdx.x * (4 * RW) + wave * RW;
+    const int r0 = (blockIdx.x * WB + wave) * RW;
     const int nU = K / EU, k4 = K / 4;
     const float4* xb = reinterpret_cast<const float4*>(x + int64_t(b) * K);
     float4 xv[NX];
 #pragma unroll
-    for (int n = 0; n < NX; ++n) xv[n] = xb[min(tid + 256 * n, k4 - 1)];
+    for (int n = 0; n < NX; ++n) xv[n] = xb[min(tid + nt * n, k4 - 1)];
     __builtin_amdgcn_sched_barrier(0);  // keep the x requests ahead of the codes
     uint4 cv[RW][NC];
 #pragma unroll
@@ -115,44 +136,74 @@ __global__ void __launch_bounds__(256) k_narrow_i8v(const uint8_t* __restrict__ 
     float m = 0.f;
 #pragma unroll
     for (int n = 0; n < NX; ++n) {
-        if (tid + 256 * n >= k4) xv[n] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (tid + nt * n >= k4) xv[n] = make_float4(0.f, 0.f, 0.f, 0.f);
         m = fmaxf(m, fmaxf(fmaxf(fabsf(xv[n].x), fabsf(xv[n].y)), fmaxf(fabsf(xv[n].z), fabsf(xv[n].w))));
     }
     m = wave_maximum(m);
     if (lane == 0) red_f[wave] = m;
     __syncthreads();
-    m = fmaxf(fmaxf(red_f[0], red_f[1]), fmaxf(red_f[2], red_f[3]));
+    m = wave_maximum(red_f[lane < WB ? lane : 0]);  // one LDS read per lane, then DPP
     float act = m / 127.0f;
     if (act == 0.0f) act = 1.0f;
-    const float inv = 1.0f / act;
-    int sq = 0;
+    const float inv = quant_inv(act), thr = quant_thr(inv);
+    // All of this thread's elements on the fast rounding, then one ballot for
+    // the rare redo by exact division.
+    float rq[NX][4];
+    bool redo = false;
+#pragma unroll
+    for (int n = 0; n < NX; ++n) {
+        redo |= !quant_fast(xv[n].x, inv, thr, rq[n][0]);
+        redo |= !quant_fast(xv[n].y, inv, thr, rq[n][1]);
+        redo |= !quant_fast(xv[n].z, inv, thr, rq[n][2]);
+        redo |= !quant_fast(xv[n].w, inv, thr, rq[n][3]);
+    }
+    if (__builtin_amdgcn_ballot_w64(redo)) {
+        if (redo) {
+#pragma unroll
+            for (int n = 0; n < NX; ++n) {
+                const float e4[4] = {xv[n].x, xv[n].y, xv[n].z, xv[n].w};
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    float r;
+                    if (!quant_fast(e4[t], inv, thr, r)) rq[n][t] = roundf(e4[t] / act);
+                }
+            }
+        }
+    }
     uint8_t* l8 = reinterpret_cast<uint8_t*>(lds);
 #pragma unroll
     for (int n = 0; n < NX; ++n) {
-        const int i = tid + 256 * n;
+        const int i = tid + nt * n;
         if (i >= k4) continue;
-        const float e4[4] = {xv[n].x, xv[n].y, xv[n].z, xv[n].w};
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-            const int q = quant_act(e4[t], act, inv);
-            sq += q;
+            const int q = quant_clamp(rq[n][t]);
             const int e = 4 * i + t;
             const int c = e / EU, r = e % EU, d = r / E, r2 = r % E, bb = r2 / KS, k = r2 % KS;
             l8[4 * ((d * nU + c) * KS + k) + bb] = uint8_t(int8_t(q));
         }
     }
-    sq = wave_total_i(sq);
-    if (lane == 0) red_i[wave] = sq;
     __syncthreads();
-    sq = red_i[0] + red_i[1] + red_i[2] + red_i[3];
     if (act_out && blockIdx.x == 0 && tid == 0) act_out[b] = act;
+    // The wave's lanes read every xq byte exactly once (lane c + 64 j holds code
+    // vector c + 64 j), so each lane's share of sum(xq) comes from the same
+    // words, by a dot with ones; -OFF * sum(xq) then rides in the row totals.
     uint32_t xw[NC][4][KS];
+    int sq = 0;
 #pragma unroll
-    for (int c = 0; c < NC; ++c)
+    for (int c = 0; c < NC; ++c) {
 #pragma unroll
         for (int d = 0; d < 4; ++d)
 #pragma unroll
             for (int k = 0; k < KS; ++k) xw[c][d][k] = lds[(d * nU + min(lane + 64 * c, nU - 1)) * KS + k];
+        if (lane + 64 * c < nU) {
+#pragma unroll
+            for (int d = 0; d < 4; ++d)
+#pragma unroll
+                for (int k = 0; k < KS; ++k) sq = __builtin_amdgcn_sdot4(int(xw[c][d][k]), 0x01010101, sq, false);
+        }
+    }
+    const int osq = N::OFF * sq;
 #pragma unroll
     for (int rw = 0; rw < RW; ++rw) {
         int acc = 0;
@@ -168,7 +219,7 @@ __global__ void __launch_bounds__(256) k_narrow_i8v(const uint8_t* __restrict__ 
                         acc = __builtin_amdgcn_sdot4(int((wd[d] >> (B * k)) & N::MASK), int(xw[c][d][k]), acc, false);
             }
         }
-        acc = N::MUL * wave_total_i(acc) - N::OFF * sq;
+        acc = wave_total_i(N::MUL * acc - osq);
         const int r = r0 + rw;
         if (lane == 0 && r < rows) {
             if (acc_out) acc_out[int64_t(b) * rows + r] = acc;
@@ -197,9 +248,9 @@ __global__ void __launch_bounds__(256) k_narrow_i8(const uint8_t* __restrict__ c
     m = fmaxf(fmaxf(red_f[0], red_f[1]), fmaxf(red_f[2], red_f[3]));
     float act = m / 127.0f;
     if (act == 0.0f) act = 1.0f;
-    const float inv = 1.0f / act;
+    const float inv = quant_inv(act), thr = quant_thr(inv);
     int8_t* l8 = reinterpret_cast<int8_t*>(lds);
-    for (int j = tid; j < K; j += 256) l8[j] = int8_t(quant_act(xb[j], act, inv));
+    for (int j = tid; j < K; j += 256) l8[j] = int8_t(quant_act(xb[j], act, inv, thr));
     __syncthreads();
     if (act_out && blockIdx.x == 0 && tid == 0) act_out[b] = act;
     const int r0 = blockIdx.x * rows_per_block, r1 = min(rows, r0 + rows_per_block);
@@ -302,18 +353,54 @@ __global__ void __launch_bounds__(256) k_native_t_sum(const double* __restrict__
     *o = TX(double(*o) + s);
 }
 
-template <int F, int NC, int NX>
-void launch_narrow_v(const DevBlob& b, const float* x, float* y, int32_t* acc, float* act, int batch, hipStream_t s) {
+// Launch geometry of k_narrow_i8v: about one block per CU (256), each of WB
+// waves (4..16) holding RW rows (1, 2 or 4), and NX float4 of x per thread.
+template <int F, int NC, int NX, int RW>
+void launch_narrow_g(const DevBlob& b, const float* x, float* y, int32_t* acc, float* act, int batch, hipStream_t s,
+                     int wb) {
     const int rows = int(b.rows), K = int(b.cols);
-    if constexpr (NC == 1) {  // 8 rows per wave while that still leaves ~200 blocks
-        if ((rows + 31) / 32 >= 192) {
-            hipLaunchKernelGGL((k_narrow_i8v<F, NC, NX, 8>), dim3(unsigned((rows + 31) / 32), unsigned(batch)),
-                               dim3(256), size_t(K), s, b.codes, b.tensor_scale, rows, K, x, y, acc, act);
-            return;
-        }
+    const int per = wb * RW;
+    hipLaunchKernelGGL((k_narrow_i8v<F, NC, NX, RW>), dim3(unsigned((rows + per - 1) / per), unsigned(batch)),
+                       dim3(unsigned(64 * wb)), size_t(K), s, b.codes, b.tensor_scale, rows, K, x, y, acc, act);
+}
+
+template <int F, int NC, int RW>
+void launch_narrow_x(const DevBlob& b, const float* x, float* y, int32_t* acc, float* act, int batch, hipStream_t s,
+                     int wb) {
+    // NX = float4 of x per thread, exact for 1..4, 6 and 8 (K <= 8192, wb >= 4).
+    // NC = RW = 4 holds 16 code vectors per lane: there the block takes enough
+    // waves for NX <= 4, which keeps the kernel within its registers.
+    if constexpr (NC == 4 && RW == 4) wb = std::max(wb, (int(b.cols) / 4 + 255) / 256);
+    const int nx = (int(b.cols) / 4 + 64 * wb - 1) / (64 * wb);
+    if (nx <= 1) launch_narrow_g<F, NC, 1, RW>(b, x, y, acc, act, batch, s, wb);
+    else if (nx <= 2) launch_narrow_g<F, NC, 2, RW>(b, x, y, acc, act, batch, s, wb);
+    else if (nx <= 3) launch_narrow_g<F, NC, 3, RW>(b, x, y, acc, act, batch, s, wb);
+    else if (nx <= 4 || (NC == 4 && RW == 4)) launch_narrow_g<F, NC, 4, RW>(b, x, y, acc, act, batch, s, wb);
+    else if constexpr (NC < 4 || RW < 4) {
+        if (nx <= 6) launch_narrow_g<F, NC, 6, RW>(b, x, y, acc, act, batch, s, wb);
+        else launch_narrow_g<F, NC, 8, RW>(b, x, y, acc, act, batch, s, wb);
     }
-    hipLaunchKernelGGL((k_narrow_i8v<F, NC, NX, 4>), dim3(unsigned((rows + 15) / 16), unsigned(batch)), dim3(256),
-                       size_t(K), s, b.codes, b.tensor_scale, rows, K, x, y, acc, act);
+}
+
+// Block shape of k_narrow_i8v: rows per block ~ rows / 256 (one block per
+// CU), as wb waves (4..16) of rw rows each. Measured on the ternary pair:
+// 2560 rows run best as 10 waves x 1 row (256 blocks), 6912 rows as 7-8 waves
+// x 4 rows (216-247 blocks; 14 x 2 is 5 % slower, 16 x 1 in 432 blocks 25 %).
+struct NarrowShape {
+    int wb, rw;
+};
+inline NarrowShape narrow_shape(int rows) {
+    const int want = (rows + 255) / 256;
+    const int rw = want <= 16 ? 1 : 4;
+    return {std::max(4, std::min(16, (want + rw - 1) / rw)), rw};
+}
+
+template <int F, int NC>
+void launch_narrow_v(const DevBlob& b, const float* x, float* y, int32_t* acc, float* act, int batch, hipStream_t s) {
+    const NarrowShape sh = narrow_shape(int(b.rows));
+    if (sh.rw == 1) launch_narrow_x<F, NC, 1>(b, x, y, acc, act, batch, s, sh.wb);
+    else if (sh.rw == 2) launch_narrow_x<F, NC, 2>(b, x, y, acc, act, batch, s, sh.wb);
+    else launch_narrow_x<F, NC, 4>(b, x, y, acc, act, batch, s, sh.wb);
 }
 
 template <int F>
@@ -321,37 +408,11 @@ int launch_narrow_f(const DevBlob& b, const float* x, float* y, int32_t* acc, fl
     const int rows = int(b.rows), K = int(b.cols);
     constexpr int EU = 128 / Narrow<F>::B;  // codes per 16-byte vector
     if (K % EU == 0 && K <= 8192 && K / EU <= 256) {
-        const int nu = K / EU, nx = (K + 1023) / 1024;  // NC = ceil(nu / 64) vectors per lane and row
-        if (nu <= 64) {
-            switch (nx) {
-            case 1: launch_narrow_v<F, 1, 1>(b, x, y, acc, act, batch, s); break;
-            case 2: launch_narrow_v<F, 1, 2>(b, x, y, acc, act, batch, s); break;
-            case 3: launch_narrow_v<F, 1, 3>(b, x, y, acc, act, batch, s); break;
-            case 4: launch_narrow_v<F, 1, 4>(b, x, y, acc, act, batch, s); break;
-            case 5: launch_narrow_v<F, 1, 5>(b, x, y, acc, act, batch, s); break;
-            case 6: launch_narrow_v<F, 1, 6>(b, x, y, acc, act, batch, s); break;
-            case 7: launch_narrow_v<F, 1, 7>(b, x, y, acc, act, batch, s); break;
-            default: launch_narrow_v<F, 1, 8>(b, x, y, acc, act, batch, s); break;
-            }
-        } else if (nu <= 128) {
-            switch (nx) {
-            case 1: case 2: launch_narrow_v<F, 2, 2>(b, x, y, acc, act, batch, s); break;
-            case 3: launch_narrow_v<F, 2, 3>(b, x, y, acc, act, batch, s); break;
-            case 4: launch_narrow_v<F, 2, 4>(b, x, y, acc, act, batch, s); break;
-            case 5: launch_narrow_v<F, 2, 5>(b, x, y, acc, act, batch, s); break;
-            case 6: launch_narrow_v<F, 2, 6>(b, x, y, acc, act, batch, s); break;
-            case 7: launch_narrow_v<F, 2, 7>(b, x, y, acc, act, batch, s); break;
-            default: launch_narrow_v<F, 2, 8>(b, x, y, acc, act, batch, s); break;
-            }
-        } else {  // Int8 rows of more than 2048 columns
-            switch (nx) {
-            case 3: launch_narrow_v<F, 4, 3>(b, x, y, acc, act, batch, s); break;
-            case 4: launch_narrow_v<F, 4, 4>(b, x, y, acc, act, batch, s); break;
-            case 5: launch_narrow_v<F, 4, 5>(b, x, y, acc, act, batch, s); break;
-            case 6: launch_narrow_v<F, 4, 6>(b, x, y, acc, act, batch, s); break;
-            case 7: launch_narrow_v<F, 4, 7>(b, x, y, acc, act, batch, s); break;
-            default: launch_narrow_v<F, 4, 8>(b, x, y, acc, act, batch, s); break;
-            }
+        const int nu = K / EU;  // NC = ceil(nu / 64) vectors per lane and row; nu <= 8192 / EU
+        if (nu <= 64) launch_narrow_v<F, 1>(b, x, y, acc, act, batch, s);
+        else if constexpr (EU <= 64) {
+            if (nu <= 128) launch_narrow_v<F, 2>(b, x, y, acc, act, batch, s);
+            else if constexpr (EU <= 32) launch_narrow_v<F, 4>(b, x, y, acc, act, batch, s);
         }
         return int(hipGetLastError());
     }
