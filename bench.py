@@ -88,16 +88,21 @@ DECODE = {
 COPY_FETCH_SCALE = 65536.0 / 32779.5
 COPY_WRITE_SCALE = 65536.0 / 65536.0
 PMC_KIB = {
-    "q4k_4096x14336": (18951.5, 56.0),
+    "q4k_4096x14336": (18946.0, 56.0),
+    "q4k_4096x4096": (5497.0, 16.0),
+    "q4k_14336x4096": (19121.5, 16.0),
+    "q8_0_4096x4096": (9329.0, 16.0),
+    "q8_0_4096x14336": (32450.56, 56.0),
+    "q8_0_14336x4096": (32657.0, 16.0),
+    "q6k_4096x4096": (7035.0, 16.0),
+    "q6k_4096x14336": (24330.0, 56.0),
+    "q6k_14336x4096": (24489.5, 16.0),
+    "q4_0_4096x4096": (5241.0, 16.0),
     "ternary_2560x6912": (2241.25, 30.84),
     "ternary_6912x2560": (2308.0, 16.0),
 }
 # Where each PMC_KIB entry comes from (the profile summary under profiles/).
-PMC_SOURCE = {
-    "q4k_4096x14336": "profiles/k_gemv_rpl_q4k_4096x14336_pmc_traffic.txt",
-    "ternary_2560x6912": "profiles/k_narrow_i8v_ternary_2560x6912.txt",
-    "ternary_6912x2560": "profiles/k_narrow_i8v_ternary_6912x2560.txt",
-}
+PMC_SOURCE = {w: f"profiles/{'k_narrow_i8v' if w.startswith('ternary') else 'k_gemv_rpl'}_{w}.txt" for w in PMC_KIB}
 METRIC = "dequant-GEMV HBM GB/s (% of peak) at 4096->14336 Q4_K b=1; decode tokens/s"
 
 
