@@ -1,6 +1,7 @@
 """GPU parity of the batched prefill (wv_matmul*) through the C ABI.
 
-Row-interleaved Q4_K blobs run the fp16-MFMA GEMM; the bar there is the
+Row-interleaved Q4_K blobs run the fp16-MFMA GEMM (each token row scaled by
+a power of two into fp16's range); the bar there is the
 north-star's bf16/fp16-MFMA tolerance: max|Y - Y_ref| / max|Y_ref| <= 2e-3
 against the f64 textbook product over the reference's dequantized weights
 (which is what welvet's M independent f64-accumulated GEMVs compute, up to
@@ -105,6 +106,40 @@ def test_prefill_other_formats_mfma(fmt, shape, m):
         y = d.matmul(x)
         assert normwise(y, ref) <= TOL_MFMA
         assert rowwise(y, ref) <= 4 * TOL_MFMA
+    d.free()
+
+
+@pytest.mark.parametrize("fmt", ["Q4_K", "Q6_K"])
+@pytest.mark.parametrize("m", [32, 64, 128, 300])
+def test_prefill_outlier_and_tiny_activations(fmt, m):
+    """Token rows the fp16 operand cannot hold unscaled: a few columns at
+    +-1e3 and at +-1e5 (past fp16's 65504), a row of activations around 1e-9
+    (fp16-subnormal), an all-zero row. Each row is scaled by a power of two
+    before the fp16 cast and back in the epilogue, so every row meets the
+    2e-3 bar on its own and nothing turns inf or NaN."""
+    rows, cols = 448, 2048
+    print(f"[gpu] prefill outliers {fmt} M={m}", flush=True)
+    rng = np.random.default_rng(11 + m)
+    w = (rng.standard_normal(rows * cols, dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+    p = wv.pack(fmt, w, rows, cols)
+    wd = oracle.unpack(oracle.Packed(p.fmt, rows, cols, p.raw, p.scales, p.meta, p.block_weights, p.mins))
+    wd = wd.reshape(rows, cols).astype(np.float64)
+    d = wv.upload(p)
+    x = rng.standard_normal((m, cols)).astype(np.float32)
+    for r in range(4):
+        cs = rng.choice(cols, 5, replace=False)
+        x[r, cs] = rng.choice([-1.0, 1.0], 5) * 1e3
+        x[r + 4, cs] = rng.choice([-1.0, 1.0], 5) * 1e5
+    x[8] *= np.float32(1e-9)
+    x[9] = 0.0
+    x[m - 1, :3] = [7e4, -9e4, 3.3e5]  # the last (possibly ragged) token tile too
+    ref = x.astype(np.float64) @ wd.T
+    y = d.matmul(x)
+    assert np.isfinite(y).all()
+    assert np.array_equal(y[9], np.zeros(rows, np.float32))
+    err = rowwise(y, ref)
+    print(f"[gpu]   rowwise err {err:.3e}", flush=True)
+    assert err <= TOL_MFMA
     d.free()
 
 

@@ -4,13 +4,15 @@
 // (forwardSIMDBlockFused, layers/dense/simd_block.go:17-39), within the 2e-3
 // tolerance of an fp16 contraction.
 //
-// For token tiles of 64 and more, X is first converted once to fp16
-// (k_x_f16), so the GEMM streams half the bytes for the operand every N-tile
-// re-reads and spends no VALU on it. A 32-token tile reads X as f32 and packs
-// it while staging instead (one launch less; its X traffic is small). Global
-// loads run D K-steps ahead of use in a register ring: a step holds only 64
-// columns, so one step of look-ahead would expose a full memory latency per
-// step.
+// X is first converted once to fp16 (k_x_f16r), so the GEMM streams half the
+// bytes for the operand every N-tile re-reads and spends no VALU on it. Each
+// token row is scaled by a power of two that puts its max|x| in [2^14, 2^15)
+// before the cast, and the epilogue multiplies the row back: the scaling is
+// exact, so rows that fit fp16 get the same fp16 values as an unscaled cast,
+// while outlier rows (|x| > 65504) stay finite and rows of tiny activations
+// keep their precision instead of going subnormal. Global loads run D K-steps
+// ahead of use in a register ring: a step holds only 64 columns, so one step of
+// look-ahead would expose a full memory latency per step.
 //
 // Tiles: a block computes BM tokens x 128 output rows (two 64-row groups),
 // stepping K by 64 columns (two 32-column chunks of a super-block), with both
@@ -34,6 +36,7 @@
 #include <cstdint>
 #include <type_traits>
 
+#include "wave_ops.h"
 #include "wv_internal.h"
 
 namespace wv {
@@ -357,29 +360,75 @@ struct GemmLin {
 
 struct GemmArgs {
     RplArgs w;
-    const uint4* xh;  // [M][K/8] fp16 8-column blocks in permuted k order (BM >= 64)
-    const float* x;   // [M][K] f32, packed while staged (BM == 32)
+    const uint4* xh;       // [M][K/8] fp16 8-column blocks in permuted k order, row m scaled by 1 / xscale[m]
+    const float* xscale;   // [M] power-of-two factor of each row's fp16 copy
     float* y;         // [M][rows] (splits == 1) or partials [split][M][rows]
     int M, K;
     int sb_per_split;
 };
 
-// X f32 [n8 blocks of 8] -> fp16 blocks in k order [0,4,1,5,2,6,3,7]
-// (dequant8, ORD 0) or [0,2,4,6,1,3,5,7] (dequant8p, ORD 1).
+// 8 columns of X times `up`, as fp16 pairs in the k order ORD.
 template <int ORD>
-__global__ void __launch_bounds__(256) k_x_f16(const float4* __restrict__ x, uint4* __restrict__ xh, int64_t n8) {
-    const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
-    if (i >= n8) return;
-    const float4 lo = x[2 * i], hi = x[2 * i + 1];
+__device__ __forceinline__ uint4 pack_x8(float4 lo, float4 hi, float up) {
+    lo = make_float4(lo.x * up, lo.y * up, lo.z * up, lo.w * up);
+    hi = make_float4(hi.x * up, hi.y * up, hi.z * up, hi.w * up);
     if constexpr (ORD == 0)
-        xh[i] = make_uint4(pack_h2(lo.x, hi.x), pack_h2(lo.y, hi.y), pack_h2(lo.z, hi.z), pack_h2(lo.w, hi.w));
+        return make_uint4(pack_h2(lo.x, hi.x), pack_h2(lo.y, hi.y), pack_h2(lo.z, hi.z), pack_h2(lo.w, hi.w));
     else
-        xh[i] = make_uint4(pack_h2(lo.x, lo.z), pack_h2(hi.x, hi.z), pack_h2(lo.y, lo.w), pack_h2(hi.y, hi.w));
+        return make_uint4(pack_h2(lo.x, lo.z), pack_h2(hi.x, hi.z), pack_h2(lo.y, lo.w), pack_h2(hi.y, hi.w));
+}
+__device__ __forceinline__ float absmax8(float4 lo, float4 hi) {
+    return fmaxf(fmaxf(fmaxf(fabsf(lo.x), fabsf(lo.y)), fmaxf(fabsf(lo.z), fabsf(lo.w))),
+                 fmaxf(fmaxf(fabsf(hi.x), fabsf(hi.y)), fmaxf(fabsf(hi.z), fabsf(hi.w))));
+}
+// The row's factor from its max|x| (the block-wide reduction), 2^-shift.
+__device__ __forceinline__ float row_shift_up(float mx, float* red, float* xscale_m, int t) {
+    mx = wave_maximum(mx);
+    if ((t & 63) == 0) red[t >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    int sh = 0;  // x is multiplied by 2^sh
+    if (mx > 0.f && mx <= 3.4028235e38f) sh = min(126, max(-126, 14 - ilogbf(mx)));
+    if (t == 0) *xscale_m = ldexpf(1.0f, -sh);
+    return ldexpf(1.0f, sh);
+}
+// X f32 [M][K] -> fp16 blocks of 8 in k order [0,4,1,5,2,6,3,7] (dequant8,
+// ORD 0) or [0,2,4,6,1,3,5,7] (dequant8p, ORD 1), one block per token row:
+// the row's max|x| picks xscale = 2^e with max|x| / xscale in [2^14, 2^15)
+// (1 for an all-zero or non-finite row), and the blocks hold x / xscale.
+// Rows of up to 256 * kXRegs blocks of 8 are read once, into registers.
+constexpr int kXRegs = 8;
+template <int ORD>
+__global__ void __launch_bounds__(256) k_x_f16r(const float4* __restrict__ x, uint4* __restrict__ xh,
+                                                 float* __restrict__ xscale, int kb8) {
+    __shared__ float red[4];
+    const int m = blockIdx.x, t = threadIdx.x;
+    const float4* xr = x + int64_t(m) * kb8 * 2;
+    uint4* out = xh + int64_t(m) * kb8;
+    float mx = 0.f;
+    if (kb8 <= 256 * kXRegs) {
+        float4 lo[kXRegs], hi[kXRegs];
+#pragma unroll
+        for (int j = 0; j < kXRegs; ++j) {
+            const int i = min(t + 256 * j, kb8 - 1);
+            lo[j] = xr[2 * i];
+            hi[j] = xr[2 * i + 1];
+        }
+#pragma unroll
+        for (int j = 0; j < kXRegs; ++j) mx = fmaxf(mx, absmax8(lo[j], hi[j]));
+        const float up = row_shift_up(mx, red, xscale + m, t);
+#pragma unroll
+        for (int j = 0; j < kXRegs; ++j)
+            if (t + 256 * j < kb8) out[t + 256 * j] = pack_x8<ORD>(lo[j], hi[j], up);
+        return;
+    }
+    for (int i = t; i < kb8; i += 256) mx = fmaxf(mx, absmax8(xr[2 * i], xr[2 * i + 1]));
+    const float up = row_shift_up(mx, red, xscale + m, t);
+    for (int i = t; i < kb8; i += 256) out[i] = pack_x8<ORD>(xr[2 * i], xr[2 * i + 1], up);
 }
 
 template <int BM, int WM, int D>
 __global__ void __launch_bounds__(256) k_gemm_q4k(GemmArgs ga) {
-    constexpr bool kXF32 = BM == 32;
     constexpr int WN = 4 / WM;
     constexpr int TM = BM / WM / 32, TN = BN / WN / 32;
     constexpr int XB = BM * (BK / 8) / 256;  // 8-column X blocks per thread per K-step
@@ -407,8 +456,7 @@ __global__ void __launch_bounds__(256) k_gemm_q4k(GemmArgs ga) {
         uint4 c;
         uint32_t meta;
         float2 dd;
-        uint4 xv[XB];  // fp16 block, or (f32 X) columns 0..3 as bits
-        float4 xh[kXF32 ? XB : 1];  // (f32 X) columns 4..7
+        uint4 xv[XB];  // fp16 blocks of X
     };
     auto load = [&](int s, Regs& r) {
         const int sb = sb0 + s / 4, j = 2 * (s & 3) + jj;
@@ -420,13 +468,7 @@ __global__ void __launch_bounds__(256) k_gemm_q4k(GemmArgs ga) {
 #pragma unroll
         for (int i = 0; i < XB; ++i) {
             const int f = t + 256 * i, m = min(mblk * BM + f / 8, ga.M - 1);
-            if constexpr (kXF32) {
-                const float4* xp = reinterpret_cast<const float4*>(ga.x + (int64_t(m) * kb8 + k8 + f % 8) * 8);
-                r.xv[i] = __builtin_bit_cast(uint4, xp[0]);
-                r.xh[i] = xp[1];
-            } else {
-                r.xv[i] = ga.xh[int64_t(m) * kb8 + k8 + f % 8];
-            }
+            r.xv[i] = ga.xh[int64_t(m) * kb8 + k8 + f % 8];
         }
     };
     auto store = [&](const Regs& r, int buf) {
@@ -444,12 +486,7 @@ __global__ void __launch_bounds__(256) k_gemm_q4k(GemmArgs ga) {
 #pragma unroll
         for (int i = 0; i < XB; ++i) {
             const int f = t + 256 * i;
-            uint4 v = r.xv[i];
-            if constexpr (kXF32) {  // k order [0,4,1,5,2,6,3,7], as the nibble extraction pairs W
-                const float4 lo = __builtin_bit_cast(float4, r.xv[i]), hi = r.xh[i];
-                v = make_uint4(pack_h2(lo.x, hi.x), pack_h2(lo.y, hi.y), pack_h2(lo.z, hi.z), pack_h2(lo.w, hi.w));
-            }
-            *reinterpret_cast<uint4*>(&xs[buf][(f / 8) * LDK + 8 * (f % 8)]) = v;
+            *reinterpret_cast<uint4*>(&xs[buf][(f / 8) * LDK + 8 * (f % 8)]) = r.xv[i];
         }
     };
 
@@ -513,7 +550,7 @@ __global__ void __launch_bounds__(256) k_gemm_q4k(GemmArgs ga) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int m = mblk * BM + wm * (BM / WM) + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (m < ga.M) out[int64_t(m) * a.rows + n] = acc[i][j][r];
+                if (m < ga.M) out[int64_t(m) * a.rows + n] = acc[i][j][r] * ga.xscale[m];
             }
         }
 }
@@ -630,7 +667,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int m = mblk * BM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (m < ga.M) out[int64_t(m) * a.rows + n] = acc[i][T][r];
+                if (m < ga.M) out[int64_t(m) * a.rows + n] = acc[i][T][r] * ga.xscale[m];
             }
         }
 }
@@ -692,7 +729,7 @@ bool gemm_supported(const DevBlob& b, int M) {
 
 // Token tiles from kPwMin up run k_gemm_q4k_pw (256-row tiles, one block per
 // CU); smaller ones k_gemm_q4k (128-row tiles). At M = 32 both kernels take
-// 20.5 us, and k_gemm_q4k needs no fp16 copy of X.
+// 20.5 us.
 constexpr int kPwMin = 128;
 bool use_pw(const DevBlob& b, int bm) { return bm >= kPwMin || b.fmt != FMT_Q4_K; }
 void gemm_plan(const DevBlob& b, int M, int& bm, int& splits, int& sb_per_split) {
@@ -714,13 +751,14 @@ void gemm_plan(const DevBlob& b, int M, int& bm, int& splits, int& sb_per_split)
     splits = (a.nsb + sb_per_split - 1) / sb_per_split;
 }
 
-// Scratch floats: the fp16 copy of X (M*K halves, token tiles of 64 and more)
-// followed by the split-K partials.
+// Scratch floats: the fp16 copy of X (M*K halves), the M row factors, then
+// the split-K partials (each piece 256-byte aligned).
+size_t gemm_x_floats(const DevBlob& b, int M) { return (size_t(M) * size_t(b.cols) / 2 + 63) / 64 * 64; }
+size_t gemm_scale_floats(int M) { return (size_t(M) + 63) / 64 * 64; }
 size_t gemm_scratch_floats(const DevBlob& b, int M) {
     int bm = 0, splits = 1, per = 0;
     gemm_plan(b, M, bm, splits, per);
-    const size_t xh = bm == 32 && !use_pw(b, bm) ? 0 : (size_t(M) * size_t(b.cols) / 2 + 63) / 64 * 64;
-    return xh + (splits > 1 ? size_t(splits) * size_t(M) * size_t(b.rows) : 0);
+    return gemm_x_floats(b, M) + gemm_scale_floats(M) + (splits > 1 ? size_t(splits) * size_t(M) * size_t(b.rows) : 0);
 }
 
 // The packed-W GEMM for b's format with TM 32-token tiles per wave.
@@ -755,25 +793,22 @@ int launch_gemm(const DevBlob& b, const float* d_x, float* d_y, int M, void* str
     if (!gemm_supported(b, M)) return int(hipErrorInvalidValue);
     int bm = 0, splits = 1, per = 0;
     gemm_plan(b, M, bm, splits, per);
-    if (gemm_scratch_floats(b, M) && !d_scratch) return int(hipErrorInvalidValue);
-    uint4* xh = nullptr;
-    float* part = d_scratch;
+    if (!d_scratch) return int(hipErrorInvalidValue);
     const bool pw = use_pw(b, bm);
-    if (bm != 32 || pw) {
-        const int64_t n8 = int64_t(M) * b.cols / 8;
-        xh = reinterpret_cast<uint4*>(d_scratch);
-        part = d_scratch + (size_t(M) * size_t(b.cols) / 2 + 63) / 64 * 64;
-        if (pw)
-            hipLaunchKernelGGL(k_x_f16<1>, dim3(unsigned((n8 + 255) / 256)), dim3(256), 0, s,
-                               reinterpret_cast<const float4*>(d_x), xh, n8);
-        else
-            hipLaunchKernelGGL(k_x_f16<0>, dim3(unsigned((n8 + 255) / 256)), dim3(256), 0, s,
-                               reinterpret_cast<const float4*>(d_x), xh, n8);
-    }
+    uint4* xh = reinterpret_cast<uint4*>(d_scratch);
+    float* xscale = d_scratch + gemm_x_floats(b, M);
+    float* part = xscale + gemm_scale_floats(M);
+    const int kb8 = int(b.cols / 8);
+    if (pw)
+        hipLaunchKernelGGL(k_x_f16r<1>, dim3(unsigned(M)), dim3(256), 0, s, reinterpret_cast<const float4*>(d_x), xh,
+                           xscale, kb8);
+    else
+        hipLaunchKernelGGL(k_x_f16r<0>, dim3(unsigned(M)), dim3(256), 0, s, reinterpret_cast<const float4*>(d_x), xh,
+                           xscale, kb8);
     GemmArgs ga;
     ga.w = b.rpl;
     ga.xh = xh;
-    ga.x = d_x;
+    ga.xscale = xscale;
     ga.y = splits > 1 ? part : d_y;
     ga.M = M;
     ga.K = int(b.cols);
