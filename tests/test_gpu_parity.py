@@ -387,3 +387,37 @@ def test_nonfinite_x_propagates(fmt, shape):
     ref = oracle.reference_y(oracle_packed(p), x[2:])[0]
     assert normwise(y[2], ref) <= TOL  # the finite batch row is unaffected
     d.free()
+
+
+@pytest.mark.parametrize("shape", [(14336, 4096), (4096, 14336)])
+def test_q4k_outlier_activations(shape):
+    """x ~ N(0, 1) with 8 channels at +-1e3 and 4 at +-1e5 (LLM-style
+    outliers) through the row-interleaved Q4_K kernel, whose x planes are 24-bit
+    fixed point with one exponent per 32-column chunk. Bars: the 1e-5
+    normwise one, and per row the kernel's error model, |y - y_ref| <=
+    sum_k |w_k| * 2^-23 * max|x| over k's chunk (the fixed-point step) +
+    2^-20 * sum_k |w_k x_k| (f32 accumulation), with every row's error
+    printed relative to that row's sum_k |w_k x_k|."""
+    rows, cols = shape
+    print(f"[gpu] outliers Q4_K {cols}->{rows}", flush=True)
+    w, rng = weights(rows, cols, 77)
+    x = rng.standard_normal(cols).astype(np.float32)
+    cs = rng.choice(cols, 12, replace=False)
+    x[cs[:8]] = rng.choice([-1.0, 1.0], 8) * 1e3
+    x[cs[8:]] = rng.choice([-1.0, 1.0], 4) * 1e5
+    p, d = upload("Q4_K", w, rows, cols)
+    assert d.info()["layout"] == "row-interleaved"
+    op = oracle_packed(p)
+    ref = oracle.reference_y(op, x)[0]
+    y = d.matvec(x).astype(np.float64)
+    assert normwise(y, ref) <= TOL
+    wa = np.abs(oracle.unpack(op).reshape(rows, cols).astype(np.float64))
+    cmax = np.repeat(np.abs(x.astype(np.float64)).reshape(-1, 32).max(axis=1), 32)
+    scale = wa @ np.abs(x.astype(np.float64))
+    bound = wa @ (cmax * 2.0 ** -23) + 2.0 ** -20 * scale
+    err = np.abs(y - ref)
+    rel = err / scale
+    print(f"[gpu]   err/sum|w x|: max {rel.max():.2e} median {np.median(rel):.2e}; "
+          f"err/bound max {(err / bound).max():.3f}", flush=True)
+    assert (err <= bound).all()
+    d.free()
