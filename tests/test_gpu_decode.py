@@ -163,3 +163,68 @@ def test_decode_full_width_one_layer():
     dec, ref, keep = build(cfg, "Q4_K", 21, kv_fill=2047)
     check_against_oracle(dec, ref, token=17, pos=2047, steps=1)
     dec.free()
+
+
+@pytest.mark.timeout(900)
+def test_decode_config5_full():
+    """BASELINE config 5 as bench.py runs it: 32 layers (4 distinct Q4_K layers
+    cycled), hidden 4096, 32/8 heads x 128, SwiGLU 14336, vocab 32000, RoPE
+    5e5, RMSNorm 1e-5, 2047 cached positions + this step. One greedy step
+    against the f64 oracle (token, and logits within 1e-5 normwise), then two
+    fixed-position steps eager and as graph replays: finite, bit-identical,
+    and each against the oracle."""
+    print("[gpu] decode config 5 (32 layers, vocab 32000)", flush=True)
+    cfg = Config(n_layers=32, hidden=4096, n_heads=32, n_kv_heads=8, head_dim=128, ffn=14336, vocab=32000,
+                 max_seq=2048, rope_theta=5e5, rms_eps=1e-5)
+    rng = np.random.default_rng(55)
+    names = ("q", "k", "v", "o", "gate", "up", "down")
+    shapes = {"q": (cfg.q_dim, cfg.hidden), "k": (cfg.kv_dim, cfg.hidden), "v": (cfg.kv_dim, cfg.hidden),
+              "o": (cfg.hidden, cfg.q_dim), "gate": (cfg.ffn, cfg.hidden), "up": (cfg.ffn, cfg.hidden),
+              "down": (cfg.hidden, cfg.ffn)}
+    distinct = []
+    for i in range(4):
+        ps = [wv.pack("Q4_K", rng.standard_normal(shapes[n][0] * shapes[n][1], dtype=np.float32) * np.float32(0.02),
+                      *shapes[n]) for n in names]
+        dense = {n: dr.DenseW(p) for n, p in zip(names, ps)}
+        an = (1.0 + 0.1 * rng.standard_normal(cfg.hidden)).astype(np.float32)
+        fn = (1.0 + 0.1 * rng.standard_normal(cfg.hidden)).astype(np.float32)
+        distinct.append((ps, dense, an, fn))
+        print(f"[gpu]   distinct layer {i} packed", flush=True)
+    dec = Decoder(cfg)
+    ref_layers = []
+    for L in range(cfg.n_layers):
+        ps, dense, an, fn = distinct[L % 4]
+        dec.set_layer(L, [wv.upload(p) for p in ps], an, fn)
+        ref_layers.append((dense, an, fn))
+    pl = wv.pack("Q4_K", rng.standard_normal(cfg.vocab * cfg.hidden, dtype=np.float32) * np.float32(0.02),
+                 cfg.vocab, cfg.hidden)
+    fnorm = (1.0 + 0.1 * rng.standard_normal(cfg.hidden)).astype(np.float32)
+    emb = rng.standard_normal((cfg.vocab, cfg.hidden), dtype=np.float32)
+    dec.set_output(wv.upload(pl), fnorm, emb)
+    ref = dr.DecodeRef(cfg, ref_layers, dr.DenseW(pl), fnorm, emb)
+    for L in range(cfg.n_layers):
+        k = rng.standard_normal((cfg.max_seq - 1, cfg.kv_dim), dtype=np.float32)
+        v = rng.standard_normal((cfg.max_seq - 1, cfg.kv_dim), dtype=np.float32)
+        dec.set_kv(L, 0, k, v)
+        ref.set_kv(L, 0, k, v)
+    print("[gpu]   model resident", flush=True)
+    pos = cfg.max_seq - 1
+    tok = int(check_against_oracle(dec, ref, token=17, pos=pos, steps=1)[0])
+    # fixed position: each step recomputes position `pos` from the previous step's token
+    t_e, l_e = dec.generate(tok, pos, 2, advance_pos=False, want_logits=True)
+    assert np.isfinite(l_e).all()
+    dec.use_graph(True)
+    for _ in range(2):
+        t_g, l_g = dec.generate(tok, pos, 2, advance_pos=False, want_logits=True)
+        assert np.array_equal(t_e, t_g) and np.array_equal(l_e, l_g)
+    t = tok
+    for i in range(2):
+        rl, rt = ref.step(t, pos)
+        top2 = np.sort(rl)[-2:]
+        if top2[1] - top2[0] > TOL * np.abs(rl).max():
+            assert t_e[i] == rt
+        t = int(t_e[i])
+    err = float(np.abs(l_e.astype(np.float64) - rl).max() / np.abs(rl).max())
+    print(f"[gpu]   fixed-position logits normwise err {err:.3e}", flush=True)
+    assert err <= TOL
+    dec.free()
