@@ -421,3 +421,63 @@ def test_q4k_outlier_activations(shape):
           f"err/bound max {(err / bound).max():.3f}", flush=True)
     assert (err <= bound).all()
     d.free()
+
+
+def shared_scale_blob(kind, rows, cols, seed):
+    """AffinePacked with 32/128/256-column groups (BlobFromMLXAffine4-style:
+    random 4-bit words, per-group scale and bias) or BinaryPacked g128 (random
+    sign words, one scale per 128 weights)."""
+    rng = np.random.default_rng(seed)
+    if kind == "binary128":
+        words = rng.integers(0, 2**32, size=rows * cols // 32, dtype=np.uint64).astype(np.uint32)
+        scales = (np.abs(rng.standard_normal(rows * cols // 128)) * 0.02 + 1e-3).astype(np.float32)
+        return wv.PackedBlob("BinaryPacked", rows, cols, words.view(np.uint8), scales, None, 128), rng
+    group = int(kind[len("affine"):])
+    words = rng.integers(0, 2**32, size=rows * cols // 8, dtype=np.uint64).astype(np.uint32)
+    ng = rows * cols // group
+    scales = (np.abs(rng.standard_normal(ng)) * 0.01 + 1e-3).astype(np.float32)
+    mins = (rng.standard_normal(ng) * 0.05).astype(np.float32)
+    return wv.PackedBlob("AffinePacked", rows, cols, words.view(np.uint8), scales, np.array([4], np.uint8), group,
+                         mins=mins), rng
+
+
+def upload_blob(p, force_raw):
+    old = os.environ.get("WV_FORCE_RAW")
+    os.environ["WV_FORCE_RAW"] = "1" if force_raw else "0"
+    try:
+        return wv.upload(p)
+    finally:
+        if old is None:
+            os.environ.pop("WV_FORCE_RAW")
+        else:
+            os.environ["WV_FORCE_RAW"] = old
+
+
+@pytest.mark.parametrize("kind", ["affine32", "affine128", "affine256", "binary128"])
+@pytest.mark.parametrize("shape,batch", [((300, 2048), 3), ((130, 8192), 2), ((64, 256), 1), ((1000, 4096), 11)])
+def test_shared_scale_groups_row_interleaved(kind, shape, batch):
+    """AffinePacked groups of 32, 128 and 256 columns and BinaryPacked g128 on
+    the row-interleaved layout (one scale, and min, per 2^GSH chunks): the
+    forward (batch rows, K split at 130x8192, batch 11 past the split's 8),
+    MatVecT, the reference layout's result, and the prefill GEMM at M = 40."""
+    rows, cols = shape
+    print(f"[gpu] shared-scale {kind} {cols}->{rows} batch {batch}", flush=True)
+    p, rng = shared_scale_blob(kind, rows, cols, rows + batch)
+    op = oracle_packed(p)
+    d = upload_blob(p, False)
+    assert d.info()["layout"] == "row-interleaved"
+    x = rng.standard_normal((batch, cols)).astype(np.float32)
+    ref = oracle.reference_y(op, x)
+    y = d.matvec(x)
+    assert normwise(y, ref) <= TOL
+    dr_ = upload_blob(p, True)
+    assert dr_.info()["layout"] == "raw"
+    assert normwise(dr_.matvec(x), ref) <= TOL
+    dr_.free()
+    wd = oracle.unpack(op).reshape(rows, cols).astype(np.float64)
+    gy = rng.standard_normal((2, rows)).astype(np.float32)
+    gx0 = rng.standard_normal((2, cols)).astype(np.float32)
+    assert normwise(d.matvec_t(gy, gx0), gx0 + gy.astype(np.float64) @ wd) <= TOL
+    xm = rng.standard_normal((40, cols)).astype(np.float32)
+    assert normwise(d.matmul(xm), xm.astype(np.float64) @ wd.T) <= 2e-3
+    d.free()

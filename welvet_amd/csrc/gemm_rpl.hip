@@ -329,15 +329,17 @@ struct GemmCodes1 {
 };
 
 // The linear-code formats (the linear IQ formats, TernaryPacked, BinaryPacked
-// g32): w = scale*(q - MID2/2), one scale per 32 columns or two (SG16, one
-// per k16 step); one-bit codes read +-scale = (2*scale)*(q - 1/2).
-template <int FB, bool SG16, int MID2>
+// g32 and g128): w = scale*(q - MID2/2), one scale per 32 columns, two (SG16,
+// one per k16 step) or one per 2^GSH chunks; one-bit codes read +-scale =
+// (2*scale)*(q - 1/2).
+template <int FB, bool SG16, int MID2, int GSH = 0>
 struct GemmLin {
     using Codes = std::conditional_t<FB == 1, GemmCodes1, GemmCodes<FB>>;
+    static constexpr int NW = SG16 ? 16 : (8 >> GSH);  // metadata words per lane and super-block
     struct Ch { typename Codes::C c; uint32_t s0, s1; };
     static __device__ __forceinline__ Ch load(const RplArgs& a, int64_t ci, int64_t si, int j, int lane) {
-        const uint32_t* m = reinterpret_cast<const uint32_t*>(a.meta) + (si * 64 + lane) * (SG16 ? 16 : 8);
-        const uint32_t s0 = m[SG16 ? 2 * j : j];
+        const uint32_t* m = reinterpret_cast<const uint32_t*>(a.meta) + (si * 64 + lane) * NW;
+        const uint32_t s0 = m[SG16 ? 2 * j : (j >> GSH)];
         return {Codes::load(a, ci, lane), s0, SG16 ? m[2 * j + 1] : s0};
     }
     static __device__ __forceinline__ void bops(const Ch& c, int lane, half8 (&bf)[2][2]) {
@@ -774,9 +776,21 @@ int launch_pw(const DevBlob& b, dim3 grid, hipStream_t s, const GemmArgs& ga) {
     case FMT_Q4_1: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmB32<4, true, 0, 0u>, TM, 4>), grid, dim3(256), 0, s, ga); return 0;
     case FMT_Q5_0: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmB32<5, false, 16, 0u>, TM, 4>), grid, dim3(256), 0, s, ga); return 0;
     case FMT_Q5_1: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmB32<5, true, 0, 0u>, TM, 4>), grid, dim3(256), 0, s, ga); return 0;
-    case FMT_AFFINE: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmB32<4, true, 0, 0u, 1>, TM, 4>), grid, dim3(256), 0, s, ga); return 0;
-    case FMT_IQ1_S:
-    case FMT_BINARY: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmLin<1, false, 1>, TM, 4>), grid, dim3(256), 0, s, ga); return 0;
+    case FMT_AFFINE:
+        switch (b.block_weights) {
+        case 32: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmB32<4, true, 0, 0u, 0>, TM, 4>), grid, dim3(256), 0, s, ga); return 0;
+        case 64: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmB32<4, true, 0, 0u, 1>, TM, 4>), grid, dim3(256), 0, s, ga); return 0;
+        case 128: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmB32<4, true, 0, 0u, 2>, TM, 4>), grid, dim3(256), 0, s, ga); return 0;
+        case 256: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmB32<4, true, 0, 0u, 3>, TM, 4>), grid, dim3(256), 0, s, ga); return 0;
+        default: return int(hipErrorInvalidValue);
+        }
+    case FMT_BINARY:
+        if (b.block_weights == 128) {
+            hipLaunchKernelGGL((k_gemm_q4k_pw<GemmLin<1, false, 1, 2>, TM, 4>), grid, dim3(256), 0, s, ga);
+            return 0;
+        }
+        [[fallthrough]];
+    case FMT_IQ1_S: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmLin<1, false, 1>, TM, 4>), grid, dim3(256), 0, s, ga); return 0;
     case FMT_IQ2_XXS: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmLin<2, false, 3>, TM, 4>), grid, dim3(256), 0, s, ga); return 0;
     case FMT_IQ2_XS: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmLin<2, true, 3>, TM, 4>), grid, dim3(256), 0, s, ga); return 0;
     case FMT_IQ3_XXS: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmLin<3, false, 7>, TM, 4>), grid, dim3(256), 0, s, ga); return 0;

@@ -232,7 +232,8 @@ struct RplKxI : RplQ4KI {
 template <int B, bool MIN, int OFF, uint32_t XR, int GSH = 0>
 struct RplB32I {
     // GSH: chunk j's scale (and min) is group j >> GSH of the super-block
-    // (AffinePacked with 64-column groups: GSH = 1); NG groups, the mins follow the scales.
+    // (AffinePacked with 32-, 64-, 128-, 256-column groups: GSH = 0..3); NG
+    // groups, the mins follow the scales.
     static constexpr int NG = 8 >> GSH, NW = MIN ? 2 * NG : NG;
     static constexpr bool kIntX = true;
     static constexpr bool kWords2 = MIN;
@@ -245,9 +246,15 @@ struct RplB32I {
         return r;
     }
     static __device__ __forceinline__ Sb load_sb(const RplArgs& a, int64_t si, int lane) {
-        const uint4* m = reinterpret_cast<const uint4*>(a.meta) + (si * 64 + lane) * (NW / 4);
         Sb r;
         const uint4 z = make_uint4(0u, 0u, 0u, 0u);
+        if constexpr (NW == 2) {  // one scale and one min per super-block
+            const uint2 v = ld_stream(reinterpret_cast<const uint2*>(a.meta) + si * 64 + lane);
+            r.s0 = make_uint4(v.x, v.y, 0u, 0u);
+            r.s1 = r.m0 = r.m1 = z;
+            return r;
+        }
+        const uint4* m = reinterpret_cast<const uint4*>(a.meta) + (si * 64 + lane) * (NW / 4);
         r.s0 = ld_stream(m);
         r.s1 = NW >= 8 ? ld_stream(m + 1) : z;
         r.m0 = NW >= 12 ? ld_stream(m + 2) : z;
@@ -265,9 +272,11 @@ struct RplB32I {
         sb.s0.x = w;
         return sb;
     }
-    static __device__ __forceinline__ Sb with_word2(Sb sb, uint32_t w) {  // the slot word2(sb, 0) reads
+    static __device__ __forceinline__ Sb with_word2(Sb sb, uint32_t w) {  // the slot word2(sb, 0) reads: word NG
         if constexpr (NG == 8) sb.m0.x = w;
-        else sb.s1.x = w;
+        else if constexpr (NG == 4) sb.s1.x = w;
+        else if constexpr (NG == 2) sb.s0.z = w;
+        else sb.s0.y = w;
         return sb;
     }
     static __device__ __forceinline__ uint32_t spread(const Ch& ch, int s) {
@@ -301,18 +310,22 @@ using RplQ4I = RplB32I<4, false, 8, 0x88888888u>;
 using RplQ41I = RplB32I<4, true, 0, 0u>;
 using RplQ50I = RplB32I<5, false, 16, 0u>;
 using RplQ51I = RplB32I<5, true, 0, 0u>;
-using RplAff64I = RplB32I<4, true, 0, 0u, 1>;  // AffinePacked, 64-column groups: w = scale*code + min
+template <int GSH>
+using RplAffI = RplB32I<4, true, 0, 0u, GSH>;  // AffinePacked, 32 << GSH-column groups: w = scale*code + min
 
 // The linear IQ formats at their default code width and scale group
 // (quant/iq.go:49-68, 169-180): w = scale*(q - mid), and for one-bit codes
 // w = +-scale = (2*scale)*(q - 1/2). Planes as RplKxI (B = 2, 3) or Q4_K's
 // nibbles (B = 4); one-bit codes sit in a 32-bit plane arranged as the
 // fifth bits of Q5_K. Scales come from the blob's Scales array: one f32 per
-// chunk (scale group 32) or two (group 16, words 2j and 2j + 1).
-template <int B, bool SG16, int MID2>
+// chunk (scale group 32), two (group 16, words 2j and 2j + 1), or one per
+// 2^GSH chunks (BinaryPacked g128: GSH = 2, two words per super-block).
+template <int B, bool SG16, int MID2, int GSH = 0>
 struct RplIQI {
     static constexpr bool kIntX = true;
     static constexpr bool kWords2 = SG16;
+    static constexpr int kGsh = GSH;
+    static constexpr int NW = SG16 ? 16 : (8 >> GSH);  // metadata words per lane and super-block
     static constexpr float kMid = 0.5f * MID2;
     static constexpr float kScaleMul = B == 1 ? 2.0f : 1.0f;  // +-scale = (2*scale)*(q - 1/2)
     struct Ch { uint4 c; uint32_t h; };
@@ -331,15 +344,22 @@ struct RplIQI {
         return r;
     }
     static __device__ __forceinline__ Sb load_sb(const RplArgs& a, int64_t si, int lane) {
-        const uint4* m = reinterpret_cast<const uint4*>(a.meta) + (si * 64 + lane) * (SG16 ? 4 : 2);
         Sb r;
+        const uint4 z = make_uint4(0u, 0u, 0u, 0u);
+        if constexpr (NW == 2) {
+            const uint2 v = ld_stream(reinterpret_cast<const uint2*>(a.meta) + si * 64 + lane);
+            r.s0 = make_uint4(v.x, v.y, 0u, 0u);
+            r.s1 = r.m0 = r.m1 = z;
+            return r;
+        }
+        const uint4* m = reinterpret_cast<const uint4*>(a.meta) + (si * 64 + lane) * (NW / 4);
         r.s0 = ld_stream(m);
         r.s1 = ld_stream(m + 1);
         if constexpr (SG16) {
             r.m0 = ld_stream(m + 2);
             r.m1 = ld_stream(m + 3);
         } else {
-            r.m0 = r.m1 = make_uint4(0u, 0u, 0u, 0u);
+            r.m0 = r.m1 = z;
         }
         return r;
     }
@@ -348,7 +368,7 @@ struct RplIQI {
                                 sb.m0.x, sb.m0.y, sb.m0.z, sb.m0.w, sb.m1.x, sb.m1.y, sb.m1.z, sb.m1.w};
         return w[k];
     }
-    static __device__ __forceinline__ uint32_t word(const Sb& sb, int j) { return sw(sb, SG16 ? 2 * j : j); }
+    static __device__ __forceinline__ uint32_t word(const Sb& sb, int j) { return sw(sb, SG16 ? 2 * j : (j >> GSH)); }
     static __device__ __forceinline__ uint32_t word2(const Sb& sb, int j) { return sw(sb, 2 * j + 1); }
     static __device__ __forceinline__ Sb with_word(Sb sb, uint32_t w) {
         sb.s0.x = w;
@@ -397,6 +417,7 @@ struct RplIQI {
     }
 };
 using RplIQ1S = RplIQI<1, false, 1>;
+using RplBin128 = RplIQI<1, false, 1, 2>;  // BinaryPacked g128: +-scale per 128 weights
 using RplIQ2XXS = RplIQI<2, false, 3>;
 using RplIQ2XS = RplIQI<2, true, 3>;
 using RplIQ3XXS = RplIQI<3, false, 7>;
@@ -1033,8 +1054,9 @@ struct TB32 : RplB32I<B, MIN, OFF, XR, GSH> {
         if constexpr (GSH == 0) {
             const uint2* m2 = reinterpret_cast<const uint2*>(m);
             return {ld_stream(m2 + jp), MIN ? ld_stream(m2 + 4 + jp) : make_uint2(0u, 0u)};
-        } else {  // both chunks in group jp
-            const uint32_t sc = m[jp], mn = MIN ? m[P::NG + jp] : 0u;
+        } else {  // both chunks in group (2 jp) >> GSH
+            const int g = (2 * jp) >> GSH;
+            const uint32_t sc = m[g], mn = MIN ? m[P::NG + g] : 0u;
             return {make_uint2(sc, sc), make_uint2(mn, mn)};
         }
     }
@@ -1070,6 +1092,10 @@ struct TIQ : PQ {
     static __device__ __forceinline__ TM load_tm(const RplArgs& a, int64_t si, int lane, int jp) {
         if constexpr (PQ::kWords2) {
             return {ld_stream(reinterpret_cast<const uint4*>(a.meta) + (si * 64 + lane) * 4 + jp)};
+        } else if constexpr (PQ::kGsh > 0) {  // both chunks share group (2 jp) >> GSH
+            const uint32_t v = ld_stream(reinterpret_cast<const uint32_t*>(a.meta) + (si * 64 + lane) * PQ::NW +
+                                         ((2 * jp) >> PQ::kGsh));
+            return {make_uint4(v, v, 0u, 0u)};
         } else {
             const uint2 v = ld_stream(reinterpret_cast<const uint2*>(a.meta) + (si * 64 + lane) * 4 + jp);
             return {make_uint4(v.x, v.y, 0u, 0u)};
@@ -1321,7 +1347,7 @@ bool rpl_words2(const DevBlob& b) {
     switch (b.fmt) {
     case FMT_Q4_1: return RplQ41I::kWords2;
     case FMT_Q5_1: return RplQ51I::kWords2;
-    case FMT_AFFINE: return RplAff64I::kWords2;
+    case FMT_AFFINE: return RplAffI<1>::kWords2;  // every Affine group width: scale and min
     case FMT_TERNARY: return RplTernI::kWords2;
     case FMT_IQ2_XS: return RplIQ2XS::kWords2;
     case FMT_IQ3_S: return RplIQ3S::kWords2;
@@ -1344,9 +1370,18 @@ int launch_rpl_ex(const DevBlob& b, const float* d_x, float* d_y, int batch, voi
     case FMT_Q4_1: return launch_rpl_t<RplQ41I>(b, d_x, d_y, batch, s, ex);
     case FMT_Q5_0: return launch_rpl_t<RplQ50I>(b, d_x, d_y, batch, s, ex);
     case FMT_Q5_1: return launch_rpl_t<RplQ51I>(b, d_x, d_y, batch, s, ex);
-    case FMT_AFFINE: return launch_rpl_t<RplAff64I>(b, d_x, d_y, batch, s, ex);
+    case FMT_AFFINE:
+        switch (b.block_weights) {
+        case 32: return launch_rpl_t<RplAffI<0>>(b, d_x, d_y, batch, s, ex);
+        case 64: return launch_rpl_t<RplAffI<1>>(b, d_x, d_y, batch, s, ex);
+        case 128: return launch_rpl_t<RplAffI<2>>(b, d_x, d_y, batch, s, ex);
+        case 256: return launch_rpl_t<RplAffI<3>>(b, d_x, d_y, batch, s, ex);
+        default: return int(hipErrorInvalidValue);
+        }
     case FMT_TERNARY: return launch_rpl_t<RplTernI>(b, d_x, d_y, batch, s, ex);
-    case FMT_BINARY: return launch_rpl_t<RplIQ1S>(b, d_x, d_y, batch, s, ex);  // +-scale per 32, as IQ1_S
+    case FMT_BINARY:  // +-scale per 32 as IQ1_S, or per 128
+        return b.block_weights == 128 ? launch_rpl_t<RplBin128>(b, d_x, d_y, batch, s, ex)
+                                      : launch_rpl_t<RplIQ1S>(b, d_x, d_y, batch, s, ex);
     case FMT_IQ1_S: return launch_rpl_t<RplIQ1S>(b, d_x, d_y, batch, s, ex);
     case FMT_IQ2_XXS: return launch_rpl_t<RplIQ2XXS>(b, d_x, d_y, batch, s, ex);
     case FMT_IQ2_XS: return launch_rpl_t<RplIQ2XS>(b, d_x, d_y, batch, s, ex);
@@ -1376,11 +1411,11 @@ bool rpl_items(const DevBlob& b, RplItems& it) {
     LinCodes lc;
     if (rpl_lin_spec(b.fmt, b.block_weights, b.iq_bits, b.iq_sg, lc)) {
         const int cb = lc.bits == 4 ? 16 : lc.bits >= 2 ? 8 : 4;
-        it = {cb, lc.bits == 3 ? 4 : 0, lc.sg == 16 ? 64 : 32, 0};
+        it = {cb, lc.bits == 3 ? 4 : 0, 4 * (256 / lc.sg), 0};
         return true;
     }
-    if (b.fmt == FMT_AFFINE && b.block_weights == 64) {
-        it = {16, 0, 32, 0};
+    if (b.fmt == FMT_AFFINE && rpl_affine_group(b.block_weights)) {
+        it = {16, 0, 8 * (256 / b.block_weights), 0};
         return true;
     }
     switch (b.fmt) {
@@ -1574,9 +1609,18 @@ int launch_rpl_matvec_t(const DevBlob& b, const float* d_gy, float* d_gx, int ba
     case FMT_Q4_1: return launch_rpl_tr<TB32<4, true, 0, 0u>>(b, d_gy, d_gx, batch, s, d_scratch);
     case FMT_Q5_0: return launch_rpl_tr<TB32<5, false, 16, 0u>>(b, d_gy, d_gx, batch, s, d_scratch);
     case FMT_Q5_1: return launch_rpl_tr<TB32<5, true, 0, 0u>>(b, d_gy, d_gx, batch, s, d_scratch);
-    case FMT_AFFINE: return launch_rpl_tr<TB32<4, true, 0, 0u, 1>>(b, d_gy, d_gx, batch, s, d_scratch);
+    case FMT_AFFINE:
+        switch (b.block_weights) {
+        case 32: return launch_rpl_tr<TB32<4, true, 0, 0u, 0>>(b, d_gy, d_gx, batch, s, d_scratch);
+        case 64: return launch_rpl_tr<TB32<4, true, 0, 0u, 1>>(b, d_gy, d_gx, batch, s, d_scratch);
+        case 128: return launch_rpl_tr<TB32<4, true, 0, 0u, 2>>(b, d_gy, d_gx, batch, s, d_scratch);
+        case 256: return launch_rpl_tr<TB32<4, true, 0, 0u, 3>>(b, d_gy, d_gx, batch, s, d_scratch);
+        default: return int(hipErrorInvalidValue);
+        }
     case FMT_TERNARY: return launch_rpl_tr<TIQ<RplTernI>>(b, d_gy, d_gx, batch, s, d_scratch);
-    case FMT_BINARY: return launch_rpl_tr<TIQ<RplIQ1S>>(b, d_gy, d_gx, batch, s, d_scratch);
+    case FMT_BINARY:
+        return b.block_weights == 128 ? launch_rpl_tr<TIQ<RplBin128>>(b, d_gy, d_gx, batch, s, d_scratch)
+                                      : launch_rpl_tr<TIQ<RplIQ1S>>(b, d_gy, d_gx, batch, s, d_scratch);
     case FMT_IQ1_S: return launch_rpl_tr<TIQ<RplIQ1S>>(b, d_gy, d_gx, batch, s, d_scratch);
     case FMT_IQ2_XXS: return launch_rpl_tr<TIQ<RplIQ2XXS>>(b, d_gy, d_gx, batch, s, d_scratch);
     case FMT_IQ2_XS: return launch_rpl_tr<TIQ<RplIQ2XS>>(b, d_gy, d_gx, batch, s, d_scratch);

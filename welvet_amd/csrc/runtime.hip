@@ -337,7 +337,8 @@ void build_rpl_lin(const LinCodes& lc, const uint8_t* raw, size_t raw_len, const
     const int bits = lc.bits, sg = lc.sg;
     auto scale_at = [&](int64_t g) { return size_t(g) < n_scales && scales ? scales[g] : 1.0f; };
     const int64_t rg = (rows + 63) / 64, nch = cols / 32, nsb = cols / 256;
-    const int cb = bits == 4 ? 16 : bits >= 2 ? 8 : 4, mb = sg == 16 ? 64 : 32;
+    const int nw = 256 / sg;  // scales per lane and super-block
+    const int cb = bits == 4 ? 16 : bits >= 2 ? 8 : 4, mb = 4 * nw;
     o.codes = img.add(size_t(rg * nch * 64 * cb));
     if (bits == 3) o.hi = img.add(size_t(rg * nch * 64 * 4));
     o.meta = img.add(size_t(rg * nsb * 64 * mb));
@@ -352,14 +353,9 @@ void build_rpl_lin(const LinCodes& lc, const uint8_t* raw, size_t raw_len, const
                 if (row >= rows) continue;
                 for (int64_t sb = 0; sb < nsb; ++sb) {
                     float* m = reinterpret_cast<float*>(meta + ((g * nsb + sb) * 64 + lane) * mb);
+                    for (int w = 0; w < nw; ++w) m[w] = scale_at((row * cols + sb * 256) / sg + w);
                     for (int p = 0; p < 8; ++p) {
                         const int64_t i0 = row * cols + sb * 256 + p * 32;
-                        if (sg == 16) {
-                            m[2 * p] = scale_at(i0 / 16);
-                            m[2 * p + 1] = scale_at(i0 / 16 + 1);
-                        } else {
-                            m[p] = scale_at(i0 / 32);
-                        }
                         uint8_t qv[32];
                         for (int k = 0; k < 32; ++k) {
                             const int64_t bit = (i0 + k) * bits;
@@ -404,11 +400,12 @@ void build_rpl_lin(const LinCodes& lc, const uint8_t* raw, size_t raw_len, const
 // AffinePacked with 64-column groups (affine_g64.go:124-161): 4-bit codes,
 // element i at nibble i of Raw (low nibble first), as Q4_K's planes; meta per
 // super-block and lane: the 4 group scales, then the 4 group mins (f32).
-void build_rpl_affine(const uint8_t* raw, const float* scales, const float* mins, int64_t rows, int64_t cols, Image& img,
-                      RplOffsets& o) {
-    const int64_t rg = (rows + 63) / 64, nch = cols / 32, nsb = cols / 256, gpr = cols / 64;
+void build_rpl_affine(const uint8_t* raw, const float* scales, const float* mins, int64_t rows, int64_t cols, int bw,
+                      Image& img, RplOffsets& o) {
+    const int ng = 256 / bw;  // groups per super-block: ng scales, then ng mins, per lane
+    const int64_t rg = (rows + 63) / 64, nch = cols / 32, nsb = cols / 256, gpr = cols / bw;
     o.codes = img.add(size_t(rg * nch * 64 * 16));
-    o.meta = img.add(size_t(rg * nsb * 64 * 32));
+    o.meta = img.add(size_t(rg * nsb * 64 * 8 * ng));
     uint8_t* base = img.bytes.data();
     uint8_t* codes = base + o.codes;
     uint8_t* meta = base + o.meta;
@@ -417,10 +414,10 @@ void build_rpl_affine(const uint8_t* raw, const float* scales, const float* mins
             const int64_t row = g * 64 + lane;
             if (row >= rows) continue;
             for (int64_t sb = 0; sb < nsb; ++sb) {
-                float* m = reinterpret_cast<float*>(meta + ((g * nsb + sb) * 64 + lane) * 32);
-                for (int q = 0; q < 4; ++q) {
-                    m[q] = scales[row * gpr + sb * 4 + q];
-                    m[4 + q] = mins[row * gpr + sb * 4 + q];
+                float* m = reinterpret_cast<float*>(meta + ((g * nsb + sb) * 64 + lane) * 8 * ng);
+                for (int q = 0; q < ng; ++q) {
+                    m[q] = scales[row * gpr + sb * ng + q];
+                    m[ng + q] = mins[row * gpr + sb * ng + q];
                 }
                 for (int p = 0; p < 8; ++p)
                     std::memcpy(codes + (((p * rg + g) * nsb + sb) * 64 + lane) * 16, raw + (row * cols + sb * 256 + p * 32) / 2, 16);
@@ -645,9 +642,9 @@ int wv_blob_upload(int format, int64_t rows, int64_t cols, int32_t block_weights
     } else if (LinCodes lc; !raw_only && rpl_lin_spec(format, block_weights, b.iq_bits, b.iq_sg, lc) && cols % 256 == 0) {
         b.layout = LAYOUT_RPL;
         build_rpl_lin(lc, raw, raw_len, scales, n_scales, rows, cols, img, ro);
-    } else if (!raw_only && format == FMT_AFFINE && block_weights == 64 && cols % 256 == 0) {
+    } else if (!raw_only && format == FMT_AFFINE && rpl_affine_group(block_weights) && cols % 256 == 0) {
         b.layout = LAYOUT_RPL;
-        build_rpl_affine(raw, scales, mins, rows, cols, img, ro);
+        build_rpl_affine(raw, scales, mins, rows, cols, block_weights, img, ro);
     } else {
         b.layout = LAYOUT_RAW;
         // 16 bytes of padding: the vectorized decoder reads whole aligned

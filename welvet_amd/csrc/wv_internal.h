@@ -83,7 +83,7 @@ inline bool iq_rpl_spec(int fmt, int bits, int sg) {
 // Formats whose codes form one matrix-wide LSB-first stream of `bits`-bit
 // codes with one f32 scale per `sg` weights: the linear IQ formats,
 // TernaryPacked (2 bits, 16 weights; code 3 reads as 1) and BinaryPacked with
-// 32-weight groups (1 bit). Missing Ternary / Binary scales read as 1.
+// 32- or 128-weight groups (1 bit). Missing Ternary / Binary scales read as 1.
 struct LinCodes {
     int bits = 0, sg = 0;
     bool remap3 = false;
@@ -97,11 +97,16 @@ inline bool rpl_lin_spec(int fmt, int block_weights, int iq_bits, int iq_sg, Lin
         lc = {2, 16, true};
         return true;
     }
-    if (fmt == FMT_BINARY && block_weights != 128) {
-        lc = {1, 32, false};
+    if (fmt == FMT_BINARY) {
+        lc = {1, block_weights == 128 ? 128 : 32, false};
         return true;
     }
     return false;
+}
+// AffinePacked group widths the row-interleaved layout takes: groups that
+// tile a 256-column super-block (one scale and min per 2^GSH chunks).
+inline bool rpl_affine_group(int block_weights) {
+    return block_weights == 32 || block_weights == 64 || block_weights == 128 || block_weights == 256;
 }
 
 // IQ4_NL grid: a data table whose values must equal quant/iq.go:23-40.
