@@ -79,7 +79,7 @@ def test_quant_matvec_contract():
     dn.free()
 
 
-EPI = [("Q4_K", (512, 1024), "row-interleaved"), ("IQ4_NL", (300, 512), "raw"),
+EPI = [("Q4_K", (512, 1024), "row-interleaved"), ("IQ4_NL", (300, 544), "raw"),
        ("Q6_K", (100, 700), "raw"), ("NativeInt4", (300, 512), "narrow"), ("none", (200, 300), "f32")]
 
 

@@ -174,7 +174,7 @@ def test_prefill_q4k_baseline(shape, m):
 
 @pytest.mark.parametrize("fmt,m", [("Q8_0", 8), ("Q6_K", 8), ("Q5_K", 3), ("IQ4_NL", 9), ("IQ4_NL", 40)])
 def test_prefill_other_formats_use_batched_gemv(fmt, m):
-    """Up to 8 token rows (and IQ4_NL, on the reference layout, at any M) run
+    """Up to 8 token rows (and IQ4_NL, whose grid is float, at any M) run
     the batched GEMVs, with the GEMV bar."""
     rows, cols = 300, 1024
     print(f"[gpu] prefill {fmt} M={m} via batched gemv", flush=True)

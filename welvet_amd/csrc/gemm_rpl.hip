@@ -723,9 +723,10 @@ void launch_bm(const GemmArgs& ga, dim3 grid, hipStream_t s) {
 }  // namespace
 
 // Q4_K at every M; every other row-interleaved format from 9 token rows up
-// (up to 8 rows, one batched GEMV launch reads the weights once).
+// (up to 8 rows, one batched GEMV launch reads the weights once), except
+// IQ4_NL, whose float grid has no B-operand builder: it runs batched GEMVs.
 bool gemm_supported(const DevBlob& b, int M) {
-    if (b.layout != LAYOUT_RPL) return false;
+    if (b.layout != LAYOUT_RPL || b.fmt == FMT_IQ4_NL) return false;  // IQ4_NL's float grid: batched GEMV
     return b.fmt == FMT_Q4_K || M > 8;
 }
 

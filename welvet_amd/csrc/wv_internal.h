@@ -84,6 +84,9 @@ inline bool iq_rpl_spec(int fmt, int bits, int sg) {
 // codes with one f32 scale per `sg` weights: the linear IQ formats,
 // TernaryPacked (2 bits, 16 weights; code 3 reads as 1) and BinaryPacked with
 // 32- or 128-weight groups (1 bit). Missing Ternary / Binary scales read as 1.
+// IQ4_NL (4-bit codes into a float grid, one scale per 32) takes the same
+// planes as IQ4_XS's codes with 8 scales per super-block; its kernels look
+// the grid up per weight.
 struct LinCodes {
     int bits = 0, sg = 0;
     bool remap3 = false;
@@ -91,6 +94,10 @@ struct LinCodes {
 inline bool rpl_lin_spec(int fmt, int block_weights, int iq_bits, int iq_sg, LinCodes& lc) {
     if (iq_rpl_spec(fmt, iq_bits, iq_sg)) {
         lc = {iq_bits, iq_sg, false};
+        return true;
+    }
+    if (fmt == FMT_IQ4_NL && iq_bits == 4 && iq_sg == 32) {
+        lc = {4, 32, false};
         return true;
     }
     if (fmt == FMT_TERNARY) {
