@@ -20,10 +20,13 @@
  *     points copy in, compute and copy out synchronously.
  *   - All entry points are thread-safe (handle table under a mutex,
  *     thread-local error text). A blob holds weights only: the scratch a call
- *     needs (K-split or slice partials) is allocated per call on the call's
- *     stream, so concurrent calls on one blob, from several threads or on
- *     several streams, do not share memory. Blob and decoder handles must
- *     not be freed while another thread still calls with them.
+ *     needs (K-split or slice partials) is one of a few per-device slots that
+ *     the call holds until its launches are enqueued, with the GPU ordering a
+ *     slot's next user after its last one, so concurrent calls on one blob,
+ *     from several threads or on several streams, never share partials. The
+ *     slots grow on first use of a larger shape (hipMalloc) and are kept for
+ *     the process. Blob and decoder handles must not be freed while another
+ *     thread still calls with them.
  */
 #ifndef WELVET_HIP_H
 #define WELVET_HIP_H

@@ -48,6 +48,12 @@ struct DeviceState {
     bool ready = false;
     hipStream_t stream = nullptr;
     float* scratch = nullptr;  // this device's address of the file-scope `scratch` array
+    // Stream-ordered pool of the per-call buffers (K-split partials, host
+    // staging). Its release threshold is unbounded, so memory freed by one
+    // call stays in the pool for the next instead of going back to the driver
+    // at each synchronization; the library's own pool leaves the device's
+    // default pool as other users configured it.
+    hipMemPool_t pool = nullptr;
 };
 
 std::mutex g_mu;  // guards g_blobs, g_next, g_dev
@@ -68,6 +74,15 @@ int ensure_device_locked(int dev) {
         if (e != hipSuccess) return hip_fail(e, "wv_init: hipGetSymbolAddress(scratch)");
         e = hipStreamCreateWithFlags(&g_dev[dev].stream, hipStreamNonBlocking);
         if (e != hipSuccess) return hip_fail(e, "wv_init: hipStreamCreate");
+        hipMemPoolProps props{};
+        props.allocType = hipMemAllocationTypePinned;
+        props.location.type = hipMemLocationTypeDevice;
+        props.location.id = dev;
+        e = hipMemPoolCreate(&g_dev[dev].pool, &props);
+        if (e != hipSuccess) return hip_fail(e, "wv_init: hipMemPoolCreate");
+        uint64_t keep = UINT64_MAX;
+        e = hipMemPoolSetAttribute(g_dev[dev].pool, hipMemPoolAttrReleaseThreshold, &keep);
+        if (e != hipSuccess) return hip_fail(e, "wv_init: hipMemPoolSetAttribute");
         g_dev[dev].scratch = static_cast<float*>(sp);
         g_dev[dev].ready = true;
     }
@@ -90,25 +105,103 @@ hipStream_t stream_or_default(void* s, int dev) {
 }
 
 
-// Scratch of one call (K-split or slice partials), stream-ordered: allocated
-// on the call's stream and released after its kernels, so concurrent calls on
-// one blob never share it.
+// Allocation from the current device's library pool, in stream order (the
+// staging buffers of the host entry points, which wait for their stream).
+hipError_t pool_alloc(void** p, size_t bytes, hipStream_t st) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= 64 || !g_dev[dev].pool) return hipErrorNotInitialized;
+    return hipMallocFromPoolAsync(p, bytes, g_dev[dev].pool, st);
+}
+
+// Scratch of the K-split / slice partials of one call. A call owns a slot of
+// its device from before its first launch until its last launch is enqueued,
+// under the device's slot lock; the slot's event, recorded after those
+// launches, marks when the GPU is done with it. A call takes the slot last
+// used on its own stream, else an idle slot, else the least recently used
+// one, and unless the slot is idle its stream waits for the slot's event on
+// the GPU (on the same stream that wait is already implied; it is kept so
+// that a stream handle reused after a destroy cannot overlap the old
+// stream's work). So two launches that could overlap never share partials,
+// and steady-state calls allocate nothing (a stream-ordered allocation and
+// free per call cost 4-10 us against 12-13 us of MatVecT). Slots only grow;
+// they live as long as the process.
+constexpr int kScratchSlots = 4;
+struct ScratchSlot {
+    float* p = nullptr;
+    size_t floats = 0;
+    hipEvent_t done = nullptr;
+    hipStream_t last = nullptr;  // stream of the last use
+    uint64_t stamp = 0;
+};
+struct DeviceScratch {
+    std::mutex mu;
+    ScratchSlot slot[kScratchSlots];
+    uint64_t clock = 0;
+};
+DeviceScratch g_scratch[64];
+
 struct CallScratch {
-    void* p = nullptr;
+    DeviceScratch* ds = nullptr;
+    ScratchSlot* sl = nullptr;
     hipStream_t s = nullptr;
+    std::unique_lock<std::mutex> lk;
     int get(size_t floats, hipStream_t st, const char* what) {
         if (!floats) return WV_OK;
+        int dev = 0;
+        hipError_t e = hipGetDevice(&dev);
+        if (e != hipSuccess) return hip_fail(e, what);
+        if (dev < 0 || dev >= 64) return fail(WV_E_ARG, "%s: device %d", what, dev);
+        ds = &g_scratch[dev];
+        lk = std::unique_lock<std::mutex>(ds->mu);
         s = st;
-        const hipError_t e = hipMallocAsync(&p, floats * sizeof(float), st);
-        if (e != hipSuccess) {
-            p = nullptr;
+        ScratchSlot* pick = nullptr;
+        for (ScratchSlot& c : ds->slot)
+            if (c.p && c.last == st) { pick = &c; break; }
+        if (!pick)
+            for (ScratchSlot& c : ds->slot)
+                if (!c.p || hipEventQuery(c.done) == hipSuccess) { pick = &c; break; }
+        if (!pick) {
+            pick = &ds->slot[0];
+            for (ScratchSlot& c : ds->slot)
+                if (c.stamp < pick->stamp) pick = &c;
+        }
+        bool wait = pick->p && hipEventQuery(pick->done) != hipSuccess;
+        // The event only orders later launches after the slot's last ones (and
+        // tells the host when they are done); no data passes through it to
+        // the host, so it skips the system-scope fence and its cache
+        // writeback (with the fence each record cost 2-3 us of MatVecT).
+        if (!pick->done &&
+            (e = hipEventCreateWithFlags(&pick->done, hipEventDisableTiming | hipEventDisableSystemFence)) != hipSuccess) {
+            pick->done = nullptr;
             return hip_fail(e, what);
         }
+        if (pick->floats < floats) {  // grow: the old buffer may still be in use on the GPU
+            if (pick->p) {
+                if ((e = hipEventSynchronize(pick->done)) != hipSuccess) return hip_fail(e, what);
+                (void)hipFree(pick->p);
+                pick->p = nullptr;
+                pick->floats = 0;
+            }
+            const size_t n = std::max<size_t>(floats, size_t(1) << 16);
+            if ((e = hipMalloc(reinterpret_cast<void**>(&pick->p), n * sizeof(float))) != hipSuccess) {
+                pick->p = nullptr;
+                return hip_fail(e, what);
+            }
+            pick->floats = n;
+            wait = false;
+        }
+        if (wait && (e = hipStreamWaitEvent(st, pick->done, 0)) != hipSuccess) return hip_fail(e, what);
+        sl = pick;
         return WV_OK;
     }
-    float* f() const { return static_cast<float*>(p); }
+    float* f() const { return sl ? sl->p : nullptr; }
     ~CallScratch() {
-        if (p) (void)hipFreeAsync(p, s);
+        if (!sl) return;
+        (void)hipEventRecord(sl->done, s);
+        sl->last = s;
+        sl->stamp = ++ds->clock;
     }
 };
 
@@ -122,7 +215,7 @@ struct Staging {
     template <class T = float>
     T* out(size_t n) {
         void* p = nullptr;
-        if (err == hipSuccess) err = hipMallocAsync(&p, std::max<size_t>(n, 1) * sizeof(T), s);
+        if (err == hipSuccess) err = pool_alloc(&p, std::max<size_t>(n, 1) * sizeof(T), s);
         if (err == hipSuccess) bufs.push_back(p);
         return static_cast<T*>(p);
     }
