@@ -438,6 +438,7 @@ __global__ void __launch_bounds__(256) k_gemm_q4k(GemmArgs ga) {
     static_assert(4 % D == 0, "D must divide the 4 K-steps of a super-block");
     __shared__ __attribute__((aligned(16))) _Float16 xs[2][BM * LDK];
     __shared__ __attribute__((aligned(16))) _Float16 ws[2][BN * LDK];
+    __shared__ float xsc[BM];  // the tile's row factors, for the epilogue
 
     const RplArgs& a = ga.w;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
@@ -448,6 +449,9 @@ __global__ void __launch_bounds__(256) k_gemm_q4k(GemmArgs ga) {
     const int steps = (sb1 - sb0) * 4;
     const int64_t nsb_total = int64_t(a.rg_count) * a.nsb;
     const int kb8 = ga.K / 8;
+    // Row factors of the tile's tokens, staged once; the main loop's barriers
+    // order these writes before the epilogue reads them.
+    if (t < BM) xsc[t] = ga.xscale[min(mblk * BM + t, ga.M - 1)];
 
     // This thread's W slot: row group gl of the block, chunk jj of the step.
     const int gl = (t >> 6) & 1, jj = t >> 7;
@@ -552,7 +556,7 @@ __global__ void __launch_bounds__(256) k_gemm_q4k(GemmArgs ga) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int m = mblk * BM + wm * (BM / WM) + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (m < ga.M) out[int64_t(m) * a.rows + n] = acc[i][j][r] * ga.xscale[m];
+                if (m < ga.M) out[int64_t(m) * a.rows + n] = acc[i][j][r] * xsc[m - mblk * BM];
             }
         }
 }
@@ -576,6 +580,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
     constexpr int XB = BM * (BK / 8) / 256;  // 8-column X blocks per thread per K-step
     static_assert(XB >= 1 && 4 % D == 0, "shape");
     __shared__ __attribute__((aligned(16))) _Float16 xs[2][BM * LDK];
+    __shared__ float xsc[BM];  // the tile's row factors, for the epilogue
 
     const RplArgs& a = ga.w;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
@@ -585,6 +590,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
     const int steps = (sb1 - sb0) * 4;
     const int64_t nsb_total = int64_t(a.rg_count) * a.nsb;
     const int kb8 = ga.K / 8;
+    // Row factors of the tile's tokens, staged once; the main loop's barriers
+    // order these writes before the epilogue reads them.
+    if (t < BM) xsc[t] = ga.xscale[min(mblk * BM + t, ga.M - 1)];
     const int g = min(nblk * 4 + wave, a.rg_count - 1);  // this wave's row group
 
     struct Regs {
@@ -669,7 +677,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int m = mblk * BM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (m < ga.M) out[int64_t(m) * a.rows + n] = acc[i][T][r] * ga.xscale[m];
+                if (m < ga.M) out[int64_t(m) * a.rows + n] = acc[i][T][r] * xsc[m - mblk * BM];
             }
         }
 }
