@@ -398,9 +398,9 @@ __device__ __forceinline__ float row_shift_up(float mx, float* red, float* xscal
 // ORD 0) or [0,2,4,6,1,3,5,7] (dequant8p, ORD 1), one block per token row:
 // the row's max|x| picks xscale = 2^e with max|x| / xscale in [2^14, 2^15)
 // (1 for an all-zero or non-finite row), and the blocks hold x / xscale.
-// Rows of up to 256 * kXRegs blocks of 8 are read once, into registers.
-constexpr int kXRegs = 8;
-template <int ORD>
+// A row of up to 256 * NR blocks of 8 is read once, into registers, with every
+// load issued before the first use (slots past the row re-read its last block).
+template <int ORD, int NR>
 __global__ void __launch_bounds__(256) k_x_f16r(const float4* __restrict__ x, uint4* __restrict__ xh,
                                                  float* __restrict__ xscale, int kb8) {
     __shared__ float red[4];
@@ -408,25 +408,35 @@ __global__ void __launch_bounds__(256) k_x_f16r(const float4* __restrict__ x, ui
     const float4* xr = x + int64_t(m) * kb8 * 2;
     uint4* out = xh + int64_t(m) * kb8;
     float mx = 0.f;
-    if (kb8 <= 256 * kXRegs) {
-        float4 lo[kXRegs], hi[kXRegs];
+    if constexpr (NR > 0) {
+        float4 lo[NR], hi[NR];
 #pragma unroll
-        for (int j = 0; j < kXRegs; ++j) {
+        for (int j = 0; j < NR; ++j) {
             const int i = min(t + 256 * j, kb8 - 1);
             lo[j] = xr[2 * i];
             hi[j] = xr[2 * i + 1];
         }
 #pragma unroll
-        for (int j = 0; j < kXRegs; ++j) mx = fmaxf(mx, absmax8(lo[j], hi[j]));
+        for (int j = 0; j < NR; ++j) mx = fmaxf(mx, absmax8(lo[j], hi[j]));
         const float up = row_shift_up(mx, red, xscale + m, t);
 #pragma unroll
-        for (int j = 0; j < kXRegs; ++j)
+        for (int j = 0; j < NR; ++j)
             if (t + 256 * j < kb8) out[t + 256 * j] = pack_x8<ORD>(lo[j], hi[j], up);
-        return;
+    } else {  // longer rows: two passes, the second mostly from L2
+        for (int i = t; i < kb8; i += 256) mx = fmaxf(mx, absmax8(xr[2 * i], xr[2 * i + 1]));
+        const float up = row_shift_up(mx, red, xscale + m, t);
+        for (int i = t; i < kb8; i += 256) out[i] = pack_x8<ORD>(xr[2 * i], xr[2 * i + 1], up);
     }
-    for (int i = t; i < kb8; i += 256) mx = fmaxf(mx, absmax8(xr[2 * i], xr[2 * i + 1]));
-    const float up = row_shift_up(mx, red, xscale + m, t);
-    for (int i = t; i < kb8; i += 256) out[i] = pack_x8<ORD>(xr[2 * i], xr[2 * i + 1], up);
+}
+template <int ORD>
+void launch_x_f16r(const float* x, uint4* xh, float* xscale, int M, int kb8, hipStream_t s) {
+    const float4* x4 = reinterpret_cast<const float4*>(x);
+    const dim3 g = dim3(unsigned(M)), b = dim3(256);
+    if (kb8 <= 256) hipLaunchKernelGGL((k_x_f16r<ORD, 1>), g, b, 0, s, x4, xh, xscale, kb8);
+    else if (kb8 <= 512) hipLaunchKernelGGL((k_x_f16r<ORD, 2>), g, b, 0, s, x4, xh, xscale, kb8);
+    else if (kb8 <= 1024) hipLaunchKernelGGL((k_x_f16r<ORD, 4>), g, b, 0, s, x4, xh, xscale, kb8);
+    else if (kb8 <= 2048) hipLaunchKernelGGL((k_x_f16r<ORD, 8>), g, b, 0, s, x4, xh, xscale, kb8);
+    else hipLaunchKernelGGL((k_x_f16r<ORD, 0>), g, b, 0, s, x4, xh, xscale, kb8);
 }
 
 template <int BM, int WM, int D>
@@ -822,12 +832,8 @@ int launch_gemm(const DevBlob& b, const float* d_x, float* d_y, int M, void* str
     float* xscale = d_scratch + gemm_x_floats(b, M);
     float* part = xscale + gemm_scale_floats(M);
     const int kb8 = int(b.cols / 8);
-    if (pw)
-        hipLaunchKernelGGL(k_x_f16r<1>, dim3(unsigned(M)), dim3(256), 0, s, reinterpret_cast<const float4*>(d_x), xh,
-                           xscale, kb8);
-    else
-        hipLaunchKernelGGL(k_x_f16r<0>, dim3(unsigned(M)), dim3(256), 0, s, reinterpret_cast<const float4*>(d_x), xh,
-                           xscale, kb8);
+    if (pw) launch_x_f16r<1>(d_x, xh, xscale, M, kb8, s);
+    else launch_x_f16r<0>(d_x, xh, xscale, M, kb8, s);
     GemmArgs ga;
     ga.w = b.rpl;
     ga.xh = xh;
