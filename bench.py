@@ -50,6 +50,13 @@ WORKLOADS = {
     "ternary_2560x6912": ("NativeTernary", 6912, 2560, "DTypeTernary int8 GEMV 2560->6912 b=1"),
     "ternary_6912x2560": ("NativeTernary", 2560, 6912, "DTypeTernary int8 GEMV 6912->2560 b=1"),
 }
+# The other narrow weights.Store DTypes on Dense's int8 path, at the ternary pair's shapes.
+WORKLOADS.update({
+    f"{d.lower()}_{a}x{b}": (f"Native{d}", b, a, f"DType{d} int8 GEMV {a}->{b} b=1")
+    for d in ("Int8", "Int4", "Int2", "Binary") for a, b in ((2560, 6912), (6912, 2560))
+})
+WORKLOADS.update({f"{d.lower()}_14336x4096": (f"Native{d}", 4096, 14336, f"DType{d} int8 GEMV 14336->4096 b=1")
+                  for d in ("Int8", "Int4")})
 # Every other packed format at the headline shape (row-interleaved where the format has it, else the reference layout).
 WORKLOADS.update({
     f"{f.lower()}_4096x14336": (f, 14336, 4096, f"{f} dequant-GEMV 4096->14336 b=1")

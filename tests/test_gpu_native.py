@@ -47,12 +47,13 @@ def native_blob(dt, rows, cols, seed):
 
 @pytest.mark.parametrize("dt", NARROW)
 @pytest.mark.parametrize("shape", [(6912, 2560), (2560, 6912), (300, 1024), (4500, 1024), (9001, 768), (4200, 8192),
-                                   (37, 100), (5, 4104)])
+                                   (1000, 14336), (300, 32768), (37, 100), (5, 4104)])
 def test_narrow_int8_path_bit_exact(dt, shape):
     """(6912, 2560) and (2560, 6912) are BASELINE config 3's shapes; 4500 and
     9001 rows give each wave 4 rows (9001 leaves a ragged last block);
-    4200 x 8192 holds 4 code vectors per lane and row for Int4 (Int8 leaves
-    the vector kernel there: its rows exceed 256 code vectors);
+    4200 x 8192 holds 4 code vectors per lane and row for Int4 and 8 for
+    Int8; 14336 and 32768 columns (the longest narrow row) take the kernel
+    that walks each row's code vectors;
     37x100 and 5x4104 leave the vector kernel (rows not whole code vectors, or
     a row of Binary codes that is not 16-byte aligned) for the per-element one."""
     import torch

@@ -228,6 +228,112 @@ __global__ void __launch_bounds__(1024) k_narrow_i8v(const uint8_t* __restrict__
     }
 }
 
+// Rows of whole code vectors longer than k_narrow_i8v takes (K <= 32768): the
+// same prologue, LDS layout and dot, one row per wave, each lane walking its
+// code vectors c = lane + 64 i four at a time with the next four loaded while
+// the current ones are summed.
+template <int F, int NX>
+__global__ void __launch_bounds__(1024) k_narrow_i8l(const uint8_t* __restrict__ codes, float scale, int rows, int K,
+                                                    const float* __restrict__ x, float* __restrict__ y,
+                                                    int32_t* __restrict__ acc_out, float* __restrict__ act_out) {
+    using N = Narrow<F>;
+    constexpr int B = N::B, KS = 8 / B, E = 32 / B, EU = 128 / B, NCI = 4;
+    extern __shared__ uint32_t lds[];
+    __shared__ float red_f[16];
+    const int nt = blockDim.x, WB = nt >> 6;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int b = blockIdx.y;
+    const int r = blockIdx.x * WB + wave;
+    const int nU = K / EU, k4 = K / 4;
+    const float4* xb = reinterpret_cast<const float4*>(x + int64_t(b) * K);
+    float4 xv[NX];
+#pragma unroll
+    for (int n = 0; n < NX; ++n) xv[n] = xb[min(tid + nt * n, k4 - 1)];
+    __builtin_amdgcn_sched_barrier(0);
+    const uint4* rowp = reinterpret_cast<const uint4*>(codes + int64_t(min(r, rows - 1)) * (K / 8 * B));
+    uint4 cur[NCI];
+#pragma unroll
+    for (int n = 0; n < NCI; ++n) cur[n] = rowp[min(lane + 64 * n, nU - 1)];
+    __builtin_amdgcn_sched_barrier(0);
+    float m = 0.f;
+#pragma unroll
+    for (int n = 0; n < NX; ++n) {
+        if (tid + nt * n >= k4) xv[n] = make_float4(0.f, 0.f, 0.f, 0.f);
+        m = fmaxf(m, fmaxf(fmaxf(fabsf(xv[n].x), fabsf(xv[n].y)), fmaxf(fabsf(xv[n].z), fabsf(xv[n].w))));
+    }
+    m = wave_maximum(m);
+    if (lane == 0) red_f[wave] = m;
+    __syncthreads();
+    m = wave_maximum(red_f[lane < WB ? lane : 0]);
+    float act = m / 127.0f;
+    if (act == 0.0f) act = 1.0f;
+    const float inv = quant_inv(act), thr = quant_thr(inv);
+    float rq[NX][4];
+    bool redo = false;
+#pragma unroll
+    for (int n = 0; n < NX; ++n) {
+        redo |= !quant_fast(xv[n].x, inv, thr, rq[n][0]);
+        redo |= !quant_fast(xv[n].y, inv, thr, rq[n][1]);
+        redo |= !quant_fast(xv[n].z, inv, thr, rq[n][2]);
+        redo |= !quant_fast(xv[n].w, inv, thr, rq[n][3]);
+    }
+    if (__builtin_amdgcn_ballot_w64(redo)) {
+        if (redo) {
+#pragma unroll
+            for (int n = 0; n < NX; ++n) {
+                const float e4[4] = {xv[n].x, xv[n].y, xv[n].z, xv[n].w};
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    float q;
+                    if (!quant_fast(e4[t], inv, thr, q)) rq[n][t] = roundf(e4[t] / act);
+                }
+            }
+        }
+    }
+    uint8_t* l8 = reinterpret_cast<uint8_t*>(lds);
+#pragma unroll
+    for (int n = 0; n < NX; ++n) {
+        const int i = tid + nt * n;
+        if (i >= k4) continue;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int e = 4 * i + t;
+            const int c = e / EU, rr = e % EU, d = rr / E, r2 = rr % E, bb = r2 / KS, k = r2 % KS;
+            l8[4 * ((d * nU + c) * KS + k) + bb] = uint8_t(int8_t(quant_clamp(rq[n][t])));
+        }
+    }
+    __syncthreads();
+    if (act_out && blockIdx.x == 0 && tid == 0) act_out[b] = act;
+    int acc = 0, sq = 0;
+    for (int c0 = 0; c0 < nU; c0 += 64 * NCI) {
+        uint4 nxt[NCI];
+#pragma unroll
+        for (int n = 0; n < NCI; ++n) nxt[n] = rowp[min(c0 + 64 * NCI + lane + 64 * n, nU - 1)];
+#pragma unroll
+        for (int n = 0; n < NCI; ++n) {
+            const int c = c0 + lane + 64 * n;
+            if (c < nU) {
+                const uint32_t wd[4] = {cur[n].x ^ N::XR, cur[n].y ^ N::XR, cur[n].z ^ N::XR, cur[n].w ^ N::XR};
+#pragma unroll
+                for (int d = 0; d < 4; ++d)
+#pragma unroll
+                    for (int k = 0; k < KS; ++k) {
+                        const uint32_t xw = lds[(d * nU + c) * KS + k];
+                        sq = __builtin_amdgcn_sdot4(int(xw), 0x01010101, sq, false);
+                        acc = __builtin_amdgcn_sdot4(int((wd[d] >> (B * k)) & N::MASK), int(xw), acc, false);
+                    }
+            }
+        }
+#pragma unroll
+        for (int n = 0; n < NCI; ++n) cur[n] = nxt[n];
+    }
+    acc = wave_total_i(N::MUL * acc - N::OFF * sq);
+    if (lane == 0 && r < rows) {
+        if (acc_out) acc_out[int64_t(b) * rows + r] = acc;
+        if (y) y[int64_t(b) * rows + r] = float(acc) * act * scale;  // simd.go:142
+    }
+}
+
 // Any shape (K <= 32768): xq in LDS in plain order, one wave per row, codes
 // read per element by flat index (rows need not start on a byte).
 template <int F>
@@ -397,23 +503,37 @@ inline NarrowShape narrow_shape(int rows) {
 
 template <int F, int NC>
 void launch_narrow_v(const DevBlob& b, const float* x, float* y, int32_t* acc, float* act, int batch, hipStream_t s) {
-    const NarrowShape sh = narrow_shape(int(b.rows));
-    if (sh.rw == 1) launch_narrow_x<F, NC, 1>(b, x, y, acc, act, batch, s, sh.wb);
-    else if (sh.rw == 2) launch_narrow_x<F, NC, 2>(b, x, y, acc, act, batch, s, sh.wb);
-    else launch_narrow_x<F, NC, 4>(b, x, y, acc, act, batch, s, sh.wb);
+    if constexpr (NC == 8) {  // 8 code vectors per lane and row (Int8 rows of up to 8192): one row per wave
+        launch_narrow_x<F, NC, 1>(b, x, y, acc, act, batch, s, std::max(4, std::min(16, (int(b.rows) + 255) / 256)));
+    } else {
+        const NarrowShape sh = narrow_shape(int(b.rows));
+        if (sh.rw == 1) launch_narrow_x<F, NC, 1>(b, x, y, acc, act, batch, s, sh.wb);
+        else if (sh.rw == 2) launch_narrow_x<F, NC, 2>(b, x, y, acc, act, batch, s, sh.wb);
+        else launch_narrow_x<F, NC, 4>(b, x, y, acc, act, batch, s, sh.wb);
+    }
 }
 
 template <int F>
 int launch_narrow_f(const DevBlob& b, const float* x, float* y, int32_t* acc, float* act, int batch, hipStream_t s) {
     const int rows = int(b.rows), K = int(b.cols);
     constexpr int EU = 128 / Narrow<F>::B;  // codes per 16-byte vector
-    if (K % EU == 0 && K <= 8192 && K / EU <= 256) {
+    if (K % EU == 0 && K <= 8192) {
         const int nu = K / EU;  // NC = ceil(nu / 64) vectors per lane and row; nu <= 8192 / EU
         if (nu <= 64) launch_narrow_v<F, 1>(b, x, y, acc, act, batch, s);
         else if constexpr (EU <= 64) {
             if (nu <= 128) launch_narrow_v<F, 2>(b, x, y, acc, act, batch, s);
-            else if constexpr (EU <= 32) launch_narrow_v<F, 4>(b, x, y, acc, act, batch, s);
+            else if constexpr (EU <= 32) {
+                if (nu <= 256) launch_narrow_v<F, 4>(b, x, y, acc, act, batch, s);
+                else if constexpr (EU <= 16) launch_narrow_v<F, 8>(b, x, y, acc, act, batch, s);
+            }
         }
+        return int(hipGetLastError());
+    }
+    if (K % EU == 0) {  // longer rows of whole code vectors (K <= 32768): one row per wave of 16-wave blocks
+        const dim3 g = dim3(unsigned((rows + 15) / 16), unsigned(batch)), blk = dim3(1024);
+        const int nx = (K / 4 + 1023) / 1024;
+        if (nx <= 4) hipLaunchKernelGGL((k_narrow_i8l<F, 4>), g, blk, size_t(K), s, b.codes, b.tensor_scale, rows, K, x, y, acc, act);
+        else hipLaunchKernelGGL((k_narrow_i8l<F, 8>), g, blk, size_t(K), s, b.codes, b.tensor_scale, rows, K, x, y, acc, act);
         return int(hipGetLastError());
     }
     const int rpb = 16;
