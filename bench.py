@@ -149,9 +149,29 @@ def host_info():
     return dict(nproc=nproc, cores_available=avail, cpu_model=model, threads=threads)
 
 
-def cpu_baseline(packed, x, rows, cols, ternary, nbytes, budget_s, threads):
+def parity_vs(y_gpu, y_ref, exact):
+    """GPU output against the CPU restatement's output for the same call: the
+    normwise error max|dy| / max|y_ref| and the per-element relative error over
+    the elements with |y_ref| > 1e-3 * max|y_ref|."""
+    y_gpu = np.asarray(y_gpu, np.float64).reshape(-1)
+    y_ref = np.asarray(y_ref, np.float64).reshape(-1)
+    scale = float(np.abs(y_ref).max())
+    dy = np.abs(y_gpu - y_ref)
+    big = np.abs(y_ref) > 1e-3 * scale
+    rel = dy[big] / np.abs(y_ref[big])
+    out = {"normwise_err": float(dy.max() / scale) if scale > 0 else float(dy.max()),
+           "per_element_rel_err_max": float(rel.max()) if rel.size else 0.0,
+           "per_element_rel_err_median": float(np.median(rel)) if rel.size else 0.0,
+           "elements_compared": int(big.sum()), "outputs": int(y_ref.size)}
+    if exact:
+        out["bit_exact"] = bool(np.array_equal(y_gpu.astype(np.float32), y_ref.astype(np.float32)))
+    return out
+
+
+def cpu_baseline(packed, x, rows, cols, ternary, nbytes, budget_s, threads, y_gpu=None):
     """CPU restatement of welvet's Go/SIMD Dense path (oracle/), timed here on
-    `threads` row-shard threads and on one thread."""
+    `threads` row-shard threads and on one thread. With `y_gpu`, the result
+    also carries the GPU output's parity against the restatement's output."""
     import oracle
     info = host_info()
     op = oracle.Packed(packed.fmt if not ternary else 0, rows, cols, packed.raw, packed.scales, packed.meta,
@@ -171,7 +191,11 @@ def cpu_baseline(packed, x, rows, cols, ternary, nbytes, budget_s, threads):
         dt = oracle.DTYPES[packed.name]
         n, sec = timed(lambda: oracle.narrow_i8_forward(dt, packed.raw, np.float32(packed.tensor_scale), rows, cols, x),
                        budget_s)
-        return dict(value=round(nbytes / sec / 1e9, 3), unit="GB/s", cores=1, kind="port",
+        par = None
+        if y_gpu is not None:
+            par = parity_vs(y_gpu, oracle.narrow_i8_forward(dt, packed.raw, np.float32(packed.tensor_scale), rows,
+                                                            cols, x)[0], exact=True)
+        return dict(value=round(nbytes / sec / 1e9, 3), unit="GB/s", cores=1, kind="port", parity=par,
                     one_thread_value=round(nbytes / sec / 1e9, 3), nproc=info["nproc"],
                     cores_available=info["cores_available"], cpu_model=info["cpu_model"],
                     sample=f"{n} full calls of forwardSIMDNarrowI8 restated (serial, re-expands codes every call, "
@@ -179,11 +203,12 @@ def cpu_baseline(packed, x, rows, cols, ternary, nbytes, budget_s, threads):
     t0 = time.perf_counter()
     simd = oracle.SimdPath(op)
     cache_s = time.perf_counter() - t0
-    simd.matvec(x, nthreads=threads)  # warm
+    y_cpu = simd.matvec(x, nthreads=threads)  # warm
     n, sec = timed(lambda: simd.matvec(x, nthreads=threads), budget_s)
     n1, sec1 = timed(lambda: simd.matvec(x, nthreads=1), budget_s / 3)
     simd.close()
-    return dict(value=round(nbytes / sec / 1e9, 3), unit="GB/s", cores=threads, kind="port",
+    par = None if y_gpu is None else parity_vs(y_gpu, y_cpu, exact=False)
+    return dict(value=round(nbytes / sec / 1e9, 3), unit="GB/s", cores=threads, kind="port", parity=par,
                 one_thread_value=round(nbytes / sec1 / 1e9, 3), nproc=info["nproc"],
                 cores_available=info["cores_available"], cpu_model=info["cpu_model"],
                 sample=f"{n} full GEMVs of the restated fused SIMD path on {threads} row-shard threads "
@@ -254,6 +279,7 @@ def main():
     blobs[0].matvec_dev(tx.data_ptr(), ty.data_ptr(), 1, sh)
     stream.synchronize()
     assert torch.isfinite(ty).all().item(), "non-finite output"
+    y_gate = ty.cpu().numpy().copy()
 
     # The launch loop calls the C entry point directly (arguments converted
     # once) so that host-side dispatch stays shorter than one kernel.
@@ -349,7 +375,8 @@ def main():
         info = host_info()
         threads = args.cpu_threads or info["threads"]
         print(f"[bench] cpu baseline ({threads} threads, ~{args.cpu_budget_s:.0f} s)", file=sys.stderr, flush=True)
-        result["cpu_baseline"] = cpu_baseline(packed, x, rows, cols, ternary, nbytes, args.cpu_budget_s, threads)
+        result["cpu_baseline"] = cpu_baseline(packed, x, rows, cols, ternary, nbytes, args.cpu_budget_s, threads,
+                                              y_gpu=y_gate)
     if args.copy_probe:
         src = torch.empty(args.copy_probe << 20, dtype=torch.uint8, device="cuda")
         dst = torch.empty_like(src)
@@ -403,15 +430,17 @@ def prefill_main(args, torch, wv):
     run(1)
     stream.synchronize()
     assert torch.isfinite(ty).all().item(), "non-finite output"
+    y_gate = ty.cpu().numpy().copy()
     steps = max(20, min(args.steps, 400))
     warmup = max(5, min(args.warmup, 40))
-    run(warmup)
-    stream.synchronize()
+    # e0 is recorded behind the enqueued warmup launches with no
+    # synchronisation, so the GPU is busy when the timed region starts.
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    e0.record(stream)
-    run(steps)
-    e1.record(stream)
+    with torch.cuda.stream(stream):
+        run(warmup)
+        e0.record(stream)
+        run(steps)
+        e1.record(stream)
     e1.synchronize()
     ms = e0.elapsed_time(e1) / steps
     tflops = flops / (ms * 1e-3) / 1e12
@@ -432,21 +461,25 @@ def prefill_main(args, torch, wv):
     }
     if not args.no_cpu:
         import oracle
-        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        info = host_info()
+        threads = args.cpu_threads or info["threads"]
         op = oracle.Packed(packed.fmt, rows, cols, packed.raw, packed.scales, packed.meta, packed.block_weights)
         simd = oracle.SimdPath(op)
         simd.matvec(x[0], nthreads=threads)
         n = 0
+        ys = []
         t0 = time.perf_counter()
         while n < m and time.perf_counter() - t0 < args.cpu_budget_s:
-            simd.matvec(x[n], nthreads=threads)
+            ys.append(simd.matvec(x[n], nthreads=threads))
             n += 1
         dt = (time.perf_counter() - t0) / n
         simd.close()
         result["cpu_baseline"] = {
             "value": round(2.0 * rows * cols / dt / 1e12, 5), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "nproc": info["nproc"], "cpu_model": info["cpu_model"],
+            "parity": parity_vs(y_gate[:n], np.stack(ys), exact=False),
             "sample": f"{n} of the M row GEMVs the reference runs for this block (restated fused SIMD path, "
-                      f"{threads} row-shard threads), {dt * 1e3:.3f} ms per row"}
+                      f"{threads} row-shard threads), {dt * 1e3:.3f} ms per row; parity over those rows"}
     for b in blobs:
         b.free()
     print(json.dumps(result), flush=True)
@@ -483,15 +516,17 @@ def matvect_main(args, torch, wv):
     run(1)
     stream.synchronize()
     assert torch.isfinite(tx).all().item(), "non-finite output"
+    gx_gate = tx.cpu().numpy().copy()  # gx after one accumulation into zeros
     steps = max(20, min(args.steps, 1000))
     warmup = max(5, min(args.warmup, 100))
-    run(warmup)
-    stream.synchronize()
+    # e0 is recorded behind the enqueued warmup launches with no
+    # synchronisation, so the GPU is busy when the timed region starts.
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    e0.record(stream)
-    run(steps)
-    e1.record(stream)
+    with torch.cuda.stream(stream):
+        run(warmup)
+        e0.record(stream)
+        run(steps)
+        e1.record(stream)
     e1.synchronize()
     ms = e0.elapsed_time(e1) / steps
     gbs = nbytes / (ms * 1e-3) / 1e9
@@ -511,6 +546,7 @@ def matvect_main(args, torch, wv):
         import oracle
         op = oracle.Packed(packed.fmt, rows, cols, packed.raw, packed.scales, packed.meta, packed.block_weights,
                            packed.mins)
+        gx_ref = oracle.matvec_t_scalar(op, gy, np.zeros(cols, np.float32))
         gx = np.zeros(cols, np.float32)
         n = 0
         t0 = time.perf_counter()
@@ -518,8 +554,10 @@ def matvect_main(args, torch, wv):
             gx = oracle.matvec_t_scalar(op, gy, gx)
             n += 1
         dt = (time.perf_counter() - t0) / n
+        info = host_info()
         result["cpu_baseline"] = {
             "value": round(nbytes / dt / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "nproc": info["nproc"], "cpu_model": info["cpu_model"], "parity": parity_vs(gx_gate, gx_ref, exact=False),
             "sample": f"{n} calls of the restated scalar quant.MatVecT (the reference's only MatVecT path, "
                       f"serial), {dt * 1e3:.3f} ms/call"}
     for b in blobs:

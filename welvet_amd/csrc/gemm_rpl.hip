@@ -1,35 +1,30 @@
-// gemm_rpl.hip — batched prefill on the row-interleaved Q4_K layout:
+// gemm_rpl.hip — batched prefill on the row-interleaved layouts:
 // Y[M][rows] = X[M][cols] * W^T with fp16 MFMA (v_mfma_f32_32x32x16_f16) and
 // f32 accumulation. It replaces welvet's M independent GEMVs for a token block
 // (forwardSIMDBlockFused, layers/dense/simd_block.go:17-39), within the 2e-3
 // tolerance of an fp16 contraction.
 //
 // X is first converted once to fp16 (k_x_f16r), so the GEMM streams half the
-// bytes for the operand every N-tile re-reads and spends no VALU on it. Each
+// bytes for the operand every row tile re-reads and spends no VALU on it. Each
 // token row is scaled by a power of two that puts its max|x| in [2^14, 2^15)
 // before the cast, and the epilogue multiplies the row back: the scaling is
 // exact, so rows that fit fp16 get the same fp16 values as an unscaled cast,
 // while outlier rows (|x| > 65504) stay finite and rows of tiny activations
-// keep their precision instead of going subnormal. Global loads run D K-steps
-// ahead of use in a register ring: a step holds only 64 columns, so one step of
-// look-ahead would expose a full memory latency per step.
+// keep their precision instead of going subnormal.
 //
-// Tiles: a block computes BM tokens x 128 output rows (two 64-row groups),
-// stepping K by 64 columns (two 32-column chunks of a super-block), with both
-// operands double-buffered in LDS as fp16 [row][64 + 8 pad]. Per K-step each
-// of the 256 threads dequantizes one (row, chunk) of W: 16 bytes of nibbles
-// -> 32 fp16 weights with packed-half math (0x6400 | q is 1024 + q exactly;
-// subtract 1024, then fma with the group's scale and min), and copies one or
-// more 8-column blocks of fp16 X. Within every 8-column block both operands are
-// stored in the same permuted k order [0,4,1,5,2,6,3,7], the order in which
-// the nibble extraction produces pairs; a dot product over the block does not
-// depend on the order. K is split over gridDim.z when the tile grid alone
-// would leave CUs idle; the splits' partials meet in a fixed-order sum.
-//
-// Token blocks of more than 64 use k_gemm_q4k_pw instead: W goes from the
-// planes straight into MFMA B operands (a lane swap puts the row-interleaved
-// chunks into the 32x32x16 operand layout) and only X passes through LDS. It
-// serves every row-interleaved format (per-format B-operand builders).
+// W goes from the row-interleaved planes straight into MFMA B operands: a
+// lane holds 32 columns of its row per chunk, and a lane swap puts them into
+// the 32x32x16 operand layout (per-format B-operand builders). Within every
+// 8-column block both operands are in k order [0,2,4,6,1,3,5,7], the order in
+// which the code spread produces pairs; a dot product over the block does not
+// depend on the order. Two kernels:
+//   * k_gemm_rg, up to 64 tokens: a block per 64-row group, its waves
+//     splitting K and reading X fragments straight from global memory, every
+//     weight dequantized once;
+//   * k_gemm_q4k_pw, more tokens: 256-row x 128-token tiles with X staged
+//     through LDS.
+// K is split over gridDim.z when the tile grid alone would leave CUs idle;
+// the splits' partials meet in a fixed-order sum.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -47,7 +42,6 @@ typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int BN = 128;       // output rows per block (2 row groups)
 constexpr int BK = 64;        // columns per K-step
 constexpr int LDK = BK + 8;   // LDS row stride in halves (144 B: conflict-free 16 B row reads)
 
@@ -61,53 +55,33 @@ __device__ __forceinline__ uint32_t pack_h2(float a, float b) {
     return __builtin_bit_cast(uint32_t, h);
 }
 
-// 8 weights of code word v (nibble k = column k) -> 4 half2 in k order
-// [0,4,1,5,2,6,3,7]: w = sc*q + mn computed as fma(q, sc, mn) in fp16.
-__device__ __forceinline__ uint4 dequant8(uint32_t v, half2v sc, half2v mn) {
-    const half2v k1024 = {_Float16(1024.0f), _Float16(1024.0f)};
-    uint32_t p[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t hb = ((v >> (4 * i)) & 0x000F000Fu) | 0x64006400u;
-        const half2v q = __builtin_bit_cast(half2v, hb) - k1024;
-        p[i] = __builtin_bit_cast(uint32_t, q * sc + mn);
-    }
-    return make_uint4(p[0], p[1], p[2], p[3]);
-}
-
-// The same 8 weights in k order [0,2,4,6,1,3,5,7]: the even and odd nibbles
-// are masked to bytes once each, and v_perm_b32 interleaves two of those bytes
-// with the 0x64 exponent byte per half2 (7 instructions for the spread
-// instead of 11).
-__device__ __forceinline__ uint4 dequant8p(uint32_t v, half2v sc, half2v mn) {
-    const half2v k1024 = {_Float16(1024.0f), _Float16(1024.0f)};
-    const uint32_t lo = v & 0x0F0F0F0Fu, hi = (v >> 4) & 0x0F0F0F0Fu;
-    const uint32_t e = 0x64646464u;
-    const uint32_t hb[4] = {__builtin_amdgcn_perm(e, lo, 0x04010400u), __builtin_amdgcn_perm(e, lo, 0x04030402u),
-                            __builtin_amdgcn_perm(e, hi, 0x04010400u), __builtin_amdgcn_perm(e, hi, 0x04030402u)};
-    uint32_t p[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const half2v q = __builtin_bit_cast(half2v, hb[i]) - k1024;
-        p[i] = __builtin_bit_cast(uint32_t, q * sc + mn);
-    }
-    return make_uint4(p[0], p[1], p[2], p[3]);
-}
-
-// The same from two spread words (byte b of `se` / `so` = the code of column
-// 2b / 2b + 1 of an 8-column run, any width up to 5 bits): k order
-// [0,2,4,6,1,3,5,7] as dequant8p.
+// 8 weights from two spread words (byte b of `se` / `so` = the code of
+// column 2b / 2b + 1 of an 8-column run) -> 4 half2 w = fma(q, sc, mn) in
+// fp16, in k order [0,2,4,6,1,3,5,7].
+// Codes of up to 4 bits convert with v_cvt_scalef32_pk_f16_fp8: a byte q <
+// 16 read as fp8 e4m3 is q * 2^-9 exactly (exponent fields 0 and 1 share the
+// step 2^-9), and the instruction applies the exponent of its f32 scale, so
+// scale 512 gives q as fp16 for two bytes in one instruction. Wider codes
+// (up to 5 bits) take the exponent-byte form: 0x64 | q is 1024 + q in fp16.
+template <int FB>
 __device__ __forceinline__ uint4 dequant8s(uint32_t se, uint32_t so, half2v sc, half2v mn) {
-    const half2v k1024 = {_Float16(1024.0f), _Float16(1024.0f)};
-    const uint32_t e = 0x64646464u;
-    const uint32_t hb[4] = {__builtin_amdgcn_perm(e, se, 0x04010400u), __builtin_amdgcn_perm(e, se, 0x04030402u),
-                            __builtin_amdgcn_perm(e, so, 0x04010400u), __builtin_amdgcn_perm(e, so, 0x04030402u)};
+    half2v q[4];
+    if constexpr (FB <= 4) {
+        q[0] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(se, 512.0f, false);
+        q[1] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(se, 512.0f, true);
+        q[2] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(so, 512.0f, false);
+        q[3] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(so, 512.0f, true);
+    } else {
+        const half2v k1024 = {_Float16(1024.0f), _Float16(1024.0f)};
+        const uint32_t e = 0x64646464u;
+        q[0] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(e, se, 0x04010400u)) - k1024;
+        q[1] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(e, se, 0x04030402u)) - k1024;
+        q[2] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(e, so, 0x04010400u)) - k1024;
+        q[3] = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(e, so, 0x04030402u)) - k1024;
+    }
     uint32_t p[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const half2v q = __builtin_bit_cast(half2v, hb[i]) - k1024;
-        p[i] = __builtin_bit_cast(uint32_t, q * sc + mn);
-    }
+    for (int i = 0; i < 4; ++i) p[i] = __builtin_bit_cast(uint32_t, q[i] * sc + mn);
     return make_uint4(p[0], p[1], p[2], p[3]);
 }
 
@@ -198,8 +172,8 @@ struct GemmKQ {  // Q2_K, Q3_K, Q4_K, Q5_K: w = (d/255)*u*q + (dmin/127)*m
             const _Float16 mn0 = _Float16(dm127 * float(int8_t(gm >> 16)));
             const _Float16 mn1 = _Float16(dm127 * float(int32_t(gm) >> 24));
             const half2v s0 = {sc0, sc0}, s1 = {sc1, sc1}, n0 = {mn0, mn0}, n1 = {mn1, mn1};
-            bf[T][0] = __builtin_bit_cast(half8, dequant8s(se[T][0], so[T][0], s0, n0));
-            bf[T][1] = __builtin_bit_cast(half8, dequant8s(se[T][1], so[T][1], s1, n1));
+            bf[T][0] = __builtin_bit_cast(half8, dequant8s<FB>(se[T][0], so[T][0], s0, n0));
+            bf[T][1] = __builtin_bit_cast(half8, dequant8s<FB>(se[T][1], so[T][1], s1, n1));
         }
     }
 };
@@ -232,8 +206,8 @@ struct GemmQ6 {  // Q6_K: q = lo4 | hi2 << 4, w = (d/255)*u*(q - 32)
             const _Float16 sc0 = _Float16(d255 * float(mt[T] & 0xFFu)), sc1 = _Float16(d255 * float((mt[T] >> 8) & 0xFFu));
             const _Float16 mn0 = _Float16(-32.0f) * sc0, mn1 = _Float16(-32.0f) * sc1;
             const half2v s0 = {sc0, sc0}, s1 = {sc1, sc1}, n0 = {mn0, mn0}, n1 = {mn1, mn1};
-            bf[T][0] = __builtin_bit_cast(half8, dequant8s(se[T][0], so[T][0], s0, n0));
-            bf[T][1] = __builtin_bit_cast(half8, dequant8s(se[T][1], so[T][1], s1, n1));
+            bf[T][0] = __builtin_bit_cast(half8, dequant8s<6>(se[T][0], so[T][0], s0, n0));
+            bf[T][1] = __builtin_bit_cast(half8, dequant8s<6>(se[T][1], so[T][1], s1, n1));
         }
     }
 };
@@ -301,8 +275,8 @@ struct GemmB32 {
             const float scf = __uint_as_float(st[T]);
             const _Float16 sc = _Float16(scf), mn = _Float16(MIN ? __uint_as_float(mt[T]) : -float(OFF) * scf);
             const half2v s2 = {sc, sc}, n2 = {mn, mn};
-            bf[T][0] = __builtin_bit_cast(half8, dequant8s(se[T][0], so[T][0], s2, n2));
-            bf[T][1] = __builtin_bit_cast(half8, dequant8s(se[T][1], so[T][1], s2, n2));
+            bf[T][0] = __builtin_bit_cast(half8, dequant8s<FB>(se[T][0], so[T][0], s2, n2));
+            bf[T][1] = __builtin_bit_cast(half8, dequant8s<FB>(se[T][1], so[T][1], s2, n2));
         }
     }
 };
@@ -355,29 +329,29 @@ struct GemmLin {
                 const float scf = __uint_as_float(kk ? t1[T] : t0[T]) * mul;
                 const _Float16 sc = _Float16(scf), mn = _Float16(-mid * scf);
                 const half2v s2 = {sc, sc}, n2 = {mn, mn};
-                bf[T][kk] = __builtin_bit_cast(half8, dequant8s(se[T][kk], so[T][kk], s2, n2));
+                bf[T][kk] = __builtin_bit_cast(half8, dequant8s<FB>(se[T][kk], so[T][kk], s2, n2));
             }
     }
 };
 
 struct GemmArgs {
     RplArgs w;
-    const uint4* xh;       // [M][K/8] fp16 8-column blocks in permuted k order, row m scaled by 1 / xscale[m]
+    // fp16 8-column blocks of X in permuted k order, row m scaled by
+    // 1 / xscale[m]: [M][K/8] row-major, or for k_gemm_rg in MFMA A-fragment
+    // order [K/16][ceil(M/32)][64] (lane l of fragment (q, tile): token
+    // 32*tile + l%32, block 2q + l/32; tokens past M are zero)
+    const uint4* xh;
     const float* xscale;   // [M] power-of-two factor of each row's fp16 copy
     float* y;         // [M][rows] (splits == 1) or partials [split][M][rows]
     int M, K;
     int sb_per_split;
 };
 
-// 8 columns of X times `up`, as fp16 pairs in the k order ORD.
-template <int ORD>
+// 8 columns of X times `up`, as fp16 pairs in k order [0,2,4,6,1,3,5,7].
 __device__ __forceinline__ uint4 pack_x8(float4 lo, float4 hi, float up) {
     lo = make_float4(lo.x * up, lo.y * up, lo.z * up, lo.w * up);
     hi = make_float4(hi.x * up, hi.y * up, hi.z * up, hi.w * up);
-    if constexpr (ORD == 0)
-        return make_uint4(pack_h2(lo.x, hi.x), pack_h2(lo.y, hi.y), pack_h2(lo.z, hi.z), pack_h2(lo.w, hi.w));
-    else
-        return make_uint4(pack_h2(lo.x, lo.z), pack_h2(hi.x, hi.z), pack_h2(lo.y, lo.w), pack_h2(hi.y, hi.w));
+    return make_uint4(pack_h2(lo.x, lo.z), pack_h2(hi.x, hi.z), pack_h2(lo.y, lo.w), pack_h2(hi.y, hi.w));
 }
 __device__ __forceinline__ float absmax8(float4 lo, float4 hi) {
     return fmaxf(fmaxf(fmaxf(fabsf(lo.x), fabsf(lo.y)), fmaxf(fabsf(lo.z), fabsf(lo.w))),
@@ -394,19 +368,32 @@ __device__ __forceinline__ float row_shift_up(float mx, float* red, float* xscal
     if (t == 0) *xscale_m = ldexpf(1.0f, -sh);
     return ldexpf(1.0f, sh);
 }
-// X f32 [M][K] -> fp16 blocks of 8 in k order [0,4,1,5,2,6,3,7] (dequant8,
-// ORD 0) or [0,2,4,6,1,3,5,7] (dequant8p, ORD 1), one block per token row:
+// X f32 [M][K] -> fp16 blocks of 8 in the B operands' k order
+// [0,2,4,6,1,3,5,7] (pack_x8), one block per token row:
 // the row's max|x| picks xscale = 2^e with max|x| / xscale in [2^14, 2^15)
 // (1 for an all-zero or non-finite row), and the blocks hold x / xscale.
 // A row of up to 256 * NR blocks of 8 is read once, into registers, with every
 // load issued before the first use (slots past the row re-read its last block).
-template <int ORD, int NR>
+// FRAG writes the A-fragment order of GemmArgs::xh (block i of row m at
+// ((i/2)*mt + m/32)*64 + m%32 + 32*(i%2)); its grid covers the padded rows,
+// which get zeros.
+template <int NR, bool FRAG>
 __global__ void __launch_bounds__(256) k_x_f16r(const float4* __restrict__ x, uint4* __restrict__ xh,
-                                                 float* __restrict__ xscale, int kb8) {
+                                                 float* __restrict__ xscale, int kb8, int M) {
     __shared__ float red[4];
     const int m = blockIdx.x, t = threadIdx.x;
+    const int mt = (M + 31) / 32;
+    auto put = [&](int i, uint4 v) {
+        if constexpr (FRAG)
+            xh[(int64_t(i >> 1) * mt + (m >> 5)) * 64 + (m & 31) + 32 * (i & 1)] = v;
+        else
+            xh[int64_t(m) * kb8 + i] = v;
+    };
+    if (FRAG && m >= M) {
+        for (int i = t; i < kb8; i += 256) put(i, make_uint4(0u, 0u, 0u, 0u));
+        return;
+    }
     const float4* xr = x + int64_t(m) * kb8 * 2;
-    uint4* out = xh + int64_t(m) * kb8;
     float mx = 0.f;
     if constexpr (NR > 0) {
         float4 lo[NR], hi[NR];
@@ -421,157 +408,24 @@ __global__ void __launch_bounds__(256) k_x_f16r(const float4* __restrict__ x, ui
         const float up = row_shift_up(mx, red, xscale + m, t);
 #pragma unroll
         for (int j = 0; j < NR; ++j)
-            if (t + 256 * j < kb8) out[t + 256 * j] = pack_x8<ORD>(lo[j], hi[j], up);
+            if (t + 256 * j < kb8) put(t + 256 * j, pack_x8(lo[j], hi[j], up));
     } else {  // longer rows: two passes, the second mostly from L2
         for (int i = t; i < kb8; i += 256) mx = fmaxf(mx, absmax8(xr[2 * i], xr[2 * i + 1]));
         const float up = row_shift_up(mx, red, xscale + m, t);
-        for (int i = t; i < kb8; i += 256) out[i] = pack_x8<ORD>(xr[2 * i], xr[2 * i + 1], up);
+        for (int i = t; i < kb8; i += 256) put(i, pack_x8(xr[2 * i], xr[2 * i + 1], up));
     }
 }
-template <int ORD>
+template <bool FRAG>
 void launch_x_f16r(const float* x, uint4* xh, float* xscale, int M, int kb8, hipStream_t s) {
     const float4* x4 = reinterpret_cast<const float4*>(x);
-    const dim3 g = dim3(unsigned(M)), b = dim3(256);
-    if (kb8 <= 256) hipLaunchKernelGGL((k_x_f16r<ORD, 1>), g, b, 0, s, x4, xh, xscale, kb8);
-    else if (kb8 <= 512) hipLaunchKernelGGL((k_x_f16r<ORD, 2>), g, b, 0, s, x4, xh, xscale, kb8);
-    else if (kb8 <= 1024) hipLaunchKernelGGL((k_x_f16r<ORD, 4>), g, b, 0, s, x4, xh, xscale, kb8);
-    else if (kb8 <= 2048) hipLaunchKernelGGL((k_x_f16r<ORD, 8>), g, b, 0, s, x4, xh, xscale, kb8);
-    else hipLaunchKernelGGL((k_x_f16r<ORD, 0>), g, b, 0, s, x4, xh, xscale, kb8);
+    const dim3 g = dim3(unsigned(FRAG ? (M + 31) / 32 * 32 : M)), b = dim3(256);
+    if (kb8 <= 256) hipLaunchKernelGGL((k_x_f16r<1, FRAG>), g, b, 0, s, x4, xh, xscale, kb8, M);
+    else if (kb8 <= 512) hipLaunchKernelGGL((k_x_f16r<2, FRAG>), g, b, 0, s, x4, xh, xscale, kb8, M);
+    else if (kb8 <= 1024) hipLaunchKernelGGL((k_x_f16r<4, FRAG>), g, b, 0, s, x4, xh, xscale, kb8, M);
+    else if (kb8 <= 2048) hipLaunchKernelGGL((k_x_f16r<8, FRAG>), g, b, 0, s, x4, xh, xscale, kb8, M);
+    else hipLaunchKernelGGL((k_x_f16r<0, FRAG>), g, b, 0, s, x4, xh, xscale, kb8, M);
 }
 
-template <int BM, int WM, int D>
-__global__ void __launch_bounds__(256) k_gemm_q4k(GemmArgs ga) {
-    constexpr int WN = 4 / WM;
-    constexpr int TM = BM / WM / 32, TN = BN / WN / 32;
-    constexpr int XB = BM * (BK / 8) / 256;  // 8-column X blocks per thread per K-step
-    static_assert(XB >= 1, "BM too small");
-    static_assert(4 % D == 0, "D must divide the 4 K-steps of a super-block");
-    __shared__ __attribute__((aligned(16))) _Float16 xs[2][BM * LDK];
-    __shared__ __attribute__((aligned(16))) _Float16 ws[2][BN * LDK];
-    __shared__ float xsc[BM];  // the tile's row factors, for the epilogue
-
-    const RplArgs& a = ga.w;
-    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int wm = wave / WN, wn = wave % WN;
-    const int nblk = blockIdx.x, mblk = blockIdx.y, split = blockIdx.z;
-    const int sb0 = split * ga.sb_per_split;
-    const int sb1 = min(a.nsb, sb0 + ga.sb_per_split);
-    const int steps = (sb1 - sb0) * 4;
-    const int64_t nsb_total = int64_t(a.rg_count) * a.nsb;
-    const int kb8 = ga.K / 8;
-    // Row factors of the tile's tokens, staged once; the main loop's barriers
-    // order these writes before the epilogue reads them.
-    if (t < BM) xsc[t] = ga.xscale[min(mblk * BM + t, ga.M - 1)];
-
-    // This thread's W slot: row group gl of the block, chunk jj of the step.
-    const int gl = (t >> 6) & 1, jj = t >> 7;
-    const int g = min(nblk * 2 + gl, a.rg_count - 1);
-    const int wrow = gl * 64 + lane;
-
-    struct Regs {
-        uint4 c;
-        uint32_t meta;
-        float2 dd;
-        uint4 xv[XB];  // fp16 blocks of X
-    };
-    auto load = [&](int s, Regs& r) {
-        const int sb = sb0 + s / 4, j = 2 * (s & 3) + jj;
-        const int64_t si = int64_t(g) * a.nsb + sb;
-        r.c = ld_nt(reinterpret_cast<const uint4*>(a.codes) + (int64_t(j) * nsb_total + si) * 64 + lane);
-        r.meta = reinterpret_cast<const uint32_t*>(a.meta)[(si * 64 + lane) * 8 + j];
-        r.dd = reinterpret_cast<const float2*>(a.dd)[si * 64 + lane];
-        const int k8 = sb * 32 + (s & 3) * 8;
-#pragma unroll
-        for (int i = 0; i < XB; ++i) {
-            const int f = t + 256 * i, m = min(mblk * BM + f / 8, ga.M - 1);
-            r.xv[i] = ga.xh[int64_t(m) * kb8 + k8 + f % 8];
-        }
-    };
-    auto store = [&](const Regs& r, int buf) {
-        // W: 32 weights of row wrow, columns 32*jj .. 32*jj+31 of the step.
-        const uint32_t gm = r.meta;  // (u'0, u'1, m0, m1)
-        const float d255 = r.dd.x * (1.0f / 255.0f), dm127 = r.dd.y * (1.0f / 127.0f);
-        const _Float16 sc0 = _Float16(d255 * float(gm & 0xFFu)), sc1 = _Float16(d255 * float((gm >> 8) & 0xFFu));
-        const _Float16 mn0 = _Float16(dm127 * float(int8_t(gm >> 16))), mn1 = _Float16(dm127 * float(int32_t(gm) >> 24));
-        const half2v s0 = {sc0, sc0}, s1 = {sc1, sc1}, n0 = {mn0, mn0}, n1 = {mn1, mn1};
-        uint4* wd = reinterpret_cast<uint4*>(&ws[buf][wrow * LDK + 32 * jj]);
-        wd[0] = dequant8(r.c.x, s0, n0);
-        wd[1] = dequant8(r.c.y, s0, n0);
-        wd[2] = dequant8(r.c.z, s1, n1);
-        wd[3] = dequant8(r.c.w, s1, n1);
-#pragma unroll
-        for (int i = 0; i < XB; ++i) {
-            const int f = t + 256 * i;
-            *reinterpret_cast<uint4*>(&xs[buf][(f / 8) * LDK + 8 * (f % 8)]) = r.xv[i];
-        }
-    };
-
-    f32x16 acc[TM][TN];
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-
-    // D register slots; slot d holds step s with s % D == d. Loads are
-    // unconditional (indices clamped to the last step) so that every wait
-    // is an exact count.
-    // The scheduling barriers keep every slot's loads in program order, in
-    // the prologue as in the loop: if the two orders differ, the wait at the
-    // loop head becomes a wait for all outstanding loads.
-    Regs ring[D];
-#pragma unroll
-    for (int d = 0; d < D; ++d) {
-        load(min(d, steps - 1), ring[d]);
-        __builtin_amdgcn_sched_barrier(0);
-    }
-    for (int s0 = 0; s0 < steps; s0 += D) {
-#pragma unroll
-        for (int d = 0; d < D; ++d) {
-            const int s = s0 + d, buf = s & 1;
-            store(ring[d], buf);
-            __builtin_amdgcn_sched_barrier(0);
-            load(min(s + D, steps - 1), ring[d]);
-            __builtin_amdgcn_sched_barrier(0);
-            __syncthreads();
-#pragma unroll
-            for (int ks = 0; ks < BK / 16; ++ks) {
-                half8 af[TM], bf[TN];
-#pragma unroll
-                for (int i = 0; i < TM; ++i)
-                    af[i] = *reinterpret_cast<const half8*>(
-                        &xs[buf][(wm * (BM / WM) + i * 32 + (lane & 31)) * LDK + ks * 16 + 8 * (lane >> 5)]);
-#pragma unroll
-                for (int j = 0; j < TN; ++j)
-                    bf[j] = *reinterpret_cast<const half8*>(
-                        &ws[buf][(wn * (BN / WN) + j * 32 + (lane & 31)) * LDK + ks * 16 + 8 * (lane >> 5)]);
-#pragma unroll
-                for (int i = 0; i < TM; ++i)
-#pragma unroll
-                    for (int j = 0; j < TN; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
-            }
-        }
-    }
-
-    // C[i][j] of a 32x32 tile: lane holds j = lane % 32, i = 8*(r/4) + 4*(lane/32) + r%4.
-    float* out = ga.y + int64_t(split) * ga.M * a.rows;
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) {
-            const int n = nblk * BN + wn * (BN / WN) + j * 32 + (lane & 31);
-            if (n >= a.rows) continue;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int m = mblk * BM + wm * (BM / WM) + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (m < ga.M) out[int64_t(m) * a.rows + n] = acc[i][j][r] * xsc[m - mblk * BM];
-            }
-        }
-}
-
-// Packed-W variant for token tiles of 128: W never passes through LDS.
 // Each of the 4 waves owns one 64-row group of the block's 256 rows and loads
 // its row group's codes straight from the row-interleaved planes (lane l = row
 // l, 16 bytes = 32 columns per chunk). One v_permlane32_swap per code-word
@@ -692,6 +546,123 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
         }
 }
 
+// The token-block GEMM for few tokens (TM 32-token tiles, TM = 1 or 2): one
+// block per (64-row group, token block, K split), its W waves splitting the
+// split's super-blocks (`per` consecutive ones each). A wave loads its row
+// group's codes from the planes as k_gemm_q4k_pw does (B operands through
+// lane swaps) and its fp16 X fragments straight from global memory (one
+// contiguous 1 KB per wave and load: the A-fragment order of GemmArgs::xh),
+// so the main loop has no barrier and no LDS traffic. A step is 64 columns
+// (two chunks, four k16 MFMA steps); codes run DC steps ahead of use and X
+// fragments (L2 hits: every row group's blocks read the same X) DX steps
+// ahead, in register rings. Every weight is dequantized once per token block.
+// The W waves' partial tiles meet in LDS after the loop and are added in wave
+// order (deterministic), one 32-token tile at a time.
+template <class GP, int TM, int DC, int DX>
+__global__ void __launch_bounds__(512) k_gemm_rg(GemmArgs ga, int per) {
+    constexpr int BM = 32 * TM;
+    static_assert(4 % DC == 0 && 4 % DX == 0, "the rings must divide the 4 steps of a super-block");
+    constexpr int DU = DC > DX ? DC : DX;  // loop unroll: both ring positions are compile-time
+    extern __shared__ float red[];  // [W][2][16][64] partial tiles of one 32-token tile
+    const RplArgs& a = ga.w;
+    const int t = threadIdx.x, lane = t & 63, W = blockDim.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);  // wave-uniform: chunk addresses stay scalar
+    const int g = blockIdx.x, mblk = blockIdx.y, split = blockIdx.z;
+    const int sb0 = split * ga.sb_per_split;
+    const int sb1 = min(a.nsb, sb0 + ga.sb_per_split);
+    const int wsb0 = sb0 + wave * per;
+    const int steps = max(0, min(sb1, wsb0 + per) - wsb0) * 4;
+    const int64_t nsb_total = int64_t(a.rg_count) * a.nsb;
+    const int mt = (ga.M + 31) / 32;  // 32-token tiles of the fragment-ordered X
+
+    struct Codes {
+        typename GP::Ch c[2];  // the step's two chunks of this lane's row
+    };
+    struct Xf {
+        uint4 v[TM][4];  // A fragments of the step's 4 k16 steps
+    };
+    auto load_c = [&](int s, Codes& r) {
+        const int64_t si = int64_t(g) * a.nsb + wsb0 + s / 4;
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) {
+            const int j = 2 * (s & 3) + jj;
+            r.c[jj] = GP::load(a, int64_t(j) * nsb_total + si, si, j, lane);
+        }
+    };
+    auto load_x = [&](int s, Xf& r) {
+        const int64_t q0 = int64_t(wsb0) * 16 + 4 * s;  // first k16 step of the step
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) r.v[i][ks] = ga.xh[((q0 + ks) * mt + mblk * TM + i) * 64 + lane];
+    };
+
+    f32x16 acc[TM][2];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    if (steps > 0) {
+        Codes cr[DC];
+        Xf xr[DX];
+#pragma unroll
+        for (int d = 0; d < DU; ++d) {
+            if (d < DC) load_c(min(d, steps - 1), cr[d % DC]);
+            if (d < DX) load_x(min(d, steps - 1), xr[d % DX]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        for (int s0 = 0; s0 < steps; s0 += DU) {
+#pragma unroll
+            for (int d = 0; d < DU; ++d) {
+                const int s = s0 + d;
+                const Codes cc = cr[d % DC];
+                const Xf xc = xr[d % DX];
+                __builtin_amdgcn_sched_barrier(0);
+                load_c(min(s + DC, steps - 1), cr[d % DC]);
+                load_x(min(s + DX, steps - 1), xr[d % DX]);
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int jj = 0; jj < 2; ++jj) {
+                    half8 bf[2][2];  // [tile][k16 step]
+                    GP::bops(cc.c[jj], lane, bf);
+#pragma unroll
+                    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+                        for (int i = 0; i < TM; ++i) {
+                            const half8 af = __builtin_bit_cast(half8, xc.v[i][2 * jj + kk]);
+#pragma unroll
+                            for (int T = 0; T < 2; ++T)
+                                acc[i][T] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf[T][kk], acc[i][T], 0, 0, 0);
+                        }
+                }
+            }
+        }
+    }
+
+    // C[i][j] of a 32x32 tile: lane holds j = lane % 32, i = 8*(r/4) + 4*(lane/32) + r%4.
+    float* out = ga.y + int64_t(split) * ga.M * a.rows;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+        if (i > 0) __syncthreads();  // the previous tile's sums have been read
+#pragma unroll
+        for (int T = 0; T < 2; ++T)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) red[((wave * 2 + T) * 16 + r) * 64 + lane] = acc[i][T][r];
+        __syncthreads();
+        for (int v = t; v < 2048; v += 64 * W) {
+            const int T = v >> 10, r = (v >> 6) & 15, l = v & 63;
+            float sum = 0.f;
+            for (int w = 0; w < W; ++w) sum += red[((w * 2 + T) * 16 + r) * 64 + l];
+            const int n = g * 64 + T * 32 + (l & 31);
+            const int m = mblk * BM + i * 32 + 8 * (r >> 2) + 4 * (l >> 5) + (r & 3);
+            if (n < a.rows && m < ga.M) out[int64_t(m) * a.rows + n] = sum * ga.xscale[m];
+        }
+    }
+}
+
 // y[i] = sum_k part[k*n + i], k ascending; each thread owns 4 consecutive
 // outputs (float4 when n % 4 == 0 and y is 16-byte aligned; the partials
 // always are) and issues up to 8 splits' loads before adding them.
@@ -733,11 +704,6 @@ __global__ void __launch_bounds__(256) k_split_sum(const float* __restrict__ par
     reinterpret_cast<float4*>(y)[i4] = s;
 }
 
-template <int BM, int WM>
-void launch_bm(const GemmArgs& ga, dim3 grid, hipStream_t s) {
-    hipLaunchKernelGGL((k_gemm_q4k<BM, WM, 4>), grid, dim3(256), 0, s, ga);
-}
-
 }  // namespace
 
 // Q4_K at every M; every other row-interleaved format from 9 token rows up
@@ -748,38 +714,52 @@ bool gemm_supported(const DevBlob& b, int M) {
     return b.fmt == FMT_Q4_K || M > 8;
 }
 
-// Token tiles from kPwMin up run k_gemm_q4k_pw (256-row tiles, one block per
-// CU); smaller ones k_gemm_q4k (128-row tiles). At M = 32 both kernels take
-// 20.5 us.
-constexpr int kPwMin = 128;
-bool use_pw(const DevBlob& b, int bm) { return bm >= kPwMin || b.fmt != FMT_Q4_K; }
-void gemm_plan(const DevBlob& b, int M, int& bm, int& splits, int& sb_per_split) {
+// Which kernel runs a token block, its tile height (bm tokens), the K split
+// (splits of sb_per_split super-blocks) and, for k_gemm_rg, its waves per
+// block W and super-blocks per wave `per`:
+//   * up to 64 tokens: k_gemm_rg (one block per 64-row group, up to 8 waves
+//     splitting K, one or two 32-token tiles), K split over blocks only while
+//     the row groups alone give fewer than 200 blocks;
+//   * more: k_gemm_q4k_pw (256-row tiles of 128 tokens, one block per CU), K
+//     split while whole tiles leave CUs idle.
+enum { GEMM_PW = 1, GEMM_RG = 2 };
+constexpr int kRgWaves = 8;  // k_gemm_rg waves per block (2 per SIMD)
+struct GemmPlan {
+    int kind, bm, splits, sb_per_split, W, per;
+};
+constexpr int kRgMaxM = 64;
+GemmPlan gemm_plan(const DevBlob& b, int M) {
     const RplArgs& a = b.rpl;
-    bm = M <= 32 ? 32 : M <= 64 ? 64 : 128;
+    GemmPlan p{GEMM_PW, M <= 32 ? 32 : M <= 64 ? 64 : 128, 1, a.nsb, 1, 1};
     int want = 1;
-    if (use_pw(b, bm)) {
-        // Split K while whole tiles leave CUs idle, never past one block per CU.
-        const int64_t tiles = int64_t((a.rows + 255) / 256) * ((M + bm - 1) / bm);
-        want = int(std::max<int64_t>(1, 256 / tiles));
+    if (M <= kRgMaxM) {
+        p.kind = GEMM_RG;
+        const int64_t tiles = int64_t(a.rg_count) * ((M + p.bm - 1) / p.bm);
+        want = int(std::max<int64_t>(1, (200 + tiles - 1) / tiles));
+        want = std::min(want, std::max(1, a.nsb / 8));  // each split >= 8 super-blocks
     } else {
-        const int64_t tiles = int64_t((a.rows + BN - 1) / BN) * ((M + bm - 1) / bm);
-        // Split K only while the tile grid alone leaves CUs idle (~384 blocks fill
-        // the 256 CUs at the 1-2 blocks each that the register/LDS budget allows).
-        want = int(std::max<int64_t>(1, (384 + tiles - 1) / tiles));
+        const int64_t tiles = int64_t((a.rows + 255) / 256) * ((M + p.bm - 1) / p.bm);
+        want = int(std::max<int64_t>(1, 256 / tiles));
+        want = std::min(want, std::max(1, a.nsb / 2));  // each split >= 2 super-blocks
     }
-    want = std::min(want, std::max(1, a.nsb / 2));  // each split >= 2 super-blocks
-    sb_per_split = (a.nsb + want - 1) / want;
-    splits = (a.nsb + sb_per_split - 1) / sb_per_split;
+    p.sb_per_split = (a.nsb + want - 1) / want;
+    p.splits = (a.nsb + p.sb_per_split - 1) / p.sb_per_split;
+    if (p.kind == GEMM_RG) {
+        p.per = (p.sb_per_split + kRgWaves - 1) / kRgWaves;
+        p.W = (p.sb_per_split + p.per - 1) / p.per;
+    }
+    return p;
 }
 
 // Scratch floats: the fp16 copy of X (M*K halves), the M row factors, then
 // the split-K partials (each piece 256-byte aligned).
-size_t gemm_x_floats(const DevBlob& b, int M) { return (size_t(M) * size_t(b.cols) / 2 + 63) / 64 * 64; }
+size_t gemm_x_floats(const DevBlob& b, int M) {
+    return ((size_t(M) + 31) / 32 * 32 * size_t(b.cols) / 2 + 63) / 64 * 64;  // tokens padded to 32 (A fragments)
+}
 size_t gemm_scale_floats(int M) { return (size_t(M) + 63) / 64 * 64; }
 size_t gemm_scratch_floats(const DevBlob& b, int M) {
-    int bm = 0, splits = 1, per = 0;
-    gemm_plan(b, M, bm, splits, per);
-    return gemm_x_floats(b, M) + gemm_scale_floats(M) + (splits > 1 ? size_t(splits) * size_t(M) * size_t(b.rows) : 0);
+    const GemmPlan p = gemm_plan(b, M);
+    return gemm_x_floats(b, M) + gemm_scale_floats(M) + (p.splits > 1 ? size_t(p.splits) * size_t(M) * size_t(b.rows) : 0);
 }
 
 // The packed-W GEMM for b's format with TM 32-token tiles per wave.
@@ -821,19 +801,65 @@ int launch_pw(const DevBlob& b, dim3 grid, hipStream_t s, const GemmArgs& ga) {
     }
 }
 
+template <class GP, int TM>
+void rg_go(dim3 grid, int W, int per, hipStream_t s, const GemmArgs& ga) {
+    constexpr int DC = TM == 1 ? 4 : 2, DX = TM == 1 ? 2 : 1;
+    const size_t lds = size_t(W) * 2 * 16 * 64 * sizeof(float);
+    hipLaunchKernelGGL((k_gemm_rg<GP, TM, DC, DX>), grid, dim3(unsigned(64 * W)), lds, s, ga, per);
+}
+
+// k_gemm_rg for b's format; TM token tiles per block, `per` super-blocks per
+// wave, W waves (at most kRgWaves).
+template <int TM>
+int launch_rg(const DevBlob& b, dim3 grid, int W, int per, hipStream_t s, const GemmArgs& ga) {
+    switch (b.fmt) {
+    case FMT_Q2_K: rg_go<GemmKQ<2>, TM>(grid, W, per, s, ga); return 0;
+    case FMT_Q3_K: rg_go<GemmKQ<3>, TM>(grid, W, per, s, ga); return 0;
+    case FMT_Q5_K: rg_go<GemmKQ<5>, TM>(grid, W, per, s, ga); return 0;
+    case FMT_Q6_K: rg_go<GemmQ6, TM>(grid, W, per, s, ga); return 0;
+    case FMT_Q8_0: rg_go<GemmQ8, TM>(grid, W, per, s, ga); return 0;
+    case FMT_Q4_0: rg_go<GemmB32<4, false, 8, 0x88888888u>, TM>(grid, W, per, s, ga); return 0;
+    case FMT_Q4_1: rg_go<GemmB32<4, true, 0, 0u>, TM>(grid, W, per, s, ga); return 0;
+    case FMT_Q5_0: rg_go<GemmB32<5, false, 16, 0u>, TM>(grid, W, per, s, ga); return 0;
+    case FMT_Q5_1: rg_go<GemmB32<5, true, 0, 0u>, TM>(grid, W, per, s, ga); return 0;
+    case FMT_AFFINE:
+        switch (b.block_weights) {
+        case 32: rg_go<GemmB32<4, true, 0, 0u, 0>, TM>(grid, W, per, s, ga); return 0;
+        case 64: rg_go<GemmB32<4, true, 0, 0u, 1>, TM>(grid, W, per, s, ga); return 0;
+        case 128: rg_go<GemmB32<4, true, 0, 0u, 2>, TM>(grid, W, per, s, ga); return 0;
+        case 256: rg_go<GemmB32<4, true, 0, 0u, 3>, TM>(grid, W, per, s, ga); return 0;
+        default: return int(hipErrorInvalidValue);
+        }
+    case FMT_BINARY:
+        if (b.block_weights == 128) {
+            rg_go<GemmLin<1, false, 1, 2>, TM>(grid, W, per, s, ga);
+            return 0;
+        }
+        [[fallthrough]];
+    case FMT_IQ1_S: rg_go<GemmLin<1, false, 1>, TM>(grid, W, per, s, ga); return 0;
+    case FMT_IQ2_XXS: rg_go<GemmLin<2, false, 3>, TM>(grid, W, per, s, ga); return 0;
+    case FMT_IQ2_XS: rg_go<GemmLin<2, true, 3>, TM>(grid, W, per, s, ga); return 0;
+    case FMT_IQ3_XXS: rg_go<GemmLin<3, false, 7>, TM>(grid, W, per, s, ga); return 0;
+    case FMT_IQ3_S: rg_go<GemmLin<3, true, 7>, TM>(grid, W, per, s, ga); return 0;
+    case FMT_IQ4_XS: rg_go<GemmLin<4, true, 15>, TM>(grid, W, per, s, ga); return 0;
+    case FMT_TERNARY: rg_go<GemmLin<2, true, 2>, TM>(grid, W, per, s, ga); return 0;
+    case FMT_Q4_K: rg_go<GemmKQ<4>, TM>(grid, W, per, s, ga); return 0;
+    default: return int(hipErrorInvalidValue);
+    }
+}
+
 int launch_gemm(const DevBlob& b, const float* d_x, float* d_y, int M, void* stream, float* d_scratch) {
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (!gemm_supported(b, M)) return int(hipErrorInvalidValue);
-    int bm = 0, splits = 1, per = 0;
-    gemm_plan(b, M, bm, splits, per);
+    const GemmPlan p = gemm_plan(b, M);
+    const int bm = p.bm, splits = p.splits;
     if (!d_scratch) return int(hipErrorInvalidValue);
-    const bool pw = use_pw(b, bm);
     uint4* xh = reinterpret_cast<uint4*>(d_scratch);
     float* xscale = d_scratch + gemm_x_floats(b, M);
     float* part = xscale + gemm_scale_floats(M);
     const int kb8 = int(b.cols / 8);
-    if (pw) launch_x_f16r<1>(d_x, xh, xscale, M, kb8, s);
-    else launch_x_f16r<0>(d_x, xh, xscale, M, kb8, s);
+    if (p.kind == GEMM_RG) launch_x_f16r<true>(d_x, xh, xscale, M, kb8, s);
+    else launch_x_f16r<false>(d_x, xh, xscale, M, kb8, s);
     GemmArgs ga;
     ga.w = b.rpl;
     ga.xh = xh;
@@ -841,15 +867,15 @@ int launch_gemm(const DevBlob& b, const float* d_x, float* d_y, int M, void* str
     ga.y = splits > 1 ? part : d_y;
     ga.M = M;
     ga.K = int(b.cols);
-    ga.sb_per_split = per;
-    if (pw) {
-        const dim3 grid(unsigned((b.rows + 255) / 256), unsigned((M + bm - 1) / bm), unsigned(splits));
-        const int e = bm == 32 ? launch_pw<1>(b, grid, s, ga) : bm == 64 ? launch_pw<2>(b, grid, s, ga) : launch_pw<4>(b, grid, s, ga);
+    ga.sb_per_split = p.sb_per_split;
+    if (p.kind == GEMM_RG) {
+        const dim3 grid(unsigned(b.rpl.rg_count), unsigned((M + bm - 1) / bm), unsigned(splits));
+        const int e = bm == 32 ? launch_rg<1>(b, grid, p.W, p.per, s, ga) : launch_rg<2>(b, grid, p.W, p.per, s, ga);
         if (e) return e;
     } else {
-        const dim3 grid(unsigned((b.rows + BN - 1) / BN), unsigned((M + bm - 1) / bm), unsigned(splits));
-        if (bm == 32) launch_bm<32, 1>(ga, grid, s);
-        else launch_bm<64, 2>(ga, grid, s);
+        const dim3 grid(unsigned((b.rows + 255) / 256), unsigned((M + bm - 1) / bm), unsigned(splits));
+        const int e = launch_pw<4>(b, grid, s, ga);
+        if (e) return e;
     }
     if (splits > 1) {
         const int64_t n = int64_t(M) * b.rows;
