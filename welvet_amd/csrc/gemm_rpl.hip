@@ -452,7 +452,6 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
     const int sb0 = split * ga.sb_per_split;
     const int sb1 = min(a.nsb, sb0 + ga.sb_per_split);
     const int steps = (sb1 - sb0) * 4;
-    const int64_t nsb_total = int64_t(a.rg_count) * a.nsb;
     const int kb8 = ga.K / 8;
     // Row factors of the tile's tokens, staged once; the main loop's barriers
     // order these writes before the epilogue reads them.
@@ -469,7 +468,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
 #pragma unroll
         for (int jj = 0; jj < 2; ++jj) {
             const int j = 2 * (s & 3) + jj;
-            r.c[jj] = GP::load(a, int64_t(j) * nsb_total + si, si, j, lane);
+            r.c[jj] = GP::load(a, rpl_chunk(a, si, j), si, j, lane);
         }
         const int k8 = sb * 32 + (s & 3) * 8;
 #pragma unroll
@@ -572,7 +571,6 @@ __global__ void __launch_bounds__(512) k_gemm_rg(GemmArgs ga, int per) {
     const int sb1 = min(a.nsb, sb0 + ga.sb_per_split);
     const int wsb0 = sb0 + wave * per;
     const int steps = max(0, min(sb1, wsb0 + per) - wsb0) * 4;
-    const int64_t nsb_total = int64_t(a.rg_count) * a.nsb;
     const int mt = (ga.M + 31) / 32;  // 32-token tiles of the fragment-ordered X
 
     struct Codes {
@@ -586,7 +584,7 @@ __global__ void __launch_bounds__(512) k_gemm_rg(GemmArgs ga, int per) {
 #pragma unroll
         for (int jj = 0; jj < 2; ++jj) {
             const int j = 2 * (s & 3) + jj;
-            r.c[jj] = GP::load(a, int64_t(j) * nsb_total + si, si, j, lane);
+            r.c[jj] = GP::load(a, rpl_chunk(a, si, j), si, j, lane);
         }
     };
     auto load_x = [&](int s, Xf& r) {

@@ -4,11 +4,11 @@
 // Layout (built at upload, same byte count as the reference blob): rows are
 // taken 64 at a time (a row group = the 64 lanes of a wave); the codes of a
 // 32-column chunk are stored lane-interleaved so the 64 lanes of one load read
-// 1 KiB contiguous, and chunk-step-major, [j][rg][sb][lane][16 B] with j the
-// chunk's index inside its 256-column super-block: waves step through j in
-// lock-step order, so at any time the GPU as a whole streams one contiguous
-// window of the plane (DRAM-page friendly) instead of thousands of scattered
-// 8 KiB runs. Per-super-block metadata is [rg][sb][lane][...].
+// 1 KiB contiguous. Q4_K stores a super-block's 8 chunks of one row group
+// next to each other, [rg][sb][j][lane][16 B], so the wave that owns the
+// super-block streams one contiguous 8 KiB run; the other formats store the
+// planes chunk-step-major, [j][rg][sb][lane][CB] (rpl_chunk, rpl_strides).
+// Per-super-block metadata is [rg][sb][lane][...].
 //
 // Work split: wave = (row group, super-block): 64 rows x 256 columns, i.e. 8
 // chunks of 16 B per lane. A block holds W waves = W consecutive super-blocks
@@ -665,7 +665,6 @@ __global__ void __launch_bounds__(1024) k_gemv_rpl(RplArgs a, const float* __res
     const int rg = hx / L, h = hx % L;
     const int sl = h * R + r;  // this lane's row slot inside the row group
     const int sb0 = (ks * W + wave) * S;
-    const int64_t nsb_total = int64_t(a.rg_count) * a.nsb;
     bool act[S];
     int64_t si[S];
 #pragma unroll
@@ -711,7 +710,7 @@ __global__ void __launch_bounds__(1024) k_gemv_rpl(RplArgs a, const float* __res
     for (int s = 0; s < S; ++s) sbm[s] = P::load_sb(a, si[s], sl);
     auto chunk_index = [&](int t) {  // plane index of step t's chunk for this lane
         const int s = t / CPL, j = lg + L * (t % CPL);
-        return int64_t(j) * nsb_total + si[s];
+        return rpl_chunk(a, si[s], j);
     };
     typename P::Ch ch[T];
 #pragma unroll
@@ -1295,7 +1294,6 @@ __global__ void __launch_bounds__(256) k_gemvt_rpl(RplArgs a, const float* __res
     const int sb = blockIdx.x, slice = blockIdx.y, b = blockIdx.z;
     const int nslices = gridDim.y;
     const int g0 = slice * GP;
-    const int64_t nsb_total = int64_t(a.rg_count) * a.nsb;
     const int64_t cols = int64_t(a.nsb) * 256;
     const float* gyb = gy + int64_t(b) * a.rows;
 
@@ -1315,8 +1313,8 @@ __global__ void __launch_bounds__(256) k_gemvt_rpl(RplArgs a, const float* __res
     auto load = [&](int i, Set& st) {
         const int g = min(g0 + i, a.rg_count - 1);
         const int64_t si = int64_t(g) * a.nsb + sb;
-        st.c0 = P::load_ch(a, (2 * jp) * nsb_total + si, lane);
-        st.c1 = P::load_ch(a, (2 * jp + 1) * nsb_total + si, lane);
+        st.c0 = P::load_ch(a, rpl_chunk(a, si, 2 * jp), lane);
+        st.c1 = P::load_ch(a, rpl_chunk(a, si, 2 * jp + 1), lane);
         st.tm = P::load_tm(a, si, lane, jp);
         st.gy = gyb[min(g * 64 + lane, a.rows - 1)];
     };
@@ -1518,22 +1516,32 @@ bool rpl_items(const DevBlob& b, RplItems& it) {
     }
 }
 
-// dst[p][G][sb][L] = (L even ? a : b)[p][G/2][sb][32*(G%2) + L/2], items of
-// isz bytes (a multiple of 4), G < 2*rg_in: rows 2i / 2i+1 <- a / b row i.
+// Rows 2i / 2i+1 of dst <- row i of a / b, items of isz bytes (a multiple of
+// 4), G < 2*rg_in the destination row group: with sb_major (Q4_K code
+// planes, rpl_strides) dst[G][sb][p][L] = (L even ? a : b)[G/2][sb][p][32*(G%2)
+// + L/2], otherwise the same in [p][G][sb][L] order; metadata has planes = 1.
 __global__ void __launch_bounds__(256) k_rpl_pairs(uint8_t* __restrict__ dst, const uint8_t* __restrict__ a,
                                                    const uint8_t* __restrict__ b, int isz, int64_t rg_in, int64_t nsb,
-                                                   int64_t planes) {
+                                                   int64_t planes, int sb_major) {
     const int64_t n = planes * 2 * rg_in * nsb * 64;
     const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
     if (i >= n) return;
     const int L = int(i & 63);
-    int64_t r = i >> 6;
-    const int64_t sb = r % nsb;
-    r /= nsb;
-    const int64_t G = r % (2 * rg_in);
-    const int64_t p = r / (2 * rg_in);
+    int64_t r = i >> 6, p, sb, G;
+    if (sb_major) {
+        p = r % planes;
+        r /= planes;
+        sb = r % nsb;
+        G = r / nsb;
+    } else {
+        sb = r % nsb;
+        r /= nsb;
+        G = r % (2 * rg_in);
+        p = r / (2 * rg_in);
+    }
     const uint8_t* src = (L & 1) ? b : a;
-    const int64_t si = ((p * rg_in + G / 2) * nsb + sb) * 64 + 32 * (G & 1) + (L >> 1);
+    const int64_t si = sb_major ? (((G / 2) * nsb + sb) * planes + p) * 64 + 32 * (G & 1) + (L >> 1)
+                                : ((p * rg_in + G / 2) * nsb + sb) * 64 + 32 * (G & 1) + (L >> 1);
     const uint32_t* s4 = reinterpret_cast<const uint32_t*>(src + si * isz);
     uint32_t* d4 = reinterpret_cast<uint32_t*>(dst + i * isz);
     for (int k = 0; k < isz / 4; ++k) d4[k] = s4[k];
@@ -1579,6 +1587,7 @@ void finish_fused(const DevBlob& proto, int64_t rows, int64_t rg, const FusedLay
     r.nsb = proto.rpl.nsb;
     r.rg_count = int(rg);
     r.ksplit = 1;
+    rpl_strides(proto.fmt, rg, r.nsb, r.cs_si, r.cs_j);
 }
 
 }  // namespace
@@ -1607,12 +1616,18 @@ int rpl_fuse_rows(const DevBlob* parts, int n, DevBlob& out, void* stream) {
         const RplArgs& r = parts[i].rpl;
         const size_t per = size_t(r.rg_count) * nsb * 64, off = size_t(g0) * nsb * 64;
         const size_t per_all = size_t(rg) * nsb * 64;
-        for (int p = 0; p < 8 && e == hipSuccess; ++p) {
-            e = hipMemcpyAsync(b8 + f.codes + (p * per_all + off) * it.cb, r.codes + p * per * it.cb, per * it.cb,
-                               hipMemcpyDeviceToDevice, s);
+        if (rpl_sb_major(parts[0].fmt)) {  // row-group-major planes: one contiguous run per part
+            e = hipMemcpyAsync(b8 + f.codes + off * 8 * it.cb, r.codes, per * 8 * it.cb, hipMemcpyDeviceToDevice, s);
             if (it.hb && e == hipSuccess)
-                e = hipMemcpyAsync(b8 + f.hi + (p * per_all + off) * it.hb, r.hi + p * per * it.hb, per * it.hb,
+                e = hipMemcpyAsync(b8 + f.hi + off * 8 * it.hb, r.hi, per * 8 * it.hb, hipMemcpyDeviceToDevice, s);
+        } else {  // chunk-step-major planes: one run per chunk step
+            for (int p = 0; p < 8 && e == hipSuccess; ++p) {
+                e = hipMemcpyAsync(b8 + f.codes + (p * per_all + off) * it.cb, r.codes + p * per * it.cb, per * it.cb,
                                    hipMemcpyDeviceToDevice, s);
+                if (it.hb && e == hipSuccess)
+                    e = hipMemcpyAsync(b8 + f.hi + (p * per_all + off) * it.hb, r.hi + p * per * it.hb, per * it.hb,
+                                       hipMemcpyDeviceToDevice, s);
+            }
         }
         if (e == hipSuccess) e = hipMemcpyAsync(b8 + f.meta + off * it.mb, r.meta, per * it.mb, hipMemcpyDeviceToDevice, s);
         if (it.db && e == hipSuccess)
@@ -1641,10 +1656,11 @@ int rpl_fuse_pairs(const DevBlob& a, const DevBlob& b, DevBlob& out, void* strea
     hipError_t e = hipMalloc(&base, f.total);
     if (e != hipSuccess) return int(e);
     uint8_t* b8 = static_cast<uint8_t*>(base);
+    const int sbm = rpl_sb_major(a.fmt) ? 1 : 0;
     auto run = [&](size_t off, const uint8_t* pa, const uint8_t* pb, int isz, int64_t planes) {
         const int64_t n = planes * rg * nsb * 64;
         hipLaunchKernelGGL(k_rpl_pairs, dim3(unsigned((n + 255) / 256)), dim3(256), 0, s, b8 + off, pa, pb, isz, rg_in,
-                           nsb, planes);
+                           nsb, planes, sbm);
     };
     run(f.codes, a.rpl.codes, b.rpl.codes, it.cb, 8);
     if (it.hb) run(f.hi, a.rpl.hi, b.rpl.hi, it.hb, 8);

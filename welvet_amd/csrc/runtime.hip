@@ -280,13 +280,15 @@ struct Image {
 //   Q8_0 / Q4_0: codes 32 / 16 B per 32-block; meta 8 f32 block scales.
 //   Q4_1 / Q5_0 / Q5_1: codes as Q4_0 (Q5_x: low 4 bits, plus the fifth
 //         bits as Q5_K's); meta 8 f32 scales, then (Q4_1, Q5_1) 8 f32 mins.
-// Code (and Q6_K high-bit) planes are chunk-step-major, [j][rg][sb][lane],
-// j = chunk index inside the super-block; meta/dd are [rg][sb][lane].
+// Code (and high-bit) planes are in the chunk order rpl_strides gives (j =
+// chunk index inside the super-block); meta/dd are [rg][sb][lane].
 struct RplOffsets {
     size_t codes = 0, hi = 0, meta = 0, dd = 0;
 };
 void build_rpl(int fmt, const uint8_t* raw, int64_t rows, int64_t cols, Image& img, RplOffsets& o) {
     const int64_t rg = (rows + 63) / 64, nch = cols / 32, nsb = cols / 256;
+    int64_t cs_si = 0, cs_j = 0;
+    rpl_strides(fmt, rg, nsb, cs_si, cs_j);
     const bool low2 = fmt == FMT_Q2_K || fmt == FMT_Q3_K;  // 2-bit plane (+ third bits)
     const bool bmin = fmt == FMT_Q4_1 || fmt == FMT_Q5_1;  // 32-blocks with a min
     const bool five = fmt == FMT_Q5_K || fmt == FMT_Q5_0 || fmt == FMT_Q5_1;
@@ -318,7 +320,7 @@ void build_rpl(int fmt, const uint8_t* raw, int64_t rows, int64_t cols, Image& i
                         dd[2 * mi] = f32_at(o8);
                         dd[2 * mi + 1] = f32_at(o8 + 4);
                         for (int p = 0; p < 8; ++p) {
-                            const int64_t ci = ((p * rg + g) * nsb + sb) * 64 + lane;  // [j][rg][sb][lane]
+                            const int64_t ci = ((g * nsb + sb) * cs_si + p * cs_j) * 64 + lane;
                             const uint8_t u0 = std::max<uint8_t>(o8[8 + 2 * p], 1), u1 = std::max<uint8_t>(o8[9 + 2 * p], 1);
                             if (fmt == FMT_Q4_K) {
                                 m[4 * p] = u0;
@@ -383,7 +385,7 @@ void build_rpl(int fmt, const uint8_t* raw, int64_t rows, int64_t cols, Image& i
                         const int hdr = bmin ? 8 : 4;
                         for (int p = 0; p < 8; ++p) {
                             const uint8_t* blk = raw + (row * nch + sb * 8 + p) * bb;
-                            const int64_t ci = ((p * rg + g) * nsb + sb) * 64 + lane;
+                            const int64_t ci = ((g * nsb + sb) * cs_si + p * cs_j) * 64 + lane;
                             std::memcpy(m + 4 * p, blk, 4);
                             if (bmin) std::memcpy(m + 32 + 4 * p, blk + 4, 4);
                             if (!five) {
@@ -425,11 +427,13 @@ void build_rpl(int fmt, const uint8_t* raw, int64_t rows, int64_t cols, Image& i
 // bits); 1-bit codes as one 32-bit word holding at bit s of byte b the code
 // of column 8(s/2) + 2b + s%2. Meta: per super-block 8 (group 32) or 16
 // (group 16) f32 scales.
-void build_rpl_lin(const LinCodes& lc, const uint8_t* raw, size_t raw_len, const float* scales, size_t n_scales,
-                   int64_t rows, int64_t cols, Image& img, RplOffsets& o) {
+void build_rpl_lin(int fmt, const LinCodes& lc, const uint8_t* raw, size_t raw_len, const float* scales,
+                   size_t n_scales, int64_t rows, int64_t cols, Image& img, RplOffsets& o) {
     const int bits = lc.bits, sg = lc.sg;
     auto scale_at = [&](int64_t g) { return size_t(g) < n_scales && scales ? scales[g] : 1.0f; };
     const int64_t rg = (rows + 63) / 64, nch = cols / 32, nsb = cols / 256;
+    int64_t cs_si = 0, cs_j = 0;
+    rpl_strides(fmt, rg, nsb, cs_si, cs_j);
     const int nw = 256 / sg;  // scales per lane and super-block
     const int cb = bits == 4 ? 16 : bits >= 2 ? 8 : 4, mb = 4 * nw;
     o.codes = img.add(size_t(rg * nch * 64 * cb));
@@ -458,7 +462,7 @@ void build_rpl_lin(const LinCodes& lc, const uint8_t* raw, size_t raw_len, const
                             if (lc.remap3 && qv[k] == 3) qv[k] = 1;  // TernaryPacked: code 3 decodes as 0
                         }
                         auto code = [&](int sw, int b) { return qv[8 * (sw >> 1) + 2 * b + (sw & 1)]; };
-                        const int64_t ci = ((p * rg + g) * nsb + sb) * 64 + lane;
+                        const int64_t ci = ((g * nsb + sb) * cs_si + p * cs_j) * 64 + lane;
                         uint8_t* c = codes + ci * cb;
                         std::memset(c, 0, size_t(cb));
                         if (bits == 4) {
@@ -497,6 +501,8 @@ void build_rpl_affine(const uint8_t* raw, const float* scales, const float* mins
                       Image& img, RplOffsets& o) {
     const int ng = 256 / bw;  // groups per super-block: ng scales, then ng mins, per lane
     const int64_t rg = (rows + 63) / 64, nch = cols / 32, nsb = cols / 256, gpr = cols / bw;
+    int64_t cs_si = 0, cs_j = 0;
+    rpl_strides(FMT_AFFINE, rg, nsb, cs_si, cs_j);
     o.codes = img.add(size_t(rg * nch * 64 * 16));
     o.meta = img.add(size_t(rg * nsb * 64 * 8 * ng));
     uint8_t* base = img.bytes.data();
@@ -513,7 +519,7 @@ void build_rpl_affine(const uint8_t* raw, const float* scales, const float* mins
                     m[ng + q] = mins[row * gpr + sb * ng + q];
                 }
                 for (int p = 0; p < 8; ++p)
-                    std::memcpy(codes + (((p * rg + g) * nsb + sb) * 64 + lane) * 16, raw + (row * cols + sb * 256 + p * 32) / 2, 16);
+                    std::memcpy(codes + (((g * nsb + sb) * cs_si + p * cs_j) * 64 + lane) * 16, raw + (row * cols + sb * 256 + p * 32) / 2, 16);
             }
         }
 }
@@ -734,7 +740,7 @@ int wv_blob_upload(int format, int64_t rows, int64_t cols, int32_t block_weights
         build_rpl(format, raw, rows, cols, img, ro);
     } else if (LinCodes lc; !raw_only && rpl_lin_spec(format, block_weights, b.iq_bits, b.iq_sg, lc) && cols % 256 == 0) {
         b.layout = LAYOUT_RPL;
-        build_rpl_lin(lc, raw, raw_len, scales, n_scales, rows, cols, img, ro);
+        build_rpl_lin(format, lc, raw, raw_len, scales, n_scales, rows, cols, img, ro);
     } else if (!raw_only && format == FMT_AFFINE && rpl_affine_group(block_weights) && cols % 256 == 0) {
         b.layout = LAYOUT_RPL;
         build_rpl_affine(raw, scales, mins, rows, cols, block_weights, img, ro);
@@ -776,6 +782,7 @@ int wv_blob_upload(int format, int64_t rows, int64_t cols, int32_t block_weights
         r.nsb = int(cols / 256);
         r.rg_count = int((rows + 63) / 64);
         r.ksplit = 1;
+        rpl_strides(b.fmt, r.rg_count, r.nsb, r.cs_si, r.cs_j);
     }
     std::lock_guard<std::mutex> lk(g_mu);
     const uint64_t h = g_next++;

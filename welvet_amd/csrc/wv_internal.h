@@ -143,11 +143,24 @@ enum Layout : int {
 
 // Device view of a row-interleaved blob. Rows are grouped 64 at a time (one
 // wave's lanes); chunk = 32 columns, super-block (sb) = 256 columns.
-//   codes [j][rg][sb][lane][CB]   CB = 16 B (4-bit codes), 32 B (Q8_0); j = chunk in sb
-//   hi    [j][rg][sb][lane][8 B]  Q6_K high 2 bits
+//   codes [rg][sb][j][lane][CB] (Q4_K) or [j][rg][sb][lane][CB] (the other
+//         formats); CB = 8 / 16 / 32 B per lane and chunk; j = chunk in sb
+//   hi    high code bits in the codes' order (Q6_K 8 B, Q5_x / Q3_K 4 B)
 //   meta  [rg][sb][lane][MB]      MB = 32 B (Q4_K scale/min bytes, Q8_0/Q4_0
 //                                  f32 block scales) or 16 B (Q6_K scales)
 //   dd    [rg][sb][lane] (d, dmin) f32 pair (k-quants)
+// Chunk j of super-block slot si = row group * nsb + super-block sits at chunk
+// index si * cs_si + j * cs_j (times 64 lanes). Q4_K keeps a super-block's 8
+// chunks of one row group adjacent (cs_si = 8, cs_j = 1: the owning wave
+// streams one 8 KiB run); the other formats keep them chunk-step-major
+// (cs_si = 1, cs_j = row groups * nsb: every wave reads the same chunk step
+// together), which measured faster for their wider chunks.
+inline bool rpl_sb_major(int fmt) { return fmt == FMT_Q4_K; }
+inline void rpl_strides(int fmt, int64_t rg, int64_t nsb, int64_t& cs_si, int64_t& cs_j) {
+    cs_si = rpl_sb_major(fmt) ? 8 : 1;
+    cs_j = rpl_sb_major(fmt) ? 1 : rg * nsb;
+}
+
 struct RplArgs {
     const uint8_t* codes;
     const uint8_t* hi;
@@ -158,6 +171,7 @@ struct RplArgs {
     // blob may run at once).
     float* partial;
     int rows, nsb, rg_count, ksplit;
+    int64_t cs_si, cs_j;  // chunk strides of the code planes (rpl_chunk)
     // Output epilogue of the forward kernel: RPL_STORE y = Wx;
     // RPL_ADD y += Wx (residual); RPL_SILU_MUL y = silu(aux) * Wx (SwiGLU up);
     // RPL_SWIGLU on a gate/up row-pair blob (row 2i gate i, row 2i+1 up i):
@@ -174,7 +188,9 @@ struct RplArgs {
     // With RPL_ADD: sums of the updated y^2 over each 16 rows
     // ([batch][rg*4]), the partials the next fused RMSNorm consumes.
     float* ss_out;
-};
+};// Chunk index (in lane items / 64) of chunk j of super-block slot si.
+constexpr int64_t rpl_chunk(const RplArgs& a, int64_t si, int j) { return si * a.cs_si + j * a.cs_j; }
+
 
 // Options of one forward launch on the row-interleaved layout.
 struct RplExtra {
