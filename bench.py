@@ -95,9 +95,9 @@ DECODE = {
 COPY_FETCH_SCALE = 65536.0 / 32779.5
 COPY_WRITE_SCALE = 65536.0 / 65536.0
 PMC_KIB = {
-    "q4k_4096x14336": (18946.0, 56.0),
-    "q4k_4096x4096": (5497.0, 16.0),
-    "q4k_14336x4096": (19121.5, 16.0),
+    "q4k_4096x14336": (18946.19, 56.0),
+    "q4k_4096x4096": (5499.5, 16.0),
+    "q4k_14336x4096": (19113.0, 16.0),
     "q8_0_4096x4096": (9329.0, 16.0),
     "q8_0_4096x14336": (32450.56, 56.0),
     "q8_0_14336x4096": (32657.0, 16.0),
