@@ -109,6 +109,29 @@ def test_prefill_other_formats_mfma(fmt, shape, m):
     d.free()
 
 
+@pytest.mark.parametrize("fmt", ["Q4_K", "Q8_0", "Q4_0", "IQ2_XS"])
+@pytest.mark.parametrize("m", [65, 100, 128])
+def test_prefill_four_tile_blocks(fmt, m):
+    """65 to 128 tokens on 200 row groups or more take the K-split-free
+    small-M kernel with four 32-token tiles per wave (a ragged last tile)."""
+    rows, cols = 12800, 512
+    print(f"[gpu] prefill four-tile {fmt} {cols}->{rows} M={m}", flush=True)
+    rng = np.random.default_rng(7 + m)
+    w = (rng.standard_normal(rows * cols, dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+    p = wv.pack(fmt, w, rows, cols)
+    wd = oracle.unpack(oracle.Packed(p.fmt, rows, cols, p.raw, p.scales, p.meta, p.block_weights, p.mins))
+    wd = wd.reshape(rows, cols).astype(np.float64)
+    d = wv.upload(p)
+    assert d.info()["layout"] == "row-interleaved"
+    x = rng.standard_normal((m, cols)).astype(np.float32)
+    ref = x.astype(np.float64) @ wd.T
+    for _ in range(2):
+        y = d.matmul(x)
+        assert normwise(y, ref) <= TOL_MFMA
+        assert rowwise(y, ref) <= 4 * TOL_MFMA
+    d.free()
+
+
 @pytest.mark.parametrize("fmt", ["Q4_K", "Q6_K"])
 @pytest.mark.parametrize("m", [32, 64, 128, 300])
 def test_prefill_outlier_and_tiny_activations(fmt, m):

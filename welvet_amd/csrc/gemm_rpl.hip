@@ -557,8 +557,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
 // ahead, in register rings. Every weight is dequantized once per token block.
 // The W waves' partial tiles meet in LDS after the loop and are added in wave
 // order (deterministic), one 32-token tile at a time.
-template <class GP, int TM, int DC, int DX>
-__global__ void __launch_bounds__(512) k_gemm_rg(GemmArgs ga, int per) {
+template <class GP, int TM, int DC, int DX, int NT>
+__global__ void __launch_bounds__(NT) k_gemm_rg(GemmArgs ga, int per) {
     constexpr int BM = 32 * TM;
     static_assert(4 % DC == 0 && 4 % DX == 0, "the rings must divide the 4 steps of a super-block");
     constexpr int DU = DC > DX ? DC : DX;  // loop unroll: both ring positions are compile-time
@@ -715,25 +715,30 @@ bool gemm_supported(const DevBlob& b, int M) {
 // Which kernel runs a token block, its tile height (bm tokens), the K split
 // (splits of sb_per_split super-blocks) and, for k_gemm_rg, its waves per
 // block W and super-blocks per wave `per`:
-//   * up to 64 tokens: k_gemm_rg (one block per 64-row group, up to 8 waves
+//   * up to 64 tokens: k_gemm_rg (one block per 64-row group, 8 waves
 //     splitting K, one or two 32-token tiles), K split over blocks only while
 //     the row groups alone give fewer than 200 blocks;
-//   * more: k_gemm_q4k_pw (256-row tiles of 128 tokens, one block per CU), K
-//     split while whole tiles leave CUs idle.
+//   * 65 to 128 tokens on at least 200 row groups: k_gemm_rg with four
+//     32-token tiles (4 waves, one per SIMD), no K split (4096->14336 M = 128
+//     43.5 against 45.7 us; with the split, 14336->4096, 49.3 against 45.0);
+//   * otherwise k_gemm_q4k_pw (256-row tiles of 128 tokens, one block per
+//     CU), K split while whole tiles leave CUs idle.
 enum { GEMM_PW = 1, GEMM_RG = 2 };
-constexpr int kRgWaves = 8;  // k_gemm_rg waves per block (2 per SIMD)
+// k_gemm_rg waves per block: 8 (2 per SIMD) for one or two 32-token tiles,
+// 4 (1 per SIMD) for four.
+constexpr int rg_waves(int tm) { return tm == 4 ? 4 : 8; }
 struct GemmPlan {
     int kind, bm, splits, sb_per_split, W, per;
 };
-constexpr int kRgMaxM = 64;
+constexpr int kRgMinBlocks = 200;  // k_gemm_rg blocks that fill the GPU (no K split below 65 tokens)
 GemmPlan gemm_plan(const DevBlob& b, int M) {
     const RplArgs& a = b.rpl;
     GemmPlan p{GEMM_PW, M <= 32 ? 32 : M <= 64 ? 64 : 128, 1, a.nsb, 1, 1};
     int want = 1;
-    if (M <= kRgMaxM) {
+    if (M <= 64 || (M <= 128 && a.rg_count >= kRgMinBlocks)) {
         p.kind = GEMM_RG;
         const int64_t tiles = int64_t(a.rg_count) * ((M + p.bm - 1) / p.bm);
-        want = int(std::max<int64_t>(1, (200 + tiles - 1) / tiles));
+        want = int(std::max<int64_t>(1, (kRgMinBlocks + tiles - 1) / tiles));
         want = std::min(want, std::max(1, a.nsb / 8));  // each split >= 8 super-blocks
     } else {
         const int64_t tiles = int64_t((a.rows + 255) / 256) * ((M + p.bm - 1) / p.bm);
@@ -743,7 +748,7 @@ GemmPlan gemm_plan(const DevBlob& b, int M) {
     p.sb_per_split = (a.nsb + want - 1) / want;
     p.splits = (a.nsb + p.sb_per_split - 1) / p.sb_per_split;
     if (p.kind == GEMM_RG) {
-        p.per = (p.sb_per_split + kRgWaves - 1) / kRgWaves;
+        p.per = (p.sb_per_split + rg_waves(p.bm / 32) - 1) / rg_waves(p.bm / 32);
         p.W = (p.sb_per_split + p.per - 1) / p.per;
     }
     return p;
@@ -799,15 +804,18 @@ int launch_pw(const DevBlob& b, dim3 grid, hipStream_t s, const GemmArgs& ga) {
     }
 }
 
+// Ring depths and block size per token tiles: one or two tiles run 8 waves
+// (2 per SIMD, 256 registers each), four tiles 4 waves (1 per SIMD, whose 512
+// registers hold the 128 accumulators and deeper rings).
 template <class GP, int TM>
 void rg_go(dim3 grid, int W, int per, hipStream_t s, const GemmArgs& ga) {
-    constexpr int DC = TM == 1 ? 4 : 2, DX = TM == 1 ? 2 : 1;
+    constexpr int DC = TM == 2 ? 2 : 4, DX = TM == 1 ? 2 : TM == 2 ? 1 : 2, NT = TM == 4 ? 256 : 512;
     const size_t lds = size_t(W) * 2 * 16 * 64 * sizeof(float);
-    hipLaunchKernelGGL((k_gemm_rg<GP, TM, DC, DX>), grid, dim3(unsigned(64 * W)), lds, s, ga, per);
+    hipLaunchKernelGGL((k_gemm_rg<GP, TM, DC, DX, NT>), grid, dim3(unsigned(64 * W)), lds, s, ga, per);
 }
 
 // k_gemm_rg for b's format; TM token tiles per block, `per` super-blocks per
-// wave, W waves (at most kRgWaves).
+// wave, W waves (at most rg_waves(TM)).
 template <int TM>
 int launch_rg(const DevBlob& b, dim3 grid, int W, int per, hipStream_t s, const GemmArgs& ga) {
     switch (b.fmt) {
@@ -868,7 +876,9 @@ int launch_gemm(const DevBlob& b, const float* d_x, float* d_y, int M, void* str
     ga.sb_per_split = p.sb_per_split;
     if (p.kind == GEMM_RG) {
         const dim3 grid(unsigned(b.rpl.rg_count), unsigned((M + bm - 1) / bm), unsigned(splits));
-        const int e = bm == 32 ? launch_rg<1>(b, grid, p.W, p.per, s, ga) : launch_rg<2>(b, grid, p.W, p.per, s, ga);
+        const int e = bm == 32   ? launch_rg<1>(b, grid, p.W, p.per, s, ga)
+                      : bm == 64 ? launch_rg<2>(b, grid, p.W, p.per, s, ga)
+                                 : launch_rg<4>(b, grid, p.W, p.per, s, ga);
         if (e) return e;
     } else {
         const dim3 grid(unsigned((b.rows + 255) / 256), unsigned((M + bm - 1) / bm), unsigned(splits));
