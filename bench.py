@@ -242,7 +242,7 @@ def main():
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU (every box here has one MI355X); "
-              "multi-GPU sharding is described in DESIGN.md, not run. Use --gpus 1.", file=sys.stderr)
+              "the multi-GPU sharding plan is design-only, not run. Use --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
     import torch

@@ -220,9 +220,9 @@ int wv_store_matvec(uint64_t handle, const double *x, size_t len_x, double *y, s
  * independent GEMVs. Row-interleaved blobs use fp16 MFMA with f32
  * accumulation (results within 2e-3 normwise of the f64 reference, not the
  * 1e-5 of wv_matvec): Q4_K at every m, the other row-interleaved formats
- * (wv_blob_info layout "row-interleaved") from m = 9. Every other case runs
- * the batched GEMV kernels of wv_matvec_dev. Device pointers, enqueued on
- * `stream`. */
+ * (wv_blob_info layout "row-interleaved") but IQ4_NL from m = 9. Every other
+ * case runs the batched GEMV kernels of wv_matvec_dev. Device pointers,
+ * enqueued on `stream`. */
 int wv_matmul_dev(uint64_t handle, const float *d_x, float *d_y, int32_t m, void *stream);
 
 /* Host-pointer form of wv_matmul_dev; synchronous. */
