@@ -219,7 +219,9 @@ int wv_store_matvec(uint64_t handle, const double *x, size_t len_x, double *y, s
  * batch loop of forwardSIMDQ4_0 (layers/dense/simd.go:294-299), which run M
  * independent GEMVs. Row-interleaved blobs use fp16 MFMA with f32
  * accumulation (results within 2e-3 normwise of the f64 reference, not the
- * 1e-5 of wv_matvec): Q4_K at every m, the other row-interleaved formats
+ * 1e-5 of wv_matvec; each token row and each weight row is scaled by a power
+ * of two into fp16's range and back, so outlier or tiny activations and
+ * weights keep that bar): Q4_K at every m, the other row-interleaved formats
  * (wv_blob_info layout "row-interleaved") but IQ4_NL from m = 9. Every other
  * case runs the batched GEMV kernels of wv_matvec_dev. Device pointers,
  * enqueued on `stream`. */

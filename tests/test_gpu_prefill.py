@@ -166,6 +166,47 @@ def test_prefill_outlier_and_tiny_activations(fmt, m):
     d.free()
 
 
+@pytest.mark.parametrize("fmt", ["Q4_K", "Q6_K", "Q3_K", "Q8_0", "Q4_0", "Q5_1", "IQ2_XS", "TernaryPacked",
+                                 "AffinePacked"])
+@pytest.mark.parametrize("m", [16, 64, 300])
+def test_prefill_tiny_and_huge_weight_rows(fmt, m):
+    """Weight rows the fp16 B operand cannot hold unscaled: rows scaled by
+    1e-9 (scales and weights fp16-subnormal or zero) up to 1e6 (weights past
+    65504), and an all-zero row. Each row's scales and mins are multiplied by
+    a power-of-two row factor before the fp16 cast and its outputs divided by
+    it, so the rows of every scale meet the 2e-3 normwise bar on their own
+    (and each row the 4x looser row-wise bar the other prefill tests use),
+    with nothing inf or NaN, in both GEMM kernels (16 and 64 tokens: one block
+    per row group; 300: 256-row tiles)."""
+    rows, cols = 448, 2048
+    print(f"[gpu] prefill weight rows 1e-9..1e6 {fmt} M={m}", flush=True)
+    rng = np.random.default_rng(23 + m)
+    w = rng.standard_normal((rows, cols), dtype=np.float32) * np.float32(0.02)
+    decade = rng.choice([-9, -7, -5, -3, 0, 2, 4, 6], rows)
+    w *= (10.0 ** decade).astype(np.float32)[:, None]
+    w[5] = 0.0
+    w = np.ascontiguousarray(w, np.float32).ravel()
+    p = wv.pack(fmt, w, rows, cols)
+    wd = oracle.unpack(oracle.Packed(p.fmt, rows, cols, p.raw, p.scales, p.meta, p.block_weights, p.mins))
+    wd = wd.reshape(rows, cols).astype(np.float64)
+    d = wv.upload(p)
+    assert d.info()["layout"] == "row-interleaved"
+    x = rng.standard_normal((m, cols)).astype(np.float32)
+    ref = x.astype(np.float64) @ wd.T
+    y = d.matmul(x)
+    assert np.isfinite(y).all()
+    zero = ~wd.any(axis=1)  # the zero row, unless the format decodes zeros off zero (IQ2_XS: +-scale/2)
+    assert np.array_equal(y[:, zero], np.zeros((m, int(zero.sum())), np.float32))
+    live = ~zero
+    for e in np.unique(decade):
+        sel = live & (decade == e)
+        err = normwise(y[:, sel], ref[:, sel])
+        print(f"[gpu]   rows x 1e{e}: normwise err {err:.3e}", flush=True)
+        assert err <= TOL_MFMA
+    assert rowwise(y.T[live], ref.T[live]) <= 4 * TOL_MFMA  # per weight row
+    d.free()
+
+
 _BASE = {}
 
 

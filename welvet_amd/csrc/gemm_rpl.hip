@@ -10,7 +10,12 @@
 // before the cast, and the epilogue multiplies the row back: the scaling is
 // exact, so rows that fit fp16 get the same fp16 values as an unscaled cast,
 // while outlier rows (|x| > 65504) stay finite and rows of tiny activations
-// keep their precision instead of going subnormal.
+// keep their precision instead of going subnormal. Weight rows get the same
+// treatment from a power-of-two factor stored per row at upload
+// (RplArgs::wrow) that puts the row's largest fp16 B-operand value in
+// [2^12, 2^13): the B-operand builders multiply the row's scales and mins by
+// it before their fp16 cast and the epilogue divides it back out, so rows of
+// tiny weights keep fp16's precision and rows past 65504 stay finite.
 //
 // W goes from the row-interleaved planes straight into MFMA B operands: a
 // lane holds 32 columns of its row per chunk, and a lane swap puts them into
@@ -145,10 +150,12 @@ struct GemmCodes {
     }
 };
 
-// Per-format B-operand builders of k_gemm_q4k_pw. Ch holds one 32-column
+// Per-format B-operand builders of the GEMM kernels. Ch holds one 32-column
 // chunk of the lane's row (codes, the chunk's metadata, the super-block's
 // scales); bops() returns the fp16 B operands bf[T][kk] of 32-row tile T and
-// k16 step kk, in X's k order [0,2,4,6,1,3,5,7].
+// k16 step kk, in X's k order [0,2,4,6,1,3,5,7], with the tile row's scales
+// and mins multiplied by its power-of-two row factor wk[T] (RplArgs::wrow)
+// before their fp16 cast.
 template <int FB>
 struct GemmKQ {  // Q2_K, Q3_K, Q4_K, Q5_K: w = (d/255)*u*q + (dmin/127)*m
     struct Ch { typename GemmCodes<FB>::C c; uint32_t mw; float2 dd; };
@@ -156,7 +163,7 @@ struct GemmKQ {  // Q2_K, Q3_K, Q4_K, Q5_K: w = (d/255)*u*q + (dmin/127)*m
         return {GemmCodes<FB>::load(a, ci, lane), reinterpret_cast<const uint32_t*>(a.meta)[(si * 64 + lane) * 8 + j],
                 reinterpret_cast<const float2*>(a.dd)[si * 64 + lane]};
     }
-    static __device__ __forceinline__ void bops(const Ch& c, int lane, half8 (&bf)[2][2]) {
+    static __device__ __forceinline__ void bops(const Ch& c, int lane, const float (&wk)[2], half8 (&bf)[2][2]) {
         const auto d2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(c.dd.x), __float_as_uint(c.dd.x), false, false);
         const auto m2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(c.dd.y), __float_as_uint(c.dd.y), false, false);
         const auto mt = __builtin_amdgcn_permlane32_swap(c.mw, c.mw, false, false);
@@ -164,8 +171,8 @@ struct GemmKQ {  // Q2_K, Q3_K, Q4_K, Q5_K: w = (d/255)*u*q + (dmin/127)*m
         GemmCodes<FB>::spread(c.c, lane, se, so);
 #pragma unroll
         for (int T = 0; T < 2; ++T) {
-            const float d255 = __uint_as_float(d2[T]) * (1.0f / 255.0f);
-            const float dm127 = __uint_as_float(m2[T]) * (1.0f / 127.0f);
+            const float d255 = __uint_as_float(d2[T]) * (wk[T] * (1.0f / 255.0f));
+            const float dm127 = __uint_as_float(m2[T]) * (wk[T] * (1.0f / 127.0f));
             const uint32_t gm = mt[T];
             const _Float16 sc0 = _Float16(d255 * float(gm & 0xFFu));
             const _Float16 sc1 = _Float16(d255 * float((gm >> 8) & 0xFFu));
@@ -186,7 +193,7 @@ struct GemmQ6 {  // Q6_K: q = lo4 | hi2 << 4, w = (d/255)*u*(q - 32)
                 reinterpret_cast<const uint2*>(a.hi)[ci * 64 + lane], m >> (16 * (j & 1)),
                 reinterpret_cast<const float*>(a.dd)[(si * 64 + lane) * 2]};
     }
-    static __device__ __forceinline__ void bops(const Ch& c, int lane, half8 (&bf)[2][2]) {
+    static __device__ __forceinline__ void bops(const Ch& c, int lane, const float (&wk)[2], half8 (&bf)[2][2]) {
         typename GemmCodes<4>::C nib{c.c, 0u};
         uint32_t se[2][2], so[2][2];
         GemmCodes<4>::spread(nib, lane, se, so);
@@ -202,7 +209,7 @@ struct GemmQ6 {  // Q6_K: q = lo4 | hi2 << 4, w = (d/255)*u*(q - 32)
             so[T][0] |= ((h0[T] >> (sh + 2)) & 0x03030303u) << 4;
             se[T][1] |= ((h1[T] >> sh) & 0x03030303u) << 4;
             so[T][1] |= ((h1[T] >> (sh + 2)) & 0x03030303u) << 4;
-            const float d255 = __uint_as_float(dt[T]) * (1.0f / 255.0f);
+            const float d255 = __uint_as_float(dt[T]) * (wk[T] * (1.0f / 255.0f));
             const _Float16 sc0 = _Float16(d255 * float(mt[T] & 0xFFu)), sc1 = _Float16(d255 * float((mt[T] >> 8) & 0xFFu));
             const _Float16 mn0 = _Float16(-32.0f) * sc0, mn1 = _Float16(-32.0f) * sc1;
             const half2v s0 = {sc0, sc0}, s1 = {sc1, sc1}, n0 = {mn0, mn0}, n1 = {mn1, mn1};
@@ -218,7 +225,7 @@ struct GemmQ8 {  // Q8_0: w = scale*q, q int8, 32 bytes per chunk (consecutive c
         const uint4* p = reinterpret_cast<const uint4*>(a.codes) + (ci * 64 + lane) * 2;
         return {ld_nt(p), ld_nt(p + 1), reinterpret_cast<const uint32_t*>(a.meta)[(si * 64 + lane) * 8 + j]};
     }
-    static __device__ __forceinline__ void bops(const Ch& c, int lane, half8 (&bf)[2][2]) {
+    static __device__ __forceinline__ void bops(const Ch& c, int lane, const float (&wk)[2], half8 (&bf)[2][2]) {
         (void)lane;
         const uint32_t dw[8] = {c.c0.x, c.c0.y, c.c0.z, c.c0.w, c.c1.x, c.c1.y, c.c1.z, c.c1.w};
         const auto st = __builtin_amdgcn_permlane32_swap(c.sc, c.sc, false, false);
@@ -234,7 +241,7 @@ struct GemmQ8 {  // Q8_0: w = scale*q, q int8, 32 bytes per chunk (consecutive c
                 const uint32_t lo = A[T] ^ 0x80808080u, hi = B[T] ^ 0x80808080u;  // q + 128 as unsigned bytes
                 const uint32_t hb[4] = {__builtin_amdgcn_perm(e, lo, 0x04020400u), __builtin_amdgcn_perm(e, hi, 0x04020400u),
                                         __builtin_amdgcn_perm(e, lo, 0x04030401u), __builtin_amdgcn_perm(e, hi, 0x04030401u)};
-                const _Float16 sh = _Float16(__uint_as_float(st[T]));
+                const _Float16 sh = _Float16(__uint_as_float(st[T]) * wk[T]);
                 const half2v s2 = {sh, sh};
                 uint32_t p[4];
 #pragma unroll
@@ -265,15 +272,15 @@ struct GemmB32 {
         r.mn = MIN ? m[NG + (j >> GSH)] : 0u;
         return r;
     }
-    static __device__ __forceinline__ void bops(const Ch& c, int lane, half8 (&bf)[2][2]) {
+    static __device__ __forceinline__ void bops(const Ch& c, int lane, const float (&wk)[2], half8 (&bf)[2][2]) {
         uint32_t se[2][2], so[2][2];
         GemmCodes<FB>::spread(c.c, lane, se, so);
         const auto st = __builtin_amdgcn_permlane32_swap(c.sc, c.sc, false, false);
         const auto mt = __builtin_amdgcn_permlane32_swap(c.mn, c.mn, false, false);
 #pragma unroll
         for (int T = 0; T < 2; ++T) {
-            const float scf = __uint_as_float(st[T]);
-            const _Float16 sc = _Float16(scf), mn = _Float16(MIN ? __uint_as_float(mt[T]) : -float(OFF) * scf);
+            const float scf = __uint_as_float(st[T]) * wk[T];
+            const _Float16 sc = _Float16(scf), mn = _Float16(MIN ? __uint_as_float(mt[T]) * wk[T] : -float(OFF) * scf);
             const half2v s2 = {sc, sc}, n2 = {mn, mn};
             bf[T][0] = __builtin_bit_cast(half8, dequant8s<FB>(se[T][0], so[T][0], s2, n2));
             bf[T][1] = __builtin_bit_cast(half8, dequant8s<FB>(se[T][1], so[T][1], s2, n2));
@@ -316,7 +323,7 @@ struct GemmLin {
         const uint32_t s0 = m[SG16 ? 2 * j : (j >> GSH)];
         return {Codes::load(a, ci, lane), s0, SG16 ? m[2 * j + 1] : s0};
     }
-    static __device__ __forceinline__ void bops(const Ch& c, int lane, half8 (&bf)[2][2]) {
+    static __device__ __forceinline__ void bops(const Ch& c, int lane, const float (&wk)[2], half8 (&bf)[2][2]) {
         uint32_t se[2][2], so[2][2];
         Codes::spread(c.c, lane, se, so);
         const auto t0 = __builtin_amdgcn_permlane32_swap(c.s0, c.s0, false, false);
@@ -326,13 +333,23 @@ struct GemmLin {
         for (int T = 0; T < 2; ++T)
 #pragma unroll
             for (int kk = 0; kk < 2; ++kk) {
-                const float scf = __uint_as_float(kk ? t1[T] : t0[T]) * mul;
+                const float scf = __uint_as_float(kk ? t1[T] : t0[T]) * (mul * wk[T]);
                 const _Float16 sc = _Float16(scf), mn = _Float16(-mid * scf);
                 const half2v s2 = {sc, sc}, n2 = {mn, mn};
                 bf[T][kk] = __builtin_bit_cast(half8, dequant8s<FB>(se[T][kk], so[T][kk], s2, n2));
             }
     }
 };
+
+// Row factors (RplArgs::wrow) of row group g in the B-operand layout: wk[T]
+// belongs to row 32T + lane % 32, the lane's row in 32-row tile T. Two plain
+// loads rather than one and a lane swap: nothing waits for them before the
+// first B operands (a swap right after the load would stall the wave for a
+// memory round trip before its first code loads go out).
+__device__ __forceinline__ void row_factors(const RplArgs& a, int g, int lane, float (&wk)[2]) {
+    wk[0] = a.wrow[int64_t(g) * 64 + (lane & 31)];
+    wk[1] = a.wrow[int64_t(g) * 64 + 32 + (lane & 31)];
+}
 
 struct GemmArgs {
     RplArgs w;
@@ -437,10 +454,9 @@ void launch_x_f16r(const float* x, uint4* xh, float* xscale, int M, int kb8, hip
 // LDS carries X alone: per K-step a block writes 16 KB of fp16 X and each
 // wave reads 16 KB back for 32 MFMAs (128 tokens x 64 rows x 64 columns),
 // against 96 KB per 16 MFMAs per wave with fp16 W tiles.
-template <class GP, int TM, int D>
+template <class GP, int TM, int D, bool WF>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) k_gemm_q4k_pw(GemmArgs ga) {
     constexpr int BM = 32 * TM;
-    constexpr int BNW = 256;                 // output rows per block: 4 waves x 64
     constexpr int XB = BM * (BK / 8) / 256;  // 8-column X blocks per thread per K-step
     static_assert(XB >= 1 && 4 % D == 0, "shape");
     __shared__ __attribute__((aligned(16))) _Float16 xs[2][BM * LDK];
@@ -457,6 +473,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
     // order these writes before the epilogue reads them.
     if (t < BM) xsc[t] = ga.xscale[min(mblk * BM + t, ga.M - 1)];
     const int g = min(nblk * 4 + wave, a.rg_count - 1);  // this wave's row group
+    float wk[2] = {1.0f, 1.0f};  // row factors of the lane's rows in the two 32-row tiles
+    if constexpr (WF) row_factors(a, g, lane, wk);
 
     struct Regs {
         typename GP::Ch c[2];  // the step's two chunks of this lane's row
@@ -507,8 +525,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
             __builtin_amdgcn_sched_barrier(0);
             // B operands: [chunk][tile][k16 step] as fp16 in k order [0,2,4,6,1,3,5,7]
             half8 bf[2][2][2];
-            GP::bops(c0, lane, bf[0]);
-            GP::bops(c1, lane, bf[1]);
+            GP::bops(c0, lane, wk, bf[0]);
+            GP::bops(c1, lane, wk, bf[1]);
             __syncthreads();
 #pragma unroll
             for (int jj = 0; jj < 2; ++jj)
@@ -537,10 +555,11 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
         for (int T = 0; T < 2; ++T) {
             const int n = (nblk * 4 + wave) * 64 + T * 32 + (lane & 31);
             if (n >= a.rows) continue;
+            const float wi = WF ? 1.0f / wk[T] : 1.0f;  // the row factor back out (exact: a power of two)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int m = mblk * BM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (m < ga.M) out[int64_t(m) * a.rows + n] = acc[i][T][r] * xsc[m - mblk * BM];
+                if (m < ga.M) out[int64_t(m) * a.rows + n] = acc[i][T][r] * wi * xsc[m - mblk * BM];
             }
         }
 }
@@ -557,7 +576,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
 // ahead, in register rings. Every weight is dequantized once per token block.
 // The W waves' partial tiles meet in LDS after the loop and are added in wave
 // order (deterministic), one 32-token tile at a time.
-template <class GP, int TM, int DC, int DX, int NT>
+template <class GP, int TM, int DC, int DX, int NT, bool WF>
 __global__ void __launch_bounds__(NT) k_gemm_rg(GemmArgs ga, int per) {
     constexpr int BM = 32 * TM;
     static_assert(4 % DC == 0 && 4 % DX == 0, "the rings must divide the 4 steps of a super-block");
@@ -572,6 +591,8 @@ __global__ void __launch_bounds__(NT) k_gemm_rg(GemmArgs ga, int per) {
     const int wsb0 = sb0 + wave * per;
     const int steps = max(0, min(sb1, wsb0 + per) - wsb0) * 4;
     const int mt = (ga.M + 31) / 32;  // 32-token tiles of the fragment-ordered X
+    float wk[2] = {1.0f, 1.0f};  // row factors of the lane's rows in the two 32-row tiles
+    if constexpr (WF) row_factors(a, g, lane, wk);
 
     struct Codes {
         typename GP::Ch c[2];  // the step's two chunks of this lane's row
@@ -625,7 +646,7 @@ __global__ void __launch_bounds__(NT) k_gemm_rg(GemmArgs ga, int per) {
 #pragma unroll
                 for (int jj = 0; jj < 2; ++jj) {
                     half8 bf[2][2];  // [tile][k16 step]
-                    GP::bops(cc.c[jj], lane, bf);
+                    GP::bops(cc.c[jj], lane, wk, bf);
 #pragma unroll
                     for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
@@ -646,9 +667,11 @@ __global__ void __launch_bounds__(NT) k_gemm_rg(GemmArgs ga, int per) {
     for (int i = 0; i < TM; ++i) {
         if (i > 0) __syncthreads();  // the previous tile's sums have been read
 #pragma unroll
-        for (int T = 0; T < 2; ++T)
+        for (int T = 0; T < 2; ++T) {
+            const float wi = WF ? 1.0f / wk[T] : 1.0f;  // the row factor back out (exact: a power of two)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) red[((wave * 2 + T) * 16 + r) * 64 + lane] = acc[i][T][r];
+            for (int r = 0; r < 16; ++r) red[((wave * 2 + T) * 16 + r) * 64 + lane] = acc[i][T][r] * wi;
+        }
         __syncthreads();
         for (int v = t; v < 2048; v += 64 * W) {
             const int T = v >> 10, r = (v >> 6) & 15, l = v & 63;
@@ -709,6 +732,7 @@ __global__ void __launch_bounds__(256) k_split_sum(const float* __restrict__ par
 // IQ4_NL, whose float grid has no B-operand builder: it runs batched GEMVs.
 bool gemm_supported(const DevBlob& b, int M) {
     if (b.layout != LAYOUT_RPL || b.fmt == FMT_IQ4_NL) return false;  // IQ4_NL's float grid: batched GEMV
+    if (!b.rpl.wrow) return false;  // fused images carry no row factors
     return b.fmt == FMT_Q4_K || M > 8;
 }
 
@@ -765,93 +789,83 @@ size_t gemm_scratch_floats(const DevBlob& b, int M) {
     return gemm_x_floats(b, M) + gemm_scale_floats(M) + (p.splits > 1 ? size_t(p.splits) * size_t(M) * size_t(b.rows) : 0);
 }
 
-// The packed-W GEMM for b's format with TM 32-token tiles per wave.
-template <int TM>
-int launch_pw(const DevBlob& b, dim3 grid, hipStream_t s, const GemmArgs& ga) {
+// Calls go.template run<GP>() with the B-operand builder of b's format.
+template <class Go>
+int with_builder(const DevBlob& b, const Go& go) {
     switch (b.fmt) {
-    case FMT_Q2_K: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmKQ<2>, TM, 4>), grid, dim3(256), 0, s, ga); return 0;
-    case FMT_Q3_K: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmKQ<3>, TM, 4>), grid, dim3(256), 0, s, ga); return 0;
-    case FMT_Q5_K: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmKQ<5>, TM, 4>), grid, dim3(256), 0, s, ga); return 0;
-    case FMT_Q6_K: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmQ6, TM, 4>), grid, dim3(256), 0, s, ga); return 0;
-    case FMT_Q8_0: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmQ8, TM, 4>), grid, dim3(256), 0, s, ga); return 0;
-    case FMT_Q4_0: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmB32<4, false, 8, 0x88888888u>, TM, 4>), grid, dim3(256), 0, s, ga); return 0;
-    case FMT_Q4_1: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmB32<4, true, 0, 0u>, TM, 4>), grid, dim3(256), 0, s, ga); return 0;
-    case FMT_Q5_0: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmB32<5, false, 16, 0u>, TM, 4>), grid, dim3(256), 0, s, ga); return 0;
-    case FMT_Q5_1: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmB32<5, true, 0, 0u>, TM, 4>), grid, dim3(256), 0, s, ga); return 0;
+    case FMT_Q2_K: go.template run<GemmKQ<2>>(); return 0;
+    case FMT_Q3_K: go.template run<GemmKQ<3>>(); return 0;
+    case FMT_Q4_K: go.template run<GemmKQ<4>>(); return 0;
+    case FMT_Q5_K: go.template run<GemmKQ<5>>(); return 0;
+    case FMT_Q6_K: go.template run<GemmQ6>(); return 0;
+    case FMT_Q8_0: go.template run<GemmQ8>(); return 0;
+    case FMT_Q4_0: go.template run<GemmB32<4, false, 8, 0x88888888u>>(); return 0;
+    case FMT_Q4_1: go.template run<GemmB32<4, true, 0, 0u>>(); return 0;
+    case FMT_Q5_0: go.template run<GemmB32<5, false, 16, 0u>>(); return 0;
+    case FMT_Q5_1: go.template run<GemmB32<5, true, 0, 0u>>(); return 0;
     case FMT_AFFINE:
         switch (b.block_weights) {
-        case 32: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmB32<4, true, 0, 0u, 0>, TM, 4>), grid, dim3(256), 0, s, ga); return 0;
-        case 64: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmB32<4, true, 0, 0u, 1>, TM, 4>), grid, dim3(256), 0, s, ga); return 0;
-        case 128: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmB32<4, true, 0, 0u, 2>, TM, 4>), grid, dim3(256), 0, s, ga); return 0;
-        case 256: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmB32<4, true, 0, 0u, 3>, TM, 4>), grid, dim3(256), 0, s, ga); return 0;
+        case 32: go.template run<GemmB32<4, true, 0, 0u, 0>>(); return 0;
+        case 64: go.template run<GemmB32<4, true, 0, 0u, 1>>(); return 0;
+        case 128: go.template run<GemmB32<4, true, 0, 0u, 2>>(); return 0;
+        case 256: go.template run<GemmB32<4, true, 0, 0u, 3>>(); return 0;
         default: return int(hipErrorInvalidValue);
         }
     case FMT_BINARY:
         if (b.block_weights == 128) {
-            hipLaunchKernelGGL((k_gemm_q4k_pw<GemmLin<1, false, 1, 2>, TM, 4>), grid, dim3(256), 0, s, ga);
+            go.template run<GemmLin<1, false, 1, 2>>();
             return 0;
         }
         [[fallthrough]];
-    case FMT_IQ1_S: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmLin<1, false, 1>, TM, 4>), grid, dim3(256), 0, s, ga); return 0;
-    case FMT_IQ2_XXS: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmLin<2, false, 3>, TM, 4>), grid, dim3(256), 0, s, ga); return 0;
-    case FMT_IQ2_XS: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmLin<2, true, 3>, TM, 4>), grid, dim3(256), 0, s, ga); return 0;
-    case FMT_IQ3_XXS: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmLin<3, false, 7>, TM, 4>), grid, dim3(256), 0, s, ga); return 0;
-    case FMT_IQ3_S: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmLin<3, true, 7>, TM, 4>), grid, dim3(256), 0, s, ga); return 0;
-    case FMT_IQ4_XS: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmLin<4, true, 15>, TM, 4>), grid, dim3(256), 0, s, ga); return 0;
-    case FMT_TERNARY: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmLin<2, true, 2>, TM, 4>), grid, dim3(256), 0, s, ga); return 0;
-    case FMT_Q4_K: hipLaunchKernelGGL((k_gemm_q4k_pw<GemmKQ<4>, TM, 4>), grid, dim3(256), 0, s, ga); return 0;
+    case FMT_IQ1_S: go.template run<GemmLin<1, false, 1>>(); return 0;
+    case FMT_IQ2_XXS: go.template run<GemmLin<2, false, 3>>(); return 0;
+    case FMT_IQ2_XS: go.template run<GemmLin<2, true, 3>>(); return 0;
+    case FMT_IQ3_XXS: go.template run<GemmLin<3, false, 7>>(); return 0;
+    case FMT_IQ3_S: go.template run<GemmLin<3, true, 7>>(); return 0;
+    case FMT_IQ4_XS: go.template run<GemmLin<4, true, 15>>(); return 0;
+    case FMT_TERNARY: go.template run<GemmLin<2, true, 2>>(); return 0;
     default: return int(hipErrorInvalidValue);
     }
 }
 
-// Ring depths and block size per token tiles: one or two tiles run 8 waves
-// (2 per SIMD, 256 registers each), four tiles 4 waves (1 per SIMD, whose 512
-// registers hold the 128 accumulators and deeper rings).
-template <class GP, int TM>
-void rg_go(dim3 grid, int W, int per, hipStream_t s, const GemmArgs& ga) {
-    constexpr int DC = TM == 2 ? 2 : 4, DX = TM == 1 ? 2 : TM == 2 ? 1 : 2, NT = TM == 4 ? 256 : 512;
-    const size_t lds = size_t(W) * 2 * 16 * 64 * sizeof(float);
-    hipLaunchKernelGGL((k_gemm_rg<GP, TM, DC, DX, NT>), grid, dim3(unsigned(64 * W)), lds, s, ga, per);
-}
-
-// k_gemm_rg for b's format; TM token tiles per block, `per` super-blocks per
-// wave, W waves (at most rg_waves(TM)).
-template <int TM>
-int launch_rg(const DevBlob& b, dim3 grid, int W, int per, hipStream_t s, const GemmArgs& ga) {
-    switch (b.fmt) {
-    case FMT_Q2_K: rg_go<GemmKQ<2>, TM>(grid, W, per, s, ga); return 0;
-    case FMT_Q3_K: rg_go<GemmKQ<3>, TM>(grid, W, per, s, ga); return 0;
-    case FMT_Q5_K: rg_go<GemmKQ<5>, TM>(grid, W, per, s, ga); return 0;
-    case FMT_Q6_K: rg_go<GemmQ6, TM>(grid, W, per, s, ga); return 0;
-    case FMT_Q8_0: rg_go<GemmQ8, TM>(grid, W, per, s, ga); return 0;
-    case FMT_Q4_0: rg_go<GemmB32<4, false, 8, 0x88888888u>, TM>(grid, W, per, s, ga); return 0;
-    case FMT_Q4_1: rg_go<GemmB32<4, true, 0, 0u>, TM>(grid, W, per, s, ga); return 0;
-    case FMT_Q5_0: rg_go<GemmB32<5, false, 16, 0u>, TM>(grid, W, per, s, ga); return 0;
-    case FMT_Q5_1: rg_go<GemmB32<5, true, 0, 0u>, TM>(grid, W, per, s, ga); return 0;
-    case FMT_AFFINE:
-        switch (b.block_weights) {
-        case 32: rg_go<GemmB32<4, true, 0, 0u, 0>, TM>(grid, W, per, s, ga); return 0;
-        case 64: rg_go<GemmB32<4, true, 0, 0u, 1>, TM>(grid, W, per, s, ga); return 0;
-        case 128: rg_go<GemmB32<4, true, 0, 0u, 2>, TM>(grid, W, per, s, ga); return 0;
-        case 256: rg_go<GemmB32<4, true, 0, 0u, 3>, TM>(grid, W, per, s, ga); return 0;
-        default: return int(hipErrorInvalidValue);
-        }
-    case FMT_BINARY:
-        if (b.block_weights == 128) {
-            rg_go<GemmLin<1, false, 1, 2>, TM>(grid, W, per, s, ga);
-            return 0;
-        }
-        [[fallthrough]];
-    case FMT_IQ1_S: rg_go<GemmLin<1, false, 1>, TM>(grid, W, per, s, ga); return 0;
-    case FMT_IQ2_XXS: rg_go<GemmLin<2, false, 3>, TM>(grid, W, per, s, ga); return 0;
-    case FMT_IQ2_XS: rg_go<GemmLin<2, true, 3>, TM>(grid, W, per, s, ga); return 0;
-    case FMT_IQ3_XXS: rg_go<GemmLin<3, false, 7>, TM>(grid, W, per, s, ga); return 0;
-    case FMT_IQ3_S: rg_go<GemmLin<3, true, 7>, TM>(grid, W, per, s, ga); return 0;
-    case FMT_IQ4_XS: rg_go<GemmLin<4, true, 15>, TM>(grid, W, per, s, ga); return 0;
-    case FMT_TERNARY: rg_go<GemmLin<2, true, 2>, TM>(grid, W, per, s, ga); return 0;
-    case FMT_Q4_K: rg_go<GemmKQ<4>, TM>(grid, W, per, s, ga); return 0;
-    default: return int(hipErrorInvalidValue);
+// k_gemm_q4k_pw with TM 32-token tiles per wave; WF: apply the row factors.
+template <int TM, bool WF>
+struct PwGo {
+    dim3 grid;
+    hipStream_t s;
+    const GemmArgs& ga;
+    template <class GP>
+    void run() const {
+        hipLaunchKernelGGL((k_gemm_q4k_pw<GP, TM, 4, WF>), grid, dim3(256), 0, s, ga);
     }
+};
+
+// k_gemm_rg with TM token tiles per block, `per` super-blocks per wave, W
+// waves (at most rg_waves(TM)). Ring depths and block size per token tiles:
+// one or two tiles run 8 waves (2 per SIMD, 256 registers each), four tiles 4
+// waves (1 per SIMD, whose 512 registers hold the 128 accumulators and deeper
+// rings).
+template <int TM, bool WF>
+struct RgGo {
+    dim3 grid;
+    int W, per;
+    hipStream_t s;
+    const GemmArgs& ga;
+    template <class GP>
+    void run() const {
+        constexpr int DC = TM == 2 ? 2 : 4, DX = TM == 1 ? 2 : TM == 2 ? 1 : 2, NT = TM == 4 ? 256 : 512;
+        const size_t lds = size_t(W) * 2 * 16 * 64 * sizeof(float);
+        hipLaunchKernelGGL((k_gemm_rg<GP, TM, DC, DX, NT, WF>), grid, dim3(unsigned(64 * W)), lds, s, ga, per);
+    }
+};
+
+template <bool WF>
+int launch_tiles(const DevBlob& b, const GemmPlan& p, dim3 grid, hipStream_t s, const GemmArgs& ga) {
+    if (p.kind == GEMM_RG)
+        return p.bm == 32   ? with_builder(b, RgGo<1, WF>{grid, p.W, p.per, s, ga})
+               : p.bm == 64 ? with_builder(b, RgGo<2, WF>{grid, p.W, p.per, s, ga})
+                            : with_builder(b, RgGo<4, WF>{grid, p.W, p.per, s, ga});
+    return with_builder(b, PwGo<4, WF>{grid, s, ga});
 }
 
 int launch_gemm(const DevBlob& b, const float* d_x, float* d_y, int M, void* stream, float* d_scratch) {
@@ -874,17 +888,10 @@ int launch_gemm(const DevBlob& b, const float* d_x, float* d_y, int M, void* str
     ga.M = M;
     ga.K = int(b.cols);
     ga.sb_per_split = p.sb_per_split;
-    if (p.kind == GEMM_RG) {
-        const dim3 grid(unsigned(b.rpl.rg_count), unsigned((M + bm - 1) / bm), unsigned(splits));
-        const int e = bm == 32   ? launch_rg<1>(b, grid, p.W, p.per, s, ga)
-                      : bm == 64 ? launch_rg<2>(b, grid, p.W, p.per, s, ga)
-                                 : launch_rg<4>(b, grid, p.W, p.per, s, ga);
-        if (e) return e;
-    } else {
-        const dim3 grid(unsigned((b.rows + 255) / 256), unsigned((M + bm - 1) / bm), unsigned(splits));
-        const int e = launch_pw<4>(b, grid, s, ga);
-        if (e) return e;
-    }
+    const dim3 grid(unsigned(p.kind == GEMM_RG ? b.rpl.rg_count : (b.rows + 255) / 256), unsigned((M + bm - 1) / bm),
+                    unsigned(splits));
+    const int e = b.gemm_row_factors ? launch_tiles<true>(b, p, grid, s, ga) : launch_tiles<false>(b, p, grid, s, ga);
+    if (e) return e;
     if (splits > 1) {
         const int64_t n = int64_t(M) * b.rows;
         hipLaunchKernelGGL(k_split_sum, dim3(unsigned((n / 4 + 1 + 255) / 256)), dim3(256), 0, s, part, d_y, n, splits);

@@ -4,6 +4,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -281,10 +282,32 @@ struct Image {
 //   Q4_1 / Q5_0 / Q5_1: codes as Q4_0 (Q5_x: low 4 bits, plus the fifth
 //         bits as Q5_K's); meta 8 f32 scales, then (Q4_1, Q5_1) 8 f32 mins.
 // Code (and high-bit) planes are in the chunk order rpl_strides gives (j =
-// chunk index inside the super-block); meta/dd are [rg][sb][lane].
+// chunk index inside the super-block); meta/dd are [rg][sb][lane]. A last
+// section holds one f32 per row (rg*64, 4 bytes per row beside the blob's
+// bytes): the prefill GEMM's power-of-two row factor (gemm_row_factor).
 struct RplOffsets {
-    size_t codes = 0, hi = 0, meta = 0, dd = 0;
+    size_t codes = 0, hi = 0, meta = 0, dd = 0, wrow = 0;
 };
+
+// Row factor of the prefill GEMM (gemm_rpl.hip): 2^e with bound * 2^e in
+// [2^12, 2^13), where `bound` is an upper bound on every fp16 value the
+// GEMM's B-operand builder forms for the row (|scale| * qmax + |min|, or
+// |scale| * (qmax + offset), over the row's sub-blocks). The GEMM multiplies
+// the row's scales and mins by it before their fp16 cast and the row's
+// outputs by its inverse, both exact: rows of tiny weights keep fp16's
+// precision instead of going subnormal, and rows past 65504 stay finite.
+// 1 for an all-zero or non-finite row.
+float gemm_row_factor(double bound) {
+    if (!(bound > 0.0) || !std::isfinite(bound)) return 1.0f;
+    return std::ldexp(1.0f, std::min(126, std::max(-126, 12 - std::ilogb(bound))));
+}
+// The row-factor section: one float per row of the padded row groups, 1 for padding.
+float* add_row_factors(Image& img, RplOffsets& o, int64_t rg) {
+    o.wrow = img.add(size_t(rg * 64 * 4));
+    float* w = reinterpret_cast<float*>(img.bytes.data() + o.wrow);
+    std::fill(w, w + rg * 64, 1.0f);
+    return w;
+}
 void build_rpl(int fmt, const uint8_t* raw, int64_t rows, int64_t cols, Image& img, RplOffsets& o) {
     const int64_t rg = (rows + 63) / 64, nch = cols / 32, nsb = cols / 256;
     int64_t cs_si = 0, cs_j = 0;
@@ -299,6 +322,7 @@ void build_rpl(int fmt, const uint8_t* raw, int64_t rows, int64_t cols, Image& i
     if (five || fmt == FMT_Q3_K) o.hi = img.add(size_t(rg * nch * 64 * 4));
     o.meta = img.add(size_t(rg * nsb * 64 * mb));
     if (kq) o.dd = img.add(size_t(rg * nsb * 64 * 8));
+    float* wrow = add_row_factors(img, o, rg);
     uint8_t* base = img.bytes.data();
     uint8_t* codes = base + o.codes;
     uint8_t* hi = base + o.hi;
@@ -306,12 +330,18 @@ void build_rpl(int fmt, const uint8_t* raw, int64_t rows, int64_t cols, Image& i
     float* dd = reinterpret_cast<float*>(base + o.dd);
     KSpec ks;
     k_spec(fmt, ks);
+    // GEMM value bounds per unit |scale| (gemm_row_factor): codes up to qmax
+    // with a min (k-quants, Q4_1, Q5_1), codes minus an offset (Q6_K's 32,
+    // Q4_0's 8, Q5_0's 16), Q8_0's signed bytes.
+    const double qmax = fmt == FMT_Q6_K ? 63.0 + 32.0 : fmt == FMT_Q8_0 ? 128.0
+                        : kq ? double((1 << ks.bits) - 1) : five ? (bmin ? 31.0 : 31.0 + 16.0) : (bmin ? 15.0 : 15.0 + 8.0);
     const int64_t sbb = kq ? k_super_bytes(ks) : 0;
     auto work = [&](int64_t g0, int64_t g1) {
         for (int64_t g = g0; g < g1; ++g)
             for (int lane = 0; lane < 64; ++lane) {
                 const int64_t row = g * 64 + lane;
                 if (row >= rows) continue;
+                double bound = 0.0;
                 for (int64_t sb = 0; sb < nsb; ++sb) {
                     const int64_t mi = (g * nsb + sb) * 64 + lane;
                     uint8_t* m = meta + mi * mb;
@@ -319,9 +349,13 @@ void build_rpl(int fmt, const uint8_t* raw, int64_t rows, int64_t cols, Image& i
                         const uint8_t* o8 = raw + (row * nsb + sb) * sbb;
                         dd[2 * mi] = f32_at(o8);
                         dd[2 * mi + 1] = f32_at(o8 + 4);
+                        const double d255 = std::fabs(double(f32_at(o8))) / 255.0, dm127 = std::fabs(double(f32_at(o8 + 4))) / 127.0;
                         for (int p = 0; p < 8; ++p) {
                             const int64_t ci = ((g * nsb + sb) * cs_si + p * cs_j) * 64 + lane;
                             const uint8_t u0 = std::max<uint8_t>(o8[8 + 2 * p], 1), u1 = std::max<uint8_t>(o8[9 + 2 * p], 1);
+                            for (int h = 0; h < 2; ++h)
+                                bound = std::max(bound, d255 * (h ? u1 : u0) * qmax +
+                                                            (fmt == FMT_Q6_K ? 0.0 : dm127 * std::abs(int(int8_t(o8[24 + 2 * p + h])))));
                             if (fmt == FMT_Q4_K) {
                                 m[4 * p] = u0;
                                 m[4 * p + 1] = u1;
@@ -388,6 +422,8 @@ void build_rpl(int fmt, const uint8_t* raw, int64_t rows, int64_t cols, Image& i
                             const int64_t ci = ((g * nsb + sb) * cs_si + p * cs_j) * 64 + lane;
                             std::memcpy(m + 4 * p, blk, 4);
                             if (bmin) std::memcpy(m + 32 + 4 * p, blk + 4, 4);
+                            bound = std::max(bound, std::fabs(double(f32_at(blk))) * qmax +
+                                                        (bmin ? std::fabs(double(f32_at(blk + 4))) : 0.0));
                             if (!five) {
                                 std::memcpy(codes + ci * cb, blk + hdr, size_t(cb));
                                 continue;
@@ -407,6 +443,7 @@ void build_rpl(int fmt, const uint8_t* raw, int64_t rows, int64_t cols, Image& i
                         }
                     }
                 }
+                wrow[row] = gemm_row_factor(bound);
             }
     };
     const int64_t nthreads = std::min<int64_t>(std::max(1u, std::thread::hardware_concurrency()), std::max<int64_t>(1, rg / 4));
@@ -439,6 +476,10 @@ void build_rpl_lin(int fmt, const LinCodes& lc, const uint8_t* raw, size_t raw_l
     o.codes = img.add(size_t(rg * nch * 64 * cb));
     if (bits == 3) o.hi = img.add(size_t(rg * nch * 64 * 4));
     o.meta = img.add(size_t(rg * nsb * 64 * mb));
+    float* wrow = add_row_factors(img, o, rg);
+    // GEMM value bound per unit |scale| (gemm_row_factor): w = scale*(q - mid)
+    // with mid <= qmax (one-bit codes: 2*scale*(q - 1/2)).
+    const double qmax = double((1 << bits) - 1) * (bits == 1 ? 4.0 : 2.0);
     uint8_t* base = img.bytes.data();
     uint8_t* codes = base + o.codes;
     uint8_t* hi = base + o.hi;
@@ -448,9 +489,13 @@ void build_rpl_lin(int fmt, const LinCodes& lc, const uint8_t* raw, size_t raw_l
             for (int lane = 0; lane < 64; ++lane) {
                 const int64_t row = g * 64 + lane;
                 if (row >= rows) continue;
+                double bound = 0.0;
                 for (int64_t sb = 0; sb < nsb; ++sb) {
                     float* m = reinterpret_cast<float*>(meta + ((g * nsb + sb) * 64 + lane) * mb);
-                    for (int w = 0; w < nw; ++w) m[w] = scale_at((row * cols + sb * 256) / sg + w);
+                    for (int w = 0; w < nw; ++w) {
+                        m[w] = scale_at((row * cols + sb * 256) / sg + w);
+                        bound = std::max(bound, std::fabs(double(m[w])) * qmax);
+                    }
                     for (int p = 0; p < 8; ++p) {
                         const int64_t i0 = row * cols + sb * 256 + p * 32;
                         uint8_t qv[32];
@@ -482,6 +527,7 @@ void build_rpl_lin(int fmt, const LinCodes& lc, const uint8_t* raw, size_t raw_l
                         }
                     }
                 }
+                wrow[row] = gemm_row_factor(bound);
             }
     };
     const int64_t nthreads = std::min<int64_t>(std::max(1u, std::thread::hardware_concurrency()), std::max<int64_t>(1, rg / 4));
@@ -505,6 +551,7 @@ void build_rpl_affine(const uint8_t* raw, const float* scales, const float* mins
     rpl_strides(FMT_AFFINE, rg, nsb, cs_si, cs_j);
     o.codes = img.add(size_t(rg * nch * 64 * 16));
     o.meta = img.add(size_t(rg * nsb * 64 * 8 * ng));
+    float* wrow = add_row_factors(img, o, rg);
     uint8_t* base = img.bytes.data();
     uint8_t* codes = base + o.codes;
     uint8_t* meta = base + o.meta;
@@ -512,15 +559,18 @@ void build_rpl_affine(const uint8_t* raw, const float* scales, const float* mins
         for (int lane = 0; lane < 64; ++lane) {
             const int64_t row = g * 64 + lane;
             if (row >= rows) continue;
+            double bound = 0.0;
             for (int64_t sb = 0; sb < nsb; ++sb) {
                 float* m = reinterpret_cast<float*>(meta + ((g * nsb + sb) * 64 + lane) * 8 * ng);
                 for (int q = 0; q < ng; ++q) {
                     m[q] = scales[row * gpr + sb * ng + q];
                     m[ng + q] = mins[row * gpr + sb * ng + q];
+                    bound = std::max(bound, std::fabs(double(m[q])) * 15.0 + std::fabs(double(m[ng + q])));
                 }
                 for (int p = 0; p < 8; ++p)
                     std::memcpy(codes + (((g * nsb + sb) * cs_si + p * cs_j) * 64 + lane) * 16, raw + (row * cols + sb * 256 + p * 32) / 2, 16);
             }
+            wrow[row] = gemm_row_factor(bound);
         }
 }
 
@@ -777,6 +827,9 @@ int wv_blob_upload(int format, int64_t rows, int64_t cols, int32_t block_weights
         r.hi = ro.hi ? base + ro.hi : nullptr;
         r.meta = base + ro.meta;
         r.dd = ro.dd ? reinterpret_cast<const float2_t*>(base + ro.dd) : nullptr;
+        r.wrow = reinterpret_cast<const float*>(base + ro.wrow);
+        const float* wf = reinterpret_cast<const float*>(img.bytes.data() + ro.wrow);
+        b.gemm_row_factors = std::any_of(wf, wf + rows, [](float f) { return f < 0.25f || f > 1048576.0f; });
         r.partial = nullptr;
         r.rows = int(rows);
         r.nsb = int(cols / 256);

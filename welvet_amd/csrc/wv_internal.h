@@ -149,6 +149,7 @@ enum Layout : int {
 //   meta  [rg][sb][lane][MB]      MB = 32 B (Q4_K scale/min bytes, Q8_0/Q4_0
 //                                  f32 block scales) or 16 B (Q6_K scales)
 //   dd    [rg][sb][lane] (d, dmin) f32 pair (k-quants)
+//   wrow  [rg*64] f32 power-of-two row factors of the prefill GEMM
 // Chunk j of super-block slot si = row group * nsb + super-block sits at chunk
 // index si * cs_si + j * cs_j (times 64 lanes). Q4_K keeps a super-block's 8
 // chunks of one row group adjacent (cs_si = 8, cs_j = 1: the owning wave
@@ -166,6 +167,9 @@ struct RplArgs {
     const uint8_t* hi;
     const uint8_t* meta;
     const float2_t* dd;
+    // [rg*64] power-of-two row factors of the prefill GEMM (gemm_row_factor);
+    // null on the fused images, which only the GEMV kernels read.
+    const float* wrow;
     // K-split partial sums [batch chunk][ksplit][rg*64], in scratch the caller
     // of the launch provides (never stored with the blob: two launches on one
     // blob may run at once).
@@ -243,6 +247,11 @@ struct DevBlob {
     const uint8_t* codes = nullptr;
     // LAYOUT_RPL
     RplArgs rpl{};
+    // Some row factor of rpl.wrow lies outside [2^-2, 2^20] (a row whose
+    // largest B-operand value is below 2^-8 or above 2^14): the prefill GEMM
+    // runs its kernels that apply the factors. Otherwise every row is held
+    // well by fp16 as it stands and the kernels without them run.
+    bool gemm_row_factors = false;
     void* base = nullptr;   // allocation owner
     size_t device_bytes = 0;  // bytes of the allocation
 };
