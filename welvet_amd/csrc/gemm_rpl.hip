@@ -510,6 +510,12 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
         load(min(d, steps - 1), ring[d]);
         __builtin_amdgcn_sched_barrier(0);
     }
+    // B operands: [chunk][tile][k16 step] as fp16 in k order [0,2,4,6,1,3,5,7].
+    // Step s + 1's are built (VALU) after the barrier, beside step s's MFMAs,
+    // so the matrix cores run while the next weights are dequantized.
+    half8 bf[2][2][2];
+    GP::bops(ring[0].c[0], lane, wk, bf[0]);
+    GP::bops(ring[0].c[1], lane, wk, bf[1]);
     for (int s0 = 0; s0 < steps; s0 += D) {
 #pragma unroll
         for (int d = 0; d < D; ++d) {
@@ -519,15 +525,13 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
                 const int f = t + 256 * i;
                 *reinterpret_cast<uint4*>(&xs[buf][(f / 8) * LDK + 8 * (f % 8)]) = ring[d].xv[i];
             }
-            const typename GP::Ch c0 = ring[d].c[0], c1 = ring[d].c[1];
             __builtin_amdgcn_sched_barrier(0);
             load(min(s + D, steps - 1), ring[d]);
             __builtin_amdgcn_sched_barrier(0);
-            // B operands: [chunk][tile][k16 step] as fp16 in k order [0,2,4,6,1,3,5,7]
-            half8 bf[2][2][2];
-            GP::bops(c0, lane, wk, bf[0]);
-            GP::bops(c1, lane, wk, bf[1]);
             __syncthreads();
+            half8 bn[2][2][2];  // step s + 1 (its codes sit in the next ring slot)
+            GP::bops(ring[(d + 1) % D].c[0], lane, wk, bn[0]);
+            GP::bops(ring[(d + 1) % D].c[1], lane, wk, bn[1]);
 #pragma unroll
             for (int jj = 0; jj < 2; ++jj)
 #pragma unroll
@@ -544,6 +548,12 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
                         for (int T = 0; T < 2; ++T)
                             acc[i][T] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[jj][T][kk], acc[i][T], 0, 0, 0);
                 }
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+                for (int T = 0; T < 2; ++T)
+#pragma unroll
+                    for (int kk = 0; kk < 2; ++kk) bf[jj][T][kk] = bn[jj][T][kk];
         }
     }
 
