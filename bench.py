@@ -377,13 +377,7 @@ def main():
         print(f"[bench] cpu baseline ({threads} threads, ~{args.cpu_budget_s:.0f} s)", file=sys.stderr, flush=True)
         result["cpu_baseline"] = cpu_baseline(packed, x, rows, cols, ternary, nbytes, args.cpu_budget_s, threads,
                                               y_gpu=y_gate)
-    if args.copy_probe:
-        src = torch.empty(args.copy_probe << 20, dtype=torch.uint8, device="cuda")
-        dst = torch.empty_like(src)
-        for _ in range(4):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        result["copy_probe_bytes"] = args.copy_probe << 20
+    copy_probe(args, torch, result)
     for b in blobs:
         b.free()
     del blobs
@@ -480,9 +474,23 @@ def prefill_main(args, torch, wv):
             "parity": parity_vs(y_gate[:n], np.stack(ys), exact=False),
             "sample": f"{n} of the M row GEMVs the reference runs for this block (restated fused SIMD path, "
                       f"{threads} row-shard threads), {dt * 1e3:.3f} ms per row; parity over those rows"}
+    copy_probe(args, torch, result)
     for b in blobs:
         b.free()
     print(json.dumps(result), flush=True)
+
+
+def copy_probe(args, torch, result):
+    """--copy-probe MIB: plain device-to-device copies of a known size, whose
+    FETCH_SIZE / WRITE_SIZE readings scale the kernel's counters to bytes."""
+    if not args.copy_probe:
+        return
+    src = torch.empty(args.copy_probe << 20, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(4):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    result["copy_probe_bytes"] = args.copy_probe << 20
 
 
 def matvect_main(args, torch, wv):
