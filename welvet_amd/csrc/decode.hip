@@ -813,24 +813,24 @@ int dalloc(Decoder& d, void** p, size_t bytes, const char* what) {
 }
 
 void drop_fused(Layer& ly) {
-    if (ly.has_qkv) hipFree(ly.qkv.base);
-    if (ly.has_gu) hipFree(ly.gu.base);
+    if (ly.has_qkv) (void)hipFree(ly.qkv.base);
+    if (ly.has_gu) (void)hipFree(ly.gu.base);
     ly.has_qkv = ly.has_gu = false;
 }
 
 void drop_graph(Decoder& d) {
-    if (d.exec) hipGraphExecDestroy(d.exec);
-    if (d.graph) hipGraphDestroy(d.graph);
+    if (d.exec) (void)hipGraphExecDestroy(d.exec);
+    if (d.graph) (void)hipGraphDestroy(d.graph);
     d.exec = nullptr;
     d.graph = nullptr;
 }
 
 void release(Decoder* d) {
     drop_graph(*d);
-    if (d->gemv_scratch) hipFree(d->gemv_scratch);
+    if (d->gemv_scratch) (void)hipFree(d->gemv_scratch);
     for (Layer& ly : d->layers) drop_fused(ly);
-    for (void* p : d->allocs) hipFree(p);
-    if (d->stream) hipStreamDestroy(d->stream);
+    for (void* p : d->allocs) (void)hipFree(p);
+    if (d->stream) (void)hipStreamDestroy(d->stream);
     delete d;
 }
 
@@ -1001,7 +1001,7 @@ int ready(Decoder& d) {
     }
     if (need > d.gemv_scratch_floats) {
         drop_graph(d);
-        if (d.gemv_scratch) hipFree(d.gemv_scratch);
+        if (d.gemv_scratch) (void)hipFree(d.gemv_scratch);
         d.gemv_scratch = nullptr;
         d.gemv_scratch_floats = 0;
         const hipError_t e = hipMalloc(&d.gemv_scratch, need * sizeof(float));
@@ -1030,13 +1030,13 @@ int run_steps(Decoder& d, int n_steps, int advance) {
         hipGraph_t g = nullptr;
         e = hipStreamEndCapture(d.stream, &g);
         if (k) {
-            if (g) hipGraphDestroy(g);
+            if (g) (void)hipGraphDestroy(g);
             return rt_hip_fail(hipError_t(k), "decoder: captured launch");
         }
         if (e != hipSuccess) return rt_hip_fail(e, "decoder: end capture");
         e = hipGraphInstantiate(&d.exec, g, nullptr, nullptr, 0);
         if (e != hipSuccess) {
-            hipGraphDestroy(g);
+            (void)hipGraphDestroy(g);
             return rt_hip_fail(e, "decoder: instantiate");
         }
         d.graph = g;
@@ -1172,7 +1172,7 @@ int wv_decoder_set_layer(uint64_t dec, int32_t layer, const uint64_t* blobs, con
                            (long long)b.cols, (long long)want[i][0], (long long)want[i][1]);
         nw[i] = b;
     }
-    hipSetDevice(d->device);
+    (void)hipSetDevice(d->device);
     // A captured step reads this layer's old weights and fused copies: drop
     // it, and keep the layer unusable until every part below succeeded.
     drop_graph(*d);
@@ -1211,7 +1211,7 @@ int wv_decoder_set_output(uint64_t dec, uint64_t lm_head, const float* final_nor
     if (b.rows != c.vocab || b.cols != c.hidden)
         return rt_fail(WV_E_SHAPE, "wv_decoder_set_output: LM head is %lldx%lld, want %dx%d", (long long)b.rows,
                        (long long)b.cols, c.vocab, c.hidden);
-    hipSetDevice(d->device);
+    (void)hipSetDevice(d->device);
     // A captured step holds the old head, norm and table: capture again, and
     // keep the output unusable until the copies below succeeded.
     drop_graph(*d);
@@ -1238,7 +1238,7 @@ int wv_decoder_set_kv(uint64_t dec, int32_t layer, int32_t first_pos, int32_t n_
     if (first_pos < 0 || n_pos < 0 || int64_t(first_pos) + n_pos > c.max_seq)
         return rt_fail(WV_E_SHAPE, "wv_decoder_set_kv: rows %d..%d outside max_seq %d", first_pos, first_pos + n_pos, c.max_seq);
     const size_t hd = size_t(c.head_dim), kv_dim = size_t(c.n_kv_heads) * hd;
-    hipSetDevice(d->device);
+    (void)hipSetDevice(d->device);
     hipError_t e = hipSuccess;
     // host rows [pos][kv head][hd] -> device head-major [kv head][max_seq][hd]
     for (int kh = 0; kh < c.n_kv_heads && e == hipSuccess && n_pos > 0; ++kh) {
@@ -1270,7 +1270,7 @@ int wv_decoder_generate(uint64_t dec, int32_t token, int32_t pos, int32_t n_step
         return rt_fail(WV_E_SHAPE, "wv_decoder_generate: positions %d.. exceed max_seq %d", pos, c.max_seq);
     int rc = ready(*d);
     if (rc) return rc;
-    hipSetDevice(d->device);
+    (void)hipSetDevice(d->device);
     const int32_t init[4] = {pos, token, -1, 0};
     hipError_t e = hipMemcpyAsync(d->d_state, init, sizeof init, hipMemcpyHostToDevice, d->stream);
     if (e != hipSuccess) return rt_hip_fail(e, "wv_decoder_generate: state");
@@ -1298,8 +1298,8 @@ int wv_decoder_free(uint64_t dec) {
         d = it->second;
         g_decs.erase(it);
     }
-    hipSetDevice(d->device);
-    hipStreamSynchronize(d->stream);
+    (void)hipSetDevice(d->device);
+    (void)hipStreamSynchronize(d->stream);
     release(d);
     return WV_OK;
 }

@@ -94,7 +94,7 @@ int ensure_device_locked(int dev) {
 int ensure_init() {
     std::lock_guard<std::mutex> lk(g_mu);
     if (g_current >= 0) {
-        hipSetDevice(g_current);
+        (void)hipSetDevice(g_current);
         return WV_OK;
     }
     return ensure_device_locked(0);
@@ -580,7 +580,7 @@ int upload_image(const Image& img, DevBlob& b) {
     if (e != hipSuccess) return hip_fail(e, "wv_blob_upload: hipMalloc");
     e = hipMemcpy(d, img.bytes.data(), img.bytes.size(), hipMemcpyHostToDevice);
     if (e != hipSuccess) {
-        hipFree(d);
+        (void)hipFree(d);
         return hip_fail(e, "wv_blob_upload: hipMemcpy");
     }
     b.base = d;
@@ -881,7 +881,7 @@ int wv_blob_free(uint64_t handle) {
         b = it->second;
         g_blobs.erase(it);
     }
-    hipSetDevice(b.device);
+    (void)hipSetDevice(b.device);
     hipError_t e = hipFree(b.base);
     if (e != hipSuccess) return hip_fail(e, "wv_blob_free: hipFree");
     return WV_OK;
@@ -904,7 +904,7 @@ int wv_matvec_dev(uint64_t handle, const float* d_x, float* d_y, int32_t batch, 
     if (!d_x || !d_y) return fail(WV_E_ARG, "MatVec: nil x/y");
     if (batch < 0) return fail(WV_E_SHAPE, "MatVec: negative batch %d", batch);
     if (batch == 0) return WV_OK;
-    hipSetDevice(b.device);
+    (void)hipSetDevice(b.device);
     hipStream_t s = stream_or_default(stream, b.device);
     CallScratch sc;
     int rc = sc.get(matvec_scratch_floats(b, batch), s, "MatVec: scratch");
@@ -932,7 +932,7 @@ int wv_matvec_dev_noalloc(uint64_t handle, const float* d_x, float* d_y, int32_t
     if (need > kNoAllocScratchFloats)
         return fail(WV_E_SHAPE, "MatVec (no-alloc): rows=%lld cols=%lld needs %zu floats of scratch, the fixed array holds %zu",
                     (long long)b.rows, (long long)b.cols, need, kNoAllocScratchFloats);
-    hipSetDevice(b.device);
+    (void)hipSetDevice(b.device);
     const int e = launch_matvec(b, d_x, d_y, batch, stream_or_default(stream, b.device), need ? sp : nullptr);
     if (e != hipSuccess) return hip_fail(hipError_t(e), "MatVec (no-alloc): kernel launch");
     return WV_OK;
@@ -945,7 +945,7 @@ int wv_native_acc_dev(uint64_t handle, const float* d_x, int32_t* d_acc, float* 
         return fail(WV_E_FORMAT, "native acc: blob is %s, not an Int8/Int4/Int2/Ternary/Binary store", fmt_name(b.fmt));
     if (!d_x || !d_acc) return fail(WV_E_ARG, "native acc: nil x/acc");
     if (batch <= 0) return batch < 0 ? fail(WV_E_SHAPE, "native acc: negative batch %d", batch) : WV_OK;
-    hipSetDevice(b.device);
+    (void)hipSetDevice(b.device);
     const int e = launch_narrow_acc(b, d_x, d_acc, d_act_scale, batch, stream_or_default(stream, b.device));
     if (e != hipSuccess) return hip_fail(hipError_t(e), "native acc: kernel launch");
     return WV_OK;
@@ -956,7 +956,7 @@ int wv_matvec_t_dev(uint64_t handle, const float* d_gy, float* d_gx, int32_t bat
     if (!lookup(handle, b)) return fail(WV_E_HANDLE, "MatVecT: unknown handle %llu", (unsigned long long)handle);
     if (!d_gy || !d_gx) return fail(WV_E_ARG, "MatVecT: nil gy/gx");
     if (batch <= 0) return batch < 0 ? fail(WV_E_SHAPE, "MatVecT: negative batch %d", batch) : WV_OK;
-    hipSetDevice(b.device);
+    (void)hipSetDevice(b.device);
     hipStream_t s = stream_or_default(stream, b.device);
     CallScratch sc;
     int rc = sc.get(matvec_t_scratch_floats(b, batch), s, "MatVecT: scratch");
@@ -972,7 +972,7 @@ int wv_matmul_dev(uint64_t handle, const float* d_x, float* d_y, int32_t m, void
     if (!d_x || !d_y) return fail(WV_E_ARG, "MatMul: nil x/y");
     if (m < 0) return fail(WV_E_ARG, "MatMul: negative row count %d", m);
     if (m == 0) return WV_OK;
-    hipSetDevice(b.device);
+    (void)hipSetDevice(b.device);
     hipStream_t s = stream_or_default(stream, b.device);
     const bool gemm = gemm_supported(b, m);
     CallScratch sc;
@@ -988,7 +988,7 @@ int wv_matmul(uint64_t handle, const float* x, float* y, int32_t m) {
     if (!lookup(handle, b)) return fail(WV_E_HANDLE, "MatMul: unknown handle %llu", (unsigned long long)handle);
     if (!x || !y) return fail(WV_E_ARG, "MatMul: nil x/y");
     if (m <= 0) return m < 0 ? fail(WV_E_ARG, "MatMul: negative row count %d", m) : WV_OK;
-    hipSetDevice(b.device);
+    (void)hipSetDevice(b.device);
     hipStream_t s = g_dev[b.device].stream;
     Staging st(s);
     float* dx = st.in(x, size_t(m) * size_t(b.cols));
@@ -1004,7 +1004,7 @@ int wv_matvec(uint64_t handle, const float* x, float* y, int32_t batch) {
     if (!lookup(handle, b)) return fail(WV_E_HANDLE, "MatVec: unknown handle %llu", (unsigned long long)handle);
     if (!x || !y) return fail(WV_E_ARG, "MatVec: nil x/y");
     if (batch <= 0) return batch < 0 ? fail(WV_E_SHAPE, "MatVec: negative batch %d", batch) : WV_OK;
-    hipSetDevice(b.device);
+    (void)hipSetDevice(b.device);
     hipStream_t s = g_dev[b.device].stream;
     Staging st(s);
     float* dx = st.in(x, size_t(batch) * size_t(b.cols));
@@ -1020,7 +1020,7 @@ int wv_matvec_t(uint64_t handle, const float* gy, float* gx, int32_t batch) {
     if (!lookup(handle, b)) return fail(WV_E_HANDLE, "MatVecT: unknown handle %llu", (unsigned long long)handle);
     if (!gy || !gx) return fail(WV_E_ARG, "MatVecT: nil gy/gx");
     if (batch <= 0) return batch < 0 ? fail(WV_E_SHAPE, "MatVecT: negative batch %d", batch) : WV_OK;
-    hipSetDevice(b.device);
+    (void)hipSetDevice(b.device);
     hipStream_t s = g_dev[b.device].stream;
     Staging st(s);
     float* dg = st.in(gy, size_t(batch) * size_t(b.rows));
@@ -1064,7 +1064,7 @@ int wv_dense_forward_dev(uint64_t handle, const float* d_x, float* d_pre, float*
     if (!d_post && (d_bias || act != ACT_LINEAR))
         return fail(WV_E_ARG, "dense: a bias or a non-linear activation needs a post buffer");
     if (batch <= 0) return batch < 0 ? fail(WV_E_SHAPE, "dense: negative batch %d", batch) : WV_OK;
-    hipSetDevice(b.device);
+    (void)hipSetDevice(b.device);
     hipStream_t s = stream_or_default(stream, b.device);
     CallScratch sc;
     int rc = sc.get(matvec_scratch_floats(b, batch), s, "dense: scratch");
@@ -1084,7 +1084,7 @@ int wv_dense_forward(uint64_t handle, const float* x, float* pre, float* post, i
     if (!lookup(handle, b)) return fail(WV_E_HANDLE, "dense: unknown handle %llu", (unsigned long long)handle);
     if (!x || !pre) return fail(WV_E_ARG, "dense: nil layer/input");
     if (batch <= 0) return batch < 0 ? fail(WV_E_SHAPE, "dense: negative batch %d", batch) : WV_OK;
-    hipSetDevice(b.device);
+    (void)hipSetDevice(b.device);
     hipStream_t s = g_dev[b.device].stream;
     const size_t n = size_t(batch) * size_t(b.rows);
     Staging st(s);
@@ -1105,7 +1105,7 @@ int wv_store_matvec(uint64_t handle, const double* x, size_t len_x, double* y, s
     if ((len_x && !x) || (len_y && !y)) return fail(WV_E_ARG, "weights: nil x/y");
     if (b.layout == LAYOUT_NARROW || b.layout == LAYOUT_F32) {
         if (int64_t(len_x) < b.cols || int64_t(len_y) < b.rows) return fail(WV_E_SHAPE, "weights: matvecF64 shape");
-        hipSetDevice(b.device);
+        (void)hipSetDevice(b.device);
         hipStream_t s = g_dev[b.device].stream;
         Staging st(s);
         double* dx = st.in(x, size_t(b.cols));
@@ -1135,7 +1135,7 @@ int wv_store_matvec_t(uint64_t handle, const double* gy, size_t len_gy, double* 
     if ((len_gy && !gy) || (len_gx && !gx)) return fail(WV_E_ARG, "weights: nil gy/gx");
     if (b.layout == LAYOUT_NARROW || b.layout == LAYOUT_F32) {
         if (int64_t(len_gy) < b.rows || int64_t(len_gx) < b.cols) return fail(WV_E_SHAPE, "weights: matvecTF64 shape");
-        hipSetDevice(b.device);
+        (void)hipSetDevice(b.device);
         hipStream_t s = g_dev[b.device].stream;
         Staging st(s);
         double* dg = st.in(gy, size_t(b.rows));
