@@ -68,10 +68,10 @@ PREFILL = {
     f"q4k_prefill_{i}x{o}_m{m}": ("Q4_K", o, i, m, f"Q4_K prefill GEMM {i}->{o} M={m} (fp16 MFMA)")
     for (i, o) in ((4096, 14336), (14336, 4096)) for m in (32, 128, 512)
 }
-# The other k-quants on the packed-W MFMA GEMM.
+# The other k-quants, Q8_0 and IQ4_NL on the packed-W MFMA GEMM.
 PREFILL.update({
-    f"{f.lower().replace('_', '')}_prefill_4096x14336_m{m}": (f, 14336, 4096, m, f"{f} prefill 4096->14336 M={m}")
-    for f in ("Q2_K", "Q3_K", "Q5_K", "Q6_K") for m in (32, 128, 512)
+    f"{f.lower().replace('_k', 'k')}_prefill_4096x14336_m{m}": (f, 14336, 4096, m, f"{f} prefill 4096->14336 M={m}")
+    for f in ("Q2_K", "Q3_K", "Q5_K", "Q6_K", "Q8_0", "IQ4_NL") for m in (32, 128, 512)
 })
 # quant.MatVecT (gx += W^T gy, wv_matvec_t_dev) of a Dense layer's weight:
 # name -> (format, rows, cols, description); rows = the layer's out, cols = its in.

@@ -222,7 +222,7 @@ int wv_store_matvec(uint64_t handle, const double *x, size_t len_x, double *y, s
  * 1e-5 of wv_matvec; each token row and each weight row is scaled by a power
  * of two into fp16's range and back, so outlier or tiny activations and
  * weights keep that bar): Q4_K at every m, the other row-interleaved formats
- * (wv_blob_info layout "row-interleaved") but IQ4_NL from m = 9. Every other
+ * (wv_blob_info layout "row-interleaved") from m = 9. Every other
  * case runs the batched GEMV kernels of wv_matvec_dev. Device pointers,
  * enqueued on `stream`. */
 int wv_matmul_dev(uint64_t handle, const float *d_x, float *d_y, int32_t m, void *stream);

@@ -83,14 +83,14 @@ def test_prefill_q4k_wide(shape, m):
 
 
 @pytest.mark.parametrize("fmt", ["Q2_K", "Q3_K", "Q5_K", "Q6_K", "Q8_0", "Q4_0", "Q4_1", "Q5_0", "Q5_1",
-                                 "IQ1_S", "IQ2_XXS", "IQ2_XS", "IQ3_XXS", "IQ3_S", "IQ4_XS",
+                                 "IQ1_S", "IQ2_XXS", "IQ2_XS", "IQ3_XXS", "IQ3_S", "IQ4_XS", "IQ4_NL",
                                  "TernaryPacked", "BinaryPacked", "AffinePacked"])
 @pytest.mark.parametrize("shape,m", [((256, 1024), 128), ((448, 2048), 300), ((1000, 4096), 130), ((300, 1024), 9),
                                      ((520, 2048), 33), ((256, 1024), 64)])
 def test_prefill_other_formats_mfma(fmt, shape, m):
     """Token blocks over 8 of every other row-interleaved format take the
     packed-W MFMA GEMM (32-, 64- and 128-token tiles), each with its own
-    B-operand builder."""
+    B-operand builder (IQ4_NL's looks its float grid up as fp16)."""
     rows, cols = shape
     print(f"[gpu] prefill {fmt} {cols}->{rows} M={m}", flush=True)
     rng = np.random.default_rng(rows + m)
@@ -109,7 +109,7 @@ def test_prefill_other_formats_mfma(fmt, shape, m):
     d.free()
 
 
-@pytest.mark.parametrize("fmt", ["Q4_K", "Q8_0", "Q4_0", "IQ2_XS"])
+@pytest.mark.parametrize("fmt", ["Q4_K", "Q8_0", "Q4_0", "IQ2_XS", "IQ4_NL"])
 @pytest.mark.parametrize("m", [65, 100, 128])
 def test_prefill_four_tile_blocks(fmt, m):
     """65 to 128 tokens on 200 row groups or more take the K-split-free
@@ -166,8 +166,8 @@ def test_prefill_outlier_and_tiny_activations(fmt, m):
     d.free()
 
 
-@pytest.mark.parametrize("fmt", ["Q4_K", "Q6_K", "Q3_K", "Q8_0", "Q4_0", "Q5_1", "IQ2_XS", "TernaryPacked",
-                                 "AffinePacked"])
+@pytest.mark.parametrize("fmt", ["Q4_K", "Q6_K", "Q3_K", "Q8_0", "Q4_0", "Q5_1", "IQ2_XS", "IQ4_NL",
+                                 "TernaryPacked", "AffinePacked"])
 @pytest.mark.parametrize("m", [16, 64, 300])
 def test_prefill_tiny_and_huge_weight_rows(fmt, m):
     """Weight rows the fp16 B operand cannot hold unscaled: rows scaled by
@@ -236,10 +236,9 @@ def test_prefill_q4k_baseline(shape, m):
     assert err <= TOL_MFMA
 
 
-@pytest.mark.parametrize("fmt,m", [("Q8_0", 8), ("Q6_K", 8), ("Q5_K", 3), ("IQ4_NL", 9), ("IQ4_NL", 40)])
+@pytest.mark.parametrize("fmt,m", [("Q8_0", 8), ("Q6_K", 8), ("Q5_K", 3), ("IQ4_NL", 8)])
 def test_prefill_other_formats_use_batched_gemv(fmt, m):
-    """Up to 8 token rows (and IQ4_NL, whose grid is float, at any M) run
-    the batched GEMVs, with the GEMV bar."""
+    """Up to 8 token rows run the batched GEMVs, with the GEMV bar."""
     rows, cols = 300, 1024
     print(f"[gpu] prefill {fmt} M={m} via batched gemv", flush=True)
     rng = np.random.default_rng(5)

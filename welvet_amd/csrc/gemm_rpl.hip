@@ -341,6 +341,56 @@ struct GemmLin {
     }
 };
 
+// IQ4_NL (quant/iq.go:169-180): w = scale * grid[q], the 16-value float grid
+// (kIQ4NLGrid) as fp16, one scale per 32-column chunk. The codes are Q4_K's
+// nibble planes; the grid is looked up four codes at a time with
+// v_perm_b32 from byte tables of the fp16 values' low and high bytes (codes
+// 0-7 from the first two dwords of a table, 8-15 from the last two, picked
+// per byte by the code's bit 3), and the low and high bytes are interleaved
+// into half2 pairs in k order [0,2,4,6,1,3,5,7].
+struct GemmNL {
+    static constexpr uint16_t h16(int q) { return __builtin_bit_cast(uint16_t, _Float16(kIQ4NLGrid[q])); }
+    static constexpr uint32_t tab(int n, int sh) {  // bytes 4n..4n+3 of the low (sh 0) or high (sh 8) table
+        return uint32_t((h16(4 * n) >> sh) & 0xFF) | uint32_t((h16(4 * n + 1) >> sh) & 0xFF) << 8 |
+               uint32_t((h16(4 * n + 2) >> sh) & 0xFF) << 16 | uint32_t((h16(4 * n + 3) >> sh) & 0xFF) << 24;
+    }
+    struct Ch { GemmCodes<4>::C c; uint32_t s0; };
+    static __device__ __forceinline__ Ch load(const RplArgs& a, int64_t ci, int64_t si, int j, int lane) {
+        return {GemmCodes<4>::load(a, ci, lane), reinterpret_cast<const uint32_t*>(a.meta)[(si * 64 + lane) * 8 + j]};
+    }
+    // fp16 grid values of the 4 codes in the bytes of c: half2 of bytes 0, 1 and of bytes 2, 3
+    static __device__ __forceinline__ void look4(uint32_t c, half2v& q01, half2v& q23) {
+        constexpr uint32_t L0 = tab(0, 0), L1 = tab(1, 0), L2 = tab(2, 0), L3 = tab(3, 0);
+        constexpr uint32_t H0 = tab(0, 8), H1 = tab(1, 8), H2 = tab(2, 8), H3 = tab(3, 8);
+        const uint32_t sel = c & 0x07070707u;
+        const uint32_t hi8 = ((c >> 3) & 0x01010101u) * 0xFFu;  // 0xFF in the bytes of codes 8-15
+        const uint32_t lo = (__builtin_amdgcn_perm(L3, L2, sel) & hi8) | (__builtin_amdgcn_perm(L1, L0, sel) & ~hi8);
+        const uint32_t hi = (__builtin_amdgcn_perm(H3, H2, sel) & hi8) | (__builtin_amdgcn_perm(H1, H0, sel) & ~hi8);
+        q01 = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(hi, lo, 0x05010400u));
+        q23 = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(hi, lo, 0x07030602u));
+    }
+    static __device__ __forceinline__ void bops(const Ch& c, int lane, const float (&wk)[2], half8 (&bf)[2][2]) {
+        uint32_t se[2][2], so[2][2];
+        GemmCodes<4>::spread(c.c, lane, se, so);
+        const auto st = __builtin_amdgcn_permlane32_swap(c.s0, c.s0, false, false);
+#pragma unroll
+        for (int T = 0; T < 2; ++T) {
+            const _Float16 sc = _Float16(__uint_as_float(st[T]) * wk[T]);
+            const half2v s2 = {sc, sc};
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk) {
+                half2v q[4];
+                look4(se[T][kk], q[0], q[1]);
+                look4(so[T][kk], q[2], q[3]);
+                uint32_t p[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) p[i] = __builtin_bit_cast(uint32_t, q[i] * s2);
+                bf[T][kk] = __builtin_bit_cast(half8, make_uint4(p[0], p[1], p[2], p[3]));
+            }
+        }
+    }
+};
+
 // Row factors (RplArgs::wrow) of row group g in the B-operand layout: wk[T]
 // belongs to row 32T + lane % 32, the lane's row in 32-row tile T. Two plain
 // loads rather than one and a lane swap: nothing waits for them before the
@@ -738,10 +788,9 @@ __global__ void __launch_bounds__(256) k_split_sum(const float* __restrict__ par
 }  // namespace
 
 // Q4_K at every M; every other row-interleaved format from 9 token rows up
-// (up to 8 rows, one batched GEMV launch reads the weights once), except
-// IQ4_NL, whose float grid has no B-operand builder: it runs batched GEMVs.
+// (up to 8 rows, one batched GEMV launch reads the weights once).
 bool gemm_supported(const DevBlob& b, int M) {
-    if (b.layout != LAYOUT_RPL || b.fmt == FMT_IQ4_NL) return false;  // IQ4_NL's float grid: batched GEMV
+    if (b.layout != LAYOUT_RPL) return false;
     if (!b.rpl.wrow) return false;  // fused images carry no row factors
     return b.fmt == FMT_Q4_K || M > 8;
 }
@@ -834,6 +883,7 @@ int with_builder(const DevBlob& b, const Go& go) {
     case FMT_IQ3_S: go.template run<GemmLin<3, true, 7>>(); return 0;
     case FMT_IQ4_XS: go.template run<GemmLin<4, true, 15>>(); return 0;
     case FMT_TERNARY: go.template run<GemmLin<2, true, 2>>(); return 0;
+    case FMT_IQ4_NL: go.template run<GemmNL>(); return 0;
     default: return int(hipErrorInvalidValue);
     }
 }
