@@ -8,6 +8,8 @@ against the f64 textbook product over the reference's dequantized weights
 one f32 rounding). Blobs without an MFMA kernel run the batched GEMV kernels
 and keep the GEMV bar of 1e-5.
 """
+import os
+
 import numpy as np
 import pytest
 
@@ -247,6 +249,34 @@ def test_prefill_other_formats_use_batched_gemv(fmt, m):
     d = wv.upload(p)
     x = rng.standard_normal((m, cols)).astype(np.float32)
     op = oracle.Packed(p.fmt, rows, cols, p.raw, p.scales, p.meta, p.block_weights)
+    ref = oracle.reference_y(op, x)
+    assert normwise(d.matmul(x), ref) <= TOL_F32
+    d.free()
+
+
+@pytest.mark.parametrize("fmt,cols,force_raw", [("Q4_K", 1024, True), ("IQ4_NL", 1024, True), ("Q8_0", 96, False),
+                                                ("Q4_0", 160, False)])
+def test_prefill_reference_layout_uses_batched_gemv(fmt, cols, force_raw):
+    """Blobs on the reference layout (forced, or cols not a multiple of 256)
+    take the batched GEMVs at any M, with the GEMV bar; token rows go 8 per
+    launch, so M = 20 ends on a ragged launch."""
+    rows, m = 200, 20
+    print(f"[gpu] prefill {fmt} {cols}->{rows} M={m} on the reference layout", flush=True)
+    rng = np.random.default_rng(31)
+    w = (rng.standard_normal(rows * cols) * 0.02).astype(np.float32)
+    p = wv.pack(fmt, w, rows, cols)
+    old = os.environ.get("WV_FORCE_RAW")
+    os.environ["WV_FORCE_RAW"] = "1" if force_raw else "0"
+    try:
+        d = wv.upload(p)
+    finally:
+        if old is None:
+            os.environ.pop("WV_FORCE_RAW")
+        else:
+            os.environ["WV_FORCE_RAW"] = old
+    assert d.info()["layout"] == "raw"
+    x = rng.standard_normal((m, cols)).astype(np.float32)
+    op = oracle.Packed(p.fmt, rows, cols, p.raw, p.scales, p.meta, p.block_weights, p.mins)
     ref = oracle.reference_y(op, x)
     assert normwise(d.matmul(x), ref) <= TOL_F32
     d.free()
