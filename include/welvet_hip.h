@@ -198,6 +198,21 @@ int wv_dense_forward(uint64_t handle, const float *x, float *pre, float *post, i
 int wv_dense_forward_dev(uint64_t handle, const float *d_x, float *d_pre, float *d_post, int32_t batch,
                          const double *d_bias, int32_t act, void *stream);
 
+/* dense.Forward for a block of token rows (a prefill), through the batched
+ * prefill GEMM: forwardSIMDBlockFused (layers/dense/simd_block.go:17-39),
+ * which runs the block's rows as independent GEMVs, with applyBiasAct
+ * (dense.go:145-167) after it. pre = W x as wv_matmul_dev computes it (fp16
+ * MFMA, within 2e-3 normwise, wherever wv_matmul_dev takes the GEMM: a
+ * row-interleaved blob and batch > 8, or Q4_K at any batch), then bias and
+ * act as in wv_dense_forward; every other case is wv_dense_forward itself.
+ * Arguments, errors and the post rule as wv_dense_forward. */
+int wv_dense_forward_block(uint64_t handle, const float *x, float *pre, float *post, int32_t batch,
+                           const double *bias, int32_t act);
+
+/* Device-pointer form of wv_dense_forward_block, enqueued on `stream`. */
+int wv_dense_forward_block_dev(uint64_t handle, const float *d_x, float *d_pre, float *d_post, int32_t batch,
+                               const double *d_bias, int32_t act, void *stream);
+
 /* WV_NATIVE_* DTypes only: the exact int32 accumulators (batch*rows) and the
  * per-batch-row activation scales (batch) of the int8 path, device pointers. */
 int wv_native_acc_dev(uint64_t handle, const float *d_x, int32_t *d_acc, float *d_act_scale,

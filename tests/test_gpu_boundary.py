@@ -102,6 +102,34 @@ def test_dense_forward_bias_act(fmt, shape, layout, act, with_bias):
     d.free()
 
 
+@pytest.mark.parametrize("fmt,rows,cols,batch,layout",
+                         [("Q4_K", 512, 1024, 40, "row-interleaved"), ("Q8_0", 300, 1024, 20, "row-interleaved"),
+                          ("IQ4_NL", 256, 512, 33, "row-interleaved"), ("Q4_K", 512, 1024, 5, "row-interleaved"),
+                          ("Q8_0", 300, 1024, 6, "row-interleaved"), ("Q6_K", 100, 700, 20, "raw")])
+@pytest.mark.parametrize("act", ["linear", "silu", "gelu"])
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_dense_forward_block(fmt, rows, cols, batch, layout, act, with_bias):
+    """wv_dense_forward_block: a token block's pre = W x is the prefill GEMM's
+    (bit-equal to wv_matmul, within 2e-3 of the f64 product) wherever
+    wv_matmul takes the GEMM, wv_dense_forward's GEMV otherwise (Q8_0 at 6
+    rows, the reference-layout Q6_K); bias and act as in wv_dense_forward."""
+    print(f"[gpu] dense_forward_block {fmt} {cols}->{rows} batch {batch} {act} bias={with_bias}", flush=True)
+    p, d, rng = make(fmt, rows, cols, rows + batch)
+    assert d.info()["layout"] == layout
+    x = rng.standard_normal((batch, cols)).astype(np.float32)
+    bias = rng.standard_normal(rows) * 0.1 if with_bias else None
+    gemm = layout == "row-interleaved" and (fmt == "Q4_K" or batch > 8)
+    y = d.matmul(x) if gemm else d.matvec(x)
+    want_pre, want_post = dense_ref.apply_bias_act(y, bias, act)
+    pre, post = d.dense_forward(x, bias, act, block=True)
+    assert np.array_equal(pre, want_pre)
+    assert np.abs(post.astype(np.float64) - want_post).max() <= 1e-6 * max(1.0, np.abs(want_post).max())
+    wd = oracle.unpack(packed_ref(p)).reshape(rows, cols).astype(np.float64)
+    ref = x.astype(np.float64) @ wd.T
+    assert normwise(y, ref) <= (2e-3 if gemm else TOL)
+    d.free()
+
+
 def test_dense_forward_needs_post_for_epilogue():
     p, d, rng = make("Q4_K", 64, 256, 2)
     L = wv.lib()

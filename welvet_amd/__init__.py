@@ -38,6 +38,7 @@ EXPORTS = (
     "wv_init", "wv_last_error", "wv_version", "wv_pack_sizes", "wv_pack",
     "wv_pack_native", "wv_blob_upload", "wv_blob_upload_wire", "wv_blob_free", "wv_blob_info",
     "wv_matvec", "wv_matvec_dev", "wv_matvec_dev_noalloc", "wv_quant_matvec", "wv_dense_forward", "wv_dense_forward_dev",
+    "wv_dense_forward_block", "wv_dense_forward_block_dev",
     "wv_native_acc_dev", "wv_store_matvec", "wv_matvec_t", "wv_matvec_t_dev", "wv_quant_matvec_t",
     "wv_store_matvec_t", "wv_matmul", "wv_matmul_dev", "wv_sync",
     "wv_decoder_create", "wv_decoder_set_layer", "wv_decoder_set_output", "wv_decoder_set_kv",
@@ -84,6 +85,8 @@ def lib():
     L.wv_quant_matvec_t.argtypes = [ctypes.c_uint64, _P, _SZ, _P, _SZ]
     L.wv_dense_forward.argtypes = [ctypes.c_uint64, _P, _P, _P, ctypes.c_int32, _P, ctypes.c_int32]
     L.wv_dense_forward_dev.argtypes = [ctypes.c_uint64, _P, _P, _P, ctypes.c_int32, _P, ctypes.c_int32, _P]
+    L.wv_dense_forward_block.argtypes = [ctypes.c_uint64, _P, _P, _P, ctypes.c_int32, _P, ctypes.c_int32]
+    L.wv_dense_forward_block_dev.argtypes = [ctypes.c_uint64, _P, _P, _P, ctypes.c_int32, _P, ctypes.c_int32, _P]
     L.wv_store_matvec.argtypes = [ctypes.c_uint64, _P, _SZ, _P, _SZ]
     L.wv_store_matvec_t.argtypes = [ctypes.c_uint64, _P, _SZ, _P, _SZ]
     L.wv_matvec_t.argtypes = [ctypes.c_uint64, _P, _P, ctypes.c_int32]
@@ -282,15 +285,17 @@ class DeviceBlob:
         check(lib().wv_quant_matvec_t(self.handle, gy.ctypes.data if gy.size else None, gy.size,
                                       gx.ctypes.data if gx.size else None, gx.size))
 
-    def dense_forward(self, x: np.ndarray, bias: np.ndarray | None = None, act="linear"):
-        """dense.Forward (layers/dense/dense.go:100): (pre, post) with applyBiasAct (dense.go:145-167)."""
+    def dense_forward(self, x: np.ndarray, bias: np.ndarray | None = None, act="linear", block=False):
+        """dense.Forward (layers/dense/dense.go:100): (pre, post) with applyBiasAct (dense.go:145-167).
+        block=True: a token block through the prefill GEMM (wv_dense_forward_block, 2e-3 tolerance)."""
         x = np.ascontiguousarray(x, np.float32)
         batch = x.size // self.cols
         pre = np.zeros((batch, self.rows), np.float32)
         post = np.zeros((batch, self.rows), np.float32)
         b = None if bias is None else np.ascontiguousarray(bias, np.float64)
         a = ACT[act] if isinstance(act, str) else int(act)
-        check(lib().wv_dense_forward(self.handle, x.ctypes.data, pre.ctypes.data, post.ctypes.data, batch, _p(b), a))
+        fn = lib().wv_dense_forward_block if block else lib().wv_dense_forward
+        check(fn(self.handle, x.ctypes.data, pre.ctypes.data, post.ctypes.data, batch, _p(b), a))
         if x.ndim == 1:
             return pre.reshape(self.rows), post.reshape(self.rows)
         return pre, post

@@ -1078,8 +1078,11 @@ int wv_dense_forward_dev(uint64_t handle, const float* d_x, float* d_pre, float*
     return WV_OK;
 }
 
-int wv_dense_forward(uint64_t handle, const float* x, float* pre, float* post, int32_t batch, const double* bias,
-                     int32_t act) {
+// Host-pointer form of a dense forward entry point: stage x (and the bias),
+// run `dev` on the device stream, copy pre (and post) back.
+static int dense_forward_host(uint64_t handle, const float* x, float* pre, float* post, int32_t batch,
+                              const double* bias, int32_t act,
+                              int (*dev)(uint64_t, const float*, float*, float*, int32_t, const double*, int32_t, void*)) {
     DevBlob b;
     if (!lookup(handle, b)) return fail(WV_E_HANDLE, "dense: unknown handle %llu", (unsigned long long)handle);
     if (!x || !pre) return fail(WV_E_ARG, "dense: nil layer/input");
@@ -1093,10 +1096,41 @@ int wv_dense_forward(uint64_t handle, const float* x, float* pre, float* post, i
     float* dpost = post ? st.out(n) : nullptr;
     const double* dbias = bias ? st.in(bias, size_t(b.rows)) : nullptr;
     int rc = st.rc("dense: staging");
-    if (!rc) rc = wv_dense_forward_dev(handle, dx, dpre, dpost, batch, dbias, act, s);
+    if (!rc) rc = dev(handle, dx, dpre, dpost, batch, dbias, act, s);
     if (!rc) rc = st.back(pre, dpre, n, "dense: copy pre");
     if (!rc && post) rc = st.back(post, dpost, n, "dense: copy post");
     return st.finish(rc, "dense: sync");
+}
+
+int wv_dense_forward(uint64_t handle, const float* x, float* pre, float* post, int32_t batch, const double* bias,
+                     int32_t act) {
+    return dense_forward_host(handle, x, pre, post, batch, bias, act, wv_dense_forward_dev);
+}
+
+int wv_dense_forward_block_dev(uint64_t handle, const float* d_x, float* d_pre, float* d_post, int32_t batch,
+                               const double* d_bias, int32_t act, void* stream) {
+    DevBlob b;
+    if (!lookup(handle, b)) return fail(WV_E_HANDLE, "dense: unknown handle %llu", (unsigned long long)handle);
+    if (batch <= 0 || !gemm_supported(b, batch))  // the GEMV path, with its own checks
+        return wv_dense_forward_dev(handle, d_x, d_pre, d_post, batch, d_bias, act, stream);
+    if (!d_x || !d_pre) return fail(WV_E_ARG, "dense: nil layer/input");
+    if (!act_valid(act)) return fail(WV_E_ARG, "dense: activation %d is not a core.ActivationType", act);
+    if (!d_post && (d_bias || act != ACT_LINEAR))
+        return fail(WV_E_ARG, "dense: a bias or a non-linear activation needs a post buffer");
+    (void)hipSetDevice(b.device);
+    hipStream_t s = stream_or_default(stream, b.device);
+    CallScratch sc;
+    int rc = sc.get(gemm_scratch_floats(b, batch), s, "dense: scratch");
+    if (rc) return rc;
+    int e = launch_gemm(b, d_x, d_pre, batch, s, sc.f());
+    if (e == hipSuccess && d_post) e = launch_bias_act(d_pre, d_pre, d_post, d_bias, act, b.rows, batch, s);
+    if (e != hipSuccess) return hip_fail(hipError_t(e), "dense: kernel launch");
+    return WV_OK;
+}
+
+int wv_dense_forward_block(uint64_t handle, const float* x, float* pre, float* post, int32_t batch, const double* bias,
+                           int32_t act) {
+    return dense_forward_host(handle, x, pre, post, batch, bias, act, wv_dense_forward_block_dev);
 }
 
 int wv_store_matvec(uint64_t handle, const double* x, size_t len_x, double* y, size_t len_y) {
