@@ -58,10 +58,13 @@ def test_prefill_q4k_small(shape, m):
     assert d.info()["layout"] == "row-interleaved"
     x = rng.standard_normal((m, cols)).astype(np.float32)
     ref = x.astype(np.float64) @ wd.T
+    ys = []
     for _ in range(2):  # split-K scratch is per call; results must not depend on the previous call
         y = d.matmul(x)
         assert normwise(y, ref) <= TOL_MFMA
         assert rowwise(y, ref) <= 4 * TOL_MFMA
+        ys.append(y)
+    assert np.array_equal(ys[0], ys[1])  # fixed-order sums: the same bits every call
     d.free()
 
 
@@ -77,10 +80,13 @@ def test_prefill_q4k_wide(shape, m):
     d = wv.upload(p)
     x = rng.standard_normal((m, cols)).astype(np.float32)
     ref = x.astype(np.float64) @ wd.T
+    ys = []
     for _ in range(2):
         y = d.matmul(x)
         assert normwise(y, ref) <= TOL_MFMA
         assert rowwise(y, ref) <= 4 * TOL_MFMA
+        ys.append(y)
+    assert np.array_equal(ys[0], ys[1])
     d.free()
 
 
