@@ -18,15 +18,17 @@
  *     void* (NULL = the library's own stream for the current device); they
  *     enqueue work and return without synchronising. Host-pointer entry
  *     points copy in, compute and copy out synchronously.
- *   - All entry points are thread-safe (handle table under a mutex,
- *     thread-local error text). A blob holds weights only: the scratch a call
- *     needs (K-split or slice partials) is one of a few per-device slots that
- *     the call holds until its launches are enqueued, with the GPU ordering a
- *     slot's next user after its last one, so concurrent calls on one blob,
- *     from several threads or on several streams, never share partials. The
- *     slots grow on first use of a larger shape (hipMalloc) and are kept for
- *     the process. Blob and decoder handles must not be freed while another
- *     thread still calls with them.
+ *   - Every entry point except wv_matvec_dev_noalloc is thread-safe (handle
+ *     table under a mutex, thread-local error text). A blob holds weights
+ *     only: the scratch such a call needs (K-split or slice partials) is one
+ *     of a few per-device slots that the call holds until its launches are
+ *     enqueued, with the GPU ordering a slot's next user after its last one,
+ *     so concurrent calls on one blob, from several threads or on several
+ *     streams, never share partials. The slots grow on first use of a larger
+ *     shape (hipMalloc) and are kept for the process. wv_matvec_dev_noalloc
+ *     is the exception: all its calls on one GPU share one fixed array, so
+ *     overlapping calls race (see its declaration). Blob and decoder handles
+ *     must not be freed while another thread still calls with them.
  */
 #ifndef WELVET_HIP_H
 #define WELVET_HIP_H
@@ -126,6 +128,21 @@ int wv_blob_upload(int format, int64_t rows, int64_t cols, int32_t block_weights
                    const uint8_t *meta, size_t n_meta,
                    float tensor_scale, uint64_t *handle);
 
+/* wv_blob_upload with upload options (0 = wv_blob_upload).
+ * WV_UPLOAD_REFERENCE_LAYOUT keeps the device copy in the reference's byte
+ * order (Raw, Mins, Scales as quant.Blob holds them, quant/format.go:110-131)
+ * instead of the row-interleaved layout that the formats with 256-column rows
+ * take by default; every format has kernels on that layout. It serves tests
+ * and comparisons of the two layouts: their results agree within the f32
+ * tolerance. Unknown flag bits are WV_E_ARG. */
+#define WV_UPLOAD_REFERENCE_LAYOUT 1u
+int wv_blob_upload_flags(int format, int64_t rows, int64_t cols, int32_t block_weights,
+                         const uint8_t *raw, size_t raw_len,
+                         const float *scales, size_t n_scales,
+                         const float *mins, size_t n_mins,
+                         const uint8_t *meta, size_t n_meta,
+                         float tensor_scale, uint32_t flags, uint64_t *handle);
+
 /* Uploads a packed blob straight from its ENTITY wire bytes, replacing
  * entity.DecodePackedBlob (model/entity/packed.go:37-76; the same layout as
  * weights.DecodePackedWire, weights/packed_wire.go:57-110) plus the host SIMD
@@ -183,6 +200,16 @@ int wv_matvec_dev_noalloc(uint64_t handle, const float *d_x, float *d_y, int32_t
  * cols is not read and y past rows is not written. Host pointers; synchronous.
  * WV_NATIVE_* blobs are not quant blobs (WV_E_FORMAT). */
 int wv_quant_matvec(uint64_t handle, const float *x, size_t len_x, float *y, size_t len_y);
+
+/* dense.MatVecPackedBlob (layers/dense/simd.go:570-614), the LM head's and
+ * standalone projections' entry, one vector: len_x >= cols and len_y >= rows,
+ * else WV_E_SHAPE "dense: packed matvec shape"; an unknown handle is
+ * WV_E_HANDLE "dense: nil packed blob". Its format switch covers the packed
+ * formats only: a WV_FMT_NONE blob (and a WV_NATIVE_* Store, a FormatNone
+ * blob there) is WV_E_FORMAT "dense: MatVecPackedBlob unsupported none".
+ * Otherwise as wv_quant_matvec: x past cols is not read, y past rows is not
+ * written. Host pointers; synchronous. */
+int wv_matvec_packed_blob(uint64_t handle, const float *x, size_t len_x, float *y, size_t len_y);
 
 /* dense.Forward for a linear map with bias and activation (layers/dense/
  * dense.go:100-112 -> ForwardSIMD simd.go:23-77, applyBiasAct dense.go:145-167):

@@ -1,4 +1,5 @@
 """C-ABI library checks that need no GPU: symbols, host packers, error paths."""
+import ctypes
 import os
 import re
 
@@ -87,6 +88,11 @@ def test_error_paths_without_device():
     with pytest.raises(wv.WelvetError) as e:
         wv.check(wv.lib().wv_blob_free(123456789))
     assert e.value.code == -7
+    raw = np.zeros(144 * 4, np.uint8)
+    h = ctypes.c_uint64()
+    rc = wv.lib().wv_blob_upload_flags(8, 4, 256, 256, raw.ctypes.data, raw.size, None, 0, None, 0, None, 0,
+                                       ctypes.c_float(0), 6, ctypes.byref(h))
+    assert rc == -1 and "unknown flags 0x6" in wv.lib().wv_last_error().decode()
 
 
 @pytest.mark.parametrize("shape", [(16, 256), (64, 512), (3, 64), (7, 1088)])
@@ -141,6 +147,8 @@ def test_quant_contract_errors_without_device():
     assert rc == -7 and L.wv_last_error().decode() == "MatVec: nil blob"
     rc = L.wv_quant_matvec_t(987654321, x.ctypes.data, 4, x.ctypes.data, 4)
     assert rc == -7 and L.wv_last_error().decode() == "MatVecT: nil blob"
+    rc = L.wv_matvec_packed_blob(987654321, x.ctypes.data, 4, x.ctypes.data, 4)
+    assert rc == -7 and L.wv_last_error().decode() == "dense: nil packed blob"
     xd = np.zeros(4, np.float64)
     assert L.wv_store_matvec(987654321, xd.ctypes.data, 4, xd.ctypes.data, 4) == -7
     assert L.wv_last_error().decode() == "weights: nil"

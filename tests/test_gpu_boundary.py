@@ -79,6 +79,31 @@ def test_quant_matvec_contract():
     dn.free()
 
 
+def test_matvec_packed_blob_contract():
+    """dense.MatVecPackedBlob (layers/dense/simd.go:570-614): packed formats
+    as quant.MatVec; its shape error; FormatNone (and a Store's narrow DType)
+    falls to the format switch's default error."""
+    p, d, rng = make("Q6_K", 300, 512, 4)
+    x = rng.standard_normal(512 + 3).astype(np.float32)
+    y = np.full(300 + 2, -9.0, np.float32)
+    d.matvec_packed_blob(x, y)
+    ref = oracle.reference_y(packed_ref(p), x[:512])[0]
+    assert normwise(y[:300], ref) <= TOL and list(y[300:]) == [-9.0, -9.0]
+    with pytest.raises(wv.WelvetError, match=r"^SHAPE: dense: packed matvec shape$"):
+        d.matvec_packed_blob(x[:511], y)
+    with pytest.raises(wv.WelvetError, match=r"^SHAPE: dense: packed matvec shape$"):
+        d.matvec_packed_blob(x, y[:299])
+    d.free()
+    for fmt in ("none", "NativeInt8"):
+        pn = wv.pack(fmt, np.ones(64 * 128, np.float32), 64, 128)
+        dn = wv.upload(pn)
+        yn = np.full(64, -9.0, np.float32)
+        with pytest.raises(wv.WelvetError, match=r"^FORMAT: dense: MatVecPackedBlob unsupported none$"):
+            dn.matvec_packed_blob(np.ones(128, np.float32), yn)
+        assert (yn == -9.0).all()
+        dn.free()
+
+
 EPI = [("Q4_K", (512, 1024), "row-interleaved"), ("IQ4_NL", (300, 544), "raw"),
        ("Q6_K", (100, 700), "raw"), ("NativeInt4", (300, 512), "narrow"), ("none", (200, 300), "f32")]
 

@@ -4,7 +4,6 @@ Tolerances: f32 outputs within 1e-5 normwise relative
 error of the f64 textbook GEMV over the reference's dequantized weights
 (max|y_gpu - y_ref| / max|y_ref|); DTypeTernary int32 accumulators bit-exact.
 """
-import os
 
 import numpy as np
 import pytest
@@ -42,16 +41,7 @@ def weights(rows, cols, seed):
 
 def upload(fmt, w, rows, cols, force_raw=False):
     p = wv.pack(fmt, w, rows, cols)
-    old = os.environ.get("WV_FORCE_RAW")
-    os.environ["WV_FORCE_RAW"] = "1" if force_raw else "0"
-    try:
-        d = wv.upload(p)
-    finally:
-        if old is None:
-            os.environ.pop("WV_FORCE_RAW")
-        else:
-            os.environ["WV_FORCE_RAW"] = old
-    return p, d
+    return p, wv.upload(p, reference_layout=force_raw)
 
 
 def oracle_packed(p):
@@ -285,11 +275,7 @@ def test_ternary_code3_and_missing_scales(rows, cols):
     op = oracle.Packed(p.fmt, rows, cols, p.raw, scales, None, 16)
     ref = oracle.reference_y(op, x)[0]
     for force_raw in (False, True):
-        os.environ["WV_FORCE_RAW"] = "1" if force_raw else "0"
-        try:
-            d = wv.upload(p)
-        finally:
-            os.environ.pop("WV_FORCE_RAW")
+        d = wv.upload(p, reference_layout=force_raw)
         assert d.info()["layout"] == ("raw" if force_raw else "row-interleaved")
         assert normwise(d.matvec(x), ref) <= TOL
         d.free()
@@ -443,15 +429,7 @@ def shared_scale_blob(kind, rows, cols, seed):
 
 
 def upload_blob(p, force_raw):
-    old = os.environ.get("WV_FORCE_RAW")
-    os.environ["WV_FORCE_RAW"] = "1" if force_raw else "0"
-    try:
-        return wv.upload(p)
-    finally:
-        if old is None:
-            os.environ.pop("WV_FORCE_RAW")
-        else:
-            os.environ["WV_FORCE_RAW"] = old
+    return wv.upload(p, reference_layout=force_raw)
 
 
 @pytest.mark.parametrize("kind", ["affine32", "affine128", "affine256", "binary128"])

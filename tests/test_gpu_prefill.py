@@ -8,7 +8,6 @@ against the f64 textbook product over the reference's dequantized weights
 one f32 rounding). Blobs without an MFMA kernel run the batched GEMV kernels
 and keep the GEMV bar of 1e-5.
 """
-import os
 
 import numpy as np
 import pytest
@@ -271,15 +270,7 @@ def test_prefill_reference_layout_uses_batched_gemv(fmt, cols, force_raw):
     rng = np.random.default_rng(31)
     w = (rng.standard_normal(rows * cols) * 0.02).astype(np.float32)
     p = wv.pack(fmt, w, rows, cols)
-    old = os.environ.get("WV_FORCE_RAW")
-    os.environ["WV_FORCE_RAW"] = "1" if force_raw else "0"
-    try:
-        d = wv.upload(p)
-    finally:
-        if old is None:
-            os.environ.pop("WV_FORCE_RAW")
-        else:
-            os.environ["WV_FORCE_RAW"] = old
+    d = wv.upload(p, reference_layout=force_raw)
     assert d.info()["layout"] == "raw"
     x = rng.standard_normal((m, cols)).astype(np.float32)
     op = oracle.Packed(p.fmt, rows, cols, p.raw, p.scales, p.meta, p.block_weights, p.mins)

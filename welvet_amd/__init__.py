@@ -31,13 +31,14 @@ ACT = {"linear": -1, "relu": 0, "silu": 1, "gelu": 2, "tanh": 3, "sigmoid": 4, "
 FORMAT_NAMES = {v: k for k, v in FORMATS.items()}
 LAYOUTS = {0: "raw", 1: "row-interleaved", 4: "narrow", 5: "f32"}
 
+REFERENCE_LAYOUT = 1  # WV_UPLOAD_REFERENCE_LAYOUT
 WV_E = {-1: "ARG", -2: "SHAPE", -3: "FORMAT", -4: "OOM", -5: "HIP", -6: "NODEV", -7: "HANDLE"}
 
 # Every symbol include/welvet_hip.h declares.
 EXPORTS = (
     "wv_init", "wv_last_error", "wv_version", "wv_pack_sizes", "wv_pack",
-    "wv_pack_native", "wv_blob_upload", "wv_blob_upload_wire", "wv_blob_free", "wv_blob_info",
-    "wv_matvec", "wv_matvec_dev", "wv_matvec_dev_noalloc", "wv_quant_matvec", "wv_dense_forward", "wv_dense_forward_dev",
+    "wv_pack_native", "wv_blob_upload", "wv_blob_upload_flags", "wv_blob_upload_wire", "wv_blob_free", "wv_blob_info",
+    "wv_matvec", "wv_matvec_dev", "wv_matvec_dev_noalloc", "wv_quant_matvec", "wv_matvec_packed_blob", "wv_dense_forward", "wv_dense_forward_dev",
     "wv_dense_forward_block", "wv_dense_forward_block_dev",
     "wv_native_acc_dev", "wv_store_matvec", "wv_matvec_t", "wv_matvec_t_dev", "wv_quant_matvec_t",
     "wv_store_matvec_t", "wv_matmul", "wv_matmul_dev", "wv_sync",
@@ -74,6 +75,8 @@ def lib():
     L.wv_pack_native.argtypes = [ctypes.c_int, _P, _I64, _P, _P]
     L.wv_blob_upload.argtypes = [ctypes.c_int, _I64, _I64, ctypes.c_int32, _P, _SZ, _P, _SZ, _P, _SZ, _P, _SZ,
                                  ctypes.c_float, _P]
+    L.wv_blob_upload_flags.argtypes = [ctypes.c_int, _I64, _I64, ctypes.c_int32, _P, _SZ, _P, _SZ, _P, _SZ, _P, _SZ,
+                                       ctypes.c_float, ctypes.c_uint32, _P]
     L.wv_blob_upload_wire.argtypes = [ctypes.c_int, _I64, _I64, _P, _SZ, _P]
     L.wv_blob_free.argtypes = [ctypes.c_uint64]
     L.wv_blob_info.argtypes = [ctypes.c_uint64, _P, _P, _P, _P, _P]
@@ -82,6 +85,7 @@ def lib():
     L.wv_matvec_dev_noalloc.argtypes = [ctypes.c_uint64, _P, _P, ctypes.c_int32, _P]
     L.wv_native_acc_dev.argtypes = [ctypes.c_uint64, _P, _P, _P, ctypes.c_int32, _P]
     L.wv_quant_matvec.argtypes = [ctypes.c_uint64, _P, _SZ, _P, _SZ]
+    L.wv_matvec_packed_blob.argtypes = [ctypes.c_uint64, _P, _SZ, _P, _SZ]
     L.wv_quant_matvec_t.argtypes = [ctypes.c_uint64, _P, _SZ, _P, _SZ]
     L.wv_dense_forward.argtypes = [ctypes.c_uint64, _P, _P, _P, ctypes.c_int32, _P, ctypes.c_int32]
     L.wv_dense_forward_dev.argtypes = [ctypes.c_uint64, _P, _P, _P, ctypes.c_int32, _P, ctypes.c_int32, _P]
@@ -193,14 +197,15 @@ def _p(a):
 class DeviceBlob:
     """A blob resident in HBM (wv_blob_upload); freed with free() or on GC."""
 
-    def __init__(self, packed: PackedBlob):
+    def __init__(self, packed: PackedBlob, reference_layout: bool = False):
         h = ctypes.c_uint64()
         p = packed
-        check(lib().wv_blob_upload(p.fmt, p.rows, p.cols, p.block_weights, _p(p.raw), p.raw.size,
-                                   _p(p.scales), 0 if p.scales is None else p.scales.size,
-                                   _p(p.mins), 0 if p.mins is None else p.mins.size,
-                                   _p(p.meta), 0 if p.meta is None else p.meta.size,
-                                   ctypes.c_float(p.tensor_scale), ctypes.byref(h)))
+        check(lib().wv_blob_upload_flags(p.fmt, p.rows, p.cols, p.block_weights, _p(p.raw), p.raw.size,
+                                         _p(p.scales), 0 if p.scales is None else p.scales.size,
+                                         _p(p.mins), 0 if p.mins is None else p.mins.size,
+                                         _p(p.meta), 0 if p.meta is None else p.meta.size,
+                                         ctypes.c_float(p.tensor_scale),
+                                         REFERENCE_LAYOUT if reference_layout else 0, ctypes.byref(h)))
         self.handle = h.value
         self.fmt, self.rows, self.cols = p.fmt, p.rows, p.cols
         self.packed_bytes = p.nbytes
@@ -278,6 +283,14 @@ class DeviceBlob:
         check(lib().wv_quant_matvec(self.handle, x.ctypes.data if x.size else None, x.size,
                                     y.ctypes.data if y.size else None, y.size))
 
+    def matvec_packed_blob(self, x: np.ndarray, y: np.ndarray) -> None:
+        """dense.MatVecPackedBlob(b, x, y) (layers/dense/simd.go:570-614): one vector,
+        y[:rows] overwritten; FormatNone blobs are rejected as the reference does."""
+        x = np.ascontiguousarray(x, np.float32)
+        assert y.dtype == np.float32 and y.flags.c_contiguous
+        check(lib().wv_matvec_packed_blob(self.handle, x.ctypes.data if x.size else None, x.size,
+                                          y.ctypes.data if y.size else None, y.size))
+
     def quant_matvec_t(self, gy: np.ndarray, gx: np.ndarray) -> None:
         """quant.MatVecT(b, gy, gx) (quant/matvec_t.go:5): gx[:cols] += W^T gy[:rows], checkBlobGYGX."""
         gy = np.ascontiguousarray(gy, np.float32)
@@ -333,8 +346,10 @@ class DeviceBlob:
             pass
 
 
-def upload(packed: PackedBlob) -> DeviceBlob:
-    return DeviceBlob(packed)
+def upload(packed: PackedBlob, reference_layout: bool = False) -> DeviceBlob:
+    """wv_blob_upload; reference_layout=True keeps the reference's byte order on
+    the device (WV_UPLOAD_REFERENCE_LAYOUT) instead of the row-interleaved layout."""
+    return DeviceBlob(packed, reference_layout)
 
 
 def sync(stream: int | None = None) -> None:

@@ -560,8 +560,10 @@ __global__ void __launch_bounds__(64) k_gemvt_reduce(const float* __restrict__ p
 }
 
 // applyBiasAct (layers/dense/dense.go:145-167) over y[batch][rows]: pre =
-// f32(y + bias) written to `pre`, post = f32(act(f64(pre))) to `post`.
-__global__ void __launch_bounds__(256) k_bias_act(const float* __restrict__ y, float* __restrict__ pre,
+// f32(y + bias) written to `pre`, post = f32(act(f64(pre))) to `post`. y and
+// pre may be the same buffer (in place; each thread reads its element before
+// writing it), so neither is declared __restrict__.
+__global__ void __launch_bounds__(256) k_bias_act(const float* y, float* pre,
                                                   float* __restrict__ post, const double* __restrict__ bias, int act,
                                                   int64_t rows, int64_t n) {
     const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;

@@ -244,11 +244,6 @@ struct Staging {
     }
 };
 
-bool force_raw() {
-    const char* v = std::getenv("WV_FORCE_RAW");
-    return v && v[0] == '1';
-}
-
 inline float f32_at(const uint8_t* p) { float v; std::memcpy(&v, p, 4); return v; }
 
 // Host staging of a device image: byte buffer with 256-B aligned sections.
@@ -726,10 +721,11 @@ int wv_pack_native(int format, const float* weights, int64_t n, uint8_t* codes, 
     return WV_OK;
 }
 
-int wv_blob_upload(int format, int64_t rows, int64_t cols, int32_t block_weights, const uint8_t* raw, size_t raw_len,
-                   const float* scales, size_t n_scales, const float* mins, size_t n_mins, const uint8_t* meta,
-                   size_t n_meta, float tensor_scale, uint64_t* handle) {
+int wv_blob_upload_flags(int format, int64_t rows, int64_t cols, int32_t block_weights, const uint8_t* raw,
+                         size_t raw_len, const float* scales, size_t n_scales, const float* mins, size_t n_mins,
+                         const uint8_t* meta, size_t n_meta, float tensor_scale, uint32_t flags, uint64_t* handle) {
     if (!handle || !raw) return fail(WV_E_ARG, "wv_blob_upload: nil blob");
+    if (flags & ~uint32_t(WV_UPLOAD_REFERENCE_LAYOUT)) return fail(WV_E_ARG, "wv_blob_upload: unknown flags 0x%x", flags);
     if (rows <= 0 || cols <= 0)
         return fail(WV_E_SHAPE, "wv_blob_upload: bad shape rows=%lld cols=%lld", (long long)rows, (long long)cols);
     if (!supported_format(format))
@@ -766,7 +762,7 @@ int wv_blob_upload(int format, int64_t rows, int64_t cols, int32_t block_weights
     b.tensor_scale = tensor_scale == 0.0f ? 1.0f : tensor_scale;  // expandNarrowToI8 (simd.go:153-156)
     b.device = g_current;
     Image img;
-    const bool raw_only = force_raw();
+    const bool raw_only = (flags & WV_UPLOAD_REFERENCE_LAYOUT) != 0;
     RplOffsets ro;
     IQSpec iqs;
     if (iq_spec(format, iqs)) {
@@ -842,6 +838,13 @@ int wv_blob_upload(int format, int64_t rows, int64_t cols, int32_t block_weights
     g_blobs[h] = b;
     *handle = h;
     return WV_OK;
+}
+
+int wv_blob_upload(int format, int64_t rows, int64_t cols, int32_t block_weights, const uint8_t* raw, size_t raw_len,
+                   const float* scales, size_t n_scales, const float* mins, size_t n_mins, const uint8_t* meta,
+                   size_t n_meta, float tensor_scale, uint64_t* handle) {
+    return wv_blob_upload_flags(format, rows, cols, block_weights, raw, raw_len, scales, n_scales, mins, n_mins, meta,
+                                n_meta, tensor_scale, 0u, handle);
 }
 
 int wv_blob_upload_wire(int format, int64_t rows, int64_t cols, const uint8_t* wire, size_t wire_len,
@@ -1040,6 +1043,19 @@ int wv_quant_matvec(uint64_t handle, const float* x, size_t len_x, float* y, siz
         return fail(WV_E_SHAPE, "MatVec: size mismatch rows=%lld cols=%lld len(x)=%zu len(y)=%zu", (long long)b.rows,
                     (long long)b.cols, len_x, len_y);
     if (!x || !y) return fail(WV_E_ARG, "MatVec: nil x/y");
+    return wv_matvec(handle, x, y, 1);
+}
+
+int wv_matvec_packed_blob(uint64_t handle, const float* x, size_t len_x, float* y, size_t len_y) {
+    DevBlob b;
+    if (!lookup(handle, b)) return fail(WV_E_HANDLE, "dense: nil packed blob");
+    if (int64_t(len_x) < b.cols || int64_t(len_y) < b.rows) return fail(WV_E_SHAPE, "dense: packed matvec shape");
+    // The format switch (layers/dense/simd.go:579-613) has a case for every
+    // packed format; FormatNone (and a Store's narrow DTypes, which are
+    // FormatNone blobs there) falls through to the default error.
+    if (b.layout == LAYOUT_F32 || b.layout == LAYOUT_NARROW)
+        return fail(WV_E_FORMAT, "dense: MatVecPackedBlob unsupported none");
+    if (!x || !y) return fail(WV_E_ARG, "dense: nil x/y");
     return wv_matvec(handle, x, y, 1);
 }
 
