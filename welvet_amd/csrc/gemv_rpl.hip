@@ -27,6 +27,7 @@
 #include <algorithm>
 #include <cstdint>
 #include <cstdlib>
+#include <type_traits>
 
 #include "wave_ops.h"
 #include "wv_internal.h"
@@ -867,6 +868,178 @@ __global__ void __launch_bounds__(1024) k_gemv_rpl(RplArgs a, const float* __res
     if (valid) a.partial[(int64_t(b) * a.ksplit + ks) * rows_pad + row] = sum;
 }
 
+// Q4_K forward for the one-lane-per-row plan (L = 1, S = 1; the headline
+// 4096->14336 and the decoder's gate||up). Same layout, work split and x
+// planes as k_gemv_rpl<RplQ4KI, 1, 1, 4>, with a shorter instruction stream
+// per 32-column chunk (54 VALU against 64):
+//   * the chunk's codes are one contiguous 8 KiB run per super-block (Q4_K's
+//     super-block-major order), addressed from one base with constant
+//     offsets, and the wave is either active or not for its whole life (no
+//     per-step activity test);
+//   * the group scales meet T0, T1 as floats, P = u0*T0 + u1*T1, and the
+//     chunk's fixed-point scale 2^-s multiplies P into a super-block
+//     accumulator; d/255 is applied once per super-block;
+//   * the mins accumulate as sum_g (m_g + 128)*S_g over the super-block (S_g
+//     the 16-column sums of x), and the -128*sum(x) correction is taken once
+//     from the wave's total of x.
+// The three plane accumulators of each group stay independent: a Horner
+// chain (plane 2, << 8, plane 1, << 8, plane 0) saves the combining shifts
+// but serializes the dot4 instructions and ran 12.8 against 8.3 us.
+__global__ void __launch_bounds__(1024) k_gemv_q4k(RplArgs a, const float* __restrict__ x, float* __restrict__ y) {
+    extern __shared__ float4 sm4[];
+    const int W = blockDim.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int rg = blockIdx.x, ks = blockIdx.y, b = blockIdx.z;
+    const int sb = ks * W + wave;
+    const bool act = sb < a.nsb;
+    const int sbc = act ? sb : a.nsb - 1;  // an idle wave reads a valid super-block and contributes 0
+    const int64_t si = int64_t(rg) * a.nsb + sbc;
+
+    // x first (vector loads retire in issue order), then the metadata and D chunks.
+    constexpr int D = 4;
+    const float4 xv0 = reinterpret_cast<const float4*>(x + (int64_t(b) * a.nsb + sbc) * 256)[lane];
+    float4 gv = make_float4(1.f, 1.f, 1.f, 1.f);
+    float ssv[8];
+    const float* ssb = a.nrm_ss + int64_t(b) * a.nrm_n;
+    if (a.nrm_gamma) {
+        gv = reinterpret_cast<const float4*>(a.nrm_gamma + int64_t(sbc) * 256)[lane];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int i = lane + 64 * k;
+            const float v = ssb[min(i, a.nrm_n - 1)];
+            ssv[k] = i < a.nrm_n ? v : 0.f;
+        }
+    }
+    const uint4* mp = reinterpret_cast<const uint4*>(a.meta) + (si * 64 + lane) * 2;
+    const uint4 g0 = ld_stream(mp), g1 = ld_stream(mp + 1);
+    const float2 dd = reinterpret_cast<const float2*>(a.dd)[si * 64 + lane];
+    const uint4* cp = reinterpret_cast<const uint4*>(a.codes) + si * 512 + lane;  // chunk t at cp + 64 t
+    uint4 ch[8];
+#pragma unroll
+    for (int t = 0; t < D; ++t) ch[t] = ld_stream(cp + t * 64);
+
+    float4 xv = xv0;
+    if (a.nrm_gamma) {
+        // RMSNorm of x folded in (layers/rmsnorm/cpu.go:70-85), as in k_gemv_rpl.
+        double ssp = 0.0;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) ssp += ssv[k];
+        for (int i = lane + 512; i < a.nrm_n; i += 64) ssp += ssb[i];
+        ssp = wave_total_f64(ssp);
+        const double inv = 1.0 / sqrt(ssp / double(a.nsb * 256) + a.nrm_eps);
+        xv.x = float(double(xv0.x) * inv * double(gv.x));
+        xv.y = float(double(xv0.y) * inv * double(gv.y));
+        xv.z = float(double(xv0.z) * inv * double(gv.z));
+        xv.w = float(double(xv0.w) * inv * double(gv.w));
+    }
+
+    // Stage x in this wave's LDS slice: per chunk c, 24 dwords of X byte
+    // planes [plane][lo w0..3 | hi w0..3] (as RplQ4KI) and (2^-s, s0, s1).
+    constexpr int kSlice = 256 + 16;
+    float* xs = reinterpret_cast<float*>(sm4) + wave * kSlice;
+    float* part = reinterpret_cast<float*>(sm4) + W * kSlice;
+    const float lsum = (xv.x + xv.y) + (xv.z + xv.w);
+    float gsum = lsum;
+    gsum += quad_xor1(gsum);
+    gsum += quad_xor2(gsum);  // lanes 4g..4g+3: sum of columns 16g..16g+15
+    const float xtot = wave_total(lsum);
+    {
+        const int c = lane >> 3, q = lane & 7;  // lane = 8c + q holds columns 4q..4q+3 of chunk c
+        float m = fmaxf(fmaxf(fabsf(xv.x), fabsf(xv.y)), fmaxf(fabsf(xv.z), fabsf(xv.w)));
+        m = fmaxf(m, quad_xor1(m));
+        m = fmaxf(m, quad_xor2(m));
+        m = fmaxf(m, half_mirror(m));
+        int e = 0;
+        frexpf(m, &e);
+        const int sh = m > 0.f ? 22 - e : 0;  // |x| * 2^sh < 2^22
+        const int X0 = int(rintf(ldexpf(xv.x, sh))), X1 = int(rintf(ldexpf(xv.y, sh)));
+        const int X2 = int(rintf(ldexpf(xv.z, sh))), X3 = int(rintf(ldexpf(xv.w, sh)));
+        uint16_t* h16 = reinterpret_cast<uint16_t*>(xs + c * 28);
+        const int w = q >> 1, half = q & 1;
+#pragma unroll
+        for (int pl = 0; pl < 3; ++pl) {
+            const uint32_t sel = uint32_t(pl) | (uint32_t(4 + pl) << 8) | 0x0C0C0000u;
+            const uint32_t blo = __builtin_amdgcn_perm(uint32_t(X2), uint32_t(X0), sel);
+            const uint32_t bhi = __builtin_amdgcn_perm(uint32_t(X3), uint32_t(X1), sel);
+            h16[(pl * 8 + w) * 2 + half] = uint16_t(blo);
+            h16[(pl * 8 + 4 + w) * 2 + half] = uint16_t(bhi);
+        }
+        const float s1 = half_mirror(gsum);
+        if (q == 0) {
+            float* xm = xs + c * 28 + 24;
+            xm[0] = ldexpf(1.0f, -sh);
+            xm[1] = gsum;
+            xm[2] = s1;
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    const uint32_t gw[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};  // (u'0, u'1, m0, m1) per chunk
+    float pacc = 0.f, macc = 0.f;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+        if (t + D < 8) ch[t + D] = ld_stream(cp + (t + D) * 64);
+        __builtin_amdgcn_sched_barrier(0);
+        // Keeps each step's LDS reads and arithmetic in its step: without it
+        // the compiler hoists later steps' x reads and spills.
+        asm volatile("" ::: "memory");
+        const uint4* xq = reinterpret_cast<const uint4*>(xs + t * 28);
+        uint32_t xi[24];
+#pragma unroll
+        for (int k = 0; k < 6; ++k) {
+            const uint4 tq = xq[k];
+            xi[4 * k] = tq.x;
+            xi[4 * k + 1] = tq.y;
+            xi[4 * k + 2] = tq.z;
+            xi[4 * k + 3] = tq.w;
+        }
+        const float4 xm = reinterpret_cast<const float4*>(xq)[6];
+        const uint32_t wd[4] = {ch[t].x, ch[t].y, ch[t].z, ch[t].w};
+        int A[2][3] = {{0, 0, 0}, {0, 0, 0}};
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const int gi = w >> 1;
+            const uint32_t lo = wd[w] & 0x0F0F0F0Fu, hi = (wd[w] >> 4) & 0x0F0F0F0Fu;
+            A[gi][0] = int(__builtin_amdgcn_udot4(lo, xi[w], uint32_t(A[gi][0]), false));
+            A[gi][0] = int(__builtin_amdgcn_udot4(hi, xi[4 + w], uint32_t(A[gi][0]), false));
+            A[gi][1] = int(__builtin_amdgcn_udot4(lo, xi[8 + w], uint32_t(A[gi][1]), false));
+            A[gi][1] = int(__builtin_amdgcn_udot4(hi, xi[12 + w], uint32_t(A[gi][1]), false));
+            A[gi][2] = __builtin_amdgcn_sdot4(int(lo), int(xi[16 + w]), A[gi][2], false);
+            A[gi][2] = __builtin_amdgcn_sdot4(int(hi), int(xi[20 + w]), A[gi][2], false);
+        }
+        const int T0 = A[0][0] + (A[0][1] << 8) + (A[0][2] << 16);
+        const int T1 = A[1][0] + (A[1][1] << 8) + (A[1][2] << 16);
+        const uint32_t g = gw[t];
+        const float P = fmaf(ub1(g), float(T1), ub0(g) * float(T0));
+        pacc = fmaf(P, xm.x, pacc);
+        // A NaN or infinite x reaches the row through these float group sums
+        // (the fixed-point planes would turn it into a finite value).
+        const uint32_t gx = g ^ 0x80800000u;  // bytes 2, 3: m + 128 as unsigned
+        macc = fmaf(ub2(gx), xm.y, macc);
+        macc = fmaf(ub3(gx), xm.z, macc);
+        asm volatile("" : "+v"(pacc), "+v"(macc));
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    // w = dmin*m/127 + (d*u/255)*q  (quant/kquant.go:178-188)
+    float acc = fmaf(dd.x * (1.0f / 255.0f), pacc, (dd.y * (1.0f / 127.0f)) * fmaf(-128.0f, xtot, macc));
+    if (!act) acc = 0.f;
+    part[wave * 64 + lane] = acc;
+    __syncthreads();
+    if (wave != 0) return;
+    float sum = 0.f;
+    for (int w = 0; w < W; ++w) sum += part[w * 64 + lane];
+    const int row = rg * 64 + lane;
+    if (a.ksplit == 1) {
+        finish_rows(a, y, b, row, true, lane, sum);
+        return;
+    }
+    const int64_t rows_pad = int64_t(a.rg_count) * 64;
+    a.partial[(int64_t(b) * a.ksplit + ks) * rows_pad + row] = sum;
+}
+
 // Tail of a K-split forward launch: one wave per (64-row group, batch row)
 // adds the ksplit partials in split order (8 loads issued before each group
 // of adds) and applies the launch's epilogue. A last-arriving-block tail in
@@ -988,6 +1161,14 @@ int launch_rpl_t(const DevBlob& bl, const float* x, float* y, int batch, hipStre
         const int64_t ystride = mode == RPL_SWIGLU ? a.rows / 2 : a.rows;
         const float* xb = x + int64_t(b0) * a.nsb * 256;
         float* yb = y + int64_t(b0) * ystride;
+        if constexpr (std::is_same<P, RplQ4KI>::value) {
+            if (p.L == 1 && p.S == 1 && a.cs_si == 8 && a.cs_j == 1) {  // Q4_K's super-block-major image
+                hipLaunchKernelGGL(k_gemv_q4k, grid, dim3(unsigned(64 * p.W)), lds, s, ab, xb, yb);
+                if (p.ksplit > 1)
+                    hipLaunchKernelGGL(k_rpl_ksum, dim3(unsigned(a.rg_count), unsigned(nb)), dim3(64), 0, s, ab, yb);
+                continue;
+            }
+        }
         switch (p.L * 8 + p.S) {
         case 9: launch_rpl_ls<P, 1, 1>(ab, p, grid, lds, s, xb, yb); break;
         case 10: launch_rpl_ls<P, 1, 2>(ab, p, grid, lds, s, xb, yb); break;
