@@ -48,6 +48,21 @@ template <> struct Narrow<FMT_NATIVE_BINARY> {  // bit set -> +1, clear -> -1: 2
     static constexpr uint32_t XR = 0u, MASK = 0x01010101u;
 };
 
+// Unsigned B-bit code of flat element i in the device word order of the
+// narrow codes (narrow_permute_words, runtime.hip): word i / E (E = 32/B)
+// holds its element j = 4k + b at bits 8b + B*k, i.e. in byte
+// 4*(i / E) + (j & 3) at bit B*(j >> 2). Int8 bytes are in element order.
+template <int B>
+__device__ __forceinline__ uint32_t ncode(const uint8_t* codes, int64_t i) {
+    if constexpr (B == 8) {
+        return codes[i];
+    } else {
+        constexpr int E = 32 / B;
+        const int j = int(i % E);
+        return (uint32_t(codes[(i / E) * 4 + (j & 3)]) >> (B * (j >> 2))) & ((1u << B) - 1u);
+    }
+}
+
 // int8 value of flat element i (expandNarrowToI8).
 template <int F>
 __device__ __forceinline__ int narrow_i8(const uint8_t* codes, int64_t i) {
@@ -55,10 +70,15 @@ __device__ __forceinline__ int narrow_i8(const uint8_t* codes, int64_t i) {
     if constexpr (N::B == 8) {
         return int(int8_t(codes[i]));
     } else {
-        const int per = 8 / N::B;
-        const uint32_t u = (uint32_t(codes[i / per]) >> (N::B * int(i % per))) & ((1u << N::B) - 1u);
-        return N::MUL * int(u ^ (N::XR & ((1u << N::B) - 1u))) - N::OFF;
+        return N::MUL * int(ncode<N::B>(codes, i) ^ (N::XR & ((1u << N::B) - 1u))) - N::OFF;
     }
+}
+
+// Four quantized activations (each in [-128, 127]) as the bytes of one dword.
+__device__ __forceinline__ uint32_t pack_i8x4(int q0, int q1, int q2, int q3) {
+    const uint32_t lo = __builtin_amdgcn_perm(uint32_t(q1), uint32_t(q0), 0x0C0C0400u);  // q0.b0, q1.b0
+    const uint32_t hi = __builtin_amdgcn_perm(uint32_t(q3), uint32_t(q2), 0x0C0C0400u);
+    return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
 }
 
 // quantizeActsI8's q = round-half-away(f32(x / act)) clamped to [-128, 127].
@@ -102,10 +122,11 @@ __device__ __forceinline__ int quant_act(float x, float act, float inv, float th
 //    codes' arrival;
 //  * absmax over x, act = max/127 (1 if 0), q as quant_act;
 //  * xq goes to LDS laid out for the dot: code vector c holds E = 32/B codes
-//    per dword; dword d, shifted by k*B (k < KS = 8/B) and masked, offers in
-//    byte b the code of element c*(128/B) + d*E + KS*b + k, so LDS dword
-//    (d*nU + c)*KS + k holds those four xq bytes. Lane c reads its KS dwords
-//    per d once for all its rows;
+//    per dword; in the device word order dword d, shifted by k*B (k < KS =
+//    8/B) and masked, offers in byte b the code of element c*(128/B) + d*E +
+//    4k + b, so LDS dword (d*nU + c)*KS + k holds those four xq bytes: the
+//    quantized float4 of x that starts at that element, one whole-dword store
+//    per float4. Lane c reads its KS dwords per d once for all its rows;
 //  * acc = MUL * sum u*xq - OFF * sum xq on v_dot4_i32_i8: exact.
 template <int F, int NC, int NX, int RW>
 __global__ void __launch_bounds__(1024) k_narrow_i8v(const uint8_t* __restrict__ codes, float scale, int rows, int K,
@@ -170,18 +191,13 @@ __global__ void __launch_bounds__(1024) k_narrow_i8v(const uint8_t* __restrict__
             }
         }
     }
-    uint8_t* l8 = reinterpret_cast<uint8_t*>(lds);
 #pragma unroll
     for (int n = 0; n < NX; ++n) {
         const int i = tid + nt * n;
         if (i >= k4) continue;
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const int q = quant_clamp(rq[n][t]);
-            const int e = 4 * i + t;
-            const int c = e / EU, r = e % EU, d = r / E, r2 = r % E, bb = r2 / KS, k = r2 % KS;
-            l8[4 * ((d * nU + c) * KS + k) + bb] = uint8_t(int8_t(q));
-        }
+        const int e = 4 * i, c = e / EU, r = e % EU, d = r / E, k = (r % E) >> 2;
+        lds[(d * nU + c) * KS + k] = pack_i8x4(quant_clamp(rq[n][0]), quant_clamp(rq[n][1]), quant_clamp(rq[n][2]),
+                                               quant_clamp(rq[n][3]));
     }
     __syncthreads();
     if (act_out && blockIdx.x == 0 && tid == 0) act_out[b] = act;
@@ -290,17 +306,13 @@ __global__ void __launch_bounds__(1024) k_narrow_i8l(const uint8_t* __restrict__
             }
         }
     }
-    uint8_t* l8 = reinterpret_cast<uint8_t*>(lds);
 #pragma unroll
     for (int n = 0; n < NX; ++n) {
         const int i = tid + nt * n;
         if (i >= k4) continue;
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const int e = 4 * i + t;
-            const int c = e / EU, rr = e % EU, d = rr / E, r2 = rr % E, bb = r2 / KS, k = r2 % KS;
-            l8[4 * ((d * nU + c) * KS + k) + bb] = uint8_t(int8_t(quant_clamp(rq[n][t])));
-        }
+        const int e = 4 * i, c = e / EU, rr = e % EU, d = rr / E, k = (rr % E) >> 2;
+        lds[(d * nU + c) * KS + k] = pack_i8x4(quant_clamp(rq[n][0]), quant_clamp(rq[n][1]), quant_clamp(rq[n][2]),
+                                               quant_clamp(rq[n][3]));
     }
     __syncthreads();
     if (act_out && blockIdx.x == 0 && tid == 0) act_out[b] = act;
@@ -380,10 +392,10 @@ __device__ __forceinline__ float store_w(const uint8_t* codes, int64_t i, float 
     if constexpr (F == FMT_NONE) {
         return reinterpret_cast<const float*>(codes)[i];
     } else if constexpr (F == FMT_NATIVE_TERNARY) {
-        const uint32_t u = (uint32_t(codes[i >> 2]) >> (2 * int(i & 3))) & 3u;
+        const uint32_t u = ncode<2>(codes, i);
         return u == 0 ? -scale : (u == 2 ? scale : 0.0f);
     } else if constexpr (F == FMT_NATIVE_BINARY) {
-        return (codes[i >> 3] >> int(i & 7)) & 1 ? scale : -scale;
+        return ncode<1>(codes, i) ? scale : -scale;
     } else {
         return float(narrow_i8<F>(codes, i)) * scale;
     }

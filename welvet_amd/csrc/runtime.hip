@@ -246,6 +246,24 @@ struct Staging {
 
 inline float f32_at(const uint8_t* p) { float v; std::memcpy(&v, p, 4); return v; }
 
+// Device order of the narrow DTypes' codes (LAYOUT_NARROW). The Store packs
+// B-bit codes LSB-first, so a 32-bit word holds its E = 32/B elements j at
+// bits B*j. The device word holds element j = 4k + b at bits 8b + B*k
+// (k < 8/B, b < 4): then (w >> B*k) & mask gives, in byte b, the code of
+// element 4k + b, so four consecutive elements meet four consecutive int8
+// activations in one v_dot4 (native.hip). Int8 (B = 8) is unchanged.
+void narrow_permute_words(uint8_t* p, size_t n, int B) {
+    if (B >= 8) return;
+    const int E = 32 / B;
+    const uint32_t m = (1u << B) - 1u;
+    for (size_t off = 0; off < n; off += 4) {
+        uint32_t w = 0, o = 0;
+        std::memcpy(&w, p + off, std::min<size_t>(4, n - off));  // the tail word's missing bytes read as 0
+        for (int j = 0; j < E; ++j) o |= ((w >> (B * j)) & m) << (8 * (j & 3) + B * (j >> 2));
+        std::memcpy(p + off, &o, 4);
+    }
+}
+
 // Host staging of a device image: byte buffer with 256-B aligned sections.
 struct Image {
     std::vector<uint8_t> bytes;
@@ -775,8 +793,11 @@ int wv_blob_upload_flags(int format, int64_t rows, int64_t cols, int32_t block_w
         b.layout = format == FMT_NONE ? LAYOUT_F32 : LAYOUT_NARROW;
         if (b.layout == LAYOUT_NARROW && cols > 32768)
             return fail(WV_E_SHAPE, "wv_blob_upload: %s cols %lld > 32768", fmt_name(format), (long long)cols);
-        o_codes = img.add(size_t(need));
+        // Whole 32-bit words plus 16 bytes, so that word and vector reads of
+        // the last codes stay inside the section.
+        o_codes = img.add((size_t(need) + 3) / 4 * 4 + 16);
         std::memcpy(img.bytes.data() + o_codes, raw, size_t(need));
+        if (b.layout == LAYOUT_NARROW) narrow_permute_words(img.bytes.data() + o_codes, size_t(need), narrow_bits(format));
     } else if (!raw_only &&
                (format == FMT_Q2_K || format == FMT_Q3_K || format == FMT_Q4_K || format == FMT_Q5_K ||
                 format == FMT_Q6_K || format == FMT_Q8_0 || format == FMT_Q4_0 || format == FMT_Q4_1 ||

@@ -137,7 +137,8 @@ bool pack_native(int fmt, const float* w, int64_t n, uint8_t* codes, float* scal
 enum Layout : int {
     LAYOUT_RAW = 0,        // uploaded bytes verbatim; decoded per element (any shape / format)
     LAYOUT_RPL = 1,        // Q4_K/Q6_K/Q8_0/Q4_0 with cols % 256 == 0: row-interleaved planes (gemv_rpl.hip)
-    LAYOUT_NARROW = 4,     // weights.Store Int8/Int4/Int2/Ternary/Binary codes (as uploaded) + Store.Scale
+    LAYOUT_NARROW = 4,     // weights.Store Int8/Int4/Int2/Ternary/Binary codes, bits permuted per word
+                           // (narrow_permute_words, runtime.hip) + Store.Scale
     LAYOUT_F32 = 5,        // FormatNone f32 weights, row-major (quant/none.go, Store FormatNone+Float32)
 };
 
