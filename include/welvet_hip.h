@@ -341,6 +341,23 @@ int wv_decoder_use_graph(uint64_t decoder, int32_t enable);
 int wv_decoder_generate(uint64_t decoder, int32_t token, int32_t pos, int32_t n_steps, int32_t advance_pos,
                         int32_t *tokens_out, float *last_logits);
 
+/* ForwardTokens over a prompt (model/transformer/forward.go:26-90 with the
+ * whole token block, as mha.Forward runs it with its KV cache,
+ * layers/mha/cpu.go:163-215): the n_tokens ids (host) at positions
+ * pos0 .. pos0+n_tokens-1 go through every layer as one block: RMSNorm of each
+ * row, Q/K/V of the block (the batched prefill GEMM where the blob has one,
+ * fp16 MFMA within 2e-3; the batched GEMVs otherwise), RoPE and the K/V rows
+ * appended to the cache at their positions, causal GQA attention of each row
+ * over the cache up to its own position (layers/mha/attn.go:40-118), O +
+ * residual, RMSNorm, SwiGLU + residual; then the final norm, LM head and
+ * argmax of the last row. *next_token (may be NULL) receives that argmax and
+ * last_logits (host, vocab floats, may be NULL) the last row's logits.
+ * wv_decoder_generate(*next_token, pos0 + n_tokens, ...) then continues the
+ * sequence with no host copy of the cache. Errors: WV_E_ARG "empty ids",
+ * WV_E_SHAPE when pos0 + n_tokens exceeds max_seq. Synchronous. */
+int wv_decoder_prefill(uint64_t decoder, const int32_t *tokens, int32_t n_tokens, int32_t pos0,
+                       int32_t *next_token, float *last_logits);
+
 /* Releases the decoder (not the blobs it references). */
 int wv_decoder_free(uint64_t decoder);
 

@@ -100,6 +100,18 @@ class DecodeRef:
         self.kc[layer][first_pos:first_pos + n] = np.asarray(k, np.float64).reshape(n, -1)
         self.vc[layer][first_pos:first_pos + n] = np.asarray(v, np.float64).reshape(n, -1)
 
+    def prefill(self, tokens, pos0: int = 0):
+        """ForwardTokens over a prompt block (forward.go:26-90 with seqLen =
+        len(tokens)): every op is row-wise except attention, whose causal mask
+        (layers/mha/attn.go:52-56, kPos <= qPos) limits row s to the cache rows
+        up to its own position, which hold exactly the K and V of the rows
+        before it (layers/mha/cpu.go:178-193). So the block equals these
+        per-position steps; returns the last row's (f32 logits, argmax)."""
+        out = None
+        for i, t in enumerate(tokens):
+            out = self.step(int(t), pos0 + i)
+        return out
+
     def step(self, token: int, pos: int):
         """One decode step; returns (f32 logits, argmax token)."""
         c = self.cfg

@@ -43,7 +43,7 @@ EXPORTS = (
     "wv_native_acc_dev", "wv_store_matvec", "wv_matvec_t", "wv_matvec_t_dev", "wv_quant_matvec_t",
     "wv_store_matvec_t", "wv_matmul", "wv_matmul_dev", "wv_sync",
     "wv_decoder_create", "wv_decoder_set_layer", "wv_decoder_set_output", "wv_decoder_set_kv",
-    "wv_decoder_use_graph", "wv_decoder_generate", "wv_decoder_free",
+    "wv_decoder_use_graph", "wv_decoder_generate", "wv_decoder_prefill", "wv_decoder_free",
 )
 
 
@@ -105,6 +105,7 @@ def lib():
     L.wv_decoder_use_graph.argtypes = [ctypes.c_uint64, ctypes.c_int32]
     L.wv_decoder_generate.argtypes = [ctypes.c_uint64, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
                                       _P, _P]
+    L.wv_decoder_prefill.argtypes = [ctypes.c_uint64, _P, ctypes.c_int32, ctypes.c_int32, _P, _P]
     L.wv_decoder_free.argtypes = [ctypes.c_uint64]
     _lib = L
     return L

@@ -62,6 +62,8 @@ __global__ void __launch_bounds__(256) k_embed(const float* __restrict__ table, 
 __global__ void __launch_bounds__(1024) k_rmsnorm(const float* __restrict__ x, const float* __restrict__ gamma,
                                                   float* __restrict__ y, int dim, double eps) {
     __shared__ double part[16];
+    x += int64_t(blockIdx.x) * dim;  // one row per block (the prompt forward normalizes n rows)
+    y += int64_t(blockIdx.x) * dim;
     constexpr int R = 4;
     const int n4 = dim / 4;
     float4 xv[R];
@@ -746,6 +748,149 @@ __global__ void __launch_bounds__(1024) k_argmax_advance(const float* __restrict
 }
 
 // ---------------------------------------------------------------------------
+// Prompt (multi-token) forward: ForwardTokens over a block of n tokens
+// ---------------------------------------------------------------------------
+
+// H[s] = table[tok[s]] for the n prompt rows (token ids clamped as k_embed does).
+__global__ void __launch_bounds__(256) k_embed_rows(const float* __restrict__ table, const int32_t* __restrict__ tok,
+                                                    float* __restrict__ h, int hidden, int vocab) {
+    const int s = blockIdx.y;
+    const int t = min(max(tok[s], 0), vocab - 1);
+    for (int i = blockIdx.x * 256 + threadIdx.x; i < hidden; i += gridDim.x * 256)
+        h[int64_t(s) * hidden + i] = table[int64_t(t) * hidden + i];
+}
+
+// RoPE and the KV append for prompt row s at position pos0 + s
+// (layers/mha/cpu.go:178-193, rope.go:6-21): the row's q heads are rotated in
+// place, its k heads rotated and, with its v heads, written to the caches at
+// that position. Angles and the rotation in f64 as in k_embed / k_attn_reg:
+// angle_d = pos / theta^(2d/hd), (x0, x1) -> (x0 cos - x1 sin, x0 sin + x1 cos).
+__global__ void __launch_bounds__(256) k_rope_kv_rows(float* __restrict__ q, const float* __restrict__ k,
+                                                      const float* __restrict__ v, float* __restrict__ kc,
+                                                      float* __restrict__ vc, const double* __restrict__ freq_div,
+                                                      int n_heads, int n_kv, int hd, int max_seq, int pos0) {
+    const int s = blockIdx.x, half = hd / 2, pos = pos0 + s;
+    const int qd = n_heads * hd, kvd = n_kv * hd;
+    float* qr = q + int64_t(s) * qd;
+    const float* kr = k + int64_t(s) * kvd;
+    const float* vr = v + int64_t(s) * kvd;
+    for (int i = threadIdx.x; i < (n_heads + n_kv) * half; i += 256) {
+        const int hh = i / half, d = i % half;
+        const double angle = double(pos) / freq_div[d];
+        const double c = cos(angle), sn = sin(angle);
+        if (hh < n_heads) {
+            const double x0 = qr[hh * hd + d], x1 = qr[hh * hd + d + half];
+            qr[hh * hd + d] = float(x0 * c - x1 * sn);
+            qr[hh * hd + d + half] = float(x0 * sn + x1 * c);
+        } else {
+            const int g = hh - n_heads;
+            const double x0 = kr[g * hd + d], x1 = kr[g * hd + d + half];
+            float* crow = kc + (int64_t(g) * max_seq + pos) * hd;
+            crow[d] = float(x0 * c - x1 * sn);
+            crow[d + half] = float(x0 * sn + x1 * c);
+        }
+    }
+    for (int i = threadIdx.x; i < kvd; i += 256) {
+        const int g = i / hd, d = i % hd;
+        vc[(int64_t(g) * max_seq + pos) * hd + d] = vr[i];
+    }
+}
+
+// Causal GQA attention for prompt row s (position pos0 + s) over the cache,
+// which already holds the K and V rows of every prompt position
+// (layers/mha/attn.go:40-118 with the causal mask kPos <= qPos): block (kvh, s)
+// serves the G = n_heads / n_kv query heads of KV head kvh. Keys go in chunks
+// of 64 with an online softmax in f32: scores q.k * scale, the running max
+// and sum per head, the output rescaled when the max grows; out = sum p v / sum p.
+template <int HD>
+__global__ void __launch_bounds__(256) k_attn_prefill(const float* __restrict__ q, const float* __restrict__ kc,
+                                                      const float* __restrict__ vc, float* __restrict__ out,
+                                                      int n_heads, int n_kv, int max_seq, int pos0, float scale) {
+    constexpr int CH = 64, GM = 8, PG = 256 / HD;  // PG: heads a thread's output dim serves per pass
+    __shared__ __attribute__((aligned(16))) float qs[GM * HD];
+    __shared__ float ps[GM][CH];
+    __shared__ float alpha_s[GM], l_s[GM];
+    const int G = n_heads / n_kv;
+    const int kvh = blockIdx.x, s = blockIdx.y, t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int qd = n_heads * HD;
+    const int kv_len = pos0 + s + 1;
+    for (int i = t; i < G * HD; i += 256) qs[i] = q[int64_t(s) * qd + int64_t(kvh) * G * HD + i];
+    const float* kb = kc + int64_t(kvh) * max_seq * HD;
+    const float* vb = vc + int64_t(kvh) * max_seq * HD;
+    float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};  // heads wave and wave + 4
+    float acc[GM / PG];
+#pragma unroll
+    for (int i = 0; i < GM / PG; ++i) acc[i] = 0.f;
+    const int d = t % HD;
+    __syncthreads();
+    for (int c0 = 0; c0 < kv_len; c0 += CH) {
+        // scores of (head g, key c0 + j)
+        for (int i = t; i < G * CH; i += 256) {
+            const int g = i / CH, j = i % CH, key = c0 + j;
+            float sc = -INFINITY;
+            if (key < kv_len) {
+                const float4* kr = reinterpret_cast<const float4*>(kb + int64_t(key) * HD);
+                const float4* qv = reinterpret_cast<const float4*>(qs + g * HD);
+                float a = 0.f;
+#pragma unroll 8
+                for (int e = 0; e < HD / 4; ++e) {
+                    const float4 kk = kr[e], qq = qv[e];
+                    a = fmaf(qq.x, kk.x, a);
+                    a = fmaf(qq.y, kk.y, a);
+                    a = fmaf(qq.z, kk.z, a);
+                    a = fmaf(qq.w, kk.w, a);
+                }
+                sc = a * scale;
+            }
+            ps[g][j] = sc;
+        }
+        __syncthreads();
+        // online softmax: wave w owns heads w and w + 4
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            const int g = wave + 4 * r;
+            if (g < G) {
+                const float sv = ps[g][lane];
+                const float m_new = fmaxf(m_run[r], wave_maximum(sv));
+                const float p = sv == -INFINITY ? 0.f : expf(sv - m_new);
+                const float alpha = m_run[r] == -INFINITY ? 0.f : expf(m_run[r] - m_new);
+                l_run[r] = l_run[r] * alpha + wave_total(p);
+                m_run[r] = m_new;
+                ps[g][lane] = p;
+                if (lane == 0) alpha_s[g] = alpha;
+            }
+        }
+        __syncthreads();
+        // acc[g] = acc[g] * alpha_g + sum_j p[g][j] v[c0 + j][d]
+        const int nj = min(CH, kv_len - c0);
+#pragma unroll
+        for (int i = 0; i < GM / PG; ++i) {
+            const int g = t / HD + PG * i;
+            if (g < G) acc[i] *= alpha_s[g];
+        }
+        for (int j = 0; j < nj; ++j) {
+            const float vv = vb[int64_t(c0 + j) * HD + d];
+#pragma unroll
+            for (int i = 0; i < GM / PG; ++i) {
+                const int g = t / HD + PG * i;
+                if (g < G) acc[i] = fmaf(ps[g][j], vv, acc[i]);
+            }
+        }
+        __syncthreads();
+    }
+    if (lane == 0) {
+        if (wave < G) l_s[wave] = l_run[0];
+        if (wave + 4 < G) l_s[wave + 4] = l_run[1];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < GM / PG; ++i) {
+        const int g = t / HD + PG * i;
+        if (g < G) out[int64_t(s) * qd + (int64_t(kvh) * G + g) * HD + d] = acc[i] / l_s[g];
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Decoder object
 // ---------------------------------------------------------------------------
 
@@ -793,6 +938,12 @@ struct Decoder {
     int graph_advance = -1;
     hipGraphExec_t exec = nullptr;
     hipGraph_t graph = nullptr;
+    // prompt forward (wv_decoder_prefill): rows of every prompt token, grown on demand
+    int pcap = 0;
+    float *ph = nullptr, *pn = nullptr, *pq = nullptr, *pk = nullptr, *pv = nullptr, *patt = nullptr;
+    float *pg = nullptr, *pu = nullptr, *pt = nullptr, *pscratch = nullptr;
+    int32_t* ptok = nullptr;
+    size_t pscratch_floats = 0;
 };
 
 std::mutex g_dmu;
@@ -825,8 +976,21 @@ void drop_graph(Decoder& d) {
     d.graph = nullptr;
 }
 
+void drop_prefill(Decoder& d) {
+    for (void* p : {static_cast<void*>(d.ph), static_cast<void*>(d.pn), static_cast<void*>(d.pq),
+                    static_cast<void*>(d.pk), static_cast<void*>(d.pv), static_cast<void*>(d.patt),
+                    static_cast<void*>(d.pg), static_cast<void*>(d.pu), static_cast<void*>(d.pt),
+                    static_cast<void*>(d.pscratch), static_cast<void*>(d.ptok)})
+        if (p) (void)hipFree(p);
+    d.ph = d.pn = d.pq = d.pk = d.pv = d.patt = d.pg = d.pu = d.pt = d.pscratch = nullptr;
+    d.ptok = nullptr;
+    d.pcap = 0;
+    d.pscratch_floats = 0;
+}
+
 void release(Decoder* d) {
     drop_graph(*d);
+    drop_prefill(*d);
     if (d->gemv_scratch) (void)hipFree(d->gemv_scratch);
     for (Layer& ly : d->layers) drop_fused(ly);
     for (void* p : d->allocs) (void)hipFree(p);
@@ -1012,6 +1176,107 @@ int ready(Decoder& d) {
         d.gemv_scratch_floats = need;
     }
     return WV_OK;
+}
+
+// One projection of a prompt block: the prefill GEMM where the blob has one,
+// the batched GEMVs otherwise.
+int prefill_proj(Decoder& d, const DevBlob& w, const float* x, float* y, int n) {
+    if (gemm_supported(w, n)) return launch_gemm(w, x, y, n, d.stream, d.pscratch);
+    return launch_matvec(w, x, y, n, d.stream, d.pscratch);
+}
+
+size_t prefill_proj_scratch(const DevBlob& w, int n) {
+    return gemm_supported(w, n) ? gemm_scratch_floats(w, n) : matvec_scratch_floats(w, n);
+}
+
+int ensure_prefill(Decoder& d, int n) {
+    const wv_decoder_config& c = d.c;
+    size_t need_s = 0;
+    for (const Layer& ly : d.layers)
+        for (const DevBlob& w : ly.w) need_s = std::max(need_s, prefill_proj_scratch(w, n));
+    if (n <= d.pcap && need_s <= d.pscratch_floats) return WV_OK;
+    drop_prefill(d);
+    const size_t qd = size_t(c.n_heads) * c.head_dim, kvd = size_t(c.n_kv_heads) * c.head_dim;
+    const size_t wide = std::max({size_t(c.hidden), size_t(c.ffn), qd});
+    struct {
+        void** p;
+        size_t bytes;
+    } bufs[] = {{reinterpret_cast<void**>(&d.ph), n * size_t(c.hidden) * 4},
+                {reinterpret_cast<void**>(&d.pn), n * size_t(c.hidden) * 4},
+                {reinterpret_cast<void**>(&d.pq), n * qd * 4},
+                {reinterpret_cast<void**>(&d.pk), n * kvd * 4},
+                {reinterpret_cast<void**>(&d.pv), n * kvd * 4},
+                {reinterpret_cast<void**>(&d.patt), n * qd * 4},
+                {reinterpret_cast<void**>(&d.pg), n * size_t(c.ffn) * 4},
+                {reinterpret_cast<void**>(&d.pu), n * size_t(c.ffn) * 4},
+                {reinterpret_cast<void**>(&d.pt), n * wide * 4},
+                {reinterpret_cast<void**>(&d.pscratch), std::max<size_t>(need_s, 1) * 4},
+                {reinterpret_cast<void**>(&d.ptok), size_t(n) * 4}};
+    for (auto& b : bufs) {
+        const hipError_t e = hipMalloc(b.p, std::max<size_t>(b.bytes, 256));
+        if (e != hipSuccess) {
+            *b.p = nullptr;
+            drop_prefill(d);
+            return rt_hip_fail(e, "wv_decoder_prefill: buffers");
+        }
+    }
+    d.pcap = n;
+    d.pscratch_floats = std::max<size_t>(need_s, 1);
+    return WV_OK;
+}
+
+// ForwardTokens over n prompt tokens at positions pos0 .. pos0+n-1
+// (model/transformer/forward.go:26-90 with the whole block): per layer
+// RMSNorm of every row, Q/K/V for the block, RoPE and the KV append, causal
+// attention, O + residual, RMSNorm, SwiGLU + residual; then the final norm,
+// LM head and argmax of the last row into the decoder state (state[2]).
+int enqueue_prefill(Decoder& d, int n, int pos0) {
+    const wv_decoder_config& c = d.c;
+    const int hd = c.head_dim, hidden = c.hidden;
+    const float scale = float(1.0 / std::sqrt(double(hd)));
+    const int64_t nh = int64_t(n) * hidden, nf = int64_t(n) * c.ffn;
+    auto blocks = [](int64_t m) { return dim3(unsigned((m + 255) / 256)); };
+    hipLaunchKernelGGL(k_embed_rows, dim3(unsigned((hidden + 255) / 256), unsigned(n)), dim3(256), 0, d.stream, d.embed,
+                       d.ptok, d.ph, hidden, c.vocab);
+    for (int L = 0; L < c.n_layers; ++L) {
+        Layer& ly = d.layers[L];
+        hipLaunchKernelGGL(k_rmsnorm, dim3(unsigned(n)), dim3(1024), 0, d.stream, d.ph, ly.attn_norm, d.pn, hidden, c.rms_eps);
+        int e = prefill_proj(d, ly.w[0], d.pn, d.pq, n);
+        if (!e) e = prefill_proj(d, ly.w[1], d.pn, d.pk, n);
+        if (!e) e = prefill_proj(d, ly.w[2], d.pn, d.pv, n);
+        if (e) return e;
+        hipLaunchKernelGGL(k_rope_kv_rows, dim3(unsigned(n)), dim3(256), 0, d.stream, d.pq, d.pk, d.pv, ly.kc, ly.vc,
+                           d.freq_div, c.n_heads, c.n_kv_heads, hd, c.max_seq, pos0);
+        const dim3 ag(unsigned(c.n_kv_heads), unsigned(n));
+        if (hd == 128)
+            hipLaunchKernelGGL(k_attn_prefill<128>, ag, dim3(256), 0, d.stream, d.pq, ly.kc, ly.vc, d.patt, c.n_heads,
+                               c.n_kv_heads, c.max_seq, pos0, scale);
+        else
+            hipLaunchKernelGGL(k_attn_prefill<64>, ag, dim3(256), 0, d.stream, d.pq, ly.kc, ly.vc, d.patt, c.n_heads,
+                               c.n_kv_heads, c.max_seq, pos0, scale);
+        e = prefill_proj(d, ly.w[3], d.patt, d.pt, n);
+        if (e) return e;
+        hipLaunchKernelGGL(k_add, blocks(nh), dim3(256), 0, d.stream, d.ph, d.pt, int(nh));
+        hipLaunchKernelGGL(k_rmsnorm, dim3(unsigned(n)), dim3(1024), 0, d.stream, d.ph, ly.ffn_norm, d.pn, hidden, c.rms_eps);
+        e = prefill_proj(d, ly.w[4], d.pn, d.pg, n);
+        if (!e) e = prefill_proj(d, ly.w[5], d.pn, d.pu, n);
+        if (e) return e;
+        hipLaunchKernelGGL(k_silu_mul, blocks(nf), dim3(256), 0, d.stream, d.pg, d.pu, d.pt, int(nf));
+        e = prefill_proj(d, ly.w[6], d.pt, d.pn, n);
+        if (e) return e;
+        hipLaunchKernelGGL(k_add, blocks(nh), dim3(256), 0, d.stream, d.ph, d.pn, int(nh));
+    }
+    const float* last = d.ph + int64_t(n - 1) * hidden;
+    const float* fin = last;
+    if (d.has_final_norm) {
+        hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(1024), 0, d.stream, last, d.final_norm, d.n, hidden, c.rms_eps);
+        fin = d.n;
+    }
+    const int e = proj(d, d.lm, fin, d.logits, RPL_STORE, nullptr, nullptr);
+    if (e) return e;
+    hipLaunchKernelGGL(k_argmax_advance, dim3(1), dim3(1024), 0, d.stream, d.logits, c.vocab, d.d_state, d.d_gen,
+                       c.max_seq, 0);
+    return int(hipGetLastError());
 }
 
 int run_steps(Decoder& d, int n_steps, int advance) {
@@ -1286,6 +1551,35 @@ int wv_decoder_generate(uint64_t dec, int32_t token, int32_t pos, int32_t n_step
     }
     e = hipStreamSynchronize(d->stream);
     if (e != hipSuccess) return rt_hip_fail(e, "wv_decoder_generate: sync");
+    return WV_OK;
+}
+
+int wv_decoder_prefill(uint64_t dec, const int32_t* tokens, int32_t n_tokens, int32_t pos0, int32_t* next_token,
+                       float* last_logits) {
+    Decoder* d = find(dec);
+    if (!d) return rt_fail(WV_E_HANDLE, "wv_decoder_prefill: unknown decoder %llu", (unsigned long long)dec);
+    const wv_decoder_config& c = d->c;
+    if (!tokens || n_tokens <= 0) return rt_fail(WV_E_ARG, "wv_decoder_prefill: empty ids");  // forward.go:35-37
+    if (pos0 < 0 || int64_t(pos0) + n_tokens > c.max_seq)
+        return rt_fail(WV_E_SHAPE, "wv_decoder_prefill: seq %d at position %d > MaxSeqLen %d", n_tokens, pos0, c.max_seq);
+    int rc = ready(*d);
+    if (rc) return rc;
+    (void)hipSetDevice(d->device);
+    rc = ensure_prefill(*d, n_tokens);
+    if (rc) return rc;
+    hipError_t e = hipMemcpyAsync(d->ptok, tokens, size_t(n_tokens) * 4, hipMemcpyHostToDevice, d->stream);
+    const int32_t init[4] = {pos0 + n_tokens - 1, 0, -1, 0};
+    if (e == hipSuccess) e = hipMemcpyAsync(d->d_state, init, sizeof init, hipMemcpyHostToDevice, d->stream);
+    if (e != hipSuccess) return rt_hip_fail(e, "wv_decoder_prefill: tokens");
+    const int k = enqueue_prefill(*d, n_tokens, pos0);
+    if (k) return rt_hip_fail(hipError_t(k), "wv_decoder_prefill: launch");
+    int32_t st[4] = {0, 0, 0, 0};
+    e = hipMemcpyAsync(st, d->d_state, sizeof st, hipMemcpyDeviceToHost, d->stream);
+    if (e == hipSuccess && last_logits)
+        e = hipMemcpyAsync(last_logits, d->logits, size_t(c.vocab) * 4, hipMemcpyDeviceToHost, d->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(d->stream);
+    if (e != hipSuccess) return rt_hip_fail(e, "wv_decoder_prefill: results");
+    if (next_token) *next_token = st[2];
     return WV_OK;
 }
 

@@ -1162,7 +1162,13 @@ int launch_rpl_t(const DevBlob& bl, const float* x, float* y, int batch, hipStre
         const float* xb = x + int64_t(b0) * a.nsb * 256;
         float* yb = y + int64_t(b0) * ystride;
         if constexpr (std::is_same<P, RplQ4KI>::value) {
-            if (p.L == 1 && p.S == 1 && a.cs_si == 8 && a.cs_j == 1) {  // Q4_K's super-block-major image
+            // k_gemv_q4k takes 68 VGPRs, so one 16-wave block per CU: it runs
+            // the grids that fit the GPU in one pass (the 4096->14336
+            // headline, 224 blocks). Larger grids (the decoder's gate||up,
+            // 448 blocks, and LM head, 500) keep the 64-VGPR policy kernel,
+            // two blocks per CU.
+            constexpr int64_t kCUs = 256;  // MI355X
+            if (p.L == 1 && p.S == 1 && a.cs_si == 8 && a.cs_j == 1 && int64_t(grid.x) * grid.y * grid.z <= kCUs) {
                 hipLaunchKernelGGL(k_gemv_q4k, grid, dim3(unsigned(64 * p.W)), lds, s, ab, xb, yb);
                 if (p.ksplit > 1)
                     hipLaunchKernelGGL(k_rpl_ksum, dim3(unsigned(a.rg_count), unsigned(nb)), dim3(64), 0, s, ab, yb);

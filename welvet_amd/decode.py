@@ -89,6 +89,16 @@ class Decoder:
                                         None if logits is None else logits.ctypes.data))
         return (toks[:n_steps], logits) if want_logits else toks[:n_steps]
 
+    def prefill(self, tokens, pos0: int = 0, want_logits: bool = False):
+        """ForwardTokens over a prompt block at positions pos0.. (wv_decoder_prefill):
+        fills the KV caches on the device and returns the last row's argmax (and logits)."""
+        ids = np.ascontiguousarray(tokens, np.int32).reshape(-1)
+        nxt = ctypes.c_int32()
+        logits = np.zeros(self.cfg.vocab, np.float32) if want_logits else None
+        check(lib().wv_decoder_prefill(self.handle, ids.ctypes.data if ids.size else None, ids.size, pos0,
+                                       ctypes.byref(nxt), None if logits is None else logits.ctypes.data))
+        return (nxt.value, logits) if want_logits else nxt.value
+
     def free(self) -> None:
         if self.handle:
             check(lib().wv_decoder_free(self.handle))
