@@ -79,6 +79,10 @@ MATVECT = {
     f"{f.lower()}_t_{i}x{o}": (f, o, i, f"{f} MatVecT of the {i}->{o} weight (gx[{i}] += W^T gy[{o}]) b=1")
     for f in ("Q4_K", "Q6_K", "Q8_0", "Q5_K", "Q3_K", "Q2_K", "Q4_1", "IQ4_NL") for (i, o) in ((4096, 14336), (14336, 4096))
 }
+# Streaming-read probe (libwv_probe.so): one launch reads MB bytes, one 16 B
+# non-temporal load per thread; the 38.5 MB case is the headline GEMV's
+# packed bytes, so it gives the single-launch read ceiling of that size.
+PROBE = {f"stream_read_{n}": b for n, b in (("38m", 38535168), ("11m", 11010048), ("77m", 77070336))}
 MFMA_F16_PEAK_TFLOPS = 2500.0
 # 32-layer decoder, hidden 4096, 32/8 heads x 128, SwiGLU 14336, vocab 32000, Q4_K, KV 2048
 DECODE = {
@@ -222,7 +226,7 @@ def main():
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--workload", default="q4k_4096x14336",
-                    choices=sorted(WORKLOADS) + sorted(PREFILL) + sorted(MATVECT) + sorted(DECODE))
+                    choices=sorted(WORKLOADS) + sorted(PREFILL) + sorted(MATVECT) + sorted(DECODE) + sorted(PROBE))
     ap.add_argument("--cpu-budget-s", type=float, default=10.0)
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -248,6 +252,8 @@ def main():
     import torch
     import welvet_amd as wv
 
+    if args.workload in PROBE:
+        return probe_main(args, torch)
     if args.workload in PREFILL:
         return prefill_main(args, torch, wv)
     if args.workload in MATVECT:
@@ -478,6 +484,49 @@ def prefill_main(args, torch, wv):
     for b in blobs:
         b.free()
     print(json.dumps(result), flush=True)
+
+
+def probe_main(args, torch):
+    """--workload stream_read_*: the read ceiling of one launch of that many
+    bytes, timed like the GEMV (HIP events around K back-to-back launches on
+    one stream, buffers rotated past the 256 MB Infinity Cache)."""
+    import ctypes
+    nbytes = PROBE[args.workload]
+    lib = ctypes.CDLL(os.path.join(ROOT, "welvet_amd", "libwv_probe.so"))
+    lib.wv_probe_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_void_p]
+    copies = max(8, math.ceil(1.25 * MALL_BYTES / nbytes))
+    bufs = [torch.zeros(nbytes, dtype=torch.uint8, device="cuda") for _ in range(copies)]
+    sink = torch.zeros(4, dtype=torch.int32, device="cuda")
+    stream = torch.cuda.Stream()
+    sh = stream.cuda_stream
+    ptrs = [b.data_ptr() for b in bufs]
+    torch.cuda.synchronize()
+
+    def run(n, first=0):
+        rc = 0
+        for i in range(n):
+            rc |= lib.wv_probe_stream_read(ptrs[(first + i) % copies], nbytes, sink.data_ptr(), sh)
+        assert rc == 0, "probe launch failed"
+
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        run(args.warmup)
+        e0.record(stream)
+        run(args.steps, args.warmup)
+        e1.record(stream)
+    e1.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    value = nbytes / (ms * 1e-3) / 1e9
+    print(json.dumps({
+        "metric": "streaming-read GB/s of one launch (probe)", "value": round(value, 2), "unit": "GB/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 6),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "u8", "data": "zeros",
+        "config": {"workload": f"read {nbytes} B per launch, one 16 B non-temporal load per thread, "
+                               f"{nbytes // 4096} blocks x 256", "buffers_rotated": copies},
+        "roofline": {"bound": "hbm", "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(value / HBM_PEAK_GBS, 4), "traffic": None,
+                     "event_us_per_launch": round(ms * 1e3, 3)},
+    }), flush=True)
 
 
 def copy_probe(args, torch, result):
