@@ -89,6 +89,12 @@ DECODE = {
     "decode_32l": dict(n_layers=32, hidden=4096, n_heads=32, n_kv_heads=8, head_dim=128, ffn=14336, vocab=32000,
                        kv=2048, distinct_layers=4),
 }
+# HBM bytes per decode token: the sum over one token's launches of
+# 1.9993 * FETCH_SIZE + WRITE_SIZE (per-launch medians of `rocprofv3 --pmc`
+# runs of `bench.py --no-cpu --workload decode_32l`; the launches and
+# commands are listed in DECODE_TRAFFIC_SOURCE).
+DECODE_TRAFFIC = {"decode_32l": 5_335_931_919}
+DECODE_TRAFFIC_SOURCE = "profiles/decode_32l_q4k_kernel_trace.txt"
 # Per-dispatch TCC counters of the GEMV kernel (KiB), medians over the timed
 # launches of `rocprofv3 --pmc FETCH_SIZE` and `--pmc WRITE_SIZE` runs of
 # `bench.py --no-cpu --copy-probe 64 --workload W` (the commands are in the
@@ -99,21 +105,24 @@ DECODE = {
 COPY_FETCH_SCALE = 65536.0 / 32779.5
 COPY_WRITE_SCALE = 65536.0 / 65536.0
 PMC_KIB = {
-    "q4k_4096x14336": (18946.19, 56.0),
+    "q4k_4096x14336": (18942.12, 56.0),
     "q4k_4096x4096": (5499.5, 16.0),
-    "q4k_14336x4096": (19113.0, 16.0),
-    "q8_0_4096x4096": (9329.0, 16.0),
-    "q8_0_4096x14336": (32450.56, 56.0),
-    "q8_0_14336x4096": (32657.0, 16.0),
+    "q4k_14336x4096": (19109.5, 16.0),
+    "q8_0_4096x4096": (9325.5, 16.0),
+    "q8_0_4096x14336": (32456.69, 56.0),
+    "q8_0_14336x4096": (32651.12, 16.0),
     "q6k_4096x4096": (7035.0, 16.0),
-    "q6k_4096x14336": (24330.0, 56.0),
-    "q6k_14336x4096": (24489.5, 16.0),
-    "q4_0_4096x4096": (5241.0, 16.0),
-    "ternary_2560x6912": (2241.25, 30.84),
+    "q6k_4096x14336": (24327.5, 56.0),
+    "q6k_14336x4096": (24497.5, 16.0),
+    "q4_0_4096x4096": (5242.0, 16.0),
+    "ternary_2560x6912": (2241.5, 30.84),
     "ternary_6912x2560": (2308.0, 16.0),
 }
-# Where each PMC_KIB entry comes from (the profile summary under profiles/).
+# Where each PMC_KIB entry comes from: the profile summary of the kernel that
+# workload dispatches (k_gemv_q4k serves the headline shape; the other
+# k-quant/Q8_0/Q4_0 shapes run k_gemv_rpl; the ternary DType runs k_narrow_i8v).
 PMC_SOURCE = {w: f"profiles/{'k_narrow_i8v' if w.startswith('ternary') else 'k_gemv_rpl'}_{w}.txt" for w in PMC_KIB}
+PMC_SOURCE["q4k_4096x14336"] = "profiles/k_gemv_q4k_4096x14336.txt"
 METRIC = "dequant-GEMV HBM GB/s (% of peak) at 4096->14336 Q4_K b=1; decode tokens/s"
 
 
@@ -686,7 +695,9 @@ def decode_run(args, wv, workload, steps, warmup, with_cpu):
                    "bytes_per_step": step_bytes, "weight_bytes_per_step": step_bytes - kv_bytes,
                    "kv_bytes_per_step": kv_bytes, "last_tokens": [int(t) for t in toks[-4:]]},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": DECODE_TRAFFIC.get(workload),
+                     "traffic_unit": "bytes per token",
+                     "traffic_source": DECODE_TRAFFIC_SOURCE if workload in DECODE_TRAFFIC else None},
     }
     if with_cpu:
         import oracle
