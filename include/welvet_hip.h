@@ -26,8 +26,10 @@
  *     so concurrent calls on one blob, from several threads or on several
  *     streams, never share partials. The slots grow on first use of a larger
  *     shape (hipMalloc) and are kept for the process. wv_matvec_dev_noalloc
- *     is the exception: all its calls on one GPU share one fixed array, so
- *     overlapping calls race (see its declaration). Blob and decoder handles
+ *     is the exception: all its calls on one GPU share one fixed array; calls
+ *     on one stream are ordered by it, a call on another stream while the
+ *     previous call still runs fails with WV_E_BUSY, and under graph capture
+ *     the caller orders the replays (see its declaration). Blob and decoder handles
  *     must not be freed while another thread still calls with them.
  */
 #ifndef WELVET_HIP_H
@@ -49,6 +51,7 @@ extern "C" {
 #define WV_E_HIP (-5)      /* HIP runtime error */
 #define WV_E_NODEV (-6)    /* no HIP device */
 #define WV_E_HANDLE (-7)   /* unknown / freed handle */
+#define WV_E_BUSY (-8)     /* wv_matvec_dev_noalloc: its scratch is in use by a call on another stream */
 
 /* ---- formats: quant.Format values (quant/format.go:9-39) ---- */
 enum wv_format {
@@ -188,10 +191,12 @@ int wv_matvec_dev(uint64_t handle, const float *d_x, float *d_y, int32_t batch, 
  * fixed 4 MiB device array per GPU, held until the process ends, instead of a
  * per-call allocation; a shape whose partials (up to 8 batch rows x the K
  * split x the rows padded to 64) exceed 2^20 floats fails with WV_E_SHAPE
- * before anything is enqueued. Every call
- * on a GPU shares that GPU's array: calls that overlap on one GPU (other
- * threads or streams) race; callers must order them. Results equal
- * wv_matvec_dev's. */
+ * before anything is enqueued. Every call on a GPU shares that GPU's array,
+ * so calls that overlap on one GPU would race: calls on one stream are
+ * ordered by it, and a call on another stream while the previous call's
+ * work has not finished fails with WV_E_BUSY, nothing enqueued. Under HIP
+ * graph capture that check is off and callers must order the replays
+ * themselves. Results equal wv_matvec_dev's. */
 int wv_matvec_dev_noalloc(uint64_t handle, const float *d_x, float *d_y, int32_t batch, void *stream);
 
 /* quant.MatVec (quant/matvec.go:5-35) for one vector, with its argument check

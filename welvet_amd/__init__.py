@@ -32,7 +32,7 @@ FORMAT_NAMES = {v: k for k, v in FORMATS.items()}
 LAYOUTS = {0: "raw", 1: "row-interleaved", 4: "narrow", 5: "f32"}
 
 REFERENCE_LAYOUT = 1  # WV_UPLOAD_REFERENCE_LAYOUT
-WV_E = {-1: "ARG", -2: "SHAPE", -3: "FORMAT", -4: "OOM", -5: "HIP", -6: "NODEV", -7: "HANDLE"}
+WV_E = {-1: "ARG", -2: "SHAPE", -3: "FORMAT", -4: "OOM", -5: "HIP", -6: "NODEV", -7: "HANDLE", -8: "BUSY"}
 
 # Every symbol include/welvet_hip.h declares.
 EXPORTS = (

@@ -49,6 +49,14 @@ struct DeviceState {
     bool ready = false;
     hipStream_t stream = nullptr;
     float* scratch = nullptr;  // this device's address of the file-scope `scratch` array
+    // The last wv_matvec_dev_noalloc call on this device: its stream and an
+    // event recorded after its launches (created at initialisation), so that a
+    // call on another stream while that one may still read or write `scratch`
+    // is refused instead of racing (guarded by na_mu).
+    std::mutex na_mu;
+    hipEvent_t na_done = nullptr;
+    hipStream_t na_stream = nullptr;
+    bool na_pending = false;
     // Stream-ordered pool of the per-call buffers (K-split partials, host
     // staging). Its release threshold is unbounded, so memory freed by one
     // call stays in the pool for the next instead of going back to the driver
@@ -84,6 +92,8 @@ int ensure_device_locked(int dev) {
         uint64_t keep = UINT64_MAX;
         e = hipMemPoolSetAttribute(g_dev[dev].pool, hipMemPoolAttrReleaseThreshold, &keep);
         if (e != hipSuccess) return hip_fail(e, "wv_init: hipMemPoolSetAttribute");
+        e = hipEventCreateWithFlags(&g_dev[dev].na_done, hipEventDisableTiming);
+        if (e != hipSuccess) return hip_fail(e, "wv_init: hipEventCreate");
         g_dev[dev].scratch = static_cast<float*>(sp);
         g_dev[dev].ready = true;
     }
@@ -944,10 +954,11 @@ int wv_matvec_dev_noalloc(uint64_t handle, const float* d_x, float* d_y, int32_t
     if (!d_x || !d_y) return fail(WV_E_ARG, "MatVec: nil x/y");
     if (batch < 0) return fail(WV_E_SHAPE, "MatVec: negative batch %d", batch);
     if (batch == 0) return WV_OK;
+    DeviceState& dv = g_dev[b.device];
     float* sp = nullptr;
     {
         std::lock_guard<std::mutex> lk(g_mu);
-        sp = g_dev[b.device].scratch;
+        sp = dv.scratch;
     }
     if (!sp) return fail(WV_E_NODEV, "MatVec (no-alloc): device %d has no scratch (not initialised)", b.device);
     // Every partial the split kernels read was written earlier in the same
@@ -957,8 +968,31 @@ int wv_matvec_dev_noalloc(uint64_t handle, const float* d_x, float* d_y, int32_t
         return fail(WV_E_SHAPE, "MatVec (no-alloc): rows=%lld cols=%lld needs %zu floats of scratch, the fixed array holds %zu",
                     (long long)b.rows, (long long)b.cols, need, kNoAllocScratchFloats);
     (void)hipSetDevice(b.device);
-    const int e = launch_matvec(b, d_x, d_y, batch, stream_or_default(stream, b.device), need ? sp : nullptr);
+    hipStream_t s = stream_or_default(stream, b.device);
+    // Calls on one stream are ordered by it. A call on another stream is
+    // refused while the previous call's work may still be running, which is
+    // the overlap that would share the array. Under graph capture nothing is
+    // recorded or checked: the captured launches run when the graph does, and
+    // their order is the caller's to keep.
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cap) != hipSuccess) cap = hipStreamCaptureStatusNone;
+    const bool capturing = cap != hipStreamCaptureStatusNone;
+    std::lock_guard<std::mutex> nl(dv.na_mu);
+    if (!capturing && dv.na_pending && dv.na_stream != s) {
+        const hipError_t q = hipEventQuery(dv.na_done);
+        if (q == hipErrorNotReady)
+            return fail(WV_E_BUSY, "MatVec (no-alloc): the previous call on device %d (another stream) is still running; "
+                        "order the calls or use wv_matvec_dev", b.device);
+        if (q != hipSuccess) return hip_fail(q, "MatVec (no-alloc): hipEventQuery");
+    }
+    const int e = launch_matvec(b, d_x, d_y, batch, s, need ? sp : nullptr);
     if (e != hipSuccess) return hip_fail(hipError_t(e), "MatVec (no-alloc): kernel launch");
+    if (!capturing) {
+        const hipError_t r = hipEventRecord(dv.na_done, s);
+        if (r != hipSuccess) return hip_fail(r, "MatVec (no-alloc): hipEventRecord");
+        dv.na_stream = s;
+        dv.na_pending = true;
+    }
     return WV_OK;
 }
 
