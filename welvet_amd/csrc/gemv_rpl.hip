@@ -323,6 +323,7 @@ using RplAffI = RplB32I<4, true, 0, 0u, GSH>;  // AffinePacked, 32 << GSH-column
 // 2^GSH chunks (BinaryPacked g128: GSH = 2, two words per super-block).
 template <int B, bool SG16, int MID2, int GSH = 0>
 struct RplIQI {
+    static constexpr int kBits = B;
     static constexpr bool kIntX = true;
     static constexpr bool kWords2 = SG16;
     static constexpr int kGsh = GSH;
@@ -1196,28 +1197,57 @@ int launch_rpl_t(const DevBlob& bl, const float* x, float* y, int batch, hipStre
 //
 // Lane = row, as in the forward layout, so the sum over rows runs across
 // lanes. A wave owns one chunk pair (64 columns) of one super-block and walks
-// a slice of row groups, accumulating per-lane column partials in registers
-// (acc[c] += coef_group(row) * ucode(row, c), plus one offset term per
-// 16-column group: the k-quant min or the code bias). Only after the slice
-// does it reduce across lanes, with a reduce-scatter that leaves column l in
-// lane l. The 4 waves of a block are the 4 chunk pairs of one super-block, so
-// they read the same metadata lines together (HBM once, L2 after). Slices
-// write partials [b][slice][cols] that a fixed-order pass adds to gx; a
-// single slice adds to gx directly.
+// GP consecutive row groups, accumulating per-lane column partials in
+// registers (acc[c] += coef_group(row) * ucode(row, c), plus one offset term
+// per 16-column group: the k-quant min or the code bias). Only then does it
+// reduce across lanes, with a reduce-scatter that leaves column l in lane l.
+// A block is one 64-column group and one slice of W * GP row groups: its W
+// waves add their columns in LDS in wave order, so when the column groups
+// alone fill the GPU (one slice) the block adds its total to gx and no second
+// pass runs. With several slices each block stores a partial [b][slice][cols]
+// that a fixed-order pass adds to gx.
 // ---------------------------------------------------------------------------
 
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+
+// acc[0..7] += coef * (codes of an 8-column run): byte b of `lo` holds the
+// code of column 2b, byte b of `hi` that of column 2b + 1. Codes below 16
+// (kMix) become fp16 two at a time with v_cvt_scalef32_pk_f16_fp8 (a byte
+// q < 16 read as fp8 e4m3 is q * 2^-9 exactly, and the scale 512 makes it
+// q), and an fmaf of an fp16 code widened to f32 is one v_fma_mix_f32: the
+// same single-rounding result as fmaf(float(q), coef, acc), in 12 VALU
+// operations per 8 codes instead of 16. Wider codes go through
+// v_cvt_f32_ubyte.
+template <bool kMix>
+__device__ __forceinline__ void tacc8(uint32_t lo, uint32_t hi, float coef, float* acc) {
+    asm("" : "+v"(lo), "+v"(hi));
+    if constexpr (kMix) {
+        const half2v l01 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, 512.0f, false);
+        const half2v l23 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, 512.0f, true);
+        const half2v h01 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, 512.0f, false);
+        const half2v h23 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, 512.0f, true);
+        acc[0] = fmaf(float(l01.x), coef, acc[0]);
+        acc[1] = fmaf(float(h01.x), coef, acc[1]);
+        acc[2] = fmaf(float(l01.y), coef, acc[2]);
+        acc[3] = fmaf(float(h01.y), coef, acc[3]);
+        acc[4] = fmaf(float(l23.x), coef, acc[4]);
+        acc[5] = fmaf(float(h23.x), coef, acc[5]);
+        acc[6] = fmaf(float(l23.y), coef, acc[6]);
+        acc[7] = fmaf(float(h23.y), coef, acc[7]);
+    } else {
+        acc[0] = fmaf(ub0(lo), coef, acc[0]);
+        acc[1] = fmaf(ub0(hi), coef, acc[1]);
+        acc[2] = fmaf(ub1(lo), coef, acc[2]);
+        acc[3] = fmaf(ub1(hi), coef, acc[3]);
+        acc[4] = fmaf(ub2(lo), coef, acc[4]);
+        acc[5] = fmaf(ub2(hi), coef, acc[5]);
+        acc[6] = fmaf(ub3(lo), coef, acc[6]);
+        acc[7] = fmaf(ub3(hi), coef, acc[7]);
+    }
+}
 // acc[2b], acc[2b+1] += coef * (nibbles 2b, 2b+1 of v), b = 0..3
 __device__ __forceinline__ void tacc_nib(uint32_t v, float coef, float* acc) {
-    uint32_t l = v & 0x0F0F0F0Fu, h = (v >> 4) & 0x0F0F0F0Fu;
-    asm("" : "+v"(l), "+v"(h));
-    acc[0] = fmaf(ub0(l), coef, acc[0]);
-    acc[1] = fmaf(ub0(h), coef, acc[1]);
-    acc[2] = fmaf(ub1(l), coef, acc[2]);
-    acc[3] = fmaf(ub1(h), coef, acc[3]);
-    acc[4] = fmaf(ub2(l), coef, acc[4]);
-    acc[5] = fmaf(ub2(h), coef, acc[5]);
-    acc[6] = fmaf(ub3(l), coef, acc[6]);
-    acc[7] = fmaf(ub3(h), coef, acc[7]);
+    tacc8<true>(v & 0x0F0F0F0Fu, (v >> 4) & 0x0F0F0F0Fu, coef, acc);
 }
 // acc[k] += coef * byte k of v
 __device__ __forceinline__ void tacc_u8(uint32_t v, float coef, float* acc) {
@@ -1261,16 +1291,7 @@ struct TKx : RplKxI<B> {
     }
     // the 8 codes of code word w (spread words 2w, 2w + 1), column order
     static __device__ __forceinline__ void tacc_w(const Ch& ch, int w, float coef, float* acc) {
-        uint32_t lo = RplKxI<B>::spread(ch, 2 * w), hi = RplKxI<B>::spread(ch, 2 * w + 1);
-        asm("" : "+v"(lo), "+v"(hi));
-        acc[0] = fmaf(ub0(lo), coef, acc[0]);
-        acc[1] = fmaf(ub0(hi), coef, acc[1]);
-        acc[2] = fmaf(ub1(lo), coef, acc[2]);
-        acc[3] = fmaf(ub1(hi), coef, acc[3]);
-        acc[4] = fmaf(ub2(lo), coef, acc[4]);
-        acc[5] = fmaf(ub2(hi), coef, acc[5]);
-        acc[6] = fmaf(ub3(lo), coef, acc[6]);
-        acc[7] = fmaf(ub3(hi), coef, acc[7]);
+        tacc8<(B <= 4)>(RplKxI<B>::spread(ch, 2 * w), RplKxI<B>::spread(ch, 2 * w + 1), coef, acc);
     }
     template <int jj>
     static __device__ __forceinline__ void tacc(const Ch& ch, const TM& t, float gy, float* acc, float* off) {
@@ -1304,16 +1325,7 @@ struct TB32 : RplB32I<B, MIN, OFF, XR, GSH> {
         }
     }
     static __device__ __forceinline__ void tacc_w(const Ch& ch, int w, float coef, float* acc) {
-        uint32_t lo = P::spread(ch, 2 * w), hi = P::spread(ch, 2 * w + 1);
-        asm("" : "+v"(lo), "+v"(hi));
-        acc[0] = fmaf(ub0(lo), coef, acc[0]);
-        acc[1] = fmaf(ub0(hi), coef, acc[1]);
-        acc[2] = fmaf(ub1(lo), coef, acc[2]);
-        acc[3] = fmaf(ub1(hi), coef, acc[3]);
-        acc[4] = fmaf(ub2(lo), coef, acc[4]);
-        acc[5] = fmaf(ub2(hi), coef, acc[5]);
-        acc[6] = fmaf(ub3(lo), coef, acc[6]);
-        acc[7] = fmaf(ub3(hi), coef, acc[7]);
+        tacc8<(B <= 4)>(P::spread(ch, 2 * w), P::spread(ch, 2 * w + 1), coef, acc);
     }
     template <int jj>
     static __device__ __forceinline__ void tacc(const Ch& ch, const TM& t, float gy, float* acc, float* off) {
@@ -1345,16 +1357,8 @@ struct TIQ : PQ {
         }
     }
     static __device__ __forceinline__ void tacc_w(const Ch& ch, int w, float coef, float* acc) {
-        uint32_t lo = PQ::spread(ch, 2 * w), hi = PQ::spread(ch, 2 * w + 1);
-        asm("" : "+v"(lo), "+v"(hi));
-        acc[0] = fmaf(ub0(lo), coef, acc[0]);
-        acc[1] = fmaf(ub0(hi), coef, acc[1]);
-        acc[2] = fmaf(ub1(lo), coef, acc[2]);
-        acc[3] = fmaf(ub1(hi), coef, acc[3]);
-        acc[4] = fmaf(ub2(lo), coef, acc[4]);
-        acc[5] = fmaf(ub2(hi), coef, acc[5]);
-        acc[6] = fmaf(ub3(lo), coef, acc[6]);
-        acc[7] = fmaf(ub3(hi), coef, acc[7]);
+        static_assert(PQ::kBits <= 4, "fp8 code conversion");
+        tacc8<true>(PQ::spread(ch, 2 * w), PQ::spread(ch, 2 * w + 1), coef, acc);
     }
     template <int jj>
     static __device__ __forceinline__ void tacc(const Ch& ch, const TM& t, float gy, float* acc, float* off) {
@@ -1473,14 +1477,30 @@ struct TIQ4NL : RplIQ4NL {
     }
 };
 
+// Column group of block x in XCD-aware order. Consecutive block ids go to
+// the 8 XCDs in turn, so x = 32q + 8jp + k gives super-block sb = 8q + k,
+// chunk pair jp: the four chunk pairs of a super-block (ids 8 apart) run on
+// one XCD and read its metadata lines (each lane's chunk-pair words are
+// interleaved per super-block) through one L2. Grids round the super-blocks
+// up to a multiple of 8; the blocks past nsb return at once.
+__device__ __forceinline__ void rpl_t_cg(int x, int& sb, int& jp) {
+    jp = (x >> 3) & 3;
+    sb = (x >> 5) * 8 + (x & 7);
+}
+
 template <class P, int GP>
-__global__ void __launch_bounds__(256) k_gemvt_rpl(RplArgs a, const float* __restrict__ gy, float* __restrict__ gx,
-                                                  float* __restrict__ part) {
-    const int jp = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+__global__ void __launch_bounds__(1024) k_gemvt_rpl(RplArgs a, const float* __restrict__ gy, float* __restrict__ gx,
+                                                   float* __restrict__ part) {
+    __shared__ float red[16 * 64];
+    const int W = blockDim.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
-    const int sb = blockIdx.x, slice = blockIdx.y, b = blockIdx.z;
+    int sb, jp;
+    rpl_t_cg(blockIdx.x, sb, jp);
+    if (sb >= a.nsb) return;  // uniform over the block
+    const int slice = blockIdx.y, b = blockIdx.z;
     const int nslices = gridDim.y;
-    const int g0 = slice * GP;
+    const int g0 = (slice * W + wave) * GP;
     const int64_t cols = int64_t(a.nsb) * 256;
     const float* gyb = gy + int64_t(b) * a.rows;
 
@@ -1488,10 +1508,10 @@ __global__ void __launch_bounds__(256) k_gemvt_rpl(RplArgs a, const float* __res
 #pragma unroll
     for (int k = 0; k < 64; ++k) acc[k] = 0.f;
 
-    // GP row groups per slice, fully unrolled with a 2-deep register ring so
-    // that every index is static and no load sits under a branch (either would
-    // make the next use wait for all outstanding loads). Row groups past the
-    // end are clamped to the last one and contribute gy = 0.
+    // GP row groups, fully unrolled with a 2-deep register ring so that every
+    // index is static and no load sits under a branch (either would make the
+    // next use wait for all outstanding loads). Row groups past the end are
+    // clamped to the last one and contribute gy = 0.
     struct Set {
         typename P::Ch c0, c1;
         typename P::TM tm;
@@ -1565,7 +1585,12 @@ __global__ void __launch_bounds__(256) k_gemvt_rpl(RplArgs a, const float* __res
     off[1] = reduce_scatter32(off[1], off[3]);
     const float o = row_sum16(reduce_scatter16(off[0], off[1]));
 
-    const float total = acc[0] + o;
+    // the block's waves, added in wave order
+    red[wave * 64 + lane] = acc[0] + o;
+    __syncthreads();
+    if (wave != 0) return;
+    float total = 0.f;
+    for (int w = 0; w < W; ++w) total += red[w * 64 + lane];
     const int64_t col = int64_t(sb) * 256 + jp * 64 + lane;
     float* gxb = gx + int64_t(b) * cols;
     if (nslices == 1) {
@@ -1578,17 +1603,32 @@ __global__ void __launch_bounds__(256) k_gemvt_rpl(RplArgs a, const float* __res
     part[(int64_t(b) * nslices + slice) * cols + col] = total;
 }
 
-// Row-group slices for `batch` rows: about kRplTBlocks blocks (measured on
-// MI355X); each slice takes GP (1, 2, 4 or 8) row groups.
-constexpr int kRplTBlocks = 512;
+// Row-group slices for `batch` rows. One slice (no second pass) when the
+// column groups alone give at least kRplTMinBlocks blocks; otherwise enough
+// slices for about kRplTBlocks blocks. Each block runs W <= 16 waves of GP
+// (1, 2, 4 or 8) row groups, GP the smallest that keeps W <= 16 (at least 2
+// when the slice has more than one row group), so a slice is W * GP row
+// groups.
+constexpr int kRplTMinBlocks = 180;
+constexpr int kRplTBlocks = 256;
 
-void rpl_t_plan(const RplArgs& a, int batch, int& slices, int& g_per) {
-    const int64_t per_slice = int64_t(a.nsb) * std::max(1, batch);
-    const int64_t target = kRplTBlocks;
-    const int64_t s = std::min<int64_t>(a.rg_count, std::max<int64_t>(1, (target + per_slice - 1) / per_slice));
-    const int64_t need = (a.rg_count + s - 1) / s;
-    g_per = need <= 1 ? 1 : need <= 2 ? 2 : need <= 4 ? 4 : 8;
-    slices = int((a.rg_count + g_per - 1) / g_per);
+struct RplTPlan {
+    int slices, W, GP;
+};
+RplTPlan rpl_t_plan(const RplArgs& a, int batch) {
+    const int64_t per_slice = int64_t(a.nsb) * 4 * std::max(1, batch);
+    int64_t slices = 1;
+    if (per_slice < kRplTMinBlocks) slices = (kRplTBlocks + per_slice - 1) / per_slice;
+    slices = std::min<int64_t>(slices, a.rg_count);
+    int64_t rps = (a.rg_count + slices - 1) / slices;
+    if (rps > 16 * 8) rps = 16 * 8;
+    int gp = rps > 1 ? 2 : 1;
+    while (gp < 8 && (rps + gp - 1) / gp > 8) gp *= 2;
+    RplTPlan p;
+    p.GP = gp;
+    p.W = int((rps + gp - 1) / gp);
+    p.slices = int((a.rg_count + int64_t(p.W) * gp - 1) / (int64_t(p.W) * gp));
+    return p;
 }
 
 template <class P>
@@ -1597,13 +1637,13 @@ int launch_rpl_tr(const DevBlob& bl, const float* gy, float* gx, int batch, hipS
     const int64_t cols = int64_t(a.nsb) * 256;
     for (int b0 = 0; b0 < batch; b0 += kRplTMaxBatch) {
         const int nb = std::min(kRplTMaxBatch, batch - b0);
-        int slices = 1, g_per = 1;
-        rpl_t_plan(a, nb, slices, g_per);
-        auto kern = g_per == 1 ? k_gemvt_rpl<P, 1> : g_per == 2 ? k_gemvt_rpl<P, 2> : g_per == 4 ? k_gemvt_rpl<P, 4> : k_gemvt_rpl<P, 8>;
-        if (slices > 1 && !part) return int(hipErrorInvalidValue);  // the caller owes the slice scratch
-        dim3 grid(unsigned(a.nsb), unsigned(slices), unsigned(nb));
-        hipLaunchKernelGGL(kern, grid, dim3(256), 0, s, a, gy + int64_t(b0) * a.rows, gx + int64_t(b0) * cols, part);
-        if (slices > 1) launch_gemvt_reduce(part, gx + int64_t(b0) * cols, cols, slices, nb, s);
+        const RplTPlan p = rpl_t_plan(a, nb);
+        auto kern = p.GP == 1 ? k_gemvt_rpl<P, 1> : p.GP == 2 ? k_gemvt_rpl<P, 2> : p.GP == 4 ? k_gemvt_rpl<P, 4> : k_gemvt_rpl<P, 8>;
+        if (p.slices > 1 && !part) return int(hipErrorInvalidValue);  // the caller owes the slice scratch
+        dim3 grid(unsigned((a.nsb + 7) / 8 * 32), unsigned(p.slices), unsigned(nb));
+        hipLaunchKernelGGL(kern, grid, dim3(unsigned(64 * p.W)), 0, s, a, gy + int64_t(b0) * a.rows, gx + int64_t(b0) * cols,
+                           part);
+        if (p.slices > 1) launch_gemvt_reduce(part, gx + int64_t(b0) * cols, cols, p.slices, nb, s);
     }
     return int(hipGetLastError());
 }
@@ -1870,9 +1910,8 @@ size_t rpl_t_scratch_floats(const RplArgs& a, int batch) {
     const int full = std::min(batch, kRplTMaxBatch), rest = batch % kRplTMaxBatch;
     for (int nb : {full, rest}) {
         if (nb <= 0) continue;
-        int slices = 1, g_per = 1;
-        rpl_t_plan(a, nb, slices, g_per);
-        if (slices > 1) most = std::max(most, size_t(slices) * size_t(nb) * size_t(a.nsb) * 256);
+        const RplTPlan p = rpl_t_plan(a, nb);
+        if (p.slices > 1) most = std::max(most, size_t(p.slices) * size_t(nb) * size_t(a.nsb) * 256);
     }
     return most;
 }
