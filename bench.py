@@ -123,6 +123,18 @@ PMC_KIB = {
 # k-quant/Q8_0/Q4_0 shapes run k_gemv_rpl; the ternary DType runs k_narrow_i8v).
 PMC_SOURCE = {w: f"profiles/{'k_narrow_i8v' if w.startswith('ternary') else 'k_gemv_rpl'}_{w}.txt" for w in PMC_KIB}
 PMC_SOURCE["q4k_4096x14336"] = "profiles/k_gemv_q4k_4096x14336.txt"
+# HBM bytes per MatVecT step (every kernel of the step: 1.9993 * FETCH_SIZE +
+# WRITE_SIZE per dispatch), from the profile summary each workload names.
+MATVECT_TRAFFIC = {
+    "q4_k_t_4096x14336": 39_440_862,
+    "q4_k_t_14336x4096": 39_106_364,
+    "q6_k_t_4096x14336": 50_359_233,
+    "q6_k_t_14336x4096": 49_956_485,
+    "q8_0_t_4096x14336": 68_631_762,
+    "q8_0_t_14336x4096": 67_877_482,
+}
+
+
 METRIC = "dequant-GEMV HBM GB/s (% of peak) at 4096->14336 Q4_K b=1; decode tokens/s"
 
 
@@ -605,7 +617,9 @@ def matvect_main(args, torch, wv):
         "config": {"workload": desc, "format": fmt, "rows": rows, "cols": cols, "layout": layout,
                    "weight_copies_rotated": copies, "algorithmic_bytes_per_step": nbytes},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": MATVECT_TRAFFIC.get(args.workload),
+                     "traffic_source": (f"profiles/k_gemvt_rpl_{args.workload}.txt"
+                                        if args.workload in MATVECT_TRAFFIC else None),
                      "step_us": round(ms * 1e3, 3)},
     }
     if not args.no_cpu:
@@ -628,6 +642,7 @@ def matvect_main(args, torch, wv):
                       f"serial), {dt * 1e3:.3f} ms/call"}
     for b in blobs:
         b.free()
+    copy_probe(args, torch, result)
     print(json.dumps(result), flush=True)
 
 
