@@ -761,26 +761,22 @@ __global__ void __launch_bounds__(256) k_split_sum(const float* __restrict__ par
     }
     const float4* p = reinterpret_cast<const float4*>(part) + i4;
     const int64_t n4 = n >> 2;
+    // Splits in order; each group of 8 loads (clamped to the last split, the
+    // extra ones masked out of the sum) is issued before any add.
     float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
-    int k = 0;
-    for (; k + 8 <= splits; k += 8) {
+    for (int k = 0; k < splits; k += 8) {
         float4 v[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = p[int64_t(k + j) * n4];
+        for (int j = 0; j < 8; ++j) v[j] = p[int64_t(min(k + j, splits - 1)) * n4];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            s.x += v[j].x;
-            s.y += v[j].y;
-            s.z += v[j].z;
-            s.w += v[j].w;
+            if (k + j < splits) {
+                s.x += v[j].x;
+                s.y += v[j].y;
+                s.z += v[j].z;
+                s.w += v[j].w;
+            }
         }
-    }
-    for (; k < splits; ++k) {
-        const float4 v = p[int64_t(k) * n4];
-        s.x += v.x;
-        s.y += v.y;
-        s.z += v.z;
-        s.w += v.w;
     }
     reinterpret_cast<float4*>(y)[i4] = s;
 }

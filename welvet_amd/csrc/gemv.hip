@@ -543,20 +543,23 @@ __global__ void __launch_bounds__(64) k_gemvt_reduce(const float* __restrict__ p
     const int64_t c = int64_t(blockIdx.x) * 64 + threadIdx.x;
     const int b = blockIdx.y;
     if (c >= cols) return;
-    // Partials are added in split order; each group of 8 loads is issued
-    // before any of them is added, so the latency is paid once per group.
+    // Partials are added in split order, then to gx. Each group of 8 loads
+    // (clamped to the last split, the extra ones masked out of the sum) and
+    // the gx load are issued before any add, so a step with up to 8 splits
+    // pays one memory round trip.
     const float* p = part + int64_t(b) * nsplit * cols + c;
+    float* g = gx + int64_t(b) * cols + c;
+    const float g0 = *g;
     float s = 0.0f;
-    int k = 0;
-    for (; k + 8 <= nsplit; k += 8) {
+    for (int k = 0; k < nsplit; k += 8) {
         float v[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = p[int64_t(k + j) * cols];
+        for (int j = 0; j < 8; ++j) v[j] = p[int64_t(min(k + j, nsplit - 1)) * cols];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) s += v[j];
+        for (int j = 0; j < 8; ++j)
+            if (k + j < nsplit) s += v[j];
     }
-    for (; k < nsplit; ++k) s += p[int64_t(k) * cols];
-    gx[int64_t(b) * cols + c] += s;
+    *g = g0 + s;
 }
 
 // applyBiasAct (layers/dense/dense.go:145-167) over y[batch][rows]: pre =

@@ -1042,25 +1042,26 @@ __global__ void __launch_bounds__(1024) k_gemv_q4k(RplArgs a, const float* __res
 }
 
 // Tail of a K-split forward launch: one wave per (64-row group, batch row)
-// adds the ksplit partials in split order (8 loads issued before each group
-// of adds) and applies the launch's epilogue. A last-arriving-block tail in
-// the forward kernel instead costs more: its ticket and partials must bypass
-// the caches, about 1.5 us per round trip on MI355X.
+// adds the ksplit partials in split order and applies the launch's epilogue.
+// A last-arriving-block tail in the forward kernel instead costs more: its
+// ticket and partials must bypass the caches, about 1.5 us per round trip on
+// MI355X.
 __global__ void __launch_bounds__(64) k_rpl_ksum(RplArgs a, float* __restrict__ y) {
     const int rg = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
     const int64_t rows_pad = int64_t(a.rg_count) * 64;
     const int row = rg * 64 + lane;
     const float* p = a.partial + int64_t(b) * a.ksplit * rows_pad + row;
+    // Each group of 8 loads (clamped to the last split, the extra ones masked
+    // out of the sum) is issued before any add: one round trip for up to 8.
     float s = 0.f;
-    int k = 0;
-    for (; k + 8 <= a.ksplit; k += 8) {
+    for (int k = 0; k < a.ksplit; k += 8) {
         float v[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = p[int64_t(k + j) * rows_pad];
+        for (int j = 0; j < 8; ++j) v[j] = p[int64_t(min(k + j, a.ksplit - 1)) * rows_pad];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) s += v[j];
+        for (int j = 0; j < 8; ++j)
+            if (k + j < a.ksplit) s += v[j];
     }
-    for (; k < a.ksplit; ++k) s += p[int64_t(k) * rows_pad];
     finish_rows(a, y, b, row, true, lane, s);
 }
 

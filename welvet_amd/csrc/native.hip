@@ -465,10 +465,20 @@ __global__ void __launch_bounds__(256) k_native_t_sum(const double* __restrict__
     const int b = blockIdx.y;
     if (c >= K) return;
     const double* p = part + int64_t(b) * nslices * K + c;
-    double s = 0.0;
-    for (int k = 0; k < nslices; ++k) s += p[int64_t(k) * K];
     TX* o = gx + int64_t(b) * K + c;
-    *o = TX(double(*o) + s);
+    const double g0 = double(*o);
+    // Slices in order; each group of 8 loads (clamped, the extra ones masked
+    // out of the sum) and the gx load are issued before any add.
+    double s = 0.0;
+    for (int k = 0; k < nslices; k += 8) {
+        double v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = p[int64_t(min(k + j, nslices - 1)) * K];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if (k + j < nslices) s += v[j];
+    }
+    *o = TX(g0 + s);
 }
 
 // Launch geometry of k_narrow_i8v: about one block per CU (256), each of WB
