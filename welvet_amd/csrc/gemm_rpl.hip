@@ -163,22 +163,27 @@ struct GemmKQ {  // Q2_K, Q3_K, Q4_K, Q5_K: w = (d/255)*u*q + (dmin/127)*m
         return {GemmCodes<FB>::load(a, ci, lane), reinterpret_cast<const uint32_t*>(a.meta)[(si * 64 + lane) * 8 + j],
                 reinterpret_cast<const float2*>(a.dd)[si * 64 + lane]};
     }
+    // The lane forms the fp16 scales and mins of its own row (row `lane` of
+    // the group: tile lane / 32) and the lane swap hands each lane both tiles'
+    // pairs, the same values the other lane computed.
     static __device__ __forceinline__ void bops(const Ch& c, int lane, const float (&wk)[2], half8 (&bf)[2][2]) {
-        const auto d2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(c.dd.x), __float_as_uint(c.dd.x), false, false);
-        const auto m2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(c.dd.y), __float_as_uint(c.dd.y), false, false);
-        const auto mt = __builtin_amdgcn_permlane32_swap(c.mw, c.mw, false, false);
+        float w0 = wk[0], w1 = wk[1];
+        asm("" : "+v"(w0), "+v"(w1));  // a select of values, not an indexed load of the array
+        const float wo = (lane & 32) ? w1 : w0;  // the own row's factor
+        const float d255 = c.dd.x * (wo * (1.0f / 255.0f)), dm127 = c.dd.y * (wo * (1.0f / 127.0f));
+        const uint32_t gm = c.mw;
+        const half2v scp = {_Float16(d255 * float(gm & 0xFFu)), _Float16(d255 * float((gm >> 8) & 0xFFu))};
+        const half2v mnp = {_Float16(dm127 * float(int8_t(gm >> 16))), _Float16(dm127 * float(int32_t(gm) >> 24))};
+        const auto sc2 = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, scp),
+                                                          __builtin_bit_cast(uint32_t, scp), false, false);
+        const auto mn2 = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, mnp),
+                                                          __builtin_bit_cast(uint32_t, mnp), false, false);
         uint32_t se[2][2], so[2][2];
         GemmCodes<FB>::spread(c.c, lane, se, so);
 #pragma unroll
         for (int T = 0; T < 2; ++T) {
-            const float d255 = __uint_as_float(d2[T]) * (wk[T] * (1.0f / 255.0f));
-            const float dm127 = __uint_as_float(m2[T]) * (wk[T] * (1.0f / 127.0f));
-            const uint32_t gm = mt[T];
-            const _Float16 sc0 = _Float16(d255 * float(gm & 0xFFu));
-            const _Float16 sc1 = _Float16(d255 * float((gm >> 8) & 0xFFu));
-            const _Float16 mn0 = _Float16(dm127 * float(int8_t(gm >> 16)));
-            const _Float16 mn1 = _Float16(dm127 * float(int32_t(gm) >> 24));
-            const half2v s0 = {sc0, sc0}, s1 = {sc1, sc1}, n0 = {mn0, mn0}, n1 = {mn1, mn1};
+            const half2v sp = __builtin_bit_cast(half2v, uint32_t(sc2[T])), np = __builtin_bit_cast(half2v, uint32_t(mn2[T]));
+            const half2v s0 = {sp.x, sp.x}, s1 = {sp.y, sp.y}, n0 = {np.x, np.x}, n1 = {np.y, np.y};
             bf[T][0] = __builtin_bit_cast(half8, dequant8s<FB>(se[T][0], so[T][0], s0, n0));
             bf[T][1] = __builtin_bit_cast(half8, dequant8s<FB>(se[T][1], so[T][1], s1, n1));
         }
