@@ -126,12 +126,12 @@ PMC_SOURCE["q4k_4096x14336"] = "profiles/k_gemv_q4k_4096x14336.txt"
 # HBM bytes per MatVecT step (every kernel of the step: 1.9993 * FETCH_SIZE +
 # WRITE_SIZE per dispatch), from the profile summary each workload names.
 MATVECT_TRAFFIC = {
-    "q4_k_t_4096x14336": 39_440_862,
-    "q4_k_t_14336x4096": 39_106_364,
-    "q6_k_t_4096x14336": 50_359_233,
-    "q6_k_t_14336x4096": 49_956_485,
-    "q8_0_t_4096x14336": 68_631_762,
-    "q8_0_t_14336x4096": 67_877_482,
+    "q4_k_t_4096x14336": 39_431_811,
+    "q4_k_t_14336x4096": 39_090_041,
+    "q6_k_t_4096x14336": 50_358_658,
+    "q6_k_t_14336x4096": 49_952_296,
+    "q8_0_t_4096x14336": 68_341_744,
+    "q8_0_t_14336x4096": 67_684_058,
 }
 
 
