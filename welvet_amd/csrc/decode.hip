@@ -545,20 +545,19 @@ __global__ void __launch_bounds__(256) k_attn_reg(const float* __restrict__ q, f
 }
 
 // out[h][d] = sum_c o_c[d] e^{m_c - M} / sum_c l_c e^{m_c - M} over the nc
-// chunks below kv_len, for nc <= 64*NCL. Every load is issued up front: lane
-// j of the wave holds the weights of chunks j, j+64, ... (DPP max and sum),
-// wave w accumulates chunks w, w+4, ... in order with each weight broadcast by
-// readlane, and the four waves' sums are added in LDS.
+// chunks below kv_len, for nc <= 64*NCL. Block (h, dq) takes dims 64dq..64dq+63
+// of head h (two blocks per head at HD = 128, so each CU pulls in half the
+// partials). Every load is issued up front: lane j of the wave holds the
+// weights of chunks j, j+64, ... (DPP max and sum), wave w accumulates chunks
+// w, w+4, ... of its dim in order with each weight broadcast by readlane, and
+// the four waves' sums are added in LDS.
 template <int HD, int NCL>
 __global__ void __launch_bounds__(256) k_attn_combine(const float* __restrict__ part, float* __restrict__ out,
                                                       int n_chunks, const int32_t* __restrict__ d_pos, int max_seq) {
-    constexpr int ND = HD / 64, PW = 16 * NCL;
-    __shared__ float red[4][HD];
-    const int h = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    constexpr int PW = 16 * NCL;
+    __shared__ float red[4][64];
+    const int h = blockIdx.x, dq = blockIdx.y, t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const float* ph = part + int64_t(h) * n_chunks * (HD + 2);
-    // The loads are clamped to the allocated chunks, not to the live count,
-    // so they issue together with the position's load instead of after it;
-    // chunks past the live count (stale or never written) are selected away.
     float mc[NCL], lc[NCL];
 #pragma unroll
     for (int j = 0; j < NCL; ++j) {
@@ -566,12 +565,11 @@ __global__ void __launch_bounds__(256) k_attn_combine(const float* __restrict__ 
         mc[j] = ph[cl * (HD + 2) + HD];
         lc[j] = ph[cl * (HD + 2) + HD + 1];
     }
-    float ov[PW][ND];
+    float ov[PW];
 #pragma unroll
     for (int k = 0; k < PW; ++k) {
         const int cc = min(wave + 4 * k, n_chunks - 1);
-#pragma unroll
-        for (int j = 0; j < ND; ++j) ov[k][j] = ph[cc * (HD + 2) + lane + 64 * j];
+        ov[k] = ph[cc * (HD + 2) + 64 * dq + lane];
     }
     const int kv_len = min(*d_pos + 1, max_seq);
     const int nc = min(n_chunks, (kv_len + kChunk - 1) / kChunk);
@@ -592,22 +590,18 @@ __global__ void __launch_bounds__(256) k_attn_combine(const float* __restrict__ 
         lw += lc[j] * w[j];
     }
     const float L = wave_total(lw);
-    float acc[ND];
-#pragma unroll
-    for (int j = 0; j < ND; ++j) acc[j] = 0.f;
+    float acc = 0.f;
 #pragma unroll
     for (int k = 0; k < PW; ++k) {
-        const int cc = wave + 4 * k;  // weight register (4k)/64, lane cc % 64
-        if (cc < nc) {  // uniform over the wave
+        const int cc = wave + 4 * k;
+        if (cc < nc) {
             const float wk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w[(4 * k) / 64]), cc % 64));
-#pragma unroll
-            for (int j = 0; j < ND; ++j) acc[j] = fmaf(ov[k][j], wk, acc[j]);
+            acc = fmaf(ov[k], wk, acc);
         }
     }
-#pragma unroll
-    for (int j = 0; j < ND; ++j) red[wave][lane + 64 * j] = acc[j];
+    red[wave][lane] = acc;
     __syncthreads();
-    if (t < HD) out[h * HD + t] = ((red[0][t] + red[1][t]) + (red[2][t] + red[3][t])) * (L > 0.f ? 1.0f / L : 0.f);
+    if (t < 64) out[h * HD + 64 * dq + t] = ((red[0][t] + red[1][t]) + (red[2][t] + red[3][t])) * (L > 0.f ? 1.0f / L : 0.f);
 }
 
 // The same for any nc <= 2048: thread c owns chunks c, c+256, ... for the max
@@ -1015,16 +1009,16 @@ int proj(Decoder& d, const DevBlob& w, const float* x, float* y, int mode, const
 // Enqueues one whole step on d.stream (token and position from device memory).
 // The combine variant is fixed by the chunk count the cache can reach.
 void launch_combine(Decoder& d, int hd) {
-    const dim3 grid(unsigned(d.c.n_heads));
+    const dim3 grid(unsigned(d.c.n_heads)), grid2(unsigned(d.c.n_heads), unsigned(hd / 64));  // grid2: k_attn_combine
     const int nc = d.n_chunks;
     if (nc <= 64 && hd == 128)
-        hipLaunchKernelGGL((k_attn_combine<128, 1>), grid, dim3(256), 0, d.stream, d.part, d.att, nc, d.d_pos, d.c.max_seq);
+        hipLaunchKernelGGL((k_attn_combine<128, 1>), grid2, dim3(256), 0, d.stream, d.part, d.att, nc, d.d_pos, d.c.max_seq);
     else if (nc <= 64)
-        hipLaunchKernelGGL((k_attn_combine<64, 1>), grid, dim3(256), 0, d.stream, d.part, d.att, nc, d.d_pos, d.c.max_seq);
+        hipLaunchKernelGGL((k_attn_combine<64, 1>), grid2, dim3(256), 0, d.stream, d.part, d.att, nc, d.d_pos, d.c.max_seq);
     else if (nc <= 128 && hd == 128)
-        hipLaunchKernelGGL((k_attn_combine<128, 2>), grid, dim3(256), 0, d.stream, d.part, d.att, nc, d.d_pos, d.c.max_seq);
+        hipLaunchKernelGGL((k_attn_combine<128, 2>), grid2, dim3(256), 0, d.stream, d.part, d.att, nc, d.d_pos, d.c.max_seq);
     else if (nc <= 128)
-        hipLaunchKernelGGL((k_attn_combine<64, 2>), grid, dim3(256), 0, d.stream, d.part, d.att, nc, d.d_pos, d.c.max_seq);
+        hipLaunchKernelGGL((k_attn_combine<64, 2>), grid2, dim3(256), 0, d.stream, d.part, d.att, nc, d.d_pos, d.c.max_seq);
     else
         hipLaunchKernelGGL(k_attn_combine_long, grid, dim3(256), 0, d.stream, d.part, d.att, hd, nc, d.d_pos, d.c.max_seq);
 }
