@@ -167,6 +167,24 @@ int wv_blob_free(uint64_t handle);
 int wv_blob_info(uint64_t handle, int *format, int64_t *rows, int64_t *cols,
                  size_t *device_bytes, int *layout);
 
+/* A cap on the device memory that uploaded blobs may hold on each GPU, in
+ * bytes (0, the default: no cap). The reference keeps its resident weight
+ * caches under a soft cap and answers an upload past it with "weight VRAM
+ * budget full" (webgpu/affine_cache.go:111-123, binary_cache.go, f32_cache.go),
+ * the one error its Dense layer falls back to the host on
+ * (IsAffineVRAMFull, affine_cache.go:73-83; layers/dense/webgpu.go:598-601).
+ * Here an upload that would take a device's blobs past the cap fails with
+ * WV_E_OOM "wv_blob_upload: weight VRAM budget full (...)" before anything is
+ * allocated, and wv_blob_free returns its bytes to the budget. Lowering the
+ * cap frees nothing. Copies the decoder makes for its fused projections are
+ * not counted. */
+int wv_set_weight_budget(uint64_t bytes);
+
+/* Device bytes held by uploaded blobs on the current device (the figure the
+ * budget is checked against), and the cap (0: none). Either pointer may be
+ * NULL. Reference: AffineWeightCacheBytes (webgpu/affine_cache.go:60-68). */
+int wv_weight_bytes(uint64_t *resident, uint64_t *budget);
+
 /* ---- forward: quant.MatVec / dense.MatVecPackedBlob / dense.Forward ---- */
 
 /* y[batch*rows] = W x[batch*cols] for each of `batch` rows (y overwritten).

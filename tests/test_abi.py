@@ -156,3 +156,14 @@ def test_quant_contract_errors_without_device():
     with pytest.raises(wv.WelvetError) as e:
         wv.pack_native("Q4_K", np.zeros(8, np.float32), 1, 8)
     assert e.value.code != 0
+
+
+def test_weight_budget_setting_needs_no_device():
+    """wv_set_weight_budget / wv_weight_bytes only touch host state."""
+    _, before = wv.weight_bytes()
+    wv.set_weight_budget(12345)
+    try:
+        assert wv.weight_bytes()[1] == 12345
+    finally:
+        wv.set_weight_budget(before)
+    assert wv.weight_bytes()[1] == before

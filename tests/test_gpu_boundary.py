@@ -104,6 +104,36 @@ def test_matvec_packed_blob_contract():
         dn.free()
 
 
+def test_weight_budget_full_is_oom():
+    """The resident-weight cap (the reference's soft cap on its weight caches,
+    webgpu/affine_cache.go:111-123): an upload past it is WV_E_OOM with a
+    message that IsAffineVRAMFull (affine_cache.go:73-83) classifies as VRAM
+    full, reserves nothing, and fits again once a blob is freed."""
+    p, a, rng = make("Q4_K", 256, 4096, 11)
+    r1, cap0 = wv.weight_bytes()
+    size = a.info()["device_bytes"]
+    assert size >= p.nbytes
+    wv.set_weight_budget(r1 + size // 2)
+    try:
+        with pytest.raises(wv.WelvetError) as e:
+            wv.upload(p)
+        assert e.value.code == -4
+        msg = str(e.value)
+        assert "weight VRAM budget full" in msg and "vram" in msg.lower() and "budget full" in msg
+        assert wv.weight_bytes()[0] == r1  # the failed upload holds nothing
+        a.free()
+        assert wv.weight_bytes()[0] == r1 - size
+        b = wv.upload(p)  # fits again
+        x = rng.standard_normal(4096).astype(np.float32)
+        ref = oracle.reference_y(packed_ref(p), x)[0]
+        assert normwise(b.matvec(x), ref) <= TOL
+        assert wv.weight_bytes()[0] == r1
+        b.free()
+    finally:
+        wv.set_weight_budget(cap0)
+    assert wv.weight_bytes()[0] == r1 - size
+
+
 EPI = [("Q4_K", (512, 1024), "row-interleaved"), ("IQ4_NL", (300, 544), "raw"),
        ("Q6_K", (100, 700), "raw"), ("NativeInt4", (300, 512), "narrow"), ("none", (200, 300), "f32")]
 

@@ -38,6 +38,7 @@ WV_E = {-1: "ARG", -2: "SHAPE", -3: "FORMAT", -4: "OOM", -5: "HIP", -6: "NODEV",
 EXPORTS = (
     "wv_init", "wv_last_error", "wv_version", "wv_pack_sizes", "wv_pack",
     "wv_pack_native", "wv_blob_upload", "wv_blob_upload_flags", "wv_blob_upload_wire", "wv_blob_free", "wv_blob_info",
+    "wv_set_weight_budget", "wv_weight_bytes",
     "wv_matvec", "wv_matvec_dev", "wv_matvec_dev_noalloc", "wv_quant_matvec", "wv_matvec_packed_blob", "wv_dense_forward", "wv_dense_forward_dev",
     "wv_dense_forward_block", "wv_dense_forward_block_dev",
     "wv_native_acc_dev", "wv_store_matvec", "wv_matvec_t", "wv_matvec_t_dev", "wv_quant_matvec_t",
@@ -80,6 +81,8 @@ def lib():
     L.wv_blob_upload_wire.argtypes = [ctypes.c_int, _I64, _I64, _P, _SZ, _P]
     L.wv_blob_free.argtypes = [ctypes.c_uint64]
     L.wv_blob_info.argtypes = [ctypes.c_uint64, _P, _P, _P, _P, _P]
+    L.wv_set_weight_budget.argtypes = [ctypes.c_uint64]
+    L.wv_weight_bytes.argtypes = [_P, _P]
     L.wv_matvec.argtypes = [ctypes.c_uint64, _P, _P, ctypes.c_int32]
     L.wv_matvec_dev.argtypes = [ctypes.c_uint64, _P, _P, ctypes.c_int32, _P]
     L.wv_matvec_dev_noalloc.argtypes = [ctypes.c_uint64, _P, _P, ctypes.c_int32, _P]
@@ -345,6 +348,19 @@ class DeviceBlob:
                 self.handle = 0
         except Exception:
             pass
+
+
+def set_weight_budget(nbytes: int) -> None:
+    """Cap the device bytes uploaded blobs may hold per GPU (0: no cap); an
+    upload past it raises WelvetError OOM "weight VRAM budget full"."""
+    check(lib().wv_set_weight_budget(int(nbytes)))
+
+
+def weight_bytes():
+    """(resident blob bytes on the current device, the cap or 0)."""
+    r, b = ctypes.c_uint64(), ctypes.c_uint64()
+    check(lib().wv_weight_bytes(ctypes.byref(r), ctypes.byref(b)))
+    return r.value, b.value
 
 
 def upload(packed: PackedBlob, reference_layout: bool = False) -> DeviceBlob:

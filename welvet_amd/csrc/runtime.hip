@@ -57,6 +57,7 @@ struct DeviceState {
     hipEvent_t na_done = nullptr;
     hipStream_t na_stream = nullptr;
     bool na_pending = false;
+    uint64_t resident = 0;  // device bytes of the uploaded blobs (g_mu)
     // Stream-ordered pool of the per-call buffers (K-split partials, host
     // staging). Its release threshold is unbounded, so memory freed by one
     // call stays in the pool for the next instead of going back to the driver
@@ -65,11 +66,12 @@ struct DeviceState {
     hipMemPool_t pool = nullptr;
 };
 
-std::mutex g_mu;  // guards g_blobs, g_next, g_dev
+std::mutex g_mu;  // guards g_blobs, g_next, g_dev, g_budget
 std::unordered_map<uint64_t, DevBlob> g_blobs;
 uint64_t g_next = 1;
 DeviceState g_dev[64];
 int g_current = -1;
+uint64_t g_budget = 0;  // wv_set_weight_budget: per-device cap on blob bytes, 0 = none
 
 int ensure_device_locked(int dev) {
     int n = 0;
@@ -839,8 +841,22 @@ int wv_blob_upload_flags(int format, int64_t rows, int64_t cols, int32_t block_w
             b.n_scales = int64_t(n_scales);
         }
     }
+    // Reserve the bytes against the weight budget before allocating them.
+    const uint64_t bytes = std::max<size_t>(img.bytes.size(), 256);
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        uint64_t& res = g_dev[b.device].resident;
+        if (g_budget && res + bytes > g_budget)
+            return fail(WV_E_OOM, "wv_blob_upload: weight VRAM budget full (%llu resident + %llu > %llu bytes)",
+                        (unsigned long long)res, (unsigned long long)bytes, (unsigned long long)g_budget);
+        res += bytes;
+    }
     rc = upload_image(img, b);
-    if (rc) return rc;
+    if (rc) {
+        std::lock_guard<std::mutex> lk(g_mu);
+        g_dev[b.device].resident -= bytes;
+        return rc;
+    }
     uint8_t* base = static_cast<uint8_t*>(b.base);
     if (b.layout == LAYOUT_RAW) {
         b.raw = base + o_raw;
@@ -914,10 +930,24 @@ int wv_blob_free(uint64_t handle) {
         if (it == g_blobs.end()) return fail(WV_E_HANDLE, "wv_blob_free: unknown handle %llu", (unsigned long long)handle);
         b = it->second;
         g_blobs.erase(it);
+        g_dev[b.device].resident -= std::max<size_t>(b.device_bytes, 256);
     }
     (void)hipSetDevice(b.device);
     hipError_t e = hipFree(b.base);
     if (e != hipSuccess) return hip_fail(e, "wv_blob_free: hipFree");
+    return WV_OK;
+}
+
+int wv_set_weight_budget(uint64_t bytes) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    g_budget = bytes;
+    return WV_OK;
+}
+
+int wv_weight_bytes(uint64_t* resident, uint64_t* budget) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (resident) *resident = g_current >= 0 ? g_dev[g_current].resident : 0;
+    if (budget) *budget = g_budget;
     return WV_OK;
 }
 
