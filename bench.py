@@ -89,6 +89,10 @@ DECODE = {
     "decode_32l": dict(n_layers=32, hidden=4096, n_heads=32, n_kv_heads=8, head_dim=128, ffn=14336, vocab=32000,
                        kv=2048, distinct_layers=4),
 }
+# The device prompt forward (wv_decoder_prefill) of the same model: one step
+# = one n-token prompt through all layers, its caches written, the next token
+# chosen (model/transformer/forward.go:26-90 ForwardTokens).
+PROMPT = {f"prompt_32l_{n}": dict(DECODE["decode_32l"], prompt=n) for n in (32, 128, 512)}
 # HBM bytes per decode token: the sum over one token's launches of
 # 1.9993 * FETCH_SIZE + WRITE_SIZE (per-launch medians of `rocprofv3 --pmc`
 # runs of `bench.py --no-cpu --workload decode_32l`; the launches and
@@ -247,7 +251,7 @@ def main():
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--workload", default="q4k_4096x14336",
-                    choices=sorted(WORKLOADS) + sorted(PREFILL) + sorted(MATVECT) + sorted(DECODE) + sorted(PROBE))
+                    choices=sorted(WORKLOADS) + sorted(PREFILL) + sorted(MATVECT) + sorted(DECODE) + sorted(PROMPT) + sorted(PROBE))
     ap.add_argument("--cpu-budget-s", type=float, default=10.0)
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -281,6 +285,9 @@ def main():
         return matvect_main(args, torch, wv)
     if args.workload in DECODE:
         print(json.dumps(decode_run(args, wv, args.workload, args.steps, args.warmup, not args.no_cpu)), flush=True)
+        return
+    if args.workload in PROMPT:
+        print(json.dumps(prompt_run(args, wv, args.workload)), flush=True)
         return
     fmt, rows, cols, desc = WORKLOADS[args.workload]
     ternary = fmt in wv.NATIVE
@@ -646,10 +653,12 @@ def matvect_main(args, torch, wv):
     print(json.dumps(result), flush=True)
 
 
-def decode_run(args, wv, workload, steps, warmup, with_cpu):
-    """One step = one greedy decode token of the whole 32-layer model at KV length 2048."""
+def build_decoder(wv, spec, fill_kv):
+    """The synthetic 32-layer Q4_K model of BASELINE config 5, resident on the
+    device: `distinct_layers` distinct layers of N(0, 0.02) weights cycled over
+    the layers, unit norm weights, an N(0, 1) embedding table; with fill_kv,
+    KV cache rows 0..kv-2 N(0, 1)."""
     from welvet_amd.decode import Config, Decoder
-    spec = DECODE[workload]
     kv = spec["kv"]
     cfg = Config(n_layers=spec["n_layers"], hidden=spec["hidden"], n_heads=spec["n_heads"],
                  n_kv_heads=spec["n_kv_heads"], head_dim=spec["head_dim"], ffn=spec["ffn"], vocab=spec["vocab"],
@@ -679,12 +688,21 @@ def decode_run(args, wv, workload, steps, warmup, with_cpu):
         bl = [wv.upload(p) for p in packed_sets[L % len(packed_sets)]]
         blobs += bl
         dec.set_layer(L, bl, np.ones(cfg.hidden, np.float32), np.ones(cfg.hidden, np.float32))
-        k = rng.standard_normal((kv - 1, cfg.kv_dim), dtype=np.float32)
-        v = rng.standard_normal((kv - 1, cfg.kv_dim), dtype=np.float32)
-        dec.set_kv(L, 0, k, v)
+        if fill_kv:
+            k = rng.standard_normal((kv - 1, cfg.kv_dim), dtype=np.float32)
+            v = rng.standard_normal((kv - 1, cfg.kv_dim), dtype=np.float32)
+            dec.set_kv(L, 0, k, v)
     lm = wv.upload(p_lm)
     dec.set_output(lm, np.ones(cfg.hidden, np.float32), emb)
     print(f"[bench] model resident ({time.perf_counter() - t0:.1f} s)", file=sys.stderr, flush=True)
+    return dec, cfg, rng, packed_sets, p_lm, layer_bytes, blobs + [lm]
+
+
+def decode_run(args, wv, workload, steps, warmup, with_cpu):
+    """One step = one greedy decode token of the whole 32-layer model at KV length 2048."""
+    spec = DECODE[workload]
+    kv = spec["kv"]
+    dec, cfg, rng, packed_sets, p_lm, layer_bytes, owned = build_decoder(wv, spec, True)
     dec.use_graph(True)
     pos, tok = kv - 1, 1
     steps = max(8, min(steps, 200))
@@ -753,7 +771,43 @@ def decode_run(args, wv, workload, steps, warmup, with_cpu):
                       f"f64 attention over {kv} positions, x{cfg.n_layers} layers, plus the LM head: "
                       f"{tok_s * 1e3:.1f} ms per token"}
     dec.free()
-    for b in blobs + [lm]:
+    for b in owned:
+        b.free()
+    return result
+
+
+def prompt_run(args, wv, workload):
+    """One step = one n-token prompt through the whole 32-layer model on the
+    device (wv_decoder_prefill: every layer's projections on the prefill GEMM,
+    causal attention over the block, the KV caches written, the last row's
+    logits and next token)."""
+    spec = PROMPT[workload]
+    n = spec["prompt"]
+    dec, cfg, rng, packed_sets, p_lm, layer_bytes, owned = build_decoder(wv, spec, False)
+    toks = rng.integers(0, cfg.vocab, n).astype(np.int32)
+    reps = max(3, min(args.steps, 20))
+    for _ in range(max(1, min(args.warmup, 3))):
+        dec.prefill(toks, 0)
+    t1 = time.perf_counter()
+    for _ in range(reps):
+        nxt = dec.prefill(toks, 0)
+    dt = (time.perf_counter() - t1) / reps
+    flops = 2.0 * n * (cfg.n_layers * sum(p.rows * p.cols for p in packed_sets[0]) + p_lm.rows * p_lm.cols / n)
+    result = {
+        "metric": f"prompt forward tokens/s, 32-layer Q4_K decoder, {n}-token prompt",
+        "value": round(n / dt, 1), "unit": "tokens/s", "n_gpus": 1, "steps": reps, "warmup": 1,
+        "ms_per_step": round(dt * 1e3, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32 activations, Q4_K weights (fp16 MFMA projections), f32 KV cache",
+        "data": "synthetic random init as decode_32l; prompt token ids uniform over the vocabulary",
+        "config": {"workload": f"32-layer decoder prompt forward, {n} tokens from position 0, hidden 4096, "
+                               "32/8 heads x 128, SwiGLU 14336, vocab 32000", "prompt": n,
+                   "next_token": int(nxt)},
+        "roofline": {"bound": "mfma", "achieved": round(flops / dt / 1e12, 1), "peak": 2500.0, "unit": "TFLOP/s",
+                     "frac": round(flops / dt / 1e12 / 2500.0, 4), "traffic": None,
+                     "note": "projection FLOPs only (the LM head for the last row); host-timed, synchronous calls"},
+    }
+    dec.free()
+    for b in owned:
         b.free()
     return result
 

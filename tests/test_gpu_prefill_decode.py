@@ -64,8 +64,14 @@ def check_token(tok, rl, tol):
 CASES = [("Q4_K", 33, 2e-3), ("Q4_K", 300, 2e-3), ("Q6_K", 33, 2e-3), ("Q8_0", 8, 1e-5)]
 
 
+# Head dims and heads: G = nh / nkv query heads per KV head. The MFMA
+# attention (head dims 64 and 128, G = 1, 2, 4, 8) maps G heads of 128 / G
+# positions to a block's rows; G = 3 takes the scalar kernel.
+HEADS = [(64, 8, 2), (128, 4, 1), (64, 8, 8), (128, 8, 4), (64, 8, 1), (64, 6, 2)]
+
+
 @pytest.mark.parametrize("fmt,n,tol", CASES)
-@pytest.mark.parametrize("hd,nh,nkv", [(64, 8, 2), (128, 4, 1)])
+@pytest.mark.parametrize("hd,nh,nkv", HEADS)
 def test_prefill_then_decode(fmt, n, tol, hd, nh, nkv):
     print(f"[gpu] prefill {fmt} n={n} hd={hd} heads {nh}/{nkv}", flush=True)
     cfg = Config(n_layers=2, hidden=512, n_heads=nh, n_kv_heads=nkv, head_dim=hd, ffn=1024, vocab=500, max_seq=320)

@@ -884,6 +884,151 @@ __global__ void __launch_bounds__(256) k_attn_prefill(const float* __restrict__ 
     }
 }
 
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// The same causal GQA attention for a whole prompt block on f32 MFMA
+// (v_mfma_f32_32x32x2_f32: f32 products and sums, so the scores carry no
+// fp16 rounding), flash-attention style. Block (kvh, qb) takes prompt rows
+// qb*QP .. qb*QP + QP - 1 (QP = 128 / G positions) for the G query heads of KV
+// head kvh: 4 waves of 32 rows, row R = 32*wave + lane % 32 -> position
+// qb*QP + R / G, head kvh*G + R % G. Key tiles of 32 positions, up to the
+// block's last position, go through LDS once for all 128 rows:
+//   * S^T = K Q^T (keys x rows): A = K from LDS (lane l: key l % 32, dims
+//     (HD/2)*(l/32) + st), B = Q^T from registers (the lane's own row, the same
+//     dims, pre-scaled by 1/sqrt(HD)); the accumulator holds, in lane l, row
+//     l % 32 and keys 8*(r/4) + 4*(l/32) + r%4 of the tile (r < 16);
+//   * so each lane's softmax is over its own registers plus the partner lane
+//     l ^ 32 (one lane swap for the max and one for the sum), with the running
+//     max, sum and rescale per row in the lane that owns the row;
+//   * O^T += V^T P^T (dims x rows): A = V^T from LDS (stored transposed, keys
+//     contiguous), B = P^T, which is the lane's probability registers as they
+//     stand: step st pairs keys 8*(st/4) + 4*h + st%4, h = 0, 1 (lane halves).
+// Keys past the causal end are masked to -inf; key rows past the last
+// written cache row load that row instead (never stale memory), weighted 0.
+template <int HD, int G>
+__global__ void __launch_bounds__(256) k_attn_prefill_mf(const float* __restrict__ q, const float* __restrict__ kc,
+                                                         const float* __restrict__ vc, float* __restrict__ out, int n,
+                                                         int n_heads, int max_seq, int pos0, float scale) {
+    constexpr int QP = 128 / G, KT = 32, HH = HD / 2, NT = HD / 32;
+    constexpr int KS = HD + 4;   // K row stride in LDS (floats)
+    constexpr int VS = KT + 4;   // V^T row stride (one row per dim)
+    __shared__ __attribute__((aligned(16))) float ks[KT * KS];
+    __shared__ __attribute__((aligned(16))) float vt[HD * VS];
+    const int kvh = blockIdx.x, qb = blockIdx.y;
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63, h = lane >> 5, j = lane & 31;
+    const int R = 32 * wave + j;
+    const int srow = min(qb * QP + R / G, n - 1);  // prompt row of this lane's query row (clamped rows store nothing)
+    const bool live = qb * QP + R / G < n;
+    const int head = kvh * G + R % G;
+    const int qd = n_heads * HD;
+    const int p_row = pos0 + srow;  // this row's position: keys 0..p_row
+    const int last_pos = pos0 + min(n, qb * QP + QP) - 1;  // the block's last position
+    // Q^T operand: this row's dims HH*h .. HH*h + HH - 1, scaled
+    float qv[HH];
+    {
+        const float4* qr = reinterpret_cast<const float4*>(q + int64_t(srow) * qd + int64_t(head) * HD + HH * h);
+#pragma unroll
+        for (int i = 0; i < HH / 4; ++i) {
+            const float4 v4 = qr[i];
+            qv[4 * i] = v4.x * scale;
+            qv[4 * i + 1] = v4.y * scale;
+            qv[4 * i + 2] = v4.z * scale;
+            qv[4 * i + 3] = v4.w * scale;
+        }
+    }
+    f32x16 o[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[nt][r] = 0.f;
+    float m_run = -INFINITY, l_run = 0.f;
+    const float* kb = kc + int64_t(kvh) * max_seq * HD;
+    const float* vb = vc + int64_t(kvh) * max_seq * HD;
+    const int ntiles = last_pos / KT + 1;
+    for (int kt = 0; kt < ntiles; ++kt) {
+        __syncthreads();  // the previous tile's readers are done
+        // K rows into ks (row-major), V rows into vt (transposed: vt[dim][key])
+        for (int i = t; i < KT * HD / 4; i += 256) {
+            const int key = i / (HD / 4), c4 = i % (HD / 4);
+            const int krow = min(kt * KT + key, last_pos);
+            const float4 kk = reinterpret_cast<const float4*>(kb + int64_t(krow) * HD)[c4];
+            const float4 vv = reinterpret_cast<const float4*>(vb + int64_t(krow) * HD)[c4];
+            *reinterpret_cast<float4*>(&ks[key * KS + 4 * c4]) = kk;
+            vt[(4 * c4) * VS + key] = vv.x;
+            vt[(4 * c4 + 1) * VS + key] = vv.y;
+            vt[(4 * c4 + 2) * VS + key] = vv.z;
+            vt[(4 * c4 + 3) * VS + key] = vv.w;
+        }
+        __syncthreads();
+        // S^T = K Q^T
+        f32x16 sacc;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sacc[r] = 0.f;
+        const float* krow = ks + j * KS + HH * h;
+#pragma unroll
+        for (int st4 = 0; st4 < HH / 4; ++st4) {
+            const float4 k4 = *reinterpret_cast<const float4*>(krow + 4 * st4);
+            sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(k4.x, qv[4 * st4], sacc, 0, 0, 0);
+            sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(k4.y, qv[4 * st4 + 1], sacc, 0, 0, 0);
+            sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(k4.z, qv[4 * st4 + 2], sacc, 0, 0, 0);
+            sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(k4.w, qv[4 * st4 + 3], sacc, 0, 0, 0);
+        }
+        // mask, running max and sum of this lane's row
+        float pv[16];
+        float mt = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int key = kt * KT + 8 * (r >> 2) + 4 * h + (r & 3);
+            pv[r] = key <= p_row ? sacc[r] : -INFINITY;
+            mt = fmaxf(mt, pv[r]);
+        }
+        {
+            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt), false, false);
+            mt = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+        }
+        const float m_new = fmaxf(m_run, mt);
+        float ps = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            pv[r] = pv[r] == -INFINITY ? 0.f : expf(pv[r] - m_new);
+            ps += pv[r];
+        }
+        {
+            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(ps), __float_as_uint(ps), false, false);
+            ps = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+        }
+        const float alpha = m_run == -INFINITY ? 0.f : expf(m_run - m_new);
+        l_run = l_run * alpha + ps;
+        m_run = m_new;
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[nt][r] *= alpha;
+        // O^T += V^T P^T
+#pragma unroll
+        for (int a4 = 0; a4 < 4; ++a4) {
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                const float4 v4 = *reinterpret_cast<const float4*>(&vt[(32 * nt + j) * VS + 8 * a4 + 4 * h]);
+                o[nt] = __builtin_amdgcn_mfma_f32_32x32x2f32(v4.x, pv[4 * a4], o[nt], 0, 0, 0);
+                o[nt] = __builtin_amdgcn_mfma_f32_32x32x2f32(v4.y, pv[4 * a4 + 1], o[nt], 0, 0, 0);
+                o[nt] = __builtin_amdgcn_mfma_f32_32x32x2f32(v4.z, pv[4 * a4 + 2], o[nt], 0, 0, 0);
+                o[nt] = __builtin_amdgcn_mfma_f32_32x32x2f32(v4.w, pv[4 * a4 + 3], o[nt], 0, 0, 0);
+            }
+        }
+    }
+    if (!live) return;
+    // lane l holds O^T[32nt + 8(r/4) + 4h + r%4][row l % 32]: four consecutive dims per r/4
+    const float inv = 1.0f / l_run;
+    float* orow = out + int64_t(srow) * qd + int64_t(head) * HD;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+            *reinterpret_cast<float4*>(orow + 32 * nt + 8 * a + 4 * h) =
+                make_float4(o[nt][4 * a] * inv, o[nt][4 * a + 1] * inv, o[nt][4 * a + 2] * inv, o[nt][4 * a + 3] * inv);
+}
+
 // ---------------------------------------------------------------------------
 // Decoder object
 // ---------------------------------------------------------------------------
@@ -1224,6 +1369,35 @@ int ensure_prefill(Decoder& d, int n) {
 // RMSNorm of every row, Q/K/V for the block, RoPE and the KV append, causal
 // attention, O + residual, RMSNorm, SwiGLU + residual; then the final norm,
 // LM head and argmax of the last row into the decoder state (state[2]).
+// The MFMA attention of a prompt block, for head dims 64 and 128 and 1, 2, 4
+// or 8 query heads per KV head; false: the shape takes k_attn_prefill.
+bool launch_attn_prefill_mf(Decoder& d, Layer& ly, int n, int pos0, float scale) {
+    const wv_decoder_config& c = d.c;
+    const int G = c.n_heads / c.n_kv_heads, hd = c.head_dim;
+    if ((hd != 64 && hd != 128) || (G != 1 && G != 2 && G != 4 && G != 8)) return false;
+    const dim3 grid(unsigned(c.n_kv_heads), unsigned((n + 128 / G - 1) / (128 / G)));
+    auto go = [&](auto kern) {
+        hipLaunchKernelGGL(kern, grid, dim3(256), 0, d.stream, d.pq, ly.kc, ly.vc, d.patt, n, c.n_heads, c.max_seq, pos0,
+                           scale);
+    };
+    if (hd == 128) {
+        switch (G) {
+        case 1: go(k_attn_prefill_mf<128, 1>); break;
+        case 2: go(k_attn_prefill_mf<128, 2>); break;
+        case 4: go(k_attn_prefill_mf<128, 4>); break;
+        default: go(k_attn_prefill_mf<128, 8>); break;
+        }
+    } else {
+        switch (G) {
+        case 1: go(k_attn_prefill_mf<64, 1>); break;
+        case 2: go(k_attn_prefill_mf<64, 2>); break;
+        case 4: go(k_attn_prefill_mf<64, 4>); break;
+        default: go(k_attn_prefill_mf<64, 8>); break;
+        }
+    }
+    return true;
+}
+
 int enqueue_prefill(Decoder& d, int n, int pos0) {
     const wv_decoder_config& c = d.c;
     const int hd = c.head_dim, hidden = c.hidden;
@@ -1241,13 +1415,15 @@ int enqueue_prefill(Decoder& d, int n, int pos0) {
         if (e) return e;
         hipLaunchKernelGGL(k_rope_kv_rows, dim3(unsigned(n)), dim3(256), 0, d.stream, d.pq, d.pk, d.pv, ly.kc, ly.vc,
                            d.freq_div, c.n_heads, c.n_kv_heads, hd, c.max_seq, pos0);
-        const dim3 ag(unsigned(c.n_kv_heads), unsigned(n));
-        if (hd == 128)
-            hipLaunchKernelGGL(k_attn_prefill<128>, ag, dim3(256), 0, d.stream, d.pq, ly.kc, ly.vc, d.patt, c.n_heads,
-                               c.n_kv_heads, c.max_seq, pos0, scale);
-        else
-            hipLaunchKernelGGL(k_attn_prefill<64>, ag, dim3(256), 0, d.stream, d.pq, ly.kc, ly.vc, d.patt, c.n_heads,
-                               c.n_kv_heads, c.max_seq, pos0, scale);
+        if (!launch_attn_prefill_mf(d, ly, n, pos0, scale)) {
+            const dim3 ag(unsigned(c.n_kv_heads), unsigned(n));
+            if (hd == 128)
+                hipLaunchKernelGGL(k_attn_prefill<128>, ag, dim3(256), 0, d.stream, d.pq, ly.kc, ly.vc, d.patt,
+                                   c.n_heads, c.n_kv_heads, c.max_seq, pos0, scale);
+            else
+                hipLaunchKernelGGL(k_attn_prefill<64>, ag, dim3(256), 0, d.stream, d.pq, ly.kc, ly.vc, d.patt,
+                                   c.n_heads, c.n_kv_heads, c.max_seq, pos0, scale);
+        }
         e = prefill_proj(d, ly.w[3], d.patt, d.pt, n);
         if (e) return e;
         hipLaunchKernelGGL(k_add, blocks(nh), dim3(256), 0, d.stream, d.ph, d.pt, int(nh));
