@@ -92,7 +92,7 @@ DECODE = {
 # The device prompt forward (wv_decoder_prefill) of the same model: one step
 # = one n-token prompt through all layers, its caches written, the next token
 # chosen (model/transformer/forward.go:26-90 ForwardTokens).
-PROMPT = {f"prompt_32l_{n}": dict(DECODE["decode_32l"], prompt=n) for n in (32, 128, 512)}
+PROMPT = {f"prompt_32l_{n}": dict(DECODE["decode_32l"], prompt=n) for n in (32, 128, 512, 2047)}
 # HBM bytes per decode token: the sum over one token's launches of
 # 1.9993 * FETCH_SIZE + WRITE_SIZE (per-launch medians of `rocprofv3 --pmc`
 # runs of `bench.py --no-cpu --workload decode_32l`; the launches and
