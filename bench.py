@@ -109,7 +109,7 @@ DECODE_TRAFFIC_SOURCE = "profiles/decode_32l_q4k_kernel_trace.txt"
 COPY_FETCH_SCALE = 65536.0 / 32779.5
 COPY_WRITE_SCALE = 65536.0 / 65536.0
 PMC_KIB = {
-    "q4k_4096x14336": (18942.12, 56.0),
+    "q4k_4096x14336": (18931.62, 56.0),
     "q4k_4096x4096": (5499.5, 16.0),
     "q4k_14336x4096": (19109.5, 16.0),
     "q8_0_4096x4096": (9325.5, 16.0),

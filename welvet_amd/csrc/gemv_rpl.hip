@@ -37,6 +37,8 @@ namespace {
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x16 __attribute__((ext_vector_type(16)));
 
 // Streaming (non-temporal) loads: weights are read once per launch.
 __device__ __forceinline__ uint4 ld_stream(const uint4* p) {
@@ -869,10 +871,21 @@ __global__ void __launch_bounds__(1024) k_gemv_rpl(RplArgs a, const float* __res
     if (valid) a.partial[(int64_t(b) * a.ksplit + ks) * rows_pad + row] = sum;
 }
 
+// k_gemv_q4k's x records: 32 dwords per chunk (24 of digit planes, 4 zero,
+// then 2^-s and the two group sums), 8 to a wave's slice. A 40-dword stride,
+// which puts the 32 dwords of one staging store in 32 distinct LDS banks
+// (records 0, 2, 4 and 6 share banks at 32), ran the same.
+constexpr int kQ4kRec = 32, kQ4kSlice = 8 * kQ4kRec + 16;
+
 // Q4_K forward for the one-lane-per-row plan (L = 1, S = 1; the headline
-// 4096->14336 and the decoder's gate||up). Same layout, work split and x
-// planes as k_gemv_rpl<RplQ4KI, 1, 1, 4>, with a shorter instruction stream
-// per 32-column chunk (54 VALU against 64):
+// 4096->14336). Same layout and work split as k_gemv_rpl<RplQ4KI, 1, 1, 4>,
+// the same 24-bit fixed-point x per 32-column chunk, and the same integer
+// group dots, taken on the i8 matrix cores instead of v_dot4:
+//   * x is staged as three signed digit planes (X = d0 + 256 d1 + 65536 d2),
+//     the A operand of v_mfma_i32_32x32x32_i8; the codes, lane-swapped and
+//     widened to bytes, are the B operand, so one MFMA gives 32 rows x 6
+//     (plane, group) dots of a chunk and each step takes two chunks in four
+//     MFMAs (about 62 VALU per two chunks against 108 with v_dot4);
 //   * the chunk's codes are one contiguous 8 KiB run per super-block (Q4_K's
 //     super-block-major order), addressed from one base with constant
 //     offsets, and the wave is either active or not for its whole life (no
@@ -883,9 +896,8 @@ __global__ void __launch_bounds__(1024) k_gemv_rpl(RplArgs a, const float* __res
 //   * the mins accumulate as sum_g (m_g + 128)*S_g over the super-block (S_g
 //     the 16-column sums of x), and the -128*sum(x) correction is taken once
 //     from the wave's total of x.
-// The three plane accumulators of each group stay independent: a Horner
-// chain (plane 2, << 8, plane 1, << 8, plane 0) saves the combining shifts
-// but serializes the dot4 instructions and ran 12.8 against 8.3 us.
+// The integer dots are exact, so the rows equal the v_dot4 kernel's up to the
+// association of the float sums.
 __global__ void __launch_bounds__(1024) k_gemv_q4k(RplArgs a, const float* __restrict__ x, float* __restrict__ y) {
     extern __shared__ float4 sm4[];
     const int W = blockDim.x >> 6;
@@ -935,9 +947,12 @@ __global__ void __launch_bounds__(1024) k_gemv_q4k(RplArgs a, const float* __res
         xv.w = float(double(xv0.w) * inv * double(gv.w));
     }
 
-    // Stage x in this wave's LDS slice: per chunk c, 24 dwords of X byte
-    // planes [plane][lo w0..3 | hi w0..3] (as RplQ4KI) and (2^-s, s0, s1).
-    constexpr int kSlice = 256 + 16;
+    // Stage x in this wave's LDS slice, one kRec-dword record per chunk c: the
+    // X digit planes as MFMA A-operand rows [plane][group][lo w0, w1 | hi w0, w1]
+    // (16 bytes per plane and 16-column group), 4 zero dwords, then
+    // (2^-s, s0, s1). The digits are signed: X = d0 + 256 d1 + 65536 d2 with
+    // every d in [-128, 127], from the bytes of X + 0x808080 less 128 each.
+    constexpr int kRec = kQ4kRec, kSlice = kQ4kSlice;
     float* xs = reinterpret_cast<float*>(sm4) + wave * kSlice;
     float* part = reinterpret_cast<float*>(sm4) + W * kSlice;
     const float lsum = (xv.x + xv.y) + (xv.z + xv.w);
@@ -954,73 +969,92 @@ __global__ void __launch_bounds__(1024) k_gemv_q4k(RplArgs a, const float* __res
         int e = 0;
         frexpf(m, &e);
         const int sh = m > 0.f ? 22 - e : 0;  // |x| * 2^sh < 2^22
-        const int X0 = int(rintf(ldexpf(xv.x, sh))), X1 = int(rintf(ldexpf(xv.y, sh)));
-        const int X2 = int(rintf(ldexpf(xv.z, sh))), X3 = int(rintf(ldexpf(xv.w, sh)));
-        uint16_t* h16 = reinterpret_cast<uint16_t*>(xs + c * 28);
-        const int w = q >> 1, half = q & 1;
+        constexpr int kBias = 0x808080;
+        const int X0 = int(rintf(ldexpf(xv.x, sh))) + kBias, X1 = int(rintf(ldexpf(xv.y, sh))) + kBias;
+        const int X2 = int(rintf(ldexpf(xv.z, sh))) + kBias, X3 = int(rintf(ldexpf(xv.w, sh))) + kBias;
+        uint16_t* h16 = reinterpret_cast<uint16_t*>(xs + c * kRec);
+        const int g = q >> 2, ew = (q >> 1) & 1, half = q & 1;  // code word 2g + ew of the chunk
 #pragma unroll
         for (int pl = 0; pl < 3; ++pl) {
             const uint32_t sel = uint32_t(pl) | (uint32_t(4 + pl) << 8) | 0x0C0C0000u;
-            const uint32_t blo = __builtin_amdgcn_perm(uint32_t(X2), uint32_t(X0), sel);
-            const uint32_t bhi = __builtin_amdgcn_perm(uint32_t(X3), uint32_t(X1), sel);
-            h16[(pl * 8 + w) * 2 + half] = uint16_t(blo);
-            h16[(pl * 8 + 4 + w) * 2 + half] = uint16_t(bhi);
+            const uint32_t blo = __builtin_amdgcn_perm(uint32_t(X2), uint32_t(X0), sel) ^ 0x8080u;
+            const uint32_t bhi = __builtin_amdgcn_perm(uint32_t(X3), uint32_t(X1), sel) ^ 0x8080u;
+            h16[((pl * 2 + g) * 4 + ew) * 2 + half] = uint16_t(blo);
+            h16[((pl * 2 + g) * 4 + 2 + ew) * 2 + half] = uint16_t(bhi);
         }
         const float s1 = half_mirror(gsum);
         if (q == 0) {
-            float* xm = xs + c * 28 + 24;
+            float* xm = xs + c * kRec + 28;
             xm[0] = ldexpf(1.0f, -sh);
             xm[1] = gsum;
             xm[2] = s1;
         }
+        if (q == 1) *reinterpret_cast<uint4*>(xs + c * kRec + 24) = make_uint4(0u, 0u, 0u, 0u);
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
+    // Two chunks per step on v_mfma_i32_32x32x32_i8, D = X-planes x codes^T.
+    // B: after a lane swap, lanes 0-31 hold rows 0-31 (or 32-63) with their
+    // first 16-column group, lanes 32-63 the same rows' second group; the
+    // nibbles widen to bytes. A: lane (i, h) = (l & 31, l >> 5) carries the
+    // 16 digit bytes of plane p, group h of one chunk when row i of D is a
+    // slot n = 6e + 3g + p with g = h, else zeros. Rows 0-3, 8-11, 16-19 take
+    // the slots of rows 0-31 of the weights, rows 4-7, 12-15, 20-23 those of
+    // rows 32-63, so after both MFMAs accumulator r of lane l is slot r of row l.
+    const int ir = lane & 31;
+    const int n = (ir >> 3) * 4 + (ir & 3);
+    const int en = n / 6, gn = (n % 6) / 3, pn = n % 3, setn = (ir >> 2) & 1;
+    const bool dlane = ir < 24 && gn == (lane >> 5);
+    int ao[2][2];  // [weight rows 0-31 | 32-63][chunk of the pair]: dword offset in the record
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+#pragma unroll
+        for (int e = 0; e < 2; ++e) ao[st][e] = (dlane && setn == st && en == e) ? (pn * 2 + gn) * 4 : 24;
+
     const uint32_t gw[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};  // (u'0, u'1, m0, m1) per chunk
     float pacc = 0.f, macc = 0.f;
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
-        if (t + D < 8) ch[t + D] = ld_stream(cp + (t + D) * 64);
+    for (int t0 = 0; t0 < 8; t0 += 2) {
+        if (t0 + D < 8) {
+            ch[t0 + D] = ld_stream(cp + (t0 + D) * 64);
+            ch[t0 + D + 1] = ld_stream(cp + (t0 + D + 1) * 64);
+        }
         __builtin_amdgcn_sched_barrier(0);
-        // Keeps each step's LDS reads and arithmetic in its step: without it
-        // the compiler hoists later steps' x reads and spills.
         asm volatile("" ::: "memory");
-        const uint4* xq = reinterpret_cast<const uint4*>(xs + t * 28);
-        uint32_t xi[24];
+        i32x16 acc = {};
 #pragma unroll
-        for (int k = 0; k < 6; ++k) {
-            const uint4 tq = xq[k];
-            xi[4 * k] = tq.x;
-            xi[4 * k + 1] = tq.y;
-            xi[4 * k + 2] = tq.z;
-            xi[4 * k + 3] = tq.w;
-        }
-        const float4 xm = reinterpret_cast<const float4*>(xq)[6];
-        const uint32_t wd[4] = {ch[t].x, ch[t].y, ch[t].z, ch[t].w};
-        int A[2][3] = {{0, 0, 0}, {0, 0, 0}};
+        for (int e = 0; e < 2; ++e) {
+            const int t = t0 + e;
+            const float* xr = xs + t * kRec;
+            const i32x4 A0 = *reinterpret_cast<const i32x4*>(xr + ao[0][e]);
+            const i32x4 A1 = *reinterpret_cast<const i32x4*>(xr + ao[1][e]);
+            const auto ka = __builtin_amdgcn_permlane32_swap(ch[t].x, ch[t].z, false, false);
+            const auto kb = __builtin_amdgcn_permlane32_swap(ch[t].y, ch[t].w, false, false);
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
-            const int gi = w >> 1;
-            const uint32_t lo = wd[w] & 0x0F0F0F0Fu, hi = (wd[w] >> 4) & 0x0F0F0F0Fu;
-            A[gi][0] = int(__builtin_amdgcn_udot4(lo, xi[w], uint32_t(A[gi][0]), false));
-            A[gi][0] = int(__builtin_amdgcn_udot4(hi, xi[4 + w], uint32_t(A[gi][0]), false));
-            A[gi][1] = int(__builtin_amdgcn_udot4(lo, xi[8 + w], uint32_t(A[gi][1]), false));
-            A[gi][1] = int(__builtin_amdgcn_udot4(hi, xi[12 + w], uint32_t(A[gi][1]), false));
-            A[gi][2] = __builtin_amdgcn_sdot4(int(lo), int(xi[16 + w]), A[gi][2], false);
-            A[gi][2] = __builtin_amdgcn_sdot4(int(hi), int(xi[20 + w]), A[gi][2], false);
+            for (int T = 0; T < 2; ++T) {
+                const uint32_t wa = ka[T], wb = kb[T];
+                const i32x4 Bt = {int(wa & 0x0F0F0F0Fu), int(wb & 0x0F0F0F0Fu), int((wa >> 4) & 0x0F0F0F0Fu),
+                                  int((wb >> 4) & 0x0F0F0F0Fu)};
+                acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(T == 0 ? A0 : A1, Bt, acc, 0, 0, 0);
+            }
         }
-        const int T0 = A[0][0] + (A[0][1] << 8) + (A[0][2] << 16);
-        const int T1 = A[1][0] + (A[1][1] << 8) + (A[1][2] << 16);
-        const uint32_t g = gw[t];
-        const float P = fmaf(ub1(g), float(T1), ub0(g) * float(T0));
-        pacc = fmaf(P, xm.x, pacc);
-        // A NaN or infinite x reaches the row through these float group sums
-        // (the fixed-point planes would turn it into a finite value).
-        const uint32_t gx = g ^ 0x80800000u;  // bytes 2, 3: m + 128 as unsigned
-        macc = fmaf(ub2(gx), xm.y, macc);
-        macc = fmaf(ub3(gx), xm.z, macc);
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int t = t0 + e;
+            const int T0 = acc[6 * e] + acc[6 * e + 1] * 256 + acc[6 * e + 2] * 65536;
+            const int T1 = acc[6 * e + 3] + acc[6 * e + 4] * 256 + acc[6 * e + 5] * 65536;
+            const float4 xm = *reinterpret_cast<const float4*>(xs + t * kRec + 28);
+            const uint32_t g = gw[t];
+            const float P = fmaf(ub1(g), float(T1), ub0(g) * float(T0));
+            pacc = fmaf(P, xm.x, pacc);
+            // A NaN or infinite x reaches the row through these float group sums
+            // (the fixed-point planes would turn it into a finite value).
+            const uint32_t gx = g ^ 0x80800000u;  // bytes 2, 3: m + 128 as unsigned
+            macc = fmaf(ub2(gx), xm.y, macc);
+            macc = fmaf(ub3(gx), xm.z, macc);
+        }
         asm volatile("" : "+v"(pacc), "+v"(macc));
         __builtin_amdgcn_sched_barrier(0);
     }
@@ -1164,14 +1198,15 @@ int launch_rpl_t(const DevBlob& bl, const float* x, float* y, int batch, hipStre
         const float* xb = x + int64_t(b0) * a.nsb * 256;
         float* yb = y + int64_t(b0) * ystride;
         if constexpr (std::is_same<P, RplQ4KI>::value) {
-            // k_gemv_q4k takes 68 VGPRs, so one 16-wave block per CU: it runs
+            // k_gemv_q4k takes 77 VGPRs, so one 16-wave block per CU: it runs
             // the grids that fit the GPU in one pass (the 4096->14336
             // headline, 224 blocks). Larger grids (the decoder's gate||up,
             // 448 blocks, and LM head, 500) keep the 64-VGPR policy kernel,
             // two blocks per CU.
             constexpr int64_t kCUs = 256;  // MI355X
             if (p.L == 1 && p.S == 1 && a.cs_si == 8 && a.cs_j == 1 && int64_t(grid.x) * grid.y * grid.z <= kCUs) {
-                hipLaunchKernelGGL(k_gemv_q4k, grid, dim3(unsigned(64 * p.W)), lds, s, ab, xb, yb);
+                const size_t lq = size_t(p.W) * (kQ4kSlice + 64) * sizeof(float);
+                hipLaunchKernelGGL(k_gemv_q4k, grid, dim3(unsigned(64 * p.W)), lq, s, ab, xb, yb);
                 if (p.ksplit > 1)
                     hipLaunchKernelGGL(k_rpl_ksum, dim3(unsigned(a.rg_count), unsigned(nb)), dim3(64), 0, s, ab, yb);
                 continue;
