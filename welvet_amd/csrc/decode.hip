@@ -97,6 +97,54 @@ __global__ void __launch_bounds__(1024) k_rmsnorm(const float* __restrict__ x, c
     }
 }
 
+// h += a (the residual add, per element as k_add), the updated rows written
+// back, then the RMSNorm of them into y as k_rmsnorm: the prompt forward's add
+// and norm in one pass over the rows. a and y may be the same rows: a block
+// reads its row of a before the barrier and writes y after it.
+__global__ void __launch_bounds__(1024) k_add_rmsnorm(float* __restrict__ h, const float* a,
+                                                      const float* __restrict__ gamma, float* y, int dim, double eps) {
+    __shared__ double part[16];
+    h += int64_t(blockIdx.x) * dim;
+    a += int64_t(blockIdx.x) * dim;
+    y += int64_t(blockIdx.x) * dim;
+    constexpr int R = 4;
+    const int n4 = dim / 4;
+    float4 xv[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int i = threadIdx.x + 1024 * r;
+        xv[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (i < n4) {
+            const float4 hv = reinterpret_cast<const float4*>(h)[i], av = reinterpret_cast<const float4*>(a)[i];
+            xv[r] = make_float4(hv.x + av.x, hv.y + av.y, hv.z + av.z, hv.w + av.w);
+        }
+    }
+    double s = 0.0;
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+        s += double(xv[r].x) * xv[r].x + double(xv[r].y) * xv[r].y + double(xv[r].z) * xv[r].z +
+             double(xv[r].w) * xv[r].w;
+    s = wave_total_f64(s);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
+    __syncthreads();
+    double tot = 0.0;
+    for (int w = 0; w < 16; ++w) tot += part[w];
+    const double inv = 1.0 / sqrt(tot / double(dim) + eps);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int i = threadIdx.x + 1024 * r;
+        if (i >= n4) break;
+        reinterpret_cast<float4*>(h)[i] = xv[r];
+        const float4 g = gamma ? reinterpret_cast<const float4*>(gamma)[i] : make_float4(1.f, 1.f, 1.f, 1.f);
+        float4 o;
+        o.x = float(double(xv[r].x) * inv * double(g.x));
+        o.y = float(double(xv[r].y) * inv * double(g.y));
+        o.z = float(double(xv[r].z) * inv * double(g.z));
+        o.w = float(double(xv[r].w) * inv * double(g.w));
+        reinterpret_cast<float4*>(y)[i] = o;
+    }
+}
+
 // The KV caches are head-major, [n_kv][max_seq][HD], so the K (and V) rows of
 // one chunk of one head are one contiguous kChunk*HD*4-byte run.
 //
@@ -1081,8 +1129,9 @@ struct Decoder {
     int pcap = 0;
     float *ph = nullptr, *pn = nullptr, *pq = nullptr, *pk = nullptr, *pv = nullptr, *patt = nullptr;
     float *pg = nullptr, *pu = nullptr, *pt = nullptr, *pscratch = nullptr;
+    float* pxh = nullptr;  // the fp16 GEMM operand shared by the projections of one input, then its row factors
     int32_t* ptok = nullptr;
-    size_t pscratch_floats = 0;
+    size_t pscratch_floats = 0, pxh_floats = 0;
 };
 
 std::mutex g_dmu;
@@ -1119,12 +1168,12 @@ void drop_prefill(Decoder& d) {
     for (void* p : {static_cast<void*>(d.ph), static_cast<void*>(d.pn), static_cast<void*>(d.pq),
                     static_cast<void*>(d.pk), static_cast<void*>(d.pv), static_cast<void*>(d.patt),
                     static_cast<void*>(d.pg), static_cast<void*>(d.pu), static_cast<void*>(d.pt),
-                    static_cast<void*>(d.pscratch), static_cast<void*>(d.ptok)})
+                    static_cast<void*>(d.pscratch), static_cast<void*>(d.pxh), static_cast<void*>(d.ptok)})
         if (p) (void)hipFree(p);
-    d.ph = d.pn = d.pq = d.pk = d.pv = d.patt = d.pg = d.pu = d.pt = d.pscratch = nullptr;
+    d.ph = d.pn = d.pq = d.pk = d.pv = d.patt = d.pg = d.pu = d.pt = d.pscratch = d.pxh = nullptr;
     d.ptok = nullptr;
     d.pcap = 0;
-    d.pscratch_floats = 0;
+    d.pscratch_floats = d.pxh_floats = 0;
 }
 
 void release(Decoder* d) {
@@ -1319,9 +1368,38 @@ int ready(Decoder& d) {
 
 // One projection of a prompt block: the prefill GEMM where the blob has one,
 // the batched GEMVs otherwise.
-int prefill_proj(Decoder& d, const DevBlob& w, const float* x, float* y, int n) {
-    if (gemm_supported(w, n)) return launch_gemm(w, x, y, n, d.stream, d.pscratch);
-    return launch_matvec(w, x, y, n, d.stream, d.pscratch);
+// The GEMM input of a prompt block's projection: its f32 rows (x, and u for
+// the SwiGLU product silu(x) * u) and the operand order of the fp16 copy in
+// d.pxh. Consecutive projections of one input (Q, K, V; gate and up) find the
+// copy made and convert nothing.
+struct PrefillX {
+    const float* x = nullptr;
+    const float* u = nullptr;
+    int64_t cols = 0;
+    int frag = -1;
+};
+
+// y = W x for n prompt rows; with u the input is silu(x) * u. The GEMM takes
+// the shared fp16 copy of its input (made here when cx does not hold it);
+// other blobs take the batched GEMV on f32 rows, with tmp holding the SwiGLU
+// rows.
+int prefill_proj(Decoder& d, PrefillX& cx, const DevBlob& w, const float* x, const float* u, float* y, int n,
+                 float* tmp) {
+    if (gemm_supported(w, n)) {
+        const int frag = gemm_x_frag(w, n) ? 1 : 0;
+        if (cx.x != x || cx.u != u || cx.cols != w.cols || cx.frag != frag) {
+            gemm_convert_x(x, u, int(w.cols), n, frag != 0, d.pxh, d.pxh + gemm_x_floats(w, n), d.stream);
+            cx = PrefillX{x, u, w.cols, frag};
+        }
+        return launch_gemm_xh(w, d.pxh, d.pxh + gemm_x_floats(w, n), y, n, d.stream, d.pscratch);
+    }
+    const float* xin = x;
+    if (u) {
+        const int64_t nin = int64_t(n) * w.cols;
+        hipLaunchKernelGGL(k_silu_mul, dim3(unsigned((nin + 255) / 256)), dim3(256), 0, d.stream, x, u, tmp, int(nin));
+        xin = tmp;
+    }
+    return launch_matvec(w, xin, y, n, d.stream, d.pscratch);
 }
 
 size_t prefill_proj_scratch(const DevBlob& w, int n) {
@@ -1331,9 +1409,13 @@ size_t prefill_proj_scratch(const DevBlob& w, int n) {
 int ensure_prefill(Decoder& d, int n) {
     const wv_decoder_config& c = d.c;
     size_t need_s = 0;
+    size_t need_x = 0;  // the widest fp16 copy of a GEMM input, then its row factors
     for (const Layer& ly : d.layers)
-        for (const DevBlob& w : ly.w) need_s = std::max(need_s, prefill_proj_scratch(w, n));
-    if (n <= d.pcap && need_s <= d.pscratch_floats) return WV_OK;
+        for (const DevBlob& w : ly.w) {
+            need_s = std::max(need_s, prefill_proj_scratch(w, n));
+            if (gemm_supported(w, n)) need_x = std::max(need_x, gemm_x_floats(w, n) + gemm_scale_floats(n));
+        }
+    if (n <= d.pcap && need_s <= d.pscratch_floats && need_x <= d.pxh_floats) return WV_OK;
     drop_prefill(d);
     const size_t qd = size_t(c.n_heads) * c.head_dim, kvd = size_t(c.n_kv_heads) * c.head_dim;
     const size_t wide = std::max({size_t(c.hidden), size_t(c.ffn), qd});
@@ -1350,6 +1432,7 @@ int ensure_prefill(Decoder& d, int n) {
                 {reinterpret_cast<void**>(&d.pu), n * size_t(c.ffn) * 4},
                 {reinterpret_cast<void**>(&d.pt), n * wide * 4},
                 {reinterpret_cast<void**>(&d.pscratch), std::max<size_t>(need_s, 1) * 4},
+                {reinterpret_cast<void**>(&d.pxh), std::max<size_t>(need_x, 1) * 4},
                 {reinterpret_cast<void**>(&d.ptok), size_t(n) * 4}};
     for (auto& b : bufs) {
         const hipError_t e = hipMalloc(b.p, std::max<size_t>(b.bytes, 256));
@@ -1361,6 +1444,7 @@ int ensure_prefill(Decoder& d, int n) {
     }
     d.pcap = n;
     d.pscratch_floats = std::max<size_t>(need_s, 1);
+    d.pxh_floats = std::max<size_t>(need_x, 1);
     return WV_OK;
 }
 
@@ -1402,16 +1486,21 @@ int enqueue_prefill(Decoder& d, int n, int pos0) {
     const wv_decoder_config& c = d.c;
     const int hd = c.head_dim, hidden = c.hidden;
     const float scale = float(1.0 / std::sqrt(double(hd)));
-    const int64_t nh = int64_t(n) * hidden, nf = int64_t(n) * c.ffn;
-    auto blocks = [](int64_t m) { return dim3(unsigned((m + 255) / 256)); };
     hipLaunchKernelGGL(k_embed_rows, dim3(unsigned((hidden + 255) / 256), unsigned(n)), dim3(256), 0, d.stream, d.embed,
                        d.ptok, d.ph, hidden, c.vocab);
     for (int L = 0; L < c.n_layers; ++L) {
         Layer& ly = d.layers[L];
-        hipLaunchKernelGGL(k_rmsnorm, dim3(unsigned(n)), dim3(1024), 0, d.stream, d.ph, ly.attn_norm, d.pn, hidden, c.rms_eps);
-        int e = prefill_proj(d, ly.w[0], d.pn, d.pq, n);
-        if (!e) e = prefill_proj(d, ly.w[1], d.pn, d.pk, n);
-        if (!e) e = prefill_proj(d, ly.w[2], d.pn, d.pv, n);
+        // h += the previous layer's down projection (in pn), then the norm
+        if (L == 0)
+            hipLaunchKernelGGL(k_rmsnorm, dim3(unsigned(n)), dim3(1024), 0, d.stream, d.ph, ly.attn_norm, d.pn, hidden,
+                               c.rms_eps);
+        else
+            hipLaunchKernelGGL(k_add_rmsnorm, dim3(unsigned(n)), dim3(1024), 0, d.stream, d.ph, d.pn, ly.attn_norm, d.pn,
+                               hidden, c.rms_eps);
+        PrefillX cx;  // Q, K and V share one fp16 copy of the normed rows
+        int e = prefill_proj(d, cx, ly.w[0], d.pn, nullptr, d.pq, n, d.pt);
+        if (!e) e = prefill_proj(d, cx, ly.w[1], d.pn, nullptr, d.pk, n, d.pt);
+        if (!e) e = prefill_proj(d, cx, ly.w[2], d.pn, nullptr, d.pv, n, d.pt);
         if (e) return e;
         hipLaunchKernelGGL(k_rope_kv_rows, dim3(unsigned(n)), dim3(256), 0, d.stream, d.pq, d.pk, d.pv, ly.kc, ly.vc,
                            d.freq_div, c.n_heads, c.n_kv_heads, hd, c.max_seq, pos0);
@@ -1424,18 +1513,22 @@ int enqueue_prefill(Decoder& d, int n, int pos0) {
                 hipLaunchKernelGGL(k_attn_prefill<64>, ag, dim3(256), 0, d.stream, d.pq, ly.kc, ly.vc, d.patt,
                                    c.n_heads, c.n_kv_heads, c.max_seq, pos0, scale);
         }
-        e = prefill_proj(d, ly.w[3], d.patt, d.pt, n);
+        cx = PrefillX{};
+        e = prefill_proj(d, cx, ly.w[3], d.patt, nullptr, d.pt, n, nullptr);
         if (e) return e;
-        hipLaunchKernelGGL(k_add, blocks(nh), dim3(256), 0, d.stream, d.ph, d.pt, int(nh));
-        hipLaunchKernelGGL(k_rmsnorm, dim3(unsigned(n)), dim3(1024), 0, d.stream, d.ph, ly.ffn_norm, d.pn, hidden, c.rms_eps);
-        e = prefill_proj(d, ly.w[4], d.pn, d.pg, n);
-        if (!e) e = prefill_proj(d, ly.w[5], d.pn, d.pu, n);
+        hipLaunchKernelGGL(k_add_rmsnorm, dim3(unsigned(n)), dim3(1024), 0, d.stream, d.ph, d.pt, ly.ffn_norm, d.pn,
+                           hidden, c.rms_eps);  // h += O att, then the norm
+        cx = PrefillX{};  // gate and up share one fp16 copy
+        e = prefill_proj(d, cx, ly.w[4], d.pn, nullptr, d.pg, n, d.pt);
+        if (!e) e = prefill_proj(d, cx, ly.w[5], d.pn, nullptr, d.pu, n, d.pt);
         if (e) return e;
-        hipLaunchKernelGGL(k_silu_mul, blocks(nf), dim3(256), 0, d.stream, d.pg, d.pu, d.pt, int(nf));
-        e = prefill_proj(d, ly.w[6], d.pt, d.pn, n);
+        cx = PrefillX{};
+        e = prefill_proj(d, cx, ly.w[6], d.pg, d.pu, d.pn, n, d.pt);  // down(silu(gate) * up), added by the next norm
         if (e) return e;
-        hipLaunchKernelGGL(k_add, blocks(nh), dim3(256), 0, d.stream, d.ph, d.pn, int(nh));
     }
+    // the last layer's residual add, for the one row the LM head reads
+    hipLaunchKernelGGL(k_add, dim3(unsigned((hidden + 255) / 256)), dim3(256), 0, d.stream,
+                       d.ph + int64_t(n - 1) * hidden, d.pn + int64_t(n - 1) * hidden, hidden);
     const float* last = d.ph + int64_t(n - 1) * hidden;
     const float* fin = last;
     if (d.has_final_norm) {

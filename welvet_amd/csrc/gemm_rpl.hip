@@ -440,6 +440,13 @@ __device__ __forceinline__ float row_shift_up(float mx, float* red, float* xscal
     if (t == 0) *xscale_m = ldexpf(1.0f, -sh);
     return ldexpf(1.0f, sh);
 }
+// silu(g) * u of one element, the expression of the SwiGLU kernels
+// (layers/swiglu/cpu.go:41-53).
+__device__ __forceinline__ float silu_mul1(float g, float u) { return g / (1.0f + expf(-g)) * u; }
+__device__ __forceinline__ float4 silu_mul4(float4 g, float4 u) {
+    return make_float4(silu_mul1(g.x, u.x), silu_mul1(g.y, u.y), silu_mul1(g.z, u.z), silu_mul1(g.w, u.w));
+}
+
 // X f32 [M][K] -> fp16 blocks of 8 in the B operands' k order
 // [0,2,4,6,1,3,5,7] (pack_x8), one block per token row:
 // the row's max|x| picks xscale = 2^e with max|x| / xscale in [2^14, 2^15)
@@ -448,10 +455,11 @@ __device__ __forceinline__ float row_shift_up(float mx, float* red, float* xscal
 // load issued before the first use (slots past the row re-read its last block).
 // FRAG writes the A-fragment order of GemmArgs::xh (block i of row m at
 // ((i/2)*mt + m/32)*64 + m%32 + 32*(i%2)); its grid covers the padded rows,
-// which get zeros.
-template <int NR, bool FRAG>
-__global__ void __launch_bounds__(256) k_x_f16r(const float4* __restrict__ x, uint4* __restrict__ xh,
-                                                 float* __restrict__ xscale, int kb8, int M) {
+// which get zeros. SW: x is the gate and u the up projection, and the row
+// converted is silu(x) * u (the SwiGLU product feeding the down projection).
+template <int NR, bool FRAG, bool SW>
+__global__ void __launch_bounds__(256) k_x_f16r(const float4* __restrict__ x, const float4* __restrict__ u,
+                                                 uint4* __restrict__ xh, float* __restrict__ xscale, int kb8, int M) {
     __shared__ float red[4];
     const int m = blockIdx.x, t = threadIdx.x;
     const int mt = (M + 31) / 32;
@@ -466,6 +474,8 @@ __global__ void __launch_bounds__(256) k_x_f16r(const float4* __restrict__ x, ui
         return;
     }
     const float4* xr = x + int64_t(m) * kb8 * 2;
+    const float4* ur = SW ? u + int64_t(m) * kb8 * 2 : nullptr;
+    auto ld = [&](int k) { return SW ? silu_mul4(xr[k], ur[k]) : xr[k]; };
     float mx = 0.f;
     if constexpr (NR > 0) {
         float4 lo[NR], hi[NR];
@@ -475,6 +485,20 @@ __global__ void __launch_bounds__(256) k_x_f16r(const float4* __restrict__ x, ui
             lo[j] = xr[2 * i];
             hi[j] = xr[2 * i + 1];
         }
+        if constexpr (SW) {
+            float4 ul[NR], uh[NR];
+#pragma unroll
+            for (int j = 0; j < NR; ++j) {
+                const int i = min(t + 256 * j, kb8 - 1);
+                ul[j] = ur[2 * i];
+                uh[j] = ur[2 * i + 1];
+            }
+#pragma unroll
+            for (int j = 0; j < NR; ++j) {
+                lo[j] = silu_mul4(lo[j], ul[j]);
+                hi[j] = silu_mul4(hi[j], uh[j]);
+            }
+        }
 #pragma unroll
         for (int j = 0; j < NR; ++j) mx = fmaxf(mx, absmax8(lo[j], hi[j]));
         const float up = row_shift_up(mx, red, xscale + m, t);
@@ -482,20 +506,25 @@ __global__ void __launch_bounds__(256) k_x_f16r(const float4* __restrict__ x, ui
         for (int j = 0; j < NR; ++j)
             if (t + 256 * j < kb8) put(t + 256 * j, pack_x8(lo[j], hi[j], up));
     } else {  // longer rows: two passes, the second mostly from L2
-        for (int i = t; i < kb8; i += 256) mx = fmaxf(mx, absmax8(xr[2 * i], xr[2 * i + 1]));
+        for (int i = t; i < kb8; i += 256) mx = fmaxf(mx, absmax8(ld(2 * i), ld(2 * i + 1)));
         const float up = row_shift_up(mx, red, xscale + m, t);
-        for (int i = t; i < kb8; i += 256) put(i, pack_x8(xr[2 * i], xr[2 * i + 1], up));
+        for (int i = t; i < kb8; i += 256) put(i, pack_x8(ld(2 * i), ld(2 * i + 1), up));
     }
+}
+template <bool FRAG, bool SW>
+void launch_x_f16r_t(const float* x, const float* u, uint4* xh, float* xscale, int M, int kb8, hipStream_t s) {
+    const float4* x4 = reinterpret_cast<const float4*>(x);
+    const float4* u4 = reinterpret_cast<const float4*>(u);
+    const dim3 g = dim3(unsigned(FRAG ? (M + 31) / 32 * 32 : M)), b = dim3(256);
+    if (kb8 <= 256) hipLaunchKernelGGL((k_x_f16r<1, FRAG, SW>), g, b, 0, s, x4, u4, xh, xscale, kb8, M);
+    else if (kb8 <= 512) hipLaunchKernelGGL((k_x_f16r<2, FRAG, SW>), g, b, 0, s, x4, u4, xh, xscale, kb8, M);
+    else if (kb8 <= 1024) hipLaunchKernelGGL((k_x_f16r<4, FRAG, SW>), g, b, 0, s, x4, u4, xh, xscale, kb8, M);
+    else if (kb8 <= 2048) hipLaunchKernelGGL((k_x_f16r<8, FRAG, SW>), g, b, 0, s, x4, u4, xh, xscale, kb8, M);
+    else hipLaunchKernelGGL((k_x_f16r<0, FRAG, SW>), g, b, 0, s, x4, u4, xh, xscale, kb8, M);
 }
 template <bool FRAG>
 void launch_x_f16r(const float* x, uint4* xh, float* xscale, int M, int kb8, hipStream_t s) {
-    const float4* x4 = reinterpret_cast<const float4*>(x);
-    const dim3 g = dim3(unsigned(FRAG ? (M + 31) / 32 * 32 : M)), b = dim3(256);
-    if (kb8 <= 256) hipLaunchKernelGGL((k_x_f16r<1, FRAG>), g, b, 0, s, x4, xh, xscale, kb8, M);
-    else if (kb8 <= 512) hipLaunchKernelGGL((k_x_f16r<2, FRAG>), g, b, 0, s, x4, xh, xscale, kb8, M);
-    else if (kb8 <= 1024) hipLaunchKernelGGL((k_x_f16r<4, FRAG>), g, b, 0, s, x4, xh, xscale, kb8, M);
-    else if (kb8 <= 2048) hipLaunchKernelGGL((k_x_f16r<8, FRAG>), g, b, 0, s, x4, xh, xscale, kb8, M);
-    else hipLaunchKernelGGL((k_x_f16r<0, FRAG>), g, b, 0, s, x4, xh, xscale, kb8, M);
+    launch_x_f16r_t<FRAG, false>(x, nullptr, xh, xscale, M, kb8, s);
 }
 
 // Each of the 4 waves owns one 64-row group of the block's 256 rows and loads
@@ -929,23 +958,34 @@ int launch_tiles(const DevBlob& b, const GemmPlan& p, dim3 grid, hipStream_t s, 
     return with_builder(b, PwGo<4, WF>{grid, s, ga});
 }
 
-int launch_gemm(const DevBlob& b, const float* d_x, float* d_y, int M, void* stream, float* d_scratch) {
+bool gemm_x_frag(const DevBlob& b, int M) { return gemm_plan(b, M).kind == GEMM_RG; }
+
+void gemm_convert_x(const float* d_x, const float* d_u, int cols, int M, bool frag, void* xhv, float* xscale,
+                    void* stream) {
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    uint4* xh = static_cast<uint4*>(xhv);
+    const int kb8 = cols / 8;
+    if (frag) {
+        if (d_u) launch_x_f16r_t<true, true>(d_x, d_u, xh, xscale, M, kb8, s);
+        else launch_x_f16r_t<true, false>(d_x, nullptr, xh, xscale, M, kb8, s);
+    } else {
+        if (d_u) launch_x_f16r_t<false, true>(d_x, d_u, xh, xscale, M, kb8, s);
+        else launch_x_f16r_t<false, false>(d_x, nullptr, xh, xscale, M, kb8, s);
+    }
+}
+
+int launch_gemm_xh(const DevBlob& b, const void* xh, const float* xscale, float* d_y, int M, void* stream,
+                   float* d_part) {
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (!gemm_supported(b, M)) return int(hipErrorInvalidValue);
     const GemmPlan p = gemm_plan(b, M);
     const int bm = p.bm, splits = p.splits;
-    if (!d_scratch) return int(hipErrorInvalidValue);
-    uint4* xh = reinterpret_cast<uint4*>(d_scratch);
-    float* xscale = d_scratch + gemm_x_floats(b, M);
-    float* part = xscale + gemm_scale_floats(M);
-    const int kb8 = int(b.cols / 8);
-    if (p.kind == GEMM_RG) launch_x_f16r<true>(d_x, xh, xscale, M, kb8, s);
-    else launch_x_f16r<false>(d_x, xh, xscale, M, kb8, s);
+    if (splits > 1 && !d_part) return int(hipErrorInvalidValue);
     GemmArgs ga;
     ga.w = b.rpl;
-    ga.xh = xh;
+    ga.xh = static_cast<const uint4*>(xh);
     ga.xscale = xscale;
-    ga.y = splits > 1 ? part : d_y;
+    ga.y = splits > 1 ? d_part : d_y;
     ga.M = M;
     ga.K = int(b.cols);
     ga.sb_per_split = p.sb_per_split;
@@ -955,9 +995,18 @@ int launch_gemm(const DevBlob& b, const float* d_x, float* d_y, int M, void* str
     if (e) return e;
     if (splits > 1) {
         const int64_t n = int64_t(M) * b.rows;
-        hipLaunchKernelGGL(k_split_sum, dim3(unsigned((n / 4 + 1 + 255) / 256)), dim3(256), 0, s, part, d_y, n, splits);
+        hipLaunchKernelGGL(k_split_sum, dim3(unsigned((n / 4 + 1 + 255) / 256)), dim3(256), 0, s, d_part, d_y, n, splits);
     }
     return int(hipGetLastError());
+}
+
+int launch_gemm(const DevBlob& b, const float* d_x, float* d_y, int M, void* stream, float* d_scratch) {
+    if (!gemm_supported(b, M) || !d_scratch) return int(hipErrorInvalidValue);
+    uint4* xh = reinterpret_cast<uint4*>(d_scratch);
+    float* xscale = d_scratch + gemm_x_floats(b, M);
+    float* part = xscale + gemm_scale_floats(M);
+    gemm_convert_x(d_x, nullptr, int(b.cols), M, gemm_x_frag(b, M), xh, xscale, stream);
+    return launch_gemm_xh(b, xh, xscale, d_y, M, stream, part);
 }
 
 }  // namespace wv

@@ -281,6 +281,18 @@ int rpl_fuse_pairs(const DevBlob& a, const DevBlob& b, DevBlob& out, void* strea
 bool gemm_supported(const DevBlob& b, int M);
 size_t gemm_scratch_floats(const DevBlob& b, int M);
 int launch_gemm(const DevBlob& b, const float* d_x, float* d_y, int M, void* stream, float* d_scratch);
+// The two halves of launch_gemm, for callers that feed one converted X to
+// several projections: the fp16 operand order b's plan reads (A fragments for
+// k_gemm_rg), the conversion of X (or, with d_u, of silu(X) * U) into xh and
+// xscale (gemm_x_floats / gemm_scale_floats of the widest weight), and the
+// launch on it (d_part: split-K partials, gemm_scratch_floats' tail).
+bool gemm_x_frag(const DevBlob& b, int M);
+size_t gemm_x_floats(const DevBlob& b, int M);
+size_t gemm_scale_floats(int M);
+void gemm_convert_x(const float* d_x, const float* d_u, int cols, int M, bool frag, void* xh, float* xscale,
+                    void* stream);
+int launch_gemm_xh(const DevBlob& b, const void* xh, const float* xscale, float* d_y, int M, void* stream,
+                   float* d_part);
 // MatVecT on LAYOUT_RPL (slice partials in d_scratch when the plan has several slices).
 int launch_rpl_matvec_t(const DevBlob& b, const float* d_gy, float* d_gx, int batch, void* stream, float* d_scratch);
 size_t rpl_t_scratch_floats(const RplArgs& a, int batch);
