@@ -96,6 +96,31 @@ def test_prefill_then_decode(fmt, n, tol, hd, nh, nkv):
     dec.free()
 
 
+@pytest.mark.parametrize("hd,nh,nkv", [(64, 32, 4), (128, 32, 8)])
+def test_prefill_long_prompt(hd, nh, nkv):
+    """A 1030-token prompt whose MFMA attention blocks (128 rows each) number
+    256 or more, launched longest key range first; then one decode step from
+    its caches."""
+    n = 1030
+    G = nh // nkv
+    assert nkv * -(-n // (128 // G)) >= 256
+    print(f"[gpu] long prefill n={n} hd={hd} heads {nh}/{nkv}", flush=True)
+    cfg = Config(n_layers=1, hidden=256, n_heads=nh, n_kv_heads=nkv, head_dim=hd, ffn=512, vocab=300, max_seq=1040)
+    dec, ref = build(cfg, "Q4_K", 11 + hd)
+    toks = np.random.default_rng(hd).integers(0, cfg.vocab, n)
+    nxt, logits = dec.prefill(toks, 0, want_logits=True)
+    rl, _ = ref.prefill(toks)
+    err = normwise(logits, rl)
+    print(f"[gpu]   prompt logits normwise {err:.2e}", flush=True)
+    assert err <= 2e-3
+    check_token(nxt, rl, 2e-3)
+    t_dev, l_dev = dec.generate(nxt, n, 1, advance_pos=True, want_logits=True)
+    rl, _ = ref.step(nxt, n)
+    assert normwise(l_dev, rl) <= 2e-3
+    check_token(int(t_dev[0]), rl, 2e-3)
+    dec.free()
+
+
 def test_prefill_in_two_blocks():
     """A prompt in two calls (20 rows at position 0, then 13 at 20): the second
     block attends to the cache rows the first one wrote."""

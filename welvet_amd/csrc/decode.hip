@@ -853,7 +853,8 @@ __global__ void __launch_bounds__(256) k_attn_prefill(const float* __restrict__ 
     __shared__ float ps[GM][CH];
     __shared__ float alpha_s[GM], l_s[GM];
     const int G = n_heads / n_kv;
-    const int kvh = blockIdx.x, s = blockIdx.y, t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    // the last rows (the longest key ranges) start first
+    const int kvh = blockIdx.x, s = gridDim.y - 1 - blockIdx.y, t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int qd = n_heads * HD;
     const int kv_len = pos0 + s + 1;
     for (int i = t; i < G * HD; i += 256) qs[i] = q[int64_t(s) * qd + int64_t(kvh) * G * HD + i];
@@ -962,7 +963,9 @@ __global__ void __launch_bounds__(256) k_attn_prefill_mf(const float* __restrict
     constexpr int VS = KT + 4;   // V^T row stride (one row per dim)
     __shared__ __attribute__((aligned(16))) float ks[KT * KS];
     __shared__ __attribute__((aligned(16))) float vt[HD * VS];
-    const int kvh = blockIdx.x, qb = blockIdx.y;
+    // The last position blocks walk the most key tiles: they take the first
+    // block ids, so that they start first and the short ones fill in behind.
+    const int kvh = blockIdx.x, qb = gridDim.y - 1 - blockIdx.y;
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63, h = lane >> 5, j = lane & 31;
     const int R = 32 * wave + j;
     const int srow = min(qb * QP + R / G, n - 1);  // prompt row of this lane's query row (clamped rows store nothing)
