@@ -1080,6 +1080,183 @@ __global__ void __launch_bounds__(256) k_attn_prefill_mf(const float* __restrict
                 make_float4(o[nt][4 * a] * inv, o[nt][4 * a + 1] * inv, o[nt][4 * a + 2] * inv, o[nt][4 * a + 3] * inv);
 }
 
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+
+// x = hi + lo to about 2^-16 relative: hi the nearest bf16, lo the nearest
+// bf16 to the exact f32 remainder.
+__device__ __forceinline__ void bf16_split(float x, __bf16& hi, __bf16& lo) {
+    hi = __bf16(x);
+    lo = __bf16(x - float(hi));
+}
+
+// k_attn_prefill_mf's attention with its products on bf16 MFMA
+// (v_mfma_f32_32x32x16_bf16) in three terms: every f32 operand is split as
+// hi + lo (bf16_split) and a product taken as hi*hi + hi*lo + lo*hi with f32
+// sums, about 2^-16 relative per product against f32's 2^-24, in 48 MFMAs
+// per key tile and wave instead of 128 f32 ones (each 5.3 times the cost).
+// The prompt forward uses it where the block's projections run on the fp16
+// GEMM (the 2e-3 bar); blocks on the f32 GEMVs keep the f32 kernel. Same
+// block, row and tile mapping, softmax and masking as k_attn_prefill_mf; the
+// K tile is staged as bf16 hi and lo rows, V^T likewise, and Q^T as hi and
+// lo registers. A lane half h holds k slots 8h .. 8h+7 of each 16-deep MFMA
+// step: dims 16s + 8h + b of K and Q in S^T = K Q^T; for O^T += V^T P^T the
+// keys 16s + 4h + b (b < 4) and 16s + 8 + 4h + b - 4 (b >= 4), the order in
+// which the lane's probability registers stand.
+template <int HD, int G>
+__global__ void __launch_bounds__(256) k_attn_prefill_bf(const float* __restrict__ q, const float* __restrict__ kc,
+                                                         const float* __restrict__ vc, float* __restrict__ out, int n,
+                                                         int n_heads, int max_seq, int pos0, float scale) {
+    constexpr int QP = 128 / G, KT = 32, NT = HD / 32, NS = HD / 16;
+    constexpr int KSB = HD + 8;  // bf16 K row stride in LDS
+    constexpr int VSB = KT + 8;  // bf16 V^T row stride (one row per dim)
+    __shared__ __attribute__((aligned(16))) __bf16 khi[KT * KSB];
+    __shared__ __attribute__((aligned(16))) __bf16 klo[KT * KSB];
+    __shared__ __attribute__((aligned(16))) __bf16 vhi[HD * VSB];
+    __shared__ __attribute__((aligned(16))) __bf16 vlo[HD * VSB];
+    const int kvh = blockIdx.x, qb = gridDim.y - 1 - blockIdx.y;  // longest key ranges first
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63, h = lane >> 5, j = lane & 31;
+    const int R = 32 * wave + j;
+    const int srow = min(qb * QP + R / G, n - 1);  // prompt row of this lane's query row (clamped rows store nothing)
+    const bool live = qb * QP + R / G < n;
+    const int head = kvh * G + R % G;
+    const int qd = n_heads * HD;
+    const int p_row = pos0 + srow;
+    const int last_pos = pos0 + min(n, qb * QP + QP) - 1;
+    // Q^T operand: this row's dims 16s + 8h .. 16s + 8h + 7 per step s, scaled, split
+    // scores in log2 units (1/sqrt(HD) * log2(e) folded into Q), so each
+    // exponential is one v_exp_f32
+    const float scale2 = scale * 1.44269504088896341f;
+    bf16x8 qh[NS], ql[NS];
+    {
+        const float* qr = q + int64_t(srow) * qd + int64_t(head) * HD + 8 * h;
+#pragma unroll
+        for (int st = 0; st < NS; ++st) {
+            const float4 a = *reinterpret_cast<const float4*>(qr + 16 * st);
+            const float4 b = *reinterpret_cast<const float4*>(qr + 16 * st + 4);
+            const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                __bf16 hi, lo;
+                bf16_split(v[e] * scale2, hi, lo);
+                qh[st][e] = hi;
+                ql[st][e] = lo;
+            }
+        }
+    }
+    f32x16 o[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[nt][r] = 0.f;
+    float m_run = -INFINITY, l_run = 0.f;
+    const float* kb = kc + int64_t(kvh) * max_seq * HD;
+    const float* vb = vc + int64_t(kvh) * max_seq * HD;
+    const int ntiles = last_pos / KT + 1;
+    for (int kt = 0; kt < ntiles; ++kt) {
+        __syncthreads();  // the previous tile's readers are done
+        for (int i = t; i < KT * HD / 4; i += 256) {
+            const int key = i / (HD / 4), c4 = i % (HD / 4);
+            const int krow = min(kt * KT + key, last_pos);
+            const float4 kk = reinterpret_cast<const float4*>(kb + int64_t(krow) * HD)[c4];
+            const float4 vv = reinterpret_cast<const float4*>(vb + int64_t(krow) * HD)[c4];
+            const float kv[4] = {kk.x, kk.y, kk.z, kk.w}, vw[4] = {vv.x, vv.y, vv.z, vv.w};
+            bf16x4 k_h, k_l;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                __bf16 hi, lo;
+                bf16_split(kv[e], hi, lo);
+                k_h[e] = hi;
+                k_l[e] = lo;
+                bf16_split(vw[e], hi, lo);
+                vhi[(4 * c4 + e) * VSB + key] = hi;
+                vlo[(4 * c4 + e) * VSB + key] = lo;
+            }
+            *reinterpret_cast<bf16x4*>(&khi[key * KSB + 4 * c4]) = k_h;
+            *reinterpret_cast<bf16x4*>(&klo[key * KSB + 4 * c4]) = k_l;
+        }
+        __syncthreads();
+        // S^T = K Q^T
+        f32x16 sacc;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sacc[r] = 0.f;
+#pragma unroll
+        for (int st = 0; st < NS; ++st) {
+            const bf16x8 a_h = *reinterpret_cast<const bf16x8*>(&khi[j * KSB + 16 * st + 8 * h]);
+            const bf16x8 a_l = *reinterpret_cast<const bf16x8*>(&klo[j * KSB + 16 * st + 8 * h]);
+            sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_h, qh[st], sacc, 0, 0, 0);
+            sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_h, ql[st], sacc, 0, 0, 0);
+            sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_l, qh[st], sacc, 0, 0, 0);
+        }
+        // mask, running max and sum of this lane's row
+        float pv[16];
+        float mt = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int key = kt * KT + 8 * (r >> 2) + 4 * h + (r & 3);
+            pv[r] = key <= p_row ? sacc[r] : -INFINITY;
+            mt = fmaxf(mt, pv[r]);
+        }
+        {
+            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt), false, false);
+            mt = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+        }
+        const float m_new = fmaxf(m_run, mt);
+        float ps = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            pv[r] = pv[r] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(pv[r] - m_new);
+            ps += pv[r];
+        }
+        {
+            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(ps), __float_as_uint(ps), false, false);
+            ps = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+        }
+        const float alpha = m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
+        l_run = l_run * alpha + ps;
+        m_run = m_new;
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[nt][r] *= alpha;
+        // O^T += V^T P^T, two 16-key steps
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+            bf16x8 p_h, p_l;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                __bf16 hi, lo;
+                bf16_split(pv[8 * st + e], hi, lo);
+                p_h[e] = hi;
+                p_l[e] = lo;
+            }
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                const int vrow = (32 * nt + j) * VSB + 16 * st + 4 * h;
+                const bf16x4 h0 = *reinterpret_cast<const bf16x4*>(&vhi[vrow]);
+                const bf16x4 h1 = *reinterpret_cast<const bf16x4*>(&vhi[vrow + 8]);
+                const bf16x4 l0 = *reinterpret_cast<const bf16x4*>(&vlo[vrow]);
+                const bf16x4 l1 = *reinterpret_cast<const bf16x4*>(&vlo[vrow + 8]);
+                const bf16x8 a_h = {h0[0], h0[1], h0[2], h0[3], h1[0], h1[1], h1[2], h1[3]};
+                const bf16x8 a_l = {l0[0], l0[1], l0[2], l0[3], l1[0], l1[1], l1[2], l1[3]};
+                o[nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_h, p_h, o[nt], 0, 0, 0);
+                o[nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_h, p_l, o[nt], 0, 0, 0);
+                o[nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_l, p_h, o[nt], 0, 0, 0);
+            }
+        }
+    }
+    if (!live) return;
+    // lane l holds O^T[32nt + 8(r/4) + 4h + r%4][row l % 32]: four consecutive dims per r/4
+    const float inv = 1.0f / l_run;
+    float* orow = out + int64_t(srow) * qd + int64_t(head) * HD;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+            *reinterpret_cast<float4*>(orow + 32 * nt + 8 * a + 4 * h) =
+                make_float4(o[nt][4 * a] * inv, o[nt][4 * a + 1] * inv, o[nt][4 * a + 2] * inv, o[nt][4 * a + 3] * inv);
+}
+
 // ---------------------------------------------------------------------------
 // Decoder object
 // ---------------------------------------------------------------------------
@@ -1457,8 +1634,9 @@ int ensure_prefill(Decoder& d, int n) {
 // attention, O + residual, RMSNorm, SwiGLU + residual; then the final norm,
 // LM head and argmax of the last row into the decoder state (state[2]).
 // The MFMA attention of a prompt block, for head dims 64 and 128 and 1, 2, 4
-// or 8 query heads per KV head; false: the shape takes k_attn_prefill.
-bool launch_attn_prefill_mf(Decoder& d, Layer& ly, int n, int pos0, float scale) {
+// or 8 query heads per KV head (bf: the bf16x3 products of k_attn_prefill_bf,
+// else f32); false: the shape takes k_attn_prefill.
+bool launch_attn_prefill_mf(Decoder& d, Layer& ly, int n, int pos0, float scale, bool bf) {
     const wv_decoder_config& c = d.c;
     const int G = c.n_heads / c.n_kv_heads, hd = c.head_dim;
     if ((hd != 64 && hd != 128) || (G != 1 && G != 2 && G != 4 && G != 8)) return false;
@@ -1467,19 +1645,20 @@ bool launch_attn_prefill_mf(Decoder& d, Layer& ly, int n, int pos0, float scale)
         hipLaunchKernelGGL(kern, grid, dim3(256), 0, d.stream, d.pq, ly.kc, ly.vc, d.patt, n, c.n_heads, c.max_seq, pos0,
                            scale);
     };
+    auto pick = [&](auto kf, auto kb) { bf ? go(kb) : go(kf); };
     if (hd == 128) {
         switch (G) {
-        case 1: go(k_attn_prefill_mf<128, 1>); break;
-        case 2: go(k_attn_prefill_mf<128, 2>); break;
-        case 4: go(k_attn_prefill_mf<128, 4>); break;
-        default: go(k_attn_prefill_mf<128, 8>); break;
+        case 1: pick(k_attn_prefill_mf<128, 1>, k_attn_prefill_bf<128, 1>); break;
+        case 2: pick(k_attn_prefill_mf<128, 2>, k_attn_prefill_bf<128, 2>); break;
+        case 4: pick(k_attn_prefill_mf<128, 4>, k_attn_prefill_bf<128, 4>); break;
+        default: pick(k_attn_prefill_mf<128, 8>, k_attn_prefill_bf<128, 8>); break;
         }
     } else {
         switch (G) {
-        case 1: go(k_attn_prefill_mf<64, 1>); break;
-        case 2: go(k_attn_prefill_mf<64, 2>); break;
-        case 4: go(k_attn_prefill_mf<64, 4>); break;
-        default: go(k_attn_prefill_mf<64, 8>); break;
+        case 1: pick(k_attn_prefill_mf<64, 1>, k_attn_prefill_bf<64, 1>); break;
+        case 2: pick(k_attn_prefill_mf<64, 2>, k_attn_prefill_bf<64, 2>); break;
+        case 4: pick(k_attn_prefill_mf<64, 4>, k_attn_prefill_bf<64, 4>); break;
+        default: pick(k_attn_prefill_mf<64, 8>, k_attn_prefill_bf<64, 8>); break;
         }
     }
     return true;
@@ -1507,7 +1686,9 @@ int enqueue_prefill(Decoder& d, int n, int pos0) {
         if (e) return e;
         hipLaunchKernelGGL(k_rope_kv_rows, dim3(unsigned(n)), dim3(256), 0, d.stream, d.pq, d.pk, d.pv, ly.kc, ly.vc,
                            d.freq_div, c.n_heads, c.n_kv_heads, hd, c.max_seq, pos0);
-        if (!launch_attn_prefill_mf(d, ly, n, pos0, scale)) {
+        // bf16x3 products where Q, K and V came from the fp16 GEMM (the 2e-3 bar)
+        const bool bf = gemm_supported(ly.w[0], n) && gemm_supported(ly.w[1], n) && gemm_supported(ly.w[2], n);
+        if (!launch_attn_prefill_mf(d, ly, n, pos0, scale, bf)) {
             const dim3 ag(unsigned(c.n_kv_heads), unsigned(n));
             if (hd == 128)
                 hipLaunchKernelGGL(k_attn_prefill<128>, ag, dim3(256), 0, d.stream, d.pq, ly.kc, ly.vc, d.patt,
