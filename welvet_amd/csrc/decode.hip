@@ -810,16 +810,20 @@ __global__ void __launch_bounds__(256) k_embed_rows(const float* __restrict__ ta
 __global__ void __launch_bounds__(256) k_rope_kv_rows(float* __restrict__ q, const float* __restrict__ k,
                                                       const float* __restrict__ v, float* __restrict__ kc,
                                                       float* __restrict__ vc, const double* __restrict__ freq_div,
-                                                      int n_heads, int n_kv, int hd, int max_seq, int pos0) {
+                                                      int n_heads, int n_kv, int hd, int max_seq, int pos0, int qs,
+                                                      int kvs) {
+    // qs, kvs: row strides of q and of k, v (one [n][q|k|v] block, or three)
     const int s = blockIdx.x, half = hd / 2, pos = pos0 + s;
-    const int qd = n_heads * hd, kvd = n_kv * hd;
-    float* qr = q + int64_t(s) * qd;
-    const float* kr = k + int64_t(s) * kvd;
-    const float* vr = v + int64_t(s) * kvd;
-    for (int i = threadIdx.x; i < (n_heads + n_kv) * half; i += 256) {
-        const int hh = i / half, d = i % half;
-        const double angle = double(pos) / freq_div[d];
-        const double c = cos(angle), sn = sin(angle);
+    const int kvd = n_kv * hd;
+    float* qr = q + int64_t(s) * qs;
+    const float* kr = k + int64_t(s) * kvs;
+    const float* vr = v + int64_t(s) * kvs;
+    // the angle depends on the position and the dim only: each thread takes
+    // one dim (half divides 256: head dims 64 and 128) and every HG-th head
+    const int HG = 256 / half, d = threadIdx.x % half;
+    const double angle = double(pos) / freq_div[d];
+    const double c = cos(angle), sn = sin(angle);
+    for (int hh = threadIdx.x / half; hh < n_heads + n_kv; hh += HG) {
         if (hh < n_heads) {
             const double x0 = qr[hh * hd + d], x1 = qr[hh * hd + d + half];
             qr[hh * hd + d] = float(x0 * c - x1 * sn);
@@ -847,7 +851,8 @@ __global__ void __launch_bounds__(256) k_rope_kv_rows(float* __restrict__ q, con
 template <int HD>
 __global__ void __launch_bounds__(256) k_attn_prefill(const float* __restrict__ q, const float* __restrict__ kc,
                                                       const float* __restrict__ vc, float* __restrict__ out,
-                                                      int n_heads, int n_kv, int max_seq, int pos0, float scale) {
+                                                      int n_heads, int n_kv, int max_seq, int pos0, float scale,
+                                                      int qstr) {
     constexpr int CH = 64, GM = 8, PG = 256 / HD;  // PG: heads a thread's output dim serves per pass
     __shared__ __attribute__((aligned(16))) float qs[GM * HD];
     __shared__ float ps[GM][CH];
@@ -857,7 +862,7 @@ __global__ void __launch_bounds__(256) k_attn_prefill(const float* __restrict__ 
     const int kvh = blockIdx.x, s = gridDim.y - 1 - blockIdx.y, t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int qd = n_heads * HD;
     const int kv_len = pos0 + s + 1;
-    for (int i = t; i < G * HD; i += 256) qs[i] = q[int64_t(s) * qd + int64_t(kvh) * G * HD + i];
+    for (int i = t; i < G * HD; i += 256) qs[i] = q[int64_t(s) * qstr + int64_t(kvh) * G * HD + i];  // qstr: q's row stride
     const float* kb = kc + int64_t(kvh) * max_seq * HD;
     const float* vb = vc + int64_t(kvh) * max_seq * HD;
     float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};  // heads wave and wave + 4
@@ -957,7 +962,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 template <int HD, int G>
 __global__ void __launch_bounds__(256) k_attn_prefill_mf(const float* __restrict__ q, const float* __restrict__ kc,
                                                          const float* __restrict__ vc, float* __restrict__ out, int n,
-                                                         int n_heads, int max_seq, int pos0, float scale) {
+                                                         int n_heads, int max_seq, int pos0, float scale, int qstr) {
     constexpr int QP = 128 / G, KT = 32, HH = HD / 2, NT = HD / 32;
     constexpr int KS = HD + 4;   // K row stride in LDS (floats)
     constexpr int VS = KT + 4;   // V^T row stride (one row per dim)
@@ -977,7 +982,7 @@ __global__ void __launch_bounds__(256) k_attn_prefill_mf(const float* __restrict
     // Q^T operand: this row's dims HH*h .. HH*h + HH - 1, scaled
     float qv[HH];
     {
-        const float4* qr = reinterpret_cast<const float4*>(q + int64_t(srow) * qd + int64_t(head) * HD + HH * h);
+        const float4* qr = reinterpret_cast<const float4*>(q + int64_t(srow) * qstr + int64_t(head) * HD + HH * h);
 #pragma unroll
         for (int i = 0; i < HH / 4; ++i) {
             const float4 v4 = qr[i];
@@ -1106,7 +1111,7 @@ __device__ __forceinline__ void bf16_split(float x, __bf16& hi, __bf16& lo) {
 template <int HD, int G>
 __global__ void __launch_bounds__(256) k_attn_prefill_bf(const float* __restrict__ q, const float* __restrict__ kc,
                                                          const float* __restrict__ vc, float* __restrict__ out, int n,
-                                                         int n_heads, int max_seq, int pos0, float scale) {
+                                                         int n_heads, int max_seq, int pos0, float scale, int qstr) {
     constexpr int QP = 128 / G, KT = 32, NT = HD / 32, NS = HD / 16;
     constexpr int KSB = HD + 8;  // bf16 K row stride in LDS
     constexpr int VSB = KT + 8;  // bf16 V^T row stride (one row per dim)
@@ -1129,7 +1134,7 @@ __global__ void __launch_bounds__(256) k_attn_prefill_bf(const float* __restrict
     const float scale2 = scale * 1.44269504088896341f;
     bf16x8 qh[NS], ql[NS];
     {
-        const float* qr = q + int64_t(srow) * qd + int64_t(head) * HD + 8 * h;
+        const float* qr = q + int64_t(srow) * qstr + int64_t(head) * HD + 8 * h;
 #pragma unroll
         for (int st = 0; st < NS; ++st) {
             const float4 a = *reinterpret_cast<const float4*>(qr + 16 * st);
@@ -1590,11 +1595,14 @@ int ensure_prefill(Decoder& d, int n) {
     const wv_decoder_config& c = d.c;
     size_t need_s = 0;
     size_t need_x = 0;  // the widest fp16 copy of a GEMM input, then its row factors
-    for (const Layer& ly : d.layers)
-        for (const DevBlob& w : ly.w) {
+    for (const Layer& ly : d.layers) {
+        auto need = [&](const DevBlob& w) {
             need_s = std::max(need_s, prefill_proj_scratch(w, n));
             if (gemm_supported(w, n)) need_x = std::max(need_x, gemm_x_floats(w, n) + gemm_scale_floats(n));
-        }
+        };
+        for (const DevBlob& w : ly.w) need(w);
+        if (ly.has_qkv) need(ly.qkv);
+    }
     if (n <= d.pcap && need_s <= d.pscratch_floats && need_x <= d.pxh_floats) return WV_OK;
     drop_prefill(d);
     const size_t qd = size_t(c.n_heads) * c.head_dim, kvd = size_t(c.n_kv_heads) * c.head_dim;
@@ -1604,7 +1612,7 @@ int ensure_prefill(Decoder& d, int n) {
         size_t bytes;
     } bufs[] = {{reinterpret_cast<void**>(&d.ph), n * size_t(c.hidden) * 4},
                 {reinterpret_cast<void**>(&d.pn), n * size_t(c.hidden) * 4},
-                {reinterpret_cast<void**>(&d.pq), n * qd * 4},
+                {reinterpret_cast<void**>(&d.pq), n * (qd + 2 * kvd) * 4},  // q | k | v rows of the fused GEMM
                 {reinterpret_cast<void**>(&d.pk), n * kvd * 4},
                 {reinterpret_cast<void**>(&d.pv), n * kvd * 4},
                 {reinterpret_cast<void**>(&d.patt), n * qd * 4},
@@ -1635,15 +1643,15 @@ int ensure_prefill(Decoder& d, int n) {
 // LM head and argmax of the last row into the decoder state (state[2]).
 // The MFMA attention of a prompt block, for head dims 64 and 128 and 1, 2, 4
 // or 8 query heads per KV head (bf: the bf16x3 products of k_attn_prefill_bf,
-// else f32); false: the shape takes k_attn_prefill.
-bool launch_attn_prefill_mf(Decoder& d, Layer& ly, int n, int pos0, float scale, bool bf) {
+// else f32), q's rows qstr floats apart; false: the shape takes k_attn_prefill.
+bool launch_attn_prefill_mf(Decoder& d, Layer& ly, const float* q, int qstr, int n, int pos0, float scale, bool bf) {
     const wv_decoder_config& c = d.c;
     const int G = c.n_heads / c.n_kv_heads, hd = c.head_dim;
     if ((hd != 64 && hd != 128) || (G != 1 && G != 2 && G != 4 && G != 8)) return false;
     const dim3 grid(unsigned(c.n_kv_heads), unsigned((n + 128 / G - 1) / (128 / G)));
     auto go = [&](auto kern) {
-        hipLaunchKernelGGL(kern, grid, dim3(256), 0, d.stream, d.pq, ly.kc, ly.vc, d.patt, n, c.n_heads, c.max_seq, pos0,
-                           scale);
+        hipLaunchKernelGGL(kern, grid, dim3(256), 0, d.stream, q, ly.kc, ly.vc, d.patt, n, c.n_heads, c.max_seq, pos0,
+                           scale, qstr);
     };
     auto pick = [&](auto kf, auto kb) { bf ? go(kb) : go(kf); };
     if (hd == 128) {
@@ -1679,23 +1687,37 @@ int enqueue_prefill(Decoder& d, int n, int pos0) {
         else
             hipLaunchKernelGGL(k_add_rmsnorm, dim3(unsigned(n)), dim3(1024), 0, d.stream, d.ph, d.pn, ly.attn_norm, d.pn,
                                hidden, c.rms_eps);
-        PrefillX cx;  // Q, K and V share one fp16 copy of the normed rows
-        int e = prefill_proj(d, cx, ly.w[0], d.pn, nullptr, d.pq, n, d.pt);
-        if (!e) e = prefill_proj(d, cx, ly.w[1], d.pn, nullptr, d.pk, n, d.pt);
-        if (!e) e = prefill_proj(d, cx, ly.w[2], d.pn, nullptr, d.pv, n, d.pt);
+        // Q, K and V: one GEMM on the decoder's Q|K|V stack (rows [n][q|k|v]) where
+        // it carries the row factors, else three projections sharing one fp16
+        // copy of the normed rows
+        const int qd = c.n_heads * hd, kvd = c.n_kv_heads * hd;
+        PrefillX cx;
+        float *q = d.pq, *k = d.pk, *v = d.pv;
+        int qstr = qd, kvstr = kvd, e = 0;
+        const bool fused = ly.has_qkv && gemm_supported(ly.qkv, n);
+        if (fused) {
+            e = prefill_proj(d, cx, ly.qkv, d.pn, nullptr, d.pq, n, d.pt);
+            k = d.pq + qd;
+            v = k + kvd;
+            qstr = kvstr = qd + 2 * kvd;
+        } else {
+            e = prefill_proj(d, cx, ly.w[0], d.pn, nullptr, d.pq, n, d.pt);
+            if (!e) e = prefill_proj(d, cx, ly.w[1], d.pn, nullptr, d.pk, n, d.pt);
+            if (!e) e = prefill_proj(d, cx, ly.w[2], d.pn, nullptr, d.pv, n, d.pt);
+        }
         if (e) return e;
-        hipLaunchKernelGGL(k_rope_kv_rows, dim3(unsigned(n)), dim3(256), 0, d.stream, d.pq, d.pk, d.pv, ly.kc, ly.vc,
-                           d.freq_div, c.n_heads, c.n_kv_heads, hd, c.max_seq, pos0);
+        hipLaunchKernelGGL(k_rope_kv_rows, dim3(unsigned(n)), dim3(256), 0, d.stream, q, k, v, ly.kc, ly.vc,
+                           d.freq_div, c.n_heads, c.n_kv_heads, hd, c.max_seq, pos0, qstr, kvstr);
         // bf16x3 products where Q, K and V came from the fp16 GEMM (the 2e-3 bar)
-        const bool bf = gemm_supported(ly.w[0], n) && gemm_supported(ly.w[1], n) && gemm_supported(ly.w[2], n);
-        if (!launch_attn_prefill_mf(d, ly, n, pos0, scale, bf)) {
+        const bool bf = fused || (gemm_supported(ly.w[0], n) && gemm_supported(ly.w[1], n) && gemm_supported(ly.w[2], n));
+        if (!launch_attn_prefill_mf(d, ly, q, qstr, n, pos0, scale, bf)) {
             const dim3 ag(unsigned(c.n_kv_heads), unsigned(n));
             if (hd == 128)
-                hipLaunchKernelGGL(k_attn_prefill<128>, ag, dim3(256), 0, d.stream, d.pq, ly.kc, ly.vc, d.patt,
-                                   c.n_heads, c.n_kv_heads, c.max_seq, pos0, scale);
+                hipLaunchKernelGGL(k_attn_prefill<128>, ag, dim3(256), 0, d.stream, q, ly.kc, ly.vc, d.patt,
+                                   c.n_heads, c.n_kv_heads, c.max_seq, pos0, scale, qstr);
             else
-                hipLaunchKernelGGL(k_attn_prefill<64>, ag, dim3(256), 0, d.stream, d.pq, ly.kc, ly.vc, d.patt,
-                                   c.n_heads, c.n_kv_heads, c.max_seq, pos0, scale);
+                hipLaunchKernelGGL(k_attn_prefill<64>, ag, dim3(256), 0, d.stream, q, ly.kc, ly.vc, d.patt,
+                                   c.n_heads, c.n_kv_heads, c.max_seq, pos0, scale, qstr);
         }
         cx = PrefillX{};
         e = prefill_proj(d, cx, ly.w[3], d.patt, nullptr, d.pt, n, nullptr);

@@ -821,7 +821,7 @@ __global__ void __launch_bounds__(256) k_split_sum(const float* __restrict__ par
 // (up to 8 rows, one batched GEMV launch reads the weights once).
 bool gemm_supported(const DevBlob& b, int M) {
     if (b.layout != LAYOUT_RPL) return false;
-    if (!b.rpl.wrow) return false;  // fused images carry no row factors
+    if (!b.rpl.wrow) return false;  // the gate/up pair images carry no row factors
     return b.fmt == FMT_Q4_K || M > 8;
 }
 

@@ -1811,9 +1811,9 @@ __global__ void __launch_bounds__(256) k_rpl_pairs(uint8_t* __restrict__ dst, co
 }
 
 struct FusedLayout {
-    size_t codes, hi, meta, dd, total;
+    size_t codes, hi, meta, dd, wrow, total;
 };
-FusedLayout fused_layout(const RplItems& it, int64_t rg, int64_t nsb) {
+FusedLayout fused_layout(const RplItems& it, int64_t rg, int64_t nsb, bool with_wrow = false) {
     FusedLayout f{};
     auto add = [&](size_t n) {
         const size_t off = (f.total + 255) & ~size_t(255);
@@ -1825,6 +1825,7 @@ FusedLayout fused_layout(const RplItems& it, int64_t rg, int64_t nsb) {
     f.hi = it.hb ? add(per * 8 * it.hb) : 0;
     f.meta = add(per * it.mb);
     f.dd = it.db ? add(per * it.db) : 0;
+    f.wrow = with_wrow ? add(size_t(rg) * 64 * sizeof(float)) : 0;
     return f;
 }
 
@@ -1845,6 +1846,7 @@ void finish_fused(const DevBlob& proto, int64_t rows, int64_t rg, const FusedLay
     r.hi = f.hi ? base + f.hi : nullptr;
     r.meta = base + f.meta;
     r.dd = f.dd ? reinterpret_cast<const float2_t*>(base + f.dd) : nullptr;
+    r.wrow = f.wrow ? reinterpret_cast<const float*>(base + f.wrow) : nullptr;
     r.partial = nullptr;
     r.rows = int(rows);
     r.nsb = proto.rpl.nsb;
@@ -1869,7 +1871,13 @@ int rpl_fuse_rows(const DevBlob* parts, int n, DevBlob& out, void* stream) {
         rows += b.rows;
     }
     const int64_t nsb = parts[0].rpl.nsb;
-    const FusedLayout f = fused_layout(it, rg, nsb);
+    // the stack keeps the parts' prefill-GEMM row factors when every part has them
+    bool with_wrow = true, row_factors = false;
+    for (int i = 0; i < n; ++i) {
+        with_wrow = with_wrow && parts[i].rpl.wrow;
+        row_factors = row_factors || parts[i].gemm_row_factors;
+    }
+    const FusedLayout f = fused_layout(it, rg, nsb, with_wrow);
     void* base = nullptr;
     hipError_t e = hipMalloc(&base, f.total);
     if (e != hipSuccess) return int(e);
@@ -1895,9 +1903,15 @@ int rpl_fuse_rows(const DevBlob* parts, int n, DevBlob& out, void* stream) {
         if (e == hipSuccess) e = hipMemcpyAsync(b8 + f.meta + off * it.mb, r.meta, per * it.mb, hipMemcpyDeviceToDevice, s);
         if (it.db && e == hipSuccess)
             e = hipMemcpyAsync(b8 + f.dd + off * it.db, r.dd, per * it.db, hipMemcpyDeviceToDevice, s);
+        if (with_wrow && e == hipSuccess)
+            e = hipMemcpyAsync(b8 + f.wrow + size_t(g0) * 64 * sizeof(float), r.wrow,
+                               size_t(r.rg_count) * 64 * sizeof(float), hipMemcpyDeviceToDevice, s);
         g0 += r.rg_count;
     }
-    if (e == hipSuccess) finish_fused(parts[0], rows, rg, f, b8, out);
+    if (e == hipSuccess) {
+        finish_fused(parts[0], rows, rg, f, b8, out);
+        out.gemm_row_factors = row_factors;
+    }
     if (e == hipSuccess) e = hipStreamSynchronize(s);
     if (e != hipSuccess) {
         (void)hipFree(base);  // cleanup after the error being returned
