@@ -30,7 +30,9 @@ def normwise(y, ref):
     return float(np.abs(np.asarray(y, np.float64) - ref).max() / np.abs(ref).max())
 
 
-def build(cfg: Config, fmt: str, seed: int):
+def build(cfg: Config, fmt: str, seed: int, tweak=None):
+    """tweak(name, w) may rescale rows of a projection's (rows, cols) f32
+    weights before packing."""
     rng = np.random.default_rng(seed)
     shapes = {"q": (cfg.q_dim, cfg.hidden), "k": (cfg.kv_dim, cfg.hidden), "v": (cfg.kv_dim, cfg.hidden),
               "o": (cfg.hidden, cfg.q_dim), "gate": (cfg.ffn, cfg.hidden), "up": (cfg.ffn, cfg.hidden),
@@ -41,7 +43,10 @@ def build(cfg: Config, fmt: str, seed: int):
         blobs, dense = [], {}
         for name in ("q", "k", "v", "o", "gate", "up", "down"):
             r, c = shapes[name]
-            p = wv.pack(fmt, (rng.standard_normal(r * c) * 0.02).astype(np.float32), r, c)
+            w = (rng.standard_normal(r * c) * 0.02).astype(np.float32)
+            if tweak is not None:
+                w = np.ascontiguousarray(tweak(name, w.reshape(r, c)), np.float32).ravel()
+            p = wv.pack(fmt, w, r, c)
             blobs.append(wv.upload(p))
             dense[name] = dr.DenseW(p)
         an = (1.0 + 0.1 * rng.standard_normal(cfg.hidden)).astype(np.float32)
@@ -118,6 +123,37 @@ def test_prefill_long_prompt(hd, nh, nkv):
     rl, _ = ref.step(nxt, n)
     assert normwise(l_dev, rl) <= 2e-3
     check_token(int(t_dev[0]), rl, 2e-3)
+    dec.free()
+
+
+def test_prefill_qkv_stack_row_factors():
+    """Q, K and V blobs with a few rows scaled by 1e-6: their prefill-GEMM row
+    factors (powers of two putting a row's largest fp16 operand in [2^12,
+    2^13)) pass 2^20, so the GEMM applies every row's factor. The prompt's one
+    GEMM on the decoder's Q|K|V stack must take the three blobs' factors in
+    stack order; a factor on the wrong row would scale that row's outputs by
+    the ratio of two factors."""
+    print("[gpu] prefill Q|K|V stack with row factors", flush=True)
+    cfg = Config(n_layers=2, hidden=512, n_heads=8, n_kv_heads=2, head_dim=64, ffn=1024, vocab=500, max_seq=320)
+
+    def tweak(name, w):
+        if name in ("q", "k", "v"):
+            w = w.copy()
+            w[[3, 40, w.shape[0] - 1]] *= np.float32(1e-6)
+        return w
+
+    dec, ref = build(cfg, "Q4_K", 61, tweak)
+    toks = np.random.default_rng(9).integers(0, cfg.vocab, 300)
+    nxt, logits = dec.prefill(toks, 0, want_logits=True)
+    rl, _ = ref.prefill(toks)
+    err = normwise(logits, rl)
+    print(f"[gpu]   prompt logits normwise {err:.2e}", flush=True)
+    assert np.isfinite(logits).all()
+    assert err <= 2e-3
+    check_token(nxt, rl, 2e-3)
+    t_dev, l_dev = dec.generate(nxt, 300, 1, advance_pos=True, want_logits=True)
+    rl, _ = ref.step(nxt, 300)
+    assert normwise(l_dev, rl) <= 2e-3
     dec.free()
 
 
