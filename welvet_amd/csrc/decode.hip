@@ -1119,6 +1119,12 @@ __global__ void __launch_bounds__(256) k_attn_prefill_bf(const float* __restrict
     __shared__ __attribute__((aligned(16))) __bf16 klo[KT * KSB];
     __shared__ __attribute__((aligned(16))) __bf16 vhi[HD * VSB];
     __shared__ __attribute__((aligned(16))) __bf16 vlo[HD * VSB];
+    // V^T element (dim, key): the 4-key blocks of a dim's row are XOR-swizzled
+    // by (dim / 16) % 8, so that the 32 dims one staging store writes (4c4 + e,
+    // c4 < 32, one key) fall in distinct banks (unswizzled, 20 c4 dwords apart
+    // mod 64, 8 lanes share a bank); a 4-key block stays contiguous for the
+    // 8-byte operand reads.
+    auto vt_at = [](int dim, int key) { return dim * VSB + ((((key >> 2) ^ (dim >> 4)) & 7) << 2) + (key & 3); };
     const int kvh = blockIdx.x, qb = gridDim.y - 1 - blockIdx.y;  // longest key ranges first
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63, h = lane >> 5, j = lane & 31;
     const int R = 32 * wave + j;
@@ -1174,8 +1180,9 @@ __global__ void __launch_bounds__(256) k_attn_prefill_bf(const float* __restrict
                 k_h[e] = hi;
                 k_l[e] = lo;
                 bf16_split(vw[e], hi, lo);
-                vhi[(4 * c4 + e) * VSB + key] = hi;
-                vlo[(4 * c4 + e) * VSB + key] = lo;
+                const int vi = vt_at(4 * c4 + e, key);
+                vhi[vi] = hi;
+                vlo[vi] = lo;
             }
             *reinterpret_cast<bf16x4*>(&khi[key * KSB + 4 * c4]) = k_h;
             *reinterpret_cast<bf16x4*>(&klo[key * KSB + 4 * c4]) = k_l;
@@ -1237,11 +1244,11 @@ __global__ void __launch_bounds__(256) k_attn_prefill_bf(const float* __restrict
             }
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt) {
-                const int vrow = (32 * nt + j) * VSB + 16 * st + 4 * h;
-                const bf16x4 h0 = *reinterpret_cast<const bf16x4*>(&vhi[vrow]);
-                const bf16x4 h1 = *reinterpret_cast<const bf16x4*>(&vhi[vrow + 8]);
-                const bf16x4 l0 = *reinterpret_cast<const bf16x4*>(&vlo[vrow]);
-                const bf16x4 l1 = *reinterpret_cast<const bf16x4*>(&vlo[vrow + 8]);
+                const int dim = 32 * nt + j, v0 = vt_at(dim, 16 * st + 4 * h), v1 = vt_at(dim, 16 * st + 8 + 4 * h);
+                const bf16x4 h0 = *reinterpret_cast<const bf16x4*>(&vhi[v0]);
+                const bf16x4 h1 = *reinterpret_cast<const bf16x4*>(&vhi[v1]);
+                const bf16x4 l0 = *reinterpret_cast<const bf16x4*>(&vlo[v0]);
+                const bf16x4 l1 = *reinterpret_cast<const bf16x4*>(&vlo[v1]);
                 const bf16x8 a_h = {h0[0], h0[1], h0[2], h0[3], h1[0], h1[1], h1[2], h1[3]};
                 const bf16x8 a_l = {l0[0], l0[1], l0[2], l0[3], l1[0], l1[1], l1[2], l1[3]};
                 o[nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_h, p_h, o[nt], 0, 0, 0);
