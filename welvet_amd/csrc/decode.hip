@@ -1115,10 +1115,11 @@ __global__ void __launch_bounds__(256) k_attn_prefill_bf(const float* __restrict
     constexpr int QP = 128 / G, KT = 32, NT = HD / 32, NS = HD / 16;
     constexpr int KSB = HD + 8;  // bf16 K row stride in LDS
     constexpr int VSB = KT + 8;  // bf16 V^T row stride (one row per dim)
-    __shared__ __attribute__((aligned(16))) __bf16 khi[KT * KSB];
-    __shared__ __attribute__((aligned(16))) __bf16 klo[KT * KSB];
-    __shared__ __attribute__((aligned(16))) __bf16 vhi[HD * VSB];
-    __shared__ __attribute__((aligned(16))) __bf16 vlo[HD * VSB];
+    // two tile buffers: tile kt + 1 is loaded while tile kt is used
+    __shared__ __attribute__((aligned(16))) __bf16 khi[2][KT * KSB];
+    __shared__ __attribute__((aligned(16))) __bf16 klo[2][KT * KSB];
+    __shared__ __attribute__((aligned(16))) __bf16 vhi[2][HD * VSB];
+    __shared__ __attribute__((aligned(16))) __bf16 vlo[2][HD * VSB];
     // V^T element (dim, key): the 4-key blocks of a dim's row are XOR-swizzled
     // by (dim / 16) % 8, so that the 32 dims one staging store writes (4c4 + e,
     // c4 < 32, one key) fall in distinct banks (unswizzled, 20 c4 dwords apart
@@ -1164,14 +1165,22 @@ __global__ void __launch_bounds__(256) k_attn_prefill_bf(const float* __restrict
     const float* kb = kc + int64_t(kvh) * max_seq * HD;
     const float* vb = vc + int64_t(kvh) * max_seq * HD;
     const int ntiles = last_pos / KT + 1;
-    for (int kt = 0; kt < ntiles; ++kt) {
-        __syncthreads();  // the previous tile's readers are done
-        for (int i = t; i < KT * HD / 4; i += 256) {
-            const int key = i / (HD / 4), c4 = i % (HD / 4);
+    constexpr int NI = KT * HD / 4 / 256;  // float4 items of K (and of V) per thread and tile
+    float4 pk[NI], pv[NI];
+    auto gload = [&](int kt) {
+#pragma unroll
+        for (int u = 0; u < NI; ++u) {
+            const int i = t + 256 * u, key = i / (HD / 4), c4 = i % (HD / 4);
             const int krow = min(kt * KT + key, last_pos);
-            const float4 kk = reinterpret_cast<const float4*>(kb + int64_t(krow) * HD)[c4];
-            const float4 vv = reinterpret_cast<const float4*>(vb + int64_t(krow) * HD)[c4];
-            const float kv[4] = {kk.x, kk.y, kk.z, kk.w}, vw[4] = {vv.x, vv.y, vv.z, vv.w};
+            pk[u] = reinterpret_cast<const float4*>(kb + int64_t(krow) * HD)[c4];
+            pv[u] = reinterpret_cast<const float4*>(vb + int64_t(krow) * HD)[c4];
+        }
+    };
+    auto lstore = [&](int buf) {
+#pragma unroll
+        for (int u = 0; u < NI; ++u) {
+            const int i = t + 256 * u, key = i / (HD / 4), c4 = i % (HD / 4);
+            const float kv[4] = {pk[u].x, pk[u].y, pk[u].z, pk[u].w}, vw[4] = {pv[u].x, pv[u].y, pv[u].z, pv[u].w};
             bf16x4 k_h, k_l;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
@@ -1181,21 +1190,27 @@ __global__ void __launch_bounds__(256) k_attn_prefill_bf(const float* __restrict
                 k_l[e] = lo;
                 bf16_split(vw[e], hi, lo);
                 const int vi = vt_at(4 * c4 + e, key);
-                vhi[vi] = hi;
-                vlo[vi] = lo;
+                vhi[buf][vi] = hi;
+                vlo[buf][vi] = lo;
             }
-            *reinterpret_cast<bf16x4*>(&khi[key * KSB + 4 * c4]) = k_h;
-            *reinterpret_cast<bf16x4*>(&klo[key * KSB + 4 * c4]) = k_l;
+            *reinterpret_cast<bf16x4*>(&khi[buf][key * KSB + 4 * c4]) = k_h;
+            *reinterpret_cast<bf16x4*>(&klo[buf][key * KSB + 4 * c4]) = k_l;
         }
-        __syncthreads();
+    };
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    for (int kt = 0; kt < ntiles; ++kt) {
+        const int buf = kt & 1;
+        if (kt + 1 < ntiles) gload(kt + 1);  // in flight through this tile's MFMAs
         // S^T = K Q^T
         f32x16 sacc;
 #pragma unroll
         for (int r = 0; r < 16; ++r) sacc[r] = 0.f;
 #pragma unroll
         for (int st = 0; st < NS; ++st) {
-            const bf16x8 a_h = *reinterpret_cast<const bf16x8*>(&khi[j * KSB + 16 * st + 8 * h]);
-            const bf16x8 a_l = *reinterpret_cast<const bf16x8*>(&klo[j * KSB + 16 * st + 8 * h]);
+            const bf16x8 a_h = *reinterpret_cast<const bf16x8*>(&khi[buf][j * KSB + 16 * st + 8 * h]);
+            const bf16x8 a_l = *reinterpret_cast<const bf16x8*>(&klo[buf][j * KSB + 16 * st + 8 * h]);
             sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_h, qh[st], sacc, 0, 0, 0);
             sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_h, ql[st], sacc, 0, 0, 0);
             sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_l, qh[st], sacc, 0, 0, 0);
@@ -1245,10 +1260,10 @@ __global__ void __launch_bounds__(256) k_attn_prefill_bf(const float* __restrict
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt) {
                 const int dim = 32 * nt + j, v0 = vt_at(dim, 16 * st + 4 * h), v1 = vt_at(dim, 16 * st + 8 + 4 * h);
-                const bf16x4 h0 = *reinterpret_cast<const bf16x4*>(&vhi[v0]);
-                const bf16x4 h1 = *reinterpret_cast<const bf16x4*>(&vhi[v1]);
-                const bf16x4 l0 = *reinterpret_cast<const bf16x4*>(&vlo[v0]);
-                const bf16x4 l1 = *reinterpret_cast<const bf16x4*>(&vlo[v1]);
+                const bf16x4 h0 = *reinterpret_cast<const bf16x4*>(&vhi[buf][v0]);
+                const bf16x4 h1 = *reinterpret_cast<const bf16x4*>(&vhi[buf][v1]);
+                const bf16x4 l0 = *reinterpret_cast<const bf16x4*>(&vlo[buf][v0]);
+                const bf16x4 l1 = *reinterpret_cast<const bf16x4*>(&vlo[buf][v1]);
                 const bf16x8 a_h = {h0[0], h0[1], h0[2], h0[3], h1[0], h1[1], h1[2], h1[3]};
                 const bf16x8 a_l = {l0[0], l0[1], l0[2], l0[3], l1[0], l1[1], l1[2], l1[3]};
                 o[nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_h, p_h, o[nt], 0, 0, 0);
@@ -1256,6 +1271,8 @@ __global__ void __launch_bounds__(256) k_attn_prefill_bf(const float* __restrict
                 o[nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_l, p_h, o[nt], 0, 0, 0);
             }
         }
+        if (kt + 1 < ntiles) lstore(buf ^ 1);  // the other buffer's readers finished before the last barrier
+        __syncthreads();
     }
     if (!live) return;
     // lane l holds O^T[32nt + 8(r/4) + 4h + r%4][row l % 32]: four consecutive dims per r/4
