@@ -1702,23 +1702,33 @@ int enqueue_prefill(Decoder& d, int n, int pos0) {
     const float scale = float(1.0 / std::sqrt(double(hd)));
     hipLaunchKernelGGL(k_embed_rows, dim3(unsigned((hidden + 255) / 256), unsigned(n)), dim3(256), 0, d.stream, d.embed,
                        d.ptok, d.ph, hidden, c.vocab);
+    // GEMMs that read a row-major fp16 operand: the norm before them writes it
+    auto rowmajor = [&](const DevBlob& w) { return gemm_supported(w, n) && !gemm_x_frag(w, n); };
+    float* xscale = d.pxh + (d.layers.empty() ? 0 : gemm_x_floats(d.layers[0].w[0], n));  // cols = hidden
     for (int L = 0; L < c.n_layers; ++L) {
         Layer& ly = d.layers[L];
-        // h += the previous layer's down projection (in pn), then the norm
-        if (L == 0)
+        const bool fused = ly.has_qkv && gemm_supported(ly.qkv, n);
+        const bool qkv_x = fused ? rowmajor(ly.qkv) : rowmajor(ly.w[0]) && rowmajor(ly.w[1]) && rowmajor(ly.w[2]);
+        PrefillX cx;
+        // h += the previous layer's down projection (in pn), then the norm:
+        // into Q, K and V's fp16 operand where they all read one, else f32
+        if (qkv_x) {
+            launch_norm_x_f16r(d.ph, L == 0 ? nullptr : d.pn, ly.attn_norm, nullptr, d.pxh, xscale, n, hidden,
+                               c.rms_eps, d.stream);
+            cx = PrefillX{d.pn, nullptr, hidden, 0};
+        } else if (L == 0) {
             hipLaunchKernelGGL(k_rmsnorm, dim3(unsigned(n)), dim3(1024), 0, d.stream, d.ph, ly.attn_norm, d.pn, hidden,
                                c.rms_eps);
-        else
+        } else {
             hipLaunchKernelGGL(k_add_rmsnorm, dim3(unsigned(n)), dim3(1024), 0, d.stream, d.ph, d.pn, ly.attn_norm, d.pn,
                                hidden, c.rms_eps);
+        }
         // Q, K and V: one GEMM on the decoder's Q|K|V stack (rows [n][q|k|v]) where
         // it carries the row factors, else three projections sharing one fp16
         // copy of the normed rows
         const int qd = c.n_heads * hd, kvd = c.n_kv_heads * hd;
-        PrefillX cx;
         float *q = d.pq, *k = d.pk, *v = d.pv;
         int qstr = qd, kvstr = kvd, e = 0;
-        const bool fused = ly.has_qkv && gemm_supported(ly.qkv, n);
         if (fused) {
             e = prefill_proj(d, cx, ly.qkv, d.pn, nullptr, d.pq, n, d.pt);
             k = d.pq + qd;
@@ -1746,9 +1756,15 @@ int enqueue_prefill(Decoder& d, int n, int pos0) {
         cx = PrefillX{};
         e = prefill_proj(d, cx, ly.w[3], d.patt, nullptr, d.pt, n, nullptr);
         if (e) return e;
-        hipLaunchKernelGGL(k_add_rmsnorm, dim3(unsigned(n)), dim3(1024), 0, d.stream, d.ph, d.pt, ly.ffn_norm, d.pn,
-                           hidden, c.rms_eps);  // h += O att, then the norm
+        // h += O att, then the norm (into gate and up's fp16 operand where both read one)
         cx = PrefillX{};  // gate and up share one fp16 copy
+        if (rowmajor(ly.w[4]) && rowmajor(ly.w[5])) {
+            launch_norm_x_f16r(d.ph, d.pt, ly.ffn_norm, nullptr, d.pxh, xscale, n, hidden, c.rms_eps, d.stream);
+            cx = PrefillX{d.pn, nullptr, hidden, 0};
+        } else {
+            hipLaunchKernelGGL(k_add_rmsnorm, dim3(unsigned(n)), dim3(1024), 0, d.stream, d.ph, d.pt, ly.ffn_norm, d.pn,
+                               hidden, c.rms_eps);
+        }
         e = prefill_proj(d, cx, ly.w[4], d.pn, nullptr, d.pg, n, d.pt);
         if (!e) e = prefill_proj(d, cx, ly.w[5], d.pn, nullptr, d.pu, n, d.pt);
         if (e) return e;

@@ -527,6 +527,84 @@ void launch_x_f16r(const float* x, uint4* xh, float* xscale, int M, int kb8, hip
     launch_x_f16r_t<FRAG, false>(x, nullptr, xh, xscale, M, kb8, s);
 }
 
+// The prompt forward's RMSNorm of a token block straight into the prefill
+// GEMM's fp16 operand, one block per row: with `a`, h += a first (per element,
+// the updated row written back: the residual add); then the norm with f64
+// sums, y = float(x * inv * gamma) in f64 (layers/rmsnorm/cpu.go:70-85, as the
+// decoder's k_rmsnorm); then the row's factor and fp16 blocks exactly as
+// k_x_f16r<NR, false, false> makes them from y (max|y| in [2^14, 2^15), k
+// order [0,2,4,6,1,3,5,7]); with `y`, the f32 rows as well (a and y may be
+// the same rows: a block reads its row of a before its first barrier and
+// writes y after it). An 8-column block is float4s 2b, 2b + 1, held by lanes
+// 2b, 2b + 1; the even lane packs it.
+__global__ void __launch_bounds__(1024) k_norm_x_f16r(float* __restrict__ h, const float* a,
+                                                      const float* __restrict__ gamma, float* y,
+                                                      uint4* __restrict__ xh, float* __restrict__ xscale, int dim,
+                                                      double eps) {
+    __shared__ double part[16];
+    __shared__ float redm[16];
+    const int m = blockIdx.x, t = threadIdx.x;
+    h += int64_t(m) * dim;
+    constexpr int R = 4;
+    const int n4 = dim / 4, kb8 = dim / 8;
+    float4 xv[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int i = t + 1024 * r;
+        xv[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (i < n4) {
+            xv[r] = reinterpret_cast<const float4*>(h)[i];
+            if (a) {
+                const float4 av = reinterpret_cast<const float4*>(a + int64_t(m) * dim)[i];
+                xv[r] = make_float4(xv[r].x + av.x, xv[r].y + av.y, xv[r].z + av.z, xv[r].w + av.w);
+            }
+        }
+    }
+    double ss = 0.0;
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+        ss += double(xv[r].x) * xv[r].x + double(xv[r].y) * xv[r].y + double(xv[r].z) * xv[r].z +
+              double(xv[r].w) * xv[r].w;
+    ss = wave_total_f64(ss);
+    if ((t & 63) == 0) part[t >> 6] = ss;
+    __syncthreads();
+    double tot = 0.0;
+    for (int w = 0; w < 16; ++w) tot += part[w];
+    const double inv = 1.0 / sqrt(tot / double(dim) + eps);
+    float4 yv[R];
+    float mx = 0.f;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int i = t + 1024 * r;
+        yv[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (i < n4) {
+            if (a) reinterpret_cast<float4*>(h)[i] = xv[r];
+            const float4 g = gamma ? reinterpret_cast<const float4*>(gamma)[i] : make_float4(1.f, 1.f, 1.f, 1.f);
+            yv[r].x = float(double(xv[r].x) * inv * double(g.x));
+            yv[r].y = float(double(xv[r].y) * inv * double(g.y));
+            yv[r].z = float(double(xv[r].z) * inv * double(g.z));
+            yv[r].w = float(double(xv[r].w) * inv * double(g.w));
+            if (y) reinterpret_cast<float4*>(y + int64_t(m) * dim)[i] = yv[r];
+            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(yv[r].x), fabsf(yv[r].y)), fmaxf(fabsf(yv[r].z), fabsf(yv[r].w))));
+        }
+    }
+    mx = wave_maximum(mx);
+    if ((t & 63) == 0) redm[t >> 6] = mx;
+    __syncthreads();
+    mx = redm[0];
+    for (int w = 1; w < 16; ++w) mx = fmaxf(mx, redm[w]);
+    int sh = 0;  // the rows are multiplied by 2^sh
+    if (mx > 0.f && mx <= 3.4028235e38f) sh = min(126, max(-126, 14 - ilogbf(mx)));
+    if (t == 0) xscale[m] = ldexpf(1.0f, -sh);
+    const float up = ldexpf(1.0f, sh);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int i = t + 1024 * r;
+        const float4 nb = make_float4(quad_xor1(yv[r].x), quad_xor1(yv[r].y), quad_xor1(yv[r].z), quad_xor1(yv[r].w));
+        if (!(t & 1) && i < n4 && i / 2 < kb8) xh[int64_t(m) * kb8 + i / 2] = pack_x8(yv[r], nb, up);
+    }
+}
+
 // Each of the 4 waves owns one 64-row group of the block's 256 rows and loads
 // its row group's codes straight from the row-interleaved planes (lane l = row
 // l, 16 bytes = 32 columns per chunk). One v_permlane32_swap per code-word
@@ -959,6 +1037,12 @@ int launch_tiles(const DevBlob& b, const GemmPlan& p, dim3 grid, hipStream_t s, 
 }
 
 bool gemm_x_frag(const DevBlob& b, int M) { return gemm_plan(b, M).kind == GEMM_RG; }
+
+void launch_norm_x_f16r(float* h, const float* a, const float* gamma, float* y, void* xh, float* xscale, int M, int dim,
+                        double eps, void* stream) {
+    hipLaunchKernelGGL(k_norm_x_f16r, dim3(unsigned(M)), dim3(1024), 0, static_cast<hipStream_t>(stream), h, a, gamma,
+                       y, static_cast<uint4*>(xh), xscale, dim, eps);
+}
 
 void gemm_convert_x(const float* d_x, const float* d_u, int cols, int M, bool frag, void* xhv, float* xscale,
                     void* stream) {
