@@ -465,10 +465,10 @@ __global__ void __launch_bounds__(256) k_attn_reg(const float* __restrict__ q, f
     const float4* kb = reinterpret_cast<const float4*>(kc + (int64_t(kvh) * max_seq + p0) * HD);
     const float4* vb = reinterpret_cast<const float4*>(vc + (int64_t(kvh) * max_seq + p0) * HD);
 #pragma unroll
-    for (int r = 0; r < NL; ++r) kv4[r] = kb[min(row0 + RS * r, nvalid - 1) * Q4 + col];
+    for (int r = 0; r < NL; ++r) kv4[r] = ld_nt16(kb + min(row0 + RS * r, nvalid - 1) * Q4 + col);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int r = 0; r < NL; ++r) vv4[r] = vb[min(row0 + RS * r, nvalid - 1) * Q4 + col];
+    for (int r = 0; r < NL; ++r) vv4[r] = ld_nt16(vb + min(row0 + RS * r, nvalid - 1) * Q4 + col);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int j = 0; j < QP; ++j) {

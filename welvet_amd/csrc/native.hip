@@ -151,7 +151,7 @@ __global__ void __launch_bounds__(1024) k_narrow_i8v(const uint8_t* __restrict__
     for (int rw = 0; rw < RW; ++rw) {
         const uint4* rowp = reinterpret_cast<const uint4*>(codes + int64_t(min(r0 + rw, rows - 1)) * (K / 8 * B));
 #pragma unroll
-        for (int c = 0; c < NC; ++c) cv[rw][c] = rowp[min(lane + 64 * c, nU - 1)];
+        for (int c = 0; c < NC; ++c) cv[rw][c] = ld_nt16(rowp + min(lane + 64 * c, nU - 1));
     }
     __builtin_amdgcn_sched_barrier(0);
     float m = 0.f;
@@ -269,7 +269,7 @@ __global__ void __launch_bounds__(1024) k_narrow_i8l(const uint8_t* __restrict__
     const uint4* rowp = reinterpret_cast<const uint4*>(codes + int64_t(min(r, rows - 1)) * (K / 8 * B));
     uint4 cur[NCI];
 #pragma unroll
-    for (int n = 0; n < NCI; ++n) cur[n] = rowp[min(lane + 64 * n, nU - 1)];
+    for (int n = 0; n < NCI; ++n) cur[n] = ld_nt16(rowp + min(lane + 64 * n, nU - 1));
     __builtin_amdgcn_sched_barrier(0);
     float m = 0.f;
 #pragma unroll
@@ -320,7 +320,7 @@ __global__ void __launch_bounds__(1024) k_narrow_i8l(const uint8_t* __restrict__
     for (int c0 = 0; c0 < nU; c0 += 64 * NCI) {
         uint4 nxt[NCI];
 #pragma unroll
-        for (int n = 0; n < NCI; ++n) nxt[n] = rowp[min(c0 + 64 * NCI + lane + 64 * n, nU - 1)];
+        for (int n = 0; n < NCI; ++n) nxt[n] = ld_nt16(rowp + min(c0 + 64 * NCI + lane + 64 * n, nU - 1));
 #pragma unroll
         for (int n = 0; n < NCI; ++n) {
             const int c = c0 + lane + 64 * n;
