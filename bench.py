@@ -97,7 +97,7 @@ PROMPT = {f"prompt_32l_{n}": dict(DECODE["decode_32l"], prompt=n) for n in (32, 
 # 1.9993 * FETCH_SIZE + WRITE_SIZE (per-launch medians of `rocprofv3 --pmc`
 # runs of `bench.py --no-cpu --workload decode_32l`; the launches and
 # commands are listed in DECODE_TRAFFIC_SOURCE).
-DECODE_TRAFFIC = {"decode_32l": 5_335_931_919}
+DECODE_TRAFFIC = {"decode_32l": 5_335_726_695}
 DECODE_TRAFFIC_SOURCE = "profiles/decode_32l_q4k_kernel_trace.txt"
 # Per-dispatch TCC counters of the GEMV kernel (KiB), medians over the timed
 # launches of `rocprofv3 --pmc FETCH_SIZE` and `--pmc WRITE_SIZE` runs of
