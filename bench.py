@@ -417,13 +417,20 @@ def main():
     del blobs
     if args.workload == "q4k_4096x14336" and not args.no_decode:
         # The metric's second half: decode tokens/s of BASELINE config 5.
-        d = decode_run(args, wv, "decode_32l", args.decode_steps, 4, with_cpu=not args.no_cpu)
+        d = decode_run(args, wv, "decode_32l", args.decode_steps, 4, with_cpu=not args.no_cpu, prompt_n=512)
         result["decode_tokens_per_s"] = d["value"]
         result["decode_ms_per_token"] = d["ms_per_step"]
         result["decode_roofline"] = d["roofline"]
         result["decode_config"] = d["config"]["workload"]
         if "cpu_baseline" in d:
             result["decode_cpu_baseline"] = d["cpu_baseline"]
+        # the device prompt forward of the same model (512 tokens, wv_decoder_prefill)
+        if "prompt" in d:
+            result["prompt_tokens_per_s"] = d["prompt"]["value"]
+            result["prompt_ms"] = d["prompt"]["ms_per_step"]
+            result["prompt_roofline"] = d["prompt"]["roofline"]
+        elif "prompt_error" in d:
+            result["prompt_error"] = d["prompt_error"]
     print(json.dumps(result), flush=True)
 
 
@@ -698,8 +705,10 @@ def build_decoder(wv, spec, fill_kv):
     return dec, cfg, rng, packed_sets, p_lm, layer_bytes, blobs + [lm]
 
 
-def decode_run(args, wv, workload, steps, warmup, with_cpu):
-    """One step = one greedy decode token of the whole 32-layer model at KV length 2048."""
+def decode_run(args, wv, workload, steps, warmup, with_cpu, prompt_n=0):
+    """One step = one greedy decode token of the whole 32-layer model at KV
+    length 2048. With prompt_n, an n-token prompt forward is timed on the same
+    decoder afterwards (its line under "prompt")."""
     spec = DECODE[workload]
     kv = spec["kv"]
     dec, cfg, rng, packed_sets, p_lm, layer_bytes, owned = build_decoder(wv, spec, True)
@@ -732,6 +741,11 @@ def decode_run(args, wv, workload, steps, warmup, with_cpu):
                      "traffic_unit": "bytes per token",
                      "traffic_source": DECODE_TRAFFIC_SOURCE if workload in DECODE_TRAFFIC else None},
     }
+    if prompt_n:
+        try:
+            result["prompt"] = time_prompt(dec, cfg, rng, packed_sets, p_lm, prompt_n, 10, 2)
+        except Exception as e:  # the decode line stands without it
+            result["prompt_error"] = f"{type(e).__name__}: {e}"
     if with_cpu:
         import oracle
         threads = args.cpu_threads or host_info()["threads"]
@@ -782,20 +796,29 @@ def prompt_run(args, wv, workload):
     causal attention over the block, the KV caches written, the last row's
     logits and next token)."""
     spec = PROMPT[workload]
-    n = spec["prompt"]
     dec, cfg, rng, packed_sets, p_lm, layer_bytes, owned = build_decoder(wv, spec, False)
+    result = time_prompt(dec, cfg, rng, packed_sets, p_lm, spec["prompt"], max(3, min(args.steps, 20)),
+                         max(1, min(args.warmup, 3)))
+    dec.free()
+    for b in owned:
+        b.free()
+    return result
+
+
+def time_prompt(dec, cfg, rng, packed_sets, p_lm, n, reps, warmup):
+    """Times dec.prefill of one n-token prompt from position 0 (host-timed,
+    synchronous calls) and returns its bench line."""
     toks = rng.integers(0, cfg.vocab, n).astype(np.int32)
-    reps = max(3, min(args.steps, 20))
-    for _ in range(max(1, min(args.warmup, 3))):
+    for _ in range(warmup):
         dec.prefill(toks, 0)
     t1 = time.perf_counter()
     for _ in range(reps):
         nxt = dec.prefill(toks, 0)
     dt = (time.perf_counter() - t1) / reps
     flops = 2.0 * n * (cfg.n_layers * sum(p.rows * p.cols for p in packed_sets[0]) + p_lm.rows * p_lm.cols / n)
-    result = {
+    return {
         "metric": f"prompt forward tokens/s, 32-layer Q4_K decoder, {n}-token prompt",
-        "value": round(n / dt, 1), "unit": "tokens/s", "n_gpus": 1, "steps": reps, "warmup": 1,
+        "value": round(n / dt, 1), "unit": "tokens/s", "n_gpus": 1, "steps": reps, "warmup": warmup,
         "ms_per_step": round(dt * 1e3, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f32 activations, Q4_K weights (fp16 MFMA projections), f32 KV cache",
         "data": "synthetic random init as decode_32l; prompt token ids uniform over the vocabulary",
@@ -806,10 +829,6 @@ def prompt_run(args, wv, workload):
                      "frac": round(flops / dt / 1e12 / 2500.0, 4), "traffic": None,
                      "note": "projection FLOPs only (the LM head for the last row); host-timed, synchronous calls"},
     }
-    dec.free()
-    for b in owned:
-        b.free()
-    return result
 
 
 if __name__ == "__main__":
