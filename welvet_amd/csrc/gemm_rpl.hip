@@ -23,7 +23,7 @@
 // 8-column block both operands are in k order [0,2,4,6,1,3,5,7], the order in
 // which the code spread produces pairs; a dot product over the block does not
 // depend on the order. Two kernels:
-//   * k_gemm_rg, up to 64 tokens: a block per 64-row group, its waves
+//   * k_gemm_rg, up to 128 tokens: a block per 64-row group, its waves
 //     splitting K and reading X fragments straight from global memory, every
 //     weight dequantized once;
 //   * k_gemm_q4k_pw, more tokens: 256-row x 128-token tiles with X staged
@@ -912,6 +912,9 @@ bool gemm_supported(const DevBlob& b, int M) {
 //   * 65 to 128 tokens on at least 200 row groups: k_gemm_rg with four
 //     32-token tiles (4 waves, one per SIMD), no K split (4096->14336 M = 128
 //     43.5 against 45.7 us; with the split, 14336->4096, 49.3 against 45.0);
+//   * 65 to 128 tokens on fewer row groups: k_gemm_rg with two 64-token
+//     blocks (8 waves, 2 per SIMD), K split to 200 blocks (14336->4096
+//     M = 128 42.1-42.7 against 42.7-43.4 us on k_gemm_q4k_pw split 14 ways);
 //   * otherwise k_gemm_q4k_pw (256-row tiles of 128 tokens, one block per
 //     CU), K split while whole tiles leave CUs idle.
 enum { GEMM_PW = 1, GEMM_RG = 2 };
@@ -924,9 +927,9 @@ struct GemmPlan {
 constexpr int kRgMinBlocks = 200;  // k_gemm_rg blocks that fill the GPU (no K split below 65 tokens)
 GemmPlan gemm_plan(const DevBlob& b, int M) {
     const RplArgs& a = b.rpl;
-    GemmPlan p{GEMM_PW, M <= 32 ? 32 : M <= 64 ? 64 : 128, 1, a.nsb, 1, 1};
+    GemmPlan p{GEMM_PW, M <= 32 ? 32 : M <= 64 || (M <= 128 && a.rg_count < kRgMinBlocks) ? 64 : 128, 1, a.nsb, 1, 1};
     int want = 1;
-    if (M <= 64 || (M <= 128 && a.rg_count >= kRgMinBlocks)) {
+    if (M <= 128) {
         p.kind = GEMM_RG;
         const int64_t tiles = int64_t(a.rg_count) * ((M + p.bm - 1) / p.bm);
         want = int(std::max<int64_t>(1, (kRgMinBlocks + tiles - 1) / tiles));
