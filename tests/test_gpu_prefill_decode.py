@@ -66,7 +66,10 @@ def check_token(tok, rl, tol):
         assert tok == int(np.argmax(rl))
 
 
-CASES = [("Q4_K", 33, 2e-3), ("Q4_K", 300, 2e-3), ("Q6_K", 33, 2e-3), ("Q8_0", 8, 1e-5)]
+# Token counts by GEMM plan: 33 (A-fragment operands, 32-token tiles plus a
+# padded one), 100 (A fragments, 64-token blocks on the few row groups of
+# these widths), 300 (row-major operands, 128-token tiles).
+CASES = [("Q4_K", 33, 2e-3), ("Q4_K", 100, 2e-3), ("Q4_K", 300, 2e-3), ("Q6_K", 33, 2e-3), ("Q8_0", 8, 1e-5)]
 
 
 # Head dims and heads: G = nh / nkv query heads per KV head. The MFMA

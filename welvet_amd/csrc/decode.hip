@@ -1702,20 +1702,24 @@ int enqueue_prefill(Decoder& d, int n, int pos0) {
     const float scale = float(1.0 / std::sqrt(double(hd)));
     hipLaunchKernelGGL(k_embed_rows, dim3(unsigned((hidden + 255) / 256), unsigned(n)), dim3(256), 0, d.stream, d.embed,
                        d.ptok, d.ph, hidden, c.vocab);
-    // GEMMs that read a row-major fp16 operand: the norm before them writes it
-    auto rowmajor = [&](const DevBlob& w) { return gemm_supported(w, n) && !gemm_x_frag(w, n); };
+    // The fp16 operand order a projection's GEMM reads (1: A fragments, 0:
+    // row-major), or -1 for the batched GEMV; where every GEMM after a norm
+    // reads one order, the norm writes that operand itself
+    auto xorder = [&](const DevBlob& w) { return gemm_supported(w, n) ? (gemm_x_frag(w, n) ? 1 : 0) : -1; };
     float* xscale = d.pxh + (d.layers.empty() ? 0 : gemm_x_floats(d.layers[0].w[0], n));  // cols = hidden
     for (int L = 0; L < c.n_layers; ++L) {
         Layer& ly = d.layers[L];
         const bool fused = ly.has_qkv && gemm_supported(ly.qkv, n);
-        const bool qkv_x = fused ? rowmajor(ly.qkv) : rowmajor(ly.w[0]) && rowmajor(ly.w[1]) && rowmajor(ly.w[2]);
+        const int qkv_x = fused ? xorder(ly.qkv)
+                          : xorder(ly.w[1]) == xorder(ly.w[0]) && xorder(ly.w[2]) == xorder(ly.w[0]) ? xorder(ly.w[0])
+                                                                                                       : -1;
         PrefillX cx;
         // h += the previous layer's down projection (in pn), then the norm:
         // into Q, K and V's fp16 operand where they all read one, else f32
-        if (qkv_x) {
+        if (qkv_x >= 0) {
             launch_norm_x_f16r(d.ph, L == 0 ? nullptr : d.pn, ly.attn_norm, nullptr, d.pxh, xscale, n, hidden,
-                               c.rms_eps, d.stream);
-            cx = PrefillX{d.pn, nullptr, hidden, 0};
+                               c.rms_eps, qkv_x == 1, d.stream);
+            cx = PrefillX{d.pn, nullptr, hidden, qkv_x};
         } else if (L == 0) {
             hipLaunchKernelGGL(k_rmsnorm, dim3(unsigned(n)), dim3(1024), 0, d.stream, d.ph, ly.attn_norm, d.pn, hidden,
                                c.rms_eps);
@@ -1758,9 +1762,10 @@ int enqueue_prefill(Decoder& d, int n, int pos0) {
         if (e) return e;
         // h += O att, then the norm (into gate and up's fp16 operand where both read one)
         cx = PrefillX{};  // gate and up share one fp16 copy
-        if (rowmajor(ly.w[4]) && rowmajor(ly.w[5])) {
-            launch_norm_x_f16r(d.ph, d.pt, ly.ffn_norm, nullptr, d.pxh, xscale, n, hidden, c.rms_eps, d.stream);
-            cx = PrefillX{d.pn, nullptr, hidden, 0};
+        if (const int gu_x = xorder(ly.w[4]); gu_x >= 0 && xorder(ly.w[5]) == gu_x) {
+            launch_norm_x_f16r(d.ph, d.pt, ly.ffn_norm, nullptr, d.pxh, xscale, n, hidden, c.rms_eps, gu_x == 1,
+                               d.stream);
+            cx = PrefillX{d.pn, nullptr, hidden, gu_x};
         } else {
             hipLaunchKernelGGL(k_add_rmsnorm, dim3(unsigned(n)), dim3(1024), 0, d.stream, d.ph, d.pt, ly.ffn_norm, d.pn,
                                hidden, c.rms_eps);

@@ -536,17 +536,31 @@ void launch_x_f16r(const float* x, uint4* xh, float* xscale, int M, int kb8, hip
 // order [0,2,4,6,1,3,5,7]); with `y`, the f32 rows as well (a and y may be
 // the same rows: a block reads its row of a before its first barrier and
 // writes y after it). An 8-column block is float4s 2b, 2b + 1, held by lanes
-// 2b, 2b + 1; the even lane packs it.
+// 2b, 2b + 1; the even lane packs it. FRAG writes the blocks in the
+// A-fragment order of GemmArgs::xh, as k_x_f16r<NR, true, false> does: the
+// grid covers the M rows padded to 32, and the padding rows get zeros.
+template <bool FRAG>
 __global__ void __launch_bounds__(1024) k_norm_x_f16r(float* __restrict__ h, const float* a,
                                                       const float* __restrict__ gamma, float* y,
                                                       uint4* __restrict__ xh, float* __restrict__ xscale, int dim,
-                                                      double eps) {
+                                                      double eps, int M) {
     __shared__ double part[16];
     __shared__ float redm[16];
     const int m = blockIdx.x, t = threadIdx.x;
-    h += int64_t(m) * dim;
     constexpr int R = 4;
     const int n4 = dim / 4, kb8 = dim / 8;
+    const int mt = (M + 31) / 32;
+    auto put = [&](int b, uint4 v) {
+        if constexpr (FRAG)
+            xh[(int64_t(b >> 1) * mt + (m >> 5)) * 64 + (m & 31) + 32 * (b & 1)] = v;
+        else
+            xh[int64_t(m) * kb8 + b] = v;
+    };
+    if (FRAG && m >= M) {
+        for (int b = t; b < kb8; b += 1024) put(b, make_uint4(0u, 0u, 0u, 0u));
+        return;
+    }
+    h += int64_t(m) * dim;
     float4 xv[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -601,7 +615,7 @@ __global__ void __launch_bounds__(1024) k_norm_x_f16r(float* __restrict__ h, con
     for (int r = 0; r < R; ++r) {
         const int i = t + 1024 * r;
         const float4 nb = make_float4(quad_xor1(yv[r].x), quad_xor1(yv[r].y), quad_xor1(yv[r].z), quad_xor1(yv[r].w));
-        if (!(t & 1) && i < n4 && i / 2 < kb8) xh[int64_t(m) * kb8 + i / 2] = pack_x8(yv[r], nb, up);
+        if (!(t & 1) && i < n4 && i / 2 < kb8) put(i / 2, pack_x8(yv[r], nb, up));
     }
 }
 
@@ -1042,9 +1056,14 @@ int launch_tiles(const DevBlob& b, const GemmPlan& p, dim3 grid, hipStream_t s, 
 bool gemm_x_frag(const DevBlob& b, int M) { return gemm_plan(b, M).kind == GEMM_RG; }
 
 void launch_norm_x_f16r(float* h, const float* a, const float* gamma, float* y, void* xh, float* xscale, int M, int dim,
-                        double eps, void* stream) {
-    hipLaunchKernelGGL(k_norm_x_f16r, dim3(unsigned(M)), dim3(1024), 0, static_cast<hipStream_t>(stream), h, a, gamma,
-                       y, static_cast<uint4*>(xh), xscale, dim, eps);
+                        double eps, bool frag, void* stream) {
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (frag)
+        hipLaunchKernelGGL(k_norm_x_f16r<true>, dim3(unsigned((M + 31) / 32 * 32)), dim3(1024), 0, s, h, a, gamma, y,
+                           static_cast<uint4*>(xh), xscale, dim, eps, M);
+    else
+        hipLaunchKernelGGL(k_norm_x_f16r<false>, dim3(unsigned(M)), dim3(1024), 0, s, h, a, gamma, y,
+                           static_cast<uint4*>(xh), xscale, dim, eps, M);
 }
 
 void gemm_convert_x(const float* d_x, const float* d_u, int cols, int M, bool frag, void* xhv, float* xscale,

@@ -294,10 +294,11 @@ void gemm_convert_x(const float* d_x, const float* d_u, int cols, int M, bool fr
 int launch_gemm_xh(const DevBlob& b, const void* xh, const float* xscale, float* d_y, int M, void* stream,
                    float* d_part);
 // h (+)= a, then the RMSNorm of M rows of dim (a multiple of 8, at most 16384)
-// straight into the fp16 operand a row-major (not A-fragment) plan reads,
-// and into the f32 rows y when y is given.
+// straight into the fp16 operand of the GEMM plans (row-major, or with frag
+// the A-fragment order of gemm_x_frag plans), and into the f32 rows y when y
+// is given.
 void launch_norm_x_f16r(float* h, const float* a, const float* gamma, float* y, void* xh, float* xscale, int M, int dim,
-                        double eps, void* stream);
+                        double eps, bool frag, void* stream);
 // MatVecT on LAYOUT_RPL (slice partials in d_scratch when the plan has several slices).
 int launch_rpl_matvec_t(const DevBlob& b, const float* d_gy, float* d_gx, int batch, void* stream, float* d_scratch);
 size_t rpl_t_scratch_floats(const RplArgs& a, int batch);
