@@ -921,14 +921,14 @@ bool gemm_supported(const DevBlob& b, int M) {
 // (splits of sb_per_split super-blocks) and, for k_gemm_rg, its waves per
 // block W and super-blocks per wave `per`:
 //   * up to 64 tokens: k_gemm_rg (one block per 64-row group, 8 waves
-//     splitting K, one or two 32-token tiles), K split over blocks only while
-//     the row groups alone give fewer than 200 blocks;
+//     splitting K, one or two 32-token tiles), K split over blocks by the
+//     fewest passes of the grid per unit of work (below);
 //   * 65 to 128 tokens on at least 200 row groups: k_gemm_rg with four
 //     32-token tiles (4 waves, one per SIMD), no K split (4096->14336 M = 128
 //     43.5 against 45.7 us; with the split, 14336->4096, 49.3 against 45.0);
 //   * 65 to 128 tokens on fewer row groups: k_gemm_rg with two 64-token
-//     blocks (8 waves, 2 per SIMD), K split to 200 blocks (14336->4096
-//     M = 128 42.1-42.7 against 42.7-43.4 us on k_gemm_q4k_pw split 14 ways);
+//     blocks (8 waves, 2 per SIMD), K split as above (14336->4096 M = 128
+//     42.1-42.7 against 42.7-43.4 us on k_gemm_q4k_pw split 14 ways);
 //   * otherwise k_gemm_q4k_pw (256-row tiles of 128 tokens, one block per
 //     CU), K split while whole tiles leave CUs idle.
 enum { GEMM_PW = 1, GEMM_RG = 2 };
@@ -938,16 +938,29 @@ constexpr int rg_waves(int tm) { return tm == 4 ? 4 : 8; }
 struct GemmPlan {
     int kind, bm, splits, sb_per_split, W, per;
 };
-constexpr int kRgMinBlocks = 200;  // k_gemm_rg blocks that fill the GPU (no K split below 65 tokens)
+constexpr int kRgMinBlocks = 200;  // row groups on which 128-token k_gemm_rg blocks fill the GPU unsplit
+constexpr int64_t kCUs = 256;       // MI355X
 GemmPlan gemm_plan(const DevBlob& b, int M) {
     const RplArgs& a = b.rpl;
     GemmPlan p{GEMM_PW, M <= 32 ? 32 : M <= 64 || (M <= 128 && a.rg_count < kRgMinBlocks) ? 64 : 128, 1, a.nsb, 1, 1};
     int want = 1;
     if (M <= 128) {
+        // A k_gemm_rg block fills its CU (8 waves of up to 256 registers, or
+        // 4 of 512), so the grid runs in ceil(blocks / 256) passes of
+        // 1/want of the work each: the split with the fewest passes per unit
+        // of work, the smallest of equals (no split sum where a split would
+        // only add a pass).
         p.kind = GEMM_RG;
         const int64_t tiles = int64_t(a.rg_count) * ((M + p.bm - 1) / p.bm);
-        want = int(std::max<int64_t>(1, (kRgMinBlocks + tiles - 1) / tiles));
-        want = std::min(want, std::max(1, a.nsb / 8));  // each split >= 8 super-blocks
+        const int max_split = std::max(1, a.nsb / 8);  // each split >= 8 super-blocks
+        double best = 0.0;
+        for (int w = 1; w <= max_split; ++w) {
+            const double t = double((tiles * w + kCUs - 1) / kCUs) / w;
+            if (w == 1 || t < best - 1e-9) {
+                best = t;
+                want = w;
+            }
+        }
     } else {
         const int64_t tiles = int64_t((a.rows + 255) / 256) * ((M + p.bm - 1) / p.bm);
         want = int(std::max<int64_t>(1, 256 / tiles));
