@@ -160,6 +160,29 @@ def test_prefill_qkv_stack_row_factors():
     dec.free()
 
 
+@pytest.mark.parametrize("n", [33, 100, 200])
+def test_prefill_split_projections(n):
+    """One layer at hidden 4096 and SwiGLU 8192 (Q|K|V 6144 x 4096, O 4096 x
+    4096, down 4096 x 8192), where the prompt GEMMs split K over blocks: at 33
+    and 100 tokens O splits 2 ways and down 4 and 2 ways, their slices left
+    unsummed for the norm after them to add; at 200 tokens (128-token tiles)
+    O and down split 8 ways and are summed before it."""
+    print(f"[gpu] prefill with split projections n={n}", flush=True)
+    cfg = Config(n_layers=1, hidden=4096, n_heads=32, n_kv_heads=8, head_dim=128, ffn=8192, vocab=300, max_seq=208)
+    dec, ref = build(cfg, "Q4_K", 71 + n)
+    toks = np.random.default_rng(n + 3).integers(0, cfg.vocab, n)
+    nxt, logits = dec.prefill(toks, 0, want_logits=True)
+    rl, _ = ref.prefill(toks)
+    err = normwise(logits, rl)
+    print(f"[gpu]   prompt logits normwise {err:.2e}", flush=True)
+    assert err <= 2e-3
+    check_token(nxt, rl, 2e-3)
+    t_dev, l_dev = dec.generate(nxt, n, 1, advance_pos=True, want_logits=True)
+    rl, _ = ref.step(nxt, n)
+    assert normwise(l_dev, rl) <= 2e-3
+    dec.free()
+
+
 def test_prefill_in_two_blocks():
     """A prompt in two calls (20 rows at position 0, then 13 at 20): the second
     block attends to the cache rows the first one wrote."""

@@ -1591,16 +1591,24 @@ struct PrefillX {
 // y = W x for n prompt rows; with u the input is silu(x) * u. The GEMM takes
 // the shared fp16 copy of its input (made here when cx does not hold it);
 // other blobs take the batched GEMV on f32 rows, with tmp holding the SwiGLU
-// rows.
+// rows. With `splits`, a K-split GEMM of at most 4 splits leaves its
+// unsummed slices in d.pscratch and stores their count (1: y holds the
+// result); more splits are summed into y here.
 int prefill_proj(Decoder& d, PrefillX& cx, const DevBlob& w, const float* x, const float* u, float* y, int n,
-                 float* tmp) {
+                 float* tmp, int* splits = nullptr) {
+    if (splits) *splits = 1;
     if (gemm_supported(w, n)) {
         const int frag = gemm_x_frag(w, n) ? 1 : 0;
         if (cx.x != x || cx.u != u || cx.cols != w.cols || cx.frag != frag) {
             gemm_convert_x(x, u, int(w.cols), n, frag != 0, d.pxh, d.pxh + gemm_x_floats(w, n), d.stream);
             cx = PrefillX{x, u, w.cols, frag};
         }
-        return launch_gemm_xh(w, d.pxh, d.pxh + gemm_x_floats(w, n), y, n, d.stream, d.pscratch);
+        const int e = launch_gemm_xh(w, d.pxh, d.pxh + gemm_x_floats(w, n), y, n, d.stream, d.pscratch, splits);
+        if (!e && splits && *splits > 4) {
+            launch_split_sum(d.pscratch, y, int64_t(n) * w.rows, *splits, d.stream);
+            *splits = 1;
+        }
+        return e;
     }
     const float* xin = x;
     if (u) {
@@ -1707,6 +1715,15 @@ int enqueue_prefill(Decoder& d, int n, int pos0) {
     // reads one order, the norm writes that operand itself
     auto xorder = [&](const DevBlob& w) { return gemm_supported(w, n) ? (gemm_x_frag(w, n) ? 1 : 0) : -1; };
     float* xscale = d.pxh + (d.layers.empty() ? 0 : gemm_x_floats(d.layers[0].w[0], n));  // cols = hidden
+    // The O and down projections may leave up to 4 unsummed K-split slices in
+    // d.pscratch for the fused norm after them to add (down_splits, o_splits >
+    // 1); other consumers get them summed first
+    const int64_t nh = int64_t(n) * hidden;
+    int down_splits = 1;
+    auto sum_splits = [&](int& splits, float* y) {
+        if (splits > 1) launch_split_sum(d.pscratch, y, nh, splits, d.stream);
+        splits = 1;
+    };
     for (int L = 0; L < c.n_layers; ++L) {
         Layer& ly = d.layers[L];
         const bool fused = ly.has_qkv && gemm_supported(ly.qkv, n);
@@ -1714,16 +1731,21 @@ int enqueue_prefill(Decoder& d, int n, int pos0) {
                           : xorder(ly.w[1]) == xorder(ly.w[0]) && xorder(ly.w[2]) == xorder(ly.w[0]) ? xorder(ly.w[0])
                                                                                                        : -1;
         PrefillX cx;
-        // h += the previous layer's down projection (in pn), then the norm:
-        // into Q, K and V's fp16 operand where they all read one, else f32
+        // h += the previous layer's down projection (in pn, or its split
+        // slices), then the norm: into Q, K and V's fp16 operand where they
+        // all read one, else f32
         if (qkv_x >= 0) {
-            launch_norm_x_f16r(d.ph, L == 0 ? nullptr : d.pn, ly.attn_norm, nullptr, d.pxh, xscale, n, hidden,
-                               c.rms_eps, qkv_x == 1, d.stream);
+            const float* a = L == 0 ? nullptr : down_splits > 1 ? d.pscratch : d.pn;
+            if (const int e = launch_norm_x_f16r(d.ph, a, down_splits, nh, ly.attn_norm, nullptr, d.pxh, xscale, n,
+                                                 hidden, c.rms_eps, qkv_x == 1, d.stream))
+                return e;
+            down_splits = 1;
             cx = PrefillX{d.pn, nullptr, hidden, qkv_x};
         } else if (L == 0) {
             hipLaunchKernelGGL(k_rmsnorm, dim3(unsigned(n)), dim3(1024), 0, d.stream, d.ph, ly.attn_norm, d.pn, hidden,
                                c.rms_eps);
         } else {
+            sum_splits(down_splits, d.pn);
             hipLaunchKernelGGL(k_add_rmsnorm, dim3(unsigned(n)), dim3(1024), 0, d.stream, d.ph, d.pn, ly.attn_norm, d.pn,
                                hidden, c.rms_eps);
         }
@@ -1758,15 +1780,19 @@ int enqueue_prefill(Decoder& d, int n, int pos0) {
                                    c.n_heads, c.n_kv_heads, c.max_seq, pos0, scale, qstr);
         }
         cx = PrefillX{};
-        e = prefill_proj(d, cx, ly.w[3], d.patt, nullptr, d.pt, n, nullptr);
+        int o_splits = 1;
+        e = prefill_proj(d, cx, ly.w[3], d.patt, nullptr, d.pt, n, nullptr, &o_splits);
         if (e) return e;
-        // h += O att, then the norm (into gate and up's fp16 operand where both read one)
+        // h += O att (in pt, or its split slices), then the norm (into gate
+        // and up's fp16 operand where both read one)
         cx = PrefillX{};  // gate and up share one fp16 copy
         if (const int gu_x = xorder(ly.w[4]); gu_x >= 0 && xorder(ly.w[5]) == gu_x) {
-            launch_norm_x_f16r(d.ph, d.pt, ly.ffn_norm, nullptr, d.pxh, xscale, n, hidden, c.rms_eps, gu_x == 1,
-                               d.stream);
+            e = launch_norm_x_f16r(d.ph, o_splits > 1 ? d.pscratch : d.pt, o_splits, nh, ly.ffn_norm, nullptr, d.pxh,
+                                   xscale, n, hidden, c.rms_eps, gu_x == 1, d.stream);
+            if (e) return e;
             cx = PrefillX{d.pn, nullptr, hidden, gu_x};
         } else {
+            sum_splits(o_splits, d.pt);
             hipLaunchKernelGGL(k_add_rmsnorm, dim3(unsigned(n)), dim3(1024), 0, d.stream, d.ph, d.pt, ly.ffn_norm, d.pn,
                                hidden, c.rms_eps);
         }
@@ -1774,10 +1800,12 @@ int enqueue_prefill(Decoder& d, int n, int pos0) {
         if (!e) e = prefill_proj(d, cx, ly.w[5], d.pn, nullptr, d.pu, n, d.pt);
         if (e) return e;
         cx = PrefillX{};
-        e = prefill_proj(d, cx, ly.w[6], d.pg, d.pu, d.pn, n, d.pt);  // down(silu(gate) * up), added by the next norm
+        // down(silu(gate) * up), added by the next norm
+        e = prefill_proj(d, cx, ly.w[6], d.pg, d.pu, d.pn, n, d.pt, &down_splits);
         if (e) return e;
     }
     // the last layer's residual add, for the one row the LM head reads
+    sum_splits(down_splits, d.pn);
     hipLaunchKernelGGL(k_add, dim3(unsigned((hidden + 255) / 256)), dim3(256), 0, d.stream,
                        d.ph + int64_t(n - 1) * hidden, d.pn + int64_t(n - 1) * hidden, hidden);
     const float* last = d.ph + int64_t(n - 1) * hidden;

@@ -539,9 +539,12 @@ void launch_x_f16r(const float* x, uint4* xh, float* xscale, int M, int kb8, hip
 // 2b, 2b + 1; the even lane packs it. FRAG writes the blocks in the
 // A-fragment order of GemmArgs::xh, as k_x_f16r<NR, true, false> does: the
 // grid covers the M rows padded to 32, and the padding rows get zeros.
+// `a` may be the unsummed K split of the GEMM that made it (a_splits
+// slices a_stride floats apart, at most 4): the slices are added in split
+// order, as k_split_sum adds them, every load issued before the first add.
 template <bool FRAG>
-__global__ void __launch_bounds__(1024) k_norm_x_f16r(float* __restrict__ h, const float* a,
-                                                      const float* __restrict__ gamma, float* y,
+__global__ void __launch_bounds__(1024) k_norm_x_f16r(float* __restrict__ h, const float* a, int a_splits,
+                                                      int64_t a_stride, const float* __restrict__ gamma, float* y,
                                                       uint4* __restrict__ xh, float* __restrict__ xscale, int dim,
                                                       double eps, int M) {
     __shared__ double part[16];
@@ -569,7 +572,15 @@ __global__ void __launch_bounds__(1024) k_norm_x_f16r(float* __restrict__ h, con
         if (i < n4) {
             xv[r] = reinterpret_cast<const float4*>(h)[i];
             if (a) {
-                const float4 av = reinterpret_cast<const float4*>(a + int64_t(m) * dim)[i];
+                const float4* ap = reinterpret_cast<const float4*>(a + int64_t(m) * dim) + i;
+                float4 sv[4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    if (k < a_splits) sv[k] = ap[(int64_t(k) * a_stride) >> 2];
+                float4 av = sv[0];
+#pragma unroll
+                for (int k = 1; k < 4; ++k)
+                    if (k < a_splits) av = make_float4(av.x + sv[k].x, av.y + sv[k].y, av.z + sv[k].z, av.w + sv[k].w);
                 xv[r] = make_float4(xv[r].x + av.x, xv[r].y + av.y, xv[r].z + av.z, xv[r].w + av.w);
             }
         }
@@ -1068,15 +1079,22 @@ int launch_tiles(const DevBlob& b, const GemmPlan& p, dim3 grid, hipStream_t s, 
 
 bool gemm_x_frag(const DevBlob& b, int M) { return gemm_plan(b, M).kind == GEMM_RG; }
 
-void launch_norm_x_f16r(float* h, const float* a, const float* gamma, float* y, void* xh, float* xscale, int M, int dim,
-                        double eps, bool frag, void* stream) {
+int launch_norm_x_f16r(float* h, const float* a, int a_splits, int64_t a_stride, const float* gamma, float* y, void* xh,
+                       float* xscale, int M, int dim, double eps, bool frag, void* stream) {
+    if (a_splits < 1 || a_splits > 4 || (a_stride & 3)) return int(hipErrorInvalidValue);
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (frag)
-        hipLaunchKernelGGL(k_norm_x_f16r<true>, dim3(unsigned((M + 31) / 32 * 32)), dim3(1024), 0, s, h, a, gamma, y,
-                           static_cast<uint4*>(xh), xscale, dim, eps, M);
+        hipLaunchKernelGGL(k_norm_x_f16r<true>, dim3(unsigned((M + 31) / 32 * 32)), dim3(1024), 0, s, h, a, a_splits,
+                           a_stride, gamma, y, static_cast<uint4*>(xh), xscale, dim, eps, M);
     else
-        hipLaunchKernelGGL(k_norm_x_f16r<false>, dim3(unsigned(M)), dim3(1024), 0, s, h, a, gamma, y,
-                           static_cast<uint4*>(xh), xscale, dim, eps, M);
+        hipLaunchKernelGGL(k_norm_x_f16r<false>, dim3(unsigned(M)), dim3(1024), 0, s, h, a, a_splits, a_stride, gamma,
+                           y, static_cast<uint4*>(xh), xscale, dim, eps, M);
+    return 0;
+}
+
+void launch_split_sum(const float* part, float* y, int64_t n, int splits, void* stream) {
+    hipLaunchKernelGGL(k_split_sum, dim3(unsigned((n / 4 + 1 + 255) / 256)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), part, y, n, splits);
 }
 
 void gemm_convert_x(const float* d_x, const float* d_u, int cols, int M, bool frag, void* xhv, float* xscale,
@@ -1094,7 +1112,7 @@ void gemm_convert_x(const float* d_x, const float* d_u, int cols, int M, bool fr
 }
 
 int launch_gemm_xh(const DevBlob& b, const void* xh, const float* xscale, float* d_y, int M, void* stream,
-                   float* d_part) {
+                   float* d_part, int* d_splits) {
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (!gemm_supported(b, M)) return int(hipErrorInvalidValue);
     const GemmPlan p = gemm_plan(b, M);
@@ -1112,10 +1130,8 @@ int launch_gemm_xh(const DevBlob& b, const void* xh, const float* xscale, float*
                     unsigned(splits));
     const int e = b.gemm_row_factors ? launch_tiles<true>(b, p, grid, s, ga) : launch_tiles<false>(b, p, grid, s, ga);
     if (e) return e;
-    if (splits > 1) {
-        const int64_t n = int64_t(M) * b.rows;
-        hipLaunchKernelGGL(k_split_sum, dim3(unsigned((n / 4 + 1 + 255) / 256)), dim3(256), 0, s, d_part, d_y, n, splits);
-    }
+    if (d_splits) *d_splits = splits;
+    if (splits > 1 && !d_splits) launch_split_sum(d_part, d_y, int64_t(M) * b.rows, splits, s);
     return int(hipGetLastError());
 }
 

@@ -291,14 +291,20 @@ size_t gemm_x_floats(const DevBlob& b, int M);
 size_t gemm_scale_floats(int M);
 void gemm_convert_x(const float* d_x, const float* d_u, int cols, int M, bool frag, void* xh, float* xscale,
                     void* stream);
+// With d_splits, a K-split GEMM leaves its partials in d_part
+// ([*d_splits][M][rows], unsummed; d_y is then not written) and stores the
+// split count there (1: the result is in d_y).
 int launch_gemm_xh(const DevBlob& b, const void* xh, const float* xscale, float* d_y, int M, void* stream,
-                   float* d_part);
+                   float* d_part, int* d_splits = nullptr);
+// y[i] = the sum over `splits` slices of part ([splits][n]) in split order.
+void launch_split_sum(const float* part, float* y, int64_t n, int splits, void* stream);
 // h (+)= a, then the RMSNorm of M rows of dim (a multiple of 8, at most 16384)
 // straight into the fp16 operand of the GEMM plans (row-major, or with frag
 // the A-fragment order of gemm_x_frag plans), and into the f32 rows y when y
-// is given.
-void launch_norm_x_f16r(float* h, const float* a, const float* gamma, float* y, void* xh, float* xscale, int M, int dim,
-                        double eps, bool frag, void* stream);
+// is given. a may be a_splits (1 to 4) unsummed K-split slices, a_stride
+// floats apart, added in split order.
+int launch_norm_x_f16r(float* h, const float* a, int a_splits, int64_t a_stride, const float* gamma, float* y, void* xh,
+                       float* xscale, int M, int dim, double eps, bool frag, void* stream);
 // MatVecT on LAYOUT_RPL (slice partials in d_scratch when the plan has several slices).
 int launch_rpl_matvec_t(const DevBlob& b, const float* d_gy, float* d_gx, int batch, void* stream, float* d_scratch);
 size_t rpl_t_scratch_floats(const RplArgs& a, int batch);
