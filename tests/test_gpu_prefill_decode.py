@@ -166,7 +166,8 @@ def test_prefill_split_projections(n):
     4096, down 4096 x 8192), where the prompt GEMMs split K over blocks: at 33
     and 100 tokens O splits 2 ways and down 4 and 2 ways, their slices left
     unsummed for the norm after them to add; at 200 tokens (128-token tiles)
-    O and down split 8 ways and are summed before it."""
+    O and down split 8 ways and are summed before it. The Q|K|V stack splits
+    2, 1 and 4 ways, its slices added by RoPE."""
     print(f"[gpu] prefill with split projections n={n}", flush=True)
     cfg = Config(n_layers=1, hidden=4096, n_heads=32, n_kv_heads=8, head_dim=128, ffn=8192, vocab=300, max_seq=208)
     dec, ref = build(cfg, "Q4_K", 71 + n)

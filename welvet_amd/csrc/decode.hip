@@ -807,8 +807,13 @@ __global__ void __launch_bounds__(256) k_embed_rows(const float* __restrict__ ta
 // place, its k heads rotated and, with its v heads, written to the caches at
 // that position. Angles and the rotation in f64 as in k_embed / k_attn_reg:
 // angle_d = pos / theta^(2d/hd), (x0, x1) -> (x0 cos - x1 sin, x0 sin + x1 cos).
+// SPLIT: the rows are the unsummed K-split slices of the Q|K|V stack GEMM
+// (`splits` of them, at most 4, pstride floats apart, rows [q|k|v] of qs
+// floats) and are added in split order on load; the rotated q goes to q.
+template <bool SPLIT>
 __global__ void __launch_bounds__(256) k_rope_kv_rows(float* __restrict__ q, const float* __restrict__ k,
-                                                      const float* __restrict__ v, float* __restrict__ kc,
+                                                      const float* __restrict__ v, const float* __restrict__ part,
+                                                      int splits, int64_t pstride, float* __restrict__ kc,
                                                       float* __restrict__ vc, const double* __restrict__ freq_div,
                                                       int n_heads, int n_kv, int hd, int max_seq, int pos0, int qs,
                                                       int kvs) {
@@ -818,6 +823,24 @@ __global__ void __launch_bounds__(256) k_rope_kv_rows(float* __restrict__ q, con
     float* qr = q + int64_t(s) * qs;
     const float* kr = k + int64_t(s) * kvs;
     const float* vr = v + int64_t(s) * kvs;
+    const float* pr = SPLIT ? part + int64_t(s) * qs : nullptr;
+    // element j of the row's q, k or v (off: the column where its part starts)
+    auto rd = [&](const float* r, int off, int j) {
+        if constexpr (!SPLIT) {
+            return r[j];
+        } else {
+            float p[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+                if (t < splits) p[t] = pr[int64_t(t) * pstride + off + j];
+            float x = p[0];
+#pragma unroll
+            for (int t = 1; t < 4; ++t)
+                if (t < splits) x += p[t];
+            return x;
+        }
+    };
+    const int koff = n_heads * hd, voff = koff + kvd;
     // the angle depends on the position and the dim only: each thread takes
     // one dim (half divides 256: head dims 64 and 128) and every HG-th head
     const int HG = 256 / half, d = threadIdx.x % half;
@@ -825,12 +848,12 @@ __global__ void __launch_bounds__(256) k_rope_kv_rows(float* __restrict__ q, con
     const double c = cos(angle), sn = sin(angle);
     for (int hh = threadIdx.x / half; hh < n_heads + n_kv; hh += HG) {
         if (hh < n_heads) {
-            const double x0 = qr[hh * hd + d], x1 = qr[hh * hd + d + half];
+            const double x0 = rd(qr, 0, hh * hd + d), x1 = rd(qr, 0, hh * hd + d + half);
             qr[hh * hd + d] = float(x0 * c - x1 * sn);
             qr[hh * hd + d + half] = float(x0 * sn + x1 * c);
         } else {
             const int g = hh - n_heads;
-            const double x0 = kr[g * hd + d], x1 = kr[g * hd + d + half];
+            const double x0 = rd(kr, koff, g * hd + d), x1 = rd(kr, koff, g * hd + d + half);
             float* crow = kc + (int64_t(g) * max_seq + pos) * hd;
             crow[d] = float(x0 * c - x1 * sn);
             crow[d + half] = float(x0 * sn + x1 * c);
@@ -838,7 +861,7 @@ __global__ void __launch_bounds__(256) k_rope_kv_rows(float* __restrict__ q, con
     }
     for (int i = threadIdx.x; i < kvd; i += 256) {
         const int g = i / hd, d = i % hd;
-        vc[(int64_t(g) * max_seq + pos) * hd + d] = vr[i];
+        vc[(int64_t(g) * max_seq + pos) * hd + d] = rd(vr, voff, i);
     }
 }
 
@@ -1715,9 +1738,10 @@ int enqueue_prefill(Decoder& d, int n, int pos0) {
     // reads one order, the norm writes that operand itself
     auto xorder = [&](const DevBlob& w) { return gemm_supported(w, n) ? (gemm_x_frag(w, n) ? 1 : 0) : -1; };
     float* xscale = d.pxh + (d.layers.empty() ? 0 : gemm_x_floats(d.layers[0].w[0], n));  // cols = hidden
-    // The O and down projections may leave up to 4 unsummed K-split slices in
-    // d.pscratch for the fused norm after them to add (down_splits, o_splits >
-    // 1); other consumers get them summed first
+    // The Q|K|V stack, O and down projections may leave up to 4 unsummed
+    // K-split slices in d.pscratch for the kernel after them to add (RoPE; the
+    // fused norm: down_splits, o_splits > 1); other consumers get them summed
+    // first
     const int64_t nh = int64_t(n) * hidden;
     int down_splits = 1;
     auto sum_splits = [&](int& splits, float* y) {
@@ -1754,9 +1778,9 @@ int enqueue_prefill(Decoder& d, int n, int pos0) {
         // copy of the normed rows
         const int qd = c.n_heads * hd, kvd = c.n_kv_heads * hd;
         float *q = d.pq, *k = d.pk, *v = d.pv;
-        int qstr = qd, kvstr = kvd, e = 0;
+        int qstr = qd, kvstr = kvd, e = 0, qkv_splits = 1;
         if (fused) {
-            e = prefill_proj(d, cx, ly.qkv, d.pn, nullptr, d.pq, n, d.pt);
+            e = prefill_proj(d, cx, ly.qkv, d.pn, nullptr, d.pq, n, d.pt, &qkv_splits);
             k = d.pq + qd;
             v = k + kvd;
             qstr = kvstr = qd + 2 * kvd;
@@ -1766,8 +1790,14 @@ int enqueue_prefill(Decoder& d, int n, int pos0) {
             if (!e) e = prefill_proj(d, cx, ly.w[2], d.pn, nullptr, d.pv, n, d.pt);
         }
         if (e) return e;
-        hipLaunchKernelGGL(k_rope_kv_rows, dim3(unsigned(n)), dim3(256), 0, d.stream, q, k, v, ly.kc, ly.vc,
-                           d.freq_div, c.n_heads, c.n_kv_heads, hd, c.max_seq, pos0, qstr, kvstr);
+        if (qkv_splits > 1)
+            hipLaunchKernelGGL(k_rope_kv_rows<true>, dim3(unsigned(n)), dim3(256), 0, d.stream, q, k, v, d.pscratch,
+                               qkv_splits, int64_t(n) * qstr, ly.kc, ly.vc, d.freq_div, c.n_heads, c.n_kv_heads, hd,
+                               c.max_seq, pos0, qstr, kvstr);
+        else
+            hipLaunchKernelGGL(k_rope_kv_rows<false>, dim3(unsigned(n)), dim3(256), 0, d.stream, q, k, v, nullptr, 1,
+                               int64_t(0), ly.kc, ly.vc, d.freq_div, c.n_heads, c.n_kv_heads, hd, c.max_seq, pos0, qstr,
+                               kvstr);
         // bf16x3 products where Q, K and V came from the fp16 GEMM (the 2e-3 bar)
         const bool bf = fused || (gemm_supported(ly.w[0], n) && gemm_supported(ly.w[1], n) && gemm_supported(ly.w[2], n));
         if (!launch_attn_prefill_mf(d, ly, q, qstr, n, pos0, scale, bf)) {
