@@ -810,6 +810,8 @@ __global__ void __launch_bounds__(256) k_embed_rows(const float* __restrict__ ta
 // SPLIT: the rows are the unsummed K-split slices of the Q|K|V stack GEMM
 // (`splits` of them, at most 4, pstride floats apart, rows [q|k|v] of qs
 // floats) and are added in split order on load; the rotated q goes to q.
+// Block (s, y) takes every gridDim.y-th pass over the row's heads (a short
+// prompt spreads a row over several blocks).
 template <bool SPLIT>
 __global__ void __launch_bounds__(256) k_rope_kv_rows(float* __restrict__ q, const float* __restrict__ k,
                                                       const float* __restrict__ v, const float* __restrict__ part,
@@ -846,7 +848,7 @@ __global__ void __launch_bounds__(256) k_rope_kv_rows(float* __restrict__ q, con
     const int HG = 256 / half, d = threadIdx.x % half;
     const double angle = double(pos) / freq_div[d];
     const double c = cos(angle), sn = sin(angle);
-    for (int hh = threadIdx.x / half; hh < n_heads + n_kv; hh += HG) {
+    for (int hh = threadIdx.x / half + HG * blockIdx.y; hh < n_heads + n_kv; hh += HG * gridDim.y) {
         if (hh < n_heads) {
             const double x0 = rd(qr, 0, hh * hd + d), x1 = rd(qr, 0, hh * hd + d + half);
             qr[hh * hd + d] = float(x0 * c - x1 * sn);
@@ -859,7 +861,7 @@ __global__ void __launch_bounds__(256) k_rope_kv_rows(float* __restrict__ q, con
             crow[d + half] = float(x0 * sn + x1 * c);
         }
     }
-    for (int i = threadIdx.x; i < kvd; i += 256) {
+    for (int i = threadIdx.x + 256 * blockIdx.y; i < kvd; i += 256 * gridDim.y) {
         const int g = i / hd, d = i % hd;
         vc[(int64_t(g) * max_seq + pos) * hd + d] = rd(vr, voff, i);
     }
@@ -1790,12 +1792,15 @@ int enqueue_prefill(Decoder& d, int n, int pos0) {
             if (!e) e = prefill_proj(d, cx, ly.w[2], d.pn, nullptr, d.pv, n, d.pt);
         }
         if (e) return e;
+        // up to 256 / n blocks per row, at most one per pass over the heads
+        const int passes = (c.n_heads + c.n_kv_heads + 256 / (hd / 2) - 1) / (256 / (hd / 2));
+        const dim3 rg(unsigned(n), unsigned(std::max(1, std::min(passes, 256 / n))));
         if (qkv_splits > 1)
-            hipLaunchKernelGGL(k_rope_kv_rows<true>, dim3(unsigned(n)), dim3(256), 0, d.stream, q, k, v, d.pscratch,
+            hipLaunchKernelGGL(k_rope_kv_rows<true>, rg, dim3(256), 0, d.stream, q, k, v, d.pscratch,
                                qkv_splits, int64_t(n) * qstr, ly.kc, ly.vc, d.freq_div, c.n_heads, c.n_kv_heads, hd,
                                c.max_seq, pos0, qstr, kvstr);
         else
-            hipLaunchKernelGGL(k_rope_kv_rows<false>, dim3(unsigned(n)), dim3(256), 0, d.stream, q, k, v, nullptr, 1,
+            hipLaunchKernelGGL(k_rope_kv_rows<false>, rg, dim3(256), 0, d.stream, q, k, v, nullptr, 1,
                                int64_t(0), ly.kc, ly.vc, d.freq_div, c.n_heads, c.n_kv_heads, hd, c.max_seq, pos0, qstr,
                                kvstr);
         // bf16x3 products where Q, K and V came from the fp16 GEMM (the 2e-3 bar)
