@@ -1133,10 +1133,17 @@ __device__ __forceinline__ void bf16_split(float x, __bf16& hi, __bf16& lo) {
 // step: dims 16s + 8h + b of K and Q in S^T = K Q^T; for O^T += V^T P^T the
 // keys 16s + 4h + b (b < 4) and 16s + 8 + 4h + b - 4 (b >= 4), the order in
 // which the lane's probability registers stand.
-template <int HD, int G>
+// KSPLIT: block z of gridDim.z takes the z-th of gridDim.z even ranges of its
+// key tiles and stores, per row and head, the unnormalized output, the
+// running max (log2 units) and the running sum to part ([z][n][heads][HD + 4],
+// 16-byte rows: the output, then the max and the sum)
+// for k_attn_prefill_merge; a range past a row's causal end leaves max
+// -inf and sum 0, and range 0 always holds key 0.
+template <int HD, int G, bool KSPLIT = false>
 __global__ void __launch_bounds__(256) k_attn_prefill_bf(const float* __restrict__ q, const float* __restrict__ kc,
                                                          const float* __restrict__ vc, float* __restrict__ out, int n,
-                                                         int n_heads, int max_seq, int pos0, float scale, int qstr) {
+                                                         int n_heads, int max_seq, int pos0, float scale, int qstr,
+                                                         float* __restrict__ part) {
     constexpr int QP = 128 / G, KT = 32, NT = HD / 32, NS = HD / 16;
     constexpr int KSB = HD + 8;  // bf16 K row stride in LDS
     constexpr int VSB = KT + 8;  // bf16 V^T row stride (one row per dim)
@@ -1190,6 +1197,12 @@ __global__ void __launch_bounds__(256) k_attn_prefill_bf(const float* __restrict
     const float* kb = kc + int64_t(kvh) * max_seq * HD;
     const float* vb = vc + int64_t(kvh) * max_seq * HD;
     const int ntiles = last_pos / KT + 1;
+    int kt0 = 0, kt1 = ntiles;  // this block's key tiles
+    if constexpr (KSPLIT) {
+        const int per = (ntiles + int(gridDim.z) - 1) / int(gridDim.z);
+        kt0 = min(ntiles, int(blockIdx.z) * per);
+        kt1 = min(ntiles, kt0 + per);
+    }
     constexpr int NI = KT * HD / 4 / 256;  // float4 items of K (and of V) per thread and tile
     float4 pk[NI], pv[NI];
     auto gload = [&](int kt) {
@@ -1222,12 +1235,14 @@ __global__ void __launch_bounds__(256) k_attn_prefill_bf(const float* __restrict
             *reinterpret_cast<bf16x4*>(&klo[buf][key * KSB + 4 * c4]) = k_l;
         }
     };
-    gload(0);
-    lstore(0);
+    if (!KSPLIT || kt0 < kt1) {  // an unsplit block always has a tile
+        gload(kt0);
+        lstore(0);
+    }
     __syncthreads();
-    for (int kt = 0; kt < ntiles; ++kt) {
-        const int buf = kt & 1;
-        if (kt + 1 < ntiles) gload(kt + 1);  // in flight through this tile's MFMAs
+    for (int kt = kt0; kt < kt1; ++kt) {
+        const int buf = (kt - kt0) & 1;
+        if (kt + 1 < kt1) gload(kt + 1);  // in flight through this tile's MFMAs
         // S^T = K Q^T
         f32x16 sacc;
 #pragma unroll
@@ -1296,11 +1311,25 @@ __global__ void __launch_bounds__(256) k_attn_prefill_bf(const float* __restrict
                 o[nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_l, p_h, o[nt], 0, 0, 0);
             }
         }
-        if (kt + 1 < ntiles) lstore(buf ^ 1);  // the other buffer's readers finished before the last barrier
+        if (kt + 1 < kt1) lstore(buf ^ 1);  // the other buffer's readers finished before the last barrier
         __syncthreads();
     }
     if (!live) return;
     // lane l holds O^T[32nt + 8(r/4) + 4h + r%4][row l % 32]: four consecutive dims per r/4
+    if constexpr (KSPLIT) {
+        float* prow = part + ((int64_t(blockIdx.z) * n + srow) * n_heads + head) * (HD + 4);
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+            for (int a = 0; a < 4; ++a)
+                *reinterpret_cast<float4*>(prow + 32 * nt + 8 * a + 4 * h) =
+                    make_float4(o[nt][4 * a], o[nt][4 * a + 1], o[nt][4 * a + 2], o[nt][4 * a + 3]);
+        if (h == 0) {
+            prow[HD] = m_run;
+            prow[HD + 1] = l_run;
+        }
+        return;
+    }
     const float inv = 1.0f / l_run;
     float* orow = out + int64_t(srow) * qd + int64_t(head) * HD;
 #pragma unroll
@@ -1309,6 +1338,42 @@ __global__ void __launch_bounds__(256) k_attn_prefill_bf(const float* __restrict
         for (int a = 0; a < 4; ++a)
             *reinterpret_cast<float4*>(orow + 32 * nt + 8 * a + 4 * h) =
                 make_float4(o[nt][4 * a] * inv, o[nt][4 * a + 1] * inv, o[nt][4 * a + 2] * inv, o[nt][4 * a + 3] * inv);
+}
+
+// The key-split prompt attention's rows: per (row, head), the ks ranges'
+// outputs o_z, maxima m_z (log2 units) and sums l_z meet as
+// sum_z 2^(m_z - M) o_z / sum_z 2^(m_z - M) l_z, M = max_z m_z (ranges with
+// m_z = -inf count 0). One block per (row, head), one thread per dim, every
+// range's values loaded before the first add.
+template <int HD>
+__global__ void __launch_bounds__(HD) k_attn_prefill_merge(const float* __restrict__ part, float* __restrict__ out,
+                                                           int n, int n_heads, int ks) {
+    constexpr int KS = 8;
+    const int s = blockIdx.x, head = blockIdx.y, dim = threadIdx.x;
+    float mv[KS], lv[KS], ov[KS];
+#pragma unroll
+    for (int z = 0; z < KS; ++z) {
+        if (z < ks) {
+            const float* p = part + ((int64_t(z) * n + s) * n_heads + head) * (HD + 4);
+            mv[z] = p[HD];
+            lv[z] = p[HD + 1];
+            ov[z] = p[dim];
+        }
+    }
+    float M = mv[0];
+#pragma unroll
+    for (int z = 1; z < KS; ++z)
+        if (z < ks) M = fmaxf(M, mv[z]);
+    float num = 0.f, den = 0.f;
+#pragma unroll
+    for (int z = 0; z < KS; ++z) {
+        if (z < ks && mv[z] != -INFINITY) {
+            const float w = exp2f(mv[z] - M);
+            num = fmaf(w, ov[z], num);
+            den = fmaf(w, lv[z], den);
+        }
+    }
+    out[(int64_t(s) * n_heads + head) * HD + dim] = num / den;
 }
 
 // ---------------------------------------------------------------------------
@@ -1644,6 +1709,21 @@ int prefill_proj(Decoder& d, PrefillX& cx, const DevBlob& w, const float* x, con
     return launch_matvec(w, xin, y, n, d.stream, d.pscratch);
 }
 
+// Key splits of the bf16x3 prompt attention: its (KV head, 128 / G position)
+// blocks, when under one pass of the GPU, each take ks ranges of their key
+// tiles, ks = min(8, 256 / blocks, key tiles of the longest range); the
+// pos0-free bound sizes the scratch.
+int attn_key_splits(const wv_decoder_config& c, int n, int pos0) {
+    const int G = c.n_heads / c.n_kv_heads;
+    const int64_t blocks = int64_t(c.n_kv_heads) * ((n + 128 / G - 1) / (128 / G));
+    const int64_t tiles = pos0 < 0 ? 8 : (int64_t(pos0) + n - 1) / 32 + 1;
+    return int(std::max<int64_t>(1, std::min<int64_t>({8, 256 / std::max<int64_t>(blocks, 1), tiles})));
+}
+size_t attn_part_floats(const wv_decoder_config& c, int n) {
+    const int ks = attn_key_splits(c, n, -1);
+    return ks > 1 ? size_t(ks) * n * c.n_heads * (c.head_dim + 4) : 0;
+}
+
 size_t prefill_proj_scratch(const DevBlob& w, int n) {
     return gemm_supported(w, n) ? gemm_scratch_floats(w, n) : matvec_scratch_floats(w, n);
 }
@@ -1660,6 +1740,7 @@ int ensure_prefill(Decoder& d, int n) {
         for (const DevBlob& w : ly.w) need(w);
         if (ly.has_qkv) need(ly.qkv);
     }
+    need_s = std::max(need_s, attn_part_floats(c, n));  // the key-split attention's ranges (between RoPE and O)
     if (n <= d.pcap && need_s <= d.pscratch_floats && need_x <= d.pxh_floats) return WV_OK;
     drop_prefill(d);
     const size_t qd = size_t(c.n_heads) * c.head_dim, kvd = size_t(c.n_kv_heads) * c.head_dim;
@@ -1705,26 +1786,40 @@ bool launch_attn_prefill_mf(Decoder& d, Layer& ly, const float* q, int qstr, int
     const wv_decoder_config& c = d.c;
     const int G = c.n_heads / c.n_kv_heads, hd = c.head_dim;
     if ((hd != 64 && hd != 128) || (G != 1 && G != 2 && G != 4 && G != 8)) return false;
-    const dim3 grid(unsigned(c.n_kv_heads), unsigned((n + 128 / G - 1) / (128 / G)));
+    const int ks = bf ? attn_key_splits(c, n, pos0) : 1;
+    const dim3 grid(unsigned(c.n_kv_heads), unsigned((n + 128 / G - 1) / (128 / G)), unsigned(ks));
     auto go = [&](auto kern) {
         hipLaunchKernelGGL(kern, grid, dim3(256), 0, d.stream, q, ly.kc, ly.vc, d.patt, n, c.n_heads, c.max_seq, pos0,
                            scale, qstr);
     };
-    auto pick = [&](auto kf, auto kb) { bf ? go(kb) : go(kf); };
+    auto gob = [&](auto kern, auto kern_split) {
+        if (ks == 1)
+            hipLaunchKernelGGL(kern, grid, dim3(256), 0, d.stream, q, ly.kc, ly.vc, d.patt, n, c.n_heads, c.max_seq,
+                               pos0, scale, qstr, nullptr);
+        else
+            hipLaunchKernelGGL(kern_split, grid, dim3(256), 0, d.stream, q, ly.kc, ly.vc, d.patt, n, c.n_heads,
+                               c.max_seq, pos0, scale, qstr, d.pscratch);
+    };
     if (hd == 128) {
         switch (G) {
-        case 1: pick(k_attn_prefill_mf<128, 1>, k_attn_prefill_bf<128, 1>); break;
-        case 2: pick(k_attn_prefill_mf<128, 2>, k_attn_prefill_bf<128, 2>); break;
-        case 4: pick(k_attn_prefill_mf<128, 4>, k_attn_prefill_bf<128, 4>); break;
-        default: pick(k_attn_prefill_mf<128, 8>, k_attn_prefill_bf<128, 8>); break;
+        case 1: bf ? gob(k_attn_prefill_bf<128, 1>, k_attn_prefill_bf<128, 1, true>) : go(k_attn_prefill_mf<128, 1>); break;
+        case 2: bf ? gob(k_attn_prefill_bf<128, 2>, k_attn_prefill_bf<128, 2, true>) : go(k_attn_prefill_mf<128, 2>); break;
+        case 4: bf ? gob(k_attn_prefill_bf<128, 4>, k_attn_prefill_bf<128, 4, true>) : go(k_attn_prefill_mf<128, 4>); break;
+        default: bf ? gob(k_attn_prefill_bf<128, 8>, k_attn_prefill_bf<128, 8, true>) : go(k_attn_prefill_mf<128, 8>); break;
         }
+        if (ks > 1)
+            hipLaunchKernelGGL(k_attn_prefill_merge<128>, dim3(unsigned(n), unsigned(c.n_heads)), dim3(128), 0,
+                               d.stream, d.pscratch, d.patt, n, c.n_heads, ks);
     } else {
         switch (G) {
-        case 1: pick(k_attn_prefill_mf<64, 1>, k_attn_prefill_bf<64, 1>); break;
-        case 2: pick(k_attn_prefill_mf<64, 2>, k_attn_prefill_bf<64, 2>); break;
-        case 4: pick(k_attn_prefill_mf<64, 4>, k_attn_prefill_bf<64, 4>); break;
-        default: pick(k_attn_prefill_mf<64, 8>, k_attn_prefill_bf<64, 8>); break;
+        case 1: bf ? gob(k_attn_prefill_bf<64, 1>, k_attn_prefill_bf<64, 1, true>) : go(k_attn_prefill_mf<64, 1>); break;
+        case 2: bf ? gob(k_attn_prefill_bf<64, 2>, k_attn_prefill_bf<64, 2, true>) : go(k_attn_prefill_mf<64, 2>); break;
+        case 4: bf ? gob(k_attn_prefill_bf<64, 4>, k_attn_prefill_bf<64, 4, true>) : go(k_attn_prefill_mf<64, 4>); break;
+        default: bf ? gob(k_attn_prefill_bf<64, 8>, k_attn_prefill_bf<64, 8, true>) : go(k_attn_prefill_mf<64, 8>); break;
         }
+        if (ks > 1)
+            hipLaunchKernelGGL(k_attn_prefill_merge<64>, dim3(unsigned(n), unsigned(c.n_heads)), dim3(64), 0, d.stream,
+                               d.pscratch, d.patt, n, c.n_heads, ks);
     }
     return true;
 }
