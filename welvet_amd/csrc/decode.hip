@@ -1782,7 +1782,21 @@ int ensure_prefill(Decoder& d, int n) {
 // The MFMA attention of a prompt block, for head dims 64 and 128 and 1, 2, 4
 // or 8 query heads per KV head (bf: the bf16x3 products of k_attn_prefill_bf,
 // else f32), q's rows qstr floats apart; false: the shape takes k_attn_prefill.
-bool launch_attn_prefill_mf(Decoder& d, Layer& ly, const float* q, int qstr, int n, int pos0, float scale, bool bf) {
+// The key-split attention's ranges merged into the f32 rows d.patt.
+void launch_attn_merge(Decoder& d, int n, int ks) {
+    const wv_decoder_config& c = d.c;
+    if (c.head_dim == 128)
+        hipLaunchKernelGGL(k_attn_prefill_merge<128>, dim3(unsigned(n), unsigned(c.n_heads)), dim3(128), 0, d.stream,
+                           d.pscratch, d.patt, n, c.n_heads, ks);
+    else
+        hipLaunchKernelGGL(k_attn_prefill_merge<64>, dim3(unsigned(n), unsigned(c.n_heads)), dim3(64), 0, d.stream,
+                           d.pscratch, d.patt, n, c.n_heads, ks);
+}
+
+// With ks_out, a key-split launch leaves its ranges in d.pscratch unmerged
+// and stores their count there (1: d.patt holds the rows).
+bool launch_attn_prefill_mf(Decoder& d, Layer& ly, const float* q, int qstr, int n, int pos0, float scale, bool bf,
+                            int* ks_out = nullptr) {
     const wv_decoder_config& c = d.c;
     const int G = c.n_heads / c.n_kv_heads, hd = c.head_dim;
     if ((hd != 64 && hd != 128) || (G != 1 && G != 2 && G != 4 && G != 8)) return false;
@@ -1807,9 +1821,6 @@ bool launch_attn_prefill_mf(Decoder& d, Layer& ly, const float* q, int qstr, int
         case 4: bf ? gob(k_attn_prefill_bf<128, 4>, k_attn_prefill_bf<128, 4, true>) : go(k_attn_prefill_mf<128, 4>); break;
         default: bf ? gob(k_attn_prefill_bf<128, 8>, k_attn_prefill_bf<128, 8, true>) : go(k_attn_prefill_mf<128, 8>); break;
         }
-        if (ks > 1)
-            hipLaunchKernelGGL(k_attn_prefill_merge<128>, dim3(unsigned(n), unsigned(c.n_heads)), dim3(128), 0,
-                               d.stream, d.pscratch, d.patt, n, c.n_heads, ks);
     } else {
         switch (G) {
         case 1: bf ? gob(k_attn_prefill_bf<64, 1>, k_attn_prefill_bf<64, 1, true>) : go(k_attn_prefill_mf<64, 1>); break;
@@ -1817,10 +1828,9 @@ bool launch_attn_prefill_mf(Decoder& d, Layer& ly, const float* q, int qstr, int
         case 4: bf ? gob(k_attn_prefill_bf<64, 4>, k_attn_prefill_bf<64, 4, true>) : go(k_attn_prefill_mf<64, 4>); break;
         default: bf ? gob(k_attn_prefill_bf<64, 8>, k_attn_prefill_bf<64, 8, true>) : go(k_attn_prefill_mf<64, 8>); break;
         }
-        if (ks > 1)
-            hipLaunchKernelGGL(k_attn_prefill_merge<64>, dim3(unsigned(n), unsigned(c.n_heads)), dim3(64), 0, d.stream,
-                               d.pscratch, d.patt, n, c.n_heads, ks);
     }
+    if (ks_out) *ks_out = ks;
+    else if (ks > 1) launch_attn_merge(d, n, ks);
     return true;
 }
 
@@ -1900,7 +1910,8 @@ int enqueue_prefill(Decoder& d, int n, int pos0) {
                                kvstr);
         // bf16x3 products where Q, K and V came from the fp16 GEMM (the 2e-3 bar)
         const bool bf = fused || (gemm_supported(ly.w[0], n) && gemm_supported(ly.w[1], n) && gemm_supported(ly.w[2], n));
-        if (!launch_attn_prefill_mf(d, ly, q, qstr, n, pos0, scale, bf)) {
+        int attn_ks = 1;
+        if (!launch_attn_prefill_mf(d, ly, q, qstr, n, pos0, scale, bf, &attn_ks)) {
             const dim3 ag(unsigned(c.n_kv_heads), unsigned(n));
             if (hd == 128)
                 hipLaunchKernelGGL(k_attn_prefill<128>, ag, dim3(256), 0, d.stream, q, ly.kc, ly.vc, d.patt,
@@ -1910,6 +1921,18 @@ int enqueue_prefill(Decoder& d, int n, int pos0) {
                                    c.n_heads, c.n_kv_heads, c.max_seq, pos0, scale, qstr);
         }
         cx = PrefillX{};
+        if (attn_ks > 1) {
+            // the key ranges merged straight into the O projection's fp16
+            // operand where it runs on the GEMM, else into the f32 rows
+            bool merged = false;
+            if (gemm_supported(ly.w[3], n)) {
+                const int fr = gemm_x_frag(ly.w[3], n) ? 1 : 0;
+                merged = launch_merge_x_f16r(d.pscratch, attn_ks, c.n_heads, hd, n, fr != 0, d.pxh,
+                                             d.pxh + gemm_x_floats(ly.w[3], n), d.stream) == 0;
+                if (merged) cx = PrefillX{d.patt, nullptr, ly.w[3].cols, fr};
+            }
+            if (!merged) launch_attn_merge(d, n, attn_ks);
+        }
         int o_splits = 1;
         e = prefill_proj(d, cx, ly.w[3], d.patt, nullptr, d.pt, n, nullptr, &o_splits);
         if (e) return e;

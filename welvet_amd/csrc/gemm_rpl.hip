@@ -511,6 +511,76 @@ __global__ void __launch_bounds__(256) k_x_f16r(const float4* __restrict__ x, co
         for (int i = t; i < kb8; i += 256) put(i, pack_x8(ld(2 * i), ld(2 * i + 1), up));
     }
 }
+// The key-split prompt attention's merge straight into the O projection's
+// fp16 operand: per row and head, sum_z 2^(m_z - M) o_z / sum_z 2^(m_z - M) l_z
+// over the ks ranges of part ([ks][M][heads][hd + 4]: the unnormalized
+// output, then the running max in log2 units and the running sum; ranges
+// with m_z = -inf count 0), in the order and arithmetic of the decoder's
+// k_attn_prefill_merge, then the row factor and blocks as k_x_f16r<NR, FRAG,
+// false> makes them from the merged rows. Every range's values of a slot are
+// loaded before the first add.
+template <int NR, bool FRAG>
+__global__ void __launch_bounds__(256) k_merge_x_f16r(const float* __restrict__ part, int ks, int n_heads, int hd,
+                                                       uint4* __restrict__ xh, float* __restrict__ xscale, int kb8,
+                                                       int M) {
+    constexpr int KS = 8;
+    __shared__ float red[4];
+    const int m = blockIdx.x, t = threadIdx.x;
+    const int mt = (M + 31) / 32;
+    auto put = [&](int i, uint4 v) {
+        if constexpr (FRAG)
+            xh[(int64_t(i >> 1) * mt + (m >> 5)) * 64 + (m & 31) + 32 * (i & 1)] = v;
+        else
+            xh[int64_t(m) * kb8 + i] = v;
+    };
+    if (FRAG && m >= M) {
+        for (int i = t; i < kb8; i += 256) put(i, make_uint4(0u, 0u, 0u, 0u));
+        return;
+    }
+    const int ps = hd + 4;
+    float4 lo[NR], hi[NR];
+    float mx = 0.f;
+#pragma unroll
+    for (int j = 0; j < NR; ++j) {
+        const int i = min(t + 256 * j, kb8 - 1), col = 8 * i, head = col / hd, dim = col % hd;
+        float mv[KS], lv[KS];
+        float4 ol[KS], oh[KS];
+#pragma unroll
+        for (int z = 0; z < KS; ++z) {
+            if (z < ks) {
+                const float* pz = part + ((int64_t(z) * M + m) * n_heads + head) * ps;
+                mv[z] = pz[hd];
+                lv[z] = pz[hd + 1];
+                ol[z] = *reinterpret_cast<const float4*>(pz + dim);
+                oh[z] = *reinterpret_cast<const float4*>(pz + dim + 4);
+            }
+        }
+        float Mz = mv[0];
+#pragma unroll
+        for (int z = 1; z < KS; ++z)
+            if (z < ks) Mz = fmaxf(Mz, mv[z]);
+        float4 nl = make_float4(0.f, 0.f, 0.f, 0.f), nh = nl;
+        float den = 0.f;
+#pragma unroll
+        for (int z = 0; z < KS; ++z) {
+            if (z < ks && mv[z] != -INFINITY) {
+                const float w = exp2f(mv[z] - Mz);
+                nl = make_float4(fmaf(w, ol[z].x, nl.x), fmaf(w, ol[z].y, nl.y), fmaf(w, ol[z].z, nl.z),
+                                 fmaf(w, ol[z].w, nl.w));
+                nh = make_float4(fmaf(w, oh[z].x, nh.x), fmaf(w, oh[z].y, nh.y), fmaf(w, oh[z].z, nh.z),
+                                 fmaf(w, oh[z].w, nh.w));
+                den = fmaf(w, lv[z], den);
+            }
+        }
+        lo[j] = make_float4(nl.x / den, nl.y / den, nl.z / den, nl.w / den);
+        hi[j] = make_float4(nh.x / den, nh.y / den, nh.z / den, nh.w / den);
+        mx = fmaxf(mx, absmax8(lo[j], hi[j]));
+    }
+    const float up = row_shift_up(mx, red, xscale + m, t);
+#pragma unroll
+    for (int j = 0; j < NR; ++j)
+        if (t + 256 * j < kb8) put(t + 256 * j, pack_x8(lo[j], hi[j], up));
+}
 template <bool FRAG, bool SW>
 void launch_x_f16r_t(const float* x, const float* u, uint4* xh, float* xscale, int M, int kb8, hipStream_t s) {
     const float4* x4 = reinterpret_cast<const float4*>(x);
@@ -1089,6 +1159,20 @@ int launch_norm_x_f16r(float* h, const float* a, int a_splits, int64_t a_stride,
     else
         hipLaunchKernelGGL(k_norm_x_f16r<false>, dim3(unsigned(M)), dim3(1024), 0, s, h, a, a_splits, a_stride, gamma,
                            y, static_cast<uint4*>(xh), xscale, dim, eps, M);
+    return 0;
+}
+
+int launch_merge_x_f16r(const float* part, int ks, int n_heads, int hd, int M, bool frag, void* xhv, float* xscale,
+                        void* stream) {
+    const int kb8 = n_heads * hd / 8;
+    if (ks < 1 || ks > 8 || hd % 8 || kb8 > 1024) return int(hipErrorInvalidValue);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    uint4* xh = static_cast<uint4*>(xhv);
+    const dim3 g(unsigned(frag ? (M + 31) / 32 * 32 : M)), b(256);
+    auto go = [&](auto kern) { hipLaunchKernelGGL(kern, g, b, 0, s, part, ks, n_heads, hd, xh, xscale, kb8, M); };
+    if (kb8 <= 256) frag ? go(k_merge_x_f16r<1, true>) : go(k_merge_x_f16r<1, false>);
+    else if (kb8 <= 512) frag ? go(k_merge_x_f16r<2, true>) : go(k_merge_x_f16r<2, false>);
+    else frag ? go(k_merge_x_f16r<4, true>) : go(k_merge_x_f16r<4, false>);
     return 0;
 }
 

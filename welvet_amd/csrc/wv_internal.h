@@ -298,6 +298,12 @@ int launch_gemm_xh(const DevBlob& b, const void* xh, const float* xscale, float*
                    float* d_part, int* d_splits = nullptr);
 // y[i] = the sum over `splits` slices of part ([splits][n]) in split order.
 void launch_split_sum(const float* part, float* y, int64_t n, int splits, void* stream);
+// The key-split prompt attention's ranges (part: [ks][M][n_heads][hd + 4],
+// ks <= 8) merged straight into the fp16 operand of a GEMM over the
+// n_heads * hd columns (row-major, or with frag the A-fragment order), with
+// its row factors in xscale.
+int launch_merge_x_f16r(const float* part, int ks, int n_heads, int hd, int M, bool frag, void* xh, float* xscale,
+                        void* stream);
 // h (+)= a, then the RMSNorm of M rows of dim (a multiple of 8, at most 16384)
 // straight into the fp16 operand of the GEMM plans (row-major, or with frag
 // the A-fragment order of gemm_x_frag plans), and into the f32 rows y when y
